@@ -1,0 +1,250 @@
+# SPDX-License-Identifier: MPL-2.0
+"""ctypes binding of libbaremetal_hip.so (the MI355X backend + engine).
+
+The library's C ABI is declared in include/backend.h (the reference's
+backend interface, src/backend/backend.h:12-67), include/baremetal.h (the
+engine API, reference include/baremetal.h:120-206) and include/bm_q8.h /
+include/bm_synth.h (MI355X additions).  This module only marshals numpy
+arrays across that ABI; it never computes anything itself, and it raises if
+the built library is missing instead of falling back to any other path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbaremetal_hip.so")
+
+_lib = None
+
+
+class BackendError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """Load the product library (fails loudly if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise BackendError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH, mode=C.RTLD_GLOBAL)
+    vp, sz, i, d, u64 = C.c_void_p, C.c_size_t, C.c_int, C.c_double, C.c_uint64
+    sig = {
+        "backend_create": (vp, []),
+        "backend_destroy": (None, [vp]),
+        "backend_get_allocated_memory": (sz, [vp]),
+        "backend_get_peak_allocated_memory": (sz, [vp]),
+        "backend_get_device_info": (None, [vp, vp]),
+        "backend_get_gpu_busy_ms": (d, [vp]),
+        "backend_get_command_buffers": (u64, [vp]),
+        "backend_reset_gpu_timing": (None, [vp]),
+        "backend_encode_wait_timed": (d, [vp]),
+        "backend_buffer_alloc": (vp, [vp, sz]),
+        "backend_buffer_free": (None, [vp]),
+        "backend_buffer_map": (vp, [vp]),
+        "backend_buffer_unmap": (None, [vp]),
+        "backend_buffer_size": (sz, [vp]),
+        "backend_kernel_create": (vp, [vp, C.c_char_p]),
+        "backend_kernel_destroy": (None, [vp]),
+        "backend_kernel_dispatch": (i, [vp, vp, vp, vp, i, i, i, i, i, i, i]),
+        "backend_synchronize": (None, [vp]),
+        "backend_encode_begin": (vp, [vp]),
+        "backend_encode_dispatch": (i, [vp, vp, vp, vp, i, i, i, i, i, i, i]),
+        "backend_encode_commit": (None, [vp]),
+        "backend_encode_wait": (None, [vp]),
+        "bm_synth_tensor_seed": (u64, [u64, i, i, i]),
+        "bm_synth_normal_f32": (None, [u64, C.c_float, vp, sz]),
+        "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L
+    return L
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [
+        ("max_threads_per_threadgroup", C.c_int),
+        ("max_threadgroup_memory", C.c_size_t),
+        ("max_buffer_bytes", C.c_size_t),
+        ("recommended_max_working_set", C.c_size_t),
+        ("has_unified_memory", C.c_int),
+    ]
+
+
+def _ptr(a: np.ndarray) -> C.c_void_p:
+    assert a.flags["C_CONTIGUOUS"]
+    return C.c_void_p(a.ctypes.data)
+
+
+# ---------------------------------------------------------------- synth
+
+def synth_seed(base: int, model_id: int, layer: int, matrix_id: int) -> int:
+    return int(lib().bm_synth_tensor_seed(base, model_id, layer, matrix_id))
+
+
+def synth_normal(seed: int, sigma: float, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    lib().bm_synth_normal_f32(seed, sigma, _ptr(out), n)
+    return out
+
+
+def synth_uniform_int(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.int32)
+    lib().bm_synth_uniform_int(seed, lo, hi, _ptr(out), n)
+    return out
+
+
+# ---------------------------------------------------------------- backend
+
+class Buffer:
+    def __init__(self, be: "Backend", nbytes: int):
+        self.be = be
+        self.nbytes = int(nbytes)
+        self.h = lib().backend_buffer_alloc(be.ctx, self.nbytes)
+        if not self.h:
+            raise BackendError(f"backend_buffer_alloc({nbytes}) failed")
+
+    def write(self, arr, offset: int = 0) -> "Buffer":
+        a = np.ascontiguousarray(arr)
+        nb = a.nbytes
+        if offset + nb > self.nbytes:
+            raise ValueError("write past end of buffer")
+        p = lib().backend_buffer_map(self.h)
+        if not p:
+            raise BackendError("backend_buffer_map failed")
+        C.memmove(p + offset, a.ctypes.data, nb)
+        lib().backend_buffer_unmap(self.h)
+        return self
+
+    def read(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        nb = count * dt.itemsize
+        if offset + nb > self.nbytes:
+            raise ValueError("read past end of buffer")
+        p = lib().backend_buffer_map(self.h)
+        if not p:
+            raise BackendError("backend_buffer_map failed")
+        out = np.empty(count, dtype=dt)
+        C.memmove(out.ctypes.data, p + offset, nb)
+        # read-only access: no unmap, so the shadow is not pushed back
+        return out
+
+    def free(self):
+        # after Backend.close() the context is gone and so is the memory
+        if self.h and self.be.ctx:
+            lib().backend_buffer_free(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Kernel:
+    def __init__(self, be: "Backend", name: str):
+        self.name = name
+        self.h = lib().backend_kernel_create(be.ctx, name.encode())
+        if not self.h:
+            raise BackendError(f"kernel not found: {name}")
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().backend_kernel_destroy(self.h)
+                self.h = None
+        except Exception:
+            pass
+
+
+def _buf_array(bufs, offsets):
+    n = len(bufs)
+    arr = (C.c_void_p * n)(*[b.h for b in bufs])
+    off = None
+    if offsets is not None:
+        off = (C.c_size_t * n)(*offsets)
+    return n, arr, off
+
+
+class Encoder:
+    def __init__(self, be: "Backend"):
+        self.be = be
+        self.h = lib().backend_encode_begin(be.ctx)
+        if not self.h:
+            raise BackendError("backend_encode_begin failed")
+
+    def dispatch(self, k: Kernel, bufs, grid, tg, offsets=None) -> int:
+        n, arr, off = _buf_array(bufs, offsets)
+        g = list(grid) + [1] * (3 - len(grid))
+        t = list(tg) + [1] * (3 - len(tg))
+        return lib().backend_encode_dispatch(self.h, k.h, arr, off, n, g[0], g[1], g[2], t[0], t[1], t[2])
+
+    def commit(self):
+        lib().backend_encode_commit(self.h)
+
+    def wait_timed(self) -> float:
+        ms = lib().backend_encode_wait_timed(self.h)
+        self.h = None
+        return ms
+
+
+class Backend:
+    def __init__(self):
+        self.ctx = lib().backend_create()
+        if not self.ctx:
+            raise BackendError("backend_create failed (no HIP device?)")
+        self._kernels = {}
+
+    def info(self) -> DeviceInfo:
+        di = DeviceInfo()
+        lib().backend_get_device_info(self.ctx, C.byref(di))
+        return di
+
+    def alloc(self, nbytes: int) -> Buffer:
+        return Buffer(self, nbytes)
+
+    def upload(self, arr) -> Buffer:
+        a = np.ascontiguousarray(arr)
+        return Buffer(self, max(a.nbytes, 4)).write(a)
+
+    def params(self, *vals, dtype=np.int32) -> Buffer:
+        return self.upload(np.array(vals, dtype=dtype))
+
+    def kernel(self, name: str) -> Kernel:
+        if name not in self._kernels:
+            self._kernels[name] = Kernel(self, name)
+        return self._kernels[name]
+
+    def dispatch(self, name: str, bufs, grid, tg, offsets=None) -> int:
+        """One synchronous dispatch (backend_kernel_dispatch)."""
+        k = self.kernel(name)
+        n, arr, off = _buf_array(bufs, offsets)
+        g = list(grid) + [1] * (3 - len(grid))
+        t = list(tg) + [1] * (3 - len(tg))
+        return lib().backend_kernel_dispatch(self.ctx, k.h, arr, off, n, g[0], g[1], g[2], t[0], t[1], t[2])
+
+    def encoder(self) -> Encoder:
+        return Encoder(self)
+
+    def synchronize(self):
+        lib().backend_synchronize(self.ctx)
+
+    def allocated(self) -> int:
+        return int(lib().backend_get_allocated_memory(self.ctx))
+
+    def close(self):
+        if self.ctx:
+            self._kernels.clear()
+            lib().backend_destroy(self.ctx)
+            self.ctx = None

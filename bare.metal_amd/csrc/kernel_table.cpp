@@ -1,0 +1,32 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * kernel_table.cpp — the named gfx950 kernels the HIP backend resolves in
+ * backend_kernel_create.  Names and buffer orders follow the reference's
+ * Metal kernels where one exists (cited per entry); the rest are MI355X
+ * additions whose buffer orders are documented in include/bm_q8.h.
+ *
+ * Columns: name, buffers bound, by-value buffer mask, written buffer mask.
+ */
+#include "bmk.h"
+
+extern "C" {
+int bmk_launch_quantize_q8(const bmk_launch_t* a);
+int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a);
+int bmk_launch_q8_matvec(const bmk_launch_t* a);
+int bmk_launch_q8_matmul(const bmk_launch_t* a);
+}
+
+#define B(i) (1u << (i))
+
+extern "C" const bmk_desc_t bmk_table[] = {
+    /* new: the host loop of reference quant.c:54-71 as a device kernel;
+     * {src f32, dst q8, params{n}} */
+    {"quantize_q8", 3, B(2), B(1), bmk_launch_quantize_q8},
+    /* new: reference quant.c:62-71 (bf16 source); {src bf16, dst q8, params{n}} */
+    {"quantize_q8_bf16", 3, B(2), B(1), bmk_launch_quantize_q8_bf16},
+    /* reference forward.metal:575-623; {inp, weight, bias, out, params{BT,C,OC,has_bias}} */
+    {"matmul_forward_q8_vec", 5, B(4), B(3), bmk_launch_q8_matvec},
+    /* reference forward.metal:625-649; same buffers */
+    {"matmul_forward_q8", 5, B(4), B(3), bmk_launch_q8_matmul},
+    {nullptr, 0, 0, 0, nullptr},
+};

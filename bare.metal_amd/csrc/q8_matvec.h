@@ -1,0 +1,41 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * q8_matvec.h — problem descriptors shared by the Q8 matvec kernels, their
+ * launchers and the engine's fused decode launches.
+ */
+#ifndef BMK_Q8_MATVEC_H
+#define BMK_Q8_MATVEC_H
+
+#include <hip/hip_runtime.h>
+
+#define MV_MAX_PROBS 8
+#define MV_U 4
+
+/* One y = W x (+ bias) problem; W is OC rows of nb 36-byte Q8 blocks. */
+typedef struct {
+    const unsigned char* w;
+    const float* x;
+    float* y;
+    const float* bias; /* NULL: no bias */
+    int OC;
+    int nb;            /* C / 32 */
+    int tiles;         /* row tiles (filled by the launcher) */
+    int pad_;
+} MvProb;
+
+typedef struct {
+    MvProb p[MV_MAX_PROBS];
+    int nprob;
+} MvGroup;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+int mv_tiles_for(int OC, int C, int U);
+int mv_launch_group(MvGroup* g, hipStream_t s);
+int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_map, int n_tiles, hipStream_t s);
+#ifdef __cplusplus
+}
+#endif
+
+#endif

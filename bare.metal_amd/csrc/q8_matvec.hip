@@ -1,0 +1,271 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * q8_matvec.hip — decode-time Q8_0 dequant matrix-vector products on gfx950.
+ *
+ *   y[r] = sum_b scale[r,b] * sum_{j<32} q[r,b,j] * x[32b+j]   (+ bias[r])
+ *
+ * Reference semantics: matmul_forward_q8_vec (src/kernels/forward.metal:575-623)
+ * for BT == 1 and matmul_forward_q8 (forward.metal:625-649) for BT > 1, with
+ * the buffer order {inp, weight, bias, out, params{BT,C,OC,has_bias}}
+ * (reference scheduler.c:794-799,840-847).  The weights stay in the
+ * reference's array-of-structs layout: row r is C/32 consecutive 36-byte
+ * blocks {f32 scale; int8 q[32]} (reference quant.h:17-32).
+ *
+ * gfx950 mapping (one workgroup = 256 lanes = 4 waves):
+ *   - lane t owns block column b = t % nb of row slot t / nb, with
+ *     nb = C/32 <= 256, so 256/nb rows are in flight per pass and every
+ *     lane keeps the 32 activations of its column in registers for all rows;
+ *   - a lane reads its 36-byte block with one dwordx4 + dwordx4 + dword load;
+ *     consecutive lanes read consecutive blocks, so a wave streams ~2.3 KB of
+ *     contiguous weight bytes per row pass;
+ *   - U passes are issued before any arithmetic (U*36 bytes in flight per
+ *     lane) to cover HBM latency;
+ *   - the nb per-block partials of a row meet in LDS and one lane per row
+ *     adds them in block order (deterministic, no atomics).
+ * Rows are split into tiles of (256/nb)*U rows; a launch may cover up to
+ * MV_MAX_PROBS independent problems (used to fuse q/k/v and gate/up), or an
+ * arbitrary list of problems described in device memory.
+ * HBM roofline: 1.125 bytes per weight + 4 bytes per x and y element.
+ */
+#include "bmk.h"
+#include "q8_matvec.h"
+
+namespace {
+
+constexpr int MV_THREADS = 256;
+
+struct Blk {
+    float s;
+    uint4 q0, q1;
+};
+
+__device__ __forceinline__ Blk load_block(const unsigned char* p) {
+    Blk b;
+    unsigned char raw[36];
+    __builtin_memcpy(raw, __builtin_assume_aligned(p, 4), 36);
+    __builtin_memcpy(&b.s, raw, 4);
+    __builtin_memcpy(&b.q0, raw + 4, 16);
+    __builtin_memcpy(&b.q1, raw + 20, 16);
+    return b;
+}
+
+__device__ __forceinline__ float dot4(unsigned int w, const float* x) {
+    float a = x[0] * (float)(signed char)(w & 0xffu);
+    a = fmaf(x[1], (float)(signed char)((w >> 8) & 0xffu), a);
+    a = fmaf(x[2], (float)(signed char)((w >> 16) & 0xffu), a);
+    a = fmaf(x[3], (float)(signed char)(w >> 24), a);
+    return a;
+}
+
+__device__ __forceinline__ float block_dot(const Blk& b, const float* xs) {
+    float s0 = dot4(b.q0.x, xs + 0) + dot4(b.q0.y, xs + 4);
+    float s1 = dot4(b.q0.z, xs + 8) + dot4(b.q0.w, xs + 12);
+    float s2 = dot4(b.q1.x, xs + 16) + dot4(b.q1.y, xs + 20);
+    float s3 = dot4(b.q1.z, xs + 24) + dot4(b.q1.w, xs + 28);
+    return ((s0 + s1) + (s2 + s3)) * b.s;
+}
+
+/* One row tile of one problem.  Requires nb <= MV_THREADS. */
+template <int U>
+__device__ __forceinline__ void mv_tile(const MvProb& p, int tile, float* red) {
+    const int nb = p.nb;
+    const int slots = MV_THREADS / nb;
+    const int rows_per_tile = slots * U;
+    const int t = threadIdx.x;
+    const int slot = t / nb;
+    const int b = t - slot * nb;
+    const bool lane_on = slot < slots;
+    const long row0 = (long)tile * rows_per_tile;
+    const size_t row_bytes = (size_t)nb * 36;
+
+    float xs[32];
+    if (lane_on) {
+        const float* xp = p.x + 32 * b;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 v;
+            __builtin_memcpy(&v, __builtin_assume_aligned(xp + 4 * i, 4), 16);
+            xs[4 * i + 0] = v.x; xs[4 * i + 1] = v.y; xs[4 * i + 2] = v.z; xs[4 * i + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) xs[i] = 0.0f;
+    }
+
+    Blk blk[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const long r = row0 + slot + (long)u * slots;
+        if (lane_on && r < p.OC) {
+            blk[u] = load_block(p.w + (size_t)r * row_bytes + (size_t)b * 36);
+        } else {
+            blk[u].s = 0.0f;
+            blk[u].q0 = make_uint4(0, 0, 0, 0);
+            blk[u].q1 = make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (lane_on) red[(slot + u * slots) * nb + b] = block_dot(blk[u], xs);
+    }
+    __syncthreads();
+    for (int rl = t; rl < rows_per_tile; rl += MV_THREADS) {
+        const long r = row0 + rl;
+        if (r < p.OC) {
+            const float* rp = red + rl * nb;
+            float acc = 0.0f;
+            for (int k = 0; k < nb; k++) acc += rp[k];
+            if (p.bias) acc += p.bias[r];
+            p.y[r] = acc;
+        }
+    }
+}
+
+/* Rows longer than MV_THREADS blocks: the workgroup walks one row at a time. */
+__device__ __forceinline__ void mv_row_wide(const MvProb& p, long r, float* red) {
+    const int t = threadIdx.x;
+    const unsigned char* wr = p.w + (size_t)r * p.nb * 36;
+    float acc = 0.0f;
+    for (int b = t; b < p.nb; b += MV_THREADS) {
+        float xs[32];
+        const float* xp = p.x + 32 * b;
+#pragma unroll
+        for (int i = 0; i < 32; i++) xs[i] = xp[i];
+        acc += block_dot(load_block(wr + (size_t)b * 36), xs);
+    }
+    red[t] = acc;
+    __syncthreads();
+    if (t == 0) {
+        float s = 0.0f;
+        for (int k = 0; k < MV_THREADS; k++) s += red[k];
+        if (p.bias) s += p.bias[r];
+        p.y[r] = s;
+    }
+    __syncthreads();
+}
+
+template <int U>
+__device__ __forceinline__ void mv_dispatch(const MvProb& p, int tile, float* red) {
+    if (p.nb <= MV_THREADS) {
+        mv_tile<U>(p, tile, red);
+    } else {
+        mv_row_wide(p, tile, red);
+    }
+}
+
+/* Up to MV_MAX_PROBS problems passed by value. */
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q8_matvec(MvGroup g) {
+    __shared__ float red[MV_THREADS * U];
+    int tile = blockIdx.x;
+    int i = 0;
+    while (i + 1 < g.nprob && tile >= g.p[i].tiles) {
+        tile -= g.p[i].tiles;
+        i++;
+    }
+    mv_dispatch<U>(g.p[i], tile, red);
+}
+
+/* Any number of problems; tile_map[blockIdx.x] = (problem << 20) | tile. */
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_list(const MvProb* __restrict__ probs,
+                                                               const unsigned int* __restrict__ tile_map) {
+    __shared__ float red[MV_THREADS * U];
+    const unsigned int m = tile_map[blockIdx.x];
+    const MvProb p = probs[m >> 20];
+    mv_dispatch<U>(p, (int)(m & 0xfffffu), red);
+}
+
+} // namespace
+
+/* ------------------------------------------------------------------ */
+
+extern "C" int mv_tiles_for(int OC, int C, int U) {
+    const int nb = C / 32;
+    if (nb > MV_THREADS) return OC;
+    const int rows = (MV_THREADS / nb) * U;
+    return (OC + rows - 1) / rows;
+}
+
+extern "C" int mv_launch_group(MvGroup* g, hipStream_t s) {
+    long total = 0;
+    for (int i = 0; i < g->nprob; i++) {
+        g->p[i].tiles = mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, MV_U);
+        total += g->p[i].tiles;
+    }
+    if (total <= 0) return 0;
+    hipLaunchKernelGGL(k_q8_matvec<MV_U>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
+    if (n_tiles <= 0) return 0;
+    hipLaunchKernelGGL(k_q8_matvec_list<MV_U>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, d_probs,
+                       d_tile_map);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* matmul_forward_q8_vec / matmul_forward_q8 with BT below the GEMM cut-over:
+ * buffers {inp f32 [BT][C], weight q8 [OC][C/32], bias f32 [OC], out f32 [BT][OC],
+ * params int {BT, C, OC, has_bias}}.  The Metal grid (OC*128 or OC rounded to
+ * 32, BT) is not needed: the launch shape follows from the parameters. */
+extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 4, 16, "params");
+    const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);
+    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0 && C % 32 == 0, "q8 matvec: bad shape BT=%d C=%d OC=%d", BT, C, OC);
+    if (BT == 0 || OC == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
+    BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * 36, "weight");
+    if (has_bias) BMK_NEED_BYTES(a, 2, (size_t)OC * 4, "bias");
+    BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0,
+                "q8 matvec: misaligned buffer offset");
+    for (int bt = 0; bt < BT; bt += MV_MAX_PROBS) {
+        MvGroup g;
+        g.nprob = BT - bt < MV_MAX_PROBS ? BT - bt : MV_MAX_PROBS;
+        for (int i = 0; i < g.nprob; i++) {
+            MvProb& p = g.p[i];
+            p.w = (const unsigned char*)a->dev[1];
+            p.x = (const float*)a->dev[0] + (size_t)(bt + i) * C;
+            p.y = (float*)a->dev[3] + (size_t)(bt + i) * OC;
+            p.bias = has_bias ? (const float*)a->dev[2] : nullptr;
+            p.OC = OC;
+            p.nb = C / 32;
+            p.tiles = 0;
+        }
+        if (mv_launch_group(&g, a->stream) != 0) return -1;
+    }
+    return 0;
+}
+
+/* matmul_forward_q8 (reference forward.metal:625-649): BT rows of activations.
+ * BT below GEMM_MIN_BT streams the weights through the fp32 matvec once per
+ * row; larger BT goes to the bf16-MFMA GEMM (q8_gemm.hip). */
+#include "q8_gemm.h"
+#define GEMM_MIN_BT 16
+extern "C" int bmk_launch_q8_matmul(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 4, 16, "params");
+    const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);
+    if (BT < GEMM_MIN_BT || has_bias) return bmk_launch_q8_matvec(a);
+    BMK_REQUIRE(OC >= 0 && C > 0 && C % 32 == 0, "q8 matmul: bad shape BT=%d C=%d OC=%d", BT, C, OC);
+    if (OC == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
+    BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * 36, "weight");
+    BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0,
+                "q8 matmul: misaligned buffer offset");
+    GmGroup g;
+    g.nprob = 1;
+    g.p[0].A = (const float*)a->dev[0];
+    g.p[0].W = (const unsigned char*)a->dev[1];
+    g.p[0].C = (float*)a->dev[3];
+    g.p[0].M = BT;
+    g.p[0].N = OC;
+    g.p[0].K = C;
+    g.p[0].lda = C;
+    g.p[0].ldc = OC;
+    g.p[0].tiles = 0;
+    return gm_launch_group(&g, a->stream);
+}

@@ -1,0 +1,122 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * q8_pack.hip — fp32/bf16 -> Q8_0 block quantize/pack on gfx950.
+ *
+ * Output format (reference src/baremetal/quant.h:17-32): an array of 36-byte
+ * blocks {float scale; int8 q[32]}, block b covering source elements
+ * 32b..32b+31.  Per block (reference src/baremetal/quant.c:10-29):
+ *   amax  = max |p_i|   (strict '>' from 0, so NaN elements never win)
+ *   scale = amax / 127.0f              (IEEE division, round to nearest)
+ *   scale == 0  ->  every q_i = 0, stored scale = +0
+ *   inv   = 1.0f / scale                (IEEE division)
+ *   q_i   = clamp((int)lroundf(p_i * inv), -128, 127)
+ * lroundf rounds half away from zero.  For finite blocks |p_i * inv| never
+ * exceeds 127.0001, so the clamp never fires; p_i * inv is NaN or infinite
+ * only when the block holds an Inf or when 1/scale overflows (scale below
+ * 2^-128), and there x86-64's lroundf returns LONG_MIN, whose int conversion
+ * is 0 — the value used here.
+ *
+ * The hardware division on this path is correctly rounded: the file is built
+ * without fast-math, so '/' lowers to the v_div_scale/v_div_fmas/v_div_fixup
+ * sequence, and fp32 denormals are kept.
+ *
+ * Mapping: 8 lanes per block, each lane owns 4 consecutive elements (one
+ * 16-byte load), so a wave reads 1 KiB of contiguous source and writes 288
+ * contiguous bytes of blocks.  The block max is a 3-step xor shuffle inside
+ * the 8-lane group.  HBM-bound: 4 (or 2) + 1.125 bytes per element.
+ */
+#include "bmk.h"
+
+namespace {
+
+__device__ __forceinline__ int q8_round_clamp(float y) {
+    /* NaN or infinite -> 0 (see header). */
+    if (!(fabsf(y) <= 3.402823466e38f)) return 0;
+    float t = truncf(y);
+    if (fabsf(y - t) >= 0.5f) t += copysignf(1.0f, y); /* y - t is exact */
+    t = fminf(fmaxf(t, -128.0f), 127.0f);
+    return (int)t;
+}
+
+template <bool SRC_BF16>
+__device__ __forceinline__ void load4(const void* src, long e, float v[4]) {
+    if (SRC_BF16) {
+        const unsigned short* s = (const unsigned short*)src + e;
+        uint2 raw;
+        __builtin_memcpy(&raw, __builtin_assume_aligned(s, 8), 8);
+        v[0] = __uint_as_float(raw.x << 16);
+        v[1] = __uint_as_float(raw.x & 0xffff0000u);
+        v[2] = __uint_as_float(raw.y << 16);
+        v[3] = __uint_as_float(raw.y & 0xffff0000u);
+    } else {
+        const float* s = (const float*)src + e;
+        float4 raw;
+        __builtin_memcpy(&raw, __builtin_assume_aligned(s, 4), 16);
+        v[0] = raw.x; v[1] = raw.y; v[2] = raw.z; v[3] = raw.w;
+    }
+}
+
+template <bool SRC_BF16>
+__global__ __launch_bounds__(256) void k_quantize_q8(const void* __restrict__ src, unsigned char* __restrict__ dst,
+                                                     long nblocks) {
+    const long gt = (long)blockIdx.x * 256 + threadIdx.x;
+    const long blk = gt >> 3;
+    const int j = threadIdx.x & 7;
+    const bool active = blk < nblocks;
+
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (active) load4<SRC_BF16>(src, blk * 32 + 4 * j, v);
+
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = fabsf(v[i]);
+        m = (a > m) ? a : m;
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        float o = __shfl_xor(m, off, 8);
+        m = (o > m) ? o : m;
+    }
+
+    const float scale = m / 127.0f;
+    unsigned int packed = 0u;
+    if (scale != 0.0f) {
+        const float inv = 1.0f / scale;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int q = q8_round_clamp(v[i] * inv);
+            packed |= ((unsigned int)q & 0xffu) << (8 * i);
+        }
+    }
+    if (active) {
+        unsigned char* b = dst + blk * 36;
+        unsigned int* bw = (unsigned int*)__builtin_assume_aligned(b, 4);
+        bw[1 + j] = packed;
+        if (j == 0) bw[0] = __float_as_uint(scale);
+    }
+}
+
+template <bool SRC_BF16>
+int launch_quantize(const bmk_launch_t* a) {
+    /* buffers: [0] src (fp32 or bf16), [1] dst q8 blocks, [2] params {n} */
+    BMK_NEED_BYTES(a, 2, 4, "params");
+    const long n = (long)(unsigned int)bmk_pi(a, 2, 0);
+    BMK_REQUIRE(n > 0 && n % 32 == 0, "quantize_q8: n=%ld must be a positive multiple of 32", n);
+    const long nblocks = n / 32;
+    BMK_NEED_BYTES(a, 0, n * (SRC_BF16 ? 2 : 4), "src");
+    BMK_NEED_BYTES(a, 1, nblocks * 36, "dst");
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & (SRC_BF16 ? 7 : 3)) == 0 && ((uintptr_t)a->dev[1] & 3) == 0,
+                "quantize_q8: misaligned src/dst offset");
+    const long threads = nblocks * 8;
+    const unsigned grid = (unsigned)((threads + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q8<SRC_BF16>, dim3(grid), dim3(256), 0, a->stream, (const void*)a->dev[0],
+                       (unsigned char*)a->dev[1], nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+} // namespace
+
+extern "C" int bmk_launch_quantize_q8(const bmk_launch_t* a) { return launch_quantize<false>(a); }
+extern "C" int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a) { return launch_quantize<true>(a); }

@@ -1,0 +1,45 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * decode_oracle.h — CPU restatement of the reference's decode step (test
+ * infrastructure only; see decode_oracle.c).
+ */
+#ifndef BM_DECODE_ORACLE_H
+#define BM_DECODE_ORACLE_H
+
+#include <stdint.h>
+
+/* Weights as the reference lays them out (model.c:125-172): per matrix
+ * type, all layers back to back; Q8 matrices as 36-byte blocks, rows of
+ * C/32 blocks. */
+typedef struct {
+    int D, H, NH, NKV, HD, L, V, MS;
+    float theta, eps;
+    const float* emb;        /* [V][D] fp32, also the tied LM head */
+    const float* ln1;        /* [L][D] */
+    const float* ln2;        /* [L][D] */
+    const float* lnf;        /* [D] */
+    const uint8_t* wq;       /* [L][NH*HD][D/32] */
+    const uint8_t* wk;       /* [L][KV][D/32] */
+    const uint8_t* wv;       /* [L][KV][D/32] */
+    const uint8_t* wo;       /* [L][D][NH*HD/32] */
+    const uint8_t* wg;       /* [L][H][D/32] */
+    const uint8_t* wu;       /* [L][H][D/32] */
+    const uint8_t* wd;       /* [L][D][H/32] */
+    const uint8_t* head_q8;  /* NULL: fp32 tied head (the reference's Q8 mode) */
+} orc_model_t;
+
+typedef struct orc_decoder_s orc_decoder_t;
+
+orc_decoder_t* orc_decoder_create(const orc_model_t* m, int nthreads);
+void orc_decoder_destroy(orc_decoder_t* d);
+/* One token at position pos; writes V logits.  Returns 0 or -1. */
+int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits);
+int orc_argmax_first(const double* v, int n, double* top1, double* top2);
+/* Greedy run in the reference's driver order (tools/run.c:121-185): step
+ * prompt tokens, then the previous pick (or forced[] when non-NULL, for
+ * teacher forcing).  Emits steps-n_prompt+1 tokens and their top-2 margins;
+ * returns the count or -1. */
+int orc_generate(orc_decoder_t* d, const int* prompt, int n_prompt, int steps, const int* forced, int* out_tokens,
+                 double* out_margin);
+
+#endif

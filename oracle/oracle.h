@@ -1,0 +1,25 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * oracle.h — CPU restatement of the reference's Q8 path (test
+ * infrastructure only; see oracle.c).
+ */
+#ifndef BM_ORACLE_H
+#define BM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+size_t   orc_quantize_q8(const float* src, uint8_t* dst, size_t n);
+size_t   orc_quantize_q8_bf16(const uint16_t* src, uint8_t* dst, size_t n);
+uint16_t orc_bf16_rne(float f);
+void     orc_bf16_round_array(const float* src, float* dst, size_t n);
+void     orc_q8_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int C, int OC);
+void     orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N);
+
+/* CPU baseline (cpu_baseline.c): fp32 Q8 matvec in the reference's
+ * arithmetic, SIMD + OpenMP over rows. */
+void     orc_cpu_q8_matvec_f32(const uint8_t* w, const float* x, float* y, int C, int OC, int nthreads);
+int      orc_cpu_max_threads(void);
+const char* orc_cpu_isa(void);
+
+#endif

@@ -1,0 +1,192 @@
+# SPDX-License-Identifier: MPL-2.0
+"""ctypes binding of oracle/liboracle.so and oracle/_ref/libref_quant.so.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libref_quant.so")
+
+_o = None
+_r = None
+
+
+def _p(a):
+    return C.c_void_p(a.ctypes.data)
+
+
+def oracle() -> C.CDLL:
+    global _o
+    if _o is None:
+        if not os.path.exists(ORACLE_PATH):
+            raise RuntimeError(f"{ORACLE_PATH} not built (make -C oracle)")
+        L = C.CDLL(ORACLE_PATH)
+        vp, sz, i = C.c_void_p, C.c_size_t, C.c_int
+        L.orc_quantize_q8.restype = sz
+        L.orc_quantize_q8.argtypes = [vp, vp, sz]
+        L.orc_quantize_q8_bf16.restype = sz
+        L.orc_quantize_q8_bf16.argtypes = [vp, vp, sz]
+        L.orc_bf16_rne.restype = C.c_uint16
+        L.orc_bf16_rne.argtypes = [C.c_float]
+        L.orc_bf16_round_array.argtypes = [vp, vp, sz]
+        L.orc_q8_matvec_f64.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_q8_gemm_bf16_f64.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_cpu_q8_matvec_f32.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_cpu_max_threads.restype = i
+        L.orc_cpu_isa.restype = C.c_char_p
+        L.orc_decoder_create.restype = vp
+        L.orc_decoder_create.argtypes = [vp, i]
+        L.orc_decoder_destroy.argtypes = [vp]
+        L.orc_decoder_step.restype = i
+        L.orc_decoder_step.argtypes = [vp, i, i, vp]
+        L.orc_generate.restype = i
+        L.orc_generate.argtypes = [vp, vp, i, i, vp, vp, vp]
+        _o = L
+    return _o
+
+
+def ref_quant():
+    """The reference's own quant.c built by oracle/Makefile (None if absent)."""
+    global _r
+    if _r is None:
+        if not os.path.exists(REF_PATH):
+            return None
+        L = C.CDLL(REF_PATH)
+        L.bmt_quantize_q8.restype = C.c_size_t
+        L.bmt_quantize_q8.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        L.bmt_quantize_q8_bf16.restype = C.c_size_t
+        L.bmt_quantize_q8_bf16.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        _r = L
+    return _r
+
+
+# ---------------------------------------------------------------- helpers
+
+def quantize_q8(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.zeros(src.size // 32 * 36, dtype=np.uint8)
+    n = oracle().orc_quantize_q8(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def quantize_q8_bf16(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint16)
+    out = np.zeros(src.size // 32 * 36, dtype=np.uint8)
+    n = oracle().orc_quantize_q8_bf16(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def ref_quantize_q8(src: np.ndarray):
+    L = ref_quant()
+    if L is None:
+        return None
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.zeros(src.size // 32 * 36, dtype=np.uint8)
+    n = L.bmt_quantize_q8(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def ref_quantize_q8_bf16(src: np.ndarray):
+    L = ref_quant()
+    if L is None:
+        return None
+    src = np.ascontiguousarray(src, dtype=np.uint16)
+    out = np.zeros(src.size // 32 * 36, dtype=np.uint8)
+    n = L.bmt_quantize_q8_bf16(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def q8_matvec_f64(w: np.ndarray, x: np.ndarray, BT: int, C_: int, OC: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros(BT * OC, dtype=np.float64)
+    oracle().orc_q8_matvec_f64(_p(w), _p(x), _p(y), BT, C_, OC)
+    return y
+
+
+def q8_gemm_bf16_f64(w: np.ndarray, a: np.ndarray, M: int, K: int, N: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    c = np.zeros(M * N, dtype=np.float64)
+    oracle().orc_q8_gemm_bf16_f64(_p(w), _p(a), _p(c), M, K, N)
+    return c
+
+
+def bf16_rne(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty_like(a)
+    oracle().orc_bf16_round_array(_p(a), _p(out), a.size)
+    return out
+
+
+def cpu_q8_matvec_f32(w: np.ndarray, x: np.ndarray, C_: int, OC: int, nthreads: int) -> np.ndarray:
+    y = np.zeros(OC, dtype=np.float32)
+    oracle().orc_cpu_q8_matvec_f32(_p(w), _p(x), _p(y), C_, OC, nthreads)
+    return y
+
+
+# ---------------------------------------------------------------- decode oracle
+
+class OrcModel(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("D", "H", "NH", "NKV", "HD", "L", "V", "MS")] + [
+        ("theta", C.c_float), ("eps", C.c_float),
+    ] + [(n, C.c_void_p) for n in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8")]
+
+
+class Decoder:
+    """Keeps the numpy arrays alive for as long as the C decoder uses them."""
+
+    def __init__(self, dims: dict, arrays: dict, nthreads: int = 8):
+        self._keep = dict(arrays)
+        m = OrcModel()
+        for k in ("D", "H", "NH", "NKV", "HD", "L", "V", "MS"):
+            setattr(m, k, int(dims[k]))
+        m.theta = float(dims.get("theta", 10000.0))
+        m.eps = float(dims.get("eps", 1e-5))
+        for k in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8"):
+            a = arrays.get(k)
+            setattr(m, k, a.ctypes.data if a is not None else None)
+        self._m = m
+        self.V = int(dims["V"])
+        self.h = oracle().orc_decoder_create(C.byref(m), nthreads)
+        if not self.h:
+            raise MemoryError("orc_decoder_create failed")
+
+    def step(self, token: int, pos: int) -> np.ndarray:
+        out = np.zeros(self.V, dtype=np.float64)
+        if oracle().orc_decoder_step(self.h, token, pos, _p(out)) != 0:
+            raise ValueError("orc_decoder_step rejected its input")
+        return out
+
+    def generate(self, prompt, steps: int, forced=None):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        n_out = steps - len(prompt) + 1
+        toks = np.zeros(max(n_out, 1), dtype=np.int32)
+        marg = np.zeros(max(n_out, 1), dtype=np.float64)
+        f = None
+        if forced is not None:
+            f = np.ascontiguousarray(forced, dtype=np.int32)
+        n = oracle().orc_generate(self.h, _p(prompt), len(prompt), steps,
+                                  _p(f) if f is not None else None, _p(toks), _p(marg))
+        if n < 0:
+            raise ValueError("orc_generate failed")
+        return toks[:n], marg[:n]
+
+    def close(self):
+        if self.h:
+            oracle().orc_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

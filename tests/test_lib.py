@@ -1,0 +1,66 @@
+# SPDX-License-Identifier: MPL-2.0
+"""The C-ABI library loads and exports every function include/*.h declares
+(no GPU calls)."""
+import ctypes
+import glob
+import os
+import re
+
+import bmhip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+DECL = re.compile(r"^\s*(?:[A-Za-z_][\w\s\*]*?[\s\*])([A-Za-z_]\w*)\s*\(", re.M)
+
+
+def declared_functions():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        src = open(h).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        src = re.sub(r"//[^\n]*", "", src)
+        for line in src.split(";"):
+            line = line.strip()
+            if not line or line.startswith("#") or "typedef" in line or "{" in line or "static" in line:
+                continue
+            m = DECL.search(line)
+            if m and m.group(1) not in ("if", "for", "while", "return", "sizeof"):
+                names.add(m.group(1))
+    return sorted(names)
+
+
+def test_every_declared_symbol_is_exported():
+    lib = bmhip.lib()
+    names = declared_functions()
+    assert "backend_create" in names and "backend_encode_wait_timed" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_backend_abi_is_complete():
+    """The 22 functions of the reference's backend interface (backend.h:17-67)."""
+    want = """backend_create backend_destroy backend_get_allocated_memory
+    backend_get_peak_allocated_memory backend_get_device_info backend_get_gpu_busy_ms
+    backend_get_command_buffers backend_reset_gpu_timing backend_encode_wait_timed
+    backend_buffer_alloc backend_buffer_free backend_buffer_map backend_buffer_unmap
+    backend_buffer_size backend_kernel_create backend_kernel_destroy backend_kernel_dispatch
+    backend_synchronize backend_encode_begin backend_encode_dispatch backend_encode_commit
+    backend_encode_wait""".split()
+    assert len(want) == 22
+    lib = bmhip.lib()
+    for n in want:
+        assert hasattr(lib, n), n
+
+
+def test_null_handles_are_safe():
+    """*_free/destroy(NULL) are no-ops and NULL encoders/kernels are rejected
+    (reference device.m:144-159,182-191; dispatch.m:56,110)."""
+    L = bmhip.lib()
+    L.backend_buffer_free(None)
+    L.backend_kernel_destroy(None)
+    L.backend_destroy(None)
+    assert L.backend_buffer_map(None) is None
+    assert L.backend_buffer_size(None) == 0
+    assert L.backend_encode_dispatch(None, None, None, None, 0, 1, 1, 1, 1, 1, 1) == -1
+    assert L.backend_kernel_dispatch(None, None, None, None, 0, 1, 1, 1, 1, 1, 1) == -1
+    assert L.backend_kernel_create(None, b"quantize_q8") is None
+    assert L.backend_get_gpu_busy_ms(None) == 0.0

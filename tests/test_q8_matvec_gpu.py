@@ -1,0 +1,92 @@
+# SPDX-License-Identifier: MPL-2.0
+"""matmul_forward_q8_vec / matmul_forward_q8 (BT < 16) on the GPU vs the
+fp64 oracle.  Tolerance: normwise max|y-r|/max|r| <= 1e-3 (fp32 accumulate);
+integer-exact inputs must match bit for bit."""
+import numpy as np
+import pytest
+
+import bmhip
+import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+RTOL = 1e-3
+
+
+def run_mv(be, w, x, BT, C, OC, kernel="matmul_forward_q8_vec", bias=None):
+    bw = be.upload(w)
+    bx = be.upload(x)
+    bb = be.upload(bias if bias is not None else np.zeros(max(OC, 1), np.float32))
+    by = be.alloc(max(BT * OC * 4, 4))
+    p = be.params(BT, C, OC, 1 if bias is not None else 0)
+    grid = (OC * 128, BT) if kernel.endswith("_vec") else ((OC + 31) & ~31, BT)
+    tg = (128,) if kernel.endswith("_vec") else (32,)
+    assert be.dispatch(kernel, [bx, bw, bb, by, p], grid, tg) == 0
+    return by.read(np.float32, BT * OC)
+
+
+def normwise(y, r):
+    return np.abs(y - r).max() / max(np.abs(r).max(), 1e-30)
+
+
+SHAPES = [  # (OC, C): configs 1-3 plus edge cases
+    (1536, 576), (576, 576), (192, 576), (576, 1536),
+    (960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960),
+    (1, 32), (7, 64), (1000, 8192), (3, 8224),
+]
+
+
+@pytest.mark.parametrize("OC,C", SHAPES)
+def test_matvec_shapes(be, OC, C):
+    w = po.quantize_q8(bmhip.synth_normal(bmhip.synth_seed(7, 1, OC, C), 0.02, OC * C))
+    x = bmhip.synth_normal(bmhip.synth_seed(7, 2, OC, C), 1.0, C)
+    y = run_mv(be, w, x, 1, C, OC)
+    r = po.q8_matvec_f64(w, x, 1, C, OC)
+    assert normwise(y, r) <= RTOL, normwise(y, r)
+
+
+def test_matvec_integer_exact_bitwise(be):
+    rng = np.random.default_rng(1)
+    OC, C = 777, 576
+    nb = C // 32
+    blk = np.zeros((OC * nb, 36), np.uint8)
+    blk[:, :4] = (2.0 ** rng.integers(-3, 3, OC * nb)).astype(np.float32).view(np.uint8).reshape(-1, 4)
+    blk[:, 4:] = rng.integers(-128, 128, (OC * nb, 32)).astype(np.int8).view(np.uint8)
+    w = blk.ravel()
+    x = rng.integers(-4, 5, C).astype(np.float32)
+    y = run_mv(be, w, x, 1, C, OC)
+    r = po.q8_matvec_f64(w, x, 1, C, OC)
+    assert np.array_equal(y.astype(np.float64), r)
+
+
+def test_matvec_bias(be):
+    OC, C = 300, 576
+    w = po.quantize_q8(bmhip.synth_normal(11, 0.02, OC * C))
+    x = bmhip.synth_normal(12, 1.0, C)
+    b = bmhip.synth_normal(13, 1.0, OC)
+    y = run_mv(be, w, x, 1, C, OC, bias=b)
+    r = po.q8_matvec_f64(w, x, 1, C, OC) + b
+    assert normwise(y, r) <= RTOL
+
+
+@pytest.mark.parametrize("BT", [2, 8, 15])
+def test_matmul_small_batch(be, BT):
+    OC, C = 960, 960
+    w = po.quantize_q8(bmhip.synth_normal(21, 0.02, OC * C))
+    x = bmhip.synth_normal(22, 1.0, BT * C)
+    y = run_mv(be, w, x, BT, C, OC, kernel="matmul_forward_q8")
+    r = po.q8_matvec_f64(w, x, BT, C, OC)
+    assert normwise(y, r) <= RTOL
+
+
+def test_matvec_rejects_short_buffers(be):
+    OC, C = 64, 576
+    w = po.quantize_q8(bmhip.synth_normal(31, 0.02, OC * C))
+    bx = be.upload(np.ones(C, np.float32))
+    bw = be.upload(w[:-36])  # one block short
+    by = be.alloc(OC * 4)
+    rc = be.dispatch("matmul_forward_q8_vec", [bx, bw, be.alloc(OC * 4), by, be.params(1, C, OC, 0)],
+                     (OC * 128, 1), (128,))
+    assert rc == -1
+    rc = be.dispatch("matmul_forward_q8_vec", [bx, be.upload(w), be.alloc(OC * 4), by, be.params(1, 48, OC, 0)],
+                     (OC * 128, 1), (128,))
+    assert rc == -1  # C not a multiple of 32

@@ -1,0 +1,69 @@
+# SPDX-License-Identifier: MPL-2.0
+"""quantize_q8 / quantize_q8_bf16 on the GPU vs the oracle: bit-exact."""
+import os
+
+import numpy as np
+import pytest
+
+import bmhip
+import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "q8_pack_golden.npz")
+
+
+def gpu_pack(be, x: np.ndarray, bf16=False) -> np.ndarray:
+    n = x.size
+    src = be.upload(x)
+    dst = be.alloc(max(n // 32 * 36, 4))
+    rc = be.dispatch("quantize_q8_bf16" if bf16 else "quantize_q8", [src, dst, be.params(n)], (n // 4,), (256,))
+    assert rc == 0
+    return dst.read(np.uint8, n // 32 * 36)
+
+
+@pytest.mark.parametrize("case", ["special", "normal002", "normal1", "wide", "ties"])
+def test_pack_golden(be, case):
+    g = np.load(GOLDEN)
+    assert np.array_equal(gpu_pack(be, g[case + "_in"]), g[case + "_q8"])
+
+
+def test_pack_golden_bf16(be):
+    g = np.load(GOLDEN)
+    assert np.array_equal(gpu_pack(be, g["bf16_in"], bf16=True), g["bf16_q8"])
+
+
+@pytest.mark.parametrize("rows,cols", [(1536, 576), (576, 1536), (960, 960), (49152, 576), (1, 32), (3, 96)])
+def test_pack_config_shapes(be, rows, cols):
+    seed = bmhip.synth_seed(99, 0, rows, cols)
+    x = bmhip.synth_normal(seed, 0.02, rows * cols)
+    assert np.array_equal(gpu_pack(be, x), po.quantize_q8(x))
+
+
+def test_pack_wide_range_and_specials(be):
+    rng = np.random.default_rng(5)
+    n = 32 * 65536
+    x = (np.exp(rng.uniform(-90, 88, n)) * rng.choice([-1, 1], n)).astype(np.float32)
+    idx = rng.integers(0, n, 256)
+    x[idx[:64]] = np.nan
+    x[idx[64:96]] = np.inf
+    x[idx[96:128]] = -0.0
+    x[idx[128:]] = np.float32(3e-41)
+    assert np.array_equal(gpu_pack(be, x), po.quantize_q8(x))
+
+
+def test_pack_bf16_random(be):
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal(32 * 40000) * 0.02).astype(np.float32)
+    hb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(gpu_pack(be, hb, bf16=True), po.quantize_q8_bf16(hb))
+
+
+def test_pack_rejects_bad_lengths(be):
+    """n % 32 != 0 or n == 0: rejected before launch (reference quant.c:55 returns 0)."""
+    src = be.upload(np.ones(64, np.float32))
+    dst = be.alloc(72)
+    assert be.dispatch("quantize_q8", [src, dst, be.params(33)], (8,), (256,)) == -1
+    assert be.dispatch("quantize_q8", [src, dst, be.params(0)], (8,), (256,)) == -1
+    # destination too small for n
+    assert be.dispatch("quantize_q8", [src, be.alloc(36), be.params(64)], (16,), (256,)) == -1
+    assert not dst.read(np.uint8).any()
