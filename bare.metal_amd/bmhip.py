@@ -60,6 +60,8 @@ def lib() -> C.CDLL:
         "bm_synth_tensor_seed": (u64, [u64, i, i, i]),
         "bm_synth_normal_f32": (None, [u64, C.c_float, vp, sz]),
         "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
+        "bm_q8_mv_tiles": (i, [i, i]),
+        "bm_q8_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -100,6 +102,29 @@ def synth_uniform_int(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.int32)
     lib().bm_synth_uniform_int(seed, lo, hi, _ptr(out), n)
     return out
+
+
+# ---------------------------------------------------------------- Q8 multi-matvec plan
+
+def mv_plan(w_off, x_off, y_off, OC, C_):
+    """Plan table (bytes) and workgroup count of a matmul_forward_q8_vec_multi
+    launch over the problems given by the five equal-length sequences."""
+    n = len(OC)
+    w = np.ascontiguousarray(w_off, dtype=np.uint64)
+    x = np.ascontiguousarray(x_off, dtype=np.uint64)
+    y = np.ascontiguousarray(y_off, dtype=np.uint64)
+    oc = np.ascontiguousarray(OC, dtype=np.int32)
+    c = np.ascontiguousarray(C_, dtype=np.int32)
+    nt = C.c_int(0)
+    need = lib().bm_q8_mv_plan(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), None, 0, C.byref(nt))
+    if need < 0:
+        raise ValueError("bm_q8_mv_plan rejected the problem list")
+    plan = np.zeros((need + 7) // 8, dtype=np.uint64)
+    got = lib().bm_q8_mv_plan(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), _ptr(plan), plan.nbytes,
+                              C.byref(nt))
+    if got != need:
+        raise ValueError("bm_q8_mv_plan failed")
+    return plan.view(np.uint8)[:need].copy(), nt.value
 
 
 # ---------------------------------------------------------------- backend

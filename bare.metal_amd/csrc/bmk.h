@@ -36,6 +36,8 @@ typedef struct {
     uint32_t        val_mask;    /* bit i: buffer i is read by value at encode time */
     uint32_t        out_mask;    /* bit i: the kernel may write buffer i */
     bmk_launcher_fn launch;
+    uint32_t        dev_mask;    /* bit i (with val_mask): also copied to the device, for kernels that
+                                    read a host-validated table from device memory */
 } bmk_desc_t;
 
 #ifdef __cplusplus

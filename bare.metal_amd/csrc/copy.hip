@@ -1,0 +1,51 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * copy.hip — device-to-device byte copy as a named kernel ("copy_buffer").
+ * Used where the engine moves data between buffers on the stream (the
+ * reference does such copies on the host through map, e.g.
+ * src/baremetal/scheduler.c:1739-1759), and as the plain copy of known size
+ * that calibrates HBM byte counters.  16 bytes per lane per step, grid-stride.
+ */
+#include "bmk.h"
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, long n16) {
+    const long stride = (long)gridDim.x * 256;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void k_copy1(const unsigned char* __restrict__ src, unsigned char* __restrict__ dst,
+                                               long n) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+} // namespace
+
+/* buffers {0 src, 1 dst, 2 params int64{nbytes}} */
+extern "C" int bmk_launch_copy_buffer(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 8, "params");
+    long long nb;
+    __builtin_memcpy(&nb, a->val[2], 8);
+    BMK_REQUIRE(nb >= 0, "copy_buffer: negative size");
+    if (nb == 0) return 0;
+    BMK_NEED_BYTES(a, 0, nb, "src");
+    BMK_NEED_BYTES(a, 1, nb, "dst");
+    const unsigned char* s = (const unsigned char*)a->dev[0];
+    unsigned char* d = (unsigned char*)a->dev[1];
+    const long n16 = ((((uintptr_t)s | (uintptr_t)d) & 15) == 0) ? nb / 16 : 0;
+    if (n16 > 0) {
+        long blocks = (n16 + 255) / 256;
+        if (blocks > 256 * 16) blocks = 256 * 16; /* 16 workgroups per CU, grid-stride beyond */
+        hipLaunchKernelGGL(k_copy16, dim3((unsigned)blocks), dim3(256), 0, a->stream, (const uint4*)s, (uint4*)d, n16);
+        BMK_LAUNCH_CHECK();
+    }
+    const long tail = nb - n16 * 16;
+    if (tail > 0) {
+        hipLaunchKernelGGL(k_copy1, dim3((unsigned)((tail + 255) / 256)), dim3(256), 0, a->stream, s + n16 * 16,
+                           d + n16 * 16, tail);
+        BMK_LAUNCH_CHECK();
+    }
+    return 0;
+}

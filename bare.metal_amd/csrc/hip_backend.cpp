@@ -345,6 +345,7 @@ extern "C" int backend_encode_dispatch(backend_encoder_t* enc, backend_kernel_t*
                 if (!shadow_pull(b)) return -1;
             }
             a.val[i] = (const char*)b->host + off;
+            if ((d->dev_mask & (1u << i)) && !shadow_push(b)) return -1;
         } else {
             if (!shadow_push(b)) return -1;
         }

@@ -14,6 +14,8 @@ int bmk_launch_quantize_q8(const bmk_launch_t* a);
 int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a);
 int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
+int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
+int bmk_launch_copy_buffer(const bmk_launch_t* a);
 }
 
 #define B(i) (1u << (i))
@@ -28,5 +30,10 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"matmul_forward_q8_vec", 5, B(4), B(3), bmk_launch_q8_matvec},
     /* reference forward.metal:625-649; same buffers */
     {"matmul_forward_q8", 5, B(4), B(3), bmk_launch_q8_matmul},
-    {nullptr, 0, 0, 0, nullptr},
+    /* new: every Q8 matvec of a decode token in one launch; {params{nprob,n_tiles},
+     * plan{MvDesc[nprob], u32 tile_map[n_tiles]}, weight arena, x arena, y arena} */
+    {"matmul_forward_q8_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_matvec_multi, B(1)},
+    /* new: device-to-device copy; {src, dst, params int64{nbytes}} */
+    {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
+    {nullptr, 0, 0, 0, nullptr, 0},
 };

@@ -28,12 +28,22 @@ typedef struct {
     int nprob;
 } MvGroup;
 
+/* One problem of a multi-matrix launch, addressed by offsets into three
+ * arenas (weights in bytes, activations and outputs in floats).  Problem p
+ * owns workgroups tile0 .. tile0+tiles-1 of the launch. */
+typedef struct {
+    unsigned long long w_off, x_off, y_off;
+    int OC, C, tile0, tiles;
+} MvDesc;
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 int mv_tiles_for(int OC, int C, int U);
 int mv_launch_group(MvGroup* g, hipStream_t s);
 int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_map, int n_tiles, hipStream_t s);
+int mv_launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
+                    const unsigned int* d_tile_map, int n_tiles, hipStream_t s);
 #ifdef __cplusplus
 }
 #endif

@@ -176,6 +176,27 @@ __global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_list(const MvProb* __r
     mv_dispatch<U>(p, (int)(m & 0xfffffu), red);
 }
 
+/* Any number of problems addressed by arena offsets; tile_map[blockIdx.x]
+ * is the problem index, the tile is blockIdx.x - desc.tile0. */
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_multi(const unsigned char* __restrict__ W,
+                                                                const float* __restrict__ X, float* __restrict__ Y,
+                                                                const MvDesc* __restrict__ desc,
+                                                                const unsigned int* __restrict__ tile_map) {
+    __shared__ float red[MV_THREADS * U];
+    const MvDesc d = desc[tile_map[blockIdx.x]];
+    MvProb p;
+    p.w = W + d.w_off;
+    p.x = X + d.x_off;
+    p.y = Y + d.y_off;
+    p.bias = nullptr;
+    p.OC = d.OC;
+    p.nb = d.C / 32;
+    p.tiles = d.tiles;
+    p.pad_ = 0;
+    mv_dispatch<U>(p, (int)blockIdx.x - d.tile0, red);
+}
+
 } // namespace
 
 /* ------------------------------------------------------------------ */
@@ -205,6 +226,58 @@ extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_
                        d_tile_map);
     BMK_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
+                               const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
+    if (n_tiles <= 0) return 0;
+    hipLaunchKernelGGL(k_q8_matvec_multi<MV_U>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y, d_desc,
+                       d_tile_map);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* matmul_forward_q8_vec_multi: every Q8 matvec of one decode token (or any
+ * set of independent y = W x problems) in one launch.
+ * buffers {0 params int {nprob, n_tiles} (by value),
+ *          1 plan: MvDesc[nprob] then uint32 tile_map[n_tiles] (read on the
+ *            host to validate, and by the kernel from device memory),
+ *          2 weight arena (Q8 blocks), 3 activation arena f32, 4 output arena f32}.
+ * Every descriptor and tile-map entry is checked against the arena sizes
+ * before anything is launched. */
+extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 0, 8, "params");
+    const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
+    BMK_REQUIRE(nprob >= 0 && n_tiles >= 0, "q8 matvec multi: bad counts nprob=%d n_tiles=%d", nprob, n_tiles);
+    if (nprob == 0 || n_tiles == 0) return 0;
+    const size_t desc_bytes = (size_t)nprob * sizeof(MvDesc);
+    BMK_NEED_BYTES(a, 1, desc_bytes + (size_t)n_tiles * 4, "plan");
+    BMK_REQUIRE(((uintptr_t)a->dev[1] & 7) == 0 && ((uintptr_t)a->val[1] & 7) == 0, "q8 matvec multi: plan offset must be 8-byte aligned");
+    BMK_REQUIRE(((uintptr_t)a->dev[2] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0 && ((uintptr_t)a->dev[4] & 3) == 0,
+                "q8 matvec multi: misaligned arena offset");
+    const MvDesc* desc = (const MvDesc*)a->val[1];
+    const unsigned int* tmap = (const unsigned int*)((const char*)a->val[1] + desc_bytes);
+    long next_tile = 0;
+    for (int i = 0; i < nprob; i++) {
+        const MvDesc& d = desc[i];
+        BMK_REQUIRE(d.OC > 0 && d.C > 0 && d.C % 32 == 0, "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, d.OC, d.C);
+        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, MV_U) && d.tile0 == next_tile,
+                    "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
+                    mv_tiles_for(d.OC, d.C, MV_U), next_tile);
+        BMK_REQUIRE((d.w_off & 3) == 0, "q8 matvec multi: problem %d weight offset not 4-byte aligned", i);
+        BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * 36 <= a->bytes[2] &&
+                    d.x_off + (unsigned long long)d.C <= a->bytes[3] / 4 &&
+                    d.y_off + (unsigned long long)d.OC <= a->bytes[4] / 4,
+                    "q8 matvec multi: problem %d lies outside its arenas", i);
+        next_tile += d.tiles;
+    }
+    BMK_REQUIRE(next_tile == n_tiles, "q8 matvec multi: tiles sum to %ld, n_tiles=%d", next_tile, n_tiles);
+    for (int i = 0; i < nprob; i++)
+        for (int t = desc[i].tile0; t < desc[i].tile0 + desc[i].tiles; t++)
+            BMK_REQUIRE(tmap[t] == (unsigned)i, "q8 matvec multi: tile_map[%d]=%u, expected %d", t, tmap[t], i);
+    return mv_launch_multi((const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
+                           (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
+                           n_tiles, a->stream);
 }
 
 /* matmul_forward_q8_vec / matmul_forward_q8 with BT below the GEMM cut-over:

@@ -1,0 +1,46 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * bm_q8.h — MI355X additions to the Q8 operator set, beside the reference's
+ * backend interface (backend.h).  They have no counterpart in the reference:
+ * the reference dispatches one Q8 matvec per weight tensor
+ * (reference src/baremetal/scheduler.c:747-754,949-990) and quantizes on the
+ * host (reference src/baremetal/quant.c:54-71).
+ *
+ * Named kernels added to the backend's kernel table (bound like any other
+ * kernel through backend_encode_dispatch; buffer order listed):
+ *   "quantize_q8"        {src f32 [n], dst Q8 blocks [n/32], params int{n}}
+ *   "quantize_q8_bf16"   {src bf16 [n], dst Q8 blocks [n/32], params int{n}}
+ *   "matmul_forward_q8_vec_multi"
+ *                        {params int{nprob, n_tiles}, plan (bm_q8_mv_plan),
+ *                         weight arena, activation arena f32, output arena f32}
+ *   "copy_buffer"        {src, dst, params int64{nbytes}}
+ */
+#ifndef BM_Q8_H
+#define BM_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Workgroups one y = W x problem of OC rows and C columns takes in a
+ * matmul_forward_q8_vec_multi launch; -1 if C is not a positive multiple of 32. */
+int  bm_q8_mv_tiles(int OC, int C);
+
+/* Writes the plan table of a matmul_forward_q8_vec_multi launch over nprob
+ * problems: problem i reads Q8 rows at byte offset w_off[i] of the weight
+ * arena, C[i] floats at float offset x_off[i] of the activation arena, and
+ * writes OC[i] floats at float offset y_off[i] of the output arena.
+ * With plan == NULL only the size is computed.  Returns the table's size in
+ * bytes (plan must be 8-byte aligned and hold that many), or -1; *n_tiles
+ * receives the launch's workgroup count. */
+long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
+                   const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -49,6 +49,27 @@ void orc_cpu_q8_matvec_f32(const uint8_t* w, const float* x, float* y, int C, in
     }
 }
 
+/* Many independent problems (one decode token's projections): the rows of
+ * all problems form one index space split evenly over the threads. */
+void orc_cpu_q8_matvec_multi(const uint8_t* w, const float* x, float* y, int nprob, const uint64_t* w_off,
+                             const uint64_t* x_off, const uint64_t* y_off, const int* OC, const int* C,
+                             int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    long total = 0;
+    for (int i = 0; i < nprob; i++) total += OC[i];
+#pragma omp parallel num_threads(nthreads)
+    {
+        int t = omp_get_thread_num(), nt = omp_get_num_threads();
+        long g0 = total * t / nt, g1 = total * (t + 1) / nt, base = 0;
+        for (int i = 0; i < nprob && base < g1; i++) {
+            long r0 = g0 > base ? g0 - base : 0, r1 = g1 - base < OC[i] ? g1 - base : OC[i];
+            if (r0 < r1)
+                rows_f32(w + w_off[i], x + x_off[i], y + y_off[i], C[i], (int)r0, (int)r1);
+            base += OC[i];
+        }
+    }
+}
+
 int orc_cpu_max_threads(void) { return omp_get_max_threads(); }
 
 const char* orc_cpu_isa(void) {

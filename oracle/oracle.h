@@ -19,6 +19,9 @@ void     orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M
 /* CPU baseline (cpu_baseline.c): fp32 Q8 matvec in the reference's
  * arithmetic, SIMD + OpenMP over rows. */
 void     orc_cpu_q8_matvec_f32(const uint8_t* w, const float* x, float* y, int C, int OC, int nthreads);
+void     orc_cpu_q8_matvec_multi(const uint8_t* w, const float* x, float* y, int nprob, const uint64_t* w_off,
+                                 const uint64_t* x_off, const uint64_t* y_off, const int* OC, const int* C,
+                                 int nthreads);
 int      orc_cpu_max_threads(void);
 const char* orc_cpu_isa(void);
 

@@ -40,6 +40,7 @@ def oracle() -> C.CDLL:
         L.orc_q8_matvec_f64.argtypes = [vp, vp, vp, i, i, i]
         L.orc_q8_gemm_bf16_f64.argtypes = [vp, vp, vp, i, i, i]
         L.orc_cpu_q8_matvec_f32.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_cpu_q8_matvec_multi.argtypes = [vp, vp, vp, i, vp, vp, vp, vp, vp, i]
         L.orc_cpu_max_threads.restype = i
         L.orc_cpu_isa.restype = C.c_char_p
         L.orc_decoder_create.restype = vp
@@ -131,6 +132,16 @@ def cpu_q8_matvec_f32(w: np.ndarray, x: np.ndarray, C_: int, OC: int, nthreads: 
     y = np.zeros(OC, dtype=np.float32)
     oracle().orc_cpu_q8_matvec_f32(_p(w), _p(x), _p(y), C_, OC, nthreads)
     return y
+
+
+def cpu_q8_matvec_multi(w, x, y, w_off, x_off, y_off, OC, C_, nthreads: int) -> None:
+    """y[y_off[i]:+OC[i]] = W_i x_i for every problem i (fp32, SIMD + OpenMP)."""
+    arrs = [np.ascontiguousarray(a, dtype=np.uint64) for a in (w_off, x_off, y_off)]
+    oc = np.ascontiguousarray(OC, dtype=np.int32)
+    c = np.ascontiguousarray(C_, dtype=np.int32)
+    assert w.dtype == np.uint8 and x.dtype == np.float32 and y.dtype == np.float32
+    oracle().orc_cpu_q8_matvec_multi(_p(w), _p(x), _p(y), len(oc), _p(arrs[0]), _p(arrs[1]), _p(arrs[2]),
+                                     _p(oc), _p(c), nthreads)
 
 
 # ---------------------------------------------------------------- decode oracle

@@ -7,6 +7,7 @@ import os
 import re
 
 import bmhip
+import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DECL = re.compile(r"^\s*(?:[A-Za-z_][\w\s\*]*?[\s\*])([A-Za-z_]\w*)\s*\(", re.M)
@@ -64,3 +65,26 @@ def test_null_handles_are_safe():
     assert L.backend_kernel_dispatch(None, None, None, None, 0, 1, 1, 1, 1, 1, 1) == -1
     assert L.backend_kernel_create(None, b"quantize_q8") is None
     assert L.backend_get_gpu_busy_ms(None) == 0.0
+
+
+def test_mv_plan_layout():
+    """bm_q8_mv_plan: descriptors in order, tile_map names each problem's workgroups."""
+    import numpy as np
+
+    OC = [960, 320, 49152, 5, 3]
+    C = [960, 960, 960, 2560, 9600]
+    plan, n_tiles = bmhip.mv_plan([0, 1, 2, 3, 4], [5, 6, 7, 8, 9], [10, 11, 12, 13, 14], OC, C)
+    tiles = [bmhip.lib().bm_q8_mv_tiles(o, c) for o, c in zip(OC, C)]
+    # 256 lanes hold 256 // (C/32) rows per pass, 4 passes per workgroup; C/32 > 256: one row each
+    assert tiles == [-(-960 // 32), -(-320 // 32), 49152 // 32, 1, 3]
+    assert n_tiles == sum(tiles)
+    desc = np.frombuffer(plan[:40 * 5].tobytes(), dtype=np.dtype([("w", "<u8"), ("x", "<u8"), ("y", "<u8"),
+                                                                   ("OC", "<i4"), ("C", "<i4"),
+                                                                   ("t0", "<i4"), ("nt", "<i4")]))
+    assert list(desc["w"]) == [0, 1, 2, 3, 4] and list(desc["y"]) == [10, 11, 12, 13, 14]
+    assert list(desc["t0"]) == list(np.cumsum([0] + tiles[:-1]))
+    tmap = np.frombuffer(plan[40 * 5:].tobytes(), dtype=np.uint32)
+    assert list(tmap) == sum(([i] * t for i, t in enumerate(tiles)), [])
+    assert bmhip.lib().bm_q8_mv_tiles(10, 48) == -1
+    with pytest.raises(ValueError):
+        bmhip.mv_plan([0], [0], [0], [4], [33])

@@ -90,3 +90,41 @@ def test_matvec_rejects_short_buffers(be):
     rc = be.dispatch("matmul_forward_q8_vec", [bx, be.upload(w), be.alloc(OC * 4), by, be.params(1, 48, OC, 0)],
                      (OC * 128, 1), (128,))
     assert rc == -1  # C not a multiple of 32
+
+
+def test_matvec_multi_launch(be):
+    """matmul_forward_q8_vec_multi over a mixed problem list (incl. a row wider than 256 blocks)."""
+    shapes = [(960, 960), (320, 960), (5, 2560), (1536, 576), (3, 8224), (49152, 576), (1, 32)]
+    ws, xs = [], []
+    for i, (OC, C) in enumerate(shapes):
+        ws.append(po.quantize_q8(bmhip.synth_normal(bmhip.synth_seed(41, 0, i, 0), 0.02, OC * C)))
+        xs.append(bmhip.synth_normal(bmhip.synth_seed(41, 0, i, 1), 1.0, C))
+    w_off = np.cumsum([0] + [w.size for w in ws[:-1]])
+    x_off = np.cumsum([0] + [x.size for x in xs[:-1]])
+    y_off = np.cumsum([0] + [s[0] for s in shapes[:-1]])
+    plan, n_tiles = bmhip.mv_plan(w_off, x_off, y_off, [s[0] for s in shapes], [s[1] for s in shapes])
+    W, X = be.upload(np.concatenate(ws)), be.upload(np.concatenate(xs))
+    Y = be.alloc(4 * sum(s[0] for s in shapes))
+    rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(len(shapes), n_tiles), be.upload(plan), W, X, Y],
+                     (n_tiles * 256,), (256,))
+    assert rc == 0
+    y = Y.read(np.float32)
+    for i, (OC, C) in enumerate(shapes):
+        r = po.q8_matvec_f64(ws[i], xs[i], 1, C, OC)
+        got = y[y_off[i]:y_off[i] + OC]
+        assert normwise(got, r) <= RTOL, (i, normwise(got, r))
+
+
+def test_matvec_multi_rejects_bad_plans(be):
+    OC, C = 64, 576
+    w = po.quantize_q8(bmhip.synth_normal(51, 0.02, OC * C))
+    W, X, Y = be.upload(w), be.upload(np.ones(C, np.float32)), be.alloc(OC * 4)
+    plan, n_tiles = bmhip.mv_plan([0], [0], [0], [OC], [C])
+    k = "matmul_forward_q8_vec_multi"
+    bad = plan.copy()
+    bad[-4:] = np.array([7], np.uint32).view(np.uint8)  # tile map names a problem that does not exist
+    assert be.dispatch(k, [be.params(1, n_tiles), be.upload(bad), W, X, Y], (n_tiles * 256,), (256,)) == -1
+    big, nt2 = bmhip.mv_plan([36], [0], [0], [OC], [C])  # weights run one block past the arena
+    assert be.dispatch(k, [be.params(1, nt2), be.upload(big), W, X, Y], (nt2 * 256,), (256,)) == -1
+    assert be.dispatch(k, [be.params(1, n_tiles + 1), be.upload(plan), W, X, Y], (n_tiles * 256,), (256,)) == -1
+    assert not Y.read(np.float32).any()
