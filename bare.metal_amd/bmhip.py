@@ -62,6 +62,33 @@ def lib() -> C.CDLL:
         "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
         "bm_q8_mv_tiles": (i, [i, i]),
         "bm_q8_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
+        "bm_create": (vp, [i]),
+        "bm_destroy": (None, [vp]),
+        "bm_get_supported_precision": (i, [vp]),
+        "bm_create_model": (vp, [vp, vp]),
+        "bm_destroy_model": (None, [vp]),
+        "bm_compile": (None, [vp]),
+        "bm_create_session": (vp, [vp, vp]),
+        "bm_create_session_batched": (vp, [vp, vp, i, i]),
+        "bm_step": (C.POINTER(C.c_float), [vp, i]),
+        "bm_step_batch": (C.POINTER(C.c_float), [vp, vp]),
+        "bm_forward": (C.POINTER(C.c_float), [vp, vp, i]),
+        "bm_reset_session": (None, [vp]),
+        "bm_destroy_session": (None, [vp]),
+        "bm_profile_begin": (None, [vp]),
+        "bm_profile_end": (None, [vp, vp, vp, vp]),
+        "bm_run_tokens": (i, [vp, vp, vp, i, i, C.c_float, i, C.c_float, u64, vp, vp]),
+        "bm_create_sampler": (vp, [i, C.c_float, C.c_float, u64]),
+        "bm_sample": (i, [vp, vp]),
+        "bm_destroy_sampler": (None, [vp]),
+        "bm_get_num_parameters": (i, [vp]),
+        "bm_get_arch_name": (C.c_char_p, [vp]),
+        "bm_model_set_quant_bits": (i, [vp, i]),
+        "bm_model_set_q8_head": (i, [vp, i]),
+        "bm_model_set_tensor": (i, [vp, C.c_char_p, vp, sz]),
+        "bm_model_init_synthetic": (i, [vp, u64]),
+        "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
+        "bm_session_set_graph": (i, [vp, i]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -273,3 +300,142 @@ class Backend:
             self._kernels.clear()
             lib().backend_destroy(self.ctx)
             self.ctx = None
+
+
+# ---------------------------------------------------------------- engine (include/baremetal.h)
+
+class Arch(C.Structure):
+    """bm_arch_t (reference include/baremetal.h:54-87)."""
+    _fields_ = [(n, C.c_int) for n in ("dim", "hidden_dim", "n_layers", "n_heads", "n_kv_heads", "vocab_size",
+                                       "padded_vocab_size", "max_seq_len", "norm", "activation", "pos_enc",
+                                       "attention", "precision", "bias", "weight_tie", "has_qk_norm",
+                                       "has_ffn_post_norm", "head_dim", "gated_mlp", "gemma_norm", "embed_scale",
+                                       "weight_layout")] + [
+        ("rope_theta", C.c_float), ("rope_scaling", C.c_int), ("rope_factor", C.c_float),
+        ("rope_low_freq_factor", C.c_float), ("rope_high_freq_factor", C.c_float), ("rope_original_max", C.c_float),
+    ]
+
+
+BM_DEVICE_HIP = 1
+SMOLLM2_135M = dict(D=576, H=1536, NH=9, NKV=3, HD=64, L=30, V=49152)
+SMOLLM2_360M = dict(D=960, H=2560, NH=15, NKV=5, HD=64, L=32, V=49152)
+TENSOR_IDS = {"token_embedding": 0, "wq": 1, "wk": 2, "wv": 3, "wo": 4, "w_gate": 5, "w_up": 6, "w_down": 7}
+
+
+def llama_arch(D, H, NH, NKV, HD, L, V, max_seq_len=2048, theta=10000.0) -> Arch:
+    a = Arch()
+    a.dim, a.hidden_dim, a.n_layers, a.n_heads, a.n_kv_heads = D, H, L, NH, NKV
+    a.vocab_size = a.padded_vocab_size = V
+    a.max_seq_len = max_seq_len
+    a.norm, a.activation, a.pos_enc, a.attention = 1, 1, 1, 1  # RMSNorm, SwiGLU, RoPE, GQA
+    a.precision = 0
+    a.weight_tie, a.gated_mlp, a.head_dim = 1, 1, HD
+    a.rope_theta = theta
+    return a
+
+
+def synthetic_weights(dims: dict, seed: int) -> dict:
+    """The fp32 weights bm_model_init_synthetic(seed) builds, generated on
+    the host in the reference layout (same seeds, same bits)."""
+    D, H, NH, NKV, HD, L, V = (dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V"))
+    QD, KV = NH * HD, NKV * HD
+    per = {"wq": QD * D, "wk": KV * D, "wv": KV * D, "wo": D * QD, "w_gate": H * D, "w_up": H * D, "w_down": D * H}
+    w = {"token_embedding": synth_normal(synth_seed(seed, 5, 0xFFFF, 0), 0.02, V * D)}
+    for name, n in per.items():
+        w[name] = np.concatenate([synth_normal(synth_seed(seed, 5, l, TENSOR_IDS[name]), 0.02, n) for l in range(L)])
+    w["ln1"] = np.ones(L * D, np.float32)
+    w["ln2"] = np.ones(L * D, np.float32)
+    w["lnf"] = np.ones(D, np.float32)
+    return w
+
+
+class Engine:
+    """A context + model + session of the decode engine."""
+
+    def __init__(self, dims: dict, max_seq_len: int = 512, batch: int = 1, seed=None, weights=None,
+                 q8_head: bool = False, graph: bool = True):
+        L = lib()
+        self.dims = dict(dims)
+        self.V = dims["V"]
+        self.B = batch
+        self.ctx = L.bm_create(BM_DEVICE_HIP)
+        if not self.ctx:
+            raise BackendError("bm_create failed (no HIP device?)")
+        self.arch = llama_arch(**{k: dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V")},
+                               max_seq_len=max_seq_len, theta=dims.get("theta", 10000.0))
+        self.model = L.bm_create_model(self.ctx, C.byref(self.arch))
+        if not self.model:
+            raise BackendError("bm_create_model rejected the architecture")
+        if L.bm_model_set_quant_bits(self.model, 8) != 0:
+            raise BackendError("bm_model_set_quant_bits failed")
+        if q8_head:
+            L.bm_model_set_q8_head(self.model, 1)
+        if weights is not None:
+            for name, arr in weights.items():
+                a = np.ascontiguousarray(arr, dtype=np.float32)
+                if L.bm_model_set_tensor(self.model, name.encode(), _ptr(a), a.size) != 0:
+                    raise BackendError(f"bm_model_set_tensor({name}) failed")
+        else:
+            if L.bm_model_init_synthetic(self.model, seed if seed is not None else 1) != 0:
+                raise BackendError("bm_model_init_synthetic failed")
+        L.bm_compile(self.model)
+        self.sess = L.bm_create_session_batched(self.ctx, self.model, batch, max_seq_len)
+        if not self.sess:
+            raise BackendError("bm_create_session failed")
+        L.bm_session_set_graph(self.sess, 1 if graph else 0)
+
+    def set_graph(self, on: bool):
+        lib().bm_session_set_graph(self.sess, 1 if on else 0)
+
+    def step(self, token: int) -> np.ndarray:
+        p = lib().bm_step(self.sess, int(token))
+        if not p:
+            raise BackendError("bm_step failed")
+        return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
+
+    def step_batch(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        p = lib().bm_step_batch(self.sess, _ptr(t))
+        if not p:
+            raise BackendError("bm_step_batch failed")
+        return np.ctypeslib.as_array(p, shape=(self.B, self.V)).copy()
+
+    def reset(self):
+        lib().bm_reset_session(self.sess)
+
+    def generate(self, prompt, steps: int) -> np.ndarray:
+        """prompt: [B][n_prompt] ids; returns [steps - n_prompt + 1][B] greedy tokens."""
+        pr = np.ascontiguousarray(prompt, dtype=np.int32).reshape(self.B, -1)
+        n_prompt = pr.shape[1]
+        n_out = steps - n_prompt + 1
+        out = np.zeros((max(n_out, 1), self.B), np.int32)
+        n = lib().bm_generate_greedy(self.sess, _ptr(pr), n_prompt, steps, _ptr(out))
+        if n != n_out:
+            raise BackendError(f"bm_generate_greedy returned {n}")
+        return out[:n]
+
+    def profile_begin(self):
+        lib().bm_profile_begin(self.sess)
+
+    def profile_end(self) -> float:
+        o = C.c_double(0.0)
+        lib().bm_profile_end(self.sess, None, None, C.byref(o))
+        return o.value
+
+    def close(self):
+        L = lib()
+        if self.sess:
+            L.bm_destroy_session(self.sess)
+            self.sess = None
+        if self.model:
+            L.bm_destroy_model(self.model)
+            self.model = None
+        if self.ctx:
+            L.bm_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,784 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * decode.hip — the decode-step kernels on gfx950.
+ *
+ * Two sets, sharing their device code:
+ *  1. The kernels the reference's decode scheduler dispatches by name, with
+ *     the reference's buffer orders and parameter layouts
+ *     (reference src/baremetal/scheduler.c:712-996):
+ *       rmsnorm_forward_v2      reference src/kernels/forward.metal:1019-1060
+ *       rope_forward            forward.metal:1260-1313
+ *       kv_store                forward.metal:1317-1329
+ *       attention_forward       forward.metal:1362-1465
+ *       add_forward             forward.metal:1332-1340
+ *       swiglu_forward          forward.metal:1179-1190
+ *       rmsnorm_matmul_forward  forward.metal:1636-1689
+ *     plus argmax_f32 (the host-side greedy pick of reference
+ *     tools/run.c:56-60 as a kernel: first maximal index wins).
+ *  2. The fused kernels of the engine's graph-replayed decode step
+ *     (engine.cpp): embedding gather, RMSNorm-prologue Q8 matvecs with
+ *     SwiGLU / residual epilogues, rope + KV append + attention, and the
+ *     final RMSNorm + LM head + argmax.  They read the position and tokens
+ *     from DecState in device memory (decode_state.h).
+ *
+ * Arithmetic follows the reference kernels term for term where the order is
+ * defined (RMSNorm: (x * inv_rms) * w with inv_rms = 1/sqrt(ss/C + eps);
+ * RoPE angle (float)pos * inv_freq; SiLU x/(1+exp(-x)); residual a + b);
+ * reductions run in fp32 in a fixed order of their own (the reference's
+ * order is a fast-math Metal reduction and is not defined).
+ */
+#include "bmk.h"
+#include "decode_state.h"
+#include "q8_common.h"
+
+#include <math.h>
+#include <string.h>
+
+namespace {
+
+using namespace bmk;
+
+constexpr int NT = 256;     /* threads per workgroup (4 waves) */
+constexpr int ATT_CH = 2048; /* keys per softmax chunk held in LDS */
+constexpr int HEAD_U = 4;   /* rows in flight per lane in the LM head */
+constexpr int MV_U = 4;     /* rows in flight per lane in the fused matvec */
+
+/* Sum of v over the 256 threads; every thread gets the result.  sh: 4 floats of LDS. */
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float* sh) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    __syncthreads();
+    return r;
+}
+
+/* 1/sqrt(mean(x^2) + eps) over C floats (reference forward.metal:1053-1054). */
+__device__ __forceinline__ float rms_inv(const float* x, int C, float eps, float* sh) {
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < C; j += NT) {
+        float v = x[j];
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, sh);
+    return 1.0f / sqrtf(ss / (float)C + eps);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+/* Order-preserving packing of (value, index) for an atomicMax argmax in
+ * which the larger value wins and, on equal values, the smaller index. */
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+    unsigned int u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned int)idx);
+}
+__device__ __forceinline__ int argmax_key_index(unsigned long long k) {
+    return (int)(0xFFFFFFFFu - (unsigned int)(k & 0xFFFFFFFFull));
+}
+
+/* Best (value, index) of the workgroup: larger value, then smaller index. */
+__device__ __forceinline__ unsigned long long block_argmax_key(unsigned long long k, unsigned long long* sh) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = k;
+    __syncthreads();
+    unsigned long long r = sh[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; i++) r = sh[i] > r ? sh[i] : r;
+    __syncthreads();
+    return r;
+}
+
+/* ================================================================== */
+/* Attention for one query head (one workgroup):
+ *   out[d] = sum_t softmax_t(scale * q.k_t) v_t[d],  t < S.
+ * Keys t < n_cached come from the cache rows kc/vc (stride KV floats); when
+ * cur_k (LDS) is given, key t == n_cached == S-1 is cur_k/cur_v, used from
+ * registers so that no pointer ever selects between LDS and global memory.
+ * Online softmax over chunks of ATT_CH scores held in LDS.  HD divides 256. */
+__device__ void attn_head(const float* qs, const float* kc, const float* vc, int KV, int S, int n_cached,
+                          const float* cur_k, const float* cur_v, int HD, float scale, float* sc, float* red,
+                          float* sh, float* out) {
+    const int t = threadIdx.x;
+    const int G = NT / HD, g = t / HD, d = t - g * HD;
+    float s_cur = 0.0f, v_cur = 0.0f;
+    if (cur_k) {
+        float c0 = 0.f, c1 = 0.f;
+        for (int e = 0; e < HD; e += 2) {
+            c0 = fmaf(qs[e], cur_k[e], c0);
+            c1 = fmaf(qs[e + 1], cur_k[e + 1], c1);
+        }
+        s_cur = (c0 + c1) * scale;
+        v_cur = cur_v[d];
+    }
+    float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;
+    for (int base = 0; base < S; base += ATT_CH) {
+        const int n = min(ATT_CH, S - base);
+        float lmax = -INFINITY;
+        for (int i = t; i < n; i += NT) {
+            const int tt = base + i;
+            float s;
+            if (tt < n_cached) {
+                const float* kr = kc + (size_t)tt * KV;
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+                for (int e = 0; e < HD; e += 4) {
+                    float4 kv4;
+                    __builtin_memcpy(&kv4, __builtin_assume_aligned(kr + e, 4), 16);
+                    s0 = fmaf(qs[e + 0], kv4.x, s0);
+                    s1 = fmaf(qs[e + 1], kv4.y, s1);
+                    s2 = fmaf(qs[e + 2], kv4.z, s2);
+                    s3 = fmaf(qs[e + 3], kv4.w, s3);
+                }
+                s = ((s0 + s1) + (s2 + s3)) * scale;
+            } else {
+                s = s_cur;
+            }
+            sc[i] = s;
+            lmax = fmaxf(lmax, s);
+        }
+        const float cmax = block_max(lmax, sh);
+        float lsum = 0.0f;
+        for (int i = t; i < n; i += NT) {
+            const float p = expf(sc[i] - cmax);
+            sc[i] = p;
+            lsum += p;
+        }
+        const float csum = block_sum(lsum, sh); /* its barriers also publish sc[] */
+        const float m_new = fmaxf(m_run, cmax);
+        const float a_old = expf(m_run - m_new), a_new = expf(cmax - m_new);
+        l_run = l_run * a_old + csum * a_new;
+        float part = 0.0f;
+        const int n_c = min(n, n_cached - base); /* keys of this chunk that are in the cache */
+        for (int i = g; i < n_c; i += G) part = fmaf(sc[i], vc[(size_t)(base + i) * KV + d], part);
+        if (n_c < n && g == (n_c % G) && n_c >= 0) part = fmaf(sc[n_c], v_cur, part);
+        acc = acc * a_old + part * a_new;
+        m_run = m_new;
+        __syncthreads(); /* sc[] is rewritten by the next chunk */
+    }
+    red[g * HD + d] = acc;
+    __syncthreads();
+    if (t < HD) {
+        float s = 0.0f;
+        for (int k = 0; k < G; k++) s += red[k * HD + t];
+        out[t] = s / l_run;
+    }
+}
+
+/* ================================================================== */
+/* Reference-named kernels */
+
+__global__ __launch_bounds__(NT) void k_rmsnorm(const float* __restrict__ x, const float* __restrict__ w,
+                                                float* out, int C, float eps) {
+    __shared__ float sh[4];
+    const float* xr = x + (size_t)blockIdx.x * C;
+    float* orow = out + (size_t)blockIdx.x * C;
+    const float inv = rms_inv(xr, C, eps, sh);
+    for (int j = threadIdx.x; j < C; j += NT) orow[j] = (xr[j] * inv) * w[j];
+}
+
+struct RopeTab {
+    float inv[DEC_MAX_HD / 2];
+};
+
+/* one thread per (head, rotary pair) */
+__global__ __launch_bounds__(NT) void k_rope(float* q, float* k, int NH, int NKV, int HD, int pos, RopeTab rt) {
+    const int hd2 = HD / 2;
+    const int gid = blockIdx.x * NT + threadIdx.x;
+    if (gid >= NH * hd2) return;
+    const int h = gid / hd2, i = gid - h * hd2;
+    const float fr = rt.inv[i];
+    const float ang = (float)pos * fr;
+    const float c = cosf(ang), s = sinf(ang);
+    float* qh = q + h * HD;
+    const float q0 = qh[i], q1 = qh[i + hd2];
+    qh[i] = q0 * c - q1 * s;
+    qh[i + hd2] = q0 * s + q1 * c;
+    if (h < NKV) {
+        float* kh = k + h * HD;
+        const float k0 = kh[i], k1 = kh[i + hd2];
+        kh[i] = k0 * c - k1 * s;
+        kh[i + hd2] = k0 * s + k1 * c;
+    }
+}
+
+__global__ __launch_bounds__(NT) void k_kv_store(float* kvc, const float* k, const float* v, int layer, int pos,
+                                                 int MS, int KV) {
+    const int i = blockIdx.x * NT + threadIdx.x;
+    if (i >= KV) return;
+    const size_t base = ((size_t)layer * 2 * MS + pos) * KV + i;
+    kvc[base] = k[i];
+    kvc[base + (size_t)MS * KV] = v[i];
+}
+
+__global__ __launch_bounds__(NT) void k_attention(const float* __restrict__ q, const float* __restrict__ kvc,
+                                                  float* __restrict__ out, int HD, int KV, int S, int kv_mul,
+                                                  int layer, int MS, float scale) {
+    __shared__ float qs[256];
+    __shared__ float sc[ATT_CH];
+    __shared__ float red[NT];
+    __shared__ float sh[4];
+    const int h = blockIdx.x, kh = h / kv_mul;
+    if (threadIdx.x < HD) qs[threadIdx.x] = q[h * HD + threadIdx.x];
+    __syncthreads();
+    const float* kc = kvc + (size_t)layer * 2 * MS * KV + kh * HD;
+    const float* vc = kc + (size_t)MS * KV;
+    attn_head(qs, kc, vc, KV, S, S, nullptr, nullptr, HD, scale, sc, red, sh, out + h * HD);
+}
+
+__global__ __launch_bounds__(NT) void k_add(const float* a, const float* b, float* out, int n) {
+    const int i = blockIdx.x * NT + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* up, float* out, int n) {
+    const int i = blockIdx.x * NT + threadIdx.x;
+    if (i < n) out[i] = silu_mul(gate[i], up[i]);
+}
+
+/* ================================================================== */
+/* LM head: logits[b][r] = sum_j (x[b][j] * inv_b * nw[j]) * W[r][j].
+ * fp32 rows: a lane owns 16 consecutive columns (4 dwordx4 loads per row),
+ * D/16 lanes cover a row, 256/(D/16) rows per pass, HEAD_U passes in flight.
+ * Q8 rows: a lane owns one 32-column block, as in the Q8 matvec.
+ * With st != NULL the workgroup's best (logit, index) goes into st->key[b]
+ * by atomicMax, and the last workgroup to finish turns the keys into
+ * tokens, emits them and advances the position. */
+template <bool Q8>
+__device__ __forceinline__ int head_lanes(int D) { return Q8 ? D / 32 : D / 16; }
+
+template <bool Q8>
+__global__ __launch_bounds__(NT) void k_head(DecHead a) {
+    __shared__ float red[NT * HEAD_U];
+    __shared__ float sh[4];
+    __shared__ unsigned long long shk[NT / 64];
+    __shared__ int last_wg;
+    const int t = threadIdx.x;
+    const int D = a.D;
+    const int nseg = head_lanes<Q8>(D);
+    const int slots = NT / nseg;
+    const int rows_per_tile = slots * HEAD_U;
+    const int slot = t / nseg, sg = t - slot * nseg;
+    const bool lane_on = slot < slots;
+    const long row0 = (long)blockIdx.x * rows_per_tile;
+
+    /* issue this tile's weight loads first; they do not depend on x */
+    float wf[HEAD_U][16];
+    Blk wb[HEAD_U];
+#pragma unroll
+    for (int u = 0; u < HEAD_U; u++) {
+        const long r = row0 + slot + (long)u * slots;
+        const bool ok = lane_on && r < a.V;
+        if (Q8) {
+            wb[u] = ok ? load_block(a.wq + ((size_t)r * nseg + sg) * 36) : zero_block();
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (ok) __builtin_memcpy(&v4, __builtin_assume_aligned(a.w + (size_t)r * D + 16 * sg + i, 4), 16);
+                wf[u][i] = v4.x; wf[u][i + 1] = v4.y; wf[u][i + 2] = v4.z; wf[u][i + 3] = v4.w;
+            }
+        }
+    }
+
+    for (int b = 0; b < a.B; b++) {
+        const float* xb = a.x + (size_t)b * D;
+        const float inv = rms_inv(xb, D, a.eps, sh);
+        constexpr int SEG = Q8 ? 32 : 16;
+        float xs[SEG];
+        if (lane_on) {
+#pragma unroll
+            for (int i = 0; i < SEG; i++) xs[i] = (xb[SEG * sg + i] * inv) * a.norm_w[SEG * sg + i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < SEG; i++) xs[i] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < HEAD_U; u++) {
+            float p;
+            if (Q8) {
+                p = block_dot(wb[u], xs);
+            } else {
+                float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    p0 = fmaf(xs[i], wf[u][i], p0);
+                    p1 = fmaf(xs[i + 1], wf[u][i + 1], p1);
+                    p2 = fmaf(xs[i + 2], wf[u][i + 2], p2);
+                    p3 = fmaf(xs[i + 3], wf[u][i + 3], p3);
+                }
+                p = (p0 + p1) + (p2 + p3);
+            }
+            if (lane_on) red[(slot + u * slots) * nseg + sg] = p;
+        }
+        __syncthreads();
+        unsigned long long best = 0ull;
+        for (int rl = t; rl < rows_per_tile; rl += NT) {
+            const long r = row0 + rl;
+            if (r < a.V) {
+                const float* rp = red + rl * nseg;
+                float acc = 0.0f;
+                for (int k = 0; k < nseg; k++) acc += rp[k];
+                a.logits[(size_t)b * a.V + r] = acc;
+                const unsigned long long kk = argmax_key(acc, (int)r);
+                best = kk > best ? kk : best;
+            }
+        }
+        if (a.st) {
+            best = block_argmax_key(best, shk);
+            if (t == 0) atomicMax(&a.st->key[b], best);
+        } else {
+            __syncthreads(); /* red[] is rewritten for the next row of the batch */
+        }
+    }
+
+    if (!a.st) return;
+    /* last workgroup: emit the step's tokens and advance the position */
+    if (t == 0) {
+        __threadfence();
+        const unsigned int prev = atomicAdd(&a.st->done, 1u);
+        last_wg = (prev == (unsigned int)a.tiles - 1u);
+    }
+    __syncthreads();
+    if (!last_wg) return;
+    __threadfence();
+    DecState* st = a.st;
+    const int pos = st->pos;
+    const bool emit = !st->host_mode && pos >= st->n_prompt - 1;
+    for (int b = t; b < a.B; b += NT) {
+        const unsigned long long k = atomicAdd(&st->key[b], 0ull);
+        const int tok = argmax_key_index(k);
+        st->last_token[b] = tok;
+        if (emit) a.out_tokens[(size_t)st->n_out * a.B + b] = tok;
+        st->key[b] = 0ull;
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (emit) st->n_out = st->n_out + 1;
+        st->done = 0u;
+        st->pos = pos + 1;
+        __threadfence();
+    }
+}
+
+/* argmax_f32: first index of the maximum of v[0..n) (reference tools/run.c:56-60). */
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, int n, int* out) {
+    __shared__ unsigned long long shk[16];
+    unsigned long long best = 0ull;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const unsigned long long k = argmax_key(v[i], i);
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        unsigned long long o = __shfl_xor(best, off, 64);
+        best = o > best ? o : best;
+    }
+    if ((threadIdx.x & 63) == 0) shk[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long r = shk[0];
+        for (int i = 1; i < 16; i++) r = shk[i] > r ? shk[i] : r;
+        out[0] = argmax_key_index(r);
+    }
+}
+
+/* ================================================================== */
+/* Fused engine kernels */
+
+/* x[b] = emb[token_b]; token_b from the host, the prompt, or the last argmax. */
+__global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
+    __shared__ int tok_s[DEC_MAX_B];
+    DecState* st = a.st;
+    const int B = st->B, pos = st->pos;
+    for (int b = threadIdx.x; b < B; b += NT) {
+        int tok;
+        if (st->host_mode) tok = st->host_token[b];
+        else if (pos < st->n_prompt) tok = a.prompt[(size_t)b * st->n_prompt + pos];
+        else tok = st->last_token[b];
+        if (tok < 0 || tok >= a.V) {
+            st->bad_token = 1;
+            tok = 0;
+        }
+        st->token[b] = tok;
+        tok_s[b] = tok;
+    }
+    __syncthreads();
+    for (int b = 0; b < B; b++) {
+        const float* er = a.emb + (size_t)tok_s[b] * a.D;
+        float* xr = a.x + (size_t)b * a.D;
+        for (int j = threadIdx.x; j < a.D; j += NT) xr[j] = er[j];
+    }
+}
+
+/* Fused Q8 matvec phase (see DecMv).  Lane t owns block column t % nb of
+ * row slot t / nb; MV_U row passes are loaded before any arithmetic. */
+__global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
+    __shared__ float red[NT * MV_U];
+    __shared__ float sh[4];
+    const int t = threadIdx.x;
+    int mi = 0;
+    while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
+    const int tile = (int)blockIdx.x - a.tile0[mi];
+    const int nb = a.C / 32;
+    const int slots = NT / nb;
+    const int rows_per_tile = slots * MV_U;
+    const int slot = t / nb, bc = t - slot * nb;
+    const bool lane_on = slot < slots;
+    const long row0 = (long)tile * rows_per_tile;
+    const size_t row_bytes = (size_t)nb * 36;
+    const bool glu = a.glu != 0;
+    const int OC = a.OC[mi];
+    const long nrows = glu ? 2L * OC : (long)OC;
+
+    Blk blk[MV_U];
+#pragma unroll
+    for (int u = 0; u < MV_U; u++) {
+        const long lr = row0 + slot + (long)u * slots;
+        if (lane_on && lr < nrows) {
+            const unsigned char* wm = glu ? a.w[lr & 1] : a.w[mi];
+            const long r = glu ? (lr >> 1) : lr;
+            blk[u] = load_block(wm + (size_t)r * row_bytes + (size_t)bc * 36);
+        } else {
+            blk[u] = zero_block();
+        }
+    }
+
+    for (int b = 0; b < a.B; b++) {
+        const float* xb = a.x + (size_t)b * a.ldx;
+        float inv = 1.0f;
+        if (a.norm_w) inv = rms_inv(xb, a.C, a.eps, sh);
+        float xs[32];
+        if (lane_on) {
+            const float* xp = xb + 32 * bc;
+#pragma unroll
+            for (int i = 0; i < 32; i += 4) {
+                float4 v4;
+                __builtin_memcpy(&v4, __builtin_assume_aligned(xp + i, 4), 16);
+                xs[i] = v4.x; xs[i + 1] = v4.y; xs[i + 2] = v4.z; xs[i + 3] = v4.w;
+            }
+            if (a.norm_w) {
+                const float* nw = a.norm_w + 32 * bc;
+#pragma unroll
+                for (int i = 0; i < 32; i++) xs[i] = (xs[i] * inv) * nw[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 32; i++) xs[i] = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < MV_U; u++)
+            if (lane_on) red[(slot + u * slots) * nb + bc] = block_dot(blk[u], xs);
+        __syncthreads();
+        if (glu) {
+            const int half = rows_per_tile / 2;
+            for (int rl = t; rl < half; rl += NT) {
+                const long j = (row0 >> 1) + rl;
+                if (j < OC) {
+                    const float* rg = red + (2 * rl) * nb;
+                    const float* ru = rg + nb;
+                    float g = 0.0f, u = 0.0f;
+                    for (int k = 0; k < nb; k++) {
+                        g += rg[k];
+                        u += ru[k];
+                    }
+                    a.y[0][(size_t)b * OC + j] = silu_mul(g, u);
+                }
+            }
+        } else {
+            for (int rl = t; rl < rows_per_tile; rl += NT) {
+                const long r = row0 + rl;
+                if (r >= OC) break;
+                const float* rp = red + rl * nb;
+                float acc = 0.0f;
+                for (int k = 0; k < nb; k++) acc += rp[k];
+                float* yp = a.y[mi] + (size_t)b * OC + r;
+                *yp = a.residual ? *yp + acc : acc;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/* Rope + KV append + attention.  Workgroup (h, b): query head h of sequence b.
+ * Every workgroup of a KV group ropes that group's key itself (same
+ * instructions, same bits) and uses it for the current position; the
+ * first query head of the group also appends k and v to the cache. */
+__global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
+    __shared__ float qs[256];
+    __shared__ float ks[256];
+    __shared__ float vs[256];
+    __shared__ float sc[ATT_CH];
+    __shared__ float red[NT];
+    __shared__ float sh[4];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int HD = a.HD, hd2 = HD / 2, kv_mul = a.NH / a.NKV, kh = h / kv_mul;
+    const int pos = a.st->pos;
+    const float* qh = a.q + (size_t)b * a.NH * HD + h * HD;
+    const float* kr = a.k + (size_t)b * a.KV + kh * HD;
+    const float* vr = a.v + (size_t)b * a.KV + kh * HD;
+    const int t = threadIdx.x;
+    if (t < hd2) {
+        const float fr = a.inv_freq[t];
+        const float ang = (float)pos * fr;
+        const float c = cosf(ang), s = sinf(ang);
+        const float q0 = qh[t], q1 = qh[t + hd2];
+        qs[t] = q0 * c - q1 * s;
+        qs[t + hd2] = q0 * s + q1 * c;
+        const float k0 = kr[t], k1 = kr[t + hd2];
+        ks[t] = k0 * c - k1 * s;
+        ks[t + hd2] = k0 * s + k1 * c;
+    }
+    if (t < HD) vs[t] = vr[t];
+    __syncthreads();
+    float* kc = a.kvc + (((size_t)b * a.L + a.layer) * 2 * a.MS) * a.KV + kh * HD;
+    float* vc = kc + (size_t)a.MS * a.KV;
+    if (h % kv_mul == 0 && t < HD) {
+        kc[(size_t)pos * a.KV + t] = ks[t];
+        vc[(size_t)pos * a.KV + t] = vs[t];
+    }
+    attn_head(qs, kc, vc, a.KV, pos + 1, pos, ks, vs, HD, a.scale, sc, red, sh,
+              a.out + (size_t)b * a.NH * HD + h * HD);
+}
+
+} // namespace
+
+/* Inverse frequency of every rotary pair i < HD/2 (reference
+ * src/kernels/forward.metal:1260-1279, including the llama3 frequency
+ * scaling selected by r[5]), evaluated on the host in fp32 with the C
+ * library's powf.  The table, not theta, goes to the device: the angle
+ * (float)pos * inv is taken in fp32, so a one-ulp difference in inv moves
+ * the angle by about pos ulps, and a host table keeps the frequencies
+ * bit-identical to the CPU oracle's. */
+extern "C" void bmk_rope_table(const float r[6], int hd, float* inv_out) {
+    for (int i = 0; i < hd / 2; i++) {
+        float inv = 1.0f / powf(r[0], (float)(2 * i) / (float)hd);
+        if (r[5] > 0.5f) {
+            const float pi = 3.14159265358979323846f;
+            const float factor = r[1], low = r[2], high = r[3], orig = r[4];
+            const float wavelen = 2.0f * pi / inv;
+            const float low_w = orig / low, high_w = orig / high;
+            if (wavelen > low_w) inv /= factor;
+            if (wavelen >= high_w && wavelen <= low_w) {
+                const float smooth = (orig / wavelen - low) / (high - low);
+                inv = (1.0f - smooth) * inv / factor + smooth * inv;
+            }
+        }
+        inv_out[i] = inv;
+    }
+}
+
+/* ================================================================== */
+/* Launchers of the reference-named kernels (buffer orders: reference
+ * src/baremetal/scheduler.c:835-947). */
+
+/* rmsnorm_forward_v2 {inp [N][C], weight [C], out [N][C], params int{N, C}, eps float} */
+extern "C" int bmk_launch_rmsnorm(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 3, 8, "params");
+    BMK_NEED_BYTES(a, 4, 4, "eps");
+    const int N = bmk_pi(a, 3, 0), C = bmk_pi(a, 3, 1);
+    const float eps = bmk_pf(a, 4, 0);
+    BMK_REQUIRE(N >= 0 && C > 0, "rmsnorm: bad shape N=%d C=%d", N, C);
+    if (N == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)N * C * 4, "inp");
+    BMK_NEED_BYTES(a, 1, (size_t)C * 4, "weight");
+    BMK_NEED_BYTES(a, 2, (size_t)N * C * 4, "out");
+    hipLaunchKernelGGL(k_rmsnorm, dim3(N), dim3(NT), 0, a->stream, (const float*)a->dev[0], (const float*)a->dev[1],
+                       (float*)a->dev[2], C, eps);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* rope_forward {q [NH][HD], k [NKV][HD], head_size int, pos int, rope float[6], n_kv_heads int};
+ * NH is the Metal grid width (one thread per head, reference scheduler.c:982-984). */
+extern "C" int bmk_launch_rope(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 4, "head_size");
+    BMK_NEED_BYTES(a, 3, 4, "pos");
+    BMK_NEED_BYTES(a, 4, 24, "rope");
+    BMK_NEED_BYTES(a, 5, 4, "n_kv_heads");
+    const int HD = bmk_pi(a, 2, 0), pos = bmk_pi(a, 3, 0), NKV = bmk_pi(a, 5, 0), NH = a->grid[0];
+    BMK_REQUIRE(HD > 0 && HD % 2 == 0 && NH >= 0 && NKV >= 0 && NKV <= NH && pos >= 0,
+                "rope: bad shape HD=%d NH=%d NKV=%d pos=%d", HD, NH, NKV, pos);
+    if (NH == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)NH * HD * 4, "q");
+    BMK_NEED_BYTES(a, 1, (size_t)NKV * HD * 4, "k");
+    BMK_REQUIRE(HD <= DEC_MAX_HD, "rope: head_size %d above %d", HD, DEC_MAX_HD);
+    float r[6];
+    for (int i = 0; i < 6; i++) r[i] = bmk_pf(a, 4, i);
+    RopeTab rt;
+    bmk_rope_table(r, HD, rt.inv);
+    const int n = NH * (HD / 2);
+    hipLaunchKernelGGL(k_rope, dim3((n + NT - 1) / NT), dim3(NT), 0, a->stream, (float*)a->dev[0], (float*)a->dev[1],
+                       NH, NKV, HD, pos, rt);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* kv_store {kv cache [L][2][MS][KV], k [KV], v [KV], params int{layer, pos, MS, KV}} */
+extern "C" int bmk_launch_kv_store(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 3, 16, "params");
+    const int layer = bmk_pi(a, 3, 0), pos = bmk_pi(a, 3, 1), MS = bmk_pi(a, 3, 2), KV = bmk_pi(a, 3, 3);
+    BMK_REQUIRE(layer >= 0 && MS > 0 && pos >= 0 && pos < MS && KV >= 0, "kv_store: bad params layer=%d pos=%d MS=%d KV=%d",
+                layer, pos, MS, KV);
+    if (KV == 0) return 0;
+    BMK_NEED_BYTES(a, 0, ((size_t)layer * 2 + 2) * MS * KV * 4, "kv cache");
+    BMK_NEED_BYTES(a, 1, (size_t)KV * 4, "k");
+    BMK_NEED_BYTES(a, 2, (size_t)KV * 4, "v");
+    hipLaunchKernelGGL(k_kv_store, dim3((KV + NT - 1) / NT), dim3(NT), 0, a->stream, (float*)a->dev[0],
+                       (const float*)a->dev[1], (const float*)a->dev[2], layer, pos, MS, KV);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* attention_forward {q [NH][HD], kv cache, out [NH][HD],
+ *                    params int{NH, HD, NKV, KV, S, kv_mul, layer, MS}, scale float} */
+extern "C" int bmk_launch_attention(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 3, 32, "params");
+    BMK_NEED_BYTES(a, 4, 4, "scale");
+    const int NH = bmk_pi(a, 3, 0), HD = bmk_pi(a, 3, 1), KV = bmk_pi(a, 3, 3), S = bmk_pi(a, 3, 4);
+    const int kv_mul = bmk_pi(a, 3, 5), layer = bmk_pi(a, 3, 6), MS = bmk_pi(a, 3, 7);
+    const float scale = bmk_pf(a, 4, 0);
+    BMK_REQUIRE(NH > 0 && HD > 0 && HD <= 256 && 256 % HD == 0 && HD % 4 == 0 && kv_mul > 0 && layer >= 0 && MS > 0 &&
+                    S >= 1 && S <= MS && ((NH - 1) / kv_mul + 1) * HD <= KV,
+                "attention: bad params NH=%d HD=%d KV=%d S=%d kv_mul=%d layer=%d MS=%d", NH, HD, KV, S, kv_mul, layer,
+                MS);
+    BMK_NEED_BYTES(a, 0, (size_t)NH * HD * 4, "q");
+    BMK_NEED_BYTES(a, 1, ((size_t)layer * 2 + 2) * MS * KV * 4, "kv cache");
+    BMK_NEED_BYTES(a, 2, (size_t)NH * HD * 4, "out");
+    BMK_REQUIRE(((uintptr_t)a->dev[1] & 15) == 0 && KV % 4 == 0, "attention: kv cache rows must be 16-byte aligned");
+    hipLaunchKernelGGL(k_attention, dim3(NH), dim3(NT), 0, a->stream, (const float*)a->dev[0], (const float*)a->dev[1],
+                       (float*)a->dev[2], HD, KV, S, kv_mul, layer, MS, scale);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* add_forward {a, b, out, n int} */
+extern "C" int bmk_launch_add(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 3, 4, "n");
+    const int n = bmk_pi(a, 3, 0);
+    BMK_REQUIRE(n >= 0, "add: n=%d", n);
+    if (n == 0) return 0;
+    for (int i = 0; i < 3; i++) BMK_NEED_BYTES(a, i, (size_t)n * 4, "operand");
+    hipLaunchKernelGGL(k_add, dim3((n + NT - 1) / NT), dim3(NT), 0, a->stream, (const float*)a->dev[0],
+                       (const float*)a->dev[1], (float*)a->dev[2], n);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* swiglu_forward {gate, up, out, N int} */
+extern "C" int bmk_launch_swiglu(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 3, 4, "N");
+    const int n = bmk_pi(a, 3, 0);
+    BMK_REQUIRE(n >= 0, "swiglu: N=%d", n);
+    if (n == 0) return 0;
+    for (int i = 0; i < 3; i++) BMK_NEED_BYTES(a, i, (size_t)n * 4, "operand");
+    hipLaunchKernelGGL(k_swiglu, dim3((n + NT - 1) / NT), dim3(NT), 0, a->stream, (const float*)a->dev[0],
+                       (const float*)a->dev[1], (float*)a->dev[2], n);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+static int head_tiles(int D, int V, bool q8) {
+    const int nseg = q8 ? D / 32 : D / 16;
+    const int rows = (NT / nseg) * HEAD_U;
+    return (V + rows - 1) / rows;
+}
+
+static bool head_shape_ok(int D, bool q8) {
+    return q8 ? (D % 32 == 0 && D / 32 <= NT) : (D % 16 == 0 && D / 16 <= NT);
+}
+
+/* rmsnorm_matmul_forward {x [C], norm weight [C], wcls f32 [V][C], logits [V], params int{C, V}, eps float} */
+extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 4, 8, "params");
+    BMK_NEED_BYTES(a, 5, 4, "eps");
+    const int C = bmk_pi(a, 4, 0), V = bmk_pi(a, 4, 1);
+    BMK_REQUIRE(C > 0 && V >= 0 && head_shape_ok(C, false), "rmsnorm_matmul: C=%d must be a multiple of 16 up to 4096", C);
+    if (V == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)C * 4, "x");
+    BMK_NEED_BYTES(a, 1, (size_t)C * 4, "norm weight");
+    BMK_NEED_BYTES(a, 2, (size_t)V * C * 4, "wcls");
+    BMK_NEED_BYTES(a, 3, (size_t)V * 4, "logits");
+    BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1] | (uintptr_t)a->dev[2]) & 3) == 0,
+                "rmsnorm_matmul: misaligned operand");
+    DecHead h;
+    memset(&h, 0, sizeof h);
+    h.x = (const float*)a->dev[0];
+    h.norm_w = (const float*)a->dev[1];
+    h.w = (const float*)a->dev[2];
+    h.logits = (float*)a->dev[3];
+    h.D = C;
+    h.V = V;
+    h.B = 1;
+    h.eps = bmk_pf(a, 5, 0);
+    h.tiles = head_tiles(C, V, false);
+    hipLaunchKernelGGL(k_head<false>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* argmax_f32 {values f32 [n], out int [1], params int{n}} */
+extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 4, "params");
+    const int n = bmk_pi(a, 2, 0);
+    BMK_REQUIRE(n > 0, "argmax: n=%d", n);
+    BMK_NEED_BYTES(a, 0, (size_t)n * 4, "values");
+    BMK_NEED_BYTES(a, 1, 4, "out");
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, a->stream, (const float*)a->dev[0], n, (int*)a->dev[1]);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* ================================================================== */
+/* Engine-side launchers (arguments already validated by engine.cpp). */
+
+extern "C" int dec_mv_tiles(int OC, int C, int glu) {
+    const int nb = C / 32;
+    const int rows = (NT / nb) * MV_U;
+    const long n = glu ? 2L * OC : (long)OC;
+    return (int)((n + rows - 1) / rows);
+}
+
+extern "C" int dec_head_tiles(int D, int V, int q8) { return head_tiles(D, V, q8 != 0); }
+
+extern "C" int dec_launch_embed(const DecEmbed* a, hipStream_t s) {
+    hipLaunchKernelGGL(k_embed, dim3(1), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_launch_mv(const DecMv* a, hipStream_t s) {
+    hipLaunchKernelGGL(k_dec_mv, dim3(a->tile0[a->nmat]), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
+    hipLaunchKernelGGL(k_dec_attn, dim3(a->NH, B), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_launch_head(const DecHead* a, hipStream_t s) {
+    if (a->wq)
+        hipLaunchKernelGGL(k_head<true>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    else
+        hipLaunchKernelGGL(k_head<false>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}

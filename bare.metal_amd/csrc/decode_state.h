@@ -1,0 +1,104 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * decode_state.h — the device-resident state of a decode session and the
+ * argument blocks of the fused decode kernels (decode.hip), shared with the
+ * host engine (engine.cpp).
+ *
+ * Every value that changes from one token to the next (position, input
+ * token, argmax) lives in DecState in device memory, so the kernels of one
+ * step take identical arguments at every step and the step is captured once
+ * into a hipGraph and replayed.  All B sequences of a batched session are
+ * at the same position (they are stepped in lockstep).
+ */
+#ifndef BMK_DECODE_STATE_H
+#define BMK_DECODE_STATE_H
+
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+/* RoPE inverse frequencies of pairs 0..hd/2-1 from r = {theta, factor,
+ * low, high, original max, llama3 flag} (decode.hip). */
+void bmk_rope_table(const float r[6], int hd, float* inv_out);
+#ifdef __cplusplus
+}
+#endif
+
+#define DEC_MAX_B 64
+#define DEC_MAX_MATS 3
+#define DEC_MAX_HD 256
+
+typedef struct {
+    int pos;          /* position of the step being run; the last head workgroup advances it */
+    int n_prompt;     /* generation mode: prompt length */
+    int n_out;        /* generation mode: steps whose argmax has been emitted */
+    int host_mode;    /* 1: the input tokens come from host_token[], 0: prompt, then last_token */
+    unsigned int done;/* head workgroups finished in the current step */
+    int B;
+    int bad_token;    /* set when an input token was outside [0, V) (0 was used instead) */
+    int pad_;
+    int token[DEC_MAX_B];        /* input token of the current step */
+    int host_token[DEC_MAX_B];
+    int last_token[DEC_MAX_B];   /* argmax of the last finished step */
+    unsigned long long key[DEC_MAX_B]; /* running argmax of the current step, packed (value, ~index) */
+} DecState;
+
+/* One fused Q8 matvec phase: y_i = W_i * f(x) for up to three matrices that
+ * share the input, f = identity or RMSNorm(x) * norm_w.
+ *  glu      : W_0 = gate, W_1 = up; y_0 = silu(gate x) * (up x)
+ *  residual : y_0 += previous y_0 (y_0 is the residual stream, updated in place)
+ * Batched: B input rows (stride ldx); y_i row b at y_i + b * OC_i. */
+typedef struct {
+    const float* x;
+    const float* norm_w;       /* NULL: no norm */
+    float eps;
+    int C;
+    int B;
+    int ldx;
+    int nmat;
+    int glu;
+    int residual;
+    int pad_;
+    const unsigned char* w[DEC_MAX_MATS];
+    float* y[DEC_MAX_MATS];
+    int OC[DEC_MAX_MATS];
+    int tile0[DEC_MAX_MATS + 1];   /* workgroup prefix: matrix i owns tiles tile0[i] .. tile0[i+1]-1 */
+} DecMv;
+
+/* Rope + KV append + GQA attention for one layer of a decode step. */
+typedef struct {
+    const float* q;     /* [B][NH*HD] un-roped */
+    const float* k;     /* [B][KV] un-roped */
+    const float* v;     /* [B][KV] */
+    float* kvc;         /* [B][L][2][MS][KV] */
+    float* out;         /* [B][NH*HD] */
+    const DecState* st;
+    float inv_freq[DEC_MAX_HD / 2]; /* RoPE inverse frequency per rotary pair (host table) */
+    float scale;
+    int NH, NKV, HD, KV, MS, L, layer;
+} DecAttn;
+
+/* Final RMSNorm + LM head (fp32 rows, or Q8 rows when wq != NULL) + argmax. */
+typedef struct {
+    const float* x;      /* [B][D] */
+    const float* norm_w;
+    const float* w;      /* fp32 [V][D] */
+    const unsigned char* wq; /* Q8 [V][D/32] blocks, or NULL */
+    float* logits;       /* [B][V] */
+    DecState* st;
+    int* out_tokens;     /* [n_gen][B] (generation mode) */
+    int D, V, B, tiles;
+    float eps;
+} DecHead;
+
+/* Input embedding of a decode step: x[b] = emb[token_b]. */
+typedef struct {
+    const float* emb;    /* [V][D] */
+    const int* prompt;   /* [B][n_prompt] (generation mode) */
+    float* x;            /* [B][D] */
+    DecState* st;
+    int D, V;
+} DecEmbed;
+
+#endif

@@ -1,0 +1,793 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * engine.cpp — the decode engine behind include/baremetal.h on MI355X.
+ *
+ * Reference behaviour kept (reference src/baremetal/session.c:34-185,
+ * graph.c:109-240, scheduler.c:712-996, tools/run.c:121-185):
+ *   per layer  RMSNorm -> q,k,v (Q8) -> RoPE -> KV append + attention over
+ *   pos+1 keys -> o (Q8) -> residual add -> RMSNorm -> gate, up (Q8) ->
+ *   SwiGLU -> down (Q8) -> residual add; then the final RMSNorm and the LM
+ *   head over the tied fp32 embedding; greedy = first maximal logit.
+ *
+ * MI355X design:
+ *   - weights live in HBM: one Q8 arena for every projection (packed on the
+ *     device by quantize_q8 from the host fp32 copy), fp32 embedding/head
+ *     and norm gains; fp32 KV cache [B][L][2][MS][KV];
+ *   - a step is 2 + 5L kernels (embed; per layer: RMSNorm+qkv, rope+KV
+ *     append+attention, o+residual, RMSNorm+gate/up+SwiGLU,
+ *     down+residual; head+argmax), see decode.hip;
+ *   - the position, the input tokens and the argmax live in device memory
+ *     (DecState), so the step is captured once into a hipGraph and
+ *     replayed; greedy generation runs with no host round trip per token;
+ *   - everything is ordered on the backend context's one stream.
+ */
+#include "bmk.h"
+#include "decode_state.h"
+#include "../../include/backend.h"
+#include "../../include/backend_hip_device.h"
+#include "../../include/baremetal.h"
+#include "../../include/bm_synth.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+extern "C" {
+int dec_mv_tiles(int OC, int C, int glu);
+int dec_head_tiles(int D, int V, int q8);
+int dec_launch_embed(const DecEmbed* a, hipStream_t s);
+int dec_launch_mv(const DecMv* a, hipStream_t s);
+int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
+int dec_launch_head(const DecHead* a, hipStream_t s);
+int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
+}
+
+#define HIP_TRY(call, what, fail)                                                   \
+    do {                                                                            \
+        hipError_t e_ = (call);                                                     \
+        if (e_ != hipSuccess) {                                                     \
+            BMK_ERR("%s: %s", what, hipGetErrorString(e_));                         \
+            fail;                                                                   \
+        }                                                                           \
+    } while (0)
+
+struct bm_context_s {
+    backend_ctx_t* be;
+    hipStream_t s;
+};
+
+enum { T_EMB, T_LN1, T_LN2, T_LNF, T_WQ, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_COUNT };
+static const char* const k_tensor_names[T_COUNT] = {"token_embedding", "ln1", "ln2", "lnf", "wq", "wk",
+                                                     "wv", "wo", "w_gate", "w_up", "w_down"};
+
+struct bm_model_s {
+    bm_context_t* ctx;
+    bm_arch_t arch;
+    int D, H, NH, NKV, HD, KV, QD, L, V;
+    int quant_bits;
+    int q8_head;
+    float* host[T_COUNT];   /* fp32 weights in the reference layout */
+    size_t count[T_COUNT];
+    int set[T_COUNT];
+    /* device */
+    int compiled;
+    float* d_emb;
+    float* d_ln1;
+    float* d_ln2;
+    float* d_lnf;
+    unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down */
+    unsigned char* d_head8;  /* Q8 head rows (q8_head) */
+    size_t off[7];           /* byte offset of each matrix inside one layer's slice */
+    size_t layer_bytes;
+    int nsessions;
+};
+
+struct bm_session_s {
+    bm_context_t* ctx;
+    bm_model_t* m;
+    int B, MS;
+    float *x, *q, *k, *v, *att, *h, *logits, *kvc;
+    DecState* st;
+    int* prompt;
+    int* out_tokens;
+    int prompt_cap;
+    /* host side */
+    DecState* h_st;      /* pinned staging for state writes */
+    float* h_logits;     /* pinned [B][V] */
+    int* h_io;           /* pinned tokens in/out */
+    size_t h_io_cap;
+    int pos;             /* host mirror of the position */
+    int use_graph;
+    hipGraph_t graph;
+    hipGraphExec_t gexec;
+    int prof_on;
+    double prof_ms;
+    hipEvent_t ev0, ev1;
+};
+
+/* ------------------------------------------------------------------ */
+/* context */
+
+extern "C" bm_context_t* bm_create(bm_device_t device) {
+    if (device != BM_DEVICE_HIP) {
+        BMK_ERR("bm_create: only the GPU device (BM_DEVICE_METAL / BM_DEVICE_HIP) has a backend");
+        return NULL;
+    }
+    backend_ctx_t* be = backend_create();
+    if (!be) return NULL;
+    bm_context_t* c = (bm_context_t*)calloc(1, sizeof(bm_context_t));
+    if (!c) {
+        backend_destroy(be);
+        return NULL;
+    }
+    c->be = be;
+    c->s = (hipStream_t)be->queue;
+    return c;
+}
+
+extern "C" void bm_destroy(bm_context_t* ctx) {
+    if (!ctx) return;
+    backend_destroy(ctx->be);
+    free(ctx);
+}
+
+extern "C" bm_precision_t bm_get_supported_precision(bm_context_t* ctx) {
+    return (ctx && ctx->be && ctx->be->supports_bf16) ? BM_PRECISION_BF16 : BM_PRECISION_FP32;
+}
+
+/* ------------------------------------------------------------------ */
+/* model */
+
+static size_t q8_bytes(size_t n) { return n / 32 * 36; }
+
+extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
+    if (!ctx || !a) return NULL;
+    const int D = a->dim, H = a->hidden_dim, NH = a->n_heads, NKV = a->n_kv_heads, L = a->n_layers, V = a->vocab_size;
+    const int HD = a->head_dim > 0 ? a->head_dim : (NH > 0 ? D / NH : 0);
+    if (D <= 0 || H <= 0 || NH <= 0 || NKV <= 0 || L <= 0 || V <= 0 || HD <= 0 || a->max_seq_len <= 0) {
+        BMK_ERR("bm_create_model: bad dimensions");
+        return NULL;
+    }
+    if (a->norm != BM_NORM_RMSNORM || a->activation != BM_ACT_SWIGLU || !a->gated_mlp || a->pos_enc != BM_POS_ROPE ||
+        a->bias || !a->weight_tie || a->has_qk_norm || a->has_ffn_post_norm || a->gemma_norm || a->embed_scale) {
+        BMK_ERR("bm_create_model: only RMSNorm + SwiGLU + RoPE + tied-embedding models without biases are supported");
+        return NULL;
+    }
+    const int QD = NH * HD, KV = NKV * HD;
+    /* layout constraints of the gfx950 kernels (decode.hip) */
+    if (D % 32 || H % 32 || QD % 32 || D / 32 > 256 || H / 32 > 256 || QD / 32 > 256 || D % 16 || D / 16 > 256 ||
+        NH % NKV || HD > 256 || 256 % HD || HD % 4 || KV % 4) {
+        BMK_ERR("bm_create_model: shape D=%d H=%d NH=%d NKV=%d HD=%d outside the decode kernels' layout", D, H, NH, NKV,
+                HD);
+        return NULL;
+    }
+    bm_model_t* m = (bm_model_t*)calloc(1, sizeof(bm_model_t));
+    if (!m) return NULL;
+    m->ctx = ctx;
+    m->arch = *a;
+    m->D = D; m->H = H; m->NH = NH; m->NKV = NKV; m->HD = HD; m->KV = KV; m->QD = QD; m->L = L; m->V = V;
+    m->quant_bits = 8;
+    const size_t cnt[T_COUNT] = {(size_t)V * D, (size_t)L * D, (size_t)L * D, (size_t)D, (size_t)L * QD * D,
+                                 (size_t)L * KV * D, (size_t)L * KV * D, (size_t)L * D * QD, (size_t)L * H * D,
+                                 (size_t)L * H * D, (size_t)L * D * H};
+    memcpy(m->count, cnt, sizeof cnt);
+    const size_t mats[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
+                            (size_t)H * D, (size_t)H * D, (size_t)D * H};
+    size_t o = 0;
+    for (int i = 0; i < 7; i++) {
+        m->off[i] = o;
+        o += q8_bytes(mats[i]);
+    }
+    m->layer_bytes = o;
+    return m;
+}
+
+static void model_free_device(bm_model_t* m) {
+    hipFree(m->d_emb);
+    hipFree(m->d_ln1);
+    hipFree(m->d_ln2);
+    hipFree(m->d_lnf);
+    hipFree(m->d_q8);
+    hipFree(m->d_head8);
+    m->d_emb = m->d_ln1 = m->d_ln2 = m->d_lnf = NULL;
+    m->d_q8 = m->d_head8 = NULL;
+    m->compiled = 0;
+}
+
+extern "C" void bm_destroy_model(bm_model_t* m) {
+    if (!m) return;
+    if (m->ctx) hipStreamSynchronize(m->ctx->s);
+    model_free_device(m);
+    for (int i = 0; i < T_COUNT; i++) free(m->host[i]);
+    free(m);
+}
+
+extern "C" int bm_model_set_quant_bits(bm_model_t* m, int bits) {
+    if (!m) return -1;
+    if (bits != 8) {
+        BMK_ERR("bm_model_set_quant_bits: the MI355X path implements Q8 projections only (got %d)", bits);
+        return -1;
+    }
+    m->quant_bits = 8;
+    return 0;
+}
+
+extern "C" int bm_model_set_q8_head(bm_model_t* m, int on) {
+    if (!m) return -1;
+    if (m->compiled && (on != 0) != (m->q8_head != 0)) model_free_device(m);
+    m->q8_head = on != 0;
+    return 0;
+}
+
+static float* host_tensor(bm_model_t* m, int t) {
+    if (!m->host[t]) m->host[t] = (float*)malloc(m->count[t] * sizeof(float));
+    return m->host[t];
+}
+
+extern "C" int bm_model_set_tensor(bm_model_t* m, const char* name, const float* data, size_t n) {
+    if (!m || !name || !data) return -1;
+    for (int t = 0; t < T_COUNT; t++) {
+        if (strcmp(name, k_tensor_names[t]) != 0) continue;
+        if (n != m->count[t]) {
+            BMK_ERR("bm_model_set_tensor(%s): %zu elements, expected %zu", name, n, m->count[t]);
+            return -1;
+        }
+        float* dst = host_tensor(m, t);
+        if (!dst) return -1;
+        memcpy(dst, data, n * sizeof(float));
+        m->set[t] = 1;
+        if (m->compiled) model_free_device(m);
+        return 0;
+    }
+    BMK_ERR("bm_model_set_tensor: unknown tensor %s", name);
+    return -1;
+}
+
+extern "C" int bm_model_init_synthetic(bm_model_t* m, uint64_t seed) {
+    if (!m) return -1;
+    const size_t per[T_COUNT] = {0, 0, 0, 0, (size_t)m->QD * m->D, (size_t)m->KV * m->D, (size_t)m->KV * m->D,
+                                 (size_t)m->D * m->QD, (size_t)m->H * m->D, (size_t)m->H * m->D,
+                                 (size_t)m->D * m->H};
+    for (int t = 0; t < T_COUNT; t++)
+        if (!host_tensor(m, t)) return -1;
+    bm_synth_normal_f32(bm_synth_tensor_seed(seed, 5, 0xFFFF, 0), 0.02f, m->host[T_EMB], m->count[T_EMB]);
+    bm_synth_fill_f32(1.0f, m->host[T_LN1], m->count[T_LN1]);
+    bm_synth_fill_f32(1.0f, m->host[T_LN2], m->count[T_LN2]);
+    bm_synth_fill_f32(1.0f, m->host[T_LNF], m->count[T_LNF]);
+    for (int t = T_WQ; t <= T_WD; t++)
+        for (int l = 0; l < m->L; l++)
+            bm_synth_normal_f32(bm_synth_tensor_seed(seed, 5, l, t - T_WQ + 1), 0.02f, m->host[t] + (size_t)l * per[t],
+                                per[t]);
+    for (int t = 0; t < T_COUNT; t++) m->set[t] = 1;
+    if (m->compiled) model_free_device(m);
+    return 0;
+}
+
+static int upload(float** dst, const float* src, size_t n, hipStream_t s) {
+    HIP_TRY(hipMalloc(dst, n * sizeof(float)), "hipMalloc", return -1);
+    HIP_TRY(hipMemcpyAsync(*dst, src, n * sizeof(float), hipMemcpyHostToDevice, s), "hipMemcpy H2D", return -1);
+    return 0;
+}
+
+static int model_compile(bm_model_t* m) {
+    if (m->compiled) return 0;
+    for (int t = 0; t < T_COUNT; t++)
+        if (!m->set[t]) {
+            BMK_ERR("bm_compile: tensor %s was never set", k_tensor_names[t]);
+            return -1;
+        }
+    hipStream_t s = m->ctx->s;
+    if (upload(&m->d_emb, m->host[T_EMB], m->count[T_EMB], s) || upload(&m->d_ln1, m->host[T_LN1], m->count[T_LN1], s) ||
+        upload(&m->d_ln2, m->host[T_LN2], m->count[T_LN2], s) || upload(&m->d_lnf, m->host[T_LNF], m->count[T_LNF], s)) {
+        model_free_device(m);
+        return -1;
+    }
+    HIP_TRY(hipMalloc(&m->d_q8, m->layer_bytes * m->L), "hipMalloc", { model_free_device(m); return -1; });
+    const int D = m->D, H = m->H, QD = m->QD, KV = m->KV;
+    const size_t per[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
+                           (size_t)H * D, (size_t)H * D, (size_t)D * H};
+    const int src_t[7] = {T_WQ, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD};
+    size_t stage_n = (size_t)H * D;
+    if (m->q8_head) stage_n = (size_t)m->V * D > stage_n ? (size_t)m->V * D : stage_n;
+    float* stage = NULL;
+    HIP_TRY(hipMalloc(&stage, stage_n * sizeof(float)), "hipMalloc", { model_free_device(m); return -1; });
+    int rc = 0;
+    for (int l = 0; l < m->L && rc == 0; l++)
+        for (int i = 0; i < 7 && rc == 0; i++) {
+            const float* src = m->host[src_t[i]] + (size_t)l * per[i];
+            if (hipMemcpyAsync(stage, src, per[i] * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
+            else rc = q8_pack_f32(stage, m->d_q8 + (size_t)l * m->layer_bytes + m->off[i], (long)per[i], s);
+        }
+    if (rc == 0 && m->q8_head) {
+        if (hipMalloc(&m->d_head8, q8_bytes((size_t)m->V * D)) != hipSuccess) rc = -1;
+        else rc = q8_pack_f32(m->d_emb, m->d_head8, (long)m->V * D, s);
+    }
+    if (hipStreamSynchronize(s) != hipSuccess) rc = -1;
+    hipFree(stage);
+    if (rc != 0) {
+        BMK_ERR("bm_compile: weight upload / Q8 pack failed");
+        model_free_device(m);
+        return -1;
+    }
+    m->compiled = 1;
+    return 0;
+}
+
+extern "C" void bm_compile(bm_model_t* m) {
+    if (m) (void)model_compile(m);
+}
+
+extern "C" int bm_get_num_parameters(const bm_model_t* m) {
+    if (!m) return 0;
+    size_t n = 0;
+    for (int t = 0; t < T_COUNT; t++) n += m->count[t];
+    return n > 0x7fffffff ? 0x7fffffff : (int)n;
+}
+
+extern "C" const char* bm_get_arch_name(const bm_model_t* m) { return m ? "llama" : NULL; }
+
+/* ------------------------------------------------------------------ */
+/* session */
+
+static int enqueue_step(bm_session_t* S) {
+    bm_model_t* m = S->m;
+    hipStream_t s = S->ctx->s;
+    const int D = m->D, B = S->B;
+    DecEmbed e;
+    e.emb = m->d_emb;
+    e.prompt = S->prompt;
+    e.x = S->x;
+    e.st = S->st;
+    e.D = D;
+    e.V = m->V;
+    if (dec_launch_embed(&e, s)) return -1;
+    const float eps = 1e-5f; /* reference graph.c:134,175,219 */
+    for (int l = 0; l < m->L; l++) {
+        const unsigned char* wl = m->d_q8 + (size_t)l * m->layer_bytes;
+        DecMv mv;
+        memset(&mv, 0, sizeof mv);
+        /* RMSNorm + q, k, v */
+        mv.x = S->x; mv.norm_w = m->d_ln1 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
+        mv.nmat = 3;
+        mv.w[0] = wl + m->off[0]; mv.y[0] = S->q; mv.OC[0] = m->QD;
+        mv.w[1] = wl + m->off[1]; mv.y[1] = S->k; mv.OC[1] = m->KV;
+        mv.w[2] = wl + m->off[2]; mv.y[2] = S->v; mv.OC[2] = m->KV;
+        mv.tile0[0] = 0;
+        for (int i = 0; i < 3; i++) mv.tile0[i + 1] = mv.tile0[i] + dec_mv_tiles(mv.OC[i], D, 0);
+        if (dec_launch_mv(&mv, s)) return -1;
+        /* rope + KV append + attention */
+        DecAttn at;
+        memset(&at, 0, sizeof at);
+        at.q = S->q; at.k = S->k; at.v = S->v; at.kvc = S->kvc; at.out = S->att; at.st = S->st;
+        const float rp[6] = {m->arch.rope_theta, m->arch.rope_factor, m->arch.rope_low_freq_factor,
+                             m->arch.rope_high_freq_factor, m->arch.rope_original_max,
+                             m->arch.rope_scaling == BM_ROPE_LLAMA3 ? 1.0f : 0.0f};
+        bmk_rope_table(rp, m->HD, at.inv_freq);
+        at.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
+        at.NH = m->NH; at.NKV = m->NKV; at.HD = m->HD; at.KV = m->KV; at.MS = S->MS; at.L = m->L; at.layer = l;
+        if (dec_launch_attn(&at, B, s)) return -1;
+        /* o + residual */
+        memset(&mv, 0, sizeof mv);
+        mv.x = S->att; mv.C = m->QD; mv.B = B; mv.ldx = m->QD; mv.nmat = 1; mv.residual = 1;
+        mv.w[0] = wl + m->off[3]; mv.y[0] = S->x; mv.OC[0] = D;
+        mv.tile0[1] = dec_mv_tiles(D, m->QD, 0);
+        if (dec_launch_mv(&mv, s)) return -1;
+        /* RMSNorm + gate, up + SwiGLU */
+        memset(&mv, 0, sizeof mv);
+        mv.x = S->x; mv.norm_w = m->d_ln2 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
+        mv.nmat = 1; mv.glu = 1;
+        mv.w[0] = wl + m->off[4]; mv.w[1] = wl + m->off[5]; mv.y[0] = S->h; mv.OC[0] = m->H;
+        mv.tile0[1] = dec_mv_tiles(m->H, D, 1);
+        if (dec_launch_mv(&mv, s)) return -1;
+        /* down + residual */
+        memset(&mv, 0, sizeof mv);
+        mv.x = S->h; mv.C = m->H; mv.B = B; mv.ldx = m->H; mv.nmat = 1; mv.residual = 1;
+        mv.w[0] = wl + m->off[6]; mv.y[0] = S->x; mv.OC[0] = D;
+        mv.tile0[1] = dec_mv_tiles(D, m->H, 0);
+        if (dec_launch_mv(&mv, s)) return -1;
+    }
+    DecHead hd;
+    memset(&hd, 0, sizeof hd);
+    hd.x = S->x; hd.norm_w = m->d_lnf; hd.w = m->d_emb; hd.wq = m->q8_head ? m->d_head8 : NULL;
+    hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
+    hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
+    hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
+    return dec_launch_head(&hd, s);
+}
+
+static void session_free(bm_session_t* S) {
+    if (!S) return;
+    if (S->ctx) hipStreamSynchronize(S->ctx->s);
+    if (S->gexec) hipGraphExecDestroy(S->gexec);
+    if (S->graph) hipGraphDestroy(S->graph);
+    hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
+    hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->prompt); hipFree(S->out_tokens);
+    if (S->h_st) hipHostFree(S->h_st);
+    if (S->h_logits) hipHostFree(S->h_logits);
+    if (S->h_io) hipHostFree(S->h_io);
+    if (S->ev0) hipEventDestroy(S->ev0);
+    if (S->ev1) hipEventDestroy(S->ev1);
+    if (S->m) S->m->nsessions--;
+    free(S);
+}
+
+/* Writes the whole DecState from the host (stream-ordered). */
+static int state_write(bm_session_t* S) {
+    HIP_TRY(hipMemcpyAsync(S->st, S->h_st, sizeof(DecState), hipMemcpyHostToDevice, S->ctx->s), "state write",
+            return -1);
+    return 0;
+}
+
+static int session_reset_state(bm_session_t* S, int host_mode, int n_prompt) {
+    memset(S->h_st, 0, sizeof(DecState));
+    S->h_st->B = S->B;
+    S->h_st->host_mode = host_mode;
+    S->h_st->n_prompt = n_prompt;
+    S->pos = 0;
+    return state_write(S);
+}
+
+extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t* m, int batch, int max_seq_len) {
+    if (!ctx || !m || m->ctx != ctx) return NULL;
+    if (batch < 1 || batch > DEC_MAX_B) {
+        BMK_ERR("bm_create_session_batched: batch %d outside [1, %d]", batch, DEC_MAX_B);
+        return NULL;
+    }
+    if (model_compile(m) != 0) return NULL;
+    bm_session_t* S = (bm_session_t*)calloc(1, sizeof(bm_session_t));
+    if (!S) return NULL;
+    S->ctx = ctx;
+    S->m = m;
+    m->nsessions++;
+    S->B = batch;
+    S->MS = max_seq_len > 0 ? max_seq_len : m->arch.max_seq_len;
+    S->use_graph = 1;
+    const size_t B = (size_t)batch;
+    const size_t kv_elems = B * m->L * 2 * (size_t)S->MS * m->KV;
+    bool ok = hipMalloc(&S->x, B * m->D * 4) == hipSuccess && hipMalloc(&S->q, B * m->QD * 4) == hipSuccess &&
+              hipMalloc(&S->k, B * m->KV * 4) == hipSuccess && hipMalloc(&S->v, B * m->KV * 4) == hipSuccess &&
+              hipMalloc(&S->att, B * m->QD * 4) == hipSuccess && hipMalloc(&S->h, B * m->H * 4) == hipSuccess &&
+              hipMalloc(&S->logits, B * m->V * 4) == hipSuccess && hipMalloc(&S->kvc, kv_elems * 4) == hipSuccess &&
+              hipMalloc(&S->st, sizeof(DecState)) == hipSuccess &&
+              hipMalloc(&S->out_tokens, B * (size_t)S->MS * 4) == hipSuccess &&
+              hipMalloc(&S->prompt, B * (size_t)S->MS * 4) == hipSuccess &&
+              hipHostMalloc(&S->h_st, sizeof(DecState), hipHostMallocDefault) == hipSuccess &&
+              hipHostMalloc(&S->h_logits, B * m->V * 4, hipHostMallocDefault) == hipSuccess &&
+              hipEventCreate(&S->ev0) == hipSuccess && hipEventCreate(&S->ev1) == hipSuccess;
+    if (ok) {
+        S->prompt_cap = S->MS;
+        S->h_io_cap = B * (size_t)S->MS + 64;
+        ok = hipHostMalloc(&S->h_io, S->h_io_cap * 4, hipHostMallocDefault) == hipSuccess;
+    }
+    /* a cache slot is written before it is read, but start from zeros anyway */
+    if (ok) ok = hipMemsetAsync(S->kvc, 0, kv_elems * 4, ctx->s) == hipSuccess;
+    if (ok) ok = session_reset_state(S, 1, 0) == 0;
+    if (ok) ok = hipStreamSynchronize(ctx->s) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        BMK_ERR("bm_create_session: device allocation failed");
+        session_free(S);
+        return NULL;
+    }
+    return S;
+}
+
+extern "C" bm_session_t* bm_create_session(bm_context_t* ctx, bm_model_t* m) {
+    return bm_create_session_batched(ctx, m, 1, 0);
+}
+
+extern "C" void bm_destroy_session(bm_session_t* S) { session_free(S); }
+
+extern "C" int bm_session_set_graph(bm_session_t* S, int on) {
+    if (!S) return -1;
+    S->use_graph = on != 0;
+    return 0;
+}
+
+static int ensure_graph(bm_session_t* S) {
+    if (S->gexec) return 0;
+    hipStream_t s = S->ctx->s;
+    HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture", return -1);
+    const int rc = enqueue_step(S);
+    hipGraph_t g = NULL;
+    hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != 0 || e != hipSuccess) {
+        BMK_ERR("step capture failed: %s", hipGetErrorString(e));
+        if (g) hipGraphDestroy(g);
+        (void)hipGetLastError();
+        return -1;
+    }
+    HIP_TRY(hipGraphInstantiate(&S->gexec, g, NULL, NULL, 0), "hipGraphInstantiate", {
+        hipGraphDestroy(g);
+        return -1;
+    });
+    S->graph = g;
+    return 0;
+}
+
+static int launch_step(bm_session_t* S) {
+    if (S->pos >= S->MS) {
+        BMK_ERR("decode step: position %d reached max_seq_len %d", S->pos, S->MS);
+        return -1;
+    }
+    if (S->prof_on) HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "hipEventRecord", return -1);
+    if (S->use_graph) {
+        if (ensure_graph(S) != 0) return -1;
+        HIP_TRY(hipGraphLaunch(S->gexec, S->ctx->s), "hipGraphLaunch", return -1);
+    } else if (enqueue_step(S) != 0) {
+        return -1;
+    }
+    if (S->prof_on) {
+        HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "hipEventRecord", return -1);
+        HIP_TRY(hipEventSynchronize(S->ev1), "hipEventSynchronize", return -1);
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess) S->prof_ms += ms;
+    }
+    S->pos++;
+    return 0;
+}
+
+/* Host-driven step: tokens[b] in, logits [B][V] back to the host. */
+static float* step_host(bm_session_t* S, const int* tokens) {
+    bm_model_t* m = S->m;
+    for (int b = 0; b < S->B; b++)
+        if (tokens[b] < 0 || tokens[b] >= m->V) {
+            BMK_ERR("bm_step: token %d outside [0, %d)", tokens[b], m->V);
+            return NULL;
+        }
+    if (!S->h_st->host_mode) { /* leaving generation mode: keep the position */
+        S->h_st->host_mode = 1;
+    }
+    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+    memcpy(S->h_io, tokens, (size_t)S->B * 4);
+    HIP_TRY(hipMemcpyAsync(S->st->host_token, S->h_io, (size_t)S->B * 4, hipMemcpyHostToDevice, S->ctx->s),
+            "token write", return NULL);
+    const int one = 1;
+    memcpy(&S->h_io[S->B], &one, 4);
+    HIP_TRY(hipMemcpyAsync(&S->st->host_mode, &S->h_io[S->B], 4, hipMemcpyHostToDevice, S->ctx->s), "mode write",
+            return NULL);
+    if (launch_step(S) != 0) return NULL;
+    HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)S->B * m->V * 4, hipMemcpyDeviceToHost, S->ctx->s),
+            "logits read", return NULL);
+    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+    return S->h_logits;
+}
+
+extern "C" float* bm_step(bm_session_t* S, int token) {
+    if (!S) return NULL;
+    if (S->B != 1) {
+        BMK_ERR("bm_step: batched session, use bm_step_batch");
+        return NULL;
+    }
+    return step_host(S, &token);
+}
+
+extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
+    if (!S || !tokens) return NULL;
+    return step_host(S, tokens);
+}
+
+extern "C" float* bm_forward(bm_session_t* S, const int* tokens, int n_tokens) {
+    if (!S || (!tokens && n_tokens > 0)) return NULL;
+    float* out = S->h_logits;
+    for (int i = 0; i < n_tokens; i++) {
+        out = bm_step(S, tokens[i]);
+        if (!out) return NULL;
+    }
+    return out;
+}
+
+extern "C" void bm_reset_session(bm_session_t* S) {
+    if (!S) return;
+    hipStreamSynchronize(S->ctx->s);
+    session_reset_state(S, 1, 0);
+    hipStreamSynchronize(S->ctx->s);
+}
+
+extern "C" int bm_generate_greedy(bm_session_t* S, const int* prompt, int n_prompt, int steps, int* out_tokens) {
+    if (!S || !prompt || !out_tokens || n_prompt < 1 || steps < n_prompt || steps > S->MS || n_prompt > S->prompt_cap) {
+        BMK_ERR("bm_generate_greedy: bad arguments (n_prompt=%d steps=%d max_seq_len=%d)", n_prompt, steps, S ? S->MS : 0);
+        return -1;
+    }
+    const size_t np = (size_t)S->B * n_prompt;
+    for (size_t i = 0; i < np; i++)
+        if (prompt[i] < 0 || prompt[i] >= S->m->V) {
+            BMK_ERR("bm_generate_greedy: prompt token %d outside [0, %d)", prompt[i], S->m->V);
+            return -1;
+        }
+    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
+    memcpy(S->h_io, prompt, np * 4);
+    HIP_TRY(hipMemcpyAsync(S->prompt, S->h_io, np * 4, hipMemcpyHostToDevice, S->ctx->s), "prompt write", return -1);
+    if (session_reset_state(S, 0, n_prompt) != 0) return -1;
+    for (int i = 0; i < steps; i++)
+        if (launch_step(S) != 0) return -1;
+    const int n_out = steps - n_prompt + 1;
+    const size_t nt = (size_t)n_out * S->B;
+    HIP_TRY(hipMemcpyAsync(S->h_io, S->out_tokens, nt * 4, hipMemcpyDeviceToHost, S->ctx->s), "tokens read",
+            return -1);
+    HIP_TRY(hipMemcpyAsync(S->h_st, S->st, sizeof(DecState), hipMemcpyDeviceToHost, S->ctx->s), "state read",
+            return -1);
+    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
+    if (S->h_st->n_out != n_out || S->h_st->pos != steps || S->h_st->bad_token) {
+        BMK_ERR("bm_generate_greedy: device state n_out=%d pos=%d bad_token=%d, expected n_out=%d pos=%d",
+                S->h_st->n_out, S->h_st->pos, S->h_st->bad_token, n_out, steps);
+        return -1;
+    }
+    memcpy(out_tokens, S->h_io, nt * 4);
+    return n_out;
+}
+
+extern "C" void bm_profile_begin(bm_session_t* S) {
+    if (!S) return;
+    S->prof_on = 1;
+    S->prof_ms = 0.0;
+}
+
+extern "C" void bm_profile_end(bm_session_t* S, double* attention_ms, double* mlp_ms, double* other_ms) {
+    if (attention_ms) *attention_ms = 0.0;
+    if (mlp_ms) *mlp_ms = 0.0;
+    if (other_ms) *other_ms = S ? S->prof_ms : 0.0;
+    if (S) S->prof_on = 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* sampler: reference src/baremetal/sampler.c:33-81 and tools/run.c:53-104 */
+
+struct bm_sampler_s {
+    int vocab_size;
+    float temperature;
+    float topp;
+    int top_k;
+    unsigned int rng;
+    float* probs;
+    int* idx;
+};
+
+extern "C" bm_sampler_t* bm_create_sampler(int vocab_size, float temp, float topp, uint64_t seed) {
+    if (vocab_size <= 0) return NULL;
+    bm_sampler_t* s = (bm_sampler_t*)calloc(1, sizeof(bm_sampler_t));
+    if (!s) return NULL;
+    s->vocab_size = vocab_size;
+    s->temperature = temp;
+    s->topp = topp;
+    s->rng = (unsigned int)seed;
+    s->probs = (float*)malloc((size_t)vocab_size * sizeof(float));
+    s->idx = (int*)malloc((size_t)vocab_size * sizeof(int));
+    if (!s->probs || !s->idx) {
+        bm_destroy_sampler(s);
+        return NULL;
+    }
+    return s;
+}
+
+extern "C" void bm_destroy_sampler(bm_sampler_t* s) {
+    if (!s) return;
+    free(s->probs);
+    free(s->idx);
+    free(s);
+}
+
+static int argmax_first(const float* v, int n) {
+    int best = 0;
+    for (int i = 1; i < n; i++)
+        if (v[i] > v[best]) best = i;
+    return best;
+}
+
+static const float* g_sort_vals;
+static int cmp_desc(const void* a, const void* b) {
+    const float fa = g_sort_vals[*(const int*)a], fb = g_sort_vals[*(const int*)b];
+    return fa > fb ? -1 : (fa < fb ? 1 : 0);
+}
+
+/* temperature -> softmax -> top-k mask -> top-p mask -> inverse-CDF draw */
+static int sample_probs(float* p, int* idx, int n, float temperature, int top_k, float top_p, unsigned int rng_state,
+                        const float* logits) {
+    if (temperature <= 0.0f) return argmax_first(logits, n);
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) {
+        p[i] = logits[i] / temperature;
+        if (p[i] > mx) mx = p[i];
+    }
+    float sum = 0.0f;
+    for (int i = 0; i < n; i++) {
+        p[i] = expf(p[i] - mx);
+        sum += p[i];
+    }
+    for (int i = 0; i < n; i++) p[i] /= sum;
+    if ((top_k > 0 && top_k < n) || (top_p > 0.0f && top_p < 1.0f)) {
+        for (int i = 0; i < n; i++) idx[i] = i;
+        g_sort_vals = p;
+        qsort(idx, n, sizeof(int), cmp_desc);
+    }
+    if (top_k > 0 && top_k < n) {
+        const float thresh = p[idx[top_k - 1]];
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) {
+            if (p[i] < thresh) p[i] = 0.0f;
+            s += p[i];
+        }
+        if (s > 0.0f)
+            for (int i = 0; i < n; i++) p[i] /= s;
+    }
+    if (top_p > 0.0f && top_p < 1.0f) {
+        float cum = 0.0f, cut = 0.0f;
+        for (int i = 0; i < n; i++) {
+            cum += p[idx[i]];
+            if (cum >= top_p) {
+                cut = p[idx[i]];
+                break;
+            }
+        }
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) {
+            if (p[i] < cut) p[i] = 0.0f;
+            s += p[i];
+        }
+        if (s > 0.0f)
+            for (int i = 0; i < n; i++) p[i] /= s;
+    }
+    float sum2 = 0.0f;
+    for (int i = 0; i < n; i++) sum2 += p[i];
+    unsigned int r = rng_state * 1664525u + 1013904223u;
+    r ^= r >> 13;
+    r *= 1274126177u;
+    r ^= r >> 16;
+    const float target = ((float)(r & 0xFFFFFF) / (float)0x1000000) * sum2;
+    float c = 0.0f;
+    for (int i = 0; i < n; i++) {
+        c += p[i];
+        if (c >= target && p[i] > 0.0f) return i;
+    }
+    return argmax_first(logits, n);
+}
+
+extern "C" int bm_sample(bm_sampler_t* s, const float* logits) {
+    if (!s || !logits) return 0;
+    return sample_probs(s->probs, s->idx, s->vocab_size, s->temperature, s->top_k, s->topp, s->rng++, logits);
+}
+
+/* ------------------------------------------------------------------ */
+/* driver: reference tools/run.c:121-185 */
+
+extern "C" int bm_run_tokens(bm_context_t* ctx, bm_model_t* m, const int* prompt_ids, int n_prompt, int steps,
+                             float temperature, int top_k, float top_p, uint64_t seed, bm_token_cb_t callback,
+                             void* user_data) {
+    if (!ctx || !m || n_prompt <= 0 || !prompt_ids) return -1;
+    bm_compile(m);
+    bm_session_t* S = bm_create_session(ctx, m);
+    if (!S) return -1;
+    int rc = 0;
+    if (temperature <= 0.0f && steps >= n_prompt && steps <= S->MS) {
+        /* greedy: the whole loop runs on the device, then the callback sees the tokens in order */
+        int* toks = (int*)malloc((size_t)(steps - n_prompt + 1) * sizeof(int));
+        const int n = toks ? bm_generate_greedy(S, prompt_ids, n_prompt, steps, toks) : -1;
+        if (n < 0) rc = -1;
+        for (int i = 0; i < n; i++)
+            if (callback && callback(toks[i], user_data)) break;
+        free(toks);
+    } else {
+        if (seed == 0) seed = 1;
+        unsigned int rng_state = (unsigned int)seed;
+        float* p = (float*)malloc((size_t)m->V * sizeof(float));
+        int* idx = (int*)malloc((size_t)m->V * sizeof(int));
+        int next = -1;
+        for (int pos = 0; pos < steps && p && idx; pos++) {
+            const int tok = pos < n_prompt ? prompt_ids[pos] : next;
+            float* logits = bm_step(S, tok);
+            if (!logits) {
+                rc = -1;
+                break;
+            }
+            if (pos >= n_prompt - 1) {
+                next = sample_probs(p, idx, m->V, temperature, top_k, top_p, rng_state++, logits);
+                if (callback && callback(next, user_data)) break;
+            }
+        }
+        if (!p || !idx) rc = -1;
+        free(p);
+        free(idx);
+    }
+    bm_destroy_session(S);
+    return rc;
+}

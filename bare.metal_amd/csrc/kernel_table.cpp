@@ -16,6 +16,14 @@ int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
 int bmk_launch_copy_buffer(const bmk_launch_t* a);
+int bmk_launch_rmsnorm(const bmk_launch_t* a);
+int bmk_launch_rope(const bmk_launch_t* a);
+int bmk_launch_kv_store(const bmk_launch_t* a);
+int bmk_launch_attention(const bmk_launch_t* a);
+int bmk_launch_add(const bmk_launch_t* a);
+int bmk_launch_swiglu(const bmk_launch_t* a);
+int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a);
+int bmk_launch_argmax(const bmk_launch_t* a);
 }
 
 #define B(i) (1u << (i))
@@ -35,5 +43,22 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"matmul_forward_q8_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_matvec_multi, B(1)},
     /* new: device-to-device copy; {src, dst, params int64{nbytes}} */
     {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
+    /* decode-step kernels (buffer orders: reference scheduler.c:835-947) */
+    /* reference forward.metal:1019-1060; {inp, weight, out, params{N,C}, eps} */
+    {"rmsnorm_forward_v2", 5, B(3) | B(4), B(2), bmk_launch_rmsnorm, 0},
+    /* reference forward.metal:1284-1313; {q, k, head_size, pos, rope[6], n_kv_heads}, grid = NH */
+    {"rope_forward", 6, B(2) | B(3) | B(4) | B(5), B(0) | B(1), bmk_launch_rope, 0},
+    /* reference forward.metal:1317-1329; {kv cache, k, v, params{layer,pos,MS,KV}} */
+    {"kv_store", 4, B(3), B(0), bmk_launch_kv_store, 0},
+    /* reference forward.metal:1362-1465; {q, kv cache, out, params{NH,HD,NKV,KV,S,kv_mul,layer,MS}, scale} */
+    {"attention_forward", 5, B(3) | B(4), B(2), bmk_launch_attention, 0},
+    /* reference forward.metal:1332-1340; {a, b, out, n} */
+    {"add_forward", 4, B(3), B(2), bmk_launch_add, 0},
+    /* reference forward.metal:1179-1190; {gate, up, out, N} */
+    {"swiglu_forward", 4, B(3), B(2), bmk_launch_swiglu, 0},
+    /* reference forward.metal:1636-1689; {x, norm weight, wcls f32, logits, params{C,V}, eps} */
+    {"rmsnorm_matmul_forward", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul, 0},
+    /* new: greedy pick on the device (reference tools/run.c:56-60); {values, out int, params{n}} */
+    {"argmax_f32", 3, B(2), B(1), bmk_launch_argmax, 0},
     {nullptr, 0, 0, 0, nullptr, 0},
 };

@@ -1,0 +1,70 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * q8_common.h — device helpers shared by the Q8 kernels: one 36-byte Q8_0
+ * block {f32 scale; int8 q[32]} (reference src/baremetal/quant.h:17-32)
+ * read with two dwordx4 loads and one dword load, and its dot product with
+ * 32 fp32 activations held in registers.
+ */
+#ifndef BMK_Q8_COMMON_H
+#define BMK_Q8_COMMON_H
+
+#include <hip/hip_runtime.h>
+
+namespace bmk {
+
+struct Blk {
+    float s;
+    uint4 q0, q1;
+};
+
+__device__ __forceinline__ Blk load_block(const unsigned char* p) {
+    Blk b;
+    unsigned char raw[36];
+    __builtin_memcpy(raw, __builtin_assume_aligned(p, 4), 36);
+    __builtin_memcpy(&b.s, raw, 4);
+    __builtin_memcpy(&b.q0, raw + 4, 16);
+    __builtin_memcpy(&b.q1, raw + 20, 16);
+    return b;
+}
+
+__device__ __forceinline__ float dot4(unsigned int w, const float* x) {
+    float a = x[0] * (float)(signed char)(w & 0xffu);
+    a = fmaf(x[1], (float)(signed char)((w >> 8) & 0xffu), a);
+    a = fmaf(x[2], (float)(signed char)((w >> 16) & 0xffu), a);
+    a = fmaf(x[3], (float)(signed char)(w >> 24), a);
+    return a;
+}
+
+__device__ __forceinline__ float block_dot(const Blk& b, const float* xs) {
+    float s0 = dot4(b.q0.x, xs + 0) + dot4(b.q0.y, xs + 4);
+    float s1 = dot4(b.q0.z, xs + 8) + dot4(b.q0.w, xs + 12);
+    float s2 = dot4(b.q1.x, xs + 16) + dot4(b.q1.y, xs + 20);
+    float s3 = dot4(b.q1.z, xs + 24) + dot4(b.q1.w, xs + 28);
+    return ((s0 + s1) + (s2 + s3)) * b.s;
+}
+
+
+__device__ __forceinline__ Blk zero_block() {
+    Blk b;
+    b.s = 0.0f;
+    b.q0 = make_uint4(0, 0, 0, 0);
+    b.q1 = make_uint4(0, 0, 0, 0);
+    return b;
+}
+
+/* Sum over the 64 lanes of a wave (xor butterfly; every lane gets the sum). */
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+} // namespace bmk
+
+#endif

@@ -29,41 +29,12 @@
  */
 #include "bmk.h"
 #include "q8_matvec.h"
+#include "q8_common.h"
 
 namespace {
 
+using namespace bmk;
 constexpr int MV_THREADS = 256;
-
-struct Blk {
-    float s;
-    uint4 q0, q1;
-};
-
-__device__ __forceinline__ Blk load_block(const unsigned char* p) {
-    Blk b;
-    unsigned char raw[36];
-    __builtin_memcpy(raw, __builtin_assume_aligned(p, 4), 36);
-    __builtin_memcpy(&b.s, raw, 4);
-    __builtin_memcpy(&b.q0, raw + 4, 16);
-    __builtin_memcpy(&b.q1, raw + 20, 16);
-    return b;
-}
-
-__device__ __forceinline__ float dot4(unsigned int w, const float* x) {
-    float a = x[0] * (float)(signed char)(w & 0xffu);
-    a = fmaf(x[1], (float)(signed char)((w >> 8) & 0xffu), a);
-    a = fmaf(x[2], (float)(signed char)((w >> 16) & 0xffu), a);
-    a = fmaf(x[3], (float)(signed char)(w >> 24), a);
-    return a;
-}
-
-__device__ __forceinline__ float block_dot(const Blk& b, const float* xs) {
-    float s0 = dot4(b.q0.x, xs + 0) + dot4(b.q0.y, xs + 4);
-    float s1 = dot4(b.q0.z, xs + 8) + dot4(b.q0.w, xs + 12);
-    float s2 = dot4(b.q1.x, xs + 16) + dot4(b.q1.y, xs + 20);
-    float s3 = dot4(b.q1.z, xs + 24) + dot4(b.q1.w, xs + 28);
-    return ((s0 + s1) + (s2 + s3)) * b.s;
-}
 
 /* One row tile of one problem.  Requires nb <= MV_THREADS. */
 template <int U>

@@ -120,3 +120,13 @@ int launch_quantize(const bmk_launch_t* a) {
 
 extern "C" int bmk_launch_quantize_q8(const bmk_launch_t* a) { return launch_quantize<false>(a); }
 extern "C" int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a) { return launch_quantize<true>(a); }
+
+/* Engine-side pack of n fp32 values (n a positive multiple of 32, src 4-byte
+ * and dst 4-byte aligned; checked by the caller). */
+extern "C" int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s) {
+    const long nblocks = n / 32;
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q8<false>, dim3(grid), dim3(256), 0, s, (const void*)src, dst, nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}

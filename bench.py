@@ -157,6 +157,49 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
     }
 
 
+def e2e_decode(cpu_steps: int, cpu_threads: int):
+    """Config 5: SmolLM2-135M Q8 greedy decode, 128-token prompt + 256
+    generated tokens (383 decode steps, prompt tokens stepped one by one as
+    the reference's bm_run_tokens does), batch 1 and batch 32, driven on the
+    device by bm_generate_greedy."""
+    dims = bmhip.SMOLLM2_135M
+    n_prompt, n_gen, seed = 128, 256, 2025
+    steps = n_prompt + n_gen - 1
+    out = {"workload": "SmolLM2-135M Q8 greedy decode (fp32 tied LM head), prompt 128 + 256 generated, "
+                       "random init N(0,0.02), unit norms; decode tok/s = batch x 383 steps / time"}
+    for B in (1, 32):
+        prompts = bmhip.synth_uniform_int(seed, 0, dims["V"], B * n_prompt).reshape(B, n_prompt)
+        eng = bmhip.Engine(dims, max_seq_len=n_prompt + n_gen, seed=seed, batch=B)
+        eng.generate(prompts, steps)  # warm-up; captures the step graph
+        t0 = time.perf_counter()
+        toks = eng.generate(prompts, steps)
+        dt = time.perf_counter() - t0
+        out[f"b{B}"] = {"tok_s": round(B * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
+                        "generated_tok_s": round(B * n_gen / dt, 1), "first_tokens": [int(t) for t in toks[:8, 0]]}
+        eng.close()
+        log(f"[bench] e2e B={B}: {B * steps / dt:.1f} tok/s, {dt * 1e3 / steps:.3f} ms/step")
+    if cpu_steps > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import pyoracle as po
+
+        w = bmhip.synthetic_weights(dims, seed)
+        arrs = {"emb": w["token_embedding"], "ln1": w["ln1"], "ln2": w["ln2"], "lnf": w["lnf"]}
+        for src, dst in (("wq", "wq"), ("wk", "wk"), ("wv", "wv"), ("wo", "wo"), ("w_gate", "wg"),
+                         ("w_up", "wu"), ("w_down", "wd")):
+            arrs[dst] = po.quantize_q8(w[src])
+        dec = po.Decoder(dict(dims, MS=n_prompt + n_gen), arrs, nthreads=cpu_threads)
+        prompt = bmhip.synth_uniform_int(seed, 0, dims["V"], n_prompt)
+        dec.step(int(prompt[0]), 0)
+        t0 = time.perf_counter()
+        for pos in range(1, cpu_steps + 1):
+            dec.step(int(prompt[pos]), pos)
+        dt = time.perf_counter() - t0
+        out["cpu_port_b1"] = {"tok_s": round(cpu_steps / dt, 2), "cores": cpu_threads, "kind": "port",
+                              "sample": f"{cpu_steps} decode steps of the C oracle (fp64 reductions)"}
+        dec.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -165,6 +208,8 @@ def main():
     ap.add_argument("--model", choices=sorted(MODELS), default="360m")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
+    ap.add_argument("--e2e", type=int, default=1, help="also time config-5 greedy decode (0: skip)")
+    ap.add_argument("--e2e-cpu-steps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -204,6 +249,12 @@ def main():
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(wl, args.cpu_seconds, args.cpu_threads)
         log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+    bytes_per_step, w_bytes = wl.bytes_per_step, wl.w_bytes
+    pack_gbps = round(5.125 * wl.pack_elems / (wl.pack_ms * 1e-3) / 1e9, 2) if wl.pack_ms > 0 else None
+    del wl
+    be.close()
+
+    e2e = e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads) if args.e2e else None
 
     mid, D, H, NH, NKV, HD, L = MODELS[args.model]
     line = {
@@ -223,8 +274,8 @@ def main():
             "workload": f"SmolLM2-{args.model.upper()} Q8 decode projections, batch 1: {L} layers x "
                         f"(q,k,v,o,gate,up,down) + Q8 LM head {V}x{D}, one matmul_forward_q8_vec_multi "
                         f"launch per token",
-            "bytes_per_step": wl.bytes_per_step,
-            "q8_weight_bytes": wl.w_bytes,
+            "bytes_per_step": bytes_per_step,
+            "q8_weight_bytes": w_bytes,
             "matrices": len(probs),
             "weights": "int8 Q8_0 blocks (32 x int8 + fp32 scale), N(0,0.02) quantized on device",
             "activations": "fp32 N(0,1), one vector per matrix",
@@ -239,9 +290,9 @@ def main():
         },
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
-        "pack_gbps": round(5.125 * wl.pack_elems / (wl.pack_ms * 1e-3) / 1e9, 2) if wl.pack_ms > 0 else None,
+        "pack_gbps_incl_upload": pack_gbps,
+        "e2e_decode": e2e,
     }
-    be.close()
     print(json.dumps(line), flush=True)
 
 

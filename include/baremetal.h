@@ -1,0 +1,185 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * baremetal.h — the engine API of the MI355X decode path.
+ *
+ * The types and the functions in the first part keep the names, argument
+ * meanings and return conventions of the reference's public API
+ * (reference include/baremetal.h:16-206), restricted to Q8 inference:
+ * a context on the GPU, a model described by bm_arch_t, bm_compile, a
+ * session, bm_step / bm_forward and the greedy/sampling driver
+ * bm_run_tokens.  The second part holds MI355X additions that have no
+ * counterpart in the reference (weight input without a checkpoint loader,
+ * batched sessions, device-driven greedy generation).
+ *
+ * Differences a caller of the reference sees:
+ *   - BM_DEVICE_METAL selects "the GPU", here the HIP device; BM_DEVICE_HIP
+ *     is the same value.  BM_DEVICE_CPU has no backend, as in the reference
+ *     (reference src/baremetal/context.c:16-22), and bm_create returns NULL.
+ *   - Projections run only in Q8 (quant_bits 8); the LM head runs in fp32
+ *     over the tied embedding (the reference's Q8 mode, reference
+ *     src/baremetal/graph.c:228-238) or, on request, in Q8.
+ *   - Weights come from bm_model_set_tensor or bm_model_init_synthetic;
+ *     checkpoint files are not read.
+ *   - bm_forward steps prompt tokens one at a time (the reference's
+ *     bm_forward prefills with an S-sized graph when pos == 0; the logits it
+ *     returns are those of the last token either way).
+ */
+#ifndef BAREMETAL_H
+#define BAREMETAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- Architecture descriptor (reference include/baremetal.h:18-87) ---- */
+
+typedef enum { BM_NORM_LAYERNORM, BM_NORM_RMSNORM } bm_norm_t;
+typedef enum { BM_ACT_GELU, BM_ACT_SWIGLU } bm_act_t;
+typedef enum { BM_POS_LEARNED, BM_POS_ROPE } bm_pos_t;
+typedef enum { BM_ATTN_MHA, BM_ATTN_GQA } bm_attn_t;
+typedef enum { BM_ROPE_NONE = 0, BM_ROPE_LLAMA3 = 1 } bm_rope_scaling_t;
+typedef enum { BM_PRECISION_FP32, BM_PRECISION_FP16, BM_PRECISION_BF16 } bm_precision_t;
+typedef enum { BM_DEVICE_CPU, BM_DEVICE_METAL, BM_DEVICE_HIP = BM_DEVICE_METAL } bm_device_t;
+
+typedef struct {
+    int dim;
+    int hidden_dim;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int vocab_size;
+    int padded_vocab_size;
+    int max_seq_len;
+
+    bm_norm_t      norm;
+    bm_act_t       activation;
+    bm_pos_t       pos_enc;
+    bm_attn_t      attention;
+    bm_precision_t precision;
+
+    int bias;
+    int weight_tie;
+    int has_qk_norm;
+    int has_ffn_post_norm;
+    int head_dim;
+    int gated_mlp;
+    int gemma_norm;
+    int embed_scale;
+    int weight_layout;
+
+    float rope_theta;
+
+    bm_rope_scaling_t rope_scaling;
+    float rope_factor;
+    float rope_low_freq_factor;
+    float rope_high_freq_factor;
+    float rope_original_max;
+} bm_arch_t;
+
+typedef struct bm_context_s bm_context_t;
+typedef struct bm_model_s   bm_model_t;
+typedef struct bm_session_s bm_session_t;
+typedef struct bm_sampler_s bm_sampler_t;
+
+/* ---- Reference API (reference include/baremetal.h:120-175) ---- */
+
+bm_context_t*  bm_create(bm_device_t device);
+void           bm_destroy(bm_context_t* ctx);
+bm_precision_t bm_get_supported_precision(bm_context_t* ctx);
+
+/* Accepts the SmolLM2 / llama family the decode path implements: RMSNorm,
+ * SwiGLU gated MLP, RoPE, GQA, tied embeddings, no biases.  NULL (logged)
+ * for anything else. */
+bm_model_t*    bm_create_model(bm_context_t* ctx, const bm_arch_t* arch);
+void           bm_destroy_model(bm_model_t* model);
+
+/* Uploads the weights and packs every projection to Q8 on the device
+ * (the reference quantizes on the host at session creation,
+ * reference src/baremetal/scheduler.c:364-384). */
+void           bm_compile(bm_model_t* model);
+
+bm_session_t*  bm_create_session(bm_context_t* ctx, bm_model_t* model);
+/* Logits of the token at the session's position (V floats, valid until the
+ * next call on the session); the position advances.  NULL on error. */
+float*         bm_step(bm_session_t* sess, int token);
+float*         bm_forward(bm_session_t* sess, const int* tokens, int n_tokens);
+void           bm_reset_session(bm_session_t* sess);
+void           bm_destroy_session(bm_session_t* sess);
+
+/* GPU time of the steps run between begin and end, all reported as
+ * other_ms (the reference never fills the attention/MLP split either,
+ * reference src/baremetal/scheduler.c:994). */
+void           bm_profile_begin(bm_session_t* sess);
+void           bm_profile_end(bm_session_t* sess, double* attention_ms, double* mlp_ms, double* other_ms);
+
+typedef int (*bm_token_cb_t)(int token_id, void* user_data);
+
+/* Reference tools/run.c:121-185: step every prompt token, then feed back
+ * the sampled token; temperature <= 0 picks the first maximal logit.
+ * Returns 0, or -1 on bad arguments. */
+int            bm_run_tokens(bm_context_t* ctx, bm_model_t* model, const int* prompt_ids, int n_prompt, int steps,
+                             float temperature, int top_k, float top_p, uint64_t seed, bm_token_cb_t callback,
+                             void* user_data);
+
+/* Reference src/baremetal/sampler.c: temperature -> softmax -> top-k ->
+ * top-p -> inverse-CDF draw with an LCG; temperature <= 0 is argmax. */
+bm_sampler_t*  bm_create_sampler(int vocab_size, float temp, float topp, uint64_t seed);
+int            bm_sample(bm_sampler_t* sampler, const float* logits);
+void           bm_destroy_sampler(bm_sampler_t* sampler);
+
+int            bm_get_num_parameters(const bm_model_t* model);
+const char*    bm_get_arch_name(const bm_model_t* model);
+
+/* ---- MI355X additions (no reference counterpart) ---- */
+
+/* Quantization of the projections: 8 (Q8_0) is the only value accepted
+ * (the reference's CLI sets model->quant_bits, reference tools/cli.c:886). */
+int            bm_model_set_quant_bits(bm_model_t* model, int bits);
+/* 1: the LM head runs on Q8 rows quantized from the tied embedding;
+ * 0 (default): fp32 rows, as the reference. */
+int            bm_model_set_q8_head(bm_model_t* model, int on);
+
+/* Host fp32 weights in the reference's layout (reference
+ * src/baremetal/model.c:125-172: one array per matrix type, layers back to
+ * back, rows of the output dimension).  Names and element counts:
+ *   "token_embedding" V*D   "ln1" L*D   "ln2" L*D   "lnf" D
+ *   "wq" L*NH*HD*D  "wk" L*KV*D  "wv" L*KV*D  "wo" L*D*NH*HD
+ *   "w_gate" L*H*D  "w_up" L*H*D  "w_down" L*D*H
+ * Returns 0, or -1 for an unknown name or a wrong count. */
+int            bm_model_set_tensor(bm_model_t* model, const char* name, const float* data, size_t n);
+
+/* Random-init weights (no checkpoint): every projection of every layer and
+ * the tied embedding drawn from N(0, 0.02) with the seed
+ * bm_synth_tensor_seed(seed, 5, layer, id) (include/bm_synth.h), id =
+ * 0 token_embedding (layer 0xFFFF), 1 wq, 2 wk, 3 wv, 4 wo, 5 w_gate,
+ * 6 w_up, 7 w_down; RMSNorm gains 1.0. */
+int            bm_model_init_synthetic(bm_model_t* model, uint64_t seed);
+
+/* A session that steps `batch` independent sequences in lockstep (all at
+ * the same position) with per-sequence KV caches; max_seq_len 0 takes the
+ * model's.  bm_create_session is batch 1. */
+bm_session_t*  bm_create_session_batched(bm_context_t* ctx, bm_model_t* model, int batch, int max_seq_len);
+
+/* One step of every sequence: tokens[b] in, logits [batch][V] out. */
+float*         bm_step_batch(bm_session_t* sess, const int* tokens);
+
+/* Greedy generation driven on the device: from position 0, the prompt
+ * prompt[b * n_prompt + i] is fed, then each sequence's argmax (first
+ * maximal index) is fed back, for `steps` positions in total; no host
+ * round trip between steps (the step is a replayed hipGraph).  Writes
+ * steps - n_prompt + 1 tokens per sequence to out_tokens[i * batch + b]
+ * (the same tokens bm_run_tokens emits) and returns that count, or -1. */
+int            bm_generate_greedy(bm_session_t* sess, const int* prompt, int n_prompt, int steps, int* out_tokens);
+
+/* 0: launch the step's kernels one by one instead of replaying the
+ * captured graph (same kernels, same results).  Default 1. */
+int            bm_session_set_graph(bm_session_t* sess, int on);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BAREMETAL_H */

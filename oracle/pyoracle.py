@@ -48,6 +48,8 @@ def oracle() -> C.CDLL:
         L.orc_decoder_destroy.argtypes = [vp]
         L.orc_decoder_step.restype = i
         L.orc_decoder_step.argtypes = [vp, i, i, vp]
+        L.orc_argmax_first.restype = i
+        L.orc_argmax_first.argtypes = [vp, i, vp, vp]
         L.orc_generate.restype = i
         L.orc_generate.argtypes = [vp, vp, i, i, vp, vp, vp]
         _o = L

@@ -1,0 +1,173 @@
+# SPDX-License-Identifier: MPL-2.0
+"""The decode-step kernels the reference scheduler dispatches by name, bound
+with the reference's buffer orders (reference src/baremetal/scheduler.c:
+835-947) through the backend C ABI, against fp64 restatements of the
+reference kernels (reference src/kernels/forward.metal).  fp32 kernels:
+normwise error <= 1e-5; data movement and argmax: exact."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import bmhip
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def nw(y, r):
+    return float(np.abs(y.astype(np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def f32(*a):
+    return np.array(a, np.float32)
+
+
+@pytest.mark.parametrize("N,C", [(1, 576), (3, 960), (2, 7), (1, 4096)])
+def test_rmsnorm_forward_v2(be, N, C):
+    rng = np.random.default_rng(N * C)
+    x = rng.standard_normal(N * C).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    out = be.alloc(N * C * 4)
+    rc = be.dispatch("rmsnorm_forward_v2", [be.upload(x), be.upload(w), out, be.params(N, C), be.upload(f32(1e-5))],
+                     (256,), (256,))
+    assert rc == 0
+    xr = x.reshape(N, C).astype(np.float64)
+    want = xr / np.sqrt((xr * xr).mean(axis=1, keepdims=True) + 1e-5) * w
+    assert nw(out.read(np.float32), want.ravel()) <= TOL
+
+
+_libm = ctypes.CDLL("libm.so.6")
+_libm.powf.restype = ctypes.c_float
+_libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+
+
+def rope_ref(v, heads, HD, pos, theta):
+    """Rotate-half RoPE in fp64 of the fp32 angle (float)pos * inv; inv from
+    the C library's powf, as the oracle (and the device's host-side table)
+    evaluate it: the angle is sensitive to one ulp of inv at large pos."""
+    v = v.reshape(-1, HD).astype(np.float64).copy()
+    inv = np.array([np.float32(1.0) / np.float32(_libm.powf(theta, float(np.float32(2 * i) / np.float32(HD))))
+                    for i in range(HD // 2)], np.float32)
+    ang = (np.float32(pos) * inv).astype(np.float32).astype(np.float64)
+    c, s = np.cos(ang), np.sin(ang)
+    a, b = v[:heads, :HD // 2].copy(), v[:heads, HD // 2:].copy()
+    v[:heads, :HD // 2] = a * c - b * s
+    v[:heads, HD // 2:] = a * s + b * c
+    return v.ravel()
+
+
+@pytest.mark.parametrize("NH,NKV,HD,pos", [(9, 3, 64, 0), (9, 3, 64, 137), (15, 5, 64, 383), (4, 4, 128, 5000)])
+def test_rope_forward(be, NH, NKV, HD, pos):
+    rng = np.random.default_rng(pos)
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    k = rng.standard_normal(NKV * HD).astype(np.float32)
+    bq, bk = be.upload(q), be.upload(k)
+    rope = f32(10000.0, 0, 0, 0, 0, 0)
+    rc = be.dispatch("rope_forward", [bq, bk, be.params(HD), be.params(pos), be.upload(rope), be.params(NKV)],
+                     (NH,), (min(NH, 256),))
+    assert rc == 0
+    assert nw(bq.read(np.float32), rope_ref(q, NH, HD, pos, 10000.0)) <= TOL
+    assert nw(bk.read(np.float32), rope_ref(k, NKV, HD, pos, 10000.0)) <= TOL
+    if pos == 0:  # rotation by 0: exact identity
+        assert np.array_equal(bq.read(np.float32), q)
+
+
+def test_kv_store_places_rows(be):
+    L, MS, KV = 3, 16, 192
+    cache = be.alloc(L * 2 * MS * KV * 4)
+    k = np.arange(KV, dtype=np.float32)
+    v = -np.arange(KV, dtype=np.float32)
+    assert be.dispatch("kv_store", [cache, be.upload(k), be.upload(v), be.params(2, 5, MS, KV)], (KV,), (KV,)) == 0
+    c = cache.read(np.float32).reshape(L, 2, MS, KV)
+    assert np.array_equal(c[2, 0, 5], k) and np.array_equal(c[2, 1, 5], v)
+    c[2, :, 5] = 0
+    assert not c.any()
+    # pos beyond the cache is rejected before launch
+    assert be.dispatch("kv_store", [cache, be.upload(k), be.upload(v), be.params(2, MS, MS, KV)], (KV,), (KV,)) == -1
+
+
+def attn_ref(q, cache, NH, HD, KV, S, kv_mul, layer, MS, scale):
+    c = cache.reshape(-1, 2, MS, KV).astype(np.float64)
+    out = np.zeros(NH * HD)
+    for h in range(NH):
+        kh = h // kv_mul
+        K = c[layer, 0, :S, kh * HD:(kh + 1) * HD]
+        V = c[layer, 1, :S, kh * HD:(kh + 1) * HD]
+        s = K @ q[h * HD:(h + 1) * HD].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        out[h * HD:(h + 1) * HD] = (p / p.sum()) @ V
+    return out
+
+
+@pytest.mark.parametrize("NH,NKV,HD,S,MS", [(9, 3, 64, 1, 8), (9, 3, 64, 384, 512), (15, 5, 64, 100, 128),
+                                            (4, 2, 128, 3000, 4096), (8, 8, 32, 2049, 2100)])
+def test_attention_forward(be, NH, NKV, HD, S, MS):
+    rng = np.random.default_rng(S)
+    KV, L, layer = NKV * HD, 2, 1
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    cache = (rng.standard_normal(L * 2 * MS * KV) * 0.5).astype(np.float32)
+    out = be.alloc(NH * HD * 4)
+    scale = 1.0 / np.sqrt(HD)
+    p = be.params(NH, HD, NKV, KV, S, NH // NKV, layer, MS)
+    rc = be.dispatch("attention_forward", [be.upload(q), be.upload(cache), out, p, be.upload(f32(scale))],
+                     (NH * HD,), (HD,))
+    assert rc == 0
+    want = attn_ref(q, cache, NH, HD, KV, S, NH // NKV, layer, MS, np.float32(scale))
+    assert nw(out.read(np.float32), want) <= TOL
+
+
+def test_attention_single_key_is_v(be):
+    NH, NKV, HD, MS = 9, 3, 64, 4
+    KV = NKV * HD
+    rng = np.random.default_rng(1)
+    cache = rng.standard_normal(2 * MS * KV).astype(np.float32)
+    out = be.alloc(NH * HD * 4)
+    p = be.params(NH, HD, NKV, KV, 1, 3, 0, MS)
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    assert be.dispatch("attention_forward", [be.upload(q), be.upload(cache), out, p, be.upload(f32(0.125))],
+                       (NH * HD,), (HD,)) == 0
+    v0 = cache.reshape(2, MS, KV)[1, 0]
+    want = np.concatenate([v0[(h // 3) * HD:(h // 3 + 1) * HD] for h in range(NH)])
+    assert np.array_equal(out.read(np.float32), want)
+
+
+def test_add_and_swiglu(be):
+    rng = np.random.default_rng(2)
+    n = 1536
+    a = rng.standard_normal(n).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    o = be.alloc(n * 4)
+    assert be.dispatch("add_forward", [be.upload(a), be.upload(b), o, be.params(n)], (n,), (256,)) == 0
+    assert np.array_equal(o.read(np.float32), a + b)
+    assert be.dispatch("swiglu_forward", [be.upload(a), be.upload(b), o, be.params(n)], (n,), (256,)) == 0
+    g = a.astype(np.float64)
+    assert nw(o.read(np.float32), g / (1 + np.exp(-g)) * b) <= TOL
+
+
+@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300)])
+def test_rmsnorm_matmul_forward(be, C, V):
+    rng = np.random.default_rng(C)
+    x = rng.standard_normal(C).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    W = (rng.standard_normal(V * C) * 0.02).astype(np.float32)
+    out = be.alloc(V * 4)
+    rc = be.dispatch("rmsnorm_matmul_forward", [be.upload(x), be.upload(g), be.upload(W), out, be.params(C, V),
+                                                be.upload(f32(1e-5))], ((V + 255) & ~255,), (256,))
+    assert rc == 0
+    xd = x.astype(np.float64)
+    xn = xd / np.sqrt((xd * xd).mean() + 1e-5) * g
+    assert nw(out.read(np.float32), W.reshape(V, C).astype(np.float64) @ xn) <= TOL
+
+
+def test_argmax_first_index(be):
+    v = np.zeros(49152, np.float32)
+    v[[10, 40000, 7]] = 2.5
+    out = be.alloc(4)
+    assert be.dispatch("argmax_f32", [be.upload(v), out, be.params(v.size)], (1024,), (1024,)) == 0
+    assert out.read(np.int32)[0] == 7
+    rng = np.random.default_rng(3)
+    for _ in range(3):
+        v = rng.standard_normal(49152).astype(np.float32)
+        assert be.dispatch("argmax_f32", [be.upload(v), out, be.params(v.size)], (1024,), (1024,)) == 0
+        assert out.read(np.int32)[0] == int(np.argmax(v))
