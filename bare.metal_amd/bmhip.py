@@ -89,6 +89,7 @@ def lib() -> C.CDLL:
         "bm_model_init_synthetic": (i, [vp, u64]),
         "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
         "bm_session_set_graph": (i, [vp, i]),
+        "bm_profile_phases": (C.c_long, [vp, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -417,10 +418,19 @@ class Engine:
     def profile_begin(self):
         lib().bm_profile_begin(self.sess)
 
-    def profile_end(self) -> float:
-        o = C.c_double(0.0)
-        lib().bm_profile_end(self.sess, None, None, C.byref(o))
-        return o.value
+    PHASES = ("embed", "rmsnorm_qkv", "rope_kv_attention", "o_residual", "rmsnorm_gateup_swiglu",
+              "down_residual", "norm_head_argmax")
+
+    def profile_end(self) -> dict:
+        """Ends profiling; per-phase ms per step and the reference-style split."""
+        ms = (C.c_double * 7)()
+        n = lib().bm_profile_phases(self.sess, ms)
+        a, m, o = C.c_double(), C.c_double(), C.c_double()
+        lib().bm_profile_end(self.sess, C.byref(a), C.byref(m), C.byref(o))
+        n = max(int(n), 1)
+        out = {k: ms[i] / n for i, k in enumerate(self.PHASES)}
+        out.update(attention_ms=a.value / n, mlp_ms=m.value / n, other_ms=o.value / n, steps=n)
+        return out
 
     def close(self):
         L = lib()

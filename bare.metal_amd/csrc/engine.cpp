@@ -102,7 +102,12 @@ struct bm_session_s {
     hipGraphExec_t gexec;
     int prof_on;
     double prof_ms;
+    double prof_phase[BM_PROF_PHASES]; /* ms per phase kind, summed over layers and steps */
+    long prof_steps;
     hipEvent_t ev0, ev1;
+    hipEvent_t* pev;     /* one event after every kernel of a profiled step */
+    int n_pev;
+    int mark;            /* next event index while a profiled step is enqueued, -1: not profiling */
 };
 
 /* ------------------------------------------------------------------ */
@@ -329,6 +334,15 @@ extern "C" const char* bm_get_arch_name(const bm_model_t* m) { return m ? "llama
 /* ------------------------------------------------------------------ */
 /* session */
 
+/* Kernel kinds of a step, in launch order within a layer. */
+enum { PH_EMBED, PH_QKV, PH_ATTN, PH_O, PH_GATEUP, PH_DOWN, PH_HEAD };
+
+static int mark(bm_session_t* S) {
+    if (S->mark < 0) return 0;
+    HIP_TRY(hipEventRecord(S->pev[S->mark++], S->ctx->s), "hipEventRecord", return -1);
+    return 0;
+}
+
 static int enqueue_step(bm_session_t* S) {
     bm_model_t* m = S->m;
     hipStream_t s = S->ctx->s;
@@ -340,7 +354,7 @@ static int enqueue_step(bm_session_t* S) {
     e.st = S->st;
     e.D = D;
     e.V = m->V;
-    if (dec_launch_embed(&e, s)) return -1;
+    if (mark(S) || dec_launch_embed(&e, s) || mark(S)) return -1;
     const float eps = 1e-5f; /* reference graph.c:134,175,219 */
     for (int l = 0; l < m->L; l++) {
         const unsigned char* wl = m->d_q8 + (size_t)l * m->layer_bytes;
@@ -354,7 +368,7 @@ static int enqueue_step(bm_session_t* S) {
         mv.w[2] = wl + m->off[2]; mv.y[2] = S->v; mv.OC[2] = m->KV;
         mv.tile0[0] = 0;
         for (int i = 0; i < 3; i++) mv.tile0[i + 1] = mv.tile0[i] + dec_mv_tiles(mv.OC[i], D, 0);
-        if (dec_launch_mv(&mv, s)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
         /* rope + KV append + attention */
         DecAttn at;
         memset(&at, 0, sizeof at);
@@ -365,26 +379,26 @@ static int enqueue_step(bm_session_t* S) {
         bmk_rope_table(rp, m->HD, at.inv_freq);
         at.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
         at.NH = m->NH; at.NKV = m->NKV; at.HD = m->HD; at.KV = m->KV; at.MS = S->MS; at.L = m->L; at.layer = l;
-        if (dec_launch_attn(&at, B, s)) return -1;
+        if (dec_launch_attn(&at, B, s) || mark(S)) return -1;
         /* o + residual */
         memset(&mv, 0, sizeof mv);
         mv.x = S->att; mv.C = m->QD; mv.B = B; mv.ldx = m->QD; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[3]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->QD, 0);
-        if (dec_launch_mv(&mv, s)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
         /* RMSNorm + gate, up + SwiGLU */
         memset(&mv, 0, sizeof mv);
         mv.x = S->x; mv.norm_w = m->d_ln2 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
         mv.nmat = 1; mv.glu = 1;
         mv.w[0] = wl + m->off[4]; mv.w[1] = wl + m->off[5]; mv.y[0] = S->h; mv.OC[0] = m->H;
         mv.tile0[1] = dec_mv_tiles(m->H, D, 1);
-        if (dec_launch_mv(&mv, s)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
         /* down + residual */
         memset(&mv, 0, sizeof mv);
         mv.x = S->h; mv.C = m->H; mv.B = B; mv.ldx = m->H; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[6]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->H, 0);
-        if (dec_launch_mv(&mv, s)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
     }
     DecHead hd;
     memset(&hd, 0, sizeof hd);
@@ -392,7 +406,8 @@ static int enqueue_step(bm_session_t* S) {
     hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
     hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
-    return dec_launch_head(&hd, s);
+    if (dec_launch_head(&hd, s) || mark(S)) return -1;
+    return 0;
 }
 
 static void session_free(bm_session_t* S) {
@@ -407,6 +422,8 @@ static void session_free(bm_session_t* S) {
     if (S->h_io) hipHostFree(S->h_io);
     if (S->ev0) hipEventDestroy(S->ev0);
     if (S->ev1) hipEventDestroy(S->ev1);
+    for (int i = 0; i < S->n_pev; i++) hipEventDestroy(S->pev[i]);
+    free(S->pev);
     if (S->m) S->m->nsessions--;
     free(S);
 }
@@ -442,6 +459,7 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
     S->B = batch;
     S->MS = max_seq_len > 0 ? max_seq_len : m->arch.max_seq_len;
     S->use_graph = 1;
+    S->mark = -1;
     const size_t B = (size_t)batch;
     const size_t kv_elems = B * m->L * 2 * (size_t)S->MS * m->KV;
     bool ok = hipMalloc(&S->x, B * m->D * 4) == hipSuccess && hipMalloc(&S->q, B * m->QD * 4) == hipSuccess &&
@@ -510,18 +528,34 @@ static int launch_step(bm_session_t* S) {
         BMK_ERR("decode step: position %d reached max_seq_len %d", S->pos, S->MS);
         return -1;
     }
-    if (S->prof_on) HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "hipEventRecord", return -1);
-    if (S->use_graph) {
+    if (S->prof_on) {
+        /* profiled steps run eagerly with an event after every kernel */
+        const int need = 3 + 5 * S->m->L;
+        if (S->n_pev < need) {
+            hipEvent_t* ev = (hipEvent_t*)realloc(S->pev, (size_t)need * sizeof(hipEvent_t));
+            if (!ev) return -1;
+            S->pev = ev;
+            for (; S->n_pev < need; S->n_pev++)
+                HIP_TRY(hipEventCreate(&S->pev[S->n_pev]), "hipEventCreate", return -1);
+        }
+        S->mark = 0;
+        const int rc = enqueue_step(S);
+        const int n = S->mark;
+        S->mark = -1;
+        if (rc != 0) return -1;
+        HIP_TRY(hipEventSynchronize(S->pev[n - 1]), "hipEventSynchronize", return -1);
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, S->pev[0], S->pev[n - 1]) == hipSuccess) S->prof_ms += ms;
+        for (int i = 1; i < n; i++) {
+            const int kind = i == 1 ? PH_EMBED : (i == n - 1 ? PH_HEAD : PH_QKV + (i - 2) % 5);
+            if (hipEventElapsedTime(&ms, S->pev[i - 1], S->pev[i]) == hipSuccess) S->prof_phase[kind] += ms;
+        }
+        S->prof_steps++;
+    } else if (S->use_graph) {
         if (ensure_graph(S) != 0) return -1;
         HIP_TRY(hipGraphLaunch(S->gexec, S->ctx->s), "hipGraphLaunch", return -1);
     } else if (enqueue_step(S) != 0) {
         return -1;
-    }
-    if (S->prof_on) {
-        HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "hipEventRecord", return -1);
-        HIP_TRY(hipEventSynchronize(S->ev1), "hipEventSynchronize", return -1);
-        float ms = 0.f;
-        if (hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess) S->prof_ms += ms;
     }
     S->pos++;
     return 0;
@@ -621,13 +655,22 @@ extern "C" void bm_profile_begin(bm_session_t* S) {
     if (!S) return;
     S->prof_on = 1;
     S->prof_ms = 0.0;
+    S->prof_steps = 0;
+    for (int i = 0; i < BM_PROF_PHASES; i++) S->prof_phase[i] = 0.0;
 }
 
 extern "C" void bm_profile_end(bm_session_t* S, double* attention_ms, double* mlp_ms, double* other_ms) {
-    if (attention_ms) *attention_ms = 0.0;
-    if (mlp_ms) *mlp_ms = 0.0;
-    if (other_ms) *other_ms = S ? S->prof_ms : 0.0;
+    const double* p = S ? S->prof_phase : NULL;
+    if (attention_ms) *attention_ms = p ? p[PH_QKV] + p[PH_ATTN] + p[PH_O] : 0.0;
+    if (mlp_ms) *mlp_ms = p ? p[PH_GATEUP] + p[PH_DOWN] : 0.0;
+    if (other_ms) *other_ms = p ? p[PH_EMBED] + p[PH_HEAD] : 0.0;
     if (S) S->prof_on = 0;
+}
+
+extern "C" long bm_profile_phases(bm_session_t* S, double* ms) {
+    if (!S || !ms) return -1;
+    for (int i = 0; i < BM_PROF_PHASES; i++) ms[i] = S->prof_phase[i];
+    return S->prof_steps;
 }
 
 /* ------------------------------------------------------------------ */

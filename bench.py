@@ -42,6 +42,16 @@ MODELS = {
 MATS = ("q", "k", "v", "o", "gate", "up", "down")
 
 
+def measured_traffic(model: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes scaled by a plain copy (profiles/)."""
+    p = os.path.join(ROOT, "profiles", f"q8_matvec_multi_{model}.traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)["bytes_per_launch"]
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -174,8 +184,12 @@ def e2e_decode(cpu_steps: int, cpu_threads: int):
         t0 = time.perf_counter()
         toks = eng.generate(prompts, steps)
         dt = time.perf_counter() - t0
+        eng.profile_begin()  # one more pass, kernel by kernel with events, for the per-phase split
+        eng.generate(prompts, steps)
+        ph = eng.profile_end()
         out[f"b{B}"] = {"tok_s": round(B * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
-                        "generated_tok_s": round(B * n_gen / dt, 1), "first_tokens": [int(t) for t in toks[:8, 0]]}
+                        "generated_tok_s": round(B * n_gen / dt, 1), "first_tokens": [int(t) for t in toks[:8, 0]],
+                        "phase_us_per_step": {k: round(v * 1e3, 2) for k, v in ph.items() if k != "steps"}}
         eng.close()
         log(f"[bench] e2e B={B}: {B * steps / dt:.1f} tok/s, {dt * 1e3 / steps:.3f} ms/step")
     if cpu_steps > 0:
@@ -209,12 +223,31 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
     ap.add_argument("--e2e", type=int, default=1, help="also time config-5 greedy decode (0: skip)")
+    ap.add_argument("--matvec", type=int, default=1, help="0: only the config-5 decode leg (for kernel traces)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.calib_copy_mib > 0:
+        be = bmhip.Backend()
+        n = args.calib_copy_mib << 20
+        src, dst = be.alloc(n), be.alloc(n)
+        enc = be.encoder()
+        for _ in range(5):
+            if enc.dispatch(be.kernel("copy_buffer"), [src, dst, be.params(n, dtype=np.int64)], (n // 16,), (256,)):
+                raise RuntimeError("copy_buffer rejected")
+        ms = enc.wait_timed() / 5
+        be.close()
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "us_per_copy": round(ms * 1e3, 2),
+                          "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        return
+    if not args.matvec:
+        print(json.dumps({"e2e_decode": e2e_decode(0, args.cpu_threads)}), flush=True)
+        return
     be = bmhip.Backend()
     probs = problem_list(args.model)
     t0 = time.perf_counter()
@@ -286,7 +319,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(args.model),
         },
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),

@@ -109,9 +109,13 @@ float*         bm_forward(bm_session_t* sess, const int* tokens, int n_tokens);
 void           bm_reset_session(bm_session_t* sess);
 void           bm_destroy_session(bm_session_t* sess);
 
-/* GPU time of the steps run between begin and end, all reported as
- * other_ms (the reference never fills the attention/MLP split either,
- * reference src/baremetal/scheduler.c:994). */
+/* GPU time of the steps run between begin and end, split as the reference
+ * declares it: attention block (RMSNorm + q/k/v, RoPE + KV append +
+ * attention, o + residual), MLP block (RMSNorm + gate/up + SwiGLU, down +
+ * residual) and other (embedding, final norm + LM head + argmax).  The
+ * reference declares the split but fills only other_ms (reference
+ * src/baremetal/scheduler.c:994).  While profiling, steps are launched one
+ * kernel at a time with a HIP event after each kernel (no graph replay). */
 void           bm_profile_begin(bm_session_t* sess);
 void           bm_profile_end(bm_session_t* sess, double* attention_ms, double* mlp_ms, double* other_ms);
 
@@ -177,6 +181,13 @@ int            bm_generate_greedy(bm_session_t* sess, const int* prompt, int n_p
 /* 0: launch the step's kernels one by one instead of replaying the
  * captured graph (same kernels, same results).  Default 1. */
 int            bm_session_set_graph(bm_session_t* sess, int on);
+
+/* Per-kernel-kind GPU ms accumulated since bm_profile_begin, in step order:
+ * [0] embedding, [1] RMSNorm + q/k/v, [2] RoPE + KV append + attention,
+ * [3] o + residual, [4] RMSNorm + gate/up + SwiGLU, [5] down + residual,
+ * [6] final norm + LM head + argmax.  Returns the number of profiled steps. */
+#define BM_PROF_PHASES 7
+long           bm_profile_phases(bm_session_t* sess, double* ms);
 
 #ifdef __cplusplus
 }
