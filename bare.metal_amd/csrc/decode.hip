@@ -40,8 +40,7 @@ using namespace bmk;
 
 constexpr int NT = 256;     /* threads per workgroup (4 waves) */
 constexpr int ATT_CH = 2048; /* keys per softmax chunk held in LDS */
-constexpr int HEAD_U = 4;   /* rows in flight per lane in the LM head */
-constexpr int MV_U = 4;     /* rows in flight per lane in the fused matvec */
+constexpr int HEAD_U = 8;   /* rows in flight per lane in the LM head (bandwidth-bound: 113 MB fp32 at 135M) */
 
 /* Sum of v over the 256 threads; every thread gets the result.  sh: 4 floats of LDS. */
 __device__ __forceinline__ float block_sum(float v, float* sh) {
@@ -50,6 +49,21 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
     if ((threadIdx.x & 63) == 0) sh[w] = v;
     __syncthreads();
     float r = (sh[0] + sh[1]) + (sh[2] + sh[3]);
+    __syncthreads();
+    return r;
+}
+
+/* Sum over a workgroup of WT threads (WT/64 waves); every thread gets it. */
+template <int WT>
+__device__ __forceinline__ float block_sum_t(float v, float* sh) {
+    v = wave_sum(v);
+    if (WT == 64) return v;
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) sh[w] = v;
+    __syncthreads();
+    float r = sh[0];
+#pragma unroll
+    for (int i = 1; i < WT / 64; i++) r += sh[i];
     __syncthreads();
     return r;
 }
@@ -298,16 +312,31 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
 
     for (int b = 0; b < a.B; b++) {
         const float* xb = a.x + (size_t)b * D;
-        const float inv = rms_inv(xb, D, a.eps, sh);
         constexpr int SEG = Q8 ? 32 : 16;
-        float xs[SEG];
+        float xs[SEG], nw[SEG];
         if (lane_on) {
 #pragma unroll
-            for (int i = 0; i < SEG; i++) xs[i] = (xb[SEG * sg + i] * inv) * a.norm_w[SEG * sg + i];
+            for (int i = 0; i < SEG; i += 4) {
+                float4 v4, g4;
+                __builtin_memcpy(&v4, __builtin_assume_aligned(xb + SEG * sg + i, 4), 16);
+                __builtin_memcpy(&g4, __builtin_assume_aligned(a.norm_w + SEG * sg + i, 4), 16);
+                xs[i] = v4.x; xs[i + 1] = v4.y; xs[i + 2] = v4.z; xs[i + 3] = v4.w;
+                nw[i] = g4.x; nw[i + 1] = g4.y; nw[i + 2] = g4.z; nw[i + 3] = g4.w;
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < SEG; i++) xs[i] = 0.0f;
+            for (int i = 0; i < SEG; i++) xs[i] = nw[i] = 0.0f;
         }
+        /* RMSNorm from registers: the lanes of row slot 0 hold every column once */
+        float ss = 0.0f;
+        if (lane_on && slot == 0) {
+#pragma unroll
+            for (int i = 0; i < SEG; i++) ss = fmaf(xs[i], xs[i], ss);
+        }
+        ss = block_sum(ss, sh);
+        const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int i = 0; i < SEG; i++) xs[i] = (xs[i] * inv) * nw[i];
 #pragma unroll
         for (int u = 0; u < HEAD_U; u++) {
             float p;
@@ -426,18 +455,22 @@ __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
     }
 }
 
-/* Fused Q8 matvec phase (see DecMv).  Lane t owns block column t % nb of
- * row slot t / nb; MV_U row passes are loaded before any arithmetic. */
-__global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
-    __shared__ float red[NT * MV_U];
-    __shared__ float sh[4];
+/* Fused Q8 matvec phase (see DecMv).  WT threads per workgroup; lane t
+ * owns block column t % nb of row slot t / nb (nb = C/32 <= WT); U row
+ * passes are loaded before any arithmetic.  Small WT and U give many
+ * workgroups of few rows: decode matrices are small, and spreading one over
+ * hundreds of CUs keeps each CU's share to a single memory round trip. */
+template <int WT, int U>
+__global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
+    __shared__ float red[WT * U];
+    __shared__ float sh[WT / 64];
     const int t = threadIdx.x;
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
     const int tile = (int)blockIdx.x - a.tile0[mi];
     const int nb = a.C / 32;
-    const int slots = NT / nb;
-    const int rows_per_tile = slots * MV_U;
+    const int slots = a.slots;
+    const int rows_per_tile = slots * U;
     const int slot = t / nb, bc = t - slot * nb;
     const bool lane_on = slot < slots;
     const long row0 = (long)tile * rows_per_tile;
@@ -446,9 +479,9 @@ __global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
     const int OC = a.OC[mi];
     const long nrows = glu ? 2L * OC : (long)OC;
 
-    Blk blk[MV_U];
+    Blk blk[U];
 #pragma unroll
-    for (int u = 0; u < MV_U; u++) {
+    for (int u = 0; u < U; u++) {
         const long lr = row0 + slot + (long)u * slots;
         if (lane_on && lr < nrows) {
             const unsigned char* wm = glu ? a.w[lr & 1] : a.w[mi];
@@ -460,10 +493,11 @@ __global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
     }
 
     for (int b = 0; b < a.B; b++) {
+        /* every global load of this row is issued before the first reduction:
+         * the lane's 32 activations, its 32 norm gains and, for the residual
+         * epilogue, the old value of the output row the thread will finish */
         const float* xb = a.x + (size_t)b * a.ldx;
-        float inv = 1.0f;
-        if (a.norm_w) inv = rms_inv(xb, a.C, a.eps, sh);
-        float xs[32];
+        float xs[32], nw[32];
         if (lane_on) {
             const float* xp = xb + 32 * bc;
 #pragma unroll
@@ -473,21 +507,39 @@ __global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
                 xs[i] = v4.x; xs[i + 1] = v4.y; xs[i + 2] = v4.z; xs[i + 3] = v4.w;
             }
             if (a.norm_w) {
-                const float* nw = a.norm_w + 32 * bc;
+                const float* np = a.norm_w + 32 * bc;
 #pragma unroll
-                for (int i = 0; i < 32; i++) xs[i] = (xs[i] * inv) * nw[i];
+                for (int i = 0; i < 32; i += 4) {
+                    float4 v4;
+                    __builtin_memcpy(&v4, __builtin_assume_aligned(np + i, 4), 16);
+                    nw[i] = v4.x; nw[i + 1] = v4.y; nw[i + 2] = v4.z; nw[i + 3] = v4.w;
+                }
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 32; i++) xs[i] = 0.0f;
+            for (int i = 0; i < 32; i++) xs[i] = nw[i] = 0.0f;
+        }
+        float res0 = 0.0f;
+        if (!glu && a.residual && t < rows_per_tile && row0 + t < OC) res0 = a.y[mi][(size_t)b * OC + row0 + t];
+        if (a.norm_w) {
+            /* the lanes of row slot 0 hold every column exactly once */
+            float ss = 0.0f;
+            if (lane_on && slot == 0) {
+#pragma unroll
+                for (int i = 0; i < 32; i++) ss = fmaf(xs[i], xs[i], ss);
+            }
+            ss = block_sum_t<WT>(ss, sh);
+            const float inv = 1.0f / sqrtf(ss / (float)a.C + a.eps);
+#pragma unroll
+            for (int i = 0; i < 32; i++) xs[i] = (xs[i] * inv) * nw[i];
         }
 #pragma unroll
-        for (int u = 0; u < MV_U; u++)
+        for (int u = 0; u < U; u++)
             if (lane_on) red[(slot + u * slots) * nb + bc] = block_dot(blk[u], xs);
         __syncthreads();
         if (glu) {
             const int half = rows_per_tile / 2;
-            for (int rl = t; rl < half; rl += NT) {
+            for (int rl = t; rl < half; rl += WT) {
                 const long j = (row0 >> 1) + rl;
                 if (j < OC) {
                     const float* rg = red + (2 * rl) * nb;
@@ -501,59 +553,177 @@ __global__ __launch_bounds__(NT) void k_dec_mv(DecMv a) {
                 }
             }
         } else {
-            for (int rl = t; rl < rows_per_tile; rl += NT) {
+            for (int rl = t; rl < rows_per_tile; rl += WT) {
                 const long r = row0 + rl;
                 if (r >= OC) break;
                 const float* rp = red + rl * nb;
                 float acc = 0.0f;
                 for (int k = 0; k < nb; k++) acc += rp[k];
                 float* yp = a.y[mi] + (size_t)b * OC + r;
-                *yp = a.residual ? *yp + acc : acc;
+                if (a.residual) acc = (rl == t ? res0 : *yp) + acc;
+                *yp = acc;
             }
         }
         __syncthreads();
     }
 }
 
-/* Rope + KV append + attention.  Workgroup (h, b): query head h of sequence b.
- * Every workgroup of a KV group ropes that group's key itself (same
- * instructions, same bits) and uses it for the current position; the
- * first query head of the group also appends k and v to the cache. */
+/* Rope + KV append + attention of one decode step; workgroup (h, b) =
+ * query head h of sequence b.  The engine's cache holds, per (sequence,
+ * layer), K per KV head as [HD/4][MS] float4 (4 dimensions of one
+ * position per 16 bytes; lanes scoring consecutive keys read consecutive
+ * 16-byte slots, so a wave's load is 1 KB contiguous) and V row-major
+ * ([MS][KV]).
+ *  - every workgroup of a KV group ropes the group's key itself (same
+ *    instructions, same bits) and uses it for the current position; the
+ *    group's first query head appends k and v to the cache;
+ *  - scores: one key per lane, its HD loads all in flight;
+ *  - P.V: 16 key groups x HD/4 float4 columns (coalesced 16-byte loads);
+ *  - online softmax over chunks of ATT_CH keys held in LDS.
+ * HDT > 0 fixes the head size at compile time (q in registers). */
+template <int HDT>
 __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
-    __shared__ float qs[256];
-    __shared__ float ks[256];
-    __shared__ float vs[256];
+    constexpr int HDMAX = HDT > 0 ? HDT : DEC_MAX_HD;
+    __shared__ float qs[HDMAX];
+    __shared__ float ks[HDMAX];
+    __shared__ float vs[HDMAX];
     __shared__ float sc[ATT_CH];
-    __shared__ float red[NT];
+    __shared__ float4 red4[NT];
     __shared__ float sh[4];
+    const int HD = HDT > 0 ? HDT : a.HD;
+    const int HD4 = HD / 4, KG = NT / HD4;
     const int h = blockIdx.x, b = blockIdx.y;
-    const int HD = a.HD, hd2 = HD / 2, kv_mul = a.NH / a.NKV, kh = h / kv_mul;
+    const int kv_mul = a.NH / a.NKV, kh = h / kv_mul;
     const int pos = a.st->pos;
+    const int t = threadIdx.x;
     const float* qh = a.q + (size_t)b * a.NH * HD + h * HD;
     const float* kr = a.k + (size_t)b * a.KV + kh * HD;
     const float* vr = a.v + (size_t)b * a.KV + kh * HD;
-    const int t = threadIdx.x;
-    if (t < hd2) {
+    if (t < HD / 2) {
         const float fr = a.inv_freq[t];
         const float ang = (float)pos * fr;
         const float c = cosf(ang), s = sinf(ang);
-        const float q0 = qh[t], q1 = qh[t + hd2];
+        const float q0 = qh[t], q1 = qh[t + HD / 2];
         qs[t] = q0 * c - q1 * s;
-        qs[t + hd2] = q0 * s + q1 * c;
-        const float k0 = kr[t], k1 = kr[t + hd2];
+        qs[t + HD / 2] = q0 * s + q1 * c;
+        const float k0 = kr[t], k1 = kr[t + HD / 2];
         ks[t] = k0 * c - k1 * s;
-        ks[t + hd2] = k0 * s + k1 * c;
+        ks[t + HD / 2] = k0 * s + k1 * c;
     }
     if (t < HD) vs[t] = vr[t];
     __syncthreads();
-    float* kc = a.kvc + (((size_t)b * a.L + a.layer) * 2 * a.MS) * a.KV + kh * HD;
-    float* vc = kc + (size_t)a.MS * a.KV;
+    const size_t slab = (size_t)a.MS * a.KV;
+    float* kT = a.kvc + ((size_t)b * a.L + a.layer) * 2 * slab + (size_t)kh * HD * a.MS;
+    float* vc = a.kvc + (((size_t)b * a.L + a.layer) * 2 + 1) * slab + kh * HD;
     if (h % kv_mul == 0 && t < HD) {
-        kc[(size_t)pos * a.KV + t] = ks[t];
+        kT[((size_t)(t >> 2) * a.MS + pos) * 4 + (t & 3)] = ks[t];
         vc[(size_t)pos * a.KV + t] = vs[t];
     }
-    attn_head(qs, kc, vc, a.KV, pos + 1, pos, ks, vs, HD, a.scale, sc, red, sh,
-              a.out + (size_t)b * a.NH * HD + h * HD);
+    float qr[HDT > 0 ? HDT : 1];
+    if (HDT > 0) {
+#pragma unroll
+        for (int e = 0; e < (HDT > 0 ? HDT : 1); e++) qr[e] = qs[e];
+    }
+    float s_cur;
+    {
+        float c0 = 0.f, c1 = 0.f;
+        for (int e = 0; e < HD; e += 2) {
+            c0 = fmaf(qs[e], ks[e], c0);
+            c1 = fmaf(qs[e + 1], ks[e + 1], c1);
+        }
+        s_cur = (c0 + c1) * a.scale;
+    }
+    const int S = pos + 1, n_cached = pos;
+    const int kg = t / HD4, dg = t - kg * HD4;
+    float m_run = -INFINITY, l_run = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int base = 0; base < S; base += ATT_CH) {
+        const int n = min(ATT_CH, S - base);
+        float lmax = -INFINITY;
+        for (int i = t; i < n; i += NT) {
+            const int tt = base + i;
+            float s;
+            if (tt < n_cached) {
+                const float* kcol = kT + (size_t)tt * 4;
+                const size_t step = (size_t)a.MS * 4;
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+                if (HDT > 0) {
+                    float4 k4[HDT > 0 ? HDT / 4 : 1];
+#pragma unroll
+                    for (int j = 0; j < (HDT > 0 ? HDT / 4 : 1); j++)
+                        __builtin_memcpy(&k4[j], __builtin_assume_aligned(kcol + j * step, 16), 16);
+#pragma unroll
+                    for (int j = 0; j < (HDT > 0 ? HDT / 4 : 1); j++) {
+                        s0 = fmaf(qr[4 * j + 0], k4[j].x, s0);
+                        s1 = fmaf(qr[4 * j + 1], k4[j].y, s1);
+                        s2 = fmaf(qr[4 * j + 2], k4[j].z, s2);
+                        s3 = fmaf(qr[4 * j + 3], k4[j].w, s3);
+                    }
+                } else {
+                    for (int j = 0; j < HD / 4; j++) {
+                        float4 k4;
+                        __builtin_memcpy(&k4, __builtin_assume_aligned(kcol + j * step, 16), 16);
+                        s0 = fmaf(qs[4 * j + 0], k4.x, s0);
+                        s1 = fmaf(qs[4 * j + 1], k4.y, s1);
+                        s2 = fmaf(qs[4 * j + 2], k4.z, s2);
+                        s3 = fmaf(qs[4 * j + 3], k4.w, s3);
+                    }
+                }
+                s = ((s0 + s1) + (s2 + s3)) * a.scale;
+            } else {
+                s = s_cur;
+            }
+            sc[i] = s;
+            lmax = fmaxf(lmax, s);
+        }
+        const float cmax = block_max(lmax, sh);
+        float lsum = 0.0f;
+        for (int i = t; i < n; i += NT) {
+            const float p = expf(sc[i] - cmax);
+            sc[i] = p;
+            lsum += p;
+        }
+        const float csum = block_sum(lsum, sh); /* its barriers also publish sc[] */
+        const float m_new = fmaxf(m_run, cmax);
+        const float a_old = expf(m_run - m_new), a_new = expf(cmax - m_new);
+        l_run = l_run * a_old + csum * a_new;
+        const int n_c = min(n, n_cached - base); /* keys of this chunk that are in the cache */
+        float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+        for (int i = kg; i < n_c; i += KG) {
+            float4 v4;
+            __builtin_memcpy(&v4, __builtin_assume_aligned(vc + (size_t)(base + i) * a.KV + 4 * dg, 16), 16);
+            const float p = sc[i];
+            part.x = fmaf(p, v4.x, part.x);
+            part.y = fmaf(p, v4.y, part.y);
+            part.z = fmaf(p, v4.z, part.z);
+            part.w = fmaf(p, v4.w, part.w);
+        }
+        if (n_c < n && kg == n_c % KG) {
+            const float p = sc[n_c];
+            part.x = fmaf(p, vs[4 * dg + 0], part.x);
+            part.y = fmaf(p, vs[4 * dg + 1], part.y);
+            part.z = fmaf(p, vs[4 * dg + 2], part.z);
+            part.w = fmaf(p, vs[4 * dg + 3], part.w);
+        }
+        acc.x = acc.x * a_old + part.x * a_new;
+        acc.y = acc.y * a_old + part.y * a_new;
+        acc.z = acc.z * a_old + part.z * a_new;
+        acc.w = acc.w * a_old + part.w * a_new;
+        m_run = m_new;
+        __syncthreads(); /* sc[] is rewritten by the next chunk */
+    }
+    red4[t] = acc;
+    __syncthreads();
+    if (t < HD) {
+        const int c4 = t >> 2, lane = t & 3;
+        float sum = 0.0f;
+        for (int k = 0; k < KG; k++) {
+            const float4 r = red4[k * HD4 + c4];
+            sum += lane == 0 ? r.x : lane == 1 ? r.y : lane == 2 ? r.z : r.w;
+        }
+        a.out[(size_t)b * a.NH * HD + h * HD + t] = sum / l_run;
+    }
 }
 
 } // namespace
@@ -747,11 +917,26 @@ extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {
 /* ================================================================== */
 /* Engine-side launchers (arguments already validated by engine.cpp). */
 
-extern "C" int dec_mv_tiles(int OC, int C, int glu) {
+/* Launch shape of a fused matvec phase over C columns: the smallest
+ * workgroup that holds a row's C/32 block columns, one row pass per lane;
+ * a SwiGLU phase keeps whole (gate, up) row pairs in a tile. */
+static void dec_mv_shape(int C, int glu, int* wt, int* slots) {
     const int nb = C / 32;
-    const int rows = (NT / nb) * MV_U;
+    *wt = nb <= 64 ? 64 : (nb <= 128 ? 128 : 256);
+    *slots = *wt / nb;
+    if (glu && *slots == 1 && *wt < 256) { /* a pair needs two row slots */
+        *wt *= 2;
+        *slots = *wt / nb;
+    }
+    if (glu && (*slots & 1)) *slots = *slots > 1 ? *slots - 1 : 0;
+}
+
+extern "C" int dec_mv_tiles(int OC, int C, int glu) {
+    int wt, slots;
+    dec_mv_shape(C, glu, &wt, &slots);
+    if (slots == 0) return -1; /* a gate/up pair wider than one workgroup: not supported */
     const long n = glu ? 2L * OC : (long)OC;
-    return (int)((n + rows - 1) / rows);
+    return (int)((n + slots - 1) / slots);
 }
 
 extern "C" int dec_head_tiles(int D, int V, int q8) { return head_tiles(D, V, q8 != 0); }
@@ -762,14 +947,23 @@ extern "C" int dec_launch_embed(const DecEmbed* a, hipStream_t s) {
     return 0;
 }
 
-extern "C" int dec_launch_mv(const DecMv* a, hipStream_t s) {
-    hipLaunchKernelGGL(k_dec_mv, dim3(a->tile0[a->nmat]), dim3(NT), 0, s, *a);
+extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
+    DecMv a = *a_in;
+    int wt;
+    dec_mv_shape(a.C, a.glu, &wt, &a.slots);
+    if (a.slots == 0) return -1;
+    const dim3 grid(a.tile0[a.nmat]);
+    if (wt == 64) hipLaunchKernelGGL((k_dec_mv<64, 1>), grid, dim3(64), 0, s, a);
+    else if (wt == 128) hipLaunchKernelGGL((k_dec_mv<128, 1>), grid, dim3(128), 0, s, a);
+    else hipLaunchKernelGGL((k_dec_mv<256, 1>), grid, dim3(256), 0, s, a);
     BMK_LAUNCH_CHECK();
     return 0;
 }
 
 extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
-    hipLaunchKernelGGL(k_dec_attn, dim3(a->NH, B), dim3(NT), 0, s, *a);
+    if (a->HD == 64) hipLaunchKernelGGL(k_dec_attn<64>, dim3(a->NH, B), dim3(NT), 0, s, *a);
+    else if (a->HD == 128) hipLaunchKernelGGL(k_dec_attn<128>, dim3(a->NH, B), dim3(NT), 0, s, *a);
+    else hipLaunchKernelGGL(k_dec_attn<0>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     BMK_LAUNCH_CHECK();
     return 0;
 }

@@ -59,19 +59,22 @@ typedef struct {
     int nmat;
     int glu;
     int residual;
-    int pad_;
+    int slots;                 /* rows per row pass of a workgroup (set by the launcher; even for glu) */
     const unsigned char* w[DEC_MAX_MATS];
     float* y[DEC_MAX_MATS];
     int OC[DEC_MAX_MATS];
     int tile0[DEC_MAX_MATS + 1];   /* workgroup prefix: matrix i owns tiles tile0[i] .. tile0[i+1]-1 */
 } DecMv;
 
-/* Rope + KV append + GQA attention for one layer of a decode step. */
+/* Rope + KV append + GQA attention for one layer of a decode step.  The
+ * cache is [B][L][2][MS*KV]: per (sequence, layer) first K, per KV head
+ * [HD/4][MS] float4 (4 dimensions of one position per 16 bytes), then V
+ * row-major ([MS][KV]). */
 typedef struct {
     const float* q;     /* [B][NH*HD] un-roped */
     const float* k;     /* [B][KV] un-roped */
     const float* v;     /* [B][KV] */
-    float* kvc;         /* [B][L][2][MS][KV] */
+    float* kvc;
     float* out;         /* [B][NH*HD] */
     const DecState* st;
     float inv_freq[DEC_MAX_HD / 2]; /* RoPE inverse frequency per rotary pair (host table) */

@@ -12,7 +12,7 @@
  * MI355X design:
  *   - weights live in HBM: one Q8 arena for every projection (packed on the
  *     device by quantize_q8 from the host fp32 copy), fp32 embedding/head
- *     and norm gains; fp32 KV cache [B][L][2][MS][KV];
+ *     and norm gains; fp32 KV cache [B][L][2][MS*KV] (K per KV head as [HD/4][MS] float4, V row-major);
  *   - a step is 2 + 5L kernels (embed; per layer: RMSNorm+qkv, rope+KV
  *     append+attention, o+residual, RMSNorm+gate/up+SwiGLU,
  *     down+residual; head+argmax), see decode.hip;
@@ -161,7 +161,7 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
     const int QD = NH * HD, KV = NKV * HD;
     /* layout constraints of the gfx950 kernels (decode.hip) */
     if (D % 32 || H % 32 || QD % 32 || D / 32 > 256 || H / 32 > 256 || QD / 32 > 256 || D % 16 || D / 16 > 256 ||
-        NH % NKV || HD > 256 || 256 % HD || HD % 4 || KV % 4) {
+        NH % NKV || HD > 256 || 256 % HD || HD % 4 || KV % 4 || dec_mv_tiles(H, D, 1) < 0) {
         BMK_ERR("bm_create_model: shape D=%d H=%d NH=%d NKV=%d HD=%d outside the decode kernels' layout", D, H, NH, NKV,
                 HD);
         return NULL;
@@ -469,6 +469,7 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
               hipMalloc(&S->st, sizeof(DecState)) == hipSuccess &&
               hipMalloc(&S->out_tokens, B * (size_t)S->MS * 4) == hipSuccess &&
               hipMalloc(&S->prompt, B * (size_t)S->MS * 4) == hipSuccess &&
+
               hipHostMalloc(&S->h_st, sizeof(DecState), hipHostMallocDefault) == hipSuccess &&
               hipHostMalloc(&S->h_logits, B * m->V * 4, hipHostMallocDefault) == hipSuccess &&
               hipEventCreate(&S->ev0) == hipSuccess && hipEventCreate(&S->ev1) == hipSuccess;

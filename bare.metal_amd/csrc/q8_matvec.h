@@ -9,7 +9,8 @@
 #include <hip/hip_runtime.h>
 
 #define MV_MAX_PROBS 8
-#define MV_U 4
+#define MV_U 4        /* rows in flight per lane for small launches */
+#define MV_U_WIDE 8   /* rows in flight per lane when the launch has work for every CU many times over */
 
 /* One y = W x (+ bias) problem; W is OC rows of nb 36-byte Q8 blocks. */
 typedef struct {

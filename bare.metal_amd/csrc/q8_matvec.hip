@@ -179,14 +179,26 @@ extern "C" int mv_tiles_for(int OC, int C, int U) {
     return (OC + rows - 1) / rows;
 }
 
+/* Tiles at MV_U above which a launch uses MV_U_WIDE rows per lane: enough
+ * workgroups to give each of MI355X's 256 CUs several even at the wider tile.
+ * More bytes in flight per lane is what lifts a streaming matvec toward the
+ * HBM roofline; fewer, wider tiles would starve the CUs on small matrices. */
+#define MV_WIDE_MIN_TILES 4096
+
 extern "C" int mv_launch_group(MvGroup* g, hipStream_t s) {
     long total = 0;
+    for (int i = 0; i < g->nprob; i++) total += mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, MV_U);
+    if (total <= 0) return 0;
+    const int U = total >= MV_WIDE_MIN_TILES ? MV_U_WIDE : MV_U;
+    total = 0;
     for (int i = 0; i < g->nprob; i++) {
-        g->p[i].tiles = mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, MV_U);
+        g->p[i].tiles = mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, U);
         total += g->p[i].tiles;
     }
-    if (total <= 0) return 0;
-    hipLaunchKernelGGL(k_q8_matvec<MV_U>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
+    if (U == MV_U_WIDE)
+        hipLaunchKernelGGL(k_q8_matvec<MV_U_WIDE>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
+    else
+        hipLaunchKernelGGL(k_q8_matvec<MV_U>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -202,7 +214,7 @@ extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_
 extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
                                const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
     if (n_tiles <= 0) return 0;
-    hipLaunchKernelGGL(k_q8_matvec_multi<MV_U>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y, d_desc,
+    hipLaunchKernelGGL(k_q8_matvec_multi<MV_U_WIDE>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y, d_desc,
                        d_tile_map);
     BMK_LAUNCH_CHECK();
     return 0;
@@ -232,9 +244,9 @@ extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
     for (int i = 0; i < nprob; i++) {
         const MvDesc& d = desc[i];
         BMK_REQUIRE(d.OC > 0 && d.C > 0 && d.C % 32 == 0, "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, d.OC, d.C);
-        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, MV_U) && d.tile0 == next_tile,
+        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, MV_U_WIDE) && d.tile0 == next_tile,
                     "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
-                    mv_tiles_for(d.OC, d.C, MV_U), next_tile);
+                    mv_tiles_for(d.OC, d.C, MV_U_WIDE), next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 matvec multi: problem %d weight offset not 4-byte aligned", i);
         BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * 36 <= a->bytes[2] &&
                     d.x_off + (unsigned long long)d.C <= a->bytes[3] / 4 &&

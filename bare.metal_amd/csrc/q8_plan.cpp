@@ -13,7 +13,7 @@
 
 extern "C" int bm_q8_mv_tiles(int OC, int C) {
     if (OC <= 0 || C <= 0 || C % 32) return -1;
-    return mv_tiles_for(OC, C, MV_U);
+    return mv_tiles_for(OC, C, MV_U_WIDE);
 }
 
 extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
@@ -40,7 +40,7 @@ extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* 
         d[i].OC = OC[i];
         d[i].C = C[i];
         d[i].tile0 = t0;
-        d[i].tiles = mv_tiles_for(OC[i], C[i], MV_U);
+        d[i].tiles = mv_tiles_for(OC[i], C[i], MV_U_WIDE);
         for (int k = 0; k < d[i].tiles; k++) map[t0 + k] = (unsigned int)i;
         t0 += d[i].tiles;
     }

@@ -75,8 +75,8 @@ def test_mv_plan_layout():
     C = [960, 960, 960, 2560, 9600]
     plan, n_tiles = bmhip.mv_plan([0, 1, 2, 3, 4], [5, 6, 7, 8, 9], [10, 11, 12, 13, 14], OC, C)
     tiles = [bmhip.lib().bm_q8_mv_tiles(o, c) for o, c in zip(OC, C)]
-    # 256 lanes hold 256 // (C/32) rows per pass, 4 passes per workgroup; C/32 > 256: one row each
-    assert tiles == [-(-960 // 32), -(-320 // 32), 49152 // 32, 1, 3]
+    # 256 lanes hold 256 // (C/32) rows per pass, 8 passes per workgroup; C/32 > 256: one row each
+    assert tiles == [-(-960 // 64), -(-320 // 64), 49152 // 64, 1, 3]
     assert n_tiles == sum(tiles)
     desc = np.frombuffer(plan[:40 * 5].tobytes(), dtype=np.dtype([("w", "<u8"), ("x", "<u8"), ("y", "<u8"),
                                                                    ("OC", "<i4"), ("C", "<i4"),
