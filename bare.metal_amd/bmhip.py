@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
         "bm_q8_mv_tiles": (i, [i, i]),
         "bm_q8_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
+        "bm_q8_gemm_tiles": (i, [i, i, i]),
+        "bm_q8_gemm_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_create": (vp, [i]),
         "bm_destroy": (None, [vp]),
         "bm_get_supported_precision": (i, [vp]),
@@ -152,6 +154,22 @@ def mv_plan(w_off, x_off, y_off, OC, C_):
                               C.byref(nt))
     if got != need:
         raise ValueError("bm_q8_mv_plan failed")
+    return plan.view(np.uint8)[:need].copy(), nt.value
+
+
+def gemm_plan(a_off, w_off, c_off, M, N, K, lda, ldc):
+    """Plan table (bytes) and workgroup count of a matmul_forward_q8_multi launch."""
+    n = len(M)
+    u = [np.ascontiguousarray(v, dtype=np.uint64) for v in (a_off, w_off, c_off)]
+    ints = [np.ascontiguousarray(v, dtype=np.int32) for v in (M, N, K, lda, ldc)]
+    nt = C.c_int(0)
+    args = [_ptr(v) for v in u] + [_ptr(v) for v in ints]
+    need = lib().bm_q8_gemm_plan(n, *args, None, 0, C.byref(nt))
+    if need < 0:
+        raise ValueError("bm_q8_gemm_plan rejected the problem list")
+    plan = np.zeros((need + 7) // 8, dtype=np.uint64)
+    if lib().bm_q8_gemm_plan(n, *args, _ptr(plan), plan.nbytes, C.byref(nt)) != need:
+        raise ValueError("bm_q8_gemm_plan failed")
     return plan.view(np.uint8)[:need].copy(), nt.value
 
 

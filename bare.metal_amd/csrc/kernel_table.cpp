@@ -16,6 +16,8 @@ int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
 int bmk_launch_copy_buffer(const bmk_launch_t* a);
+int bmk_launch_q8_gemm_multi(const bmk_launch_t* a);
+int bmk_launch_cast_bf16(const bmk_launch_t* a);
 int bmk_launch_rmsnorm(const bmk_launch_t* a);
 int bmk_launch_rope(const bmk_launch_t* a);
 int bmk_launch_kv_store(const bmk_launch_t* a);
@@ -41,6 +43,11 @@ extern "C" const bmk_desc_t bmk_table[] = {
     /* new: every Q8 matvec of a decode token in one launch; {params{nprob,n_tiles},
      * plan{MvDesc[nprob], u32 tile_map[n_tiles]}, weight arena, x arena, y arena} */
     {"matmul_forward_q8_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_matvec_multi, B(1)},
+    /* new: many prefill GEMMs (bf16 MFMA) in one launch; {params{nprob,n_tiles},
+     * plan{GmDesc[nprob], u32 tile_map[n_tiles]}, A arena, weight arena, C arena} */
+    {"matmul_forward_q8_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_gemm_multi, B(1)},
+    /* new: fp32 -> bf16 activation cast (RNE); {src, dst, params int64{n}} */
+    {"cast_f32_bf16", 3, B(2), B(1), bmk_launch_cast_bf16, 0},
     /* new: device-to-device copy; {src, dst, params int64{nbytes}} */
     {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
     /* decode-step kernels (buffer orders: reference scheduler.c:835-947) */

@@ -8,6 +8,9 @@
 #include <hip/hip_runtime.h>
 
 #define GM_MAX_PROBS 8
+#define GM_BM 128   /* C tile rows (tokens) per workgroup */
+#define GM_BN 128   /* C tile columns (output features) per workgroup */
+#define GM_IDLE_TILE 0xffffffffu /* tile-map entry of a workgroup with no tile */
 
 /* C[M][N] (row stride ldc) = A[M][K] (row stride lda) x W^T, W = N rows of K/32 Q8 blocks. */
 typedef struct {
@@ -23,6 +26,14 @@ typedef struct {
     GmProb p[GM_MAX_PROBS];
     int nprob;
 } GmGroup;
+
+/* One problem of a multi-GEMM launch, addressed by offsets into three arenas
+ * (activations and outputs in floats, weights in bytes); it owns workgroups
+ * tile0 .. tile0+tiles-1 (row-major over its M x N tiles). */
+typedef struct {
+    unsigned long long a_off, w_off, c_off;
+    int M, N, K, lda, ldc, tile0, tiles, pad_;
+} GmDesc;
 
 #ifdef __cplusplus
 extern "C" {

@@ -7,6 +7,7 @@
  */
 #include "bmk.h"
 #include "q8_matvec.h"
+#include "q8_gemm.h"
 #include "../../include/bm_q8.h"
 
 #include <string.h>
@@ -43,6 +44,81 @@ extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* 
         d[i].tiles = mv_tiles_for(OC[i], C[i], MV_U_WIDE);
         for (int k = 0; k < d[i].tiles; k++) map[t0 + k] = (unsigned int)i;
         t0 += d[i].tiles;
+    }
+    return (long)need;
+}
+
+extern "C" int bm_q8_gemm_tiles(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32) return -1;
+    return gm_tiles_for(M, N);
+}
+
+/* Workgroup order of a multi-GEMM launch.  MI355X dispatches workgroup b
+ * to XCD b % 8, and each XCD has its own L2.  Every (problem, N tile) pair
+ * is given to one XCD, round-robin, and its M tiles run back to back
+ * there: the pair's weight rows (a 128-row panel of Q8 blocks) come from
+ * HBM once and are reused from that XCD's L2 by the other M tiles, and each
+ * XCD keeps the activation rows it touches resident.
+ * tile_map[8*j + x] = (problem << 16) | tile (row-major over the problem's
+ * M x N tiles), the j-th entry of XCD x's queue; queues shorter than the
+ * longest are padded with GM_IDLE_TILE (the workgroup returns at once), so
+ * the launch has 8 x (longest queue) workgroups. */
+#define GM_XCDS 8
+
+static long gemm_queue_len(int nprob, const int* M, const int* N, long* per_xcd) {
+    for (int x = 0; x < GM_XCDS; x++) per_xcd[x] = 0;
+    long pair = 0;
+    for (int i = 0; i < nprob; i++) {
+        const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
+        for (int n = 0; n < tn; n++, pair++) per_xcd[pair % GM_XCDS] += tm;
+    }
+    long longest = 0;
+    for (int x = 0; x < GM_XCDS; x++) longest = per_xcd[x] > longest ? per_xcd[x] : longest;
+    return longest;
+}
+
+extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                                const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
+                                size_t plan_bytes, int* n_tiles_out) {
+    if (nprob < 0 || nprob > 0xffff || (nprob > 0 && (!a_off || !w_off || !c_off || !M || !N || !K || !lda || !ldc)))
+        return -1;
+    for (int i = 0; i < nprob; i++) {
+        const int t = bm_q8_gemm_tiles(M[i], N[i], K[i]);
+        if (t < 0 || t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
+    }
+    long per_xcd[GM_XCDS];
+    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, per_xcd);
+    if (slots > 0x7fffffffL) return -1;
+    const size_t need = (size_t)nprob * sizeof(GmDesc) + (size_t)slots * 4;
+    if (n_tiles_out) *n_tiles_out = (int)slots;
+    if (!plan) return (long)need;
+    if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
+    GmDesc* d = (GmDesc*)plan;
+    unsigned int* map = (unsigned int*)((char*)plan + (size_t)nprob * sizeof(GmDesc));
+    int t0 = 0;
+    for (int i = 0; i < nprob; i++) {
+        d[i].a_off = a_off[i];
+        d[i].w_off = w_off[i];
+        d[i].c_off = c_off[i];
+        d[i].M = M[i];
+        d[i].N = N[i];
+        d[i].K = K[i];
+        d[i].lda = lda[i];
+        d[i].ldc = ldc[i];
+        d[i].tile0 = t0;
+        d[i].tiles = gm_tiles_for(M[i], N[i]);
+        d[i].pad_ = 0;
+        t0 += d[i].tiles;
+    }
+    for (long b = 0; b < slots; b++) map[b] = GM_IDLE_TILE;
+    long fill[GM_XCDS] = {0};
+    long pair = 0;
+    for (int i = 0; i < nprob; i++) {
+        const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
+        for (int n = 0; n < tn; n++, pair++) {
+            const int x = (int)(pair % GM_XCDS);
+            for (int m = 0; m < tm; m++) map[(long)GM_XCDS * fill[x]++ + x] = ((unsigned int)i << 16) | (unsigned)(m * tn + n);
+        }
     }
     return (long)need;
 }

@@ -167,6 +167,92 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
     }
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def gemm_leg(steps: int, warmup: int):
+    """Config 4: prefill Q8 GEMM at SmolLM2-135M shapes, M = 512 tokens, all
+    30 layers x (q,k,v,o,gate,up,down) in one matmul_forward_q8_multi launch.
+    Activations: one 512x576 and one 512x1536 fp32 N(0,1) matrix (cast to
+    bf16 inside the kernel); weights: independently seeded N(0,0.02), packed
+    to Q8 on the device; fp32 outputs."""
+    be = bmhip.Backend()
+    mid, D, H, NH, NKV, HD, L = MODELS["135m"]
+    M = 512
+    probs = problem_list("135m", head=False)
+    a1 = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, 4, 0, 1), 1.0, M * D)
+    a2 = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, 4, 0, 2), 1.0, M * H)
+    A32 = be.upload(np.concatenate([a1, a2]))
+    Abuf = be.alloc(2 * (a1.size + a2.size))  # bf16 copy, written by cast_f32_bf16 inside every step
+    wl = Workload.__new__(Workload)  # reuse the Q8 weight packing of the matvec workload
+    wl.be = be
+    wl.probs = probs
+    OC = np.array([p[4] for p in probs], np.int64)
+    K = np.array([p[5] for p in probs], np.int64)
+    wbytes = OC * (K // 32) * 36
+    wl.w_off = np.concatenate([[0], np.cumsum(wbytes)[:-1]]).astype(np.uint64)
+    wl.x_off = np.concatenate([[0], np.cumsum(K)[:-1]]).astype(np.uint64)
+    wl.OC, wl.C = OC.astype(np.int32), K.astype(np.int32)
+    wl.W = be.alloc(int(wbytes.sum()))
+    wl.X = be.alloc(4 * int(K.sum()))
+    wl.pack_ms = 0.0
+    wl._fill()
+    a_off = np.array([0 if k == D else M * D for k in K], np.uint64)
+    c_sizes = M * OC
+    c_off = np.concatenate([[0], np.cumsum(c_sizes)[:-1]]).astype(np.uint64)
+    Cbuf = be.alloc(4 * int(c_sizes.sum()))
+    plan, n_tiles = bmhip.gemm_plan(a_off, wl.w_off, c_off, [M] * len(probs), OC, K, K, OC)
+    pbuf, params = be.upload(plan), be.params(len(probs), n_tiles, 1)
+    kern = be.kernel("matmul_forward_q8_multi")
+    cast = be.kernel("cast_f32_bf16")
+    cast_bufs = [A32, Abuf, be.params(a1.size + a2.size, dtype=np.int64)]
+    bufs = [params, pbuf, Abuf, wl.W, Cbuf]
+
+    def step(enc):
+        """One step: cast the step's activations to bf16, then every GEMM."""
+        if enc.dispatch(cast, cast_bufs, (a1.size + a2.size,), (256,)) or \
+                enc.dispatch(kern, bufs, (n_tiles * 256,), (256,)):
+            raise RuntimeError("prefill GEMM dispatch rejected")
+
+    enc = be.encoder()
+    for _ in range(max(warmup, 1)):
+        step(enc)
+    enc.wait_timed()
+    # the multi launch must equal the single-problem matmul_forward_q8 on a few problems
+    c_all = Cbuf.read(np.float32)
+    for i in (0, 1, 6, len(probs) - 1):
+        N_, K_ = int(OC[i]), int(K[i])
+        out = be.alloc(4 * M * N_)
+        rc = be.dispatch("matmul_forward_q8", [A32, wl.W, out, out, be.params(M, K_, N_, 0)],
+                         ((N_ + 31) & ~31, M), (32,), offsets=[4 * int(a_off[i]), int(wl.w_off[i]), 0, 0, 0])
+        if rc != 0 or not np.array_equal(out.read(np.float32), c_all[int(c_off[i]):int(c_off[i]) + M * N_]):
+            raise RuntimeError(f"multi GEMM differs from the single launch on {probs[i][0]}")
+    enc = be.encoder()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step(enc)
+    ms = enc.wait_timed() / steps
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    flops = 2.0 * M * float((OC * K).sum())
+    bytes_ = float(wbytes.sum()) + 4.0 * M * float(K.sum()) + 4.0 * float(c_sizes.sum())
+    tflops = flops / (ms * 1e-3) / 1e12
+    bound = min(MFMA_BF16_PEAK_TFLOPS, flops / bytes_ * HBM_PEAK_GBS / 1e3)
+    be.close()
+    log(f"[bench] prefill GEMM: {ms * 1e3:.1f} us per 30-layer launch, {tflops:.1f} TFLOP/s "
+        f"({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of bf16 MFMA peak, {tflops / bound:.1%} of min(peak, AI*BW))")
+    return {
+        "workload": "SmolLM2-135M prefill Q8 GEMM, M=512: 30 layers x (q,k,v,o,gate,up,down) in one launch, "
+                    "bf16 MFMA with fp32 accumulate; a step = cast of the two fp32 activation matrices to bf16 "
+                    "+ the GEMM launch",
+        "flops_per_launch": flops, "flops_per_layer": flops / L, "bytes_per_launch": bytes_,
+        "us_per_launch": round(ms * 1e3, 2), "wall_us_per_launch": round(wall * 1e3, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "min_peak_ai_bw": round(bound, 1), "frac_of_min_bound": round(tflops / bound, 4)},
+        "workgroups": n_tiles,
+    }
+
+
 def e2e_decode(cpu_steps: int, cpu_threads: int):
     """Config 5: SmolLM2-135M Q8 greedy decode, 128-token prompt + 256
     generated tokens (383 decode steps, prompt tokens stepped one by one as
@@ -224,6 +310,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("OMP_NUM_THREADS", "16") or 16))
     ap.add_argument("--e2e", type=int, default=1, help="also time config-5 greedy decode (0: skip)")
     ap.add_argument("--matvec", type=int, default=1, help="0: only the config-5 decode leg (for kernel traces)")
+    ap.add_argument("--gemm", type=int, default=1, help="also time the config-4 prefill GEMM (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
@@ -246,7 +333,12 @@ def main():
                           "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
         return
     if not args.matvec:
-        print(json.dumps({"e2e_decode": e2e_decode(0, args.cpu_threads)}), flush=True)
+        out = {}
+        if args.gemm:
+            out["prefill_gemm"] = gemm_leg(max(args.steps // 10, 10), 3)
+        if args.e2e:
+            out["e2e_decode"] = e2e_decode(0, args.cpu_threads)
+        print(json.dumps(out), flush=True)
         return
     be = bmhip.Backend()
     probs = problem_list(args.model)
@@ -287,6 +379,7 @@ def main():
     del wl
     be.close()
 
+    gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
     e2e = e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads) if args.e2e else None
 
     mid, D, H, NH, NKV, HD, L = MODELS[args.model]
@@ -324,6 +417,7 @@ def main():
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
         "pack_gbps_incl_upload": pack_gbps,
+        "prefill_gemm": gemm,
         "e2e_decode": e2e,
     }
     print(json.dumps(line), flush=True)

@@ -13,6 +13,11 @@
  *   "matmul_forward_q8_vec_multi"
  *                        {params int{nprob, n_tiles}, plan (bm_q8_mv_plan),
  *                         weight arena, activation arena f32, output arena f32}
+ *   "matmul_forward_q8_multi"
+ *                        {params int{nprob, n_tiles[, a_bf16]}, plan (bm_q8_gemm_plan),
+ *                         activation arena (f32, or bf16 when a_bf16 = 1),
+ *                         weight arena, output arena f32}
+ *   "cast_f32_bf16"      {src f32 [n], dst bf16 [n], params int64{n}} (round to nearest even)
  *   "copy_buffer"        {src, dst, params int64{nbytes}}
  */
 #ifndef BM_Q8_H
@@ -38,6 +43,20 @@ int  bm_q8_mv_tiles(int OC, int C);
  * receives the launch's workgroup count. */
 long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                    const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
+
+/* Workgroups of one C[M][N] = A[M][K] x W^T prefill GEMM in a
+ * matmul_forward_q8_multi launch (128 x 128 output tiles); -1 if K is not a
+ * positive multiple of 32. */
+int  bm_q8_gemm_tiles(int M, int N, int K);
+
+/* Plan table of a matmul_forward_q8_multi launch: problem i reads A at
+ * float offset a_off[i] (row stride lda[i]) of the activation arena, Q8
+ * rows at byte offset w_off[i] of the weight arena, and writes C at float
+ * offset c_off[i] (row stride ldc[i]) of the output arena.  Same return
+ * convention as bm_q8_mv_plan. */
+long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                     const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
+                     size_t plan_bytes, int* n_tiles);
 
 #ifdef __cplusplus
 }

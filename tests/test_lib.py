@@ -88,3 +88,31 @@ def test_mv_plan_layout():
     assert bmhip.lib().bm_q8_mv_tiles(10, 48) == -1
     with pytest.raises(ValueError):
         bmhip.mv_plan([0], [0], [0], [4], [33])
+
+
+def test_gemm_plan_layout():
+    import numpy as np
+
+    plan, n = bmhip.gemm_plan([0, 10], [0, 36], [0, 7], [512, 100], [576, 70], [576, 96], [576, 96], [576, 70])
+    # 128x128 tiles: ceil(512/128) * ceil(576/128) = 20 and 1; six (problem, N tile) pairs
+    # round-robin over 8 XCD queues of 4, 4, 4, 4, 4, 1, 0, 0 tiles -> 8 x 4 workgroups
+    assert n == 32
+    assert bmhip.lib().bm_q8_gemm_tiles(512, 576, 576) == 20
+    assert bmhip.lib().bm_q8_gemm_tiles(16, 16, 48) == -1
+    tmap = np.frombuffer(plan[2 * 56:].tobytes(), dtype=np.uint32)  # GmDesc is 56 bytes
+    # every (problem, tile) exactly once, the rest idle; workgroup b runs on
+    # XCD b % 8 and an N-tile's M tiles stay on one XCD
+    tmap = tmap[tmap != 0xFFFFFFFF]
+    pairs = sorted((int(v) >> 16, int(v) & 0xFFFF) for v in tmap)
+    assert pairs == [(0, t) for t in range(20)] + [(1, 0)]
+    xcd_of = {}
+    full = np.frombuffer(plan[2 * 56:].tobytes(), dtype=np.uint32)
+    for b, v in enumerate(full):
+        if v == 0xFFFFFFFF:
+            continue
+        p, t = int(v) >> 16, int(v) & 0xFFFF
+        n = t % (5 if p == 0 else 1)
+        xcd_of.setdefault((p, n), set()).add(b % 8)
+    assert all(len(x) == 1 for x in xcd_of.values())
+    with pytest.raises(ValueError):
+        bmhip.gemm_plan([0], [0], [0], [4], [4], [64], [32], [4])  # lda < K
