@@ -19,7 +19,7 @@
  * elements.  The global loads of step s+2 are issued before the 32 MFMAs
  * of step s, and step s+1 is converted into the other LDS buffer after
  * them: two steps of MFMA work cover each load's latency, with one
- * barrier per step.
+ * barrier per step (details at gemm_tile).
  * Launches: up to GM_MAX_PROBS problems by value (matmul_forward_q8), or any
  * number of problems described by a device table (matmul_forward_q8_multi).
  */
@@ -36,15 +36,10 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int BM = GM_BM, BN = GM_BN, NTH = 256;
-constexpr int GEMM_BK = 64;        /* K step of the launched kernels (see gemm_tile) */
-constexpr bool TWO_STAGE = false;  /* prefetch depth of the launched kernels (see gemm_tile) */
-constexpr int GEMM_BK_BF16 = 64;   /* K step of the bf16-activation kernel */
-constexpr bool TWO_STAGE_BF16 = true;
-constexpr bool DEEP_W_BF16 = false;  /* bf16 kernel: W four steps ahead, A two */
-
-/* LDS of one tile: 2 buffers x (A slab + W slab), rows of BK + 8 bf16 */
-template <int BK>
-constexpr int gemm_lds_elems() { return 4 * BM * (BK + 8); }
+constexpr int GEMM_BK = 64;         /* K step: two Q8 blocks */
+constexpr int LDK = GEMM_BK + 8;    /* LDS row in bf16 elements; the padding spreads rows over the banks */
+constexpr int SLAB = BM * LDK;      /* one operand slab (BM == BN) */
+constexpr int GEMM_LDS = 4 * SLAB;  /* 2 buffers x (A slab + W slab), bf16 elements */
 
 /* fp32 pair -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32) */
 __device__ __forceinline__ unsigned int pk_bf16(float lo, float hi) {
@@ -57,19 +52,17 @@ __device__ __forceinline__ unsigned int pk_bf16(float lo, float hi) {
 
 __device__ __forceinline__ float sbyte(unsigned int w, int k) { return (float)(signed char)((w >> (8 * k)) & 0xffu); }
 
-/* One K step of one loader thread (BK = 64: two Q8 blocks, BK = 32: one).
- * A (fp32): rows t/(BK/4) + (1024/BK)*p (p < BK/8), columns 4*(t % (BK/4))
- * .. +4; A (bf16): rows t/(BK/8) + (2048/BK)*p (p < BK/16), columns
- * 8*(t % (BK/8)) .. +8.  Either way the lanes of a row read it
- * contiguously and a wave instruction covers whole rows.  W: row t/2;
- * BK = 64: Q8 block 2*step + t%2 (36 bytes), BK = 32: half t%2 of the
- * step's block (scale + 16 bytes). */
-template <int BK, bool ABF16>
+/* Register stage of one loader thread for one K step (two Q8 blocks).
+ * A (fp32): rows t/16 + 16p (p < 8), columns 4*(t%16) .. +4; A (bf16):
+ * rows t/8 + 32p (p < 4), columns 8*(t%8) .. +8.  Either way the lanes of a
+ * row read it contiguously and a wave instruction covers whole rows.
+ * W: row t/2, Q8 block 2*step + t%2 (36 bytes: scale, 32 int8). */
+template <bool ABF16>
 struct Stage {
-    float4 a[ABF16 ? 1 : BK / 8];
-    uint4 ab[ABF16 ? BK / 16 : 1];
+    float4 a[ABF16 ? 1 : 8];
+    uint4 ab[ABF16 ? 4 : 1];
     float s;
-    uint4 q[BK / 32];
+    uint4 q[2];
 };
 
 __device__ __forceinline__ uint4 dq8(const uint4& q, int half, float s) {
@@ -82,140 +75,83 @@ __device__ __forceinline__ uint4 dq8(const uint4& q, int half, float s) {
     return r;
 }
 
-/* One 128x128 tile of C.  lds: 2 buffers x (A slab + W slab).
- * DEPTH2 = false: per K step s, issue the global loads of step s+1, run the
- * MFMAs of step s from LDS, convert step s+1 into the other buffer,
- * barrier.  DEPTH2 = true: two register stages; the loads of step s+2 are
- * issued before the MFMAs of step s. */
-template <int BK, bool DEPTH2, bool ABF16, bool DEEPW = false>
+/* One 128x128 tile of C; lds holds 2 buffers x (A slab + W slab).
+ *
+ * K runs in steps of 64 (two Q8 blocks).  The nb/2 full steps form a
+ * two-stage pipeline: the global loads of step s+2 are issued before the
+ * 32 MFMAs of step s, and step s+1 is stored into the other LDS buffer
+ * after them, with one barrier per step.  The loop body has no data
+ * dependent selects and issues the same loads on every path (past the
+ * last step it reloads that step, an L2 hit that is never stored), so the
+ * compiler's wait before a store counts only the loads that feed it; a
+ * conditional load or an early consumer of a load's registers makes it
+ * drain the whole queue instead.  An odd block count leaves a half step,
+ * run after the loop with the out-of-range half zeroed.
+ * Rows past M (or N) only feed C entries that are never stored, so the
+ * loaders clamp them to the last row instead of branching.  Offsets are
+ * 32-bit from workgroup-uniform bases (the launchers check that they fit). */
+template <bool ABF16>
 __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const unsigned char* __restrict__ W,
                                           float* __restrict__ Cm, int M, int N, int K, int lda, int ldc, int tm,
                                           int tn, unsigned short* lds) {
-    constexpr int LDK = BK + 8;
-    constexpr int SLAB = BM * LDK;
-    constexpr int CPR = ABF16 ? BK / 8 : BK / 4; /* 16-byte chunks of an A row */
-    constexpr int RPP = NTH / CPR;               /* A rows per loader pass */
-    constexpr int NPASS = BM / RPP;              /* BK/16 (bf16) or BK/8 (fp32) */
-    constexpr int EPC = ABF16 ? 8 : 4;           /* A elements per chunk */
+    constexpr int CPR = ABF16 ? GEMM_BK / 8 : GEMM_BK / 4; /* 16-byte chunks of an A row */
+    constexpr int RPP = NTH / CPR;                         /* A rows per loader pass */
+    constexpr int NPASS = BM / RPP;
+    constexpr int EPC = ABF16 ? 8 : 4;                     /* A elements per chunk */
     const int t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int m0 = tm * BM, n0 = tn * BN;
     const int nb = K / 32;
-    const int nsteps = (K + BK - 1) / BK;
-    const int lr = t >> 1, lh = t & 1;           /* W loader: row, half */
-    const int ar = t / CPR, ac = t % CPR;        /* A loader: first row, float4 column */
-    /* Rows past M (or N) only feed C entries that are never stored, so the
-     * loaders clamp them to the last row instead of branching; only a K
-     * block past the end (odd block count with BK = 64) must contribute
-     * zero, which the selects below provide.  Offsets are 32-bit from
-     * workgroup-uniform bases (the launchers check that they fit). */
+    const int nfull = nb >> 1;
+    const int lr = t >> 1, lh = t & 1;    /* W loader: row, block of the pair */
+    const int ar = t / CPR, ac = t % CPR; /* A loader: first row, chunk */
     const float* Af = (const float*)Av + (ABF16 ? 0 : (size_t)m0 * lda);
     const unsigned short* Ah = (const unsigned short*)Av + (ABF16 ? (size_t)m0 * lda : 0);
     const unsigned char* Wb = W + (size_t)n0 * nb * 36;
     unsigned int aoff[NPASS];
 #pragma unroll
     for (int p = 0; p < NPASS; p++) aoff[p] = (unsigned)min(ar + RPP * p, M - 1 - m0) * (unsigned)lda + (unsigned)(EPC * ac);
-    const unsigned int woff = (unsigned)min(lr, N - 1 - n0) * (unsigned)(nb * 36);
+    const unsigned int woff = (unsigned)min(lr, N - 1 - n0) * (unsigned)(nb * 36) + (unsigned)lh * 36u;
 
-    /* split loaders for the deep-W pipeline: A stages and W stages rotate separately */
-    auto load_a = [&](int step, Stage<BK, ABF16>& st) {
-        const bool ka = (BK * step + EPC * ac) / 32 < nb;
-        const unsigned int col = ka ? (unsigned)(step * BK) : 0u;
+    auto load_a = [&](unsigned int col, Stage<ABF16>& st) {
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
-            if (ABF16) {
-                uint4 v;
-                __builtin_memcpy(&v, __builtin_assume_aligned(Ah + aoff[p] + col, 4), 16);
-                st.ab[p] = ka ? v : make_uint4(0, 0, 0, 0);
-            } else {
-                float4 v;
-                __builtin_memcpy(&v, __builtin_assume_aligned(Af + aoff[p] + col, 4), 16);
-                st.a[p] = ka ? v : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            if (ABF16)
+                __builtin_memcpy(&st.ab[p], __builtin_assume_aligned(Ah + aoff[p] + col, 4), 16);
+            else
+                __builtin_memcpy(&st.a[p], __builtin_assume_aligned(Af + aoff[p] + col, 4), 16);
         }
     };
-    auto load_w = [&](int step, Stage<BK, ABF16>& st) {
-        const int kb = BK == 64 ? 2 * step + lh : step;
-        const bool kw = kb < nb;
-        const unsigned char* blk = Wb + woff + (unsigned)(kw ? kb : 0) * 36u;
-        float sc;
-        __builtin_memcpy(&sc, __builtin_assume_aligned(blk, 4), 4);
-        if (BK == 64) {
-            __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4, 4), 16);
-            __builtin_memcpy(&st.q[BK / 32 - 1], __builtin_assume_aligned(blk + 20, 4), 16);
-        } else {
-            __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4 + 16 * lh, 4), 16);
-        }
-        st.s = kw ? sc : 0.0f;
+    auto load_w = [&](const unsigned char* blk, Stage<ABF16>& st) {
+        __builtin_memcpy(&st.s, __builtin_assume_aligned(blk, 4), 4);
+        __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4, 4), 16);
+        __builtin_memcpy(&st.q[1], __builtin_assume_aligned(blk + 20, 4), 16);
     };
-    auto load = [&](int step, Stage<BK, ABF16>& st) {
-        /* column BK*step + EPC*ac lies in Q8 block (BK*step + EPC*ac) / 32 */
-        const bool ka = (BK * step + EPC * ac) / 32 < nb;
-        const unsigned int col = ka ? (unsigned)(step * BK) : 0u;
-#pragma unroll
-        for (int p = 0; p < NPASS; p++) {
-            if (ABF16) {
-                uint4 v;
-                __builtin_memcpy(&v, __builtin_assume_aligned(Ah + aoff[p] + col, 4), 16);
-                st.ab[p] = ka ? v : make_uint4(0, 0, 0, 0);
-            } else {
-                float4 v;
-                __builtin_memcpy(&v, __builtin_assume_aligned(Af + aoff[p] + col, 4), 16);
-                st.a[p] = ka ? v : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-        }
-        const int kb = BK == 64 ? 2 * step + lh : step; /* this thread's Q8 block */
-        const bool kw = kb < nb;
-        const unsigned char* blk = Wb + woff + (unsigned)(kw ? kb : 0) * 36u;
-        float sc;
-        __builtin_memcpy(&sc, __builtin_assume_aligned(blk, 4), 4);
-        if (BK == 64) {
-            __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4, 4), 16);
-            __builtin_memcpy(&st.q[BK / 32 - 1], __builtin_assume_aligned(blk + 20, 4), 16);
-        } else {
-            __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4 + 16 * lh, 4), 16);
-        }
-        st.s = kw ? sc : 0.0f; /* a zero scale turns the (finite) q into zeros */
+    auto load = [&](int step, Stage<ABF16>& st) {
+        load_a((unsigned)step * GEMM_BK, st);
+        load_w(Wb + woff + (unsigned)step * 72u, st);
     };
-    auto store_aw = [&](int buf, const Stage<BK, ABF16>& sa, const Stage<BK, ABF16>& sw) {
+    /* zero_a: this thread's A chunk lies past K (half step only); the W
+     * block past K arrives with scale 0, which zeroes its (finite) q. */
+    auto store = [&](int buf, const Stage<ABF16>& st, bool zero_a) {
         unsigned short* As = lds + buf * 2 * SLAB;
         unsigned short* Bs = As + SLAB;
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
             if (ABF16) {
-                *(uint4*)&As[(ar + RPP * p) * LDK + 8 * ac] = sa.ab[p];
+                *(uint4*)&As[(ar + RPP * p) * LDK + 8 * ac] = zero_a ? make_uint4(0, 0, 0, 0) : st.ab[p];
             } else {
-                uint2 v;
-                v.x = pk_bf16(sa.a[p].x, sa.a[p].y);
-                v.y = pk_bf16(sa.a[p].z, sa.a[p].w);
-                *(uint2*)&As[(ar + RPP * p) * LDK + 4 * ac] = v;
+                const float4 v = zero_a ? make_float4(0.f, 0.f, 0.f, 0.f) : st.a[p];
+                uint2 u;
+                u.x = pk_bf16(v.x, v.y);
+                u.y = pk_bf16(v.z, v.w);
+                *(uint2*)&As[(ar + RPP * p) * LDK + 4 * ac] = u;
             }
         }
-        uint4* bp = (uint4*)&Bs[lr * LDK + (BK / 2) * lh];
+        uint4* bp = (uint4*)&Bs[lr * LDK + 32 * lh];
 #pragma unroll
-        for (int i = 0; i < BK / 32; i++) {
-            bp[2 * i] = dq8(sw.q[i], 0, sw.s);
-            bp[2 * i + 1] = dq8(sw.q[i], 1, sw.s);
-        }
-    };
-    auto store = [&](int buf, const Stage<BK, ABF16>& st) {
-        unsigned short* As = lds + buf * 2 * SLAB;
-        unsigned short* Bs = As + SLAB;
-#pragma unroll
-        for (int p = 0; p < NPASS; p++) {
-            if (ABF16) {
-                *(uint4*)&As[(ar + RPP * p) * LDK + 8 * ac] = st.ab[p];
-            } else {
-                uint2 v;
-                v.x = pk_bf16(st.a[p].x, st.a[p].y);
-                v.y = pk_bf16(st.a[p].z, st.a[p].w);
-                *(uint2*)&As[(ar + RPP * p) * LDK + 4 * ac] = v;
-            }
-        }
-        uint4* bp = (uint4*)&Bs[lr * LDK + (BK / 2) * lh];
-#pragma unroll
-        for (int i = 0; i < BK / 32; i++) {
+        for (int i = 0; i < 2; i++) {
             bp[2 * i] = dq8(st.q[i], 0, st.s);
             bp[2 * i + 1] = dq8(st.q[i], 1, st.s);
         }
@@ -232,7 +168,7 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
         const unsigned short* As = lds + buf * 2 * SLAB;
         const unsigned short* Bs = As + SLAB;
 #pragma unroll
-        for (int ks = 0; ks < BK; ks += 32) {
+        for (int ks = 0; ks < GEMM_BK; ks += 32) {
             bf16x8 fa[4], fb[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) fa[i] = *(const bf16x8*)&As[(wm + 16 * i + (lane & 15)) * LDK + ks + kq];
@@ -246,84 +182,79 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
         }
     };
 
-    if (!DEPTH2 && !DEEPW) {
-        Stage<BK, ABF16> s0;
+    if (nfull > 0) {
+        Stage<ABF16> s0, s1;
         load(0, s0);
-        store(0, s0);
-        __syncthreads();
-        for (int step = 0; step < nsteps; step++) {
-            const int cur = step & 1;
-            if (step + 1 < nsteps) load(step + 1, s0);
-            mfma_step(cur);
-            if (step + 1 < nsteps) store(cur ^ 1, s0);
-            __syncthreads();
-        }
-    } else if (DEEPW) {
-        /* A two steps ahead (stages a0, a1), W four steps ahead (w0..w3).
-         * Step s: issue A(s+2) into a[s%2] and W(s+4) into w[s%4], run the
-         * MFMAs of step s, store A(s+1), W(s+1) into the other LDS buffer.
-         * Unrolled by four so that every stage is named statically. */
-        Stage<BK, ABF16> a0, a1, w0, w1, w2, w3;
-        load_a(0, a0);
-        load_w(0, w0);
-        if (nsteps > 1) { load_a(1, a1); load_w(1, w1); }
-        if (nsteps > 2) load_w(2, w2);
-        if (nsteps > 3) load_w(3, w3);
-        store_aw(0, a0, w0);
-        __syncthreads();
-#define GM_STEP(S, AC, AN, WC, WN)                                  \
-        if ((S) < nsteps) {                                         \
-            if ((S) + 2 < nsteps) load_a((S) + 2, AC);              \
-            if ((S) + 4 < nsteps) load_w((S) + 4, WC);              \
-            mfma_step((S) & 1);                                     \
-            if ((S) + 1 < nsteps) store_aw(((S) + 1) & 1, AN, WN);  \
-            __syncthreads();                                        \
-        }
-        for (int st4 = 0; st4 < nsteps; st4 += 4) {
-            GM_STEP(st4 + 0, a0, a1, w0, w1)
-            GM_STEP(st4 + 1, a1, a0, w1, w2)
-            GM_STEP(st4 + 2, a0, a1, w2, w3)
-            GM_STEP(st4 + 3, a1, a0, w3, w0)
-        }
-#undef GM_STEP
-    } else {
-        Stage<BK, ABF16> s0, s1;
-        load(0, s0);
-        if (nsteps > 1) load(1, s1);
-        store(0, s0);
+        load(min(1, nfull - 1), s1);
+        store(0, s0, false);
         __syncthreads();
         int step = 0;
-        /* steps two at a time so that the register stages are named statically */
-        for (; step + 2 <= nsteps; step += 2) {
-            if (step + 2 < nsteps) load(step + 2, s0); /* s0 is free: step's data is in LDS buffer 0 */
+        /* two steps per iteration so that the register stages are named statically */
+        for (; step + 2 <= nfull; step += 2) {
+            load(min(step + 2, nfull - 1), s0); /* s0 is free: step's data is in LDS buffer 0 */
+            __builtin_amdgcn_sched_barrier(0);  /* keep the loads ahead of the MFMAs */
             mfma_step(0);
-            store(1, s1);
+            __builtin_amdgcn_sched_barrier(0);
+            store(1, s1, false);
             __syncthreads();
-            if (step + 3 < nsteps) load(step + 3, s1);
+            load(min(step + 3, nfull - 1), s1);
+            __builtin_amdgcn_sched_barrier(0);
             mfma_step(1);
-            if (step + 2 < nsteps) store(0, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            /* unconditional, so that the loads of s0 cannot be sunk next to
+             * it; past the end it rewrites buffer 0, which only the half
+             * step reuses, after the barrier */
+            store(0, s0, false);
             __syncthreads();
         }
-        if (step < nsteps) mfma_step(0); /* odd step count: the last step sits in buffer 0 */
+        if (step < nfull) mfma_step(0); /* odd step count: the last step sits in buffer 0 */
+    }
+    if (nb & 1) {
+        /* Half step: block nb-1 = 2*nfull.  Buffer (nfull & 1) is free: its
+         * last reader was followed by a barrier. */
+        Stage<ABF16> st;
+        const int buf = nfull & 1;
+        const bool past_a = EPC * ac >= 32; /* this thread's A chunk lies past K */
+        load_a(past_a ? 0u : (unsigned)nfull * GEMM_BK, st);
+        /* block 2*nfull + 1 (lh = 1) would lie past the row: read block nb-1
+         * again and give it scale 0 */
+        load_w(Wb + woff + (unsigned)nfull * 72u - (unsigned)lh * 36u, st);
+        if (lh) st.s = 0.0f;
+        store(buf, st, past_a);
+        __syncthreads();
+        mfma_step(buf);
     }
 
-    /* D layout of a 16x16 MFMA tile: lane holds rows 4*(lane/16)+v, column lane%16 */
+    /* Epilogue, 16x16 D layout: lane holds rows 4*(lane/16)+v, column
+     * lane%16.  Interior tiles store without bounds checks from one base
+     * with 32-bit offsets (each wave instruction writes 4 rows x 64 bytes);
+     * staging the tile through LDS for whole-row stores measured slower. */
+    float* Ct = Cm + (size_t)(m0 + wm + 4 * (lane >> 4)) * ldc + n0 + wn + (lane & 15);
+    if (m0 + BM <= M && n0 + BN <= N) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int col = n0 + wn + 16 * j + (lane & 15);
-            if (col >= N) continue;
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int row = m0 + wm + 16 * i + (lane >> 4) * 4 + v;
-                if (row < M) Cm[(size_t)row * ldc + col] = acc[i][j][v];
+                for (int v = 0; v < 4; v++) Ct[(unsigned)(16 * i + v) * (unsigned)ldc + 16 * j] = acc[i][j][v];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int col = n0 + wn + 16 * j + (lane & 15);
+                if (col >= N) continue;
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int row = m0 + wm + 16 * i + 4 * (lane >> 4) + v;
+                    if (row < M) Cm[(size_t)row * ldc + col] = acc[i][j][v];
+                }
             }
-        }
+    }
 }
 
-__global__ __launch_bounds__(NTH) void k_q8_gemm(GmGroup g) {
-    __shared__ __attribute__((aligned(16))) unsigned short lds[gemm_lds_elems<GEMM_BK>()];
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q8_gemm(GmGroup g) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
     int tile = blockIdx.x;
     int pi = 0;
     while (pi + 1 < g.nprob && tile >= g.p[pi].tiles) {
@@ -332,25 +263,22 @@ __global__ __launch_bounds__(NTH) void k_q8_gemm(GmGroup g) {
     }
     const GmProb& p = g.p[pi];
     const int tiles_n = (p.N + BN - 1) / BN;
-    gemm_tile<GEMM_BK, TWO_STAGE, false>(p.A, p.W, p.C, p.M, p.N, p.K, p.lda, p.ldc, tile / tiles_n, tile % tiles_n,
-                                         lds);
+    gemm_tile<false>(p.A, p.W, p.C, p.M, p.N, p.K, p.lda, p.ldc, tile / tiles_n, tile % tiles_n, lds);
 }
 
 /* Activations in fp32 (cast to bf16 while staging) or already in bf16. */
 template <bool ABF16>
-__global__ __launch_bounds__(NTH) void k_q8_gemm_multi(const void* __restrict__ A, const unsigned char* __restrict__ W,
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q8_gemm_multi(const void* __restrict__ A, const unsigned char* __restrict__ W,
                                                        float* __restrict__ C, const GmDesc* __restrict__ desc,
                                                        const unsigned int* __restrict__ tile_map) {
-    constexpr int BKM = ABF16 ? GEMM_BK_BF16 : GEMM_BK;
-    __shared__ __attribute__((aligned(16))) unsigned short lds[gemm_lds_elems<BKM>()];
+    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
     const unsigned int tm_ = tile_map[blockIdx.x];
     if (tm_ == GM_IDLE_TILE) return;
     const GmDesc d = desc[tm_ >> 16];
     const int tile = (int)(tm_ & 0xffffu);
     const int tiles_n = (d.N + BN - 1) / BN;
     const void* Ad = ABF16 ? (const void*)((const unsigned short*)A + d.a_off) : (const void*)((const float*)A + d.a_off);
-    gemm_tile<BKM, ABF16 ? TWO_STAGE_BF16 : TWO_STAGE, ABF16, ABF16 && DEEP_W_BF16>(
-        Ad, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc, tile / tiles_n, tile % tiles_n, lds);
+    gemm_tile<ABF16>(Ad, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc, tile / tiles_n, tile % tiles_n, lds);
 }
 
 /* fp32 -> bf16 (round to nearest even), 8 elements per lane */

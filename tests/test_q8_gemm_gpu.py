@@ -27,6 +27,8 @@ def normwise(y, r):
 @pytest.mark.parametrize("M,K,N", [
     (512, 576, 576), (512, 576, 192), (512, 576, 1536), (512, 1536, 576),
     (16, 576, 576), (100, 96, 70), (513, 64, 65), (64, 32, 64),
+    # odd block counts: a half step after an even (K=160) and an odd (K=224) number of full steps
+    (40, 160, 96), (33, 224, 130),
 ])
 def test_gemm_vs_oracle(be, M, K, N):
     w = po.quantize_q8(bmhip.synth_normal(bmhip.synth_seed(4, 0, N, K), 0.02, N * K))
