@@ -253,7 +253,7 @@ def gemm_leg(steps: int, warmup: int):
     }
 
 
-def e2e_decode(cpu_steps: int, cpu_threads: int):
+def e2e_decode(cpu_steps: int, cpu_threads: int, graph: bool = True):
     """Config 5: SmolLM2-135M Q8 greedy decode, 128-token prompt + 256
     generated tokens (383 decode steps, prompt tokens stepped one by one as
     the reference's bm_run_tokens does), batch 1 and batch 32, driven on the
@@ -266,6 +266,7 @@ def e2e_decode(cpu_steps: int, cpu_threads: int):
     for B in (1, 32):
         prompts = bmhip.synth_uniform_int(seed, 0, dims["V"], B * n_prompt).reshape(B, n_prompt)
         eng = bmhip.Engine(dims, max_seq_len=n_prompt + n_gen, seed=seed, batch=B)
+        eng.set_graph(graph)
         eng.generate(prompts, steps)  # warm-up; captures the step graph
         t0 = time.perf_counter()
         toks = eng.generate(prompts, steps)
@@ -314,6 +315,8 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
+    ap.add_argument("--e2e-graph", type=int, default=1,
+                    help="0: decode steps launched eagerly instead of replaying the captured graph (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -337,7 +340,7 @@ def main():
         if args.gemm:
             out["prefill_gemm"] = gemm_leg(max(args.steps // 10, 10), 3)
         if args.e2e:
-            out["e2e_decode"] = e2e_decode(0, args.cpu_threads)
+            out["e2e_decode"] = e2e_decode(0, args.cpu_threads, bool(args.e2e_graph))
         print(json.dumps(out), flush=True)
         return
     be = bmhip.Backend()
@@ -380,7 +383,8 @@ def main():
     be.close()
 
     gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
-    e2e = e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads) if args.e2e else None
+    e2e = (e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads, bool(args.e2e_graph))
+           if args.e2e else None)
 
     mid, D, H, NH, NKV, HD, L = MODELS[args.model]
     line = {
