@@ -39,6 +39,7 @@ namespace {
 using namespace bmk;
 
 constexpr int NT = 256;     /* threads per workgroup (4 waves) */
+typedef float bmv_f32x4 __attribute__((ext_vector_type(4))); /* fp32 MFMA accumulator tile */
 constexpr int ATT_CH = 2048; /* keys per softmax chunk held in LDS */
 constexpr int HEAD_U = 8;   /* rows in flight per lane in the LM head (bandwidth-bound: 113 MB fp32 at 135M) */
 
@@ -273,6 +274,37 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
  * With st != NULL the workgroup's best (logit, index) goes into st->key[b]
  * by atomicMax, and the last workgroup to finish turns the keys into
  * tokens, emits them and advances the position. */
+/* Last workgroup of a head launch (every workgroup calls this after its
+ * atomicMax): emit the step's tokens and advance the position. */
+__device__ void head_finish(const DecHead& a, int& last_wg) {
+    const int t = threadIdx.x;
+    if (t == 0) {
+        __threadfence();
+        const unsigned int prev = atomicAdd(&a.st->done, 1u);
+        last_wg = (prev == (unsigned int)a.tiles - 1u);
+    }
+    __syncthreads();
+    if (!last_wg) return;
+    __threadfence();
+    DecState* st = a.st;
+    const int pos = st->pos;
+    const bool emit = !st->host_mode && pos >= st->n_prompt - 1;
+    for (int b = t; b < a.B; b += blockDim.x) {
+        const unsigned long long k = atomicAdd(&st->key[b], 0ull);
+        const int tok = argmax_key_index(k);
+        st->last_token[b] = tok;
+        if (emit) a.out_tokens[(size_t)st->n_out * a.B + b] = tok;
+        st->key[b] = 0ull;
+    }
+    __syncthreads();
+    if (t == 0) {
+        if (emit) st->n_out = st->n_out + 1;
+        st->done = 0u;
+        st->pos = pos + 1;
+        __threadfence();
+    }
+}
+
 template <bool Q8>
 __device__ __forceinline__ int head_lanes(int D) { return Q8 ? D / 32 : D / 16; }
 
@@ -377,32 +409,116 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
     }
 
     if (!a.st) return;
-    /* last workgroup: emit the step's tokens and advance the position */
-    if (t == 0) {
-        __threadfence();
-        const unsigned int prev = atomicAdd(&a.st->done, 1u);
-        last_wg = (prev == (unsigned int)a.tiles - 1u);
+    head_finish(a, last_wg);
+}
+
+/* Batched LM head (B >= 2) on fp32 MFMA: a workgroup scores 64 vocabulary
+ * rows (16 per wave, each wave over the whole of D) for every batch row;
+ * same operand feed as k_dec_bmv (lane: 8 consecutive k of its own row per
+ * 32 columns).  Final RMSNorm applied as inv_rms(x[b]) * sum_k x g w.  Row
+ * maxima: across the 16 columns of a wave by shuffles, across waves through
+ * LDS, then one atomicMax per batch row; the last workgroup emits the
+ * tokens (head_finish). */
+template <int NBT, bool Q8>
+__global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
+    __shared__ unsigned long long shk[4][16 * NBT];
+    __shared__ int last_wg;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int D = a.D, nkb = D / 32;
+    const long r = (long)blockIdx.x * 64 + wave * 16 + c;
+    const long rc = r < a.V ? r : (long)a.V - 1;
+    const float* xr[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) xr[bt] = a.x + (size_t)min(16 * bt + c, a.B - 1) * D + 8 * g;
+    const float* nwp = a.norm_w + 8 * g;
+    bmv_f32x4 acc[NBT];
+    float ss[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) {
+        acc[bt] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
+        ss[bt] = 0.f;
     }
+    for (int kb = 0; kb < nkb; kb++) {
+        float wv[8], s = 1.0f;
+        if (Q8) {
+            const unsigned char* blk = a.wq + ((size_t)rc * nkb + kb) * 36;
+            unsigned int q0, q1;
+            __builtin_memcpy(&s, __builtin_assume_aligned(blk, 4), 4);
+            __builtin_memcpy(&q0, __builtin_assume_aligned(blk + 4 + 8 * g, 4), 4);
+            __builtin_memcpy(&q1, __builtin_assume_aligned(blk + 8 + 8 * g, 4), 4);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                wv[i] = q8_byte(q0, i);
+                wv[4 + i] = q8_byte(q1, i);
+            }
+        } else {
+            float4 w0, w1;
+            const float* wp = a.w + (size_t)rc * D + 32 * kb + 8 * g;
+            __builtin_memcpy(&w0, __builtin_assume_aligned(wp, 4), 16);
+            __builtin_memcpy(&w1, __builtin_assume_aligned(wp + 4, 4), 16);
+            wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+            wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+        }
+        float4 g0, g1;
+        __builtin_memcpy(&g0, __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
+        __builtin_memcpy(&g1, __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
+        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+        for (int bt = 0; bt < NBT; bt++) {
+            float4 x0, x1;
+            __builtin_memcpy(&x0, __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
+            __builtin_memcpy(&x1, __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
+            float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                ss[bt] = fmaf(xv[i], xv[i], ss[bt]);
+                xv[i] *= gv[i];
+            }
+            if (Q8) {
+                bmv_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], d, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[bt][v] = fmaf(s, d[v], acc[bt][v]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[bt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[bt], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) {
+        float sq = ss[bt];
+        sq += __shfl_xor(sq, 16);
+        sq += __shfl_xor(sq, 32); /* every lane: sum of squares of batch row 16*bt + c */
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int b = 16 * bt + 4 * g + v;
+            const float inv = 1.0f / sqrtf(__shfl(sq, 4 * g + v) / (float)D + a.eps);
+            const float val = acc[bt][v] * inv;
+            unsigned long long key = 0ull;
+            if (r < a.V && b < a.B) {
+                a.logits[(size_t)b * a.V + r] = val;
+                key = argmax_key(val, (int)r);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const unsigned long long o = __shfl_xor(key, off, 64);
+                key = o > key ? o : key;
+            }
+            if (c == 0) shk[wave][b] = key;
+        }
+    }
+    if (!a.st) return;
     __syncthreads();
-    if (!last_wg) return;
-    __threadfence();
-    DecState* st = a.st;
-    const int pos = st->pos;
-    const bool emit = !st->host_mode && pos >= st->n_prompt - 1;
     for (int b = t; b < a.B; b += NT) {
-        const unsigned long long k = atomicAdd(&st->key[b], 0ull);
-        const int tok = argmax_key_index(k);
-        st->last_token[b] = tok;
-        if (emit) a.out_tokens[(size_t)st->n_out * a.B + b] = tok;
-        st->key[b] = 0ull;
+        unsigned long long best = shk[0][b];
+#pragma unroll
+        for (int w = 1; w < 4; w++) best = shk[w][b] > best ? shk[w][b] : best;
+        atomicMax(&a.st->key[b], best);
     }
-    __syncthreads();
-    if (t == 0) {
-        if (emit) st->n_out = st->n_out + 1;
-        st->done = 0u;
-        st->pos = pos + 1;
-        __threadfence();
-    }
+    head_finish(a, last_wg);
 }
 
 /* argmax_f32: first index of the maximum of v[0..n) (reference tools/run.c:56-60). */
@@ -565,6 +681,136 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
             }
         }
         __syncthreads();
+    }
+}
+
+/* Batched fused Q8 matvec (decode with B >= 2) on fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32: D[16][16] += A[16][4] x B[4][16]).
+ *
+ * A workgroup owns 16 output rows of one matrix (a SwiGLU tile: rows
+ * j0..j0+7 of gate and of up) for every batch row, 16 batch rows per MFMA
+ * tile (NBT tiles).  Its 4 waves take the K blocks round-robin; the partial
+ * tiles are summed through LDS in wave order (the same bits at every run).
+ * Per K block, lane l (column c = l%16, k group g = l/16) feeds 8 MFMAs with
+ * A = x[b0 + c][32kb + 8g + t] (times the norm gain) and B = q[n0 + c][32kb
+ * + 8g + t] (t = 0..7): 8 int8 weights of its own row, converted exactly to
+ * fp32; the block result D is scaled by the row's block scale, as the
+ * reference scales each block's dot product (forward.metal:575-623).
+ * RMSNorm: y[b] = inv_rms(x[b]) * sum_k x[b][k] g[k] w[n][k]; the sum of
+ * squares rides along with the x loads (each x element is loaded by exactly
+ * one lane per batch tile).  D layout: lane l holds rows 4*(l/16)+v (batch
+ * rows) of column l%16 (output row). */
+constexpr int BMV_NT = 256;
+
+template <int NBT>
+__global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
+    __shared__ bmv_f32x4 part[4][NBT][64];
+    __shared__ float ssq[4][16 * NBT];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int c = lane & 15, g = lane >> 4;
+    int mi = 0;
+    while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
+    const int tile = (int)blockIdx.x - a.tile0[mi];
+    const bool glu = a.glu != 0;
+    const int OC = a.OC[mi];
+    const int nb = a.C / 32;
+    const size_t row_bytes = (size_t)nb * 36;
+    /* this lane's weight row (clamped: rows past OC feed outputs never stored) */
+    const int row = glu ? tile * 8 + (c & 7) : tile * 16 + c;
+    const unsigned char* wrow = (glu ? a.w[c >> 3] : a.w[mi]) + (size_t)min(row, OC - 1) * row_bytes + 4 + 8 * g;
+    const float* xr[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) xr[bt] = a.x + (size_t)min(16 * bt + c, a.B - 1) * a.ldx + 8 * g;
+    const float* nwp = a.norm_w ? a.norm_w + 8 * g : nullptr;
+
+    bmv_f32x4 acc[NBT];
+    float ss[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) {
+        acc[bt] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
+        ss[bt] = 0.f;
+    }
+    for (int kb = wave; kb < nb; kb += 4) {
+        const unsigned char* blk = wrow + (size_t)kb * 36;
+        float s;
+        unsigned int q0, q1;
+        __builtin_memcpy(&s, __builtin_assume_aligned(blk - 4 - 8 * g, 4), 4);
+        __builtin_memcpy(&q0, __builtin_assume_aligned(blk, 4), 4);
+        __builtin_memcpy(&q1, __builtin_assume_aligned(blk + 4, 4), 4);
+        float gv[8];
+        if (nwp) {
+            float4 g0, g1;
+            __builtin_memcpy(&g0, __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
+            __builtin_memcpy(&g1, __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
+            gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
+            gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+        }
+        float xv[NBT][8];
+#pragma unroll
+        for (int bt = 0; bt < NBT; bt++) {
+            float4 x0, x1;
+            __builtin_memcpy(&x0, __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
+            __builtin_memcpy(&x1, __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
+            xv[bt][0] = x0.x; xv[bt][1] = x0.y; xv[bt][2] = x0.z; xv[bt][3] = x0.w;
+            xv[bt][4] = x1.x; xv[bt][5] = x1.y; xv[bt][6] = x1.z; xv[bt][7] = x1.w;
+        }
+        float wv[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            wv[i] = q8_byte(q0, i);
+            wv[4 + i] = q8_byte(q1, i);
+        }
+#pragma unroll
+        for (int bt = 0; bt < NBT; bt++) {
+            if (nwp) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    ss[bt] = fmaf(xv[bt][i], xv[bt][i], ss[bt]);
+                    xv[bt][i] *= gv[i];
+                }
+            }
+            bmv_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[bt][i], wv[i], d, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[bt][v] = fmaf(s, d[v], acc[bt][v]);
+        }
+    }
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) {
+        part[wave][bt][lane] = acc[bt];
+        if (nwp) {
+            float v = ss[bt];
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            if (g == 0) ssq[wave][16 * bt + c] = v;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int bt = 0; bt < NBT; bt++) {
+        bmv_f32x4 y = part[0][bt][lane];
+#pragma unroll
+        for (int w = 1; w < 4; w++) y += part[w][bt][lane];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int b = 16 * bt + 4 * g + v;
+            float val = y[v];
+            if (nwp) {
+                const int bi = 4 * g + v + 16 * bt;
+                const float sq = ((ssq[0][bi] + ssq[1][bi]) + ssq[2][bi]) + ssq[3][bi];
+                val *= 1.0f / sqrtf(sq / (float)a.C + a.eps);
+            }
+            if (glu) {
+                const float up = __shfl_xor(val, 8);
+                const int j = tile * 8 + c;
+                if (c < 8 && j < OC && b < a.B) a.y[0][(size_t)b * OC + j] = silu_mul(val, up);
+            } else if (row < OC && b < a.B) {
+                float* yp = a.y[mi] + (size_t)b * OC + row;
+                *yp = a.residual ? *yp + val : val;
+            }
+        }
     }
 }
 
@@ -947,8 +1193,24 @@ extern "C" int dec_launch_embed(const DecEmbed* a, hipStream_t s) {
     return 0;
 }
 
+/* Workgroups of one matrix in the batched (B >= 2) matvec: 16 output rows,
+ * or 8 (gate, up) row pairs. */
+static int dec_bmv_tiles(int OC, int glu) { return glu ? (OC + 7) / 8 : (OC + 15) / 16; }
+
 extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
     DecMv a = *a_in;
+    if (a.B >= 2) {
+        if (a.B > DEC_MAX_B || a.C % 32 || (a.ldx & 3) || ((uintptr_t)a.x & 15)) return -1;
+        a.tile0[0] = 0;
+        for (int i = 0; i < a.nmat; i++) a.tile0[i + 1] = a.tile0[i] + dec_bmv_tiles(a.OC[i], a.glu);
+        const dim3 grid(a.tile0[a.nmat]);
+        if (a.B <= 16) hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
+        else if (a.B <= 32) hipLaunchKernelGGL(k_dec_bmv<2>, grid, dim3(BMV_NT), 0, s, a);
+        else if (a.B <= 48) hipLaunchKernelGGL(k_dec_bmv<3>, grid, dim3(BMV_NT), 0, s, a);
+        else hipLaunchKernelGGL(k_dec_bmv<4>, grid, dim3(BMV_NT), 0, s, a);
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
     int wt;
     dec_mv_shape(a.C, a.glu, &wt, &a.slots);
     if (a.slots == 0) return -1;
@@ -968,7 +1230,27 @@ extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
     return 0;
 }
 
-extern "C" int dec_launch_head(const DecHead* a, hipStream_t s) {
+extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
+    if (a_in->B >= 2) {
+        DecHead a = *a_in;
+        if (a.B > DEC_MAX_B || a.D % 32) return -1;
+        a.tiles = (a.V + 63) / 64;
+        const dim3 grid(a.tiles);
+        const bool q8 = a.wq != nullptr;
+#define HEAD_B(NBT)                                                                \
+        do {                                                                       \
+            if (q8) hipLaunchKernelGGL((k_head_b<NBT, true>), grid, dim3(NT), 0, s, a); \
+            else hipLaunchKernelGGL((k_head_b<NBT, false>), grid, dim3(NT), 0, s, a);   \
+        } while (0)
+        if (a.B <= 16) HEAD_B(1);
+        else if (a.B <= 32) HEAD_B(2);
+        else if (a.B <= 48) HEAD_B(3);
+        else HEAD_B(4);
+#undef HEAD_B
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
+    const DecHead* a = a_in;
     if (a->wq)
         hipLaunchKernelGGL(k_head<true>, dim3(a->tiles), dim3(NT), 0, s, *a);
     else

@@ -27,6 +27,9 @@ __device__ __forceinline__ Blk load_block(const unsigned char* p) {
     return b;
 }
 
+/* int8 k (0..3) of a packed dword, exactly as fp32 */
+__device__ __forceinline__ float q8_byte(unsigned int w, int k) { return (float)(signed char)((w >> (8 * k)) & 0xffu); }
+
 __device__ __forceinline__ float dot4(unsigned int w, const float* x) {
     float a = x[0] * (float)(signed char)(w & 0xffu);
     a = fmaf(x[1], (float)(signed char)((w >> 8) & 0xffu), a);
