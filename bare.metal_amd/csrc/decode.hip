@@ -700,12 +700,13 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
  * squares rides along with the x loads (each x element is loaded by exactly
  * one lane per batch tile).  D layout: lane l holds rows 4*(l/16)+v (batch
  * rows) of column l%16 (output row). */
-constexpr int BMV_NT = 256;
+constexpr int BMV_WAVES = 16;             /* waves per workgroup, splitting the K blocks */
+constexpr int BMV_NT = 64 * BMV_WAVES;
 
 template <int NBT>
 __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
-    __shared__ bmv_f32x4 part[4][NBT][64];
-    __shared__ float ssq[4][16 * NBT];
+    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
+    __shared__ float ssq[BMV_WAVES][16 * NBT];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int c = lane & 15, g = lane >> 4;
     int mi = 0;
@@ -730,7 +731,7 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
         acc[bt] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
         ss[bt] = 0.f;
     }
-    for (int kb = wave; kb < nb; kb += 4) {
+    for (int kb = wave; kb < nb; kb += BMV_WAVES) {
         const unsigned char* blk = wrow + (size_t)kb * 36;
         float s;
         unsigned int q0, q1;
@@ -792,14 +793,16 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
     for (int bt = 0; bt < NBT; bt++) {
         bmv_f32x4 y = part[0][bt][lane];
 #pragma unroll
-        for (int w = 1; w < 4; w++) y += part[w][bt][lane];
+        for (int w = 1; w < BMV_WAVES; w++) y += part[w][bt][lane];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int b = 16 * bt + 4 * g + v;
             float val = y[v];
             if (nwp) {
                 const int bi = 4 * g + v + 16 * bt;
-                const float sq = ((ssq[0][bi] + ssq[1][bi]) + ssq[2][bi]) + ssq[3][bi];
+                float sq = ssq[0][bi];
+#pragma unroll
+                for (int w = 1; w < BMV_WAVES; w++) sq += ssq[w][bi];
                 val *= 1.0f / sqrtf(sq / (float)a.C + a.eps);
             }
             if (glu) {
