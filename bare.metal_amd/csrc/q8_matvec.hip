@@ -29,7 +29,10 @@
  */
 #include "bmk.h"
 #include "q8_matvec.h"
+#include "decode_state.h"
 #include "q8_common.h"
+
+#include <string.h>
 
 namespace {
 
@@ -263,6 +266,8 @@ extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
                            n_tiles, a->stream);
 }
 
+extern "C" int dec_launch_mv(const DecMv* a, hipStream_t s);
+
 /* matmul_forward_q8_vec / matmul_forward_q8 with BT below the GEMM cut-over:
  * buffers {inp f32 [BT][C], weight q8 [OC][C/32], bias f32 [OC], out f32 [BT][OC],
  * params int {BT, C, OC, has_bias}}.  The Metal grid (OC*128 or OC rounded to
@@ -278,6 +283,22 @@ extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
     BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
     BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0,
                 "q8 matvec: misaligned buffer offset");
+    if (BT >= 2 && BT <= DEC_MAX_B && !has_bias && ((uintptr_t)a->dev[0] & 15) == 0) {
+        /* several rows: the batched fp32-MFMA matvec (decode.hip) reads each
+         * weight once for all rows */
+        DecMv m;
+        memset(&m, 0, sizeof m);
+        m.x = (const float*)a->dev[0];
+        m.C = C;
+        m.B = BT;
+        m.ldx = C;
+        m.nmat = 1;
+        m.w[0] = (const unsigned char*)a->dev[1];
+        m.y[0] = (float*)a->dev[3];
+        m.OC[0] = OC;
+        BMK_REQUIRE(dec_launch_mv(&m, a->stream) == 0, "q8 matvec: batched launch failed (BT=%d C=%d OC=%d)", BT, C, OC);
+        return 0;
+    }
     for (int bt = 0; bt < BT; bt += MV_MAX_PROBS) {
         MvGroup g;
         g.nprob = BT - bt < MV_MAX_PROBS ? BT - bt : MV_MAX_PROBS;
@@ -297,8 +318,9 @@ extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
 }
 
 /* matmul_forward_q8 (reference forward.metal:625-649): BT rows of activations.
- * BT below GEMM_MIN_BT streams the weights through the fp32 matvec once per
- * row; larger BT goes to the bf16-MFMA GEMM (q8_gemm.hip). */
+ * BT below GEMM_MIN_BT stays on fp32 (the batched fp32-MFMA matvec for
+ * 2 <= BT, the matvec for one row); larger BT goes to the bf16-MFMA GEMM
+ * (q8_gemm.hip). */
 #include "q8_gemm.h"
 #define GEMM_MIN_BT 16
 extern "C" int bmk_launch_q8_matmul(const bmk_launch_t* a) {
