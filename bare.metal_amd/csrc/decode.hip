@@ -439,53 +439,62 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
         acc[bt] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
         ss[bt] = 0.f;
     }
-    for (int kb = 0; kb < nkb; kb++) {
-        float wv[8], s = 1.0f;
+    /* one K block of operands; the next block's loads are issued before the
+     * current block's MFMAs */
+    struct Ops {
+        float wv[8], s, gv[8], xv[NBT][8];
+    };
+    auto load = [&](int kb, Ops& o) {
+        o.s = 1.0f;
         if (Q8) {
             const unsigned char* blk = a.wq + ((size_t)rc * nkb + kb) * 36;
             unsigned int q0, q1;
-            __builtin_memcpy(&s, __builtin_assume_aligned(blk, 4), 4);
+            __builtin_memcpy(&o.s, __builtin_assume_aligned(blk, 4), 4);
             __builtin_memcpy(&q0, __builtin_assume_aligned(blk + 4 + 8 * g, 4), 4);
             __builtin_memcpy(&q1, __builtin_assume_aligned(blk + 8 + 8 * g, 4), 4);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                wv[i] = q8_byte(q0, i);
-                wv[4 + i] = q8_byte(q1, i);
+                o.wv[i] = q8_byte(q0, i);
+                o.wv[4 + i] = q8_byte(q1, i);
             }
         } else {
-            float4 w0, w1;
             const float* wp = a.w + (size_t)rc * D + 32 * kb + 8 * g;
-            __builtin_memcpy(&w0, __builtin_assume_aligned(wp, 4), 16);
-            __builtin_memcpy(&w1, __builtin_assume_aligned(wp + 4, 4), 16);
-            wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
-            wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+            __builtin_memcpy(&o.wv[0], __builtin_assume_aligned(wp, 4), 16);
+            __builtin_memcpy(&o.wv[4], __builtin_assume_aligned(wp + 4, 4), 16);
         }
-        float4 g0, g1;
-        __builtin_memcpy(&g0, __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
-        __builtin_memcpy(&g1, __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
-        const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        __builtin_memcpy(&o.gv[0], __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
+        __builtin_memcpy(&o.gv[4], __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
 #pragma unroll
         for (int bt = 0; bt < NBT; bt++) {
-            float4 x0, x1;
-            __builtin_memcpy(&x0, __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
-            __builtin_memcpy(&x1, __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
-            float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+            __builtin_memcpy(&o.xv[bt][0], __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
+            __builtin_memcpy(&o.xv[bt][4], __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
+        }
+    };
+    Ops cur, nxt;
+    load(0, cur);
+    for (int kb = 0; kb < nkb; kb++) {
+        load(min(kb + 1, nkb - 1), nxt);
+#pragma unroll
+        for (int bt = 0; bt < NBT; bt++) {
+            float xv[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                ss[bt] = fmaf(xv[i], xv[i], ss[bt]);
-                xv[i] *= gv[i];
+                ss[bt] = fmaf(cur.xv[bt][i], cur.xv[bt][i], ss[bt]);
+                xv[i] = cur.xv[bt][i] * cur.gv[i];
             }
             if (Q8) {
                 bmv_f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 8; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], d, 0, 0, 0);
+                for (int i = 0; i < 8; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], cur.wv[i], d, 0, 0, 0);
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[bt][v] = fmaf(s, d[v], acc[bt][v]);
+                for (int v = 0; v < 4; v++) acc[bt][v] = fmaf(cur.s, d[v], acc[bt][v]);
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; i++) acc[bt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], acc[bt], 0, 0, 0);
+                for (int i = 0; i < 8; i++)
+                    acc[bt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], cur.wv[i], acc[bt], 0, 0, 0);
             }
         }
+        cur = nxt;
     }
 #pragma unroll
     for (int bt = 0; bt < NBT; bt++) {
@@ -548,10 +557,10 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ v, in
 
 /* x[b] = emb[token_b]; token_b from the host, the prompt, or the last argmax. */
 __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
-    __shared__ int tok_s[DEC_MAX_B];
+    __shared__ int tok_s;
     DecState* st = a.st;
-    const int B = st->B, pos = st->pos;
-    for (int b = threadIdx.x; b < B; b += NT) {
+    const int b = blockIdx.x, pos = st->pos;
+    if (threadIdx.x == 0) {
         int tok;
         if (st->host_mode) tok = st->host_token[b];
         else if (pos < st->n_prompt) tok = a.prompt[(size_t)b * st->n_prompt + pos];
@@ -561,14 +570,12 @@ __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
             tok = 0;
         }
         st->token[b] = tok;
-        tok_s[b] = tok;
+        tok_s = tok;
     }
     __syncthreads();
-    for (int b = 0; b < B; b++) {
-        const float* er = a.emb + (size_t)tok_s[b] * a.D;
-        float* xr = a.x + (size_t)b * a.D;
-        for (int j = threadIdx.x; j < a.D; j += NT) xr[j] = er[j];
-    }
+    const float* er = a.emb + (size_t)tok_s * a.D;
+    float* xr = a.x + (size_t)b * a.D;
+    for (int j = threadIdx.x; j < a.D; j += NT) xr[j] = er[j];
 }
 
 /* Fused Q8 matvec phase (see DecMv).  WT threads per workgroup; lane t
@@ -688,8 +695,8 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
  * (v_mfma_f32_16x16x4_f32: D[16][16] += A[16][4] x B[4][16]).
  *
  * A workgroup owns 16 output rows of one matrix (a SwiGLU tile: rows
- * j0..j0+7 of gate and of up) for every batch row, 16 batch rows per MFMA
- * tile (NBT tiles).  Its 4 waves take the K blocks round-robin; the partial
+ * j0..j0+7 of gate and of up) for 16*NBT batch rows (blockIdx.y selects
+ * them), 16 per MFMA tile.  Its waves take the K blocks round-robin; the partial
  * tiles are summed through LDS in wave order (the same bits at every run).
  * Per K block, lane l (column c = l%16, k group g = l/16) feeds 8 MFMAs with
  * A = x[b0 + c][32kb + 8g + t] (times the norm gain) and B = q[n0 + c][32kb
@@ -700,7 +707,7 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
  * squares rides along with the x loads (each x element is loaded by exactly
  * one lane per batch tile).  D layout: lane l holds rows 4*(l/16)+v (batch
  * rows) of column l%16 (output row). */
-constexpr int BMV_WAVES = 16;             /* waves per workgroup, splitting the K blocks */
+constexpr int BMV_WAVES = 8;              /* waves per workgroup, splitting the K blocks */
 constexpr int BMV_NT = 64 * BMV_WAVES;
 
 template <int NBT>
@@ -712,6 +719,7 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
     const int tile = (int)blockIdx.x - a.tile0[mi];
+    const int b0 = 16 * NBT * (int)blockIdx.y; /* first batch row of this workgroup */
     const bool glu = a.glu != 0;
     const int OC = a.OC[mi];
     const int nb = a.C / 32;
@@ -721,7 +729,7 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
     const unsigned char* wrow = (glu ? a.w[c >> 3] : a.w[mi]) + (size_t)min(row, OC - 1) * row_bytes + 4 + 8 * g;
     const float* xr[NBT];
 #pragma unroll
-    for (int bt = 0; bt < NBT; bt++) xr[bt] = a.x + (size_t)min(16 * bt + c, a.B - 1) * a.ldx + 8 * g;
+    for (int bt = 0; bt < NBT; bt++) xr[bt] = a.x + (size_t)min(b0 + 16 * bt + c, a.B - 1) * a.ldx + 8 * g;
     const float* nwp = a.norm_w ? a.norm_w + 8 * g : nullptr;
 
     bmv_f32x4 acc[NBT];
@@ -796,7 +804,7 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
         for (int w = 1; w < BMV_WAVES; w++) y += part[w][bt][lane];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int b = 16 * bt + 4 * g + v;
+            const int b = b0 + 16 * bt + 4 * g + v;
             float val = y[v];
             if (nwp) {
                 const int bi = 4 * g + v + 16 * bt;
@@ -1191,7 +1199,8 @@ extern "C" int dec_mv_tiles(int OC, int C, int glu) {
 extern "C" int dec_head_tiles(int D, int V, int q8) { return head_tiles(D, V, q8 != 0); }
 
 extern "C" int dec_launch_embed(const DecEmbed* a, hipStream_t s) {
-    hipLaunchKernelGGL(k_embed, dim3(1), dim3(NT), 0, s, *a);
+    if (a->B < 1 || a->B > DEC_MAX_B) return -1;
+    hipLaunchKernelGGL(k_embed, dim3(a->B), dim3(NT), 0, s, *a); /* workgroup b: sequence b */
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -1206,11 +1215,10 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
         if (a.B > DEC_MAX_B || a.C % 32 || (a.ldx & 3) || ((uintptr_t)a.x & 15)) return -1;
         a.tile0[0] = 0;
         for (int i = 0; i < a.nmat; i++) a.tile0[i + 1] = a.tile0[i] + dec_bmv_tiles(a.OC[i], a.glu);
-        const dim3 grid(a.tile0[a.nmat]);
-        if (a.B <= 16) hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
-        else if (a.B <= 32) hipLaunchKernelGGL(k_dec_bmv<2>, grid, dim3(BMV_NT), 0, s, a);
-        else if (a.B <= 48) hipLaunchKernelGGL(k_dec_bmv<3>, grid, dim3(BMV_NT), 0, s, a);
-        else hipLaunchKernelGGL(k_dec_bmv<4>, grid, dim3(BMV_NT), 0, s, a);
+        /* one workgroup per (row tile, 16 batch rows): more workgroups than
+         * one per row tile, each weight tile is read from L2 again */
+        const dim3 grid(a.tile0[a.nmat], (a.B + 15) / 16);
+        hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
         BMK_LAUNCH_CHECK();
         return 0;
     }

@@ -101,7 +101,7 @@ typedef struct {
     const int* prompt;   /* [B][n_prompt] (generation mode) */
     float* x;            /* [B][D] */
     DecState* st;
-    int D, V;
+    int D, V, B;         /* B: the session's batch (one workgroup per sequence) */
 } DecEmbed;
 
 #endif

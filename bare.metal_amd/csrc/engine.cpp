@@ -354,6 +354,7 @@ static int enqueue_step(bm_session_t* S) {
     e.st = S->st;
     e.D = D;
     e.V = m->V;
+    e.B = B;
     if (mark(S) || dec_launch_embed(&e, s) || mark(S)) return -1;
     const float eps = 1e-5f; /* reference graph.c:134,175,219 */
     for (int l = 0; l < m->L; l++) {
