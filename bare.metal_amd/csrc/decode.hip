@@ -983,6 +983,172 @@ __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
     }
 }
 
+/* Decode attention of one KV-head group: workgroup (KV head kh, sequence b)
+ * serves all kv_mul query heads of the group, so each cached key and value
+ * row is read once for all of them (GQA).  Its AG_WAVES waves split the
+ * positions 0..pos into contiguous ranges; a wave walks its range in chunks
+ * of 64 keys:
+ *  - scores: lane = key, the key's HD/4 float4 loads issued together (the
+ *    [HD/4][MS] K layout makes a wave's load 1 KB contiguous), one dot
+ *    product per query head;
+ *  - online softmax per head with wave reductions;
+ *  - P.V: lane = (key group, float4 column), all of its value loads issued
+ *    together, the weights p read back from the wave's LDS row.
+ * The waves' (max, sum, partial output) are merged in wave order through
+ * LDS.  Thread 0..HD/2 ropes the group's queries and the new key; the new
+ * key and value are appended to the cache and used from LDS at position pos. */
+constexpr int AG_WAVES = 8;
+
+template <int HD, int KVM>
+__global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
+    constexpr int W = AG_WAVES;
+    constexpr int AG_MAXM = KVM; /* query heads per KV head (compile time: registers, not scratch) */
+    constexpr int HD4 = HD / 4, KGW = 64 / HD4; /* P.V: key groups per wave */
+    __shared__ float qs[AG_MAXM][HD];
+    __shared__ float kcur[HD];
+    __shared__ float vcur[HD];
+    __shared__ float ps[W][AG_MAXM][64];
+    __shared__ float4 po[W][AG_MAXM][HD4];
+    __shared__ float pm[W][AG_MAXM];
+    __shared__ float pl[W][AG_MAXM];
+    const int kh = blockIdx.x, b = blockIdx.y;
+    constexpr int kv_mul = KVM;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int pos = a.st->pos, S = pos + 1;
+    if (t < HD / 2) {
+        const float fr = a.inv_freq[t];
+        const float ang = (float)pos * fr;
+        const float c = cosf(ang), sn = sinf(ang);
+        for (int j = 0; j < kv_mul; j++) {
+            const float* qh = a.q + (size_t)b * a.NH * HD + (size_t)(kh * kv_mul + j) * HD;
+            const float q0 = qh[t], q1 = qh[t + HD / 2];
+            qs[j][t] = q0 * c - q1 * sn;
+            qs[j][t + HD / 2] = q0 * sn + q1 * c;
+        }
+        const float* kr = a.k + (size_t)b * a.KV + kh * HD;
+        const float k0v = kr[t], k1v = kr[t + HD / 2];
+        kcur[t] = k0v * c - k1v * sn;
+        kcur[t + HD / 2] = k0v * sn + k1v * c;
+    }
+    if (t < HD) vcur[t] = a.v[(size_t)b * a.KV + kh * HD + t];
+    __syncthreads();
+    const size_t slab = (size_t)a.MS * a.KV;
+    float* kT = a.kvc + ((size_t)b * a.L + a.layer) * 2 * slab + (size_t)kh * HD * a.MS;
+    float* vc = a.kvc + (((size_t)b * a.L + a.layer) * 2 + 1) * slab + kh * HD;
+    if (t < HD) {
+        kT[((size_t)(t >> 2) * a.MS + pos) * 4 + (t & 3)] = kcur[t];
+        vc[(size_t)pos * a.KV + t] = vcur[t];
+    }
+    const int per = (S + W - 1) / W;
+    const int w0 = wave * per, w1 = min(S, w0 + per);
+    float m_run[AG_MAXM], l_run[AG_MAXM];
+    float4 acc[AG_MAXM];
+#pragma unroll
+    for (int j = 0; j < AG_MAXM; j++) {
+        m_run[j] = -INFINITY;
+        l_run[j] = 0.0f;
+        acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const int kg = lane / HD4, dg = lane % HD4;
+    const size_t kstep = (size_t)a.MS * 4;
+    for (int c0 = w0; c0 < w1; c0 += 64) {
+        const int n = min(64, w1 - c0);
+        const int key = c0 + lane;
+        const bool valid = lane < n;
+        float4 k4[HD4];
+        if (valid && key < pos) {
+#pragma unroll
+            for (int e = 0; e < HD4; e++)
+                __builtin_memcpy(&k4[e], __builtin_assume_aligned(kT + (size_t)key * 4 + e * kstep, 16), 16);
+        } else {
+#pragma unroll
+            for (int e = 0; e < HD4; e++) k4[e] = make_float4(kcur[4 * e], kcur[4 * e + 1], kcur[4 * e + 2], kcur[4 * e + 3]);
+        }
+#pragma unroll
+        for (int j = 0; j < AG_MAXM; j++) {
+            float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+            for (int e = 0; e < HD4; e++) {
+                s0 = fmaf(qs[j][4 * e + 0], k4[e].x, s0);
+                s1 = fmaf(qs[j][4 * e + 1], k4[e].y, s1);
+                s2 = fmaf(qs[j][4 * e + 2], k4[e].z, s2);
+                s3 = fmaf(qs[j][4 * e + 3], k4[e].w, s3);
+            }
+            const float sc = valid ? ((s0 + s1) + (s2 + s3)) * a.scale : -INFINITY;
+            const float mn = fmaxf(m_run[j], wave_max(sc));
+            const float p = valid ? expf(sc - mn) : 0.0f;
+            const float alpha = expf(m_run[j] - mn);
+            l_run[j] = l_run[j] * alpha + wave_sum(p);
+            acc[j].x *= alpha;
+            acc[j].y *= alpha;
+            acc[j].z *= alpha;
+            acc[j].w *= alpha;
+            m_run[j] = mn;
+            ps[wave][j][lane] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        /* P.V over this lane's 64/KGW key slots, in two halves (half the value
+         * registers live at a time), each half's loads issued together */
+        constexpr int R = 64 / KGW, RH = R > 1 ? R / 2 : 1;
+#pragma unroll
+        for (int h0 = 0; h0 < R; h0 += RH) {
+            float4 v4[RH];
+#pragma unroll
+            for (int r = 0; r < RH; r++) {
+                const int i = kg + (h0 + r) * KGW;
+                if (i < n && c0 + i < pos)
+                    __builtin_memcpy(&v4[r], __builtin_assume_aligned(vc + (size_t)(c0 + i) * a.KV + 4 * dg, 16), 16);
+                else
+                    v4[r] = make_float4(vcur[4 * dg], vcur[4 * dg + 1], vcur[4 * dg + 2], vcur[4 * dg + 3]);
+            }
+#pragma unroll
+            for (int j = 0; j < AG_MAXM; j++) {
+#pragma unroll
+                for (int r = 0; r < RH; r++) {
+                    const int i = kg + (h0 + r) * KGW;
+                    const float p = i < n ? ps[wave][j][i] : 0.0f;
+                    acc[j].x = fmaf(p, v4[r].x, acc[j].x);
+                    acc[j].y = fmaf(p, v4[r].y, acc[j].y);
+                    acc[j].z = fmaf(p, v4[r].z, acc[j].z);
+                    acc[j].w = fmaf(p, v4[r].w, acc[j].w);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier(); /* ps is rewritten by the next chunk */
+    }
+#pragma unroll
+    for (int j = 0; j < AG_MAXM; j++) {
+#pragma unroll
+        for (int off = HD4; off < 64; off <<= 1) {
+            acc[j].x += __shfl_xor(acc[j].x, off);
+            acc[j].y += __shfl_xor(acc[j].y, off);
+            acc[j].z += __shfl_xor(acc[j].z, off);
+            acc[j].w += __shfl_xor(acc[j].w, off);
+        }
+        if (lane < HD4) po[wave][j][lane] = acc[j];
+        if (lane == 0) {
+            pm[wave][j] = m_run[j];
+            pl[wave][j] = l_run[j];
+        }
+    }
+    __syncthreads();
+    for (int u = t; u < kv_mul * HD; u += 64 * W) {
+        const int j = u / HD, d = u - j * HD;
+        float M = -INFINITY;
+        for (int w = 0; w < W; w++) M = fmaxf(M, pm[w][j]);
+        float num = 0.0f, den = 0.0f;
+        for (int w = 0; w < W; w++) {
+            if (pm[w][j] == -INFINITY) continue;
+            const float f = expf(pm[w][j] - M);
+            const float4 o = po[w][j][d >> 2];
+            const int c = d & 3;
+            den = fmaf(f, pl[w][j], den);
+            num = fmaf(f, c == 0 ? o.x : c == 1 ? o.y : c == 2 ? o.z : o.w, num);
+        }
+        a.out[(size_t)b * a.NH * HD + (size_t)(kh * kv_mul + j) * HD + d] = num / den;
+    }
+}
+
 } // namespace
 
 /* Inverse frequency of every rotary pair i < HD/2 (reference
@@ -1234,6 +1400,26 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
 }
 
 extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
+    const int kvm = a->NH / a->NKV;
+    /* B >= 2: one workgroup per KV-head group (K and V rows read once for the
+     * group's query heads).  B = 1: one workgroup per query head, which puts
+     * three times as many CUs on the step's few rows and measured faster. */
+    if (B >= 2 && (a->HD == 16 || a->HD == 32 || a->HD == 64) && kvm >= 1 && kvm <= 4) {
+        const dim3 g(a->NKV, B), tb(64 * AG_WAVES);
+#define AG_LAUNCH(HDV)                                                                          \
+        do {                                                                                    \
+            if (kvm == 1) hipLaunchKernelGGL((k_dec_attn_g<HDV, 1>), g, tb, 0, s, *a);          \
+            else if (kvm == 2) hipLaunchKernelGGL((k_dec_attn_g<HDV, 2>), g, tb, 0, s, *a);     \
+            else if (kvm == 3) hipLaunchKernelGGL((k_dec_attn_g<HDV, 3>), g, tb, 0, s, *a);     \
+            else hipLaunchKernelGGL((k_dec_attn_g<HDV, 4>), g, tb, 0, s, *a);                   \
+        } while (0)
+        if (a->HD == 64) AG_LAUNCH(64);
+        else if (a->HD == 32) AG_LAUNCH(32);
+        else AG_LAUNCH(16);
+#undef AG_LAUNCH
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
     if (a->HD == 64) hipLaunchKernelGGL(k_dec_attn<64>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     else if (a->HD == 128) hipLaunchKernelGGL(k_dec_attn<128>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     else hipLaunchKernelGGL(k_dec_attn<0>, dim3(a->NH, B), dim3(NT), 0, s, *a);

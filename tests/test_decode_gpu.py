@@ -132,6 +132,26 @@ def test_engine_step_matches_oracle(dims):
     assert max(errs) <= LOGIT_TOL, errs
 
 
+@pytest.mark.parametrize("B", [1, 2])
+def test_long_context_matches_oracle(B):
+    """1100 positions: each of the attention kernel's 8 waves walks several
+    64-key chunks (online softmax across chunks, then across waves)."""
+    w = bmhip.synthetic_weights(SMALL, 23)
+    n = 1100
+    toks = bmhip.synth_uniform_int(24, 0, SMALL["V"], n * B).reshape(n, B)
+    eng = bmhip.Engine(SMALL, max_seq_len=n, weights=w, batch=B)
+    orcs = [oracle_decoder(SMALL, w, n) for _ in range(B)]
+    worst = 0.0
+    for pos in range(n):
+        y = eng.step_batch(toks[pos]) if B > 1 else eng.step(int(toks[pos, 0]))[None, :]
+        for b in range(B):
+            r = orcs[b].step(int(toks[pos, b]), pos)
+            if pos % 50 == 0 or pos >= n - 3:
+                worst = max(worst, normwise(y[b], r))
+    eng.close()
+    assert worst <= LOGIT_TOL, worst
+
+
 def test_engine_synthetic_init_equals_host_weights():
     """bm_model_init_synthetic builds exactly the weights bmhip.synthetic_weights does."""
     a = bmhip.Engine(SMALL, max_seq_len=16, seed=77)
