@@ -839,7 +839,8 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
  *  - online softmax over chunks of ATT_CH keys held in LDS.
  * HDT > 0 fixes the head size at compile time (q in registers). */
 template <int HDT>
-__global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
+__device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, const float* qh, const float* kr,
+                                              const float* vr) {
     constexpr int HDMAX = HDT > 0 ? HDT : DEC_MAX_HD;
     __shared__ float qs[HDMAX];
     __shared__ float ks[HDMAX];
@@ -849,13 +850,9 @@ __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
     __shared__ float sh[4];
     const int HD = HDT > 0 ? HDT : a.HD;
     const int HD4 = HD / 4, KG = NT / HD4;
-    const int h = blockIdx.x, b = blockIdx.y;
     const int kv_mul = a.NH / a.NKV, kh = h / kv_mul;
     const int pos = a.st->pos;
     const int t = threadIdx.x;
-    const float* qh = a.q + (size_t)b * a.NH * HD + h * HD;
-    const float* kr = a.k + (size_t)b * a.KV + kh * HD;
-    const float* vr = a.v + (size_t)b * a.KV + kh * HD;
     if (t < HD / 2) {
         const float fr = a.inv_freq[t];
         const float ang = (float)pos * fr;
@@ -982,6 +979,16 @@ __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
         a.out[(size_t)b * a.NH * HD + h * HD + t] = sum / l_run;
     }
 }
+
+template <int HDT>
+__global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
+    const int HD = HDT > 0 ? HDT : a.HD;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int kh = h / (a.NH / a.NKV);
+    dec_attn_head<HDT>(a, h, b, a.q + (size_t)b * a.NH * HD + h * HD, a.k + (size_t)b * a.KV + kh * HD,
+                       a.v + (size_t)b * a.KV + kh * HD);
+}
+
 
 /* Decode attention of one KV-head group: workgroup (KV head kh, sequence b)
  * serves all kv_mul query heads of the group, so each cached key and value

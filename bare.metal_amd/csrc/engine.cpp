@@ -106,6 +106,7 @@ struct bm_session_s {
     long prof_steps;
     hipEvent_t ev0, ev1;
     hipEvent_t* pev;     /* one event after every kernel of a profiled step */
+    int* pkind;          /* phase kind of the interval that ends at pev[i] */
     int n_pev;
     int mark;            /* next event index while a profiled step is enqueued, -1: not profiling */
 };
@@ -337,8 +338,11 @@ extern "C" const char* bm_get_arch_name(const bm_model_t* m) { return m ? "llama
 /* Kernel kinds of a step, in launch order within a layer. */
 enum { PH_EMBED, PH_QKV, PH_ATTN, PH_O, PH_GATEUP, PH_DOWN, PH_HEAD };
 
-static int mark(bm_session_t* S) {
+/* Profiled steps: an event after every kernel, tagged with the phase the
+ * interval before it belongs to (-1: the step's first event). */
+static int mark(bm_session_t* S, int kind) {
     if (S->mark < 0) return 0;
+    S->pkind[S->mark] = kind;
     HIP_TRY(hipEventRecord(S->pev[S->mark++], S->ctx->s), "hipEventRecord", return -1);
     return 0;
 }
@@ -355,22 +359,12 @@ static int enqueue_step(bm_session_t* S) {
     e.D = D;
     e.V = m->V;
     e.B = B;
-    if (mark(S) || dec_launch_embed(&e, s) || mark(S)) return -1;
+    if (mark(S, -1) || dec_launch_embed(&e, s) || mark(S, PH_EMBED)) return -1;
     const float eps = 1e-5f; /* reference graph.c:134,175,219 */
     for (int l = 0; l < m->L; l++) {
         const unsigned char* wl = m->d_q8 + (size_t)l * m->layer_bytes;
         DecMv mv;
         memset(&mv, 0, sizeof mv);
-        /* RMSNorm + q, k, v */
-        mv.x = S->x; mv.norm_w = m->d_ln1 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
-        mv.nmat = 3;
-        mv.w[0] = wl + m->off[0]; mv.y[0] = S->q; mv.OC[0] = m->QD;
-        mv.w[1] = wl + m->off[1]; mv.y[1] = S->k; mv.OC[1] = m->KV;
-        mv.w[2] = wl + m->off[2]; mv.y[2] = S->v; mv.OC[2] = m->KV;
-        mv.tile0[0] = 0;
-        for (int i = 0; i < 3; i++) mv.tile0[i + 1] = mv.tile0[i] + dec_mv_tiles(mv.OC[i], D, 0);
-        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
-        /* rope + KV append + attention */
         DecAttn at;
         memset(&at, 0, sizeof at);
         at.q = S->q; at.k = S->k; at.v = S->v; at.kvc = S->kvc; at.out = S->att; at.st = S->st;
@@ -380,26 +374,36 @@ static int enqueue_step(bm_session_t* S) {
         bmk_rope_table(rp, m->HD, at.inv_freq);
         at.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
         at.NH = m->NH; at.NKV = m->NKV; at.HD = m->HD; at.KV = m->KV; at.MS = S->MS; at.L = m->L; at.layer = l;
-        if (dec_launch_attn(&at, B, s) || mark(S)) return -1;
+        /* RMSNorm + q, k, v */
+        mv.x = S->x; mv.norm_w = m->d_ln1 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
+        mv.nmat = 3;
+        mv.w[0] = wl + m->off[0]; mv.y[0] = S->q; mv.OC[0] = m->QD;
+        mv.w[1] = wl + m->off[1]; mv.y[1] = S->k; mv.OC[1] = m->KV;
+        mv.w[2] = wl + m->off[2]; mv.y[2] = S->v; mv.OC[2] = m->KV;
+        mv.tile0[0] = 0;
+        for (int i = 0; i < 3; i++) mv.tile0[i + 1] = mv.tile0[i] + dec_mv_tiles(mv.OC[i], D, 0);
+        if (dec_launch_mv(&mv, s) || mark(S, PH_QKV)) return -1;
+        /* rope + KV append + attention */
+        if (dec_launch_attn(&at, B, s) || mark(S, PH_ATTN)) return -1;
         /* o + residual */
         memset(&mv, 0, sizeof mv);
         mv.x = S->att; mv.C = m->QD; mv.B = B; mv.ldx = m->QD; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[3]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->QD, 0);
-        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S, PH_O)) return -1;
         /* RMSNorm + gate, up + SwiGLU */
         memset(&mv, 0, sizeof mv);
         mv.x = S->x; mv.norm_w = m->d_ln2 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
         mv.nmat = 1; mv.glu = 1;
         mv.w[0] = wl + m->off[4]; mv.w[1] = wl + m->off[5]; mv.y[0] = S->h; mv.OC[0] = m->H;
         mv.tile0[1] = dec_mv_tiles(m->H, D, 1);
-        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S, PH_GATEUP)) return -1;
         /* down + residual */
         memset(&mv, 0, sizeof mv);
         mv.x = S->h; mv.C = m->H; mv.B = B; mv.ldx = m->H; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[6]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->H, 0);
-        if (dec_launch_mv(&mv, s) || mark(S)) return -1;
+        if (dec_launch_mv(&mv, s) || mark(S, PH_DOWN)) return -1;
     }
     DecHead hd;
     memset(&hd, 0, sizeof hd);
@@ -407,7 +411,7 @@ static int enqueue_step(bm_session_t* S) {
     hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
     hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
-    if (dec_launch_head(&hd, s) || mark(S)) return -1;
+    if (dec_launch_head(&hd, s) || mark(S, PH_HEAD)) return -1;
     return 0;
 }
 
@@ -425,6 +429,7 @@ static void session_free(bm_session_t* S) {
     if (S->ev1) hipEventDestroy(S->ev1);
     for (int i = 0; i < S->n_pev; i++) hipEventDestroy(S->pev[i]);
     free(S->pev);
+    free(S->pkind);
     if (S->m) S->m->nsessions--;
     free(S);
 }
@@ -537,6 +542,9 @@ static int launch_step(bm_session_t* S) {
             hipEvent_t* ev = (hipEvent_t*)realloc(S->pev, (size_t)need * sizeof(hipEvent_t));
             if (!ev) return -1;
             S->pev = ev;
+            int* pk = (int*)realloc(S->pkind, (size_t)need * sizeof(int));
+            if (!pk) return -1;
+            S->pkind = pk;
             for (; S->n_pev < need; S->n_pev++)
                 HIP_TRY(hipEventCreate(&S->pev[S->n_pev]), "hipEventCreate", return -1);
         }
@@ -549,8 +557,9 @@ static int launch_step(bm_session_t* S) {
         float ms = 0.f;
         if (hipEventElapsedTime(&ms, S->pev[0], S->pev[n - 1]) == hipSuccess) S->prof_ms += ms;
         for (int i = 1; i < n; i++) {
-            const int kind = i == 1 ? PH_EMBED : (i == n - 1 ? PH_HEAD : PH_QKV + (i - 2) % 5);
-            if (hipEventElapsedTime(&ms, S->pev[i - 1], S->pev[i]) == hipSuccess) S->prof_phase[kind] += ms;
+            const int kind = S->pkind[i];
+            if (kind >= 0 && hipEventElapsedTime(&ms, S->pev[i - 1], S->pev[i]) == hipSuccess)
+                S->prof_phase[kind] += ms;
         }
         S->prof_steps++;
     } else if (S->use_graph) {
