@@ -412,6 +412,16 @@ class Engine:
             raise BackendError("bm_step failed")
         return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
 
+    def forward(self, tokens) -> np.ndarray:
+        """bm_forward: a prompt at position 0 of a batch-1 session is prefilled
+        in one pass; otherwise the tokens are stepped one by one.  Returns the
+        logits after the last token."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        p = lib().bm_forward(self.sess, _ptr(t), int(t.size))
+        if not p:
+            raise BackendError("bm_forward failed")
+        return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
+
     def step_batch(self, tokens) -> np.ndarray:
         t = np.ascontiguousarray(tokens, dtype=np.int32)
         p = lib().bm_step_batch(self.sess, _ptr(t))

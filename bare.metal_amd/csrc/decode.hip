@@ -838,9 +838,15 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
  *  - P.V: 16 key groups x HD/4 float4 columns (coalesced 16-byte loads);
  *  - online softmax over chunks of ATT_CH keys held in LDS.
  * HDT > 0 fixes the head size at compile time (q in registers). */
+/* Attention of query head h of sequence b at position pos, given the
+ * un-roped q row, the group's un-roped k row and its v row of that
+ * position.  Keys before pos come from the cache; append = true writes this
+ * position's k and v to the cache (first head of the group), false leaves
+ * the cache alone (prefill: every position is already there).  The output
+ * row is a.out + out_row * NH * HD. */
 template <int HDT>
-__device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, const float* qh, const float* kr,
-                                              const float* vr) {
+__device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, int pos, bool append, int out_row,
+                                              const float* qh, const float* kr, const float* vr) {
     constexpr int HDMAX = HDT > 0 ? HDT : DEC_MAX_HD;
     __shared__ float qs[HDMAX];
     __shared__ float ks[HDMAX];
@@ -851,7 +857,6 @@ __device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, co
     const int HD = HDT > 0 ? HDT : a.HD;
     const int HD4 = HD / 4, KG = NT / HD4;
     const int kv_mul = a.NH / a.NKV, kh = h / kv_mul;
-    const int pos = a.st->pos;
     const int t = threadIdx.x;
     if (t < HD / 2) {
         const float fr = a.inv_freq[t];
@@ -869,7 +874,7 @@ __device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, co
     const size_t slab = (size_t)a.MS * a.KV;
     float* kT = a.kvc + ((size_t)b * a.L + a.layer) * 2 * slab + (size_t)kh * HD * a.MS;
     float* vc = a.kvc + (((size_t)b * a.L + a.layer) * 2 + 1) * slab + kh * HD;
-    if (h % kv_mul == 0 && t < HD) {
+    if (append && h % kv_mul == 0 && t < HD) {
         kT[((size_t)(t >> 2) * a.MS + pos) * 4 + (t & 3)] = ks[t];
         vc[(size_t)pos * a.KV + t] = vs[t];
     }
@@ -976,7 +981,7 @@ __device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, co
             const float4 r = red4[k * HD4 + c4];
             sum += lane == 0 ? r.x : lane == 1 ? r.y : lane == 2 ? r.z : r.w;
         }
-        a.out[(size_t)b * a.NH * HD + h * HD + t] = sum / l_run;
+        a.out[(size_t)out_row * a.NH * HD + h * HD + t] = sum / l_run;
     }
 }
 
@@ -985,7 +990,7 @@ __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
     const int HD = HDT > 0 ? HDT : a.HD;
     const int h = blockIdx.x, b = blockIdx.y;
     const int kh = h / (a.NH / a.NKV);
-    dec_attn_head<HDT>(a, h, b, a.q + (size_t)b * a.NH * HD + h * HD, a.k + (size_t)b * a.KV + kh * HD,
+    dec_attn_head<HDT>(a, h, b, a.st->pos, true, b, a.q + (size_t)b * a.NH * HD + h * HD, a.k + (size_t)b * a.KV + kh * HD,
                        a.v + (size_t)b * a.KV + kh * HD);
 }
 
@@ -1154,6 +1159,84 @@ __global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
         }
         a.out[(size_t)b * a.NH * HD + (size_t)(kh * kv_mul + j) * HD + d] = num / den;
     }
+}
+
+/* ------------------------------------------------------------------ */
+/* Prefill (bm_forward on a whole prompt at position 0, batch 1): every
+ * prompt position at once, the projections on the bf16-MFMA GEMM
+ * (q8_gemm.hip), as the reference's prefill graph runs them on its BT > 1
+ * Q8 path (graph.c:273-381, scheduler.c:1015-1332). */
+
+/* x[p] = emb[tok[p]] */
+__global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, const float* __restrict__ emb,
+                                                 float* __restrict__ x, int D) {
+    const int p = blockIdx.x;
+    const float* er = emb + (size_t)tok[p] * D;
+    float* xr = x + (size_t)p * D;
+    for (int j = threadIdx.x; j < D; j += NT) xr[j] = er[j];
+}
+
+/* Row p: x += add (when add is given: the residual), then out = bf16 of
+ * RMSNorm(x) * w, the activation of the next GEMM. */
+__global__ __launch_bounds__(NT) void k_pf_norm_bf16(float* __restrict__ x, const float* __restrict__ add,
+                                                     const float* __restrict__ w, unsigned short* __restrict__ out,
+                                                     int D, float eps) {
+    __shared__ float sh[4];
+    const int p = blockIdx.x;
+    float* xr = x + (size_t)p * D;
+    float ss = 0.0f;
+    for (int j = threadIdx.x; j < D; j += NT) {
+        float v = xr[j];
+        if (add) {
+            v += add[(size_t)p * D + j];
+            xr[j] = v;
+        }
+        ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+    for (int j = threadIdx.x; j < D; j += NT) out[(size_t)p * D + j] = bf16_bits((xr[j] * inv) * w[j]);
+}
+
+/* RoPE of every position's k and the cache append of k and v (layer a.layer,
+ * sequence 0): workgroup p, thread (KV head, rotary pair). */
+__global__ __launch_bounds__(NT) void k_pf_kv(DecAttn a, const float* __restrict__ k, const float* __restrict__ v) {
+    const int p = blockIdx.x;
+    const int HD = a.HD, half = HD / 2;
+    const size_t slab = (size_t)a.MS * a.KV;
+    float* kc = a.kvc + (size_t)a.layer * 2 * slab;
+    float* vc = kc + slab;
+    for (int i = threadIdx.x; i < a.NKV * half; i += NT) {
+        const int kh = i / half, t = i - kh * half;
+        const float ang = (float)p * a.inv_freq[t];
+        const float c = cosf(ang), sn = sinf(ang);
+        const float* kr = k + (size_t)p * a.KV + kh * HD;
+        const float k0 = kr[t], k1 = kr[t + half];
+        float* kT = kc + (size_t)kh * HD * a.MS;
+        kT[((size_t)(t >> 2) * a.MS + p) * 4 + (t & 3)] = k0 * c - k1 * sn;
+        const int t2 = t + half;
+        kT[((size_t)(t2 >> 2) * a.MS + p) * 4 + (t2 & 3)] = k0 * sn + k1 * c;
+    }
+    for (int i = threadIdx.x; i < a.KV; i += NT) vc[(size_t)p * a.KV + i] = v[(size_t)p * a.KV + i];
+}
+
+/* Causal attention of every prompt position: workgroup (query head h,
+ * position p) over keys 0..p, the cache already holding all of them. */
+template <int HDT>
+__global__ __launch_bounds__(NT) void k_pf_attn(DecAttn a, const float* __restrict__ q, const float* __restrict__ k,
+                                                const float* __restrict__ v) {
+    const int HD = HDT > 0 ? HDT : a.HD;
+    const int h = blockIdx.x, p = blockIdx.y;
+    const int kh = h / (a.NH / a.NKV);
+    dec_attn_head<HDT>(a, h, 0, p, false, p, q + (size_t)p * a.NH * HD + h * HD, k + (size_t)p * a.KV + kh * HD,
+                       v + (size_t)p * a.KV + kh * HD);
+}
+
+/* out = bf16(silu(g) * u) */
+__global__ __launch_bounds__(NT) void k_pf_swiglu_bf16(const float* __restrict__ g, const float* __restrict__ u,
+                                                       unsigned short* __restrict__ out, long n) {
+    const long i = (long)blockIdx.x * NT + threadIdx.x;
+    if (i < n) out[i] = bf16_bits(silu_mul(g[i], u[i]));
 }
 
 } // namespace
@@ -1459,6 +1542,40 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
         hipLaunchKernelGGL(k_head<true>, dim3(a->tiles), dim3(NT), 0, s, *a);
     else
         hipLaunchKernelGGL(k_head<false>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* Prefill launchers (arguments validated by engine.cpp). */
+
+extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(NT), 0, s, tok, emb, x, D);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
+                                hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, add, w, out, D, eps);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n,
+                                hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_kv, dim3(n), dim3(NT), 0, s, *a, k, v);
+    BMK_LAUNCH_CHECK();
+    const dim3 g(a->NH, n);
+    if (a->HD == 64) hipLaunchKernelGGL(k_pf_attn<64>, g, dim3(NT), 0, s, *a, q, k, v);
+    else if (a->HD == 128) hipLaunchKernelGGL(k_pf_attn<128>, g, dim3(NT), 0, s, *a, q, k, v);
+    else hipLaunchKernelGGL(k_pf_attn<0>, g, dim3(NT), 0, s, *a, q, k, v);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_swiglu_bf16, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, g, u, out, n);
     BMK_LAUNCH_CHECK();
     return 0;
 }

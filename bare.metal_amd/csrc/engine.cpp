@@ -23,6 +23,8 @@
  */
 #include "bmk.h"
 #include "decode_state.h"
+#include "q8_gemm.h"
+#include "../../include/bm_q8.h"
 #include "../../include/backend.h"
 #include "../../include/backend_hip_device.h"
 #include "../../include/baremetal.h"
@@ -32,12 +34,23 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 extern "C" {
 int dec_mv_tiles(int OC, int C, int glu);
 int dec_head_tiles(int D, int V, int q8);
 int dec_launch_embed(const DecEmbed* a, hipStream_t s);
 int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
+int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
+int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
+                     hipStream_t s);
+int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, hipStream_t s);
+int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s);
+int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
+                    int n_tiles, hipStream_t s);
+int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
 int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 }
@@ -87,6 +100,14 @@ struct bm_session_s {
     bm_model_t* m;
     int B, MS;
     float *x, *q, *k, *v, *att, *h, *logits, *kvc;
+    /* prefill buffers, allocated on the first bm_forward over a prompt */
+    int pf_cap;              /* rows they hold */
+    float *pf_x, *pf_qkv, *pf_att, *pf_o, *pf_gu;
+    unsigned short* pf_a16;  /* bf16 activations of the next GEMM */
+    int* pf_tok;
+    unsigned char* pf_plan;  /* device GEMM plans */
+    unsigned char* h_plan;   /* pinned staging of the plans */
+    size_t pf_plan_cap;
     DecState* st;
     int* prompt;
     int* out_tokens;
@@ -422,6 +443,9 @@ static void session_free(bm_session_t* S) {
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
     hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->prompt); hipFree(S->out_tokens);
+    hipFree(S->pf_x); hipFree(S->pf_qkv); hipFree(S->pf_att); hipFree(S->pf_o); hipFree(S->pf_gu);
+    hipFree(S->pf_a16); hipFree(S->pf_tok); hipFree(S->pf_plan);
+    if (S->h_plan) hipHostFree(S->h_plan);
     if (S->h_st) hipHostFree(S->h_st);
     if (S->h_logits) hipHostFree(S->h_logits);
     if (S->h_io) hipHostFree(S->h_io);
@@ -612,8 +636,185 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
     return step_host(S, tokens);
 }
 
+/* ------------------------------------------------------------------ */
+/* prefill: a whole prompt at position 0 (reference session.c:86-139) */
+
+static int prefill_buffers(bm_session_t* S, int n) {
+    if (S->pf_cap >= n) return 0;
+    bm_model_t* m = S->m;
+    hipFree(S->pf_x); hipFree(S->pf_qkv); hipFree(S->pf_att); hipFree(S->pf_o); hipFree(S->pf_gu);
+    hipFree(S->pf_a16); hipFree(S->pf_tok);
+    S->pf_x = S->pf_qkv = S->pf_att = S->pf_o = S->pf_gu = NULL;
+    S->pf_a16 = NULL;
+    S->pf_tok = NULL;
+    S->pf_cap = 0;
+    const size_t N = (size_t)n;
+    const size_t widest = (size_t)std::max(std::max(m->D, m->H), m->QD);
+    if (hipMalloc(&S->pf_x, N * m->D * 4) != hipSuccess ||
+        hipMalloc(&S->pf_qkv, N * (m->QD + 2 * (size_t)m->KV) * 4) != hipSuccess ||
+        hipMalloc(&S->pf_att, N * m->QD * 4) != hipSuccess || hipMalloc(&S->pf_o, N * m->D * 4) != hipSuccess ||
+        hipMalloc(&S->pf_gu, N * 2 * (size_t)m->H * 4) != hipSuccess ||
+        hipMalloc(&S->pf_a16, N * widest * 2) != hipSuccess || hipMalloc(&S->pf_tok, N * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        BMK_ERR("bm_forward: prefill buffers for %d tokens could not be allocated", n);
+        return -1;
+    }
+    S->pf_cap = n;
+    return 0;
+}
+
+/* One GEMM launch of the prefill: its plan's place in the plan buffer. */
+struct PfGemm {
+    size_t off;
+    int nprob, n_tiles;
+};
+
+/* Appends the plan of one multi-GEMM launch to the staging buffer. */
+static int pf_plan(bm_session_t* S, size_t* used, PfGemm* g, int nprob, const uint64_t* a_off, const uint64_t* w_off,
+                   const uint64_t* c_off, const int* M, const int* N, const int* K, const int* lda, const int* ldc) {
+    int nt = 0;
+    const long need = bm_q8_gemm_plan(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, NULL, 0, &nt);
+    if (need < 0) return -1;
+    const size_t at = (*used + 7) & ~(size_t)7;
+    if (at + (size_t)need > S->pf_plan_cap) return -1;
+    if (bm_q8_gemm_plan(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, S->h_plan + at, (size_t)need, &nt) != need)
+        return -1;
+    g->off = at;
+    g->nprob = nprob;
+    g->n_tiles = nt;
+    *used = at + (size_t)need;
+    return 0;
+}
+
+static int prefill(bm_session_t* S, const int* tokens, int n) {
+    bm_model_t* m = S->m;
+    hipStream_t s = S->ctx->s;
+    const int D = m->D, H = m->H, QD = m->QD, KV = m->KV, L = m->L;
+    const float eps = 1e-5f; /* reference graph.c:134,175,219 */
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->V) {
+            BMK_ERR("bm_forward: token %d outside [0, %d)", tokens[i], m->V);
+            return -1;
+        }
+    if (prefill_buffers(S, n)) return -1;
+    /* GEMM plans, per layer: q/k/v, o, gate/up, down (generous bound on the size) */
+    const size_t per_layer = 4 * (7 * sizeof(GmDesc) + 8) +
+                             4 * sizeof(unsigned int) * 8 * ((size_t)(n + GM_BM - 1) / GM_BM) *
+                                 (3 + (size_t)(QD + 2 * KV + 2 * D + 2 * H) / GM_BN + 4);
+    const size_t plan_bytes = per_layer * L + 64;
+    if (S->pf_plan_cap < plan_bytes) {
+        hipFree(S->pf_plan);
+        if (S->h_plan) hipHostFree(S->h_plan);
+        S->pf_plan = NULL;
+        S->h_plan = NULL;
+        S->pf_plan_cap = 0;
+        if (hipMalloc(&S->pf_plan, plan_bytes) != hipSuccess ||
+            hipHostMalloc(&S->h_plan, plan_bytes, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            BMK_ERR("bm_forward: prefill plan buffers could not be allocated");
+            return -1;
+        }
+        S->pf_plan_cap = plan_bytes;
+    }
+    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
+    std::vector<PfGemm> g((size_t)4 * L);
+    size_t used = 0;
+    const uint64_t nn = (uint64_t)n;
+    for (int l = 0; l < L; l++) {
+        const uint64_t lw = (uint64_t)l * m->layer_bytes;
+        {
+            const uint64_t a[3] = {0, 0, 0}, w[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
+            const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
+            const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
+            if (pf_plan(S, &used, &g[4 * l + 0], 3, a, w, c, M, N, K, lda, N)) return -1;
+        }
+        {
+            const uint64_t a = 0, w = lw + m->off[3], c = 0;
+            const int M = n, N = D, K = QD;
+            if (pf_plan(S, &used, &g[4 * l + 1], 1, &a, &w, &c, &M, &N, &K, &K, &N)) return -1;
+        }
+        {
+            const uint64_t a[2] = {0, 0}, w[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
+            const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
+            if (pf_plan(S, &used, &g[4 * l + 2], 2, a, w, c, M, N, K, K, N)) return -1;
+        }
+        {
+            const uint64_t a = 0, w = lw + m->off[6], c = 0;
+            const int M = n, N = D, K = H;
+            if (pf_plan(S, &used, &g[4 * l + 3], 1, &a, &w, &c, &M, &N, &K, &K, &N)) return -1;
+        }
+    }
+    memcpy(S->h_io, tokens, (size_t)n * 4);
+    HIP_TRY(hipMemcpyAsync(S->pf_tok, S->h_io, (size_t)n * 4, hipMemcpyHostToDevice, s), "token write", return -1);
+    HIP_TRY(hipMemcpyAsync(S->pf_plan, S->h_plan, used, hipMemcpyHostToDevice, s), "plan write", return -1);
+
+    DecAttn at;
+    memset(&at, 0, sizeof at);
+    at.kvc = S->kvc;
+    at.out = S->pf_att;
+    const float rp[6] = {m->arch.rope_theta, m->arch.rope_factor, m->arch.rope_low_freq_factor,
+                         m->arch.rope_high_freq_factor, m->arch.rope_original_max,
+                         m->arch.rope_scaling == BM_ROPE_LLAMA3 ? 1.0f : 0.0f};
+    bmk_rope_table(rp, m->HD, at.inv_freq);
+    at.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
+    at.NH = m->NH; at.NKV = m->NKV; at.HD = m->HD; at.KV = KV; at.MS = S->MS; at.L = L;
+
+    float* q = S->pf_qkv;
+    float* k = q + (size_t)n * QD;
+    float* v = k + (size_t)n * KV;
+    float* gt = S->pf_gu;
+    float* up = gt + (size_t)n * H;
+    auto gemm = [&](const PfGemm& p, float* C) {
+        return gm_launch_multi(S->pf_a16, 1, m->d_q8, C, S->pf_plan + p.off, p.nprob, p.n_tiles, s);
+    };
+    if (dec_pf_embed(S->pf_tok, m->d_emb, S->pf_x, n, D, s)) return -1;
+    for (int l = 0; l < L; l++) {
+        at.layer = l;
+        /* residual of the previous layer's down projection, RMSNorm, q/k/v */
+        if (dec_pf_norm_bf16(S->pf_x, l ? S->pf_o : NULL, m->d_ln1 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||
+            gemm(g[4 * l + 0], S->pf_qkv) ||
+            /* RoPE, cache append, causal attention */
+            dec_pf_attention(&at, q, k, v, n, s) || gm_cast_bf16(S->pf_att, S->pf_a16, (long)n * QD, s) ||
+            /* o, residual, RMSNorm, gate/up, SwiGLU, down */
+            gemm(g[4 * l + 1], S->pf_o) ||
+            dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_ln2 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||
+            gemm(g[4 * l + 2], S->pf_gu) || dec_pf_swiglu_bf16(gt, up, S->pf_a16, (long)n * H, s) ||
+            gemm(g[4 * l + 3], S->pf_o))
+            return -1;
+    }
+    /* last residual (the bf16 output is not used), then the head on the last position */
+    if (dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_lnf, S->pf_a16, n, D, eps, s)) return -1;
+    DecHead hd;
+    memset(&hd, 0, sizeof hd);
+    hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_emb;
+    hd.wq = m->q8_head ? m->d_head8 : NULL;
+    hd.logits = S->logits; hd.st = NULL; hd.out_tokens = NULL;
+    hd.D = D; hd.V = m->V; hd.B = 1; hd.eps = eps;
+    hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
+    if (dec_launch_head(&hd, s)) return -1;
+    /* the decode steps continue at position n */
+    memset(S->h_st, 0, sizeof(DecState));
+    S->h_st->B = S->B;
+    S->h_st->host_mode = 1;
+    S->h_st->pos = n;
+    if (state_write(S)) return -1;
+    HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)m->V * 4, hipMemcpyDeviceToHost, s), "logits read",
+            return -1);
+    HIP_TRY(hipStreamSynchronize(s), "sync", return -1);
+    S->pos = n;
+    return 0;
+}
+
+/* Reference session.c:141-149: a prompt at position 0 of a batch-1 session
+ * is prefilled in one pass (bf16-MFMA projections); anything else steps
+ * token by token. */
 extern "C" float* bm_forward(bm_session_t* S, const int* tokens, int n_tokens) {
     if (!S || (!tokens && n_tokens > 0)) return NULL;
+    if (n_tokens <= 0) return S->h_logits;
+    if (n_tokens > 1 && S->pos == 0 && S->B == 1 && n_tokens <= S->MS && (size_t)n_tokens <= S->h_io_cap) {
+        if (prefill(S, tokens, n_tokens) != 0) return NULL;
+        return S->h_logits;
+    }
     float* out = S->h_logits;
     for (int i = 0; i < n_tokens; i++) {
         out = bm_step(S, tokens[i]);

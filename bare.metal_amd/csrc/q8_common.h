@@ -27,6 +27,17 @@ __device__ __forceinline__ Blk load_block(const unsigned char* p) {
     return b;
 }
 
+/* fp32 -> bf16 bits, round to nearest even (v_cvt_pk_bf16_f32) */
+__device__ __forceinline__ unsigned short bf16_bits(float v) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t f = {v, 0.0f};
+    const bf16x2_t r = __builtin_convertvector(f, bf16x2_t);
+    unsigned int u;
+    __builtin_memcpy(&u, &r, 4);
+    return (unsigned short)(u & 0xffffu);
+}
+
 /* int8 k (0..3) of a packed dword, exactly as fp32 */
 __device__ __forceinline__ float q8_byte(unsigned int w, int k) { return (float)(signed char)((w >> (8 * k)) & 0xffu); }
 

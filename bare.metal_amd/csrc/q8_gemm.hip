@@ -419,3 +419,27 @@ extern "C" int bmk_launch_cast_bf16(const bmk_launch_t* a) {
     BMK_LAUNCH_CHECK();
     return 0;
 }
+
+/* Multi-GEMM launch from a device-resident plan built by bm_q8_gemm_plan
+ * (the engine's prefill; the plan was validated when it was built). */
+extern "C" int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
+                               int n_tiles, hipStream_t s) {
+    if (nprob <= 0 || n_tiles <= 0) return 0;
+    const GmDesc* desc = (const GmDesc*)plan;
+    const unsigned int* tmap = (const unsigned int*)((const char*)plan + (size_t)nprob * sizeof(GmDesc));
+    if (a_bf16)
+        hipLaunchKernelGGL(k_q8_gemm_multi<true>, dim3((unsigned)n_tiles), dim3(NTH), 0, s, A, W, C, desc, tmap);
+    else
+        hipLaunchKernelGGL(k_q8_gemm_multi<false>, dim3((unsigned)n_tiles), dim3(NTH), 0, s, A, W, C, desc, tmap);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* fp32 -> bf16 over n elements (RNE) */
+extern "C" int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s) {
+    if (n <= 0) return 0;
+    const long n8 = n / 8;
+    hipLaunchKernelGGL(k_cast_bf16, dim3((unsigned)((n8 + NTH) / NTH)), dim3(NTH), 0, s, src, dst, n8, n);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}

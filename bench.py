@@ -253,6 +253,53 @@ def gemm_leg(steps: int, warmup: int):
     }
 
 
+def copy_ceiling(mib: int = 1024, reps: int = 5):
+    """copy_buffer over `mib` MiB (read + write), HIP events: the stream-copy
+    ceiling reported beside the matvec's bandwidth."""
+    be = bmhip.Backend()
+    n = mib << 20
+    src, dst = be.alloc(n), be.alloc(n)
+    enc = be.encoder()
+    for _ in range(reps):
+        if enc.dispatch(be.kernel("copy_buffer"), [src, dst, be.params(n, dtype=np.int64)], (n // 16,), (256,)):
+            raise RuntimeError("copy_buffer rejected")
+    ms = enc.wait_timed() / reps
+    be.close()
+    return {"copy_bytes_read": n, "copy_bytes_written": n, "us_per_copy": round(ms * 1e3, 2),
+            "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}
+
+
+def prefill_leg(reps: int = 5):
+    """SmolLM2-135M prompt prefill through bm_forward (one pass at position 0:
+    bf16-MFMA projections, causal attention, the KV cache filled), for 128-
+    and 512-token prompts; reported as prompt tokens per second, against the
+    same prompt stepped token by token."""
+    dims = bmhip.SMOLLM2_135M
+    out = {"workload": "SmolLM2-135M Q8 prefill of a random prompt via bm_forward (random init as config 5)"}
+    for n in (128, 512):
+        toks = bmhip.synth_uniform_int(2025 + n, 0, dims["V"], n)
+        eng = bmhip.Engine(dims, max_seq_len=n + 8, seed=2025)
+        eng.forward(toks)  # allocates the prefill buffers
+        ts = []
+        for _ in range(reps):
+            eng.reset()
+            t0 = time.perf_counter()
+            eng.forward(toks)
+            ts.append(time.perf_counter() - t0)
+        dt = float(np.median(ts))
+        eng.reset()
+        t0 = time.perf_counter()
+        for t in toks[:64]:
+            eng.step(int(t))
+        step_dt = (time.perf_counter() - t0) / 64
+        eng.close()
+        out[f"n{n}"] = {"ms": round(dt * 1e3, 3), "tok_s": round(n / dt, 1),
+                        "stepwise_ms_est": round(step_dt * n * 1e3, 2)}
+        log(f"[bench] prefill {n} tokens: {dt * 1e3:.2f} ms = {n / dt:.0f} tok/s "
+            f"(token by token with host round trips: {step_dt * n * 1e3:.1f} ms)")
+    return out
+
+
 def e2e_decode(cpu_steps: int, cpu_threads: int, graph: bool = True):
     """Config 5: SmolLM2-135M Q8 greedy decode, 128-token prompt + 256
     generated tokens (383 decode steps, prompt tokens stepped one by one as
@@ -312,6 +359,7 @@ def main():
     ap.add_argument("--e2e", type=int, default=1, help="also time config-5 greedy decode (0: skip)")
     ap.add_argument("--matvec", type=int, default=1, help="0: only the config-5 decode leg (for kernel traces)")
     ap.add_argument("--gemm", type=int, default=1, help="also time the config-4 prefill GEMM (0: skip)")
+    ap.add_argument("--prefill", type=int, default=1, help="also time bm_forward prompt prefill (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
@@ -323,22 +371,14 @@ def main():
         sys.exit(2)
 
     if args.calib_copy_mib > 0:
-        be = bmhip.Backend()
-        n = args.calib_copy_mib << 20
-        src, dst = be.alloc(n), be.alloc(n)
-        enc = be.encoder()
-        for _ in range(5):
-            if enc.dispatch(be.kernel("copy_buffer"), [src, dst, be.params(n, dtype=np.int64)], (n // 16,), (256,)):
-                raise RuntimeError("copy_buffer rejected")
-        ms = enc.wait_timed() / 5
-        be.close()
-        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "us_per_copy": round(ms * 1e3, 2),
-                          "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        print(json.dumps(copy_ceiling(args.calib_copy_mib)), flush=True)
         return
     if not args.matvec:
         out = {}
         if args.gemm:
             out["prefill_gemm"] = gemm_leg(max(args.steps // 10, 10), 3)
+        if args.prefill:
+            out["prefill"] = prefill_leg()
         if args.e2e:
             out["e2e_decode"] = e2e_decode(0, args.cpu_threads, bool(args.e2e_graph))
         print(json.dumps(out), flush=True)
@@ -383,6 +423,8 @@ def main():
     be.close()
 
     gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
+    prefill = prefill_leg() if args.prefill else None
+    ceiling = copy_ceiling()
     e2e = (e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads, bool(args.e2e_graph))
            if args.e2e else None)
 
@@ -417,11 +459,13 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(args.model),
+            "copy_ceiling_gbps": ceiling["gbps"],
         },
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
         "pack_gbps_incl_upload": pack_gbps,
         "prefill_gemm": gemm,
+        "prefill": prefill,
         "e2e_decode": e2e,
     }
     print(json.dumps(line), flush=True)

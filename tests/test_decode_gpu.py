@@ -152,6 +152,63 @@ def test_long_context_matches_oracle(B):
     assert worst <= LOGIT_TOL, worst
 
 
+def cosine(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+@pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1)], ids=["tiny-12", "small-40", "small-1"])
+def test_prefill_matches_stepwise(dims, n):
+    """bm_forward over a prompt at position 0 (one pass, bf16-MFMA projections)
+    against stepping the same tokens one by one, as the reference's
+    prefill_test.c:63-85 checks it: cosine > 0.9999 of the logits after the
+    prompt and after one more step (the prefilled KV cache), same argmax
+    unless the stepwise top-2 margin is within the logit difference; plus
+    the prefill logits against the fp64 oracle (normwise <= 2e-2, the bf16
+    GEMM bound)."""
+    w = bmhip.synthetic_weights(dims, 91)
+    V = dims["V"]
+    toks = [(37 * i + 11) % V for i in range(n)]
+    nxt = (37 * n + 11) % V
+    eng = bmhip.Engine(dims, max_seq_len=64, weights=w)
+    pre = eng.forward(toks)
+    pre_next = eng.step(nxt)
+    eng.reset()
+    for t in toks:
+        step = eng.step(t)
+    step_next = eng.step(nxt)
+    eng.close()
+    orc = oracle_decoder(dims, w, 64)
+    for pos, t in enumerate(toks):
+        r = orc.step(t, pos)
+    assert normwise(pre, r) <= 2e-2, normwise(pre, r)
+    for a, b in ((pre, step), (pre_next, step_next)):
+        assert cosine(a, b) > 0.9999, cosine(a, b)
+        if int(np.argmax(a)) != int(np.argmax(b)):
+            top2 = np.sort(b.astype(np.float64))[-2:]
+            assert top2[1] - top2[0] <= np.abs(a.astype(np.float64) - b).max()
+
+
+def test_prefill_smollm2_135m_prompt():
+    """Config 5's 128-token prompt through bm_forward (one pass) against 128
+    decode steps: the reference's prefill_test.c criteria at full size."""
+    dims = bmhip.SMOLLM2_135M
+    toks = bmhip.synth_uniform_int(2025, 0, dims["V"], 128)
+    eng = bmhip.Engine(dims, max_seq_len=160, seed=2025)
+    pre = eng.forward(toks)
+    pre_next = eng.step(7)
+    eng.reset()
+    for t in toks:
+        step = eng.step(int(t))
+    step_next = eng.step(7)
+    eng.close()
+    for a, b in ((pre, step), (pre_next, step_next)):
+        assert cosine(a, b) > 0.9999, cosine(a, b)
+        if int(np.argmax(a)) != int(np.argmax(b)):
+            top2 = np.sort(b.astype(np.float64))[-2:]
+            assert top2[1] - top2[0] <= np.abs(a.astype(np.float64) - b).max()
+
+
 def test_engine_synthetic_init_equals_host_weights():
     """bm_model_init_synthetic builds exactly the weights bmhip.synthetic_weights does."""
     a = bmhip.Engine(SMALL, max_seq_len=16, seed=77)
