@@ -10,9 +10,19 @@
 
 namespace {
 
+/* 4 x 16 bytes per lane per step: four loads in flight before the stores */
 __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, long n16) {
-    const long stride = (long)gridDim.x * 256;
-    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+    const long stride = (long)gridDim.x * 256 * 4;
+    long i = (long)blockIdx.x * 256 * 4 + threadIdx.x;
+    for (; i + 3 * 256 < n16; i += stride) {
+        const uint4 a = src[i], b = src[i + 256], c = src[i + 512], d = src[i + 768];
+        dst[i] = a;
+        dst[i + 256] = b;
+        dst[i + 512] = c;
+        dst[i + 768] = d;
+    }
+    for (int u = 0; u < 4; u++, i += 256)
+        if (i < n16) dst[i] = src[i];
 }
 
 __global__ __launch_bounds__(256) void k_copy1(const unsigned char* __restrict__ src, unsigned char* __restrict__ dst,
@@ -36,8 +46,8 @@ extern "C" int bmk_launch_copy_buffer(const bmk_launch_t* a) {
     unsigned char* d = (unsigned char*)a->dev[1];
     const long n16 = ((((uintptr_t)s | (uintptr_t)d) & 15) == 0) ? nb / 16 : 0;
     if (n16 > 0) {
-        long blocks = (n16 + 255) / 256;
-        if (blocks > 256 * 16) blocks = 256 * 16; /* 16 workgroups per CU, grid-stride beyond */
+        long blocks = (n16 + 1023) / 1024;
+        if (blocks > 256 * 8) blocks = 256 * 8; /* 8 workgroups per CU, grid-stride beyond */
         hipLaunchKernelGGL(k_copy16, dim3((unsigned)blocks), dim3(256), 0, a->stream, (const uint4*)s, (uint4*)d, n16);
         BMK_LAUNCH_CHECK();
     }

@@ -253,7 +253,7 @@ def gemm_leg(steps: int, warmup: int):
     }
 
 
-def copy_ceiling(mib: int = 1024, reps: int = 5):
+def copy_ceiling(mib: int = 2048, reps: int = 5):
     """copy_buffer over `mib` MiB (read + write), HIP events: the stream-copy
     ceiling reported beside the matvec's bandwidth."""
     be = bmhip.Backend()
