@@ -78,6 +78,32 @@ def test_matmul_small_batch(be, BT):
     assert normwise(y, r) <= RTOL
 
 
+@pytest.mark.parametrize("OC,C", [(960, 960), (320, 960), (2560, 960), (960, 2560), (49152, 960)])
+def test_matmul_batch8_360m_shapes(be, OC, C):
+    """SmolLM2-360M projections and LM head at BT = 8 (batched decode kernel)."""
+    BT = 8
+    w = po.quantize_q8(bmhip.synth_normal(bmhip.synth_seed(23, 1, OC, C), 0.02, OC * C))
+    x = bmhip.synth_normal(bmhip.synth_seed(23, 2, OC, C), 1.0, BT * C)
+    y = run_mv(be, w, x, BT, C, OC, kernel="matmul_forward_q8")
+    r = po.q8_matvec_f64(w, x, BT, C, OC)
+    assert normwise(y, r) <= RTOL, normwise(y, r)
+    # each row of the batch must equal the B = 1 result for that row to the same bar
+    y1 = run_mv(be, w, x[3 * C:4 * C], 1, C, OC)
+    assert normwise(y[3 * OC:4 * OC], r[3 * OC:4 * OC]) <= RTOL
+    assert normwise(y1, r[3 * OC:4 * OC]) <= RTOL
+
+
+def test_matmul_small_batch_bias(be):
+    """BT in [2, 16) with a bias (served by the per-row matvec kernel, not the batched MFMA one)."""
+    OC, C, BT = 320, 960, 5
+    w = po.quantize_q8(bmhip.synth_normal(24, 0.02, OC * C))
+    x = bmhip.synth_normal(25, 1.0, BT * C)
+    b = bmhip.synth_normal(26, 1.0, OC)
+    y = run_mv(be, w, x, BT, C, OC, kernel="matmul_forward_q8", bias=b)
+    r = po.q8_matvec_f64(w, x, BT, C, OC) + np.tile(b, BT)
+    assert normwise(y, r) <= RTOL
+
+
 def test_matvec_rejects_short_buffers(be):
     OC, C = 64, 576
     w = po.quantize_q8(bmhip.synth_normal(31, 0.02, OC * C))
