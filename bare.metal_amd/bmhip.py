@@ -87,6 +87,7 @@ def lib() -> C.CDLL:
         "bm_get_arch_name": (C.c_char_p, [vp]),
         "bm_model_set_quant_bits": (i, [vp, i]),
         "bm_model_set_q8_head": (i, [vp, i]),
+        "bm_model_set_precision": (i, [vp, i]),
         "bm_model_set_tensor": (i, [vp, C.c_char_p, vp, sz]),
         "bm_model_init_synthetic": (i, [vp, u64]),
         "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
@@ -336,6 +337,7 @@ class Arch(C.Structure):
 
 
 BM_DEVICE_HIP = 1
+PRECISIONS = {"fp32": 0, "fp16": 1, "bf16": 2}  # bm_precision_t
 SMOLLM2_135M = dict(D=576, H=1536, NH=9, NKV=3, HD=64, L=30, V=49152)
 SMOLLM2_360M = dict(D=960, H=2560, NH=15, NKV=5, HD=64, L=32, V=49152)
 TENSOR_IDS = {"token_embedding": 0, "wq": 1, "wk": 2, "wv": 3, "wo": 4, "w_gate": 5, "w_up": 6, "w_down": 7}
@@ -372,7 +374,7 @@ class Engine:
     """A context + model + session of the decode engine."""
 
     def __init__(self, dims: dict, max_seq_len: int = 512, batch: int = 1, seed=None, weights=None,
-                 q8_head: bool = False, graph: bool = True):
+                 q8_head: bool = False, graph: bool = True, precision: str = "fp32"):
         L = lib()
         self.dims = dict(dims)
         self.V = dims["V"]
@@ -382,6 +384,7 @@ class Engine:
             raise BackendError("bm_create failed (no HIP device?)")
         self.arch = llama_arch(**{k: dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V")},
                                max_seq_len=max_seq_len, theta=dims.get("theta", 10000.0))
+        self.arch.precision = PRECISIONS[precision]
         self.model = L.bm_create_model(self.ctx, C.byref(self.arch))
         if not self.model:
             raise BackendError("bm_create_model rejected the architecture")

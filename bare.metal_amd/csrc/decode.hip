@@ -271,6 +271,8 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
  * fp32 rows: a lane owns 16 consecutive columns (4 dwordx4 loads per row),
  * D/16 lanes cover a row, 256/(D/16) rows per pass, HEAD_U passes in flight.
  * Q8 rows: a lane owns one 32-column block, as in the Q8 matvec.
+ * bf16 rows: a lane owns 32 consecutive columns (4 dwordx4 loads per row),
+ * each weight widened to fp32 exactly (bits << 16).
  * With st != NULL the workgroup's best (logit, index) goes into st->key[b]
  * by atomicMax, and the last workgroup to finish turns the keys into
  * tokens, emits them and advances the position. */
@@ -305,10 +307,17 @@ __device__ void head_finish(const DecHead& a, int& last_wg) {
     }
 }
 
-template <bool Q8>
-__device__ __forceinline__ int head_lanes(int D) { return Q8 ? D / 32 : D / 16; }
+/* Weight formats of the LM head rows. */
+enum { HW_F32 = 0, HW_Q8 = 1, HW_BF16 = 2 };
 
-template <bool Q8>
+template <int WF>
+__device__ __forceinline__ int head_lanes(int D) { return WF == HW_F32 ? D / 16 : D / 32; }
+
+/* the two bf16 values of a dword, widened exactly to fp32 */
+__device__ __forceinline__ float bf16_lo(unsigned int u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(unsigned int u) { return __uint_as_float(u & 0xffff0000u); }
+
+template <int WF>
 __global__ __launch_bounds__(NT) void k_head(DecHead a) {
     __shared__ float red[NT * HEAD_U];
     __shared__ float sh[4];
@@ -316,27 +325,30 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
     __shared__ int last_wg;
     const int t = threadIdx.x;
     const int D = a.D;
-    const int nseg = head_lanes<Q8>(D);
+    const int nseg = head_lanes<WF>(D);
     const int slots = NT / nseg;
     const int rows_per_tile = slots * HEAD_U;
     const int slot = t / nseg, sg = t - slot * nseg;
     const bool lane_on = slot < slots;
     const long row0 = (long)blockIdx.x * rows_per_tile;
 
-    /* issue this tile's weight loads first; they do not depend on x */
+    /* issue this tile's weight loads first; they do not depend on x.
+     * fp32 and bf16 rows both hold 16 dwords per lane and row in wf */
     float wf[HEAD_U][16];
     Blk wb[HEAD_U];
 #pragma unroll
     for (int u = 0; u < HEAD_U; u++) {
         const long r = row0 + slot + (long)u * slots;
         const bool ok = lane_on && r < a.V;
-        if (Q8) {
+        if (WF == HW_Q8) {
             wb[u] = ok ? load_block(a.wq + ((size_t)r * nseg + sg) * 36) : zero_block();
         } else {
+            const float* src = WF == HW_F32 ? a.w + (size_t)r * D + 16 * sg
+                                            : (const float*)(a.wh + (size_t)r * D + 32 * sg);
 #pragma unroll
             for (int i = 0; i < 16; i += 4) {
                 float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (ok) __builtin_memcpy(&v4, __builtin_assume_aligned(a.w + (size_t)r * D + 16 * sg + i, 4), 16);
+                if (ok) __builtin_memcpy(&v4, __builtin_assume_aligned(src + i, 4), 16);
                 wf[u][i] = v4.x; wf[u][i + 1] = v4.y; wf[u][i + 2] = v4.z; wf[u][i + 3] = v4.w;
             }
         }
@@ -344,7 +356,7 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
 
     for (int b = 0; b < a.B; b++) {
         const float* xb = a.x + (size_t)b * D;
-        constexpr int SEG = Q8 ? 32 : 16;
+        constexpr int SEG = WF == HW_F32 ? 16 : 32;
         float xs[SEG], nw[SEG];
         if (lane_on) {
 #pragma unroll
@@ -372,9 +384,9 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
 #pragma unroll
         for (int u = 0; u < HEAD_U; u++) {
             float p;
-            if (Q8) {
+            if (WF == HW_Q8) {
                 p = block_dot(wb[u], xs);
-            } else {
+            } else if (WF == HW_F32) {
                 float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
                 for (int i = 0; i < 16; i += 4) {
@@ -382,6 +394,17 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
                     p1 = fmaf(xs[i + 1], wf[u][i + 1], p1);
                     p2 = fmaf(xs[i + 2], wf[u][i + 2], p2);
                     p3 = fmaf(xs[i + 3], wf[u][i + 3], p3);
+                }
+                p = (p0 + p1) + (p2 + p3);
+            } else {
+                float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i += 2) {
+                    const unsigned int w0 = __float_as_uint(wf[u][i]), w1 = __float_as_uint(wf[u][i + 1]);
+                    p0 = fmaf(xs[2 * i], bf16_lo(w0), p0);
+                    p1 = fmaf(xs[2 * i + 1], bf16_hi(w0), p1);
+                    p2 = fmaf(xs[2 * i + 2], bf16_lo(w1), p2);
+                    p3 = fmaf(xs[2 * i + 3], bf16_hi(w1), p3);
                 }
                 p = (p0 + p1) + (p2 + p3);
             }
@@ -419,7 +442,7 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
  * maxima: across the 16 columns of a wave by shuffles, across waves through
  * LDS, then one atomicMax per batch row; the last workgroup emits the
  * tokens (head_finish). */
-template <int NBT, bool Q8>
+template <int NBT, int WF>
 __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
     __shared__ unsigned long long shk[4][16 * NBT];
     __shared__ int last_wg;
@@ -446,7 +469,7 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
     };
     auto load = [&](int kb, Ops& o) {
         o.s = 1.0f;
-        if (Q8) {
+        if (WF == HW_Q8) {
             const unsigned char* blk = a.wq + ((size_t)rc * nkb + kb) * 36;
             unsigned int q0, q1;
             __builtin_memcpy(&o.s, __builtin_assume_aligned(blk, 4), 4);
@@ -457,10 +480,17 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
                 o.wv[i] = q8_byte(q0, i);
                 o.wv[4 + i] = q8_byte(q1, i);
             }
-        } else {
+        } else if (WF == HW_F32) {
             const float* wp = a.w + (size_t)rc * D + 32 * kb + 8 * g;
             __builtin_memcpy(&o.wv[0], __builtin_assume_aligned(wp, 4), 16);
             __builtin_memcpy(&o.wv[4], __builtin_assume_aligned(wp + 4, 4), 16);
+        } else {
+            uint4 h4;
+            __builtin_memcpy(&h4, __builtin_assume_aligned(a.wh + (size_t)rc * D + 32 * kb + 8 * g, 4), 16);
+            o.wv[0] = bf16_lo(h4.x); o.wv[1] = bf16_hi(h4.x);
+            o.wv[2] = bf16_lo(h4.y); o.wv[3] = bf16_hi(h4.y);
+            o.wv[4] = bf16_lo(h4.z); o.wv[5] = bf16_hi(h4.z);
+            o.wv[6] = bf16_lo(h4.w); o.wv[7] = bf16_hi(h4.w);
         }
         __builtin_memcpy(&o.gv[0], __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
         __builtin_memcpy(&o.gv[4], __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
@@ -482,7 +512,7 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
                 ss[bt] = fmaf(cur.xv[bt][i], cur.xv[bt][i], ss[bt]);
                 xv[i] = cur.xv[bt][i] * cur.gv[i];
             }
-            if (Q8) {
+            if (WF == HW_Q8) {
                 bmv_f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int i = 0; i < 8; i++) d = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], cur.wv[i], d, 0, 0, 0);
@@ -1376,44 +1406,56 @@ extern "C" int bmk_launch_swiglu(const bmk_launch_t* a) {
     return 0;
 }
 
-static int head_tiles(int D, int V, bool q8) {
-    const int nseg = q8 ? D / 32 : D / 16;
+static int head_tiles(int D, int V, int wf) {
+    const int nseg = wf == HW_F32 ? D / 16 : D / 32;
     const int rows = (NT / nseg) * HEAD_U;
     return (V + rows - 1) / rows;
 }
 
-static bool head_shape_ok(int D, bool q8) {
-    return q8 ? (D % 32 == 0 && D / 32 <= NT) : (D % 16 == 0 && D / 16 <= NT);
+static bool head_shape_ok(int D, int wf) {
+    return wf == HW_F32 ? (D % 16 == 0 && D / 16 <= NT) : (D % 32 == 0 && D / 32 <= NT);
 }
 
-/* rmsnorm_matmul_forward {x [C], norm weight [C], wcls f32 [V][C], logits [V], params int{C, V}, eps float} */
-extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) {
+/* rmsnorm_matmul_forward (fp32 wcls) and rmsnorm_matmul_forward_bf16_vec
+ * (bf16 wcls): {x [C], norm weight [C], wcls [V][C], logits [V],
+ * params int{C, V}, eps float} (reference forward.metal:1532-1581,
+ * 1636-1689; scheduler.c:931-940).  The grid the caller passes is not used:
+ * the launch covers V rows by itself. */
+static int launch_rmsnorm_matmul(const bmk_launch_t* a, int wf) {
+    const char* name = wf == HW_F32 ? "rmsnorm_matmul" : "rmsnorm_matmul_bf16";
+    const size_t esz = wf == HW_F32 ? 4 : 2;
     BMK_NEED_BYTES(a, 4, 8, "params");
     BMK_NEED_BYTES(a, 5, 4, "eps");
     const int C = bmk_pi(a, 4, 0), V = bmk_pi(a, 4, 1);
-    BMK_REQUIRE(C > 0 && V >= 0 && head_shape_ok(C, false), "rmsnorm_matmul: C=%d must be a multiple of 16 up to 4096", C);
+    BMK_REQUIRE(C > 0 && V >= 0 && head_shape_ok(C, wf), "%s: C=%d must be a multiple of %d up to %d", name, C,
+                wf == HW_F32 ? 16 : 32, wf == HW_F32 ? 4096 : 8192);
     if (V == 0) return 0;
     BMK_NEED_BYTES(a, 0, (size_t)C * 4, "x");
     BMK_NEED_BYTES(a, 1, (size_t)C * 4, "norm weight");
-    BMK_NEED_BYTES(a, 2, (size_t)V * C * 4, "wcls");
+    BMK_NEED_BYTES(a, 2, (size_t)V * C * esz, "wcls");
     BMK_NEED_BYTES(a, 3, (size_t)V * 4, "logits");
     BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1] | (uintptr_t)a->dev[2]) & 3) == 0,
-                "rmsnorm_matmul: misaligned operand");
+                "%s: misaligned operand", name);
     DecHead h;
     memset(&h, 0, sizeof h);
     h.x = (const float*)a->dev[0];
     h.norm_w = (const float*)a->dev[1];
-    h.w = (const float*)a->dev[2];
+    if (wf == HW_F32) h.w = (const float*)a->dev[2];
+    else h.wh = (const unsigned short*)a->dev[2];
     h.logits = (float*)a->dev[3];
     h.D = C;
     h.V = V;
     h.B = 1;
     h.eps = bmk_pf(a, 5, 0);
-    h.tiles = head_tiles(C, V, false);
-    hipLaunchKernelGGL(k_head<false>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    h.tiles = head_tiles(C, V, wf);
+    if (wf == HW_F32) hipLaunchKernelGGL(k_head<HW_F32>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    else hipLaunchKernelGGL(k_head<HW_BF16>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
     BMK_LAUNCH_CHECK();
     return 0;
 }
+
+extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_F32); }
+extern "C" int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_BF16); }
 
 /* argmax_f32 {values f32 [n], out int [1], params int{n}} */
 extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {
@@ -1452,7 +1494,8 @@ extern "C" int dec_mv_tiles(int OC, int C, int glu) {
     return (int)((n + slots - 1) / slots);
 }
 
-extern "C" int dec_head_tiles(int D, int V, int q8) { return head_tiles(D, V, q8 != 0); }
+/* wf: 0 fp32 rows, 1 Q8 rows, 2 bf16 rows */
+extern "C" int dec_head_tiles(int D, int V, int wf) { return head_tiles(D, V, wf); }
 
 extern "C" int dec_launch_embed(const DecEmbed* a, hipStream_t s) {
     if (a->B < 1 || a->B > DEC_MAX_B) return -1;
@@ -1523,11 +1566,12 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
         if (a.B > DEC_MAX_B || a.D % 32) return -1;
         a.tiles = (a.V + 63) / 64;
         const dim3 grid(a.tiles);
-        const bool q8 = a.wq != nullptr;
-#define HEAD_B(NBT)                                                                \
-        do {                                                                       \
-            if (q8) hipLaunchKernelGGL((k_head_b<NBT, true>), grid, dim3(NT), 0, s, a); \
-            else hipLaunchKernelGGL((k_head_b<NBT, false>), grid, dim3(NT), 0, s, a);   \
+        const int wf = a.wq ? HW_Q8 : (a.wh ? HW_BF16 : HW_F32);
+#define HEAD_B(NBT)                                                                          \
+        do {                                                                                 \
+            if (wf == HW_Q8) hipLaunchKernelGGL((k_head_b<NBT, HW_Q8>), grid, dim3(NT), 0, s, a);  \
+            else if (wf == HW_BF16) hipLaunchKernelGGL((k_head_b<NBT, HW_BF16>), grid, dim3(NT), 0, s, a); \
+            else hipLaunchKernelGGL((k_head_b<NBT, HW_F32>), grid, dim3(NT), 0, s, a);        \
         } while (0)
         if (a.B <= 16) HEAD_B(1);
         else if (a.B <= 32) HEAD_B(2);
@@ -1539,9 +1583,11 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
     }
     const DecHead* a = a_in;
     if (a->wq)
-        hipLaunchKernelGGL(k_head<true>, dim3(a->tiles), dim3(NT), 0, s, *a);
+        hipLaunchKernelGGL(k_head<HW_Q8>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    else if (a->wh)
+        hipLaunchKernelGGL(k_head<HW_BF16>, dim3(a->tiles), dim3(NT), 0, s, *a);
     else
-        hipLaunchKernelGGL(k_head<false>, dim3(a->tiles), dim3(NT), 0, s, *a);
+        hipLaunchKernelGGL(k_head<HW_F32>, dim3(a->tiles), dim3(NT), 0, s, *a);
     BMK_LAUNCH_CHECK();
     return 0;
 }

@@ -82,12 +82,14 @@ typedef struct {
     int NH, NKV, HD, KV, MS, L, layer;
 } DecAttn;
 
-/* Final RMSNorm + LM head (fp32 rows, or Q8 rows when wq != NULL) + argmax. */
+/* Final RMSNorm + LM head + argmax.  Rows: Q8 when wq != NULL, else bf16
+ * when wh != NULL, else fp32. */
 typedef struct {
     const float* x;      /* [B][D] */
     const float* norm_w;
     const float* w;      /* fp32 [V][D] */
     const unsigned char* wq; /* Q8 [V][D/32] blocks, or NULL */
+    const unsigned short* wh; /* bf16 [V][D], or NULL */
     float* logits;       /* [B][V] */
     DecState* st;
     int* out_tokens;     /* [n_gen][B] (generation mode) */

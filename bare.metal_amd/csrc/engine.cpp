@@ -39,7 +39,7 @@
 
 extern "C" {
 int dec_mv_tiles(int OC, int C, int glu);
-int dec_head_tiles(int D, int V, int q8);
+int dec_head_tiles(int D, int V, int wf);
 int dec_launch_embed(const DecEmbed* a, hipStream_t s);
 int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
@@ -79,6 +79,7 @@ struct bm_model_s {
     int D, H, NH, NKV, HD, KV, QD, L, V;
     int quant_bits;
     int q8_head;
+    bm_precision_t precision; /* BF16: bf16 LM head rows, FP32: fp32 rows */
     float* host[T_COUNT];   /* fp32 weights in the reference layout */
     size_t count[T_COUNT];
     int set[T_COUNT];
@@ -90,6 +91,7 @@ struct bm_model_s {
     float* d_lnf;
     unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down */
     unsigned char* d_head8;  /* Q8 head rows (q8_head) */
+    unsigned short* d_headh; /* bf16 head rows (precision BF16, no q8_head) */
     size_t off[7];           /* byte offset of each matrix inside one layer's slice */
     size_t layer_bytes;
     int nsessions;
@@ -180,6 +182,10 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
         BMK_ERR("bm_create_model: only RMSNorm + SwiGLU + RoPE + tied-embedding models without biases are supported");
         return NULL;
     }
+    if (a->precision != BM_PRECISION_FP32 && a->precision != BM_PRECISION_BF16) {
+        BMK_ERR("bm_create_model: precision %d: the LM head runs in fp32 or bf16", (int)a->precision);
+        return NULL;
+    }
     const int QD = NH * HD, KV = NKV * HD;
     /* layout constraints of the gfx950 kernels (decode.hip) */
     if (D % 32 || H % 32 || QD % 32 || D / 32 > 256 || H / 32 > 256 || QD / 32 > 256 || D % 16 || D / 16 > 256 ||
@@ -194,6 +200,7 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
     m->arch = *a;
     m->D = D; m->H = H; m->NH = NH; m->NKV = NKV; m->HD = HD; m->KV = KV; m->QD = QD; m->L = L; m->V = V;
     m->quant_bits = 8;
+    m->precision = a->precision;
     const size_t cnt[T_COUNT] = {(size_t)V * D, (size_t)L * D, (size_t)L * D, (size_t)D, (size_t)L * QD * D,
                                  (size_t)L * KV * D, (size_t)L * KV * D, (size_t)L * D * QD, (size_t)L * H * D,
                                  (size_t)L * H * D, (size_t)L * D * H};
@@ -216,6 +223,8 @@ static void model_free_device(bm_model_t* m) {
     hipFree(m->d_lnf);
     hipFree(m->d_q8);
     hipFree(m->d_head8);
+    hipFree(m->d_headh);
+    m->d_headh = NULL;
     m->d_emb = m->d_ln1 = m->d_ln2 = m->d_lnf = NULL;
     m->d_q8 = m->d_head8 = NULL;
     m->compiled = 0;
@@ -236,6 +245,20 @@ extern "C" int bm_model_set_quant_bits(bm_model_t* m, int bits) {
         return -1;
     }
     m->quant_bits = 8;
+    return 0;
+}
+
+/* Head rows in use: 1 Q8, 2 bf16, 0 fp32 (decode.hip's head formats). */
+static int head_format(const bm_model_t* m) { return m->q8_head ? 1 : (m->precision == BM_PRECISION_BF16 ? 2 : 0); }
+
+extern "C" int bm_model_set_precision(bm_model_t* m, bm_precision_t p) {
+    if (!m) return -1;
+    if (p != BM_PRECISION_FP32 && p != BM_PRECISION_BF16) {
+        BMK_ERR("bm_model_set_precision: the MI355X path runs the LM head in fp32 or bf16 (got %d)", (int)p);
+        return -1;
+    }
+    if (m->compiled && p != m->precision) model_free_device(m);
+    m->precision = p;
     return 0;
 }
 
@@ -328,6 +351,11 @@ static int model_compile(bm_model_t* m) {
     if (rc == 0 && m->q8_head) {
         if (hipMalloc(&m->d_head8, q8_bytes((size_t)m->V * D)) != hipSuccess) rc = -1;
         else rc = q8_pack_f32(m->d_emb, m->d_head8, (long)m->V * D, s);
+    } else if (rc == 0 && head_format(m) == 2) {
+        /* bf16 rows of the tied embedding, rounded to nearest even as the
+         * reference's bf16 upload does (scheduler.c:369-371,395-402) */
+        if (hipMalloc(&m->d_headh, (size_t)m->V * D * 2) != hipSuccess) rc = -1;
+        else rc = gm_cast_bf16(m->d_emb, m->d_headh, (long)m->V * D, s);
     }
     if (hipStreamSynchronize(s) != hipSuccess) rc = -1;
     hipFree(stage);
@@ -429,9 +457,10 @@ static int enqueue_step(bm_session_t* S) {
     DecHead hd;
     memset(&hd, 0, sizeof hd);
     hd.x = S->x; hd.norm_w = m->d_lnf; hd.w = m->d_emb; hd.wq = m->q8_head ? m->d_head8 : NULL;
+    hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
     hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
-    hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
+    hd.tiles = dec_head_tiles(D, m->V, head_format(m));
     if (dec_launch_head(&hd, s) || mark(S, PH_HEAD)) return -1;
     return 0;
 }
@@ -788,9 +817,10 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     memset(&hd, 0, sizeof hd);
     hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_emb;
     hd.wq = m->q8_head ? m->d_head8 : NULL;
+    hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
     hd.logits = S->logits; hd.st = NULL; hd.out_tokens = NULL;
     hd.D = D; hd.V = m->V; hd.B = 1; hd.eps = eps;
-    hd.tiles = dec_head_tiles(D, m->V, m->q8_head);
+    hd.tiles = dec_head_tiles(D, m->V, head_format(m));
     if (dec_launch_head(&hd, s)) return -1;
     /* the decode steps continue at position n */
     memset(S->h_st, 0, sizeof(DecState));

@@ -25,6 +25,7 @@ int bmk_launch_attention(const bmk_launch_t* a);
 int bmk_launch_add(const bmk_launch_t* a);
 int bmk_launch_swiglu(const bmk_launch_t* a);
 int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a);
+int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a);
 int bmk_launch_argmax(const bmk_launch_t* a);
 }
 
@@ -65,6 +66,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"swiglu_forward", 4, B(3), B(2), bmk_launch_swiglu, 0},
     /* reference forward.metal:1636-1689; {x, norm weight, wcls f32, logits, params{C,V}, eps} */
     {"rmsnorm_matmul_forward", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul, 0},
+    /* reference forward.metal:1532-1581 (the LM head at default bf16 precision,
+     * scheduler.c:776-778); {x, norm weight, wcls bf16, logits, params{C,V}, eps} */
+    {"rmsnorm_matmul_forward_bf16_vec", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_bf16, 0},
     /* new: greedy pick on the device (reference tools/run.c:56-60); {values, out int, params{n}} */
     {"argmax_f32", 3, B(2), B(1), bmk_launch_argmax, 0},
     {nullptr, 0, 0, 0, nullptr, 0},

@@ -15,14 +15,19 @@
  *   - BM_DEVICE_METAL selects "the GPU", here the HIP device; BM_DEVICE_HIP
  *     is the same value.  BM_DEVICE_CPU has no backend, as in the reference
  *     (reference src/baremetal/context.c:16-22), and bm_create returns NULL.
- *   - Projections run only in Q8 (quant_bits 8); the LM head runs in fp32
- *     over the tied embedding (the reference's Q8 mode, reference
- *     src/baremetal/graph.c:228-238) or, on request, in Q8.
+ *   - Projections run only in Q8 (quant_bits 8).  The LM head runs over the
+ *     tied embedding in the model's precision, as the reference's Q8 mode
+ *     does (reference src/baremetal/graph.c:228-238, scheduler.c:369-371,
+ *     776-778): fp32 rows (BM_PRECISION_FP32) or bf16 rows rounded to
+ *     nearest even (BM_PRECISION_BF16, what bm_get_supported_precision
+ *     returns); or, on request, Q8 rows.  BM_PRECISION_FP16 is rejected.
  *   - Weights come from bm_model_set_tensor or bm_model_init_synthetic;
  *     checkpoint files are not read.
- *   - bm_forward steps prompt tokens one at a time (the reference's
- *     bm_forward prefills with an S-sized graph when pos == 0; the logits it
- *     returns are those of the last token either way).
+ *   - bm_forward over several tokens at position 0 of a batch-1 session
+ *     runs the whole prompt in one pass, as the reference's prefill does
+ *     (reference src/baremetal/session.c:86-149); elsewhere it steps the
+ *     tokens one at a time.  The logits it returns are those of the last
+ *     token either way.
  */
 #ifndef BAREMETAL_H
 #define BAREMETAL_H
@@ -143,8 +148,12 @@ const char*    bm_get_arch_name(const bm_model_t* model);
  * (the reference's CLI sets model->quant_bits, reference tools/cli.c:886). */
 int            bm_model_set_quant_bits(bm_model_t* model, int bits);
 /* 1: the LM head runs on Q8 rows quantized from the tied embedding;
- * 0 (default): fp32 rows, as the reference. */
+ * 0 (default): rows in the model's precision, as the reference. */
 int            bm_model_set_q8_head(bm_model_t* model, int on);
+/* The reference's CLI writes model->precision after loading (reference
+ * tools/cli.c:519-524); bm_model_t is opaque here, so this sets it.
+ * BM_PRECISION_FP32 or BM_PRECISION_BF16; returns 0, or -1. */
+int            bm_model_set_precision(bm_model_t* model, bm_precision_t precision);
 
 /* Host fp32 weights in the reference's layout (reference
  * src/baremetal/model.c:125-172: one array per matrix type, layers back to

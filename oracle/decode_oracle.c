@@ -207,7 +207,7 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
         for (int r = 0; r < V; r++) logits[r] = (double)tmp[r];
         free(tmp);
     } else {
-        f32_mv(m->emb, d->xn, logits, D, V, nt);
+        f32_mv(m->head_f32 ? m->head_f32 : m->emb, d->xn, logits, D, V, nt);
     }
     return 0;
 }

@@ -26,6 +26,8 @@ typedef struct {
     const uint8_t* wu;       /* [L][H][D/32] */
     const uint8_t* wd;       /* [L][D][H/32] */
     const uint8_t* head_q8;  /* NULL: fp32 tied head (the reference's Q8 mode) */
+    const float* head_f32;   /* fp32 head rows [V][D] when head_q8 is NULL; NULL: emb.  The
+                                reference's bf16 head is emb rounded to bf16 and widened back */
 } orc_model_t;
 
 typedef struct orc_decoder_s orc_decoder_t;

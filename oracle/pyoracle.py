@@ -151,7 +151,8 @@ def cpu_q8_matvec_multi(w, x, y, w_off, x_off, y_off, OC, C_, nthreads: int) -> 
 class OrcModel(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("D", "H", "NH", "NKV", "HD", "L", "V", "MS")] + [
         ("theta", C.c_float), ("eps", C.c_float),
-    ] + [(n, C.c_void_p) for n in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8")]
+    ] + [(n, C.c_void_p) for n in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8",
+                                   "head_f32")]
 
 
 class Decoder:
@@ -164,7 +165,7 @@ class Decoder:
             setattr(m, k, int(dims[k]))
         m.theta = float(dims.get("theta", 10000.0))
         m.eps = float(dims.get("eps", 1e-5))
-        for k in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8"):
+        for k in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8", "head_f32"):
             a = arrays.get(k)
             setattr(m, k, a.ctypes.data if a is not None else None)
         self._m = m

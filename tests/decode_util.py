@@ -19,10 +19,15 @@ def q8_arrays(w: dict) -> dict:
     return out
 
 
-def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads: int = 8) -> po.Decoder:
+def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads: int = 8,
+                   precision: str = "fp32") -> po.Decoder:
+    """precision "bf16": the head rows are the tied embedding rounded to bf16
+    (reference scheduler.c:395-402), widened back to fp32 exactly."""
     arrs = q8_arrays(w)
     if q8_head:
         arrs["head_q8"] = po.quantize_q8(w["token_embedding"])
+    elif precision == "bf16":
+        arrs["head_f32"] = po.bf16_rne(w["token_embedding"])
     d = dict(dims)
     d["MS"] = ms
     return po.Decoder(d, arrs, nthreads=nthreads)

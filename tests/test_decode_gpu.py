@@ -30,14 +30,17 @@ LOGIT_TOL = 1e-4
 class RefOrderDecoder:
     """The reference scheduler's decode step, node by node, on the named kernels."""
 
-    def __init__(self, be, dims, w, MS):
+    def __init__(self, be, dims, w, MS, precision="fp32"):
         self.be, self.d, self.MS = be, dims, MS
+        self.precision = precision
         D, H, NH, NKV, HD, L, V = (dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V"))
         QD, KV = NH * HD, NKV * HD
         self.QD, self.KV = QD, KV
         self.emb = w["token_embedding"].reshape(V, D)
         self.ln1, self.ln2 = be.upload(w["ln1"]), be.upload(w["ln2"])
         self.lnf, self.wcls = be.upload(w["lnf"]), be.upload(w["token_embedding"])
+        if precision == "bf16":  # the reference uploads wcls as bf16 (scheduler.c:395-402)
+            self.wcls = be.upload((po.bf16_rne(w["token_embedding"]).view(np.uint32) >> 16).astype(np.uint16))
         self.Q = {}
         for name in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
             src = w[name]
@@ -92,17 +95,23 @@ class RefOrderDecoder:
             assert enc.dispatch(K("swiglu_forward"), [self.g, self.u, self.g, P(H)], (H,), (256,)) == 0
             self.mv(enc, self.g, "w_down", l, self.dn, H, D)
             assert enc.dispatch(K("add_forward"), [self.x, self.dn, self.x, P(D)], (D,), (256,)) == 0
-        assert enc.dispatch(K("rmsnorm_matmul_forward"), [self.x, self.lnf, self.wcls, self.logits, P(D, V),
-                                                          self.eps], ((V + 255) & ~255,), (256,)) == 0
+        if self.precision == "bf16":  # reference scheduler.c:776-778, geometry :969-972
+            assert enc.dispatch(K("rmsnorm_matmul_forward_bf16_vec"), [self.x, self.lnf, self.wcls, self.logits,
+                                                                       P(D, V), self.eps],
+                                ((V + 15) // 16 * 512,), (512,)) == 0
+        else:
+            assert enc.dispatch(K("rmsnorm_matmul_forward"), [self.x, self.lnf, self.wcls, self.logits, P(D, V),
+                                                              self.eps], ((V + 255) & ~255,), (256,)) == 0
         enc.wait_timed()
         return self.logits.read(np.float32)
 
 
-@pytest.mark.parametrize("dims", [TINY, SMALL], ids=["tiny", "small"])
-def test_reference_dispatch_order_matches_oracle(be, dims):
+@pytest.mark.parametrize("dims,precision", [(TINY, "fp32"), (SMALL, "fp32"), (SMALL, "bf16")],
+                         ids=["tiny", "small", "small-bf16head"])
+def test_reference_dispatch_order_matches_oracle(be, dims, precision):
     w = bmhip.synthetic_weights(dims, 11)
-    ref = RefOrderDecoder(be, dims, w, 32)
-    orc = oracle_decoder(dims, w, 32)
+    ref = RefOrderDecoder(be, dims, w, 32, precision)
+    orc = oracle_decoder(dims, w, 32, precision=precision)
     toks = bmhip.synth_uniform_int(5, 0, dims["V"], 12)
     for pos, t in enumerate(toks):
         y, r = ref.step(int(t), pos), orc.step(int(t), pos)
@@ -310,6 +319,46 @@ def test_q8_head_matches_oracle():
     errs, _ = teacher_forced_errors(eng, orc, bmhip.synth_uniform_int(3, 0, SMALL["V"], 8))
     eng.close()
     assert max(errs) <= LOGIT_TOL, errs
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_bf16_head_matches_oracle(batch):
+    """BM_PRECISION_BF16 (what bm_get_supported_precision returns): LM head on
+    bf16 rows of the tied embedding (reference scheduler.c:395-402,776-778)."""
+    w = bmhip.synthetic_weights(SMALL, 62)
+    eng = bmhip.Engine(SMALL, max_seq_len=16, weights=w, precision="bf16", batch=batch)
+    orc = oracle_decoder(SMALL, w, 16, precision="bf16")
+    orc32 = oracle_decoder(SMALL, w, 16)
+    toks = bmhip.synth_uniform_int(4, 0, SMALL["V"], 8)
+    if batch == 1:
+        errs, _ = teacher_forced_errors(eng, orc, toks)
+        assert max(errs) <= LOGIT_TOL, errs
+    else:
+        for pos, t in enumerate(toks):
+            y = eng.step_batch(np.full(batch, int(t), np.int32))
+            r = orc.step(int(t), pos)
+            r32 = orc32.step(int(t), pos)
+            for b in range(batch):
+                assert normwise(y[b], r) <= LOGIT_TOL, (pos, b)
+            # the bf16 rows change the logits by more than the tolerance: the test tells the heads apart
+            assert normwise(y[0], r32) > 3 * LOGIT_TOL
+    eng.close()
+
+
+def test_precision_fp16_rejected():
+    L = bmhip.lib()
+    ctx = L.bm_create(bmhip.BM_DEVICE_HIP)
+    a = bmhip.llama_arch(**{k: TINY[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V")}, max_seq_len=16)
+    a.precision = bmhip.PRECISIONS["fp16"]
+    import ctypes as C
+    assert not L.bm_create_model(ctx, C.byref(a))
+    a.precision = bmhip.PRECISIONS["bf16"]
+    m = L.bm_create_model(ctx, C.byref(a))
+    assert m
+    assert L.bm_model_set_precision(m, bmhip.PRECISIONS["fp16"]) == -1
+    assert L.bm_model_set_precision(m, bmhip.PRECISIONS["fp32"]) == 0
+    L.bm_destroy_model(m)
+    L.bm_destroy(ctx)
 
 
 def test_run_tokens_greedy_and_errors():

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import bmhip
+import pyoracle as po
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
@@ -158,6 +159,37 @@ def test_rmsnorm_matmul_forward(be, C, V):
     xd = x.astype(np.float64)
     xn = xd / np.sqrt((xd * xd).mean() + 1e-5) * g
     assert nw(out.read(np.float32), W.reshape(V, C).astype(np.float64) @ xn) <= TOL
+
+
+@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300), (32, 17)])
+def test_rmsnorm_matmul_forward_bf16_vec(be, C, V):
+    """bf16 head rows (reference forward.metal:1532-1581): each weight widened
+    exactly, fp32 products and sums; vs fp64 over the same bf16 values."""
+    rng = np.random.default_rng(C + 1)
+    x = rng.standard_normal(C).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, C).astype(np.float32)
+    Wr = po.bf16_rne((rng.standard_normal(V * C) * 0.02).astype(np.float32))  # bf16 values as fp32
+    bits = (Wr.view(np.uint32) >> 16).astype(np.uint16)
+    out = be.alloc(V * 4)
+    rc = be.dispatch("rmsnorm_matmul_forward_bf16_vec", [be.upload(x), be.upload(g), be.upload(bits), out,
+                                                         be.params(C, V), be.upload(f32(1e-5))],
+                     ((V + 15) // 16 * 512,), (512,))
+    assert rc == 0
+    xd = x.astype(np.float64)
+    xn = xd / np.sqrt((xd * xd).mean() + 1e-5) * g
+    assert nw(out.read(np.float32), Wr.reshape(V, C).astype(np.float64) @ xn) <= TOL
+
+
+def test_rmsnorm_matmul_forward_bf16_vec_rejects(be):
+    C, V = 48, 10  # C not a multiple of 32
+    out = be.alloc(V * 4)
+    bufs = [be.upload(np.ones(C, np.float32)), be.upload(np.ones(C, np.float32)),
+            be.upload(np.zeros(V * C, np.uint16)), out, be.params(C, V), be.upload(f32(1e-5))]
+    assert be.dispatch("rmsnorm_matmul_forward_bf16_vec", bufs, (512,), (512,)) == -1
+    C = 64  # wcls one row short
+    bufs = [be.upload(np.ones(C, np.float32)), be.upload(np.ones(C, np.float32)),
+            be.upload(np.zeros((V - 1) * C, np.uint16)), out, be.params(C, V), be.upload(f32(1e-5))]
+    assert be.dispatch("rmsnorm_matmul_forward_bf16_vec", bufs, (512,), (512,)) == -1
 
 
 def test_argmax_first_index(be):
