@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
         "bm_q8_mv_tiles": (i, [i, i]),
         "bm_q8_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
+        "bm_q4_mv_tiles": (i, [i, i]),
+        "bm_q4_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_q8_gemm_tiles": (i, [i, i, i]),
         "bm_q8_gemm_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_create": (vp, [i]),
@@ -137,9 +139,11 @@ def synth_uniform_int(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
 
 # ---------------------------------------------------------------- Q8 multi-matvec plan
 
-def mv_plan(w_off, x_off, y_off, OC, C_):
+def mv_plan(w_off, x_off, y_off, OC, C_, fmt: str = "q8"):
     """Plan table (bytes) and workgroup count of a matmul_forward_q8_vec_multi
-    launch over the problems given by the five equal-length sequences."""
+    (fmt "q4": matmul_forward_q4_vec_multi) launch over the problems given by
+    the five equal-length sequences."""
+    planner = lib().bm_q4_mv_plan if fmt == "q4" else lib().bm_q8_mv_plan
     n = len(OC)
     w = np.ascontiguousarray(w_off, dtype=np.uint64)
     x = np.ascontiguousarray(x_off, dtype=np.uint64)
@@ -147,14 +151,13 @@ def mv_plan(w_off, x_off, y_off, OC, C_):
     oc = np.ascontiguousarray(OC, dtype=np.int32)
     c = np.ascontiguousarray(C_, dtype=np.int32)
     nt = C.c_int(0)
-    need = lib().bm_q8_mv_plan(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), None, 0, C.byref(nt))
+    need = planner(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), None, 0, C.byref(nt))
     if need < 0:
-        raise ValueError("bm_q8_mv_plan rejected the problem list")
+        raise ValueError("the matvec planner rejected the problem list")
     plan = np.zeros((need + 7) // 8, dtype=np.uint64)
-    got = lib().bm_q8_mv_plan(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), _ptr(plan), plan.nbytes,
-                              C.byref(nt))
+    got = planner(n, _ptr(w), _ptr(x), _ptr(y), _ptr(oc), _ptr(c), _ptr(plan), plan.nbytes, C.byref(nt))
     if got != need:
-        raise ValueError("bm_q8_mv_plan failed")
+        raise ValueError("the matvec planner failed")
     return plan.view(np.uint8)[:need].copy(), nt.value
 
 

@@ -613,10 +613,9 @@ __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
  * passes are loaded before any arithmetic.  Small WT and U give many
  * workgroups of few rows: decode matrices are small, and spreading one over
  * hundreds of CUs keeps each CU's share to a single memory round trip. */
-template <int WT, int U>
-__global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
-    __shared__ float red[WT * U];
-    __shared__ float sh[WT / 64];
+template <int WT, int U, int QF>
+__device__ __forceinline__ void dec_mv_body(const DecMv& a, float* red, float* sh) {
+    typedef QFmt<QF> F;
     const int t = threadIdx.x;
     int mi = 0;
     while (mi + 1 < a.nmat && (int)blockIdx.x >= a.tile0[mi + 1]) mi++;
@@ -627,21 +626,21 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
     const int slot = t / nb, bc = t - slot * nb;
     const bool lane_on = slot < slots;
     const long row0 = (long)tile * rows_per_tile;
-    const size_t row_bytes = (size_t)nb * 36;
+    const size_t row_bytes = (size_t)nb * F::BYTES;
     const bool glu = a.glu != 0;
     const int OC = a.OC[mi];
     const long nrows = glu ? 2L * OC : (long)OC;
 
-    Blk blk[U];
+    typename F::Block blk[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const long lr = row0 + slot + (long)u * slots;
         if (lane_on && lr < nrows) {
             const unsigned char* wm = glu ? a.w[lr & 1] : a.w[mi];
             const long r = glu ? (lr >> 1) : lr;
-            blk[u] = load_block(wm + (size_t)r * row_bytes + (size_t)bc * 36);
+            blk[u] = F::load(wm + (size_t)r * row_bytes + (size_t)bc * F::BYTES);
         } else {
-            blk[u] = zero_block();
+            blk[u] = F::zero();
         }
     }
 
@@ -721,6 +720,21 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
     }
 }
 
+template <int WT, int U>
+__global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
+    __shared__ float red[WT * U];
+    __shared__ float sh[WT / 64];
+    dec_mv_body<WT, U, QF_Q8>(a, red, sh);
+}
+
+/* The same phase over Q4_0 weights. */
+template <int WT, int U>
+__global__ __launch_bounds__(WT) void k_dec_mv4(DecMv a) {
+    __shared__ float red[WT * U];
+    __shared__ float sh[WT / 64];
+    dec_mv_body<WT, U, QF_Q4>(a, red, sh);
+}
+
 /* Batched fused Q8 matvec (decode with B >= 2) on fp32 MFMA
  * (v_mfma_f32_16x16x4_f32: D[16][16] += A[16][4] x B[4][16]).
  *
@@ -740,10 +754,10 @@ __global__ __launch_bounds__(WT) void k_dec_mv(DecMv a) {
 constexpr int BMV_WAVES = 8;              /* waves per workgroup, splitting the K blocks */
 constexpr int BMV_NT = 64 * BMV_WAVES;
 
-template <int NBT>
-__global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
-    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
-    __shared__ float ssq[BMV_WAVES][16 * NBT];
+template <int NBT, int QF>
+__device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[NBT][64], float (*ssq)[16 * NBT]) {
+    constexpr int BYTES = QFmt<QF>::BYTES;
+    constexpr int LANE_OFF = QF == QF_Q4 ? 4 : 8; /* bytes of codes per lane and block */
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int c = lane & 15, g = lane >> 4;
     int mi = 0;
@@ -753,10 +767,11 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
     const bool glu = a.glu != 0;
     const int OC = a.OC[mi];
     const int nb = a.C / 32;
-    const size_t row_bytes = (size_t)nb * 36;
+    const size_t row_bytes = (size_t)nb * BYTES;
     /* this lane's weight row (clamped: rows past OC feed outputs never stored) */
     const int row = glu ? tile * 8 + (c & 7) : tile * 16 + c;
-    const unsigned char* wrow = (glu ? a.w[c >> 3] : a.w[mi]) + (size_t)min(row, OC - 1) * row_bytes + 4 + 8 * g;
+    const unsigned char* wrow =
+        (glu ? a.w[c >> 3] : a.w[mi]) + (size_t)min(row, OC - 1) * row_bytes + 4 + LANE_OFF * g;
     const float* xr[NBT];
 #pragma unroll
     for (int bt = 0; bt < NBT; bt++) xr[bt] = a.x + (size_t)min(b0 + 16 * bt + c, a.B - 1) * a.ldx + 8 * g;
@@ -770,12 +785,12 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
         ss[bt] = 0.f;
     }
     for (int kb = wave; kb < nb; kb += BMV_WAVES) {
-        const unsigned char* blk = wrow + (size_t)kb * 36;
+        const unsigned char* blk = wrow + (size_t)kb * BYTES;
         float s;
-        unsigned int q0, q1;
-        __builtin_memcpy(&s, __builtin_assume_aligned(blk - 4 - 8 * g, 4), 4);
+        unsigned int q0, q1 = 0u;
+        __builtin_memcpy(&s, __builtin_assume_aligned(blk - 4 - LANE_OFF * g, 4), 4);
         __builtin_memcpy(&q0, __builtin_assume_aligned(blk, 4), 4);
-        __builtin_memcpy(&q1, __builtin_assume_aligned(blk + 4, 4), 4);
+        if (QF == QF_Q8) __builtin_memcpy(&q1, __builtin_assume_aligned(blk + 4, 4), 4);
         float gv[8];
         if (nwp) {
             float4 g0, g1;
@@ -794,10 +809,15 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
             xv[bt][4] = x1.x; xv[bt][5] = x1.y; xv[bt][6] = x1.z; xv[bt][7] = x1.w;
         }
         float wv[8];
+        if (QF == QF_Q4) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            wv[i] = q8_byte(q0, i);
-            wv[4 + i] = q8_byte(q1, i);
+            for (int i = 0; i < 8; i++) wv[i] = q4_code(q0, i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                wv[i] = q8_byte(q0, i);
+                wv[4 + i] = q8_byte(q1, i);
+            }
         }
 #pragma unroll
         for (int bt = 0; bt < NBT; bt++) {
@@ -853,6 +873,21 @@ __global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
             }
         }
     }
+}
+
+template <int NBT>
+__global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
+    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
+    __shared__ float ssq[BMV_WAVES][16 * NBT];
+    dec_bmv_body<NBT, QF_Q8>(a, part, ssq);
+}
+
+/* The same over Q4_0 weights: a lane's 8 codes of a block are one dword. */
+template <int NBT>
+__global__ __launch_bounds__(BMV_NT) void k_dec_bmv4(DecMv a) {
+    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
+    __shared__ float ssq[BMV_WAVES][16 * NBT];
+    dec_bmv_body<NBT, QF_Q4>(a, part, ssq);
 }
 
 /* Rope + KV append + attention of one decode step; workgroup (h, b) =
@@ -1517,7 +1552,8 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
         /* one workgroup per (row tile, 16 batch rows): more workgroups than
          * one per row tile, each weight tile is read from L2 again */
         const dim3 grid(a.tile0[a.nmat], (a.B + 15) / 16);
-        hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
+        if (a.qf == QF_Q4) hipLaunchKernelGGL(k_dec_bmv4<1>, grid, dim3(BMV_NT), 0, s, a);
+        else hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
         BMK_LAUNCH_CHECK();
         return 0;
     }
@@ -1525,9 +1561,15 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
     dec_mv_shape(a.C, a.glu, &wt, &a.slots);
     if (a.slots == 0) return -1;
     const dim3 grid(a.tile0[a.nmat]);
-    if (wt == 64) hipLaunchKernelGGL((k_dec_mv<64, 1>), grid, dim3(64), 0, s, a);
-    else if (wt == 128) hipLaunchKernelGGL((k_dec_mv<128, 1>), grid, dim3(128), 0, s, a);
-    else hipLaunchKernelGGL((k_dec_mv<256, 1>), grid, dim3(256), 0, s, a);
+    if (a.qf == QF_Q4) {
+        if (wt == 64) hipLaunchKernelGGL((k_dec_mv4<64, 1>), grid, dim3(64), 0, s, a);
+        else if (wt == 128) hipLaunchKernelGGL((k_dec_mv4<128, 1>), grid, dim3(128), 0, s, a);
+        else hipLaunchKernelGGL((k_dec_mv4<256, 1>), grid, dim3(256), 0, s, a);
+    } else {
+        if (wt == 64) hipLaunchKernelGGL((k_dec_mv<64, 1>), grid, dim3(64), 0, s, a);
+        else if (wt == 128) hipLaunchKernelGGL((k_dec_mv<128, 1>), grid, dim3(128), 0, s, a);
+        else hipLaunchKernelGGL((k_dec_mv<256, 1>), grid, dim3(256), 0, s, a);
+    }
     BMK_LAUNCH_CHECK();
     return 0;
 }

@@ -44,7 +44,7 @@ typedef struct {
     unsigned long long key[DEC_MAX_B]; /* running argmax of the current step, packed (value, ~index) */
 } DecState;
 
-/* One fused Q8 matvec phase: y_i = W_i * f(x) for up to three matrices that
+/* One fused quantized matvec phase: y_i = W_i * f(x) for up to three matrices that
  * share the input, f = identity or RMSNorm(x) * norm_w.
  *  glu      : W_0 = gate, W_1 = up; y_0 = silu(gate x) * (up x)
  *  residual : y_0 += previous y_0 (y_0 is the residual stream, updated in place)
@@ -60,6 +60,7 @@ typedef struct {
     int glu;
     int residual;
     int slots;                 /* rows per row pass of a workgroup (set by the launcher; even for glu) */
+    int qf;                    /* weight blocks: 0 Q8_0 (36 bytes), 1 Q4_0 (20 bytes) */
     const unsigned char* w[DEC_MAX_MATS];
     float* y[DEC_MAX_MATS];
     int OC[DEC_MAX_MATS];

@@ -12,6 +12,10 @@
 extern "C" {
 int bmk_launch_quantize_q8(const bmk_launch_t* a);
 int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a);
+int bmk_launch_quantize_q4(const bmk_launch_t* a);
+int bmk_launch_quantize_q4_bf16(const bmk_launch_t* a);
+int bmk_launch_q4_matvec(const bmk_launch_t* a);
+int bmk_launch_q4_matvec_multi(const bmk_launch_t* a);
 int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
@@ -41,6 +45,16 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"matmul_forward_q8_vec", 5, B(4), B(3), bmk_launch_q8_matvec},
     /* reference forward.metal:625-649; same buffers */
     {"matmul_forward_q8", 5, B(4), B(3), bmk_launch_q8_matmul},
+    /* Q4_0 (reference quant.c:31-52, forward.metal:654-858): new pack kernels
+     * {src, dst q4, params{n}}; the reference's three matvec kernels, routed as
+     * scheduler.c:755-764, buffers as the Q8 ones */
+    {"quantize_q4", 3, B(2), B(1), bmk_launch_quantize_q4},
+    {"quantize_q4_bf16", 3, B(2), B(1), bmk_launch_quantize_q4_bf16},
+    {"matmul_forward_q4_vec4", 5, B(4), B(3), bmk_launch_q4_matvec},
+    {"matmul_forward_q4_vec", 5, B(4), B(3), bmk_launch_q4_matvec},
+    {"matmul_forward_q4", 5, B(4), B(3), bmk_launch_q4_matvec},
+    /* new: every Q4 matvec of a decode token in one launch (same plan as the Q8 one) */
+    {"matmul_forward_q4_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q4_matvec_multi, B(1)},
     /* new: every Q8 matvec of a decode token in one launch; {params{nprob,n_tiles},
      * plan{MvDesc[nprob], u32 tile_map[n_tiles]}, weight arena, x arena, y arena} */
     {"matmul_forward_q8_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_matvec_multi, B(1)},

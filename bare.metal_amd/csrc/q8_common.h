@@ -1,9 +1,10 @@
 /* SPDX-License-Identifier: MPL-2.0
  *
- * q8_common.h — device helpers shared by the Q8 kernels: one 36-byte Q8_0
- * block {f32 scale; int8 q[32]} (reference src/baremetal/quant.h:17-32)
- * read with two dwordx4 loads and one dword load, and its dot product with
- * 32 fp32 activations held in registers.
+ * q8_common.h — device helpers shared by the quantized kernels: one 36-byte
+ * Q8_0 block {f32 scale; int8 q[32]} (reference src/baremetal/quant.h:17-32)
+ * read with two dwordx4 loads and one dword load, one 20-byte Q4_0 block
+ * (quant.h:34-42) read with a dword and a dwordx4 load, and their dot
+ * products with 32 fp32 activations held in registers.
  */
 #ifndef BMK_Q8_COMMON_H
 #define BMK_Q8_COMMON_H
@@ -58,6 +59,61 @@ __device__ __forceinline__ float block_dot(const Blk& b, const float* xs) {
 }
 
 
+/* ---- Q4_0 blocks: 20 bytes {f32 scale; u8 qs[16]} (reference
+ * src/baremetal/quant.h:34-42); element 2j is the low nibble of qs[j],
+ * element 2j+1 the high nibble, each a two's-complement 4-bit code. */
+struct Blk4 {
+    float s;
+    uint4 q;
+};
+
+__device__ __forceinline__ Blk4 load_block4(const unsigned char* p) {
+    Blk4 b;
+    __builtin_memcpy(&b.s, __builtin_assume_aligned(p, 4), 4);
+    __builtin_memcpy(&b.q, __builtin_assume_aligned(p + 4, 4), 16);
+    return b;
+}
+
+__device__ __forceinline__ Blk4 zero_block4() {
+    Blk4 b;
+    b.s = 0.0f;
+    b.q = make_uint4(0, 0, 0, 0);
+    return b;
+}
+
+/* code k (0..7) of a dword of packed nibbles, exactly as fp32 */
+__device__ __forceinline__ float q4_code(unsigned int w, int k) { return (float)((int)(w << (28 - 4 * k)) >> 28); }
+
+__device__ __forceinline__ float dot8_q4(unsigned int w, const float* x) {
+    float a = x[0] * q4_code(w, 0);
+#pragma unroll
+    for (int k = 1; k < 8; k++) a = fmaf(x[k], q4_code(w, k), a);
+    return a;
+}
+
+__device__ __forceinline__ float block_dot(const Blk4& b, const float* xs) {
+    const float s0 = dot8_q4(b.q.x, xs + 0) + dot8_q4(b.q.y, xs + 8);
+    const float s1 = dot8_q4(b.q.z, xs + 16) + dot8_q4(b.q.w, xs + 24);
+    return (s0 + s1) * b.s;
+}
+
+/* Block formats of the quantized kernels: bytes per 32-weight block and the
+ * register form of one block. */
+enum { QF_Q8 = 0, QF_Q4 = 1 };
+template <int QF> struct QFmt;
+template <> struct QFmt<QF_Q8> {
+    static constexpr int BYTES = 36;
+    typedef Blk Block;
+    static __device__ __forceinline__ Blk load(const unsigned char* p) { return load_block(p); }
+    static __device__ __forceinline__ Blk zero();
+};
+template <> struct QFmt<QF_Q4> {
+    static constexpr int BYTES = 20;
+    typedef Blk4 Block;
+    static __device__ __forceinline__ Blk4 load(const unsigned char* p) { return load_block4(p); }
+    static __device__ __forceinline__ Blk4 zero() { return zero_block4(); }
+};
+
 __device__ __forceinline__ Blk zero_block() {
     Blk b;
     b.s = 0.0f;
@@ -65,6 +121,8 @@ __device__ __forceinline__ Blk zero_block() {
     b.q1 = make_uint4(0, 0, 0, 0);
     return b;
 }
+
+__device__ __forceinline__ Blk QFmt<QF_Q8>::zero() { return zero_block(); }
 
 /* Sum over the 64 lanes of a wave (xor butterfly; every lane gets the sum). */
 __device__ __forceinline__ float wave_sum(float v) {

@@ -11,6 +11,7 @@
 #define MV_MAX_PROBS 8
 #define MV_U 4        /* rows in flight per lane for small launches */
 #define MV_U_WIDE 8   /* rows in flight per lane when the launch has work for every CU many times over */
+#define MV_U_Q4 16    /* rows in flight per lane of the multi-matrix Q4 launch (20-byte blocks) */
 
 /* One y = W x (+ bias) problem; W is OC rows of nb 36-byte Q8 blocks. */
 typedef struct {

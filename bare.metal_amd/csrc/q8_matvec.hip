@@ -39,9 +39,11 @@ namespace {
 using namespace bmk;
 constexpr int MV_THREADS = 256;
 
-/* One row tile of one problem.  Requires nb <= MV_THREADS. */
-template <int U>
+/* One row tile of one problem.  Requires nb <= MV_THREADS.  QF: block
+ * format (Q8_0 36-byte or Q4_0 20-byte blocks). */
+template <int U, int QF>
 __device__ __forceinline__ void mv_tile(const MvProb& p, int tile, float* red) {
+    typedef QFmt<QF> F;
     const int nb = p.nb;
     const int slots = MV_THREADS / nb;
     const int rows_per_tile = slots * U;
@@ -50,7 +52,7 @@ __device__ __forceinline__ void mv_tile(const MvProb& p, int tile, float* red) {
     const int b = t - slot * nb;
     const bool lane_on = slot < slots;
     const long row0 = (long)tile * rows_per_tile;
-    const size_t row_bytes = (size_t)nb * 36;
+    const size_t row_bytes = (size_t)nb * F::BYTES;
 
     float xs[32];
     if (lane_on) {
@@ -66,16 +68,14 @@ __device__ __forceinline__ void mv_tile(const MvProb& p, int tile, float* red) {
         for (int i = 0; i < 32; i++) xs[i] = 0.0f;
     }
 
-    Blk blk[U];
+    typename F::Block blk[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const long r = row0 + slot + (long)u * slots;
         if (lane_on && r < p.OC) {
-            blk[u] = load_block(p.w + (size_t)r * row_bytes + (size_t)b * 36);
+            blk[u] = F::load(p.w + (size_t)r * row_bytes + (size_t)b * F::BYTES);
         } else {
-            blk[u].s = 0.0f;
-            blk[u].q0 = make_uint4(0, 0, 0, 0);
-            blk[u].q1 = make_uint4(0, 0, 0, 0);
+            blk[u] = F::zero();
         }
     }
 #pragma unroll
@@ -96,16 +96,18 @@ __device__ __forceinline__ void mv_tile(const MvProb& p, int tile, float* red) {
 }
 
 /* Rows longer than MV_THREADS blocks: the workgroup walks one row at a time. */
+template <int QF>
 __device__ __forceinline__ void mv_row_wide(const MvProb& p, long r, float* red) {
+    typedef QFmt<QF> F;
     const int t = threadIdx.x;
-    const unsigned char* wr = p.w + (size_t)r * p.nb * 36;
+    const unsigned char* wr = p.w + (size_t)r * p.nb * F::BYTES;
     float acc = 0.0f;
     for (int b = t; b < p.nb; b += MV_THREADS) {
         float xs[32];
         const float* xp = p.x + 32 * b;
 #pragma unroll
         for (int i = 0; i < 32; i++) xs[i] = xp[i];
-        acc += block_dot(load_block(wr + (size_t)b * 36), xs);
+        acc += block_dot(F::load(wr + (size_t)b * F::BYTES), xs);
     }
     red[t] = acc;
     __syncthreads();
@@ -118,12 +120,12 @@ __device__ __forceinline__ void mv_row_wide(const MvProb& p, long r, float* red)
     __syncthreads();
 }
 
-template <int U>
+template <int U, int QF>
 __device__ __forceinline__ void mv_dispatch(const MvProb& p, int tile, float* red) {
     if (p.nb <= MV_THREADS) {
-        mv_tile<U>(p, tile, red);
+        mv_tile<U, QF>(p, tile, red);
     } else {
-        mv_row_wide(p, tile, red);
+        mv_row_wide<QF>(p, tile, red);
     }
 }
 
@@ -137,7 +139,20 @@ __global__ __launch_bounds__(MV_THREADS) void k_q8_matvec(MvGroup g) {
         tile -= g.p[i].tiles;
         i++;
     }
-    mv_dispatch<U>(g.p[i], tile, red);
+    mv_dispatch<U, QF_Q8>(g.p[i], tile, red);
+}
+
+/* The same over Q4_0 blocks (reference forward.metal:654-858). */
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q4_matvec(MvGroup g) {
+    __shared__ float red[MV_THREADS * U];
+    int tile = blockIdx.x;
+    int i = 0;
+    while (i + 1 < g.nprob && tile >= g.p[i].tiles) {
+        tile -= g.p[i].tiles;
+        i++;
+    }
+    mv_dispatch<U, QF_Q4>(g.p[i], tile, red);
 }
 
 /* Any number of problems; tile_map[blockIdx.x] = (problem << 20) | tile. */
@@ -147,17 +162,15 @@ __global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_list(const MvProb* __r
     __shared__ float red[MV_THREADS * U];
     const unsigned int m = tile_map[blockIdx.x];
     const MvProb p = probs[m >> 20];
-    mv_dispatch<U>(p, (int)(m & 0xfffffu), red);
+    mv_dispatch<U, QF_Q8>(p, (int)(m & 0xfffffu), red);
 }
 
 /* Any number of problems addressed by arena offsets; tile_map[blockIdx.x]
  * is the problem index, the tile is blockIdx.x - desc.tile0. */
-template <int U>
-__global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_multi(const unsigned char* __restrict__ W,
-                                                                const float* __restrict__ X, float* __restrict__ Y,
-                                                                const MvDesc* __restrict__ desc,
-                                                                const unsigned int* __restrict__ tile_map) {
-    __shared__ float red[MV_THREADS * U];
+template <int U, int QF>
+__device__ __forceinline__ void mv_multi_body(const unsigned char* __restrict__ W, const float* __restrict__ X,
+                                              float* __restrict__ Y, const MvDesc* __restrict__ desc,
+                                              const unsigned int* __restrict__ tile_map, float* red) {
     const MvDesc d = desc[tile_map[blockIdx.x]];
     MvProb p;
     p.w = W + d.w_off;
@@ -168,7 +181,25 @@ __global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_multi(const unsigned c
     p.nb = d.C / 32;
     p.tiles = d.tiles;
     p.pad_ = 0;
-    mv_dispatch<U>(p, (int)blockIdx.x - d.tile0, red);
+    mv_dispatch<U, QF>(p, (int)blockIdx.x - d.tile0, red);
+}
+
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q8_matvec_multi(const unsigned char* __restrict__ W,
+                                                                const float* __restrict__ X, float* __restrict__ Y,
+                                                                const MvDesc* __restrict__ desc,
+                                                                const unsigned int* __restrict__ tile_map) {
+    __shared__ float red[MV_THREADS * U];
+    mv_multi_body<U, QF_Q8>(W, X, Y, desc, tile_map, red);
+}
+
+template <int U>
+__global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned char* __restrict__ W,
+                                                                const float* __restrict__ X, float* __restrict__ Y,
+                                                                const MvDesc* __restrict__ desc,
+                                                                const unsigned int* __restrict__ tile_map) {
+    __shared__ float red[MV_THREADS * U];
+    mv_multi_body<U, QF_Q4>(W, X, Y, desc, tile_map, red);
 }
 
 } // namespace
@@ -188,7 +219,8 @@ extern "C" int mv_tiles_for(int OC, int C, int U) {
  * HBM roofline; fewer, wider tiles would starve the CUs on small matrices. */
 #define MV_WIDE_MIN_TILES 4096
 
-extern "C" int mv_launch_group(MvGroup* g, hipStream_t s) {
+template <int QF>
+static int launch_group(MvGroup* g, hipStream_t s) {
     long total = 0;
     for (int i = 0; i < g->nprob; i++) total += mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, MV_U);
     if (total <= 0) return 0;
@@ -198,13 +230,19 @@ extern "C" int mv_launch_group(MvGroup* g, hipStream_t s) {
         g->p[i].tiles = mv_tiles_for(g->p[i].OC, g->p[i].nb * 32, U);
         total += g->p[i].tiles;
     }
-    if (U == MV_U_WIDE)
-        hipLaunchKernelGGL(k_q8_matvec<MV_U_WIDE>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
-    else
-        hipLaunchKernelGGL(k_q8_matvec<MV_U>, dim3((unsigned)total), dim3(MV_THREADS), 0, s, *g);
+    const dim3 grid((unsigned)total), tb(MV_THREADS);
+    if (QF == QF_Q4) {
+        if (U == MV_U_WIDE) hipLaunchKernelGGL(k_q4_matvec<MV_U_WIDE>, grid, tb, 0, s, *g);
+        else hipLaunchKernelGGL(k_q4_matvec<MV_U>, grid, tb, 0, s, *g);
+    } else {
+        if (U == MV_U_WIDE) hipLaunchKernelGGL(k_q8_matvec<MV_U_WIDE>, grid, tb, 0, s, *g);
+        else hipLaunchKernelGGL(k_q8_matvec<MV_U>, grid, tb, 0, s, *g);
+    }
     BMK_LAUNCH_CHECK();
     return 0;
 }
+
+extern "C" int mv_launch_group(MvGroup* g, hipStream_t s) { return launch_group<QF_Q8>(g, s); }
 
 extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
     if (n_tiles <= 0) return 0;
@@ -214,13 +252,23 @@ extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_
     return 0;
 }
 
-extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
-                               const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
+template <int QF>
+static int launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
+                        const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
     if (n_tiles <= 0) return 0;
-    hipLaunchKernelGGL(k_q8_matvec_multi<MV_U_WIDE>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y, d_desc,
-                       d_tile_map);
+    if (QF == QF_Q4)
+        hipLaunchKernelGGL(k_q4_matvec_multi<MV_U_Q4>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y,
+                           d_desc, d_tile_map);
+    else
+        hipLaunchKernelGGL(k_q8_matvec_multi<MV_U_WIDE>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y,
+                           d_desc, d_tile_map);
     BMK_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
+                               const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
+    return launch_multi<QF_Q8>(W, X, Y, d_desc, d_tile_map, n_tiles, s);
 }
 
 /* matmul_forward_q8_vec_multi: every Q8 matvec of one decode token (or any
@@ -231,7 +279,10 @@ extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y,
  *          2 weight arena (Q8 blocks), 3 activation arena f32, 4 output arena f32}.
  * Every descriptor and tile-map entry is checked against the arena sizes
  * before anything is launched. */
-extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
+template <int QF>
+static int launch_matvec_multi(const bmk_launch_t* a) {
+    const int BYTES = QFmt<QF>::BYTES;
+    const int U = QF == QF_Q4 ? MV_U_Q4 : MV_U_WIDE;
     BMK_NEED_BYTES(a, 0, 8, "params");
     const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
     BMK_REQUIRE(nprob >= 0 && n_tiles >= 0, "q8 matvec multi: bad counts nprob=%d n_tiles=%d", nprob, n_tiles);
@@ -247,11 +298,11 @@ extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
     for (int i = 0; i < nprob; i++) {
         const MvDesc& d = desc[i];
         BMK_REQUIRE(d.OC > 0 && d.C > 0 && d.C % 32 == 0, "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, d.OC, d.C);
-        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, MV_U_WIDE) && d.tile0 == next_tile,
+        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, U) && d.tile0 == next_tile,
                     "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
-                    mv_tiles_for(d.OC, d.C, MV_U_WIDE), next_tile);
+                    mv_tiles_for(d.OC, d.C, U), next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 matvec multi: problem %d weight offset not 4-byte aligned", i);
-        BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * 36 <= a->bytes[2] &&
+        BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * BYTES <= a->bytes[2] &&
                     d.x_off + (unsigned long long)d.C <= a->bytes[3] / 4 &&
                     d.y_off + (unsigned long long)d.OC <= a->bytes[4] / 4,
                     "q8 matvec multi: problem %d lies outside its arenas", i);
@@ -261,10 +312,13 @@ extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) {
     for (int i = 0; i < nprob; i++)
         for (int t = desc[i].tile0; t < desc[i].tile0 + desc[i].tiles; t++)
             BMK_REQUIRE(tmap[t] == (unsigned)i, "q8 matvec multi: tile_map[%d]=%u, expected %d", t, tmap[t], i);
-    return mv_launch_multi((const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
-                           (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
-                           n_tiles, a->stream);
+    return launch_multi<QF>((const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
+                            (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
+                            n_tiles, a->stream);
 }
+
+extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) { return launch_matvec_multi<QF_Q8>(a); }
+extern "C" int bmk_launch_q4_matvec_multi(const bmk_launch_t* a) { return launch_matvec_multi<QF_Q4>(a); }
 
 extern "C" int dec_launch_mv(const DecMv* a, hipStream_t s);
 
@@ -272,13 +326,16 @@ extern "C" int dec_launch_mv(const DecMv* a, hipStream_t s);
  * buffers {inp f32 [BT][C], weight q8 [OC][C/32], bias f32 [OC], out f32 [BT][OC],
  * params int {BT, C, OC, has_bias}}.  The Metal grid (OC*128 or OC rounded to
  * 32, BT) is not needed: the launch shape follows from the parameters. */
-extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
+template <int QF>
+static int launch_matvec(const bmk_launch_t* a) {
+    const int BYTES = QFmt<QF>::BYTES;
     BMK_NEED_BYTES(a, 4, 16, "params");
     const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);
-    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0 && C % 32 == 0, "q8 matvec: bad shape BT=%d C=%d OC=%d", BT, C, OC);
+    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0 && C % 32 == 0, "q%d matvec: bad shape BT=%d C=%d OC=%d",
+                QF == QF_Q4 ? 4 : 8, BT, C, OC);
     if (BT == 0 || OC == 0) return 0;
     BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
-    BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * 36, "weight");
+    BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * BYTES, "weight");
     if (has_bias) BMK_NEED_BYTES(a, 2, (size_t)OC * 4, "bias");
     BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
     BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0,
@@ -293,6 +350,7 @@ extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
         m.B = BT;
         m.ldx = C;
         m.nmat = 1;
+        m.qf = QF;
         m.w[0] = (const unsigned char*)a->dev[1];
         m.y[0] = (float*)a->dev[3];
         m.OC[0] = OC;
@@ -312,7 +370,40 @@ extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) {
             p.nb = C / 32;
             p.tiles = 0;
         }
-        if (mv_launch_group(&g, a->stream) != 0) return -1;
+        if (launch_group<QF>(&g, a->stream) != 0) return -1;
+    }
+    return 0;
+}
+
+extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) { return launch_matvec<QF_Q8>(a); }
+
+/* matmul_forward_q4_vec4 / matmul_forward_q4_vec / matmul_forward_q4
+ * (reference forward.metal:654-858, routing scheduler.c:755-764): the same
+ * buffers over Q4_0 weights [OC][C/32] of 20-byte blocks.  BT > DEC_MAX_B
+ * rows go through the batched kernel DEC_MAX_B rows at a time. */
+extern "C" int bmk_launch_q4_matvec(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 4, 16, "params");
+    const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);
+    if (BT <= DEC_MAX_B || has_bias || ((uintptr_t)a->dev[0] & 15)) return launch_matvec<QF_Q4>(a);
+    BMK_REQUIRE(OC >= 0 && C > 0 && C % 32 == 0, "q4 matvec: bad shape BT=%d C=%d OC=%d", BT, C, OC);
+    if (OC == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
+    BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * 20, "weight");
+    BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
+    BMK_REQUIRE(((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0, "q4 matvec: misaligned buffer offset");
+    for (int b0 = 0; b0 < BT; b0 += DEC_MAX_B) {
+        DecMv m;
+        memset(&m, 0, sizeof m);
+        m.x = (const float*)a->dev[0] + (size_t)b0 * C;
+        m.C = C;
+        m.B = BT - b0 < DEC_MAX_B ? BT - b0 : DEC_MAX_B;
+        m.ldx = C;
+        m.nmat = 1;
+        m.qf = QF_Q4;
+        m.w[0] = (const unsigned char*)a->dev[1];
+        m.y[0] = (float*)a->dev[3] + (size_t)b0 * OC;
+        m.OC[0] = OC;
+        BMK_REQUIRE(dec_launch_mv(&m, a->stream) == 0, "q4 matvec: batched launch failed (BT=%d C=%d OC=%d)", BT, C, OC);
     }
     return 0;
 }

@@ -1,6 +1,7 @@
 /* SPDX-License-Identifier: MPL-2.0
  *
- * q8_pack.hip — fp32/bf16 -> Q8_0 block quantize/pack on gfx950.
+ * q8_pack.hip — fp32/bf16 -> Q8_0 (and Q4_0, below) block quantize/pack on
+ * gfx950.
  *
  * Output format (reference src/baremetal/quant.h:17-32): an array of 36-byte
  * blocks {float scale; int8 q[32]}, block b covering source elements
@@ -116,7 +117,89 @@ int launch_quantize(const bmk_launch_t* a) {
     return 0;
 }
 
+/* ---- Q4_0 (reference src/baremetal/quant.c:31-52): scale = amax / 7.0f,
+ * codes clamp((int)lroundf(p * inv), -8, 7), element 2j in the low nibble
+ * of qs[j] and 2j+1 in the high nibble; 20-byte blocks {scale, qs[16]}.
+ * Same mapping as the Q8 pack: 8 lanes per block, 4 elements (two bytes of
+ * qs) per lane; even lanes join their odd neighbour's two bytes and store
+ * one dword. */
+__device__ __forceinline__ int q4_round_clamp(float y) {
+    if (!(fabsf(y) <= 3.402823466e38f)) return 0; /* NaN / Inf: (int)LONG_MIN == 0 */
+    float t = truncf(y);
+    if (fabsf(y - t) >= 0.5f) t += copysignf(1.0f, y);
+    t = fminf(fmaxf(t, -8.0f), 7.0f);
+    return (int)t;
+}
+
+template <bool SRC_BF16>
+__global__ __launch_bounds__(256) void k_quantize_q4(const void* __restrict__ src, unsigned char* __restrict__ dst,
+                                                     long nblocks) {
+    const long gt = (long)blockIdx.x * 256 + threadIdx.x;
+    const long blk = gt >> 3;
+    const int j = threadIdx.x & 7;
+    const bool active = blk < nblocks;
+
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (active) load4<SRC_BF16>(src, blk * 32 + 4 * j, v);
+
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a = fabsf(v[i]);
+        m = (a > m) ? a : m;
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        float o = __shfl_xor(m, off, 8);
+        m = (o > m) ? o : m;
+    }
+
+    const float scale = m / 7.0f;
+    unsigned int half = 0u; /* this lane's 4 nibbles: qs bytes 2j and 2j+1 */
+    if (scale != 0.0f) {
+        const float inv = 1.0f / scale;
+#pragma unroll
+        for (int i = 0; i < 4; i++) half |= ((unsigned int)q4_round_clamp(v[i] * inv) & 0xFu) << (4 * i);
+    }
+    const unsigned int other = __shfl_xor(half, 1, 8);
+    if (active && (j & 1) == 0) {
+        unsigned int* bw = (unsigned int*)__builtin_assume_aligned(dst + blk * 20, 4);
+        bw[1 + (j >> 1)] = half | (other << 16);
+        if (j == 0) bw[0] = __float_as_uint(scale);
+    }
+}
+
+template <bool SRC_BF16>
+int launch_quantize_q4(const bmk_launch_t* a) {
+    /* buffers: [0] src (fp32 or bf16), [1] dst q4 blocks, [2] params {n} */
+    BMK_NEED_BYTES(a, 2, 4, "params");
+    const long n = (long)(unsigned int)bmk_pi(a, 2, 0);
+    BMK_REQUIRE(n > 0 && n % 32 == 0, "quantize_q4: n=%ld must be a positive multiple of 32", n);
+    const long nblocks = n / 32;
+    BMK_NEED_BYTES(a, 0, n * (SRC_BF16 ? 2 : 4), "src");
+    BMK_NEED_BYTES(a, 1, nblocks * 20, "dst");
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & (SRC_BF16 ? 7 : 3)) == 0 && ((uintptr_t)a->dev[1] & 3) == 0,
+                "quantize_q4: misaligned src/dst offset");
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q4<SRC_BF16>, dim3(grid), dim3(256), 0, a->stream, (const void*)a->dev[0],
+                       (unsigned char*)a->dev[1], nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
 } // namespace
+
+extern "C" int bmk_launch_quantize_q4(const bmk_launch_t* a) { return launch_quantize_q4<false>(a); }
+extern "C" int bmk_launch_quantize_q4_bf16(const bmk_launch_t* a) { return launch_quantize_q4<true>(a); }
+
+/* Engine-side Q4 pack of n fp32 values (as q8_pack_f32). */
+extern "C" int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s) {
+    const long nblocks = n / 32;
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q4<false>, dim3(grid), dim3(256), 0, s, (const void*)src, dst, nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
 
 extern "C" int bmk_launch_quantize_q8(const bmk_launch_t* a) { return launch_quantize<false>(a); }
 extern "C" int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a) { return launch_quantize<true>(a); }

@@ -70,15 +70,23 @@ def problem_list(model: str, head: bool = True):
     return probs
 
 
-class Workload:
-    """Q8 weights, activations and outputs of one token's projections in three arenas."""
+FORMATS = {  # block bytes, pack kernel, multi-matvec kernel
+    "q8": (36, "quantize_q8", "matmul_forward_q8_vec_multi"),
+    "q4": (20, "quantize_q4", "matmul_forward_q4_vec_multi"),
+}
 
-    def __init__(self, be: bmhip.Backend, probs):
+
+class Workload:
+    """Quantized weights, activations and outputs of one token's projections in three arenas."""
+
+    def __init__(self, be: bmhip.Backend, probs, fmt: str = "q8", seed: int = BASE_SEED):
         self.be = be
         self.probs = probs
+        self.fmt, self.seed = fmt, seed
+        blk, self.pack_kernel, kname = FORMATS[fmt]
         OC = np.array([p[4] for p in probs], np.int64)
         C = np.array([p[5] for p in probs], np.int64)
-        wbytes = OC * (C // 32) * 36
+        wbytes = OC * (C // 32) * blk
         self.w_off = np.concatenate([[0], np.cumsum(wbytes)[:-1]]).astype(np.uint64)
         self.x_off = np.concatenate([[0], np.cumsum(C)[:-1]]).astype(np.uint64)
         self.y_off = np.concatenate([[0], np.cumsum(OC)[:-1]]).astype(np.uint64)
@@ -90,10 +98,11 @@ class Workload:
         self.Y = be.alloc(4 * int(OC.sum()))
         self.pack_ms = 0.0
         self._fill()
-        plan, self.n_tiles = bmhip.mv_plan(self.w_off, self.x_off, self.y_off, self.OC, self.C)
+        plan, self.n_tiles = bmhip.mv_plan(self.w_off, self.x_off, self.y_off, self.OC, self.C, fmt)
         self.plan = be.upload(plan)
         self.params = be.params(len(probs), self.n_tiles)
-        self.k = be.kernel("matmul_forward_q8_vec_multi")
+        self.kname = kname
+        self.k = be.kernel(kname)
 
     def _fill(self):
         be = self.be
@@ -102,16 +111,16 @@ class Workload:
         xs = np.empty(int(self.C.sum()), np.float32)
         for i, (name, mid, l, m, OC, C) in enumerate(self.probs):
             n = OC * C
-            w32 = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, mid, l, m), 0.02, n)
+            w32 = bmhip.synth_normal(bmhip.synth_seed(self.seed, mid, l, m), 0.02, n)
             stage.write(w32)
             enc = be.encoder()
-            rc = enc.dispatch(be.kernel("quantize_q8"), [stage, self.W, be.params(n)], (n // 4,), (256,),
+            rc = enc.dispatch(be.kernel(self.pack_kernel), [stage, self.W, be.params(n)], (n // 4,), (256,),
                               offsets=[0, int(self.w_off[i]), 0])
             if rc != 0:
-                raise RuntimeError(f"quantize_q8 failed for {name}")
+                raise RuntimeError(f"{self.pack_kernel} failed for {name}")
             self.pack_ms += enc.wait_timed()
             xo = int(self.x_off[i])
-            xs[xo:xo + C] = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, mid, l, 100 + m), 1.0, C)
+            xs[xo:xo + C] = bmhip.synth_normal(bmhip.synth_seed(self.seed, mid, l, 100 + m), 1.0, C)
         self.X.write(xs)
         self.pack_elems = int((self.OC.astype(np.int64) * self.C).sum())
         stage.free()
@@ -119,7 +128,7 @@ class Workload:
     def launch(self, enc) -> None:
         rc = enc.dispatch(self.k, [self.params, self.plan, self.W, self.X, self.Y], (self.n_tiles * 256,), (256,))
         if rc != 0:
-            raise RuntimeError("matmul_forward_q8_vec_multi dispatch rejected")
+            raise RuntimeError(f"{self.kname} dispatch rejected")
 
 
 def check_against_single(be, wl: Workload, idx):
@@ -168,6 +177,55 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def q4_leg(model: str, steps: int, warmup: int):
+    """Q4_0 decode projections of one token (the same matrices as the main line,
+    reference forward.metal:654-858), one matmul_forward_q4_vec_multi launch
+    per token.  At 20 bytes per 32 weights the 360M set (226 MB) fits in the
+    256 MB Infinity Cache, so two independently seeded copies are launched in
+    turn: each launch then streams its weights from HBM."""
+    be = bmhip.Backend()
+    probs = problem_list(model)
+    wls = [Workload(be, probs, "q4", BASE_SEED + k) for k in range(2)]
+    enc = be.encoder()
+    for i in range(max(warmup, 2)):
+        wls[i % 2].launch(enc)
+    enc.wait_timed()
+    # spot check: one problem of the multi launch against the single-matrix kernel
+    wl = wls[1]
+    y_all = wl.Y.read(np.float32)
+    i = 6
+    OC, C = int(wl.OC[i]), int(wl.C[i])
+    y = be.alloc(4 * OC)
+    rc = be.dispatch("matmul_forward_q4_vec4", [wl.X, wl.W, y, y, be.params(1, C, OC, 0)], (((OC + 3) >> 2) * 128, 1),
+                     (128,), offsets=[4 * int(wl.x_off[i]), int(wl.w_off[i]), 0, 0, 0])
+    yo = int(wl.y_off[i])
+    if rc != 0 or not np.array_equal(y.read(np.float32), y_all[yo:yo + OC]):
+        raise RuntimeError("Q4 multi launch differs from the single-matrix launch")
+    steps = steps - steps % 2
+    be.synchronize()
+    t0 = time.perf_counter()
+    enc = be.encoder()
+    for i in range(steps):
+        wls[i % 2].launch(enc)
+    ev_ms = enc.wait_timed()
+    wall = time.perf_counter() - t0
+    bps = wls[0].bytes_per_step
+    w_bytes = wls[0].w_bytes
+    for w in wls:
+        w.W.free()
+    be.close()
+    kern_ms = ev_ms / steps
+    achieved = bps / (kern_ms * 1e-3) / 1e9
+    log(f"[bench] q4 {model}: {kern_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
+    return {
+        "workload": f"SmolLM2-{model.upper()} Q4_0 decode projections + Q4 LM head, batch 1, one "
+                    f"matmul_forward_q4_vec_multi launch per token, two weight copies in turn",
+        "bytes_per_step": bps, "q4_weight_bytes": w_bytes, "steps": steps,
+        "kernel_us": round(kern_ms * 1e3, 3), "ms_per_step": round(wall * 1e3 / steps, 5),
+        "achieved_gbps": round(achieved, 2), "frac_hbm_peak": round(achieved / HBM_PEAK_GBS, 4),
+    }
 
 
 def gemm_leg(steps: int, warmup: int):
@@ -360,6 +418,7 @@ def main():
     ap.add_argument("--matvec", type=int, default=1, help="0: only the config-5 decode leg (for kernel traces)")
     ap.add_argument("--gemm", type=int, default=1, help="also time the config-4 prefill GEMM (0: skip)")
     ap.add_argument("--prefill", type=int, default=1, help="also time bm_forward prompt prefill (0: skip)")
+    ap.add_argument("--q4", type=int, default=1, help="also time the Q4_0 decode matvec (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
@@ -422,6 +481,7 @@ def main():
     del wl
     be.close()
 
+    q4 = q4_leg(args.model, args.steps, args.warmup) if args.q4 else None
     gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
     prefill = prefill_leg() if args.prefill else None
     ceiling = copy_ceiling()
@@ -464,6 +524,7 @@ def main():
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
         "pack_gbps_incl_upload": pack_gbps,
+        "q4_matvec": q4,
         "prefill_gemm": gemm,
         "prefill": prefill,
         "e2e_decode": e2e,

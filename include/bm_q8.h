@@ -13,6 +13,11 @@
  *   "matmul_forward_q8_vec_multi"
  *                        {params int{nprob, n_tiles}, plan (bm_q8_mv_plan),
  *                         weight arena, activation arena f32, output arena f32}
+ *   "quantize_q4"        {src f32 [n], dst Q4 blocks [n/32], params int{n}}
+ *   "quantize_q4_bf16"   {src bf16 [n], dst Q4 blocks [n/32], params int{n}}
+ *   "matmul_forward_q4_vec_multi"
+ *                        as matmul_forward_q8_vec_multi over Q4_0 rows, plan from
+ *                        bm_q4_mv_plan
  *   "matmul_forward_q8_multi"
  *                        {params int{nprob, n_tiles[, a_bf16]}, plan (bm_q8_gemm_plan),
  *                         activation arena (f32, or bf16 when a_bf16 = 1),
@@ -42,6 +47,12 @@ int  bm_q8_mv_tiles(int OC, int C);
  * bytes (plan must be 8-byte aligned and hold that many), or -1; *n_tiles
  * receives the launch's workgroup count. */
 long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
+                   const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
+
+/* The same two for a matmul_forward_q4_vec_multi launch over Q4_0 rows
+ * (20-byte blocks; w_off in bytes). */
+int  bm_q4_mv_tiles(int OC, int C);
+long bm_q4_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                    const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
 
 /* Workgroups of one C[M][N] = A[M][K] x W^T prefill GEMM in a

@@ -18,6 +18,12 @@
  *                             brute-force re-sum in a different order;
  *   orc_q8_gemm_*             row-by-row agreement with orc_q8_matvec_f64
  *                             (exact variant) and a hand-worked bf16 case;
+ *   orc_quantize_q4 / _bf16   as the Q8 pack: bit-identical to the
+ *                             reference's quant.c in oracle/_ref, committed
+ *                             golden bytes, closed-form special cases;
+ *   orc_q4_matvec_f64         one-hot and integer-exact inputs against
+ *                             closed forms, and agreement with the Q8 matvec
+ *                             on weights whose Q8 and Q4 codes coincide;
  *   orc_bf16_rne              the reference's bm_f32_to_bf16 bit trick,
  *                             checked against known roundings.
  * Parity of the Metal kernels' fp32 summation order is not pinnable (the
@@ -82,6 +88,91 @@ size_t orc_quantize_q8_bf16(const uint16_t* src, uint8_t* dst, size_t n) {
         orc_quant_block(tmp, dst + 36 * b);
     }
     return n / 32;
+}
+
+/* ---- Q4 pack: reference src/baremetal/quant.c:31-52 (block; 20-byte
+ *      {f32 scale; u8 qs[16]}, quant.h:34-42), :73-90 (fp32 / bf16 loops).
+ *      Element 2j sits in the low nibble of qs[j], element 2j+1 in the high
+ *      nibble, each a two's-complement 4-bit code in [-8, 7]. */
+
+static int orc_lround_int_clamp4(float y) {
+    if (isnan(y) || isinf(y)) return 0; /* (int)LONG_MIN, as above */
+    double t = trunc((double)y);
+    if (fabs((double)y - t) >= 0.5) t += (y < 0.0f) ? -1.0 : 1.0;
+    if (t > 7.0) t = 7.0;
+    if (t < -8.0) t = -8.0;
+    return (int)t;
+}
+
+static void orc_quant4_block(const float* p, uint8_t* dst) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+        float a = fabsf(p[i]);
+        if (a > amax) amax = a;
+    }
+    volatile float scale = amax / 7.0f;
+    float s = scale;
+    memcpy(dst, &s, 4);
+    if (s == 0.0f) {
+        memset(dst + 4, 0, 16);
+        return;
+    }
+    volatile float inv = 1.0f / s;
+    float iv = inv;
+    for (int j = 0; j < 16; j++) {
+        volatile float y0 = p[2 * j] * iv;
+        volatile float y1 = p[2 * j + 1] * iv;
+        const int lo = orc_lround_int_clamp4(y0), hi = orc_lround_int_clamp4(y1);
+        dst[4 + j] = (uint8_t)((lo & 0x0F) | ((hi & 0x0F) << 4));
+    }
+}
+
+size_t orc_quantize_q4(const float* src, uint8_t* dst, size_t n) {
+    if (n == 0 || n % 32) return 0;
+    for (size_t b = 0; b < n / 32; b++) orc_quant4_block(src + 32 * b, dst + 20 * b);
+    return n / 32;
+}
+
+size_t orc_quantize_q4_bf16(const uint16_t* src, uint8_t* dst, size_t n) {
+    if (n == 0 || n % 32) return 0;
+    float tmp[32];
+    for (size_t b = 0; b < n / 32; b++) {
+        for (int i = 0; i < 32; i++) {
+            uint32_t u = (uint32_t)src[32 * b + i] << 16;
+            memcpy(&tmp[i], &u, 4);
+        }
+        orc_quant4_block(tmp, dst + 20 * b);
+    }
+    return n / 32;
+}
+
+/* The signed 4-bit code of element j (0..31) of a Q4 block's qs[16]. */
+static inline int q4_code(const uint8_t* qs, int j) {
+    const int nib = (qs[j >> 1] >> (4 * (j & 1))) & 0x0F;
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+/* ---- Q4 matvec: reference forward.metal:654-858 (matmul_forward_q4_vec4,
+ *      _vec, and the BT>1 matmul_forward_q4): y[bt][oc] = sum_b scale[oc][b] *
+ *      sum_j x[bt][32b+j] * code[oc][b][j], exactly in double. */
+void orc_q4_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int C, int OC) {
+    const int nb = C / 32;
+    for (int bt = 0; bt < BT; bt++) {
+        const float* xr = x + (size_t)bt * C;
+        for (int oc = 0; oc < OC; oc++) {
+            const uint8_t* row = w + (size_t)oc * nb * 20;
+            double acc = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* blk = row + (size_t)b * 20;
+                float sf;
+                memcpy(&sf, blk, 4);
+                double part = 0.0;
+                for (int j = 0; j < 32; j++) part += (double)xr[32 * b + j] * (double)q4_code(blk + 4, j);
+                acc += (double)sf * part;
+            }
+            y[(size_t)bt * OC + oc] = acc;
+        }
+    }
 }
 
 /* ---- bf16 cast: reference include/baremetal/types.h:22-29 (RNE bit trick). */

@@ -15,6 +15,9 @@ uint16_t orc_bf16_rne(float f);
 void     orc_bf16_round_array(const float* src, float* dst, size_t n);
 void     orc_q8_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int C, int OC);
 void     orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N);
+size_t   orc_quantize_q4(const float* src, uint8_t* dst, size_t n);
+size_t   orc_quantize_q4_bf16(const uint16_t* src, uint8_t* dst, size_t n);
+void     orc_q4_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int C, int OC);
 
 /* CPU baseline (cpu_baseline.c): fp32 Q8 matvec in the reference's
  * arithmetic, SIMD + OpenMP over rows. */

@@ -39,6 +39,11 @@ def oracle() -> C.CDLL:
         L.orc_bf16_round_array.argtypes = [vp, vp, sz]
         L.orc_q8_matvec_f64.argtypes = [vp, vp, vp, i, i, i]
         L.orc_q8_gemm_bf16_f64.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_quantize_q4.restype = sz
+        L.orc_quantize_q4.argtypes = [vp, vp, sz]
+        L.orc_quantize_q4_bf16.restype = sz
+        L.orc_quantize_q4_bf16.argtypes = [vp, vp, sz]
+        L.orc_q4_matvec_f64.argtypes = [vp, vp, vp, i, i, i]
         L.orc_cpu_q8_matvec_f32.argtypes = [vp, vp, vp, i, i, i]
         L.orc_cpu_q8_matvec_multi.argtypes = [vp, vp, vp, i, vp, vp, vp, vp, vp, i]
         L.orc_cpu_max_threads.restype = i
@@ -67,6 +72,10 @@ def ref_quant():
         L.bmt_quantize_q8.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         L.bmt_quantize_q8_bf16.restype = C.c_size_t
         L.bmt_quantize_q8_bf16.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        L.bmt_quantize_q4.restype = C.c_size_t
+        L.bmt_quantize_q4.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+        L.bmt_quantize_q4_bf16.restype = C.c_size_t
+        L.bmt_quantize_q4_bf16.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         _r = L
     return _r
 
@@ -105,6 +114,48 @@ def ref_quantize_q8_bf16(src: np.ndarray):
     out = np.zeros(src.size // 32 * 36, dtype=np.uint8)
     n = L.bmt_quantize_q8_bf16(_p(src), _p(out), src.size)
     return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def quantize_q4(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.zeros(src.size // 32 * 20, dtype=np.uint8)
+    n = oracle().orc_quantize_q4(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def quantize_q4_bf16(src: np.ndarray) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.uint16)
+    out = np.zeros(src.size // 32 * 20, dtype=np.uint8)
+    n = oracle().orc_quantize_q4_bf16(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def ref_quantize_q4(src: np.ndarray):
+    L = ref_quant()
+    if L is None:
+        return None
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.zeros(src.size // 32 * 20, dtype=np.uint8)
+    n = L.bmt_quantize_q4(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def ref_quantize_q4_bf16(src: np.ndarray):
+    L = ref_quant()
+    if L is None:
+        return None
+    src = np.ascontiguousarray(src, dtype=np.uint16)
+    out = np.zeros(src.size // 32 * 20, dtype=np.uint8)
+    n = L.bmt_quantize_q4_bf16(_p(src), _p(out), src.size)
+    return out if n else np.zeros(0, dtype=np.uint8)
+
+
+def q4_matvec_f64(w: np.ndarray, x: np.ndarray, BT: int, C_: int, OC: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros(BT * OC, dtype=np.float64)
+    oracle().orc_q4_matvec_f64(_p(w), _p(x), _p(y), BT, C_, OC)
+    return y
 
 
 def q8_matvec_f64(w: np.ndarray, x: np.ndarray, BT: int, C_: int, OC: int) -> np.ndarray:

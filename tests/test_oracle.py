@@ -220,3 +220,93 @@ def test_cpu_baseline_matches_oracle():
     for nt in (1, 4):
         y = po.cpu_q8_matvec_f32(w, x, C, OC, nt)
         assert np.abs(y - want).max() / np.abs(want).max() < 1e-5
+
+
+# ------------------------------------------------------------------ Q4_0 (reference quant.c:31-52, forward.metal:654-858)
+
+GOLDEN_Q4 = os.path.join(os.path.dirname(__file__), "golden", "q4_pack_golden.npz")
+
+
+def q4_codes(q4: np.ndarray):
+    """(scales f32 [nb], signed codes int [nb,32]) of packed 20-byte blocks,
+    element 2j in the low nibble of byte j."""
+    b = q4.reshape(-1, 20)
+    qs = b[:, 4:].astype(np.int32)
+    nib = np.stack([qs & 0x0F, qs >> 4], axis=2).reshape(-1, 32)
+    return b[:, :4].copy().view(np.float32).ravel(), np.where(nib >= 8, nib - 16, nib)
+
+
+@pytest.mark.parametrize("case", ["special", "normal002", "normal1", "wide", "ties"])
+def test_q4_pack_matches_golden(case):
+    g = np.load(GOLDEN_Q4)
+    assert np.array_equal(po.quantize_q4(g[case + "_in"]), g[case + "_q4"])
+
+
+def test_q4_pack_bf16_matches_golden():
+    g = np.load(GOLDEN_Q4)
+    assert np.array_equal(po.quantize_q4_bf16(g["bf16_in"]), g["bf16_q4"])
+
+
+@pytest.mark.skipif(po.ref_quant() is None, reason="oracle/_ref not built (no reference tree)")
+@pytest.mark.parametrize("seed", range(4))
+def test_q4_pack_matches_reference_build(seed):
+    rng = np.random.default_rng(100 + seed)
+    n = 32 * 4096
+    x = (rng.standard_normal(n) * 0.02 if seed % 2 else rng.integers(-30, 30, n) / 4.0).astype(np.float32)
+    idx = rng.integers(0, n, 48)
+    x[idx[:16]] = np.nan
+    x[idx[16:24]] = np.inf
+    x[idx[24:32]] = -0.0
+    x[idx[32:]] = np.float32(1e-41)
+    assert np.array_equal(po.quantize_q4(x), po.ref_quantize_q4(x))
+    xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert np.array_equal(po.quantize_q4_bf16(xb), po.ref_quantize_q4_bf16(xb))
+
+
+def test_q4_pack_closed_forms():
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal(32 * 512) * 0.02).astype(np.float32)
+    s, q = q4_codes(po.quantize_q4(x))
+    xb = x.reshape(-1, 32)
+    amax = np.abs(xb).max(axis=1)
+    assert np.array_equal(s, (amax / np.float32(7.0)).astype(np.float32))
+    lead = q[np.arange(len(q)), np.abs(xb).argmax(axis=1)]
+    assert np.array_equal(np.abs(lead), np.full(len(q), 7))
+    inv = (np.float32(1.0) / s).astype(np.float32)
+    y = (xb * inv[:, None]).astype(np.float32)
+    want = np.sign(y) * np.floor(np.abs(y).astype(np.float64) + 0.5)
+    assert np.array_equal(q.astype(np.float64), np.clip(want, -8, 7))
+    # zero block: scale +0, all codes 0
+    z = po.quantize_q4(np.zeros(32, np.float32))
+    assert z.size == 20 and not z.any()
+    assert po.quantize_q4(np.zeros(48, np.float32)).size == 0
+
+
+def test_q4_matvec_nibble_order_from_reference_packer():
+    """Values already on the code grid (amax 7 -> scale 1): the reference's
+    packer stores them exactly, and a one-hot x must read each one back."""
+    v = np.array([(i % 15) - 7 for i in range(64)], np.float32)
+    v[0], v[32] = 7.0, -7.0
+    packer = po.ref_quantize_q4 if po.ref_quant() is not None else po.quantize_q4
+    w = packer(v)
+    for col in range(64):
+        x = np.zeros(64, np.float32)
+        x[col] = 1.0
+        assert po.q4_matvec_f64(w, x, 1, 64, 1)[0] == v[col]
+
+
+def test_q4_matvec_matches_q8_on_shared_codes():
+    """Blocks whose Q8 codes are the Q4 codes and share the scale give the
+    same exact product through both oracles."""
+    rng = np.random.default_rng(9)
+    OC, C, BT = 7, 96, 3
+    nb = OC * C // 32
+    codes = rng.integers(-8, 8, (nb, 32))
+    scales = rng.uniform(0.5, 2.0, nb).astype(np.float32)
+    q8 = _q8_from(scales, codes)
+    q4 = np.zeros((nb, 20), np.uint8)
+    q4[:, :4] = scales.view(np.uint8).reshape(nb, 4)
+    nib = (codes & 0x0F).astype(np.uint8)
+    q4[:, 4:] = nib[:, 0::2] | (nib[:, 1::2] << 4)
+    x = rng.standard_normal(BT * C).astype(np.float32)
+    assert np.array_equal(po.q4_matvec_f64(q4.ravel(), x, BT, C, OC), po.q8_matvec_f64(q8, x, BT, C, OC))
