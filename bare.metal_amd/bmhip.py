@@ -91,6 +91,11 @@ def lib() -> C.CDLL:
         "bm_model_set_q8_head": (i, [vp, i]),
         "bm_model_set_precision": (i, [vp, i]),
         "bm_model_set_tensor": (i, [vp, C.c_char_p, vp, sz]),
+        "bm_model_set_tensor_bf16": (i, [vp, C.c_char_p, vp, sz]),
+        "bm_load_model": (vp, [vp, C.c_char_p]),
+        "bm_load_weights": (None, [vp, C.c_char_p]),
+        "bm_arch_from_checkpoint": (i, [C.c_char_p, vp]),
+        "bm_model_arch": (i, [vp, vp]),
         "bm_model_init_synthetic": (i, [vp, u64]),
         "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
         "bm_session_set_graph": (i, [vp, i]),
@@ -376,26 +381,43 @@ def synthetic_weights(dims: dict, seed: int) -> dict:
 class Engine:
     """A context + model + session of the decode engine."""
 
-    def __init__(self, dims: dict, max_seq_len: int = 512, batch: int = 1, seed=None, weights=None,
-                 q8_head: bool = False, graph: bool = True, precision: str = "fp32"):
+    def __init__(self, dims: dict = None, max_seq_len: int = 512, batch: int = 1, seed=None, weights=None,
+                 q8_head: bool = False, graph: bool = True, precision: str = "fp32", checkpoint: str = None,
+                 tied: bool = True):
         L = lib()
-        self.dims = dict(dims)
-        self.V = dims["V"]
-        self.B = batch
         self.ctx = L.bm_create(BM_DEVICE_HIP)
         if not self.ctx:
             raise BackendError("bm_create failed (no HIP device?)")
-        self.arch = llama_arch(**{k: dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V")},
-                               max_seq_len=max_seq_len, theta=dims.get("theta", 10000.0))
-        self.arch.precision = PRECISIONS[precision]
-        self.model = L.bm_create_model(self.ctx, C.byref(self.arch))
-        if not self.model:
-            raise BackendError("bm_create_model rejected the architecture")
+        if checkpoint is not None:
+            # bm_load_model: arch from config.json, tensors from the safetensors files
+            self.model = L.bm_load_model(self.ctx, checkpoint.encode())
+            if not self.model:
+                raise BackendError(f"bm_load_model({checkpoint}) failed")
+            self.arch = Arch()
+            L.bm_model_arch(self.model, C.byref(self.arch))
+            a = self.arch
+            dims = dict(D=a.dim, H=a.hidden_dim, NH=a.n_heads, NKV=a.n_kv_heads,
+                        HD=a.head_dim or a.dim // a.n_heads, L=a.n_layers, V=a.vocab_size)
+            if precision != "fp32" and L.bm_model_set_precision(self.model, PRECISIONS[precision]) != 0:
+                raise BackendError("bm_model_set_precision failed")
+        else:
+            self.arch = llama_arch(**{k: dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V")},
+                                   max_seq_len=max_seq_len, theta=dims.get("theta", 10000.0))
+            self.arch.precision = PRECISIONS[precision]
+            self.arch.weight_tie = 1 if tied else 0
+            self.model = L.bm_create_model(self.ctx, C.byref(self.arch))
+            if not self.model:
+                raise BackendError("bm_create_model rejected the architecture")
+        self.dims = dict(dims)
+        self.V = dims["V"]
+        self.B = batch
         if L.bm_model_set_quant_bits(self.model, 8) != 0:
             raise BackendError("bm_model_set_quant_bits failed")
         if q8_head:
             L.bm_model_set_q8_head(self.model, 1)
-        if weights is not None:
+        if checkpoint is not None:
+            pass
+        elif weights is not None:
             for name, arr in weights.items():
                 a = np.ascontiguousarray(arr, dtype=np.float32)
                 if L.bm_model_set_tensor(self.model, name.encode(), _ptr(a), a.size) != 0:

@@ -53,6 +53,7 @@ int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C,
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
 int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
+int q8_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
 }
 
 #define HIP_TRY(call, what, fail)                                                   \
@@ -69,9 +70,9 @@ struct bm_context_s {
     hipStream_t s;
 };
 
-enum { T_EMB, T_LN1, T_LN2, T_LNF, T_WQ, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_COUNT };
+enum { T_EMB, T_LN1, T_LN2, T_LNF, T_WQ, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD, T_HEAD, T_COUNT };
 static const char* const k_tensor_names[T_COUNT] = {"token_embedding", "ln1", "ln2", "lnf", "wq", "wk",
-                                                     "wv", "wo", "w_gate", "w_up", "w_down"};
+                                                     "wv", "wo", "w_gate", "w_up", "w_down", "lm_head"};
 
 struct bm_model_s {
     bm_context_t* ctx;
@@ -81,6 +82,7 @@ struct bm_model_s {
     int q8_head;
     bm_precision_t precision; /* BF16: bf16 LM head rows, FP32: fp32 rows */
     float* host[T_COUNT];   /* fp32 weights in the reference layout */
+    uint16_t* host16[T_COUNT]; /* bf16 projections as a checkpoint holds them (packed to Q8 from bf16) */
     size_t count[T_COUNT];
     int set[T_COUNT];
     /* device */
@@ -89,6 +91,7 @@ struct bm_model_s {
     float* d_ln1;
     float* d_ln2;
     float* d_lnf;
+    float* d_headw;          /* untied LM head rows (fp32); NULL when tied */
     unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down */
     unsigned char* d_head8;  /* Q8 head rows (q8_head) */
     unsigned short* d_headh; /* bf16 head rows (precision BF16, no q8_head) */
@@ -178,8 +181,8 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
         return NULL;
     }
     if (a->norm != BM_NORM_RMSNORM || a->activation != BM_ACT_SWIGLU || !a->gated_mlp || a->pos_enc != BM_POS_ROPE ||
-        a->bias || !a->weight_tie || a->has_qk_norm || a->has_ffn_post_norm || a->gemma_norm || a->embed_scale) {
-        BMK_ERR("bm_create_model: only RMSNorm + SwiGLU + RoPE + tied-embedding models without biases are supported");
+        a->bias || a->has_qk_norm || a->has_ffn_post_norm || a->gemma_norm || a->embed_scale) {
+        BMK_ERR("bm_create_model: only RMSNorm + SwiGLU + RoPE models without biases are supported");
         return NULL;
     }
     if (a->precision != BM_PRECISION_FP32 && a->precision != BM_PRECISION_BF16) {
@@ -203,7 +206,7 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
     m->precision = a->precision;
     const size_t cnt[T_COUNT] = {(size_t)V * D, (size_t)L * D, (size_t)L * D, (size_t)D, (size_t)L * QD * D,
                                  (size_t)L * KV * D, (size_t)L * KV * D, (size_t)L * D * QD, (size_t)L * H * D,
-                                 (size_t)L * H * D, (size_t)L * D * H};
+                                 (size_t)L * H * D, (size_t)L * D * H, a->weight_tie ? 0 : (size_t)V * D};
     memcpy(m->count, cnt, sizeof cnt);
     const size_t mats[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
                             (size_t)H * D, (size_t)H * D, (size_t)D * H};
@@ -221,6 +224,8 @@ static void model_free_device(bm_model_t* m) {
     hipFree(m->d_ln1);
     hipFree(m->d_ln2);
     hipFree(m->d_lnf);
+    hipFree(m->d_headw);
+    m->d_headw = NULL;
     hipFree(m->d_q8);
     hipFree(m->d_head8);
     hipFree(m->d_headh);
@@ -234,7 +239,10 @@ extern "C" void bm_destroy_model(bm_model_t* m) {
     if (!m) return;
     if (m->ctx) hipStreamSynchronize(m->ctx->s);
     model_free_device(m);
-    for (int i = 0; i < T_COUNT; i++) free(m->host[i]);
+    for (int i = 0; i < T_COUNT; i++) {
+        free(m->host[i]);
+        free(m->host16[i]);
+    }
     free(m);
 }
 
@@ -274,23 +282,65 @@ static float* host_tensor(bm_model_t* m, int t) {
     return m->host[t];
 }
 
-extern "C" int bm_model_set_tensor(bm_model_t* m, const char* name, const float* data, size_t n) {
-    if (!m || !name || !data) return -1;
+static int tensor_index(const bm_model_t* m, const char* name, size_t n, const char* who) {
     for (int t = 0; t < T_COUNT; t++) {
         if (strcmp(name, k_tensor_names[t]) != 0) continue;
-        if (n != m->count[t]) {
-            BMK_ERR("bm_model_set_tensor(%s): %zu elements, expected %zu", name, n, m->count[t]);
+        if (m->count[t] == 0) {
+            BMK_ERR("%s(%s): the model has no such tensor (tied LM head)", who, name);
             return -1;
         }
+        if (n != m->count[t]) {
+            BMK_ERR("%s(%s): %zu elements, expected %zu", who, name, n, m->count[t]);
+            return -1;
+        }
+        return t;
+    }
+    BMK_ERR("%s: unknown tensor %s", who, name);
+    return -1;
+}
+
+extern "C" int bm_model_set_tensor(bm_model_t* m, const char* name, const float* data, size_t n) {
+    if (!m || !name || !data) return -1;
+    const int t = tensor_index(m, name, n, "bm_model_set_tensor");
+    if (t < 0) return -1;
+    float* dst = host_tensor(m, t);
+    if (!dst) return -1;
+    memcpy(dst, data, n * sizeof(float));
+    free(m->host16[t]);
+    m->host16[t] = NULL;
+    m->set[t] = 1;
+    if (m->compiled) model_free_device(m);
+    return 0;
+}
+
+extern "C" int bm_model_set_tensor_bf16(bm_model_t* m, const char* name, const uint16_t* data, size_t n) {
+    if (!m || !name || !data) return -1;
+    const int t = tensor_index(m, name, n, "bm_model_set_tensor_bf16");
+    if (t < 0) return -1;
+    if (t >= T_WQ && t <= T_WD) {
+        /* projections stay bf16 until the device packs them */
+        if (!m->host16[t]) m->host16[t] = (uint16_t*)malloc(n * sizeof(uint16_t));
+        if (!m->host16[t]) return -1;
+        memcpy(m->host16[t], data, n * sizeof(uint16_t));
+        free(m->host[t]);
+        m->host[t] = NULL;
+    } else {
         float* dst = host_tensor(m, t);
         if (!dst) return -1;
-        memcpy(dst, data, n * sizeof(float));
-        m->set[t] = 1;
-        if (m->compiled) model_free_device(m);
-        return 0;
+        for (size_t i = 0; i < n; i++) {
+            const uint32_t u = (uint32_t)data[i] << 16; /* exact widening */
+            memcpy(dst + i, &u, 4);
+        }
     }
-    BMK_ERR("bm_model_set_tensor: unknown tensor %s", name);
-    return -1;
+    m->set[t] = 1;
+    if (m->compiled) model_free_device(m);
+    return 0;
+}
+
+extern "C" int bm_model_arch(const bm_model_t* m, bm_arch_t* out) {
+    if (!m || !out) return -1;
+    *out = m->arch;
+    return 0;
 }
 
 extern "C" int bm_model_init_synthetic(bm_model_t* m, uint64_t seed) {
@@ -298,8 +348,12 @@ extern "C" int bm_model_init_synthetic(bm_model_t* m, uint64_t seed) {
     const size_t per[T_COUNT] = {0, 0, 0, 0, (size_t)m->QD * m->D, (size_t)m->KV * m->D, (size_t)m->KV * m->D,
                                  (size_t)m->D * m->QD, (size_t)m->H * m->D, (size_t)m->H * m->D,
                                  (size_t)m->D * m->H};
-    for (int t = 0; t < T_COUNT; t++)
+    for (int t = 0; t < T_COUNT; t++) {
+        if (m->count[t] == 0) continue;
+        free(m->host16[t]);
+        m->host16[t] = NULL;
         if (!host_tensor(m, t)) return -1;
+    }
     bm_synth_normal_f32(bm_synth_tensor_seed(seed, 5, 0xFFFF, 0), 0.02f, m->host[T_EMB], m->count[T_EMB]);
     bm_synth_fill_f32(1.0f, m->host[T_LN1], m->count[T_LN1]);
     bm_synth_fill_f32(1.0f, m->host[T_LN2], m->count[T_LN2]);
@@ -308,6 +362,8 @@ extern "C" int bm_model_init_synthetic(bm_model_t* m, uint64_t seed) {
         for (int l = 0; l < m->L; l++)
             bm_synth_normal_f32(bm_synth_tensor_seed(seed, 5, l, t - T_WQ + 1), 0.02f, m->host[t] + (size_t)l * per[t],
                                 per[t]);
+    if (m->count[T_HEAD]) /* untied: a head of its own, id 8 */
+        bm_synth_normal_f32(bm_synth_tensor_seed(seed, 5, 0xFFFF, 8), 0.02f, m->host[T_HEAD], m->count[T_HEAD]);
     for (int t = 0; t < T_COUNT; t++) m->set[t] = 1;
     if (m->compiled) model_free_device(m);
     return 0;
@@ -322,16 +378,18 @@ static int upload(float** dst, const float* src, size_t n, hipStream_t s) {
 static int model_compile(bm_model_t* m) {
     if (m->compiled) return 0;
     for (int t = 0; t < T_COUNT; t++)
-        if (!m->set[t]) {
+        if (m->count[t] && !m->set[t]) {
             BMK_ERR("bm_compile: tensor %s was never set", k_tensor_names[t]);
             return -1;
         }
     hipStream_t s = m->ctx->s;
     if (upload(&m->d_emb, m->host[T_EMB], m->count[T_EMB], s) || upload(&m->d_ln1, m->host[T_LN1], m->count[T_LN1], s) ||
-        upload(&m->d_ln2, m->host[T_LN2], m->count[T_LN2], s) || upload(&m->d_lnf, m->host[T_LNF], m->count[T_LNF], s)) {
+        upload(&m->d_ln2, m->host[T_LN2], m->count[T_LN2], s) || upload(&m->d_lnf, m->host[T_LNF], m->count[T_LNF], s) ||
+        (m->count[T_HEAD] && upload(&m->d_headw, m->host[T_HEAD], m->count[T_HEAD], s))) {
         model_free_device(m);
         return -1;
     }
+    const float* head_src = m->d_headw ? m->d_headw : m->d_emb; /* fp32 head rows */
     HIP_TRY(hipMalloc(&m->d_q8, m->layer_bytes * m->L), "hipMalloc", { model_free_device(m); return -1; });
     const int D = m->D, H = m->H, QD = m->QD, KV = m->KV;
     const size_t per[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
@@ -344,18 +402,25 @@ static int model_compile(bm_model_t* m) {
     int rc = 0;
     for (int l = 0; l < m->L && rc == 0; l++)
         for (int i = 0; i < 7 && rc == 0; i++) {
-            const float* src = m->host[src_t[i]] + (size_t)l * per[i];
-            if (hipMemcpyAsync(stage, src, per[i] * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
-            else rc = q8_pack_f32(stage, m->d_q8 + (size_t)l * m->layer_bytes + m->off[i], (long)per[i], s);
+            unsigned char* dst = m->d_q8 + (size_t)l * m->layer_bytes + m->off[i];
+            if (m->host16[src_t[i]]) { /* bf16 checkpoint: the reference's bmt_quantize_q8_bf16 on the device */
+                const uint16_t* src = m->host16[src_t[i]] + (size_t)l * per[i];
+                if (hipMemcpyAsync(stage, src, per[i] * 2, hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
+                else rc = q8_pack_bf16(stage, dst, (long)per[i], s);
+            } else {
+                const float* src = m->host[src_t[i]] + (size_t)l * per[i];
+                if (hipMemcpyAsync(stage, src, per[i] * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
+                else rc = q8_pack_f32(stage, dst, (long)per[i], s);
+            }
         }
     if (rc == 0 && m->q8_head) {
         if (hipMalloc(&m->d_head8, q8_bytes((size_t)m->V * D)) != hipSuccess) rc = -1;
-        else rc = q8_pack_f32(m->d_emb, m->d_head8, (long)m->V * D, s);
+        else rc = q8_pack_f32(head_src, m->d_head8, (long)m->V * D, s);
     } else if (rc == 0 && head_format(m) == 2) {
-        /* bf16 rows of the tied embedding, rounded to nearest even as the
-         * reference's bf16 upload does (scheduler.c:369-371,395-402) */
+        /* bf16 rows of the head (the tied embedding or lm_head), rounded to
+         * nearest even as the reference's bf16 upload does (scheduler.c:369-371,395-402) */
         if (hipMalloc(&m->d_headh, (size_t)m->V * D * 2) != hipSuccess) rc = -1;
-        else rc = gm_cast_bf16(m->d_emb, m->d_headh, (long)m->V * D, s);
+        else rc = gm_cast_bf16(head_src, m->d_headh, (long)m->V * D, s);
     }
     if (hipStreamSynchronize(s) != hipSuccess) rc = -1;
     hipFree(stage);
@@ -456,7 +521,8 @@ static int enqueue_step(bm_session_t* S) {
     }
     DecHead hd;
     memset(&hd, 0, sizeof hd);
-    hd.x = S->x; hd.norm_w = m->d_lnf; hd.w = m->d_emb; hd.wq = m->q8_head ? m->d_head8 : NULL;
+    hd.x = S->x; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
+    hd.wq = m->q8_head ? m->d_head8 : NULL;
     hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
     hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
@@ -815,7 +881,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     if (dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_lnf, S->pf_a16, n, D, eps, s)) return -1;
     DecHead hd;
     memset(&hd, 0, sizeof hd);
-    hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_emb;
+    hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
     hd.wq = m->q8_head ? m->d_head8 : NULL;
     hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
     hd.logits = S->logits; hd.st = NULL; hd.out_tokens = NULL;

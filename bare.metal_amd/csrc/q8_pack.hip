@@ -201,6 +201,16 @@ extern "C" int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStre
     return 0;
 }
 
+/* Engine-side pack of n bf16 values (the reference's bmt_quantize_q8_bf16;
+ * src 8-byte aligned, n a positive multiple of 32). */
+extern "C" int q8_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s) {
+    const long nblocks = n / 32;
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q8<true>, dim3(grid), dim3(256), 0, s, src, dst, nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
 extern "C" int bmk_launch_quantize_q8(const bmk_launch_t* a) { return launch_quantize<false>(a); }
 extern "C" int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a) { return launch_quantize<true>(a); }
 

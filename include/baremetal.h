@@ -21,8 +21,10 @@
  *     776-778): fp32 rows (BM_PRECISION_FP32) or bf16 rows rounded to
  *     nearest even (BM_PRECISION_BF16, what bm_get_supported_precision
  *     returns); or, on request, Q8 rows.  BM_PRECISION_FP16 is rejected.
- *   - Weights come from bm_model_set_tensor or bm_model_init_synthetic;
- *     checkpoint files are not read.
+ *   - Weights come from a Hugging Face checkpoint directory (bm_load_model,
+ *     bm_load_weights), bm_model_set_tensor(_bf16) or
+ *     bm_model_init_synthetic; the reference's own .bin checkpoint format
+ *     and the tokenizer are not read.
  *   - bm_forward over several tokens at position 0 of a batch-1 session
  *     runs the whole prompt in one pass, as the reference's prefill does
  *     (reference src/baremetal/session.c:86-149); elsewhere it steps the
@@ -96,10 +98,16 @@ void           bm_destroy(bm_context_t* ctx);
 bm_precision_t bm_get_supported_precision(bm_context_t* ctx);
 
 /* Accepts the SmolLM2 / llama family the decode path implements: RMSNorm,
- * SwiGLU gated MLP, RoPE, GQA, tied embeddings, no biases.  NULL (logged)
+ * SwiGLU gated MLP, RoPE, GQA, tied or untied head, no biases.  NULL (logged)
  * for anything else. */
 bm_model_t*    bm_create_model(bm_context_t* ctx, const bm_arch_t* arch);
 void           bm_destroy_model(bm_model_t* model);
+
+/* Reference include/baremetal.h:127: weights from a checkpoint directory
+ * (config.json + model.safetensors, or shards listed by
+ * model.safetensors.index.json; F32 or BF16 tensors, llama tensor names).
+ * The model must have the shape config.json describes; errors are logged. */
+void           bm_load_weights(bm_model_t* model, const char* path);
 
 /* Uploads the weights and packs every projection to Q8 on the device
  * (the reference quantizes on the host at session creation,
@@ -147,7 +155,7 @@ const char*    bm_get_arch_name(const bm_model_t* model);
 /* Quantization of the projections: 8 (Q8_0) is the only value accepted
  * (the reference's CLI sets model->quant_bits, reference tools/cli.c:886). */
 int            bm_model_set_quant_bits(bm_model_t* model, int bits);
-/* 1: the LM head runs on Q8 rows quantized from the tied embedding;
+/* 1: the LM head runs on Q8 rows quantized from the head (the tied embedding or lm_head);
  * 0 (default): rows in the model's precision, as the reference. */
 int            bm_model_set_q8_head(bm_model_t* model, int on);
 /* The reference's CLI writes model->precision after loading (reference
@@ -161,14 +169,33 @@ int            bm_model_set_precision(bm_model_t* model, bm_precision_t precisio
  *   "token_embedding" V*D   "ln1" L*D   "ln2" L*D   "lnf" D
  *   "wq" L*NH*HD*D  "wk" L*KV*D  "wv" L*KV*D  "wo" L*D*NH*HD
  *   "w_gate" L*H*D  "w_up" L*H*D  "w_down" L*D*H
+ *   "lm_head" V*D (untied models only, weight_tie 0)
  * Returns 0, or -1 for an unknown name or a wrong count. */
 int            bm_model_set_tensor(bm_model_t* model, const char* name, const float* data, size_t n);
+
+/* bf16 weights (a checkpoint's raw tensor): projections stay bf16 until
+ * bm_compile packs them to Q8 on the device from bf16 (the reference's
+ * bmt_quantize_q8_bf16); other tensors are widened exactly.  Same names. */
+int            bm_model_set_tensor_bf16(bm_model_t* model, const char* name, const uint16_t* data, size_t n);
+
+/* A model from a Hugging Face checkpoint directory: config.json gives the
+ * arch (reference src/baremetal/config.c:128-297; no lm_head tensor means a
+ * tied head), then bm_load_weights.  NULL (logged) on error. */
+bm_model_t*    bm_load_model(bm_context_t* ctx, const char* path);
+
+/* The arch bm_load_model would build from a checkpoint directory, without
+ * reading the tensors' data (host only).  Returns 0, or -1. */
+int            bm_arch_from_checkpoint(const char* path, bm_arch_t* arch);
+
+/* The model's arch as created. */
+int            bm_model_arch(const bm_model_t* model, bm_arch_t* arch);
 
 /* Random-init weights (no checkpoint): every projection of every layer and
  * the tied embedding drawn from N(0, 0.02) with the seed
  * bm_synth_tensor_seed(seed, 5, layer, id) (include/bm_synth.h), id =
  * 0 token_embedding (layer 0xFFFF), 1 wq, 2 wk, 3 wv, 4 wo, 5 w_gate,
- * 6 w_up, 7 w_down; RMSNorm gains 1.0. */
+ * 6 w_up, 7 w_down, 8 lm_head of an untied model (layer 0xFFFF);
+ * RMSNorm gains 1.0. */
 int            bm_model_init_synthetic(bm_model_t* model, uint64_t seed);
 
 /* A session that steps `batch` independent sequences in lockstep (all at

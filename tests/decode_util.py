@@ -20,14 +20,18 @@ def q8_arrays(w: dict) -> dict:
 
 
 def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads: int = 8,
-                   precision: str = "fp32") -> po.Decoder:
-    """precision "bf16": the head rows are the tied embedding rounded to bf16
-    (reference scheduler.c:395-402), widened back to fp32 exactly."""
+                   precision: str = "fp32", head_f32=None) -> po.Decoder:
+    """precision "bf16": the head rows are rounded to bf16 (reference
+    scheduler.c:395-402), widened back to fp32 exactly.  head_f32: the rows of
+    an untied head (default: the tied embedding)."""
     arrs = q8_arrays(w)
+    head = w["token_embedding"] if head_f32 is None else np.ascontiguousarray(head_f32, np.float32)
     if q8_head:
-        arrs["head_q8"] = po.quantize_q8(w["token_embedding"])
+        arrs["head_q8"] = po.quantize_q8(head)
     elif precision == "bf16":
-        arrs["head_f32"] = po.bf16_rne(w["token_embedding"])
+        arrs["head_f32"] = po.bf16_rne(head)
+    elif head_f32 is not None:
+        arrs["head_f32"] = head
     d = dict(dims)
     d["MS"] = ms
     return po.Decoder(d, arrs, nthreads=nthreads)
@@ -35,3 +39,85 @@ def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads
 
 def normwise(y, r):
     return float(np.abs(np.asarray(y, np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+# ------------------------------------------------------------------ Hugging Face checkpoint directories
+
+HF_LAYER = {  # engine tensor -> per-layer checkpoint name (reference src/baremetal/config.c:13-31)
+    "ln1": "input_layernorm.weight", "wq": "self_attn.q_proj.weight", "wk": "self_attn.k_proj.weight",
+    "wv": "self_attn.v_proj.weight", "wo": "self_attn.o_proj.weight", "ln2": "post_attention_layernorm.weight",
+    "w_gate": "mlp.gate_proj.weight", "w_up": "mlp.up_proj.weight", "w_down": "mlp.down_proj.weight",
+}
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even bf16 bits of fp32 values (the oracle's rounding)."""
+    return (po.bf16_rne(a).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def widen_bf16(a: np.ndarray) -> np.ndarray:
+    return po.bf16_rne(a)
+
+
+def hf_tensors(dims: dict, w: dict) -> dict:
+    """fp32 engine-layout weights as the checkpoint's named 2-D / 1-D tensors."""
+    D, H, NH, NKV, HD, L, V = (dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V"))
+    shapes = {"ln1": (D,), "ln2": (D,), "wq": (NH * HD, D), "wk": (NKV * HD, D), "wv": (NKV * HD, D),
+              "wo": (D, NH * HD), "w_gate": (H, D), "w_up": (H, D), "w_down": (D, H)}
+    out = {"model.embed_tokens.weight": w["token_embedding"].reshape(V, D), "model.norm.weight": w["lnf"]}
+    for name, suffix in HF_LAYER.items():
+        per = int(np.prod(shapes[name]))
+        for l in range(L):
+            out[f"model.layers.{l}.{suffix}"] = w[name][l * per:(l + 1) * per].reshape(shapes[name])
+    if "lm_head" in w:
+        out["lm_head.weight"] = w["lm_head"].reshape(V, D)
+    return out
+
+
+def write_safetensors(path: str, tensors: dict, dtype: str):
+    """The safetensors layout: u64 little-endian header length, JSON header,
+    then the tensors' bytes (F32 or BF16, row-major)."""
+    import json
+    header, blobs, off = {"__metadata__": {"format": "pt"}}, [], 0
+    for name, a in tensors.items():
+        raw = (bf16_bits(a) if dtype == "BF16" else np.ascontiguousarray(a, np.float32)).tobytes()
+        header[name] = {"dtype": dtype, "shape": list(a.shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little"))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def write_checkpoint(path: str, dims: dict, w: dict, dtype: str = "BF16", shards: int = 1, tied: bool = True,
+                     extra_config: dict = None):
+    """A Hugging Face llama checkpoint directory holding the weights w."""
+    import json
+    import os
+    os.makedirs(path, exist_ok=True)
+    D, H, NH, NKV, HD, L, V = (dims[k] for k in ("D", "H", "NH", "NKV", "HD", "L", "V"))
+    cfg = {"architectures": ["LlamaForCausalLM"], "model_type": "llama", "hidden_size": D,
+           "intermediate_size": H, "num_hidden_layers": L, "num_attention_heads": NH,
+           "num_key_value_heads": NKV, "vocab_size": V, "max_position_embeddings": 2048,
+           "rms_norm_eps": 1e-5, "rope_theta": dims.get("theta", 10000.0), "hidden_act": "silu",
+           "tie_word_embeddings": tied, "head_dim": HD, "torch_dtype": "bfloat16"}
+    cfg.update(extra_config or {})
+    with open(os.path.join(path, "config.json"), "w") as f:
+        json.dump(cfg, f)
+    t = hf_tensors(dims, w)
+    names = list(t)
+    if shards == 1:
+        write_safetensors(os.path.join(path, "model.safetensors"), t, dtype)
+        return
+    parts = [names[i::shards] for i in range(shards)]
+    wmap = {}
+    for i, part in enumerate(parts):
+        fn = f"model-{i + 1:05d}-of-{shards:05d}.safetensors"
+        write_safetensors(os.path.join(path, fn), {n: t[n] for n in part}, dtype)
+        wmap.update({n: fn for n in part})
+    with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {}, "weight_map": wmap}, f)
