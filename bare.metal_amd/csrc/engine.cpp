@@ -131,6 +131,8 @@ struct bm_session_s {
     double prof_phase[BM_PROF_PHASES]; /* ms per phase kind, summed over layers and steps */
     long prof_steps;
     hipEvent_t ev0, ev1;
+    double busy_ms;          /* GPU time of host-driven steps and prefills (HIP events) */
+    unsigned long long launches; /* step graphs / prefill passes submitted */
     hipEvent_t* pev;     /* one event after every kernel of a profiled step */
     int* pkind;          /* phase kind of the interval that ends at pev[i] */
     int n_pev;
@@ -710,10 +712,15 @@ static float* step_host(bm_session_t* S, const int* tokens) {
     memcpy(&S->h_io[S->B], &one, 4);
     HIP_TRY(hipMemcpyAsync(&S->st->host_mode, &S->h_io[S->B], 4, hipMemcpyHostToDevice, S->ctx->s), "mode write",
             return NULL);
+    HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
     if (launch_step(S) != 0) return NULL;
+    HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "event", return NULL);
     HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)S->B * m->V * 4, hipMemcpyDeviceToHost, S->ctx->s),
             "logits read", return NULL);
     HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess) S->busy_ms += ms;
+    S->launches++;
     return S->h_logits;
 }
 
@@ -908,7 +915,15 @@ extern "C" float* bm_forward(bm_session_t* S, const int* tokens, int n_tokens) {
     if (!S || (!tokens && n_tokens > 0)) return NULL;
     if (n_tokens <= 0) return S->h_logits;
     if (n_tokens > 1 && S->pos == 0 && S->B == 1 && n_tokens <= S->MS && (size_t)n_tokens <= S->h_io_cap) {
+        HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+        HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
         if (prefill(S, tokens, n_tokens) != 0) return NULL;
+        float ms = 0.f;
+        /* prefill ends synchronized on the logits read: ev0 to now is its GPU span */
+        if (hipEventRecord(S->ev1, S->ctx->s) == hipSuccess && hipEventSynchronize(S->ev1) == hipSuccess &&
+            hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess)
+            S->busy_ms += ms;
+        S->launches++;
         return S->h_logits;
     }
     float* out = S->h_logits;
@@ -917,6 +932,17 @@ extern "C" float* bm_forward(bm_session_t* S, const int* tokens, int n_tokens) {
         if (!out) return NULL;
     }
     return out;
+}
+
+extern "C" int bm_session_gpu_stats(bm_session_t* S, double* busy_ms, unsigned long long* launches, int reset) {
+    if (!S) return -1;
+    if (busy_ms) *busy_ms = S->busy_ms;
+    if (launches) *launches = S->launches;
+    if (reset) {
+        S->busy_ms = 0.0;
+        S->launches = 0;
+    }
+    return 0;
 }
 
 extern "C" void bm_reset_session(bm_session_t* S) {

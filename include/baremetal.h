@@ -218,6 +218,13 @@ int            bm_generate_greedy(bm_session_t* sess, const int* prompt, int n_p
  * captured graph (same kernels, same results).  Default 1. */
 int            bm_session_set_graph(bm_session_t* sess, int on);
 
+/* GPU time (HIP events around each submission) and submissions of the
+ * session's host-driven steps and one-pass prefills, the counterpart of the
+ * reference backend's busy time and command-buffer count
+ * (reference src/backend/backend.h:32-35); reset != 0 zeroes both after
+ * reading.  Returns 0, or -1. */
+int            bm_session_gpu_stats(bm_session_t* sess, double* busy_ms, unsigned long long* launches, int reset);
+
 /* Per-kernel-kind GPU ms accumulated since bm_profile_begin, in step order:
  * [0] embedding, [1] RMSNorm + q/k/v, [2] RoPE + KV append + attention,
  * [3] o + residual, [4] RMSNorm + gate/up + SwiGLU, [5] down + residual,
