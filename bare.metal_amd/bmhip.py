@@ -383,7 +383,7 @@ class Engine:
 
     def __init__(self, dims: dict = None, max_seq_len: int = 512, batch: int = 1, seed=None, weights=None,
                  q8_head: bool = False, graph: bool = True, precision: str = "fp32", checkpoint: str = None,
-                 tied: bool = True):
+                 tied: bool = True, quant_bits: int = 8):
         L = lib()
         self.ctx = L.bm_create(BM_DEVICE_HIP)
         if not self.ctx:
@@ -411,7 +411,7 @@ class Engine:
         self.dims = dict(dims)
         self.V = dims["V"]
         self.B = batch
-        if L.bm_model_set_quant_bits(self.model, 8) != 0:
+        if L.bm_model_set_quant_bits(self.model, quant_bits) != 0:
             raise BackendError("bm_model_set_quant_bits failed")
         if q8_head:
             L.bm_model_set_q8_head(self.model, 1)

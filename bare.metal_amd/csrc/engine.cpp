@@ -48,6 +48,10 @@ int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short*
                      hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, hipStream_t s);
 int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s);
+int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
+int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
+int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
+                       int nprob, int n_tiles, hipStream_t s);
 int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
                     int n_tiles, hipStream_t s);
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
@@ -92,7 +96,7 @@ struct bm_model_s {
     float* d_ln2;
     float* d_lnf;
     float* d_headw;          /* untied LM head rows (fp32); NULL when tied */
-    unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down */
+    unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down (Q8_0 or Q4_0 blocks) */
     unsigned char* d_head8;  /* Q8 head rows (q8_head) */
     unsigned short* d_headh; /* bf16 head rows (precision BF16, no q8_head) */
     size_t off[7];           /* byte offset of each matrix inside one layer's slice */
@@ -174,6 +178,21 @@ extern "C" bm_precision_t bm_get_supported_precision(bm_context_t* ctx) {
 
 static size_t q8_bytes(size_t n) { return n / 32 * 36; }
 
+/* Byte offsets of the 7 projections inside one layer's slice of the
+ * arena, for the model's block format (Q8_0: 36 bytes, Q4_0: 20 bytes per 32). */
+static void layer_layout(bm_model_t* m) {
+    const size_t mats[7] = {(size_t)m->QD * m->D, (size_t)m->KV * m->D, (size_t)m->KV * m->D,
+                            (size_t)m->D * m->QD, (size_t)m->H * m->D,  (size_t)m->H * m->D,
+                            (size_t)m->D * m->H};
+    const size_t blk = m->quant_bits == 4 ? 20 : 36;
+    size_t o = 0;
+    for (int i = 0; i < 7; i++) {
+        m->off[i] = o;
+        o += mats[i] / 32 * blk;
+    }
+    m->layer_bytes = o;
+}
+
 extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
     if (!ctx || !a) return NULL;
     const int D = a->dim, H = a->hidden_dim, NH = a->n_heads, NKV = a->n_kv_heads, L = a->n_layers, V = a->vocab_size;
@@ -210,14 +229,7 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
                                  (size_t)L * KV * D, (size_t)L * KV * D, (size_t)L * D * QD, (size_t)L * H * D,
                                  (size_t)L * H * D, (size_t)L * D * H, a->weight_tie ? 0 : (size_t)V * D};
     memcpy(m->count, cnt, sizeof cnt);
-    const size_t mats[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
-                            (size_t)H * D, (size_t)H * D, (size_t)D * H};
-    size_t o = 0;
-    for (int i = 0; i < 7; i++) {
-        m->off[i] = o;
-        o += q8_bytes(mats[i]);
-    }
-    m->layer_bytes = o;
+    layer_layout(m);
     return m;
 }
 
@@ -250,11 +262,13 @@ extern "C" void bm_destroy_model(bm_model_t* m) {
 
 extern "C" int bm_model_set_quant_bits(bm_model_t* m, int bits) {
     if (!m) return -1;
-    if (bits != 8) {
-        BMK_ERR("bm_model_set_quant_bits: the MI355X path implements Q8 projections only (got %d)", bits);
+    if (bits != 8 && bits != 4) {
+        BMK_ERR("bm_model_set_quant_bits: the MI355X path runs Q8_0 or Q4_0 projections (got %d)", bits);
         return -1;
     }
-    m->quant_bits = 8;
+    if (m->compiled && bits != m->quant_bits) model_free_device(m);
+    m->quant_bits = bits;
+    layer_layout(m);
     return 0;
 }
 
@@ -405,14 +419,15 @@ static int model_compile(bm_model_t* m) {
     for (int l = 0; l < m->L && rc == 0; l++)
         for (int i = 0; i < 7 && rc == 0; i++) {
             unsigned char* dst = m->d_q8 + (size_t)l * m->layer_bytes + m->off[i];
-            if (m->host16[src_t[i]]) { /* bf16 checkpoint: the reference's bmt_quantize_q8_bf16 on the device */
+            const bool q4 = m->quant_bits == 4;
+            if (m->host16[src_t[i]]) { /* bf16 checkpoint: the reference's bmt_quantize_q{8,4}_bf16 on the device */
                 const uint16_t* src = m->host16[src_t[i]] + (size_t)l * per[i];
                 if (hipMemcpyAsync(stage, src, per[i] * 2, hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
-                else rc = q8_pack_bf16(stage, dst, (long)per[i], s);
+                else rc = q4 ? q4_pack_bf16(stage, dst, (long)per[i], s) : q8_pack_bf16(stage, dst, (long)per[i], s);
             } else {
                 const float* src = m->host[src_t[i]] + (size_t)l * per[i];
                 if (hipMemcpyAsync(stage, src, per[i] * sizeof(float), hipMemcpyHostToDevice, s) != hipSuccess) rc = -1;
-                else rc = q8_pack_f32(stage, dst, (long)per[i], s);
+                else rc = q4 ? q4_pack_f32(stage, dst, (long)per[i], s) : q8_pack_f32(stage, dst, (long)per[i], s);
             }
         }
     if (rc == 0 && m->q8_head) {
@@ -481,6 +496,7 @@ static int enqueue_step(bm_session_t* S) {
         const unsigned char* wl = m->d_q8 + (size_t)l * m->layer_bytes;
         DecMv mv;
         memset(&mv, 0, sizeof mv);
+        mv.qf = m->quant_bits == 4;
         DecAttn at;
         memset(&at, 0, sizeof at);
         at.q = S->q; at.k = S->k; at.v = S->v; at.kvc = S->kvc; at.out = S->att; at.st = S->st;
@@ -503,12 +519,14 @@ static int enqueue_step(bm_session_t* S) {
         if (dec_launch_attn(&at, B, s) || mark(S, PH_ATTN)) return -1;
         /* o + residual */
         memset(&mv, 0, sizeof mv);
+        mv.qf = m->quant_bits == 4;
         mv.x = S->att; mv.C = m->QD; mv.B = B; mv.ldx = m->QD; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[3]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->QD, 0);
         if (dec_launch_mv(&mv, s) || mark(S, PH_O)) return -1;
         /* RMSNorm + gate, up + SwiGLU */
         memset(&mv, 0, sizeof mv);
+        mv.qf = m->quant_bits == 4;
         mv.x = S->x; mv.norm_w = m->d_ln2 + (size_t)l * D; mv.eps = eps; mv.C = D; mv.B = B; mv.ldx = D;
         mv.nmat = 1; mv.glu = 1;
         mv.w[0] = wl + m->off[4]; mv.w[1] = wl + m->off[5]; mv.y[0] = S->h; mv.OC[0] = m->H;
@@ -516,6 +534,7 @@ static int enqueue_step(bm_session_t* S) {
         if (dec_launch_mv(&mv, s) || mark(S, PH_GATEUP)) return -1;
         /* down + residual */
         memset(&mv, 0, sizeof mv);
+        mv.qf = m->quant_bits == 4;
         mv.x = S->h; mv.C = m->H; mv.B = B; mv.ldx = m->H; mv.nmat = 1; mv.residual = 1;
         mv.w[0] = wl + m->off[6]; mv.y[0] = S->x; mv.OC[0] = D;
         mv.tile0[1] = dec_mv_tiles(D, m->H, 0);
@@ -867,7 +886,8 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     float* gt = S->pf_gu;
     float* up = gt + (size_t)n * H;
     auto gemm = [&](const PfGemm& p, float* C) {
-        return gm_launch_multi(S->pf_a16, 1, m->d_q8, C, S->pf_plan + p.off, p.nprob, p.n_tiles, s);
+        return gm_launch_multi_qf(S->pf_a16, 1, m->quant_bits == 4, m->d_q8, C, S->pf_plan + p.off, p.nprob,
+                                  p.n_tiles, s);
     };
     if (dec_pf_embed(S->pf_tok, m->d_emb, S->pf_x, n, D, s)) return -1;
     for (int l = 0; l < L; l++) {

@@ -16,6 +16,7 @@ int bmk_launch_quantize_q4(const bmk_launch_t* a);
 int bmk_launch_quantize_q4_bf16(const bmk_launch_t* a);
 int bmk_launch_q4_matvec(const bmk_launch_t* a);
 int bmk_launch_q4_matvec_multi(const bmk_launch_t* a);
+int bmk_launch_q4_gemm_multi(const bmk_launch_t* a);
 int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
@@ -53,8 +54,10 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"matmul_forward_q4_vec4", 5, B(4), B(3), bmk_launch_q4_matvec},
     {"matmul_forward_q4_vec", 5, B(4), B(3), bmk_launch_q4_matvec},
     {"matmul_forward_q4", 5, B(4), B(3), bmk_launch_q4_matvec},
-    /* new: every Q4 matvec of a decode token in one launch (same plan as the Q8 one) */
+    /* new: every Q4 matvec of a decode token in one launch (plan: bm_q4_mv_plan) */
     {"matmul_forward_q4_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q4_matvec_multi, B(1)},
+    /* new: many prefill GEMMs over Q4_0 weights in one launch (as matmul_forward_q8_multi) */
+    {"matmul_forward_q4_multi", 5, B(0) | B(1), B(4), bmk_launch_q4_gemm_multi, B(1)},
     /* new: every Q8 matvec of a decode token in one launch; {params{nprob,n_tiles},
      * plan{MvDesc[nprob], u32 tile_map[n_tiles]}, weight arena, x arena, y arena} */
     {"matmul_forward_q8_vec_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_matvec_multi, B(1)},

@@ -40,6 +40,9 @@ extern "C" {
 #endif
 int gm_tiles_for(int M, int N);
 int gm_launch_group(GmGroup* g, hipStream_t s);
+int gm_launch_group_qf(GmGroup* g, int qf, hipStream_t s);
+int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
+                       int nprob, int n_tiles, hipStream_t s);
 #ifdef __cplusplus
 }
 #endif

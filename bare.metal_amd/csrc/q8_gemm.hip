@@ -25,10 +25,16 @@
  */
 #include "bmk.h"
 #include "q8_gemm.h"
+#include "q8_common.h"
 
 #include <stdlib.h>
 
 namespace {
+
+using bmk::QFmt;
+using bmk::QF_Q8;
+using bmk::QF_Q4;
+using bmk::q4_code;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -57,12 +63,12 @@ __device__ __forceinline__ float sbyte(unsigned int w, int k) { return (float)(s
  * rows t/8 + 32p (p < 4), columns 8*(t%8) .. +8.  Either way the lanes of a
  * row read it contiguously and a wave instruction covers whole rows.
  * W: row t/2, Q8 block 2*step + t%2 (36 bytes: scale, 32 int8). */
-template <bool ABF16>
+template <bool ABF16, int QF = QF_Q8>
 struct Stage {
     float4 a[ABF16 ? 1 : 8];
     uint4 ab[ABF16 ? 4 : 1];
     float s;
-    uint4 q[2];
+    uint4 q[QF == QF_Q4 ? 1 : 2]; /* the block's 32 codes: int8 (Q8_0) or nibbles (Q4_0) */
 };
 
 __device__ __forceinline__ uint4 dq8(const uint4& q, int half, float s) {
@@ -72,6 +78,18 @@ __device__ __forceinline__ uint4 dq8(const uint4& q, int half, float s) {
     r.y = pk_bf16(sbyte(w0, 2) * s, sbyte(w0, 3) * s);
     r.z = pk_bf16(sbyte(w1, 0) * s, sbyte(w1, 1) * s);
     r.w = pk_bf16(sbyte(w1, 2) * s, sbyte(w1, 3) * s);
+    return r;
+}
+
+/* 8 Q4_0 codes (dword `part` of the block's 16 code bytes), each
+ * times the scale and rounded to bf16, as 8 packed bf16 */
+__device__ __forceinline__ uint4 dq4(const uint4& q, int part, float s) {
+    const unsigned int w = part == 0 ? q.x : part == 1 ? q.y : part == 2 ? q.z : q.w;
+    uint4 r;
+    r.x = pk_bf16(q4_code(w, 0) * s, q4_code(w, 1) * s);
+    r.y = pk_bf16(q4_code(w, 2) * s, q4_code(w, 3) * s);
+    r.z = pk_bf16(q4_code(w, 4) * s, q4_code(w, 5) * s);
+    r.w = pk_bf16(q4_code(w, 6) * s, q4_code(w, 7) * s);
     return r;
 }
 
@@ -90,10 +108,12 @@ __device__ __forceinline__ uint4 dq8(const uint4& q, int half, float s) {
  * Rows past M (or N) only feed C entries that are never stored, so the
  * loaders clamp them to the last row instead of branching.  Offsets are
  * 32-bit from workgroup-uniform bases (the launchers check that they fit). */
-template <bool ABF16>
+template <bool ABF16, int QF = QF_Q8>
 __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const unsigned char* __restrict__ W,
                                           float* __restrict__ Cm, int M, int N, int K, int lda, int ldc, int tm,
                                           int tn, unsigned short* lds) {
+    constexpr unsigned BYTES = QFmt<QF>::BYTES; /* bytes per 32-weight block */
+    typedef Stage<ABF16, QF> St;
     constexpr int CPR = ABF16 ? GEMM_BK / 8 : GEMM_BK / 4; /* 16-byte chunks of an A row */
     constexpr int RPP = NTH / CPR;                         /* A rows per loader pass */
     constexpr int NPASS = BM / RPP;
@@ -108,13 +128,13 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     const int ar = t / CPR, ac = t % CPR; /* A loader: first row, chunk */
     const float* Af = (const float*)Av + (ABF16 ? 0 : (size_t)m0 * lda);
     const unsigned short* Ah = (const unsigned short*)Av + (ABF16 ? (size_t)m0 * lda : 0);
-    const unsigned char* Wb = W + (size_t)n0 * nb * 36;
+    const unsigned char* Wb = W + (size_t)n0 * nb * BYTES;
     unsigned int aoff[NPASS];
 #pragma unroll
     for (int p = 0; p < NPASS; p++) aoff[p] = (unsigned)min(ar + RPP * p, M - 1 - m0) * (unsigned)lda + (unsigned)(EPC * ac);
-    const unsigned int woff = (unsigned)min(lr, N - 1 - n0) * (unsigned)(nb * 36) + (unsigned)lh * 36u;
+    const unsigned int woff = (unsigned)min(lr, N - 1 - n0) * (unsigned)(nb * BYTES) + (unsigned)lh * BYTES;
 
-    auto load_a = [&](unsigned int col, Stage<ABF16>& st) {
+    auto load_a = [&](unsigned int col, St& st) {
 #pragma unroll
         for (int p = 0; p < NPASS; p++) {
             if (ABF16)
@@ -123,18 +143,18 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
                 __builtin_memcpy(&st.a[p], __builtin_assume_aligned(Af + aoff[p] + col, 4), 16);
         }
     };
-    auto load_w = [&](const unsigned char* blk, Stage<ABF16>& st) {
+    auto load_w = [&](const unsigned char* blk, St& st) {
         __builtin_memcpy(&st.s, __builtin_assume_aligned(blk, 4), 4);
         __builtin_memcpy(&st.q[0], __builtin_assume_aligned(blk + 4, 4), 16);
-        __builtin_memcpy(&st.q[1], __builtin_assume_aligned(blk + 20, 4), 16);
+        if (QF == QF_Q8) __builtin_memcpy(&st.q[QF == QF_Q8 ? 1 : 0], __builtin_assume_aligned(blk + 20, 4), 16);
     };
-    auto load = [&](int step, Stage<ABF16>& st) {
+    auto load = [&](int step, St& st) {
         load_a((unsigned)step * GEMM_BK, st);
-        load_w(Wb + woff + (unsigned)step * 72u, st);
+        load_w(Wb + woff + (unsigned)step * (2u * BYTES), st);
     };
     /* zero_a: this thread's A chunk lies past K (half step only); the W
      * block past K arrives with scale 0, which zeroes its (finite) q. */
-    auto store = [&](int buf, const Stage<ABF16>& st, bool zero_a) {
+    auto store = [&](int buf, const St& st, bool zero_a) {
         unsigned short* As = lds + buf * 2 * SLAB;
         unsigned short* Bs = As + SLAB;
 #pragma unroll
@@ -150,10 +170,15 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
             }
         }
         uint4* bp = (uint4*)&Bs[lr * LDK + 32 * lh];
+        if (QF == QF_Q4) {
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            bp[2 * i] = dq8(st.q[i], 0, st.s);
-            bp[2 * i + 1] = dq8(st.q[i], 1, st.s);
+            for (int j = 0; j < 4; j++) bp[j] = dq4(st.q[0], j, st.s);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                bp[2 * i] = dq8(st.q[QF == QF_Q8 ? i : 0], 0, st.s);
+                bp[2 * i + 1] = dq8(st.q[QF == QF_Q8 ? i : 0], 1, st.s);
+            }
         }
     };
 
@@ -183,7 +208,7 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     };
 
     if (nfull > 0) {
-        Stage<ABF16> s0, s1;
+        St s0, s1;
         load(0, s0);
         load(min(1, nfull - 1), s1);
         store(0, s0, false);
@@ -212,13 +237,13 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     if (nb & 1) {
         /* Half step: block nb-1 = 2*nfull.  Buffer (nfull & 1) is free: its
          * last reader was followed by a barrier. */
-        Stage<ABF16> st;
+        St st;
         const int buf = nfull & 1;
         const bool past_a = EPC * ac >= 32; /* this thread's A chunk lies past K */
         load_a(past_a ? 0u : (unsigned)nfull * GEMM_BK, st);
         /* block 2*nfull + 1 (lh = 1) would lie past the row: read block nb-1
          * again and give it scale 0 */
-        load_w(Wb + woff + (unsigned)nfull * 72u - (unsigned)lh * 36u, st);
+        load_w(Wb + woff + (unsigned)nfull * (2u * BYTES) - (unsigned)lh * BYTES, st);
         if (lh) st.s = 0.0f;
         store(buf, st, past_a);
         __syncthreads();
@@ -253,8 +278,8 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     }
 }
 
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q8_gemm(GmGroup g) {
-    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
+template <int QF>
+__device__ __forceinline__ void gemm_group_body(const GmGroup& g, unsigned short* lds) {
     int tile = blockIdx.x;
     int pi = 0;
     while (pi + 1 < g.nprob && tile >= g.p[pi].tiles) {
@@ -263,7 +288,31 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     const GmProb& p = g.p[pi];
     const int tiles_n = (p.N + BN - 1) / BN;
-    gemm_tile<false>(p.A, p.W, p.C, p.M, p.N, p.K, p.lda, p.ldc, tile / tiles_n, tile % tiles_n, lds);
+    gemm_tile<false, QF>(p.A, p.W, p.C, p.M, p.N, p.K, p.lda, p.ldc, tile / tiles_n, tile % tiles_n, lds);
+}
+
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q8_gemm(GmGroup g) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
+    gemm_group_body<QF_Q8>(g, lds);
+}
+
+/* The same over Q4_0 weights (reference forward.metal:829-858 at BT > 1). */
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q4_gemm(GmGroup g) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
+    gemm_group_body<QF_Q4>(g, lds);
+}
+
+template <bool ABF16, int QF>
+__device__ __forceinline__ void gemm_multi_body(const void* __restrict__ A, const unsigned char* __restrict__ W,
+                                                float* __restrict__ C, const GmDesc* __restrict__ desc,
+                                                const unsigned int* __restrict__ tile_map, unsigned short* lds) {
+    const unsigned int tm_ = tile_map[blockIdx.x];
+    if (tm_ == GM_IDLE_TILE) return;
+    const GmDesc d = desc[tm_ >> 16];
+    const int tile = (int)(tm_ & 0xffffu);
+    const int tiles_n = (d.N + BN - 1) / BN;
+    const void* Ad = ABF16 ? (const void*)((const unsigned short*)A + d.a_off) : (const void*)((const float*)A + d.a_off);
+    gemm_tile<ABF16, QF>(Ad, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc, tile / tiles_n, tile % tiles_n, lds);
 }
 
 /* Activations in fp32 (cast to bf16 while staging) or already in bf16. */
@@ -272,13 +321,15 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                        float* __restrict__ C, const GmDesc* __restrict__ desc,
                                                        const unsigned int* __restrict__ tile_map) {
     __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
-    const unsigned int tm_ = tile_map[blockIdx.x];
-    if (tm_ == GM_IDLE_TILE) return;
-    const GmDesc d = desc[tm_ >> 16];
-    const int tile = (int)(tm_ & 0xffffu);
-    const int tiles_n = (d.N + BN - 1) / BN;
-    const void* Ad = ABF16 ? (const void*)((const unsigned short*)A + d.a_off) : (const void*)((const float*)A + d.a_off);
-    gemm_tile<ABF16>(Ad, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc, tile / tiles_n, tile % tiles_n, lds);
+    gemm_multi_body<ABF16, QF_Q8>(A, W, C, desc, tile_map, lds);
+}
+
+template <bool ABF16>
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_q4_gemm_multi(const void* __restrict__ A, const unsigned char* __restrict__ W,
+                                                       float* __restrict__ C, const GmDesc* __restrict__ desc,
+                                                       const unsigned int* __restrict__ tile_map) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
+    gemm_multi_body<ABF16, QF_Q4>(A, W, C, desc, tile_map, lds);
 }
 
 /* fp32 -> bf16 (round to nearest even), 8 elements per lane */
@@ -310,6 +361,28 @@ static bool gm_offsets_fit(int M, int N, int K, int lda) {
            (unsigned long long)N * (unsigned long long)(K / 32) * 36ull < 0x80000000ull;
 }
 
+static bool gm_offsets_fit_q(int M, int N, int K, int lda, unsigned bytes) {
+    return (unsigned long long)M * (unsigned long long)lda < 0x80000000ull &&
+           (unsigned long long)N * (unsigned long long)(K / 32) * bytes < 0x80000000ull;
+}
+
+/* The group launch over Q4_0 weights (qf 1) or Q8_0 (qf 0). */
+extern "C" int gm_launch_group_qf(GmGroup* g, int qf, hipStream_t s) {
+    if (qf == 0) return gm_launch_group(g, s);
+    long total = 0;
+    for (int i = 0; i < g->nprob; i++)
+        BMK_REQUIRE(gm_offsets_fit_q(g->p[i].M, g->p[i].N, g->p[i].K, g->p[i].lda, 20u),
+                    "q4 gemm: problem %d too large for 32-bit tile offsets", i);
+    for (int i = 0; i < g->nprob; i++) {
+        g->p[i].tiles = gm_tiles_for(g->p[i].M, g->p[i].N);
+        total += g->p[i].tiles;
+    }
+    if (total <= 0) return 0;
+    hipLaunchKernelGGL(k_q4_gemm, dim3((unsigned)total), dim3(NTH), 0, s, *g);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
 extern "C" int gm_launch_group(GmGroup* g, hipStream_t s) {
     long total = 0;
     for (int i = 0; i < g->nprob; i++)
@@ -331,7 +404,9 @@ extern "C" int gm_launch_group(GmGroup* g, hipStream_t s) {
  *          1 plan: GmDesc[nprob] then uint32 tile_map[n_tiles] = (problem << 16) | tile
  *            (host-validated: a permutation of all tiles; read by the kernel),
  *          2 activation arena f32, 3 weight arena (Q8 blocks), 4 output arena f32}. */
-extern "C" int bmk_launch_q8_gemm_multi(const bmk_launch_t* a) {
+template <int QF>
+static int launch_gemm_multi(const bmk_launch_t* a) {
+    constexpr unsigned BYTES = QFmt<QF>::BYTES;
     BMK_NEED_BYTES(a, 0, 8, "params");
     const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
     const int a_bf16 = a->bytes[0] >= 12 ? bmk_pi(a, 0, 2) : 0;
@@ -356,12 +431,12 @@ extern "C" int bmk_launch_q8_gemm_multi(const bmk_launch_t* a) {
                     "q8 gemm multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
                     gm_tiles_for(d.M, d.N), next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 gemm multi: problem %d weight offset not 4-byte aligned", i);
-        BMK_REQUIRE(gm_offsets_fit(d.M, d.N, d.K, d.lda), "q8 gemm multi: problem %d too large for 32-bit tile offsets",
-                    i);
+        BMK_REQUIRE(gm_offsets_fit_q(d.M, d.N, d.K, d.lda, BYTES),
+                    "q8 gemm multi: problem %d too large for 32-bit tile offsets", i);
         BMK_REQUIRE((!a_bf16 || (d.a_off % 8 == 0 && d.lda % 8 == 0)),
                     "q8 gemm multi: problem %d bf16 rows must start 16-byte aligned", i);
         BMK_REQUIRE(d.a_off + (unsigned long long)(d.M - 1) * d.lda + d.K <= a->bytes[2] / esz &&
-                        d.w_off + (unsigned long long)d.N * (d.K / 32) * 36 <= a->bytes[3] &&
+                        d.w_off + (unsigned long long)d.N * (d.K / 32) * BYTES <= a->bytes[3] &&
                         d.c_off + (unsigned long long)(d.M - 1) * d.ldc + d.N <= a->bytes[4] / 4,
                     "q8 gemm multi: problem %d lies outside its arenas", i);
         next_tile += d.tiles;
@@ -388,17 +463,24 @@ extern "C" int bmk_launch_q8_gemm_multi(const bmk_launch_t* a) {
     BMK_REQUIRE(named == next_tile, "q8 gemm multi: tile_map names %ld of %ld tiles", named, next_tile);
     const GmDesc* dd = (const GmDesc*)a->dev[1];
     const unsigned int* dt = (const unsigned int*)((const char*)a->dev[1] + desc_bytes);
-    if (a_bf16) {
-        BMK_REQUIRE(((uintptr_t)a->dev[2] & 15) == 0, "q8 gemm multi: bf16 activation arena must be 16-byte aligned");
-        hipLaunchKernelGGL(k_q8_gemm_multi<true>, dim3((unsigned)n_tiles), dim3(NTH), 0, a->stream,
-                           (const void*)a->dev[2], (const unsigned char*)a->dev[3], (float*)a->dev[4], dd, dt);
+    if (a_bf16) BMK_REQUIRE(((uintptr_t)a->dev[2] & 15) == 0, "q8 gemm multi: bf16 activation arena must be 16-byte aligned");
+    const dim3 grid((unsigned)n_tiles), tb(NTH);
+    const void* A = (const void*)a->dev[2];
+    const unsigned char* W = (const unsigned char*)a->dev[3];
+    float* C = (float*)a->dev[4];
+    if (QF == QF_Q4) {
+        if (a_bf16) hipLaunchKernelGGL(k_q4_gemm_multi<true>, grid, tb, 0, a->stream, A, W, C, dd, dt);
+        else hipLaunchKernelGGL(k_q4_gemm_multi<false>, grid, tb, 0, a->stream, A, W, C, dd, dt);
     } else {
-        hipLaunchKernelGGL(k_q8_gemm_multi<false>, dim3((unsigned)n_tiles), dim3(NTH), 0, a->stream,
-                           (const void*)a->dev[2], (const unsigned char*)a->dev[3], (float*)a->dev[4], dd, dt);
+        if (a_bf16) hipLaunchKernelGGL(k_q8_gemm_multi<true>, grid, tb, 0, a->stream, A, W, C, dd, dt);
+        else hipLaunchKernelGGL(k_q8_gemm_multi<false>, grid, tb, 0, a->stream, A, W, C, dd, dt);
     }
     BMK_LAUNCH_CHECK();
     return 0;
 }
+
+extern "C" int bmk_launch_q8_gemm_multi(const bmk_launch_t* a) { return launch_gemm_multi<QF_Q8>(a); }
+extern "C" int bmk_launch_q4_gemm_multi(const bmk_launch_t* a) { return launch_gemm_multi<QF_Q4>(a); }
 
 /* cast_f32_bf16 {src f32 [n], dst bf16 [n], params int64{n}}: round to nearest even,
  * the activation cast of a prefill GEMM done once per matrix. */
@@ -421,18 +503,28 @@ extern "C" int bmk_launch_cast_bf16(const bmk_launch_t* a) {
 }
 
 /* Multi-GEMM launch from a device-resident plan built by bm_q8_gemm_plan
- * (the engine's prefill; the plan was validated when it was built). */
-extern "C" int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
-                               int n_tiles, hipStream_t s) {
+ * (the engine's prefill; the plan was validated when it was built); qf 1:
+ * Q4_0 weights. */
+extern "C" int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
+                                  int nprob, int n_tiles, hipStream_t s) {
     if (nprob <= 0 || n_tiles <= 0) return 0;
     const GmDesc* desc = (const GmDesc*)plan;
     const unsigned int* tmap = (const unsigned int*)((const char*)plan + (size_t)nprob * sizeof(GmDesc));
-    if (a_bf16)
-        hipLaunchKernelGGL(k_q8_gemm_multi<true>, dim3((unsigned)n_tiles), dim3(NTH), 0, s, A, W, C, desc, tmap);
-    else
-        hipLaunchKernelGGL(k_q8_gemm_multi<false>, dim3((unsigned)n_tiles), dim3(NTH), 0, s, A, W, C, desc, tmap);
+    const dim3 grid((unsigned)n_tiles), tb(NTH);
+    if (qf) {
+        if (a_bf16) hipLaunchKernelGGL(k_q4_gemm_multi<true>, grid, tb, 0, s, A, W, C, desc, tmap);
+        else hipLaunchKernelGGL(k_q4_gemm_multi<false>, grid, tb, 0, s, A, W, C, desc, tmap);
+    } else {
+        if (a_bf16) hipLaunchKernelGGL(k_q8_gemm_multi<true>, grid, tb, 0, s, A, W, C, desc, tmap);
+        else hipLaunchKernelGGL(k_q8_gemm_multi<false>, grid, tb, 0, s, A, W, C, desc, tmap);
+    }
     BMK_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
+                               int n_tiles, hipStream_t s) {
+    return gm_launch_multi_qf(A, a_bf16, 0, W, C, plan, nprob, n_tiles, s);
 }
 
 /* fp32 -> bf16 over n elements (RNE) */

@@ -379,41 +379,40 @@ extern "C" int bmk_launch_q8_matvec(const bmk_launch_t* a) { return launch_matve
 
 /* matmul_forward_q4_vec4 / matmul_forward_q4_vec / matmul_forward_q4
  * (reference forward.metal:654-858, routing scheduler.c:755-764): the same
- * buffers over Q4_0 weights [OC][C/32] of 20-byte blocks.  BT > DEC_MAX_B
- * rows go through the batched kernel DEC_MAX_B rows at a time. */
+ * buffers over Q4_0 weights [OC][C/32] of 20-byte blocks, routed as the Q8
+ * ones: one row to the matvec, 2 <= BT < 16 to the batched fp32-MFMA
+ * matvec, BT >= 16 without bias to the bf16-MFMA GEMM (q8_gemm.hip). */
+#include "q8_gemm.h"
+#define GEMM_MIN_BT 16
 extern "C" int bmk_launch_q4_matvec(const bmk_launch_t* a) {
     BMK_NEED_BYTES(a, 4, 16, "params");
     const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);
-    if (BT <= DEC_MAX_B || has_bias || ((uintptr_t)a->dev[0] & 15)) return launch_matvec<QF_Q4>(a);
-    BMK_REQUIRE(OC >= 0 && C > 0 && C % 32 == 0, "q4 matvec: bad shape BT=%d C=%d OC=%d", BT, C, OC);
+    if (BT < GEMM_MIN_BT || has_bias) return launch_matvec<QF_Q4>(a);
+    BMK_REQUIRE(OC >= 0 && C > 0 && C % 32 == 0, "q4 matmul: bad shape BT=%d C=%d OC=%d", BT, C, OC);
     if (OC == 0) return 0;
     BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
     BMK_NEED_BYTES(a, 1, (size_t)OC * (C / 32) * 20, "weight");
     BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
-    BMK_REQUIRE(((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0, "q4 matvec: misaligned buffer offset");
-    for (int b0 = 0; b0 < BT; b0 += DEC_MAX_B) {
-        DecMv m;
-        memset(&m, 0, sizeof m);
-        m.x = (const float*)a->dev[0] + (size_t)b0 * C;
-        m.C = C;
-        m.B = BT - b0 < DEC_MAX_B ? BT - b0 : DEC_MAX_B;
-        m.ldx = C;
-        m.nmat = 1;
-        m.qf = QF_Q4;
-        m.w[0] = (const unsigned char*)a->dev[1];
-        m.y[0] = (float*)a->dev[3] + (size_t)b0 * OC;
-        m.OC[0] = OC;
-        BMK_REQUIRE(dec_launch_mv(&m, a->stream) == 0, "q4 matvec: batched launch failed (BT=%d C=%d OC=%d)", BT, C, OC);
-    }
-    return 0;
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 3) == 0 && ((uintptr_t)a->dev[3] & 3) == 0,
+                "q4 matmul: misaligned buffer offset");
+    GmGroup g;
+    g.nprob = 1;
+    g.p[0].A = (const float*)a->dev[0];
+    g.p[0].W = (const unsigned char*)a->dev[1];
+    g.p[0].C = (float*)a->dev[3];
+    g.p[0].M = BT;
+    g.p[0].N = OC;
+    g.p[0].K = C;
+    g.p[0].lda = C;
+    g.p[0].ldc = OC;
+    g.p[0].tiles = 0;
+    return gm_launch_group_qf(&g, 1, a->stream);
 }
 
 /* matmul_forward_q8 (reference forward.metal:625-649): BT rows of activations.
  * BT below GEMM_MIN_BT stays on fp32 (the batched fp32-MFMA matvec for
  * 2 <= BT, the matvec for one row); larger BT goes to the bf16-MFMA GEMM
  * (q8_gemm.hip). */
-#include "q8_gemm.h"
-#define GEMM_MIN_BT 16
 extern "C" int bmk_launch_q8_matmul(const bmk_launch_t* a) {
     BMK_NEED_BYTES(a, 4, 16, "params");
     const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), has_bias = bmk_pi(a, 4, 3);

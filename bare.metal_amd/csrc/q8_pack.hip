@@ -192,6 +192,15 @@ int launch_quantize_q4(const bmk_launch_t* a) {
 extern "C" int bmk_launch_quantize_q4(const bmk_launch_t* a) { return launch_quantize_q4<false>(a); }
 extern "C" int bmk_launch_quantize_q4_bf16(const bmk_launch_t* a) { return launch_quantize_q4<true>(a); }
 
+/* Engine-side Q4 pack of n bf16 values (the reference's bmt_quantize_q4_bf16). */
+extern "C" int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s) {
+    const long nblocks = n / 32;
+    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
+    hipLaunchKernelGGL(k_quantize_q4<true>, dim3(grid), dim3(256), 0, s, src, dst, nblocks);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
 /* Engine-side Q4 pack of n fp32 values (as q8_pack_f32). */
 extern "C" int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s) {
     const long nblocks = n / 32;

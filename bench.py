@@ -155,14 +155,19 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
     x = wl.X.read(np.float32)
     y = np.zeros(int(wl.OC.sum()), np.float32)
     args = (wl.w_off, wl.x_off, wl.y_off, wl.OC, wl.C)
-    po.cpu_q8_matvec_multi(w, x, y, *args, threads)  # warm caches / threads
-    n, t0 = 0, time.perf_counter()
-    while True:
-        po.cpu_q8_matvec_multi(w, x, y, *args, threads)
-        n += 1
-        dt = time.perf_counter() - t0
-        if dt >= seconds:
-            break
+    def timed(nthreads, budget):
+        po.cpu_q8_matvec_multi(w, x, y, *args, nthreads)  # warm caches / threads
+        n, t0 = 0, time.perf_counter()
+        while True:
+            po.cpu_q8_matvec_multi(w, x, y, *args, nthreads)
+            n += 1
+            dt = time.perf_counter() - t0
+            if dt >= budget:
+                return n, dt
+
+    # the survey asks for one core and all cores: one core gets a quarter of the budget
+    n1, dt1 = timed(1, seconds / 4)
+    n, dt = timed(threads, seconds)
     gpu_y = wl.Y.read(np.float32)
     rel = float(np.abs(y - gpu_y).max() / np.abs(gpu_y).max())
     return {
@@ -173,6 +178,8 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
         "sample": f"{n} whole tokens ({len(wl.probs)} Q8 matvecs each) in {dt:.1f} s, "
                   f"fp32 SIMD ({po.oracle().orc_cpu_isa().decode()}) + OpenMP over rows; "
                   f"max rel diff vs GPU {rel:.1e}",
+        "value_1core": round(wl.bytes_per_step * n1 / dt1 / 1e9, 3),
+        "sample_1core": f"{n1} whole tokens in {dt1:.1f} s on 1 thread",
     }
 
 

@@ -15,7 +15,8 @@
  *   - BM_DEVICE_METAL selects "the GPU", here the HIP device; BM_DEVICE_HIP
  *     is the same value.  BM_DEVICE_CPU has no backend, as in the reference
  *     (reference src/baremetal/context.c:16-22), and bm_create returns NULL.
- *   - Projections run only in Q8 (quant_bits 8).  The LM head runs over the
+ *   - Projections run in Q8_0 (quant_bits 8, the default) or Q4_0
+ *     (quant_bits 4).  The LM head runs over the
  *     tied embedding in the model's precision, as the reference's Q8 mode
  *     does (reference src/baremetal/graph.c:228-238, scheduler.c:369-371,
  *     776-778): fp32 rows (BM_PRECISION_FP32) or bf16 rows rounded to
@@ -152,8 +153,9 @@ const char*    bm_get_arch_name(const bm_model_t* model);
 
 /* ---- MI355X additions (no reference counterpart) ---- */
 
-/* Quantization of the projections: 8 (Q8_0) is the only value accepted
- * (the reference's CLI sets model->quant_bits, reference tools/cli.c:886). */
+/* Quantization of the projections: 8 (Q8_0, default) or 4 (Q4_0); the
+ * reference's CLI sets model->quant_bits (reference tools/cli.c:886).
+ * Returns 0, or -1 for another value. */
 int            bm_model_set_quant_bits(bm_model_t* model, int bits);
 /* 1: the LM head runs on Q8 rows quantized from the head (the tied embedding or lm_head);
  * 0 (default): rows in the model's precision, as the reference. */

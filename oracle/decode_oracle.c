@@ -74,6 +74,35 @@ static void q8_mv(const uint8_t* w, const float* x, float* y, int C, int OC, int
     }
 }
 
+/* Q4_0 rows (reference forward.metal:654-858): 20-byte blocks, element 2j
+ * in the low nibble of byte j, 2j+1 in the high nibble, codes in [-8, 7]. */
+static void q4_mv(const uint8_t* w, const float* x, float* y, int C, int OC, int nt) {
+    const int nb = C / 32;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (int r = 0; r < OC; r++) {
+        const uint8_t* row = w + (size_t)r * nb * 20;
+        double acc = 0.0;
+        for (int b = 0; b < nb; b++) {
+            float s;
+            memcpy(&s, row + (size_t)b * 20, 4);
+            const uint8_t* qs = row + (size_t)b * 20 + 4;
+            double part = 0.0;
+            for (int j = 0; j < 32; j++) {
+                const int nib = (qs[j >> 1] >> (4 * (j & 1))) & 0x0F;
+                part += (double)x[32 * b + j] * (double)(nib >= 8 ? nib - 16 : nib);
+            }
+            acc += (double)s * part;
+        }
+        y[r] = (float)acc;
+    }
+}
+
+/* the model's projection format */
+static void proj_mv(const orc_model_t* m, const uint8_t* w, const float* x, float* y, int C, int OC, int nt) {
+    if (m->qbits == 4) q4_mv(w, x, y, C, OC, nt);
+    else q8_mv(w, x, y, C, OC, nt);
+}
+
 static void f32_mv(const float* w, const float* x, double* y, int C, int OC, int nt) {
 #pragma omp parallel for num_threads(nt) schedule(static)
     for (int r = 0; r < OC; r++) {
@@ -125,6 +154,7 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
     const orc_model_t* m = &d->m;
     const int D = m->D, H = m->H, NH = m->NH, NKV = m->NKV, HD = m->HD, L = m->L, V = m->V, MS = m->MS;
     const int KV = NKV * HD, QD = NH * HD, nbD = D / 32, nbH = H / 32, nbQ = QD / 32;
+    const size_t bb = m->qbits == 4 ? 20 : 36; /* bytes per projection block */
     const int kv_mul = NH / NKV, nt = d->nthreads;
     if (token < 0 || token >= V || pos < 0 || pos >= MS) return -1;
 
@@ -133,9 +163,9 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
 
     for (int l = 0; l < L; l++) {
         rmsnorm(d->x, m->ln1 + (size_t)l * D, d->xn, D, m->eps);
-        q8_mv(m->wq + (size_t)l * QD * nbD * 36, d->xn, d->q, D, QD, nt);
-        q8_mv(m->wk + (size_t)l * KV * nbD * 36, d->xn, d->k, D, KV, nt);
-        q8_mv(m->wv + (size_t)l * KV * nbD * 36, d->xn, d->v, D, KV, nt);
+        proj_mv(m, m->wq + (size_t)l * QD * nbD * bb, d->xn, d->q, D, QD, nt);
+        proj_mv(m, m->wk + (size_t)l * KV * nbD * bb, d->xn, d->k, D, KV, nt);
+        proj_mv(m, m->wv + (size_t)l * KV * nbD * bb, d->xn, d->v, D, KV, nt);
 
         for (int i = 0; i < HD / 2; i++) {
             float fr = rope_freq(m->theta, i, HD);
@@ -184,18 +214,18 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
             }
         }
 
-        q8_mv(m->wo + (size_t)l * D * nbQ * 36, d->att, d->o, QD, D, nt);
+        proj_mv(m, m->wo + (size_t)l * D * nbQ * bb, d->att, d->o, QD, D, nt);
         for (int j = 0; j < D; j++) d->x[j] = d->x[j] + d->o[j];
 
         rmsnorm(d->x, m->ln2 + (size_t)l * D, d->xn, D, m->eps);
-        q8_mv(m->wg + (size_t)l * H * nbD * 36, d->xn, d->g, D, H, nt);
-        q8_mv(m->wu + (size_t)l * H * nbD * 36, d->xn, d->u, D, H, nt);
+        proj_mv(m, m->wg + (size_t)l * H * nbD * bb, d->xn, d->g, D, H, nt);
+        proj_mv(m, m->wu + (size_t)l * H * nbD * bb, d->xn, d->u, D, H, nt);
         for (int j = 0; j < H; j++) {
             float gx = d->g[j];
             float silu = gx / (1.0f + expf(-gx));
             d->g[j] = silu * d->u[j];
         }
-        q8_mv(m->wd + (size_t)l * D * nbH * 36, d->g, d->dn, H, D, nt);
+        proj_mv(m, m->wd + (size_t)l * D * nbH * bb, d->g, d->dn, H, D, nt);
         for (int j = 0; j < D; j++) d->x[j] = d->x[j] + d->dn[j];
     }
 

@@ -9,8 +9,8 @@
 #include <stdint.h>
 
 /* Weights as the reference lays them out (model.c:125-172): per matrix
- * type, all layers back to back; Q8 matrices as 36-byte blocks, rows of
- * C/32 blocks. */
+ * type, all layers back to back; quantized matrices as rows of C/32 blocks
+ * (Q8_0 36 bytes, Q4_0 20 bytes). */
 typedef struct {
     int D, H, NH, NKV, HD, L, V, MS;
     float theta, eps;
@@ -28,6 +28,7 @@ typedef struct {
     const uint8_t* head_q8;  /* NULL: fp32 tied head (the reference's Q8 mode) */
     const float* head_f32;   /* fp32 head rows [V][D] when head_q8 is NULL; NULL: emb.  The
                                 reference's bf16 head is emb rounded to bf16 and widened back */
+    int qbits;               /* projections: 8 (or 0) Q8_0 36-byte blocks, 4 Q4_0 20-byte blocks */
 } orc_model_t;
 
 typedef struct orc_decoder_s orc_decoder_t;

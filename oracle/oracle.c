@@ -221,24 +221,15 @@ void orc_q8_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int 
 
 /* ---- Prefill GEMM with bf16 operands (the MFMA contract):
  *      C[m][n] = sum_k bf16(A[m][k]) * bf16(q[n][k] * scale[n][k/32]) in double. */
-void orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N) {
-    const int nb = K / 32;
-    float* wd = (float*)malloc((size_t)N * K * sizeof(float));
+/* C = A x Wd^T in double over bf16-rounded A; Wd: N rows of K dequantized
+ * weights (already bf16 values).  Frees wd. */
+static void contract_bf16_f64(float* wd, const float* a, double* c, int M, int K, int N) {
     float* ad = (float*)malloc((size_t)M * K * sizeof(float));
     if (!wd || !ad) {
         free(wd);
         free(ad);
         return;
     }
-    for (int n = 0; n < N; n++)
-        for (int b = 0; b < nb; b++) {
-            const uint8_t* blk = w + ((size_t)n * nb + b) * 36;
-            float s = q8_scale(blk);
-            for (int j = 0; j < 32; j++) {
-                volatile float v = (float)(int8_t)blk[4 + j] * s;
-                wd[(size_t)n * K + 32 * b + j] = bf16_to_f32(orc_bf16_rne(v));
-            }
-        }
     for (size_t i = 0; i < (size_t)M * K; i++) ad[i] = bf16_to_f32(orc_bf16_rne(a[i]));
     for (int m = 0; m < M; m++)
         for (int n = 0; n < N; n++) {
@@ -250,6 +241,39 @@ void orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, in
         }
     free(wd);
     free(ad);
+}
+
+void orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N) {
+    const int nb = K / 32;
+    float* wd = (float*)malloc((size_t)N * K * sizeof(float));
+    for (int n = 0; wd && n < N; n++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t* blk = w + ((size_t)n * nb + b) * 36;
+            float s = q8_scale(blk);
+            for (int j = 0; j < 32; j++) {
+                volatile float v = (float)(int8_t)blk[4 + j] * s;
+                wd[(size_t)n * K + 32 * b + j] = bf16_to_f32(orc_bf16_rne(v));
+            }
+        }
+    contract_bf16_f64(wd, a, c, M, K, N);
+}
+
+/* ---- Prefill GEMM over Q4_0 weights with bf16 operands: the same with
+ *      bf16(code * scale) (reference forward.metal:829-858 at BT > 1). */
+void orc_q4_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N) {
+    const int nb = K / 32;
+    float* wd = (float*)malloc((size_t)N * K * sizeof(float));
+    for (int n = 0; wd && n < N; n++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t* blk = w + ((size_t)n * nb + b) * 20;
+            float s;
+            memcpy(&s, blk, 4);
+            for (int j = 0; j < 32; j++) {
+                volatile float v = (float)q4_code(blk + 4, j) * s;
+                wd[(size_t)n * K + 32 * b + j] = bf16_to_f32(orc_bf16_rne(v));
+            }
+        }
+    contract_bf16_f64(wd, a, c, M, K, N);
 }
 
 /* fp32 activation rounded to bf16 and back (A10 semantics), elementwise. */

@@ -18,6 +18,7 @@ void     orc_q8_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M
 size_t   orc_quantize_q4(const float* src, uint8_t* dst, size_t n);
 size_t   orc_quantize_q4_bf16(const uint16_t* src, uint8_t* dst, size_t n);
 void     orc_q4_matvec_f64(const uint8_t* w, const float* x, double* y, int BT, int C, int OC);
+void     orc_q4_gemm_bf16_f64(const uint8_t* w, const float* a, double* c, int M, int K, int N);
 
 /* CPU baseline (cpu_baseline.c): fp32 Q8 matvec in the reference's
  * arithmetic, SIMD + OpenMP over rows. */

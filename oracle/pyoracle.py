@@ -44,6 +44,7 @@ def oracle() -> C.CDLL:
         L.orc_quantize_q4_bf16.restype = sz
         L.orc_quantize_q4_bf16.argtypes = [vp, vp, sz]
         L.orc_q4_matvec_f64.argtypes = [vp, vp, vp, i, i, i]
+        L.orc_q4_gemm_bf16_f64.argtypes = [vp, vp, vp, i, i, i]
         L.orc_cpu_q8_matvec_f32.argtypes = [vp, vp, vp, i, i, i]
         L.orc_cpu_q8_matvec_multi.argtypes = [vp, vp, vp, i, vp, vp, vp, vp, vp, i]
         L.orc_cpu_max_threads.restype = i
@@ -158,6 +159,14 @@ def q4_matvec_f64(w: np.ndarray, x: np.ndarray, BT: int, C_: int, OC: int) -> np
     return y
 
 
+def q4_gemm_bf16_f64(w: np.ndarray, a: np.ndarray, M: int, K: int, N: int) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    c = np.zeros(M * N, dtype=np.float64)
+    oracle().orc_q4_gemm_bf16_f64(_p(w), _p(a), _p(c), M, K, N)
+    return c
+
+
 def q8_matvec_f64(w: np.ndarray, x: np.ndarray, BT: int, C_: int, OC: int) -> np.ndarray:
     w = np.ascontiguousarray(w, dtype=np.uint8)
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -203,7 +212,7 @@ class OrcModel(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("D", "H", "NH", "NKV", "HD", "L", "V", "MS")] + [
         ("theta", C.c_float), ("eps", C.c_float),
     ] + [(n, C.c_void_p) for n in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8",
-                                   "head_f32")]
+                                   "head_f32")] + [("qbits", C.c_int)]
 
 
 class Decoder:
@@ -216,6 +225,7 @@ class Decoder:
             setattr(m, k, int(dims[k]))
         m.theta = float(dims.get("theta", 10000.0))
         m.eps = float(dims.get("eps", 1e-5))
+        m.qbits = int(dims.get("qbits", 8))
         for k in ("emb", "ln1", "ln2", "lnf", "wq", "wk", "wv", "wo", "wg", "wu", "wd", "head_q8", "head_f32"):
             a = arrays.get(k)
             setattr(m, k, a.ctypes.data if a is not None else None)

@@ -10,21 +10,22 @@ TINY = dict(D=64, H=128, NH=4, NKV=2, HD=16, L=2, V=256)
 SMALL = dict(D=128, H=256, NH=4, NKV=2, HD=32, L=3, V=1024)
 
 
-def q8_arrays(w: dict) -> dict:
-    """Oracle arrays (fp32 embedding/norms, Q8 projections) from fp32 weights."""
+def q8_arrays(w: dict, qbits: int = 8) -> dict:
+    """Oracle arrays (fp32 embedding/norms, Q8 or Q4 projections) from fp32 weights."""
     out = {"emb": w["token_embedding"], "ln1": w["ln1"], "ln2": w["ln2"], "lnf": w["lnf"]}
+    pack = po.quantize_q4 if qbits == 4 else po.quantize_q8
     for src, dst in (("wq", "wq"), ("wk", "wk"), ("wv", "wv"), ("wo", "wo"), ("w_gate", "wg"), ("w_up", "wu"),
                      ("w_down", "wd")):
-        out[dst] = po.quantize_q8(w[src])
+        out[dst] = pack(w[src])
     return out
 
 
 def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads: int = 8,
-                   precision: str = "fp32", head_f32=None) -> po.Decoder:
+                   precision: str = "fp32", head_f32=None, qbits: int = 8) -> po.Decoder:
     """precision "bf16": the head rows are rounded to bf16 (reference
     scheduler.c:395-402), widened back to fp32 exactly.  head_f32: the rows of
     an untied head (default: the tied embedding)."""
-    arrs = q8_arrays(w)
+    arrs = q8_arrays(w, qbits)
     head = w["token_embedding"] if head_f32 is None else np.ascontiguousarray(head_f32, np.float32)
     if q8_head:
         arrs["head_q8"] = po.quantize_q8(head)
@@ -34,6 +35,7 @@ def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads
         arrs["head_f32"] = head
     d = dict(dims)
     d["MS"] = ms
+    d["qbits"] = qbits
     return po.Decoder(d, arrs, nthreads=nthreads)
 
 

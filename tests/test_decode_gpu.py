@@ -414,3 +414,65 @@ def test_smollm2_135m_config5_greedy():
     for b in (1, 17, 31):
         assert np.array_equal(gotb[:, b], e1.generate(prompts[b], steps)[:, 0]), b
     e1.close()
+
+
+# ------------------------------------------------------------------ Q4_0 projections (quant_bits 4)
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_q4_engine_matches_oracle(batch):
+    """bm_model_set_quant_bits(4): every projection in Q4_0 (the reference's
+    --quant q4, graph.c:228-238 marks them quantized = 4), decoded by the
+    Q4 variants of the fused matvec kernels."""
+    w = bmhip.synthetic_weights(SMALL, 93)
+    eng = bmhip.Engine(SMALL, max_seq_len=32, weights=w, batch=batch, quant_bits=4)
+    orc = oracle_decoder(SMALL, w, 32, qbits=4)
+    orc8 = oracle_decoder(SMALL, w, 32)
+    toks = bmhip.synth_uniform_int(94, 0, SMALL["V"], 10)
+    for pos, t in enumerate(toks):
+        y = eng.step(int(t))[None, :] if batch == 1 else eng.step_batch(np.full(batch, int(t), np.int32))
+        r = orc.step(int(t), pos)
+        for b in range(batch):
+            assert normwise(y[b], r) <= LOGIT_TOL, (pos, b, normwise(y[b], r))
+        r8 = orc8.step(int(t), pos)
+        assert normwise(r8, r) > 10 * LOGIT_TOL  # the Q4 model is a different model: the test tells them apart
+    eng.close()
+
+
+def test_q4_prefill_and_generate():
+    """Q4 prefill (bf16-MFMA GEMM over Q4 tiles) against stepping, and greedy
+    generation against the oracle's tokens."""
+    w = bmhip.synthetic_weights(SMALL, 95)
+    n = 24
+    toks = [(41 * i + 5) % SMALL["V"] for i in range(n)]
+    eng = bmhip.Engine(SMALL, max_seq_len=64, weights=w, quant_bits=4)
+    pre = eng.forward(toks)
+    eng.reset()
+    for t in toks:
+        step = eng.step(t)
+    assert cosine(pre, step) > 0.9999, cosine(pre, step)
+    orc = oracle_decoder(SMALL, w, 64, qbits=4)
+    for pos, t in enumerate(toks):
+        r = orc.step(t, pos)
+    assert normwise(pre, r) <= 2e-2
+    got = eng.generate(np.array(toks[:8], np.int32), 20)[:, 0]
+    eng.close()
+    want, marg = oracle_decoder(SMALL, w, 64, qbits=4).generate(np.array(toks[:8], np.int32), 20)
+    agree = got == want
+    first_miss = int(np.argmin(agree)) if not agree.all() else len(agree)
+    # identical up to the first near-tie (fp32 summation order may break a tie either way)
+    assert first_miss == len(agree) or marg[first_miss] < 1e-3, (got, want, marg)
+
+
+def test_q4_from_bf16_checkpoint(tmp_path):
+    """A BF16 checkpoint run as Q4: projections packed on the device from bf16
+    (the reference's bmt_quantize_q4_bf16, quant.c:81-90)."""
+    from decode_util import widen_bf16, write_checkpoint
+    w = bmhip.synthetic_weights(TINY, 96)
+    write_checkpoint(str(tmp_path), TINY, w, dtype="BF16")
+    eng = bmhip.Engine(checkpoint=str(tmp_path), max_seq_len=32, quant_bits=4)
+    orc = oracle_decoder(TINY, {k: widen_bf16(v) for k, v in w.items()}, 32, qbits=4)
+    worst = 0.0
+    for pos, t in enumerate(bmhip.synth_uniform_int(97, 0, TINY["V"], 8)):
+        worst = max(worst, normwise(eng.step(int(t)), orc.step(int(t), pos)))
+    eng.close()
+    assert worst <= LOGIT_TOL, worst

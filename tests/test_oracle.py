@@ -310,3 +310,34 @@ def test_q4_matvec_matches_q8_on_shared_codes():
     q4[:, 4:] = nib[:, 0::2] | (nib[:, 1::2] << 4)
     x = rng.standard_normal(BT * C).astype(np.float32)
     assert np.array_equal(po.q4_matvec_f64(q4.ravel(), x, BT, C, OC), po.q8_matvec_f64(q8, x, BT, C, OC))
+
+
+def test_q4_gemm_bf16_matches_dequant_product():
+    rng = np.random.default_rng(25)
+    M, K, N = 9, 96, 11
+    w = po.quantize_q4((rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    a = rng.standard_normal(M * K).astype(np.float32)
+    c = po.q4_gemm_bf16_f64(w, a, M, K, N).reshape(M, N)
+    s, q = q4_codes(w)
+    wd32 = (q.astype(np.float32) * s[:, None]).astype(np.float32).ravel()
+    wb = po.bf16_rne(wd32).astype(np.float64).reshape(N, K)
+    ab = po.bf16_rne(a).astype(np.float64).reshape(M, K)
+    np.testing.assert_allclose(c, ab @ wb.T, rtol=1e-12, atol=1e-15)
+    # and each row of the exact-operand version is the Q4 matvec oracle
+    exact = po.q4_matvec_f64(w, a, M, K, N).reshape(M, N)
+    assert np.abs(c - exact).max() / np.abs(exact).max() < 1e-2
+
+
+def test_q4_gemm_integer_case_is_exact():
+    rng = np.random.default_rng(26)
+    M, K, N = 4, 64, 3
+    nb = N * (K // 32)
+    codes = rng.integers(-8, 8, (nb, 32))
+    scales = (2.0 ** rng.integers(-3, 2, nb)).astype(np.float32)
+    blk = np.zeros((nb, 20), np.uint8)
+    blk[:, :4] = scales.view(np.uint8).reshape(nb, 4)
+    nib = (codes & 0x0F).astype(np.uint8)
+    blk[:, 4:] = nib[:, 0::2] | (nib[:, 1::2] << 4)
+    a = rng.integers(-3, 4, M * K).astype(np.float32)
+    c = po.q4_gemm_bf16_f64(blk.ravel(), a, M, K, N)
+    assert np.array_equal(c, po.q4_matvec_f64(blk.ravel(), a, M, K, N))

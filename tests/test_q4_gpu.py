@@ -107,15 +107,70 @@ def test_q4_matvec_integer_exact_bitwise(be, BT):
     assert np.array_equal(y.astype(np.float64), po.q4_matvec_f64(w, x, BT, C, OC))
 
 
-@pytest.mark.parametrize("BT,OC,C", [(2, 960, 960), (8, 2560, 960), (15, 320, 960), (64, 576, 1536),
-                                     (70, 192, 576), (130, 96, 64)])
+@pytest.mark.parametrize("BT,OC,C", [(2, 960, 960), (8, 2560, 960), (15, 320, 960)])
 def test_q4_matmul_batched(be, BT, OC, C):
-    """2 <= BT <= 64: the batched fp32-MFMA kernel reads each block once for
-    all rows; larger BT runs it 64 rows at a time."""
+    """2 <= BT < 16: the batched fp32-MFMA kernel reads each block once for all rows."""
     w = po.quantize_q4(bmhip.synth_normal(bmhip.synth_seed(72, BT, OC, C), 0.02, OC * C))
     x = bmhip.synth_normal(bmhip.synth_seed(73, BT, OC, C), 1.0, BT * C)
     y = run_q4(be, w, x, BT, C, OC, kernel="matmul_forward_q4")
     assert normwise(y, po.q4_matvec_f64(w, x, BT, C, OC)) <= RTOL
+
+
+@pytest.mark.parametrize("M,K,N", [(512, 576, 576), (512, 1536, 576), (16, 576, 192), (70, 576, 192),
+                                   (130, 64, 96), (40, 160, 96), (33, 224, 130)])
+def test_q4_gemm_vs_oracle(be, M, K, N):
+    """BT >= 16: the bf16-MFMA GEMM over Q4 tiles; vs the oracle with the same
+    bf16 operands (1e-4, summation order only) and the exact Q4 product (1e-2)."""
+    w = po.quantize_q4(bmhip.synth_normal(bmhip.synth_seed(74, 0, N, K), 0.02, N * K))
+    a = bmhip.synth_normal(bmhip.synth_seed(74, 1, M, K), 1.0, M * K)
+    c = run_q4(be, w, a, M, K, N, kernel="matmul_forward_q4")
+    rb = po.q4_gemm_bf16_f64(w, a, M, K, N)
+    assert normwise(c, rb) <= 1e-4, normwise(c, rb)
+    rx = po.q4_matvec_f64(w, a, M, K, N)
+    assert normwise(c, rx) <= 1e-2, normwise(c, rx)
+
+
+def test_q4_gemm_integer_exact(be):
+    rng = np.random.default_rng(27)
+    M, K, N = 64, 128, 80
+    nb = N * K // 32
+    blk = np.zeros((nb, 20), np.uint8)
+    blk[:, :4] = (2.0 ** rng.integers(-2, 2, nb)).astype(np.float32).view(np.uint8).reshape(-1, 4)
+    blk[:, 4:] = rng.integers(0, 256, (nb, 16)).astype(np.uint8)
+    a = rng.integers(-3, 4, M * K).astype(np.float32)
+    c = run_q4(be, blk.ravel(), a, M, K, N, kernel="matmul_forward_q4")
+    assert np.array_equal(c.astype(np.float64), po.q4_gemm_bf16_f64(blk.ravel(), a, M, K, N))
+
+
+def test_q4_gemm_multi_launch(be):
+    """matmul_forward_q4_multi (fp32 and bf16 activations) over mixed shapes."""
+    shapes = [(512, 576, 576), (100, 96, 70), (513, 64, 65), (64, 1536, 576)]
+    ws, as_ = [], []
+    for i, (M, K, N) in enumerate(shapes):
+        ws.append(po.quantize_q4(bmhip.synth_normal(bmhip.synth_seed(75, 0, i, 0), 0.02, N * K)))
+        as_.append(bmhip.synth_normal(bmhip.synth_seed(75, 0, i, 1), 1.0, M * K))
+    a_off = np.cumsum([0] + [a.size for a in as_[:-1]])
+    w_off = np.cumsum([0] + [w.size for w in ws[:-1]])
+    c_off = np.cumsum([0] + [M * N for (M, K, N) in shapes[:-1]])
+    M_, K_, N_ = [s[0] for s in shapes], [s[1] for s in shapes], [s[2] for s in shapes]
+    plan, nt = bmhip.gemm_plan(a_off, w_off, c_off, M_, N_, K_, K_, N_)
+    a32 = np.concatenate(as_)
+    A32, W, pb = be.upload(a32), be.upload(np.concatenate(ws)), be.upload(plan)
+    A16 = be.alloc(a32.size * 2)
+    assert be.dispatch("cast_f32_bf16", [A32, A16, be.params(a32.size, dtype=np.int64)], (a32.size,), (256,)) == 0
+    ctot = sum(M * N for (M, K, N) in shapes)
+    C32, C16 = be.alloc(4 * ctot), be.alloc(4 * ctot)
+    k = "matmul_forward_q4_multi"
+    assert be.dispatch(k, [be.params(len(shapes), nt), pb, A32, W, C32], (nt * 256,), (256,)) == 0
+    assert be.dispatch(k, [be.params(len(shapes), nt, 1), pb, A16, W, C16], (nt * 256,), (256,)) == 0
+    c32, c16 = C32.read(np.float32), C16.read(np.float32)
+    assert np.array_equal(c32, c16)
+    for i, (M, K, N) in enumerate(shapes):
+        got = c32[c_off[i]:c_off[i] + M * N]
+        assert normwise(got, po.q4_gemm_bf16_f64(ws[i], as_[i], M, K, N)) <= 1e-4, i
+    # the Q4 arena one block short of the last problem's rows is rejected
+    short = be.upload(np.concatenate(ws)[:-20])
+    assert be.dispatch(k, [be.params(len(shapes), nt), pb, A32, short, C32], (nt * 256,), (256,)) == -1
 
 
 def test_q4_matvec_bias(be):
