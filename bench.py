@@ -252,6 +252,7 @@ def gemm_leg(steps: int, warmup: int):
     wl = Workload.__new__(Workload)  # reuse the Q8 weight packing of the matvec workload
     wl.be = be
     wl.probs = probs
+    wl.fmt, wl.seed, wl.pack_kernel = "q8", BASE_SEED, FORMATS["q8"][1]
     OC = np.array([p[4] for p in probs], np.int64)
     K = np.array([p[5] for p in probs], np.int64)
     wbytes = OC * (K // 32) * 36
@@ -334,7 +335,7 @@ def copy_ceiling(mib: int = 2048, reps: int = 5):
             "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}
 
 
-def prefill_leg(reps: int = 5):
+def prefill_leg(reps: int = 5, graph: bool = True):
     """SmolLM2-135M prompt prefill through bm_forward (one pass at position 0:
     bf16-MFMA projections, causal attention, the KV cache filled), for 128-
     and 512-token prompts; reported as prompt tokens per second, against the
@@ -343,7 +344,7 @@ def prefill_leg(reps: int = 5):
     out = {"workload": "SmolLM2-135M Q8 prefill of a random prompt via bm_forward (random init as config 5)"}
     for n in (128, 512):
         toks = bmhip.synth_uniform_int(2025 + n, 0, dims["V"], n)
-        eng = bmhip.Engine(dims, max_seq_len=n + 8, seed=2025)
+        eng = bmhip.Engine(dims, max_seq_len=n + 8, seed=2025, graph=graph)
         eng.forward(toks)  # allocates the prefill buffers
         ts = []
         for _ in range(reps):
@@ -444,7 +445,7 @@ def main():
         if args.gemm:
             out["prefill_gemm"] = gemm_leg(max(args.steps // 10, 10), 3)
         if args.prefill:
-            out["prefill"] = prefill_leg()
+            out["prefill"] = prefill_leg(graph=bool(args.e2e_graph))
         if args.e2e:
             out["e2e_decode"] = e2e_decode(0, args.cpu_threads, bool(args.e2e_graph))
         print(json.dumps(out), flush=True)
@@ -490,7 +491,7 @@ def main():
 
     q4 = q4_leg(args.model, args.steps, args.warmup) if args.q4 else None
     gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
-    prefill = prefill_leg() if args.prefill else None
+    prefill = prefill_leg(graph=bool(args.e2e_graph)) if args.prefill else None
     ceiling = copy_ceiling()
     e2e = (e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads, bool(args.e2e_graph))
            if args.e2e else None)
