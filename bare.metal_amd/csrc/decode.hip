@@ -1050,6 +1050,184 @@ __device__ __forceinline__ void dec_attn_head(const DecAttn& a, int h, int b, in
     }
 }
 
+/* B = 1 decode attention with the cache loads issued up front.  While the
+ * step holds at most ATT_CH keys, lane t loads the K rows of keys t (and
+ * t + NT) and the V rows of its first VJ keys in the P.V layout before the
+ * RoPE, so those loads overlap the q/k/v reads and the barriers that
+ * follow; scores, softmax and P.V then run on registers and LDS, with the
+ * same thread assignment and summation order as dec_attn_head (the same
+ * bits).  Loads of keys past the cache are not issued.  How far ahead is
+ * chosen from the step's length (more registers in flight only where there
+ * are keys to fill them); longer steps take dec_attn_head's chunked path. */
+template <int HD, int VJ, bool K2>
+__device__ __forceinline__ void attn1_body(const DecAttn& a, int h, int b, int pos, const float* qh, const float* kr,
+                                           const float* vr) {
+    constexpr int HD4 = HD / 4, KG = NT / HD4;
+    __shared__ float qs[HD];
+    __shared__ float ks[HD];
+    __shared__ float vs[HD];
+    __shared__ float sc[ATT_CH];
+    __shared__ float4 red4[NT];
+    __shared__ float sh[4];
+    const int kv_mul = a.NH / a.NKV, kh = h / kv_mul;
+    const int S = pos + 1, n_cached = pos;
+    const int t = threadIdx.x;
+    const size_t slab = (size_t)a.MS * a.KV;
+    float* kT = a.kvc + ((size_t)b * a.L + a.layer) * 2 * slab + (size_t)kh * HD * a.MS;
+    float* vc = a.kvc + (((size_t)b * a.L + a.layer) * 2 + 1) * slab + kh * HD;
+    const int kg = t / HD4, dg = t - kg * HD4;
+    float4 kp[HD4], kp2[K2 ? HD4 : 1];
+    if (t < n_cached) {
+        const float* kcol = kT + (size_t)t * 4;
+#pragma unroll
+        for (int j = 0; j < HD4; j++)
+            __builtin_memcpy(&kp[j], __builtin_assume_aligned(kcol + (size_t)j * a.MS * 4, 16), 16);
+    }
+    if (K2 && t + NT < n_cached) {
+        const float* kcol = kT + (size_t)(t + NT) * 4;
+#pragma unroll
+        for (int j = 0; j < (K2 ? HD4 : 1); j++)
+            __builtin_memcpy(&kp2[j], __builtin_assume_aligned(kcol + (size_t)j * a.MS * 4, 16), 16);
+    }
+    float4 vp[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++)
+        if (kg + KG * j < n_cached)
+            __builtin_memcpy(&vp[j], __builtin_assume_aligned(vc + (size_t)(kg + KG * j) * a.KV + 4 * dg, 16), 16);
+
+    if (t < HD / 2) {
+        const float fr = a.inv_freq[t];
+        const float ang = (float)pos * fr;
+        const float c = cosf(ang), sn = sinf(ang);
+        const float q0 = qh[t], q1 = qh[t + HD / 2];
+        qs[t] = q0 * c - q1 * sn;
+        qs[t + HD / 2] = q0 * sn + q1 * c;
+        const float k0 = kr[t], k1 = kr[t + HD / 2];
+        ks[t] = k0 * c - k1 * sn;
+        ks[t + HD / 2] = k0 * sn + k1 * c;
+    }
+    if (t < HD) vs[t] = vr[t];
+    __syncthreads();
+    if (h % kv_mul == 0 && t < HD) {
+        kT[((size_t)(t >> 2) * a.MS + pos) * 4 + (t & 3)] = ks[t];
+        vc[(size_t)pos * a.KV + t] = vs[t];
+    }
+    float qr[HD];
+#pragma unroll
+    for (int e = 0; e < HD; e++) qr[e] = qs[e];
+    float s_cur;
+    {
+        float c0 = 0.f, c1 = 0.f;
+        for (int e = 0; e < HD; e += 2) {
+            c0 = fmaf(qs[e], ks[e], c0);
+            c1 = fmaf(qs[e + 1], ks[e + 1], c1);
+        }
+        s_cur = (c0 + c1) * a.scale;
+    }
+    auto score = [&](const float4* k4) {
+        float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+        for (int j = 0; j < HD4; j++) {
+            s0 = fmaf(qr[4 * j + 0], k4[j].x, s0);
+            s1 = fmaf(qr[4 * j + 1], k4[j].y, s1);
+            s2 = fmaf(qr[4 * j + 2], k4[j].z, s2);
+            s3 = fmaf(qr[4 * j + 3], k4[j].w, s3);
+        }
+        return ((s0 + s1) + (s2 + s3)) * a.scale;
+    };
+    float lmax = -INFINITY;
+    if (t < S) {
+        const float sv = t < n_cached ? score(kp) : s_cur;
+        sc[t] = sv;
+        lmax = sv;
+    }
+    int i0 = t + NT;
+    if (K2) {
+        if (t + NT < S) {
+            const float sv = t + NT < n_cached ? score(kp2) : s_cur;
+            sc[t + NT] = sv;
+            lmax = fmaxf(lmax, sv);
+        }
+        i0 += NT;
+    }
+    for (int i = i0; i < S; i += NT) {
+        float sv = s_cur;
+        if (i < n_cached) {
+            float4 k4[HD4];
+            const float* kcol = kT + (size_t)i * 4;
+#pragma unroll
+            for (int j = 0; j < HD4; j++)
+                __builtin_memcpy(&k4[j], __builtin_assume_aligned(kcol + (size_t)j * a.MS * 4, 16), 16);
+            sv = score(k4);
+        }
+        sc[i] = sv;
+        lmax = fmaxf(lmax, sv);
+    }
+    const float cmax = block_max(lmax, sh);
+    float lsum = 0.0f;
+    for (int i = t; i < S; i += NT) {
+        const float p = expf(sc[i] - cmax);
+        sc[i] = p;
+        lsum += p;
+    }
+    const float csum = block_sum(lsum, sh); /* its barriers also publish sc[] */
+    float4 part = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+        const int i = kg + KG * j;
+        if (i < n_cached) {
+            const float p = sc[i];
+            part.x = fmaf(p, vp[j].x, part.x);
+            part.y = fmaf(p, vp[j].y, part.y);
+            part.z = fmaf(p, vp[j].z, part.z);
+            part.w = fmaf(p, vp[j].w, part.w);
+        }
+    }
+#pragma unroll 8
+    for (int i = kg + KG * VJ; i < n_cached; i += KG) {
+        float4 v4;
+        __builtin_memcpy(&v4, __builtin_assume_aligned(vc + (size_t)i * a.KV + 4 * dg, 16), 16);
+        const float p = sc[i];
+        part.x = fmaf(p, v4.x, part.x);
+        part.y = fmaf(p, v4.y, part.y);
+        part.z = fmaf(p, v4.z, part.z);
+        part.w = fmaf(p, v4.w, part.w);
+    }
+    if (kg == n_cached % KG) { /* the current position, from LDS */
+        const float p = sc[n_cached];
+        part.x = fmaf(p, vs[4 * dg + 0], part.x);
+        part.y = fmaf(p, vs[4 * dg + 1], part.y);
+        part.z = fmaf(p, vs[4 * dg + 2], part.z);
+        part.w = fmaf(p, vs[4 * dg + 3], part.w);
+    }
+    red4[t] = part;
+    __syncthreads();
+    if (t < HD) {
+        const int c4 = t >> 2, ln = t & 3;
+        float sum = 0.0f;
+        for (int k = 0; k < KG; k++) {
+            const float4 r = red4[k * HD4 + c4];
+            sum += ln == 0 ? r.x : ln == 1 ? r.y : ln == 2 ? r.z : r.w;
+        }
+        a.out[(size_t)b * a.NH * HD + h * HD + t] = sum / csum;
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(NT) void k_dec_attn1(DecAttn a) {
+    constexpr int KG = NT / (HD / 4);
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int kh = h / (a.NH / a.NKV);
+    const float* qh = a.q + (size_t)b * a.NH * HD + h * HD;
+    const float* kr = a.k + (size_t)b * a.KV + kh * HD;
+    const float* vr = a.v + (size_t)b * a.KV + kh * HD;
+    const int pos = a.st->pos; /* uniform across the workgroup: so are the branches below */
+    if (pos + 1 > ATT_CH) dec_attn_head<HD>(a, h, b, pos, true, b, qh, kr, vr);
+    else if (pos < 4 * KG) attn1_body<HD, 4, false>(a, h, b, pos, qh, kr, vr);
+    else if (pos < NT) attn1_body<HD, NT / KG, false>(a, h, b, pos, qh, kr, vr);
+    else attn1_body<HD, (3 * NT / 2) / KG, true>(a, h, b, pos, qh, kr, vr);
+}
+
 template <int HDT>
 __global__ __launch_bounds__(NT) void k_dec_attn(DecAttn a) {
     const int HD = HDT > 0 ? HDT : a.HD;
@@ -1595,7 +1773,7 @@ extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
         BMK_LAUNCH_CHECK();
         return 0;
     }
-    if (a->HD == 64) hipLaunchKernelGGL(k_dec_attn<64>, dim3(a->NH, B), dim3(NT), 0, s, *a);
+    if (a->HD == 64) hipLaunchKernelGGL(k_dec_attn1<64>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     else if (a->HD == 128) hipLaunchKernelGGL(k_dec_attn<128>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     else hipLaunchKernelGGL(k_dec_attn<0>, dim3(a->NH, B), dim3(NT), 0, s, *a);
     BMK_LAUNCH_CHECK();

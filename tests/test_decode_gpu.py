@@ -141,12 +141,13 @@ def test_engine_step_matches_oracle(dims):
     assert max(errs) <= LOGIT_TOL, errs
 
 
-@pytest.mark.parametrize("B", [1, 2])
-def test_long_context_matches_oracle(B):
-    """1100 positions: each of the attention kernel's 8 waves walks several
-    64-key chunks (online softmax across chunks, then across waves)."""
+@pytest.mark.parametrize("B,n", [(1, 1100), (2, 1100), (1, 2100)])
+def test_long_context_matches_oracle(B, n):
+    """1100 positions: each of the batched attention kernel's 8 waves walks
+    several 64-key chunks (online softmax across chunks, then across waves);
+    at B = 1 the prefetching kernel's deepest variant plus its load loop.
+    2100 positions: past one LDS chunk of scores, the chunked path."""
     w = bmhip.synthetic_weights(SMALL, 23)
-    n = 1100
     toks = bmhip.synth_uniform_int(24, 0, SMALL["V"], n * B).reshape(n, B)
     eng = bmhip.Engine(SMALL, max_seq_len=n, weights=w, batch=B)
     orcs = [oracle_decoder(SMALL, w, n) for _ in range(B)]
