@@ -1688,9 +1688,14 @@ extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {
 /* Launch shape of a fused matvec phase over C columns: the smallest
  * workgroup that holds a row's C/32 block columns, one row pass per lane;
  * a SwiGLU phase keeps whole (gate, up) row pairs in a tile. */
-static void dec_mv_shape(int C, int glu, int* wt, int* slots) {
+static void dec_mv_shape(int C, int glu, int* wt, int* slots, int* u) {
     const int nb = C / 32;
     *wt = nb <= 64 ? 64 : (nb <= 128 ? 128 : 256);
+    *u = 1;
+    if (glu && nb <= 64) { /* gate/up of a narrow row: 128 lanes, two passes (measured fastest) */
+        *wt = 128;
+        *u = 2;
+    }
     *slots = *wt / nb;
     if (glu && *slots == 1 && *wt < 256) { /* a pair needs two row slots */
         *wt *= 2;
@@ -1700,11 +1705,11 @@ static void dec_mv_shape(int C, int glu, int* wt, int* slots) {
 }
 
 extern "C" int dec_mv_tiles(int OC, int C, int glu) {
-    int wt, slots;
-    dec_mv_shape(C, glu, &wt, &slots);
+    int wt, slots, u;
+    dec_mv_shape(C, glu, &wt, &slots, &u);
     if (slots == 0) return -1; /* a gate/up pair wider than one workgroup: not supported */
     const long n = glu ? 2L * OC : (long)OC;
-    return (int)((n + slots - 1) / slots);
+    return (int)((n + (long)slots * u - 1) / ((long)slots * u));
 }
 
 /* wf: 0 fp32 rows, 1 Q8 rows, 2 bf16 rows */
@@ -1735,19 +1740,20 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
         BMK_LAUNCH_CHECK();
         return 0;
     }
-    int wt;
-    dec_mv_shape(a.C, a.glu, &wt, &a.slots);
+    int wt, u;
+    dec_mv_shape(a.C, a.glu, &wt, &a.slots, &u);
     if (a.slots == 0) return -1;
     const dim3 grid(a.tile0[a.nmat]);
-    if (a.qf == QF_Q4) {
-        if (wt == 64) hipLaunchKernelGGL((k_dec_mv4<64, 1>), grid, dim3(64), 0, s, a);
-        else if (wt == 128) hipLaunchKernelGGL((k_dec_mv4<128, 1>), grid, dim3(128), 0, s, a);
-        else hipLaunchKernelGGL((k_dec_mv4<256, 1>), grid, dim3(256), 0, s, a);
-    } else {
-        if (wt == 64) hipLaunchKernelGGL((k_dec_mv<64, 1>), grid, dim3(64), 0, s, a);
-        else if (wt == 128) hipLaunchKernelGGL((k_dec_mv<128, 1>), grid, dim3(128), 0, s, a);
-        else hipLaunchKernelGGL((k_dec_mv<256, 1>), grid, dim3(256), 0, s, a);
-    }
+#define DEC_MV(K)                                                                    \
+    do {                                                                             \
+        if (wt == 64) hipLaunchKernelGGL((K<64, 1>), grid, dim3(64), 0, s, a);       \
+        else if (wt == 128 && u == 2) hipLaunchKernelGGL((K<128, 2>), grid, dim3(128), 0, s, a); \
+        else if (wt == 128) hipLaunchKernelGGL((K<128, 1>), grid, dim3(128), 0, s, a); \
+        else hipLaunchKernelGGL((K<256, 1>), grid, dim3(256), 0, s, a);             \
+    } while (0)
+    if (a.qf == QF_Q4) DEC_MV(k_dec_mv4);
+    else DEC_MV(k_dec_mv);
+#undef DEC_MV
     BMK_LAUNCH_CHECK();
     return 0;
 }
