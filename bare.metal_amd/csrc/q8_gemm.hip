@@ -252,8 +252,13 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
 
     /* Epilogue, 16x16 D layout: lane holds rows 4*(lane/16)+v, column
      * lane%16.  Interior tiles store without bounds checks from one base
-     * with 32-bit offsets (each wave instruction writes 4 rows x 64 bytes);
-     * staging the tile through LDS for whole-row stores measured slower. */
+     * with 32-bit offsets (each wave instruction writes 4 rows x 64 bytes).
+     * C is written once and not read back by this launch, so the stores are
+     * nontemporal: they stream past the caches instead of evicting the
+     * weight panels that the other M tiles still read (measured 8-10%
+     * faster on the 135M prefill set).  Staging the tile through LDS for
+     * whole-row stores, and 16-byte stores of a transposed accumulator,
+     * both measured slower. */
     float* Ct = Cm + (size_t)(m0 + wm + 4 * (lane >> 4)) * ldc + n0 + wn + (lane & 15);
     if (m0 + BM <= M && n0 + BN <= N) {
 #pragma unroll
@@ -261,7 +266,8 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int v = 0; v < 4; v++) Ct[(unsigned)(16 * i + v) * (unsigned)ldc + 16 * j] = acc[i][j][v];
+                for (int v = 0; v < 4; v++)
+                    __builtin_nontemporal_store(acc[i][j][v], &Ct[(unsigned)(16 * i + v) * (unsigned)ldc + 16 * j]);
     } else {
 #pragma unroll
         for (int i = 0; i < 4; i++)
