@@ -30,6 +30,7 @@
 #include "bmk.h"
 #include "decode_state.h"
 #include "q8_common.h"
+#include "q8_gemm.h"
 
 #include <math.h>
 #include <string.h>
@@ -1475,6 +1476,278 @@ __global__ __launch_bounds__(NT) void k_pf_attn(DecAttn a, const float* __restri
                        v + (size_t)p * a.KV + kh * HD);
 }
 
+/* Causal attention of a block of PQB = 16 consecutive prompt positions of
+ * one query head, head size 64: softmax(q.k * scale) over keys 0..p, times
+ * V, on fp32 MFMA (v_mfma_f32_16x16x4f32).  Two sources share the kernel:
+ *  - PF_ENGINE: the engine's prefill.  q rows are un-roped ([n][NH*HD]; the
+ *    kernel applies RoPE at each position as dec_attn_head does), K and V
+ *    come from the KV cache of layer a.layer (K per KV head as
+ *    [HD/4][MS] float4, V row-major [MS][KV]), the output is bf16 (the
+ *    o-projection's operand).
+ *  - PF_FLAT: the reference's prefill attention ABI (forward.metal:1904-2114):
+ *    Q roped [S][NH][HD], K and V [S][NKV][HD], fp32 output [S][NH][HD].
+ * Keys are staged through LDS in chunks of PKC: K row-major [key][dim],
+ * V transposed [dim][key] (rows padded by 4 floats, so the 16 rows a wave
+ * reads at once fall in different banks).  The chunk is cut into 16-key
+ * sub-blocks dealt round-robin to the waves; per sub-block a wave forms
+ *   S^T (16 keys x 16 queries) = K_sb Q^T   (16 MFMAs over the 64 dims),
+ * updates a per-query online softmax, and accumulates
+ *   O^T (64 dims x 16 queries) += V_sb^T P^T (16 MFMAs).
+ * The MFMA sums run over any order of their index, so both products use a
+ * permuted one: in S^T, step s of lane group g (= lane/16) takes dimension
+ * 16g + s (a lane reads 16 consecutive dims of its key); in O^T, step s of
+ * lane group g takes key 4g + s, which is exactly the key whose score that
+ * lane holds in element s of its S^T fragment, so P^T goes from the score
+ * registers to the next MFMA with no data movement.  Each wave's (max,
+ * sum, O^T) is merged across waves through LDS at the end.  Keys at or
+ * past n are staged as zeros, masked keys score -inf.  The summation order
+ * differs from the one-query kernels; the mathematics is the same. */
+constexpr int PQB = 16;  /* prompt positions per workgroup */
+constexpr int PKC = 128; /* keys per LDS chunk */
+constexpr int PNW = 4;   /* waves per workgroup */
+constexpr int PNT = 64 * PNW;
+enum { PF_ENGINE = 0, PF_FLAT = 1 };
+
+struct PfFlat {
+    const float* Q;
+    const float* K;
+    const float* V;
+    float* out;
+    float scale;
+    int NH, S, NKV, kv_mul;
+};
+
+template <int MODE>
+__device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f, const float* __restrict__ q,
+                                              unsigned short* __restrict__ out16, int n) {
+    constexpr int HD = 64, HD4 = HD / 4;
+    constexpr int LDK = HD + 4, LDVT = PKC + 4;
+    constexpr int NSB = PKC / 16; /* sub-blocks per chunk */
+    __shared__ float Ks[PKC * LDK];   /* [key][dim] */
+    __shared__ float Vt[HD * LDVT];   /* [dim][key] */
+    __shared__ float Qs[PQB * HD];    /* roped q of the block */
+    __shared__ float Ms[PNW * PQB], Ls[PNW * PQB];
+    const int NH = MODE == PF_FLAT ? f.NH : a.NH;
+    const int kv_mul = MODE == PF_FLAT ? f.kv_mul : a.NH / a.NKV;
+    const float scale = MODE == PF_FLAT ? f.scale : a.scale;
+    const int h = blockIdx.x, p0 = blockIdx.y * PQB;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int col = lane & 15, grp = lane >> 4; /* MFMA column (query / key row) and lane group */
+    const int kh = h / kv_mul;
+    const int p = p0 + col; /* this lane's query position */
+    if (MODE == PF_FLAT) {
+        for (int i = t; i < PQB * HD; i += PNT) {
+            const int r = i / HD, e = i - r * HD;
+            Qs[i] = f.Q[((size_t)min(p0 + r, n - 1) * NH + h) * HD + e];
+        }
+    } else {
+        for (int i = t; i < PQB * (HD / 2); i += PNT) {
+            const int r = i / (HD / 2), e = i - r * (HD / 2);
+            const int pp = min(p0 + r, n - 1);
+            const float ang = (float)pp * a.inv_freq[e];
+            const float c = cosf(ang), sn = sinf(ang);
+            const float* qr = q + (size_t)pp * NH * HD + h * HD;
+            const float q0 = qr[e], q1 = qr[e + HD / 2];
+            Qs[r * HD + e] = q0 * c - q1 * sn;
+            Qs[r * HD + e + HD / 2] = q0 * sn + q1 * c;
+        }
+    }
+    __syncthreads();
+    /* Q^T fragment: step s holds q[col][16*grp + s] */
+    float qf[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++) qf[s] = Qs[col * HD + 16 * grp + s];
+    bmv_f32x4 acc[4]; /* O^T tile t: dims 16t + 4*grp + v, query col */
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[i] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.0f; /* m: per query (same in the 4 lane groups); l: this lane's keys */
+    /* K source: dims 4g..4g+3 of key j at ksrc + j * kstr + g * kgstr (floats); V: row j at vsrc + j * vstr */
+    const float *ksrc, *vsrc;
+    size_t kstr, kgstr, vstr;
+    if (MODE == PF_FLAT) {
+        const size_t KVW = (size_t)f.NKV * HD;
+        ksrc = f.K + kh * HD;
+        kstr = KVW;
+        kgstr = 4;
+        vsrc = f.V + kh * HD;
+        vstr = KVW;
+    } else {
+        const size_t slab = (size_t)a.MS * a.KV;
+        ksrc = a.kvc + (size_t)a.layer * 2 * slab + (size_t)kh * HD * a.MS;
+        kstr = 4;
+        kgstr = (size_t)a.MS * 4;
+        vsrc = a.kvc + ((size_t)a.layer * 2 + 1) * slab + kh * HD;
+        vstr = a.KV;
+    }
+    /* Chunk staging: each thread moves SPT float4 of K (element i: dims
+     * 4*(i / PKC), key i % PKC, so a wave reads consecutive keys of one
+     * cache row) and of V (key i / HD4, dims 4*(i % HD4): whole V rows).
+     * The loads of chunk c+1 are issued into registers before chunk c is
+     * computed, unconditionally (key clamped to n-1; keys at or past n
+     * become zeros when written to LDS). */
+    constexpr int SPT = PKC * HD4 / PNT;
+    float4 kreg[SPT], vreg[SPT];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < SPT; u++) {
+            const int i = t + PNT * u;
+            const int kk = min(c0 + i % PKC, n - 1), kg = i / PKC;
+            const int vk = min(c0 + i / HD4, n - 1), vg = i % HD4;
+            __builtin_memcpy(&kreg[u], __builtin_assume_aligned(ksrc + (size_t)kk * kstr + kg * kgstr, 16), 16);
+            __builtin_memcpy(&vreg[u], __builtin_assume_aligned(vsrc + (size_t)vk * vstr + 4 * vg, 16), 16);
+        }
+    };
+    const int kend = min(p0 + PQB, n); /* keys 0 .. kend-1 */
+    fetch(0);
+    for (int c0 = 0; c0 < kend; c0 += PKC) {
+        __syncthreads(); /* the previous chunk has been read */
+#pragma unroll
+        for (int u = 0; u < SPT; u++) {
+            const int i = t + PNT * u;
+            const int kk = i % PKC, kg = i / PKC, vk = i / HD4, vg = i % HD4;
+            const bool kin = c0 + kk < n, vin = c0 + vk < n;
+            const float4 kv = kreg[u], vv = vreg[u];
+            *(float4*)&Ks[kk * LDK + 4 * kg] =
+                make_float4(kin ? kv.x : 0.f, kin ? kv.y : 0.f, kin ? kv.z : 0.f, kin ? kv.w : 0.f);
+            Vt[(4 * vg + 0) * LDVT + vk] = vin ? vv.x : 0.f;
+            Vt[(4 * vg + 1) * LDVT + vk] = vin ? vv.y : 0.f;
+            Vt[(4 * vg + 2) * LDVT + vk] = vin ? vv.z : 0.f;
+            Vt[(4 * vg + 3) * LDVT + vk] = vin ? vv.w : 0.f;
+        }
+        __syncthreads();
+        if (c0 + PKC < kend) fetch(c0 + PKC);
+        for (int sb = wave; sb < NSB; sb += PNW) {
+            const int k0 = c0 + 16 * sb; /* first key of the sub-block */
+            if (k0 >= kend) break;       /* past every query of the block (wave-uniform) */
+            /* S^T[key 4*grp + v][query col] */
+            bmv_f32x4 st = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
+            const float* kr = &Ks[(16 * sb + col) * LDK + 16 * grp];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k4 = *(const float4*)&kr[4 * i];
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qf[4 * i + 0], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qf[4 * i + 1], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qf[4 * i + 2], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qf[4 * i + 3], st, 0, 0, 0);
+            }
+            float sv[4];
+            float cm = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                sv[v] = k0 + 4 * grp + v <= p ? st[v] * scale : -INFINITY;
+                cm = fmaxf(cm, sv[v]);
+            }
+            cm = fmaxf(cm, __shfl_xor(cm, 16));
+            cm = fmaxf(cm, __shfl_xor(cm, 32));
+            const float mn = fmaxf(m, cm);
+            const bool live = mn > -INFINITY; /* some key of this query admitted so far */
+            const float fr = live ? expf(m - mn) : 1.0f;
+            float pv[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) pv[v] = live ? expf(sv[v] - mn) : 0.0f;
+            l = l * fr + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) acc[ti] *= fr;
+            m = live ? mn : m;
+            /* O^T[dim 16t + col'][query] += V^T[dim][key 4*grp + s] * P^T[key][query] */
+#pragma unroll
+            for (int ti = 0; ti < 4; ti++) {
+                const float4 v4 = *(const float4*)&Vt[(16 * ti + col) * LDVT + 16 * sb + 4 * grp];
+                acc[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.x, pv[0], acc[ti], 0, 0, 0);
+                acc[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.y, pv[1], acc[ti], 0, 0, 0);
+                acc[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.z, pv[2], acc[ti], 0, 0, 0);
+                acc[ti] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.w, pv[3], acc[ti], 0, 0, 0);
+            }
+        }
+    }
+    /* this wave's sum over its keys: add the four lane groups */
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    __syncthreads(); /* every wave is done with Ks */
+    float* Ws = Ks; /* [wave][dim][query] */
+#pragma unroll
+    for (int ti = 0; ti < 4; ti++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) Ws[(wave * HD + 16 * ti + 4 * grp + v) * PQB + col] = acc[ti][v];
+    if (grp == 0) {
+        Ms[wave * PQB + col] = m;
+        Ls[wave * PQB + col] = l;
+    }
+    __syncthreads();
+    const int r = t / HD4, g = t - r * HD4; /* query r, dimensions 4g .. 4g+3 */
+    if (r >= PQB || p0 + r >= n) return;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < PNW; w++) mx = fmaxf(mx, Ms[w * PQB + r]);
+    float den = 0.f, o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+#pragma unroll
+    for (int w = 0; w < PNW; w++) {
+        const float mv = Ms[w * PQB + r];
+        const float fr = mv == -INFINITY ? 0.0f : expf(mv - mx);
+        const float* src = &Ws[(w * HD + 4 * g) * PQB + r];
+        den = fmaf(fr, Ls[w * PQB + r], den);
+        o0 = fmaf(fr, src[0 * PQB], o0);
+        o1 = fmaf(fr, src[1 * PQB], o1);
+        o2 = fmaf(fr, src[2 * PQB], o2);
+        o3 = fmaf(fr, src[3 * PQB], o3);
+    }
+    const size_t off = ((size_t)(p0 + r) * NH + h) * HD + 4 * g;
+    if (MODE == PF_FLAT) {
+        f.out[off + 0] = o0 / den;
+        f.out[off + 1] = o1 / den;
+        f.out[off + 2] = o2 / den;
+        f.out[off + 3] = o3 / den;
+    } else {
+        out16[off + 0] = bf16_bits(o0 / den);
+        out16[off + 1] = bf16_bits(o1 / den);
+        out16[off + 2] = bf16_bits(o2 / den);
+        out16[off + 3] = bf16_bits(o3 / den);
+    }
+}
+
+__global__ __launch_bounds__(PNT) void k_pf_attn_blk(DecAttn a, const float* __restrict__ q,
+                                                    unsigned short* __restrict__ out16, int n) {
+    const PfFlat f = {};
+    pf_attn_block<PF_ENGINE>(a, f, q, out16, n);
+}
+
+__global__ __launch_bounds__(PNT) void k_attn_prefill64(PfFlat f) {
+    const DecAttn a = {};
+    pf_attn_block<PF_FLAT>(a, f, nullptr, nullptr, f.S);
+}
+
+/* Any head size up to 128 on the reference's prefill attention ABI: one
+ * wave per (query position, head); lane owns dimensions lane and lane + 64;
+ * online softmax over keys 0..i with a wave-wide sum per score. */
+__global__ __launch_bounds__(NT) void k_attn_prefill_wave(PfFlat f, int HD) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.y * 4 + wave, h = blockIdx.x;
+    if (i >= f.S) return;
+    const int kh = h / f.kv_mul;
+    const size_t KVW = (size_t)f.NKV * HD;
+    const float* qi = f.Q + ((size_t)i * f.NH + h) * HD;
+    const bool d0 = lane < HD, d1 = lane + 64 < HD;
+    const float q0 = d0 ? qi[lane] : 0.f, q1 = d1 ? qi[lane + 64] : 0.f;
+    float a0 = 0.f, a1 = 0.f, m = -INFINITY, l = 0.f;
+    for (int j = 0; j <= i; j++) {
+        const float* kj = f.K + (size_t)j * KVW + kh * HD;
+        float part = (d0 ? q0 * kj[lane] : 0.f) + (d1 ? q1 * kj[lane + 64] : 0.f);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o);
+        const float sc = part * f.scale;
+        const float mn = fmaxf(m, sc);
+        const float al = expf(m - mn), be = expf(sc - mn);
+        l = l * al + be;
+        const float* vj = f.V + (size_t)j * KVW + kh * HD;
+        if (d0) a0 = a0 * al + be * vj[lane];
+        if (d1) a1 = a1 * al + be * vj[lane + 64];
+        m = mn;
+    }
+    float* oi = f.out + ((size_t)i * f.NH + h) * HD;
+    if (d0) oi[lane] = a0 / l;
+    if (d1) oi[lane + 64] = a1 / l;
+}
+
 /* out = bf16(silu(g) * u) */
 __global__ __launch_bounds__(NT) void k_pf_swiglu_bf16(const float* __restrict__ g, const float* __restrict__ u,
                                                        unsigned short* __restrict__ out, long n) {
@@ -1589,6 +1862,46 @@ extern "C" int bmk_launch_attention(const bmk_launch_t* a) {
     BMK_REQUIRE(((uintptr_t)a->dev[1] & 15) == 0 && KV % 4 == 0, "attention: kv cache rows must be 16-byte aligned");
     hipLaunchKernelGGL(k_attention, dim3(NH), dim3(NT), 0, a->stream, (const float*)a->dev[0], (const float*)a->dev[1],
                        (float*)a->dev[2], HD, KV, S, kv_mul, layer, MS, scale);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* attention_forward_prefill / _warp / _tiled (reference forward.metal:1904-2114,
+ * selected by scheduler.c:1081-1089 in prefill mode):
+ * {Q [S][NH][HD] (roped), K [S][NKV][HD], V [S][NKV][HD], out [S][NH][HD],
+ *  params int{NH, S, HD, NKV, kv_mul}, scale}.  Causal softmax(Q K^T * scale) V
+ * per head, head h reading KV head h / kv_mul.  Head size 64: blocks of 16
+ * positions per workgroup; other head sizes up to 128: one wave per
+ * (position, head).  The reference's kernels return without writing on a
+ * head size they do not handle; here such a request is an error. */
+extern "C" int bmk_launch_attention_prefill(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 4, 20, "params");
+    BMK_NEED_BYTES(a, 5, 4, "scale");
+    PfFlat f;
+    f.NH = bmk_pi(a, 4, 0);
+    f.S = bmk_pi(a, 4, 1);
+    const int HD = bmk_pi(a, 4, 2);
+    f.NKV = bmk_pi(a, 4, 3);
+    f.kv_mul = bmk_pi(a, 4, 4);
+    f.scale = bmk_pf(a, 5, 0);
+    BMK_REQUIRE(f.NH > 0 && f.S >= 0 && HD > 0 && HD <= 128 && f.NKV > 0 && f.kv_mul > 0 &&
+                    (f.NH - 1) / f.kv_mul < f.NKV,
+                "attention prefill: bad params NH=%d S=%d HD=%d NKV=%d kv_mul=%d", f.NH, f.S, HD, f.NKV, f.kv_mul);
+    if (f.S == 0) return 0;
+    const size_t qn = (size_t)f.S * f.NH * HD, kn = (size_t)f.S * f.NKV * HD;
+    BMK_NEED_BYTES(a, 0, qn * 4, "Q");
+    BMK_NEED_BYTES(a, 1, kn * 4, "K");
+    BMK_NEED_BYTES(a, 2, kn * 4, "V");
+    BMK_NEED_BYTES(a, 3, qn * 4, "out");
+    f.Q = (const float*)a->dev[0];
+    f.K = (const float*)a->dev[1];
+    f.V = (const float*)a->dev[2];
+    f.out = (float*)a->dev[3];
+    const bool aligned = (((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1] | (uintptr_t)a->dev[2] | (uintptr_t)a->dev[3]) & 15) == 0;
+    if (HD == 64 && aligned)
+        hipLaunchKernelGGL(k_attn_prefill64, dim3(f.NH, (f.S + PQB - 1) / PQB), dim3(PNT), 0, a->stream, f);
+    else
+        hipLaunchKernelGGL(k_attn_prefill_wave, dim3(f.NH, (f.S + 3) / 4), dim3(NT), 0, a->stream, f, HD);
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -1834,16 +2147,25 @@ extern "C" int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsi
     return 0;
 }
 
+/* RoPE + cache append of every position, then causal attention; the
+ * result goes to out16 as bf16 (the o-projection's operand).  Head size
+ * 64: blocks of PQB positions per workgroup, written as bf16 directly;
+ * other head sizes: one workgroup per (head, position) into a->out (fp32),
+ * then the cast. */
 extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n,
-                                hipStream_t s) {
+                                unsigned short* out16, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_kv, dim3(n), dim3(NT), 0, s, *a, k, v);
     BMK_LAUNCH_CHECK();
+    if (a->HD == 64) {
+        hipLaunchKernelGGL(k_pf_attn_blk, dim3(a->NH, (n + PQB - 1) / PQB), dim3(PNT), 0, s, *a, q, out16, n);
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
     const dim3 g(a->NH, n);
-    if (a->HD == 64) hipLaunchKernelGGL(k_pf_attn<64>, g, dim3(NT), 0, s, *a, q, k, v);
-    else if (a->HD == 128) hipLaunchKernelGGL(k_pf_attn<128>, g, dim3(NT), 0, s, *a, q, k, v);
+    if (a->HD == 128) hipLaunchKernelGGL(k_pf_attn<128>, g, dim3(NT), 0, s, *a, q, k, v);
     else hipLaunchKernelGGL(k_pf_attn<0>, g, dim3(NT), 0, s, *a, q, k, v);
     BMK_LAUNCH_CHECK();
-    return 0;
+    return gm_cast_bf16(a->out, out16, (long)n * a->NH * a->HD, s);
 }
 
 extern "C" int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s) {

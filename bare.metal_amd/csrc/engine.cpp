@@ -46,7 +46,8 @@ int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
 int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
 int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
                      hipStream_t s);
-int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, hipStream_t s);
+int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
+                     hipStream_t s);
 int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s);
 int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
@@ -896,7 +897,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
         if (dec_pf_norm_bf16(S->pf_x, l ? S->pf_o : NULL, m->d_ln1 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||
             gemm(g[4 * l + 0], S->pf_qkv) ||
             /* RoPE, cache append, causal attention */
-            dec_pf_attention(&at, q, k, v, n, s) || gm_cast_bf16(S->pf_att, S->pf_a16, (long)n * QD, s) ||
+            dec_pf_attention(&at, q, k, v, n, S->pf_a16, s) ||
             /* o, residual, RMSNorm, gate/up, SwiGLU, down */
             gemm(g[4 * l + 1], S->pf_o) ||
             dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_ln2 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||

@@ -27,6 +27,7 @@ int bmk_launch_rmsnorm(const bmk_launch_t* a);
 int bmk_launch_rope(const bmk_launch_t* a);
 int bmk_launch_kv_store(const bmk_launch_t* a);
 int bmk_launch_attention(const bmk_launch_t* a);
+int bmk_launch_attention_prefill(const bmk_launch_t* a);
 int bmk_launch_add(const bmk_launch_t* a);
 int bmk_launch_swiglu(const bmk_launch_t* a);
 int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a);
@@ -77,6 +78,11 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"kv_store", 4, B(3), B(0), bmk_launch_kv_store, 0},
     /* reference forward.metal:1362-1465; {q, kv cache, out, params{NH,HD,NKV,KV,S,kv_mul,layer,MS}, scale} */
     {"attention_forward", 5, B(3) | B(4), B(2), bmk_launch_attention, 0},
+    /* reference forward.metal:1904-2114, prefill attention (scheduler.c:1081-1089);
+     * {Q [S][NH][HD] roped, K [S][NKV][HD], V, out [S][NH][HD], params{NH,S,HD,NKV,kv_mul}, scale} */
+    {"attention_forward_prefill", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
+    {"attention_forward_prefill_warp", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
+    {"attention_forward_prefill_tiled", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
     /* reference forward.metal:1332-1340; {a, b, out, n} */
     {"add_forward", 4, B(3), B(2), bmk_launch_add, 0},
     /* reference forward.metal:1179-1190; {gate, up, out, N} */

@@ -39,6 +39,8 @@ typedef struct {
 extern "C" {
 #endif
 int gm_tiles_for(int M, int N);
+/* dst = bf16(src), round to nearest even, n elements */
+int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int gm_launch_group(GmGroup* g, hipStream_t s);
 int gm_launch_group_qf(GmGroup* g, int qf, hipStream_t s);
 int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,

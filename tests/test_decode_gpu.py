@@ -167,7 +167,14 @@ def cosine(a, b):
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
 
 
-@pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1)], ids=["tiny-12", "small-40", "small-1"])
+# head size 64: the engine's blocked prefill attention (16 positions per
+# workgroup, keys in chunks of 64)
+HD64 = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
+
+
+@pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1), (HD64, 1), (HD64, 17), (HD64, 70),
+                                    (HD64, 150)],
+                         ids=["tiny-12", "small-40", "small-1", "hd64-1", "hd64-17", "hd64-70", "hd64-150"])
 def test_prefill_matches_stepwise(dims, n):
     """bm_forward over a prompt at position 0 (one pass, bf16-MFMA projections)
     against stepping the same tokens one by one, as the reference's
@@ -180,7 +187,7 @@ def test_prefill_matches_stepwise(dims, n):
     V = dims["V"]
     toks = [(37 * i + 11) % V for i in range(n)]
     nxt = (37 * n + 11) % V
-    eng = bmhip.Engine(dims, max_seq_len=64, weights=w)
+    eng = bmhip.Engine(dims, max_seq_len=max(64, n + 8), weights=w)
     pre = eng.forward(toks)
     pre_next = eng.step(nxt)
     eng.reset()
@@ -188,7 +195,7 @@ def test_prefill_matches_stepwise(dims, n):
         step = eng.step(t)
     step_next = eng.step(nxt)
     eng.close()
-    orc = oracle_decoder(dims, w, 64)
+    orc = oracle_decoder(dims, w, max(64, n + 8))
     for pos, t in enumerate(toks):
         r = orc.step(t, pos)
     assert normwise(pre, r) <= 2e-2, normwise(pre, r)

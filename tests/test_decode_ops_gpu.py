@@ -133,6 +133,89 @@ def test_attention_single_key_is_v(be):
     assert np.array_equal(out.read(np.float32), want)
 
 
+def prefill_attn_ref(Q, K, V, NH, NKV, HD, S, kv_mul, scale):
+    """fp64 restatement of the reference's attention_forward_prefill
+    (forward.metal:1904-1948): per position i and head h, softmax over keys
+    0..i of (q_i . k_j) * scale, times V, KV head h / kv_mul."""
+    q = Q.reshape(S, NH, HD).astype(np.float64)
+    k = K.reshape(S, NKV, HD).astype(np.float64)
+    v = V.reshape(S, NKV, HD).astype(np.float64)
+    out = np.zeros((S, NH, HD))
+    causal = np.tril(np.ones((S, S), bool))
+    for h in range(NH):
+        kh = h // kv_mul
+        s = (q[:, h] @ k[:, kh].T) * float(scale)
+        s = np.where(causal, s, -np.inf)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ v[:, kh]
+    return out.reshape(-1)
+
+
+PREFILL_ATTN = ["attention_forward_prefill", "attention_forward_prefill_warp", "attention_forward_prefill_tiled"]
+
+
+def run_prefill_attn(be, name, Q, K, V, NH, NKV, HD, S, kv_mul, scale):
+    out = be.alloc(max(S * NH * HD, 1) * 4)
+    rc = be.dispatch(name, [be.upload(Q), be.upload(K), be.upload(V), out, be.params(NH, S, HD, NKV, kv_mul),
+                            be.upload(f32(scale))], (NH * S,), (256,))
+    return rc, out
+
+
+@pytest.mark.parametrize("name", PREFILL_ATTN)
+@pytest.mark.parametrize("NH,NKV,HD,S", [(9, 3, 64, 1), (9, 3, 64, 37), (9, 3, 64, 200), (15, 5, 64, 129),
+                                         (4, 2, 128, 70), (8, 8, 32, 33), (6, 2, 48, 17)])
+def test_attention_forward_prefill(be, name, NH, NKV, HD, S):
+    """The reference's prefill attention kernels (one ABI, three names):
+    causal GQA softmax attention over a whole prompt against fp64.  S covers
+    one position, partial 16-position blocks, several 64-key chunks; head
+    sizes 64 (blocked kernel) and 32/48/128 (one wave per query)."""
+    rng = np.random.default_rng(S * HD + NH)
+    Q = rng.standard_normal(S * NH * HD).astype(np.float32)
+    K = rng.standard_normal(S * NKV * HD).astype(np.float32)
+    V = rng.standard_normal(S * NKV * HD).astype(np.float32)
+    scale = np.float32(1.0 / np.sqrt(HD))
+    rc, out = run_prefill_attn(be, name, Q, K, V, NH, NKV, HD, S, NH // NKV, scale)
+    assert rc == 0
+    want = prefill_attn_ref(Q, K, V, NH, NKV, HD, S, NH // NKV, scale)
+    assert nw(out.read(np.float32), want) <= TOL
+
+
+@pytest.mark.parametrize("HD", [64, 32])
+def test_attention_prefill_equal_keys_is_running_mean(be, HD):
+    """Equal keys make every admissible score equal, so position i's output
+    is the mean of V over positions 0..i (pins the causal bound and the
+    normalisation)."""
+    NH, NKV, S = 4, 2, 150
+    rng = np.random.default_rng(5)
+    Q = rng.standard_normal(S * NH * HD).astype(np.float32)
+    K = np.tile(rng.standard_normal(NKV * HD).astype(np.float32), S)
+    V = rng.integers(-8, 9, S * NKV * HD).astype(np.float32)
+    rc, out = run_prefill_attn(be, "attention_forward_prefill", Q, K, V, NH, NKV, HD, S, 2, np.float32(0.125))
+    assert rc == 0
+    v = V.reshape(S, NKV, HD).astype(np.float64)
+    mean = np.cumsum(v, axis=0) / np.arange(1, S + 1)[:, None, None]
+    want = np.stack([mean[:, h // 2] for h in range(NH)], axis=1).reshape(-1)
+    assert nw(out.read(np.float32), want) <= TOL
+
+
+def test_attention_prefill_rejects(be):
+    NH, NKV, HD, S = 4, 2, 64, 8
+    Q = np.zeros(S * NH * HD, np.float32)
+    K = np.zeros(S * NKV * HD, np.float32)
+    # head size past 128
+    rc, _ = run_prefill_attn(be, "attention_forward_prefill", np.zeros(S * NH * 160, np.float32),
+                             np.zeros(S * NKV * 160, np.float32), np.zeros(S * NKV * 160, np.float32),
+                             NH, NKV, 160, S, 2, np.float32(0.1))
+    assert rc != 0
+    # a query head that maps past the last KV head
+    rc, _ = run_prefill_attn(be, "attention_forward_prefill", Q, K, K, NH, NKV, HD, S, 1, np.float32(0.1))
+    assert rc != 0
+    # K shorter than S positions
+    rc, _ = run_prefill_attn(be, "attention_forward_prefill", Q, K[: (S - 1) * NKV * HD], K, NH, NKV, HD, S, 2,
+                             np.float32(0.1))
+    assert rc != 0
+
+
 def test_add_and_swiglu(be):
     rng = np.random.default_rng(2)
     n = 1536
