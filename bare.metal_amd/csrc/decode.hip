@@ -278,34 +278,50 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
  * by atomicMax, and the last workgroup to finish turns the keys into
  * tokens, emits them and advances the position. */
 /* Last workgroup of a head launch (every workgroup calls this after its
- * atomicMax): emit the step's tokens and advance the position. */
+ * atomicMax): emit the step's tokens and advance the position.
+ *
+ * Everything the workgroups of the launch exchange is a device-scope atomic
+ * (the per-row argmax keys, the arrival counter), and those are performed
+ * at one point for every XCD.  A workgroup's atomicMax results are waited
+ * for before its barrier (head_key_max), so they are performed before its
+ * arrival is counted; the last arrival reads the keys atomically.  No
+ * agent-scope fence is needed: on this multi-XCD part one compiles to a
+ * writeback and an invalidate of the whole L2 (buffer_wbl2 / buffer_inv
+ * sc1), which in every one of some 900 workgroups cost more than the
+ * head's weight stream.  The plain stores of the last workgroup (tokens,
+ * position) are read by later kernels, after the launch boundary. */
 __device__ void head_finish(const DecHead& a, int& last_wg) {
     const int t = threadIdx.x;
     if (t == 0) {
-        __threadfence();
         const unsigned int prev = atomicAdd(&a.st->done, 1u);
         last_wg = (prev == (unsigned int)a.tiles - 1u);
     }
     __syncthreads();
     if (!last_wg) return;
-    __threadfence();
     DecState* st = a.st;
     const int pos = st->pos;
     const bool emit = !st->host_mode && pos >= st->n_prompt - 1;
     for (int b = t; b < a.B; b += blockDim.x) {
-        const unsigned long long k = atomicAdd(&st->key[b], 0ull);
+        const unsigned long long k = atomicExch(&st->key[b], 0ull); /* read and re-arm */
         const int tok = argmax_key_index(k);
         st->last_token[b] = tok;
         if (emit) a.out_tokens[(size_t)st->n_out * a.B + b] = tok;
-        st->key[b] = 0ull;
     }
     __syncthreads();
     if (t == 0) {
         if (emit) st->n_out = st->n_out + 1;
-        st->done = 0u;
+        atomicExch(&st->done, 0u);
         st->pos = pos + 1;
-        __threadfence();
     }
+}
+
+/* atomicMax of a workgroup's best key, waited for: the returned value is
+ * consumed (into LDS) before the caller's next barrier, so the update has
+ * been performed before the workgroup's arrival is counted. */
+__device__ __forceinline__ void head_key_max(unsigned long long* key, unsigned long long v, int* sink) {
+    const unsigned long long old = atomicMax(key, v);
+    if (old == 0xffffffffffffffffull) *sink = 1;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST); /* the compiler keeps later accesses after the wait */
 }
 
 /* Weight formats of the LM head rows. */
@@ -426,7 +442,7 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
         }
         if (a.st) {
             best = block_argmax_key(best, shk);
-            if (t == 0) atomicMax(&a.st->key[b], best);
+            if (t == 0) head_key_max(&a.st->key[b], best, &last_wg);
         } else {
             __syncthreads(); /* red[] is rewritten for the next row of the batch */
         }
@@ -556,8 +572,9 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
         unsigned long long best = shk[0][b];
 #pragma unroll
         for (int w = 1; w < 4; w++) best = shk[w][b] > best ? shk[w][b] : best;
-        atomicMax(&a.st->key[b], best);
+        head_key_max(&a.st->key[b], best, &last_wg);
     }
+    __syncthreads();
     head_finish(a, last_wg);
 }
 
