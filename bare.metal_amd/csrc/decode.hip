@@ -1428,6 +1428,21 @@ __global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
  * (q8_gemm.hip), as the reference's prefill graph runs them on its BT > 1
  * Q8 path (graph.c:273-381, scheduler.c:1015-1332). */
 
+/* A prefill GEMM output element: the sum of its ks (<= GM_KSPLIT_MAX)
+ * split-K slice copies, stride floats apart, added in slice order.  All
+ * GM_KSPLIT_MAX loads are issued before the first add (copies past ks
+ * re-read copy 0), so an element costs one memory round trip. */
+__device__ __forceinline__ float ld_slices(const float* __restrict__ p, size_t i, int ks, long stride) {
+    float v[GM_KSPLIT_MAX];
+#pragma unroll
+    for (int k = 0; k < GM_KSPLIT_MAX; k++) v[k] = p[i + (size_t)(k < ks ? k : 0) * stride];
+    float s = v[0];
+#pragma unroll
+    for (int k = 1; k < GM_KSPLIT_MAX; k++)
+        if (k < ks) s += v[k];
+    return s;
+}
+
 /* x[p] = emb[tok[p]] */
 __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, const float* __restrict__ emb,
                                                  float* __restrict__ x, int D) {
@@ -1441,7 +1456,7 @@ __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, co
  * RMSNorm(x) * w, the activation of the next GEMM. */
 __global__ __launch_bounds__(NT) void k_pf_norm_bf16(float* __restrict__ x, const float* __restrict__ add,
                                                      const float* __restrict__ w, unsigned short* __restrict__ out,
-                                                     int D, float eps) {
+                                                     int D, float eps, int ks, long stride) {
     __shared__ float sh[4];
     const int p = blockIdx.x;
     float* xr = x + (size_t)p * D;
@@ -1449,7 +1464,7 @@ __global__ __launch_bounds__(NT) void k_pf_norm_bf16(float* __restrict__ x, cons
     for (int j = threadIdx.x; j < D; j += NT) {
         float v = xr[j];
         if (add) {
-            v += add[(size_t)p * D + j];
+            v += ld_slices(add, (size_t)p * D + j, ks, stride);
             xr[j] = v;
         }
         ss = fmaf(v, v, ss);
@@ -1471,14 +1486,14 @@ __global__ __launch_bounds__(NT) void k_pf_kv(DecAttn a, const float* __restrict
         const int kh = i / half, t = i - kh * half;
         const float ang = (float)p * a.inv_freq[t];
         const float c = cosf(ang), sn = sinf(ang);
-        const float* kr = k + (size_t)p * a.KV + kh * HD;
-        const float k0 = kr[t], k1 = kr[t + half];
+        const size_t kr = (size_t)p * a.KV + kh * HD;
+        const float k0 = ld_slices(k, kr + t, a.pf_ks, a.pf_stride), k1 = ld_slices(k, kr + t + half, a.pf_ks, a.pf_stride);
         float* kT = kc + (size_t)kh * HD * a.MS;
         kT[((size_t)(t >> 2) * a.MS + p) * 4 + (t & 3)] = k0 * c - k1 * sn;
         const int t2 = t + half;
         kT[((size_t)(t2 >> 2) * a.MS + p) * 4 + (t2 & 3)] = k0 * sn + k1 * c;
     }
-    for (int i = threadIdx.x; i < a.KV; i += NT) vc[(size_t)p * a.KV + i] = v[(size_t)p * a.KV + i];
+    for (int i = threadIdx.x; i < a.KV; i += NT) vc[(size_t)p * a.KV + i] = ld_slices(v, (size_t)p * a.KV + i, a.pf_ks, a.pf_stride);
 }
 
 /* Causal attention of every prompt position: workgroup (query head h,
@@ -1563,8 +1578,9 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
             const int pp = min(p0 + r, n - 1);
             const float ang = (float)pp * a.inv_freq[e];
             const float c = cosf(ang), sn = sinf(ang);
-            const float* qr = q + (size_t)pp * NH * HD + h * HD;
-            const float q0 = qr[e], q1 = qr[e + HD / 2];
+            const size_t qr = (size_t)pp * NH * HD + h * HD;
+            const float q0 = ld_slices(q, qr + e, a.pf_ks, a.pf_stride);
+            const float q1 = ld_slices(q, qr + e + HD / 2, a.pf_ks, a.pf_stride);
             Qs[r * HD + e] = q0 * c - q1 * sn;
             Qs[r * HD + e + HD / 2] = q0 * sn + q1 * c;
         }
@@ -1767,9 +1783,9 @@ __global__ __launch_bounds__(NT) void k_attn_prefill_wave(PfFlat f, int HD) {
 
 /* out = bf16(silu(g) * u) */
 __global__ __launch_bounds__(NT) void k_pf_swiglu_bf16(const float* __restrict__ g, const float* __restrict__ u,
-                                                       unsigned short* __restrict__ out, long n) {
+                                                       unsigned short* __restrict__ out, long n, int ks, long stride) {
     const long i = (long)blockIdx.x * NT + threadIdx.x;
-    if (i < n) out[i] = bf16_bits(silu_mul(g[i], u[i]));
+    if (i < n) out[i] = bf16_bits(silu_mul(ld_slices(g, (size_t)i, ks, stride), ld_slices(u, (size_t)i, ks, stride)));
 }
 
 } // namespace
@@ -2158,8 +2174,8 @@ extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, i
 }
 
 extern "C" int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
-                                hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, add, w, out, D, eps);
+                                int ks, long stride, hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, add, w, out, D, eps, ks, stride);
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -2178,6 +2194,7 @@ extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k
         BMK_LAUNCH_CHECK();
         return 0;
     }
+    BMK_REQUIRE(a->pf_ks <= 1, "prefill attention: head size %d takes unsplit q/k/v", a->HD);
     const dim3 g(a->NH, n);
     if (a->HD == 128) hipLaunchKernelGGL(k_pf_attn<128>, g, dim3(NT), 0, s, *a, q, k, v);
     else hipLaunchKernelGGL(k_pf_attn<0>, g, dim3(NT), 0, s, *a, q, k, v);
@@ -2185,8 +2202,9 @@ extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k
     return gm_cast_bf16(a->out, out16, (long)n * a->NH * a->HD, s);
 }
 
-extern "C" int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_swiglu_bf16, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, g, u, out, n);
+extern "C" int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, int ks, long stride,
+                                  hipStream_t s) {
+    hipLaunchKernelGGL(k_pf_swiglu_bf16, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, g, u, out, n, ks, stride);
     BMK_LAUNCH_CHECK();
     return 0;
 }

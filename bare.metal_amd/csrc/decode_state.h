@@ -81,6 +81,10 @@ typedef struct {
     float inv_freq[DEC_MAX_HD / 2]; /* RoPE inverse frequency per rotary pair (host table) */
     float scale;
     int NH, NKV, HD, KV, MS, L, layer;
+    /* prefill: the q/k/v rows are the sum of pf_ks copies, pf_stride floats
+     * apart (split-K slices of the projection; 1 copy otherwise) */
+    int pf_ks;
+    long pf_stride;
 } DecAttn;
 
 /* Final RMSNorm + LM head + argmax.  Rows: Q8 when wq != NULL, else bf16

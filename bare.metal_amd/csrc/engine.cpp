@@ -45,10 +45,11 @@ int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
 int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
 int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
-                     hipStream_t s);
+                     int ks, long stride, hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
                      hipStream_t s);
-int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, hipStream_t s);
+int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, int ks, long stride,
+                       hipStream_t s);
 int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
 int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
@@ -773,9 +774,10 @@ static int prefill_buffers(bm_session_t* S, int n) {
     const size_t N = (size_t)n;
     const size_t widest = (size_t)std::max(std::max(m->D, m->H), m->QD);
     if (hipMalloc(&S->pf_x, N * m->D * 4) != hipSuccess ||
-        hipMalloc(&S->pf_qkv, N * (m->QD + 2 * (size_t)m->KV) * 4) != hipSuccess ||
-        hipMalloc(&S->pf_att, N * m->QD * 4) != hipSuccess || hipMalloc(&S->pf_o, N * m->D * 4) != hipSuccess ||
-        hipMalloc(&S->pf_gu, N * 2 * (size_t)m->H * 4) != hipSuccess ||
+        hipMalloc(&S->pf_qkv, GM_KSPLIT_MAX * N * (m->QD + 2 * (size_t)m->KV) * 4) != hipSuccess ||
+        hipMalloc(&S->pf_att, N * m->QD * 4) != hipSuccess ||
+        hipMalloc(&S->pf_o, GM_KSPLIT_MAX * N * m->D * 4) != hipSuccess ||
+        hipMalloc(&S->pf_gu, GM_KSPLIT_MAX * N * 2 * (size_t)m->H * 4) != hipSuccess ||
         hipMalloc(&S->pf_a16, N * widest * 2) != hipSuccess || hipMalloc(&S->pf_tok, N * 4) != hipSuccess) {
         (void)hipGetLastError();
         BMK_ERR("bm_forward: prefill buffers for %d tokens could not be allocated", n);
@@ -788,22 +790,37 @@ static int prefill_buffers(bm_session_t* S, int n) {
 /* One GEMM launch of the prefill: its plan's place in the plan buffer. */
 struct PfGemm {
     size_t off;
-    int nprob, n_tiles;
+    int nprob, n_tiles, ks; /* ks: K slices, each writing its own copy of C */
 };
 
-/* Appends the plan of one multi-GEMM launch to the staging buffer. */
+/* Prefill GEMM launches with fewer C tiles than this are split along K (at
+ * most GM_KSPLIT_MAX slices): a per-layer launch at prompt lengths of a few
+ * hundred tokens has tens of 128x128 tiles, and a tile's K loop takes about
+ * 0.7 us per 64-wide step on its own CU, whatever the cache state.  Each
+ * slice writes its own copy of C; the kernels that read the output add the
+ * copies in slice order, so no reduction launch is needed. */
+#define PF_SPLIT_TARGET 256
+
+/* Sizes (g == NULL) or appends the plan of one multi-GEMM launch to the
+ * staging buffer; kmax = 1 keeps the launch whole. */
 static int pf_plan(bm_session_t* S, size_t* used, PfGemm* g, int nprob, const uint64_t* a_off, const uint64_t* w_off,
-                   const uint64_t* c_off, const int* M, const int* N, const int* K, const int* lda, const int* ldc) {
-    int nt = 0;
-    const long need = bm_q8_gemm_plan(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, NULL, 0, &nt);
+                   const uint64_t* c_off, const int* M, const int* N, const int* K, const int* lda, const int* ldc,
+                   int kmax) {
+    int nt = 0, ks = 1;
+    const long need = gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, NULL, 0,
+                                    &nt, &ks);
     if (need < 0) return -1;
     const size_t at = (*used + 7) & ~(size_t)7;
-    if (at + (size_t)need > S->pf_plan_cap) return -1;
-    if (bm_q8_gemm_plan(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, S->h_plan + at, (size_t)need, &nt) != need)
-        return -1;
-    g->off = at;
-    g->nprob = nprob;
-    g->n_tiles = nt;
+    if (g) {
+        if (at + (size_t)need > S->pf_plan_cap) return -1;
+        if (gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, S->h_plan + at,
+                          (size_t)need, &nt, &ks) != need)
+            return -1;
+        g->off = at;
+        g->nprob = nprob;
+        g->n_tiles = nt;
+        g->ks = ks;
+    }
     *used = at + (size_t)need;
     return 0;
 }
@@ -819,11 +836,49 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
             return -1;
         }
     if (prefill_buffers(S, n)) return -1;
-    /* GEMM plans, per layer: q/k/v, o, gate/up, down (generous bound on the size) */
-    const size_t per_layer = 4 * (7 * sizeof(GmDesc) + 8) +
-                             4 * sizeof(unsigned int) * 8 * ((size_t)(n + GM_BM - 1) / GM_BM) *
-                                 (3 + (size_t)(QD + 2 * KV + 2 * D + 2 * H) / GM_BN + 4);
-    const size_t plan_bytes = per_layer * L + 64;
+    /* GEMM plans, per layer: q/k/v, o, gate/up, down; a first pass sizes
+     * the plan buffer and the split-K workspace, the second fills them */
+    std::vector<PfGemm> g((size_t)4 * L);
+    const uint64_t nn = (uint64_t)n;
+    /* q/k/v stay whole when the attention cannot read split copies (head size other than 64) */
+    const int kq = m->HD == 64 ? GM_KSPLIT_MAX : 1;
+    auto plans = [&](bool fill, size_t* used) -> int {
+        *used = 0;
+        for (int l = 0; l < L; l++) {
+            const uint64_t lw = (uint64_t)l * m->layer_bytes;
+            {
+                const uint64_t a[3] = {0, 0, 0}, w[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
+                const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
+                const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
+                if (pf_plan(S, used, fill ? &g[4 * l + 0] : NULL, 3, a, w, c, M, N, K, lda, N, kq)) return -1;
+            }
+            {
+                const uint64_t a = 0, w = lw + m->off[3], c = 0;
+                const int M = n, N = D, K = QD;
+                if (pf_plan(S, used, fill ? &g[4 * l + 1] : NULL, 1, &a, &w, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
+                    return -1;
+            }
+            {
+                const uint64_t a[2] = {0, 0}, w[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
+                const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
+                if (pf_plan(S, used, fill ? &g[4 * l + 2] : NULL, 2, a, w, c, M, N, K, K, N, GM_KSPLIT_MAX)) return -1;
+            }
+            {
+                const uint64_t a = 0, w = lw + m->off[6], c = 0;
+                const int M = n, N = D, K = H;
+                if (pf_plan(S, used, fill ? &g[4 * l + 3] : NULL, 1, &a, &w, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
+                    return -1;
+            }
+        }
+        return 0;
+    };
+    size_t used = 0;
+    if (plans(false, &used)) {
+        BMK_ERR("bm_forward: prefill GEMM plans rejected (%d tokens)", n);
+        return -1;
+    }
+    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
+    const size_t plan_bytes = used + 64;
     if (S->pf_plan_cap < plan_bytes) {
         hipFree(S->pf_plan);
         if (S->h_plan) hipHostFree(S->h_plan);
@@ -838,34 +893,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
         }
         S->pf_plan_cap = plan_bytes;
     }
-    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
-    std::vector<PfGemm> g((size_t)4 * L);
-    size_t used = 0;
-    const uint64_t nn = (uint64_t)n;
-    for (int l = 0; l < L; l++) {
-        const uint64_t lw = (uint64_t)l * m->layer_bytes;
-        {
-            const uint64_t a[3] = {0, 0, 0}, w[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
-            const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
-            const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
-            if (pf_plan(S, &used, &g[4 * l + 0], 3, a, w, c, M, N, K, lda, N)) return -1;
-        }
-        {
-            const uint64_t a = 0, w = lw + m->off[3], c = 0;
-            const int M = n, N = D, K = QD;
-            if (pf_plan(S, &used, &g[4 * l + 1], 1, &a, &w, &c, &M, &N, &K, &K, &N)) return -1;
-        }
-        {
-            const uint64_t a[2] = {0, 0}, w[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
-            const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
-            if (pf_plan(S, &used, &g[4 * l + 2], 2, a, w, c, M, N, K, K, N)) return -1;
-        }
-        {
-            const uint64_t a = 0, w = lw + m->off[6], c = 0;
-            const int M = n, N = D, K = H;
-            if (pf_plan(S, &used, &g[4 * l + 3], 1, &a, &w, &c, &M, &N, &K, &K, &N)) return -1;
-        }
-    }
+    if (plans(true, &used)) return -1;
     memcpy(S->h_io, tokens, (size_t)n * 4);
     HIP_TRY(hipMemcpyAsync(S->pf_tok, S->h_io, (size_t)n * 4, hipMemcpyHostToDevice, s), "token write", return -1);
     HIP_TRY(hipMemcpyAsync(S->pf_plan, S->h_plan, used, hipMemcpyHostToDevice, s), "plan write", return -1);
@@ -886,27 +914,35 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     float* v = k + (size_t)n * KV;
     float* gt = S->pf_gu;
     float* up = gt + (size_t)n * H;
-    auto gemm = [&](const PfGemm& p, float* C) {
-        return gm_launch_multi_qf(S->pf_a16, 1, m->quant_bits == 4, m->d_q8, C, S->pf_plan + p.off, p.nprob,
-                                  p.n_tiles, s);
+    /* floats between the split-K copies of each GEMM output */
+    const long st_qkv = (long)n * (QD + 2 * KV), st_o = (long)n * D, st_gu = (long)n * 2 * H;
+    auto gemm = [&](const PfGemm& p, float* C, long stride) {
+        return gm_launch_split_qf(S->pf_a16, 1, m->quant_bits == 4, m->d_q8, C, S->pf_plan + p.off, p.nprob,
+                                  p.n_tiles, (size_t)stride, s);
     };
     if (dec_pf_embed(S->pf_tok, m->d_emb, S->pf_x, n, D, s)) return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
+        at.pf_ks = g[4 * l + 0].ks;
+        at.pf_stride = st_qkv;
+        const int ks_down = l ? g[4 * l - 1].ks : 1;
         /* residual of the previous layer's down projection, RMSNorm, q/k/v */
-        if (dec_pf_norm_bf16(S->pf_x, l ? S->pf_o : NULL, m->d_ln1 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||
-            gemm(g[4 * l + 0], S->pf_qkv) ||
+        if (dec_pf_norm_bf16(S->pf_x, l ? S->pf_o : NULL, m->d_ln1 + (size_t)l * D, S->pf_a16, n, D, eps, ks_down,
+                             st_o, s) ||
+            gemm(g[4 * l + 0], S->pf_qkv, st_qkv) ||
             /* RoPE, cache append, causal attention */
             dec_pf_attention(&at, q, k, v, n, S->pf_a16, s) ||
             /* o, residual, RMSNorm, gate/up, SwiGLU, down */
-            gemm(g[4 * l + 1], S->pf_o) ||
-            dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_ln2 + (size_t)l * D, S->pf_a16, n, D, eps, s) ||
-            gemm(g[4 * l + 2], S->pf_gu) || dec_pf_swiglu_bf16(gt, up, S->pf_a16, (long)n * H, s) ||
-            gemm(g[4 * l + 3], S->pf_o))
+            gemm(g[4 * l + 1], S->pf_o, st_o) ||
+            dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_ln2 + (size_t)l * D, S->pf_a16, n, D, eps, g[4 * l + 1].ks, st_o,
+                             s) ||
+            gemm(g[4 * l + 2], S->pf_gu, st_gu) ||
+            dec_pf_swiglu_bf16(gt, up, S->pf_a16, (long)n * H, g[4 * l + 2].ks, st_gu, s) ||
+            gemm(g[4 * l + 3], S->pf_o, st_o))
             return -1;
     }
     /* last residual (the bf16 output is not used), then the head on the last position */
-    if (dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_lnf, S->pf_a16, n, D, eps, s)) return -1;
+    if (dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_lnf, S->pf_a16, n, D, eps, g[4 * L - 1].ks, st_o, s)) return -1;
     DecHead hd;
     memset(&hd, 0, sizeof hd);
     hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;

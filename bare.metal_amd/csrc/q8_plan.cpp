@@ -8,6 +8,8 @@
 #include "bmk.h"
 #include "q8_matvec.h"
 #include "q8_gemm.h"
+
+#include <vector>
 #include "../../include/bm_q8.h"
 
 #include <string.h>
@@ -79,32 +81,57 @@ extern "C" int bm_q8_gemm_tiles(int M, int N, int K) {
  * the launch has 8 x (longest queue) workgroups. */
 #define GM_XCDS 8
 
-static long gemm_queue_len(int nprob, const int* M, const int* N, long* per_xcd) {
+/* Split-K factor of a launch, the same for all its problems: 1, unless
+ * the launch has fewer than `target` C tiles; then enough K slices to reach
+ * it, at most kmax and at most one slice per two K blocks of any problem. */
+static int gemm_split(int nprob, const int* M, const int* N, const int* K, int target, int kmax) {
+    long total = 0;
+    for (int i = 0; i < nprob; i++) total += gm_tiles_for(M[i], N[i]);
+    int want = 1;
+    if (total > 0 && total < target) want = (int)((target + total - 1) / total);
+    if (want > kmax) want = kmax;
+    for (int i = 0; i < nprob; i++)
+        if (want > K[i] / 64) want = K[i] / 64;
+    return want < 1 ? 1 : want;
+}
+
+/* Workgroups per XCD queue: every (problem, N tile, K slice) group goes to
+ * one XCD, round robin, with its M tiles consecutive. */
+static long gemm_queue_len(int nprob, const int* M, const int* N, const int* ks, long* per_xcd) {
     for (int x = 0; x < GM_XCDS; x++) per_xcd[x] = 0;
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
-        for (int n = 0; n < tn; n++, pair++) per_xcd[pair % GM_XCDS] += tm;
+        for (int n = 0; n < tn; n++)
+            for (int k = 0; k < ks[i]; k++, pair++) per_xcd[pair % GM_XCDS] += tm;
     }
     long longest = 0;
     for (int x = 0; x < GM_XCDS; x++) longest = per_xcd[x] > longest ? per_xcd[x] : longest;
     return longest;
 }
 
-extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
-                                const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
-                                size_t plan_bytes, int* n_tiles_out) {
+/* Plan of one multi-GEMM launch: GmDesc[nprob], then the tile map.  A
+ * problem with ksplit > 1 (GmDesc.pad_) has tiles = C tiles * ksplit, tile
+ * index = slice * C tiles + C tile. */
+static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                           const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
+                           int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
     if (nprob < 0 || nprob > 0xffff || (nprob > 0 && (!a_off || !w_off || !c_off || !M || !N || !K || !lda || !ldc)))
         return -1;
     for (int i = 0; i < nprob; i++) {
         const int t = bm_q8_gemm_tiles(M[i], N[i], K[i]);
         if (t < 0 || t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
     }
+    const int kss = target > 0 ? gemm_split(nprob, M, N, K, target, kmax) : 1;
+    std::vector<int> ks((size_t)(nprob > 0 ? nprob : 1), kss);
+    for (int i = 0; i < nprob; i++)
+        if ((long)gm_tiles_for(M[i], N[i]) * kss > 0xffff) return -1;
     long per_xcd[GM_XCDS];
-    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, per_xcd);
+    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, ks.data(), per_xcd);
     if (slots > 0x7fffffffL) return -1;
     const size_t need = (size_t)nprob * sizeof(GmDesc) + (size_t)slots * 4;
     if (n_tiles_out) *n_tiles_out = (int)slots;
+    if (ksplit_out) *ksplit_out = kss;
     if (!plan) return (long)need;
     if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
     GmDesc* d = (GmDesc*)plan;
@@ -120,8 +147,8 @@ extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t
         d[i].lda = lda[i];
         d[i].ldc = ldc[i];
         d[i].tile0 = t0;
-        d[i].tiles = gm_tiles_for(M[i], N[i]);
-        d[i].pad_ = 0;
+        d[i].tiles = gm_tiles_for(M[i], N[i]) * ks[i];
+        d[i].pad_ = ks[i] > 1 ? ks[i] : 0;
         t0 += d[i].tiles;
     }
     for (long b = 0; b < slots; b++) map[b] = GM_IDLE_TILE;
@@ -129,10 +156,29 @@ extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
-        for (int n = 0; n < tn; n++, pair++) {
-            const int x = (int)(pair % GM_XCDS);
-            for (int m = 0; m < tm; m++) map[(long)GM_XCDS * fill[x]++ + x] = ((unsigned int)i << 16) | (unsigned)(m * tn + n);
-        }
+        for (int n = 0; n < tn; n++)
+            for (int k = 0; k < ks[i]; k++, pair++) {
+                const int x = (int)(pair % GM_XCDS);
+                for (int m = 0; m < tm; m++)
+                    map[(long)GM_XCDS * fill[x]++ + x] =
+                        ((unsigned int)i << 16) | (unsigned)(k * tm * tn + m * tn + n);
+            }
     }
     return (long)need;
+}
+
+extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                                const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
+                                size_t plan_bytes, int* n_tiles_out) {
+    return gemm_plan_impl(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes, n_tiles_out,
+                          nullptr);
+}
+
+/* The engine's prefill plans: split-K when the launch has fewer than
+ * `target` C tiles (at most kmax slices, the same for every problem). */
+extern "C" long gm_plan_split(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                              const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
+                              int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
+    return gemm_plan_impl(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, target, kmax, plan, plan_bytes, n_tiles_out,
+                          ksplit_out);
 }
