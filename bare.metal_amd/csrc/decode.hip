@@ -233,6 +233,30 @@ __global__ __launch_bounds__(NT) void k_rope(float* q, float* k, int NH, int NKV
     }
 }
 
+/* every position of a prompt: one thread per (position s, head h, rotary
+ * pair i) of q ([S][NH][HD]) and, for h < NKV, of k ([S][NKV][HD]); the
+ * angle is (float)s * inv[i], as k_rope takes it at pos = s */
+__global__ __launch_bounds__(NT) void k_rope_seq(float* q, float* k, int S, int NH, int NKV, int HD, RopeTab rt) {
+    const int hd2 = HD / 2;
+    const long gid = (long)blockIdx.x * NT + threadIdx.x;
+    if (gid >= (long)S * NH * hd2) return;
+    const int i = (int)(gid % hd2);
+    const long sh = gid / hd2;
+    const int h = (int)(sh % NH), sp = (int)(sh / NH);
+    const float ang = (float)sp * rt.inv[i];
+    const float c = cosf(ang), sn = sinf(ang);
+    float* qh = q + ((size_t)sp * NH + h) * HD;
+    const float q0 = qh[i], q1 = qh[i + hd2];
+    qh[i] = q0 * c - q1 * sn;
+    qh[i + hd2] = q0 * sn + q1 * c;
+    if (h < NKV) {
+        float* kh = k + ((size_t)sp * NKV + h) * HD;
+        const float k0 = kh[i], k1 = kh[i + hd2];
+        kh[i] = k0 * c - k1 * sn;
+        kh[i + hd2] = k0 * sn + k1 * c;
+    }
+}
+
 __global__ __launch_bounds__(NT) void k_kv_store(float* kvc, const float* k, const float* v, int layer, int pos,
                                                  int MS, int KV) {
     const int i = blockIdx.x * NT + threadIdx.x;
@@ -1857,6 +1881,31 @@ extern "C" int bmk_launch_rope(const bmk_launch_t* a) {
     const int n = NH * (HD / 2);
     hipLaunchKernelGGL(k_rope, dim3((n + NT - 1) / NT), dim3(NT), 0, a->stream, (float*)a->dev[0], (float*)a->dev[1],
                        NH, NKV, HD, pos, rt);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* rope_forward_seq {q [S][NH][HD], k [S][NKV][HD], params int{head_size,
+ * n_kv_heads, S, NH}, rope[6]} (reference forward.metal:2218-2257, the
+ * prefill graph's RoPE, scheduler.c:1097-1098): q and k of every position s
+ * rotated in place by angle s * inv_freq, inv_freq as rope_forward's. */
+extern "C" int bmk_launch_rope_seq(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 16, "params");
+    BMK_NEED_BYTES(a, 3, 24, "rope");
+    const int HD = bmk_pi(a, 2, 0), NKV = bmk_pi(a, 2, 1), S = bmk_pi(a, 2, 2), NH = bmk_pi(a, 2, 3);
+    BMK_REQUIRE(HD > 0 && HD % 2 == 0 && HD <= DEC_MAX_HD && NH >= 0 && NKV >= 0 && NKV <= NH && S >= 0,
+                "rope_forward_seq: bad shape HD=%d NH=%d NKV=%d S=%d", HD, NH, NKV, S);
+    if (NH == 0 || S == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)S * NH * HD * 4, "q");
+    BMK_NEED_BYTES(a, 1, (size_t)S * NKV * HD * 4, "k");
+    float r[6];
+    for (int i = 0; i < 6; i++) r[i] = bmk_pf(a, 3, i);
+    RopeTab rt;
+    bmk_rope_table(r, HD, rt.inv);
+    const long n = (long)S * NH * (HD / 2);
+    BMK_REQUIRE(n / NT < 0x7fffffffL, "rope_forward_seq: %ld rotations", n);
+    hipLaunchKernelGGL(k_rope_seq, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, a->stream, (float*)a->dev[0],
+                       (float*)a->dev[1], S, NH, NKV, HD, rt);
     BMK_LAUNCH_CHECK();
     return 0;
 }

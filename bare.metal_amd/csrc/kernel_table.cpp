@@ -28,6 +28,7 @@ int bmk_launch_rope(const bmk_launch_t* a);
 int bmk_launch_kv_store(const bmk_launch_t* a);
 int bmk_launch_attention(const bmk_launch_t* a);
 int bmk_launch_attention_prefill(const bmk_launch_t* a);
+int bmk_launch_rope_seq(const bmk_launch_t* a);
 int bmk_launch_add(const bmk_launch_t* a);
 int bmk_launch_swiglu(const bmk_launch_t* a);
 int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a);
@@ -78,6 +79,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"kv_store", 4, B(3), B(0), bmk_launch_kv_store, 0},
     /* reference forward.metal:1362-1465; {q, kv cache, out, params{NH,HD,NKV,KV,S,kv_mul,layer,MS}, scale} */
     {"attention_forward", 5, B(3) | B(4), B(2), bmk_launch_attention, 0},
+    /* reference forward.metal:2218-2257, prefill RoPE (scheduler.c:1097-1098);
+     * {q [S][NH][HD], k [S][NKV][HD], params{head_size,n_kv_heads,S,NH}, rope[6]} */
+    {"rope_forward_seq", 4, B(2) | B(3), B(0) | B(1), bmk_launch_rope_seq, 0},
     /* reference forward.metal:1904-2114, prefill attention (scheduler.c:1081-1089);
      * {Q [S][NH][HD] roped, K [S][NKV][HD], V, out [S][NH][HD], params{NH,S,HD,NKV,kv_mul}, scale} */
     {"attention_forward_prefill", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},

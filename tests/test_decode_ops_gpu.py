@@ -74,6 +74,41 @@ def test_rope_forward(be, NH, NKV, HD, pos):
         assert np.array_equal(bq.read(np.float32), q)
 
 
+@pytest.mark.parametrize("NH,NKV,HD,S", [(9, 3, 64, 1), (9, 3, 64, 130), (15, 5, 64, 37), (4, 4, 128, 9)])
+def test_rope_forward_seq(be, NH, NKV, HD, S):
+    """The reference's prefill RoPE (forward.metal:2218-2257): row s of q
+    [S][NH][HD] and of k [S][NKV][HD] rotated by position s.  Against the
+    fp64 rotation per position, and bit for bit against rope_forward applied
+    to the same rows one position at a time (same frequency table, same fp32
+    angle); position 0 is the identity."""
+    rng = np.random.default_rng(S * HD)
+    q = rng.standard_normal(S * NH * HD).astype(np.float32)
+    k = rng.standard_normal(S * NKV * HD).astype(np.float32)
+    rope = f32(10000.0, 0, 0, 0, 0, 0)
+    bq, bk = be.upload(q), be.upload(k)
+    assert be.dispatch("rope_forward_seq", [bq, bk, be.params(HD, NKV, S, NH), be.upload(rope)],
+                       (S * NH,), (min(S * NH, 256),)) == 0
+    gq, gk = bq.read(np.float32).reshape(S, -1), bk.read(np.float32).reshape(S, -1)
+    for s in range(S):
+        assert nw(gq[s], rope_ref(q.reshape(S, -1)[s], NH, HD, s, 10000.0)) <= TOL
+        assert nw(gk[s], rope_ref(k.reshape(S, -1)[s], NKV, HD, s, 10000.0)) <= TOL
+    assert np.array_equal(gq[0], q.reshape(S, -1)[0]) and np.array_equal(gk[0], k.reshape(S, -1)[0])
+    for s in (0, S // 2, S - 1):
+        bq1, bk1 = be.upload(q.reshape(S, -1)[s].copy()), be.upload(k.reshape(S, -1)[s].copy())
+        assert be.dispatch("rope_forward", [bq1, bk1, be.params(HD), be.params(s), be.upload(rope), be.params(NKV)],
+                           (NH,), (min(NH, 256),)) == 0
+        assert np.array_equal(bq1.read(np.float32), gq[s]) and np.array_equal(bk1.read(np.float32), gk[s])
+
+
+def test_rope_forward_seq_rejects(be):
+    q = be.alloc(4 * 64 * 4 * 4)
+    k = be.alloc(4 * 64 * 2 * 4)
+    rope = be.upload(f32(10000.0, 0, 0, 0, 0, 0))
+    assert be.dispatch("rope_forward_seq", [q, k, be.params(64, 5, 4, 4), rope], (16,), (16,)) != 0  # NKV > NH
+    assert be.dispatch("rope_forward_seq", [q, k, be.params(63, 2, 4, 4), rope], (16,), (16,)) != 0  # odd head size
+    assert be.dispatch("rope_forward_seq", [q, k, be.params(64, 2, 5, 4), rope], (20,), (20,)) != 0  # q too short
+
+
 def test_kv_store_places_rows(be):
     L, MS, KV = 3, 16, 192
     cache = be.alloc(L * 2 * MS * KV * 4)
