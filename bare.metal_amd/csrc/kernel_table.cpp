@@ -87,6 +87,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"attention_forward_prefill", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
     {"attention_forward_prefill_warp", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
     {"attention_forward_prefill_tiled", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
+    /* reference forward.metal:1802-1848, the same causal attention over [S][NH][HD]
+     * (the prefill fallback, scheduler.c:1089-1090); the reference caps S at 256 */
+    {"attention_forward_seq", 6, B(4) | B(5), B(3), bmk_launch_attention_prefill, 0},
     /* reference forward.metal:1332-1340; {a, b, out, n} */
     {"add_forward", 4, B(3), B(2), bmk_launch_add, 0},
     /* reference forward.metal:1179-1190; {gate, up, out, N} */
@@ -96,6 +99,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     /* reference forward.metal:1532-1581 (the LM head at default bf16 precision,
      * scheduler.c:776-778); {x, norm weight, wcls bf16, logits, params{C,V}, eps} */
     {"rmsnorm_matmul_forward_bf16_vec", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_bf16, 0},
+    /* reference forward.metal:1691-1735, the same head with one thread per row
+     * (scheduler.c:782-783 takes it at bf16 precision); same buffers and launch */
+    {"rmsnorm_matmul_forward_bf16", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_bf16, 0},
     /* new: greedy pick on the device (reference tools/run.c:56-60); {values, out int, params{n}} */
     {"argmax_f32", 3, B(2), B(1), bmk_launch_argmax, 0},
     {nullptr, 0, 0, 0, nullptr, 0},

@@ -186,7 +186,8 @@ def prefill_attn_ref(Q, K, V, NH, NKV, HD, S, kv_mul, scale):
     return out.reshape(-1)
 
 
-PREFILL_ATTN = ["attention_forward_prefill", "attention_forward_prefill_warp", "attention_forward_prefill_tiled"]
+PREFILL_ATTN = ["attention_forward_prefill", "attention_forward_prefill_warp", "attention_forward_prefill_tiled",
+                "attention_forward_seq"]
 
 
 def run_prefill_attn(be, name, Q, K, V, NH, NKV, HD, S, kv_mul, scale):
@@ -280,17 +281,20 @@ def test_rmsnorm_matmul_forward(be, C, V):
 
 
 @pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300), (32, 17)])
-def test_rmsnorm_matmul_forward_bf16_vec(be, C, V):
-    """bf16 head rows (reference forward.metal:1532-1581): each weight widened
-    exactly, fp32 products and sums; vs fp64 over the same bf16 values."""
+@pytest.mark.parametrize("name", ["rmsnorm_matmul_forward_bf16_vec", "rmsnorm_matmul_forward_bf16"])
+def test_rmsnorm_matmul_forward_bf16_vec(be, C, V, name):
+    """bf16 head rows (reference forward.metal:1532-1581, and the one-thread-
+    per-row rmsnorm_matmul_forward_bf16 of :1691-1735 with the same buffers):
+    each weight widened exactly, fp32 products and sums; vs fp64 over the same
+    bf16 values."""
     rng = np.random.default_rng(C + 1)
     x = rng.standard_normal(C).astype(np.float32)
     g = rng.uniform(0.5, 1.5, C).astype(np.float32)
     Wr = po.bf16_rne((rng.standard_normal(V * C) * 0.02).astype(np.float32))  # bf16 values as fp32
     bits = (Wr.view(np.uint32) >> 16).astype(np.uint16)
     out = be.alloc(V * 4)
-    rc = be.dispatch("rmsnorm_matmul_forward_bf16_vec", [be.upload(x), be.upload(g), be.upload(bits), out,
-                                                         be.params(C, V), be.upload(f32(1e-5))],
+    rc = be.dispatch(name, [be.upload(x), be.upload(g), be.upload(bits), out,
+                            be.params(C, V), be.upload(f32(1e-5))],
                      ((V + 15) // 16 * 512,), (512,))
     assert rc == 0
     xd = x.astype(np.float64)
