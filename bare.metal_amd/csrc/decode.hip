@@ -1586,7 +1586,9 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
     const int NH = MODE == PF_FLAT ? f.NH : a.NH;
     const int kv_mul = MODE == PF_FLAT ? f.kv_mul : a.NH / a.NKV;
     const float scale = MODE == PF_FLAT ? f.scale : a.scale;
-    const int h = blockIdx.x, p0 = blockIdx.y * PQB;
+    /* the last blocks of the prompt have the most keys: they take the first
+     * workgroup slots, and the short ones fill in behind them */
+    const int h = blockIdx.x, p0 = (int)(gridDim.y - 1 - blockIdx.y) * PQB;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int col = lane & 15, grp = lane >> 4; /* MFMA column (query / key row) and lane group */
     const int kh = h / kv_mul;
