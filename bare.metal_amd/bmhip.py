@@ -62,6 +62,8 @@ def lib() -> C.CDLL:
         "bm_synth_uniform_int": (None, [u64, i, i, vp, sz]),
         "bm_q8_mv_tiles": (i, [i, i]),
         "bm_q8_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
+        "bm_q8_bmv_tiles": (i, [i, i]),
+        "bm_q8_bmv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_q4_mv_tiles": (i, [i, i]),
         "bm_q4_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_q8_gemm_tiles": (i, [i, i, i]),
@@ -144,11 +146,15 @@ def synth_uniform_int(seed: int, lo: int, hi: int, n: int) -> np.ndarray:
 
 # ---------------------------------------------------------------- Q8 multi-matvec plan
 
-def mv_plan(w_off, x_off, y_off, OC, C_, fmt: str = "q8"):
+def mv_plan(w_off, x_off, y_off, OC, C_, fmt: str = "q8", bt: int = 1):
     """Plan table (bytes) and workgroup count of a matmul_forward_q8_vec_multi
     (fmt "q4": matmul_forward_q4_vec_multi) launch over the problems given by
-    the five equal-length sequences."""
-    planner = lib().bm_q4_mv_plan if fmt == "q4" else lib().bm_q8_mv_plan
+    the five equal-length sequences; bt >= 2: the batched launch's plan (the
+    same for both formats)."""
+    if bt > 1:
+        planner = lib().bm_q8_bmv_plan
+    else:
+        planner = lib().bm_q4_mv_plan if fmt == "q4" else lib().bm_q8_mv_plan
     n = len(OC)
     w = np.ascontiguousarray(w_off, dtype=np.uint64)
     x = np.ascontiguousarray(x_off, dtype=np.uint64)

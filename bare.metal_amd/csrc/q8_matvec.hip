@@ -202,7 +202,151 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
     mv_multi_body<U, QF_Q4>(W, X, Y, desc, tile_map, red);
 }
 
+/* matmul_forward_q8_vec_multi / _q4_vec_multi with BT >= 2 rows per problem
+ * (several decode sequences' projections in one launch), on fp32 MFMA
+ * (v_mfma_f32_16x16x4_f32, D[16][16] += A[16][4] x B[4][16]).
+ *
+ * A workgroup is one wave; it runs the 64-row tile blockIdx.x - tile0 of
+ * problem tile_map[blockIdx.x] (4 groups of 16 output rows) for batch rows
+ * 16*blockIdx.y .. +15 over the whole K range.  Per step of BMV_U K blocks
+ * the wave copies the 64 rows' spans of BMV_U blocks (contiguous in each
+ * row) into LDS with 16-byte loads, so every weight byte is fetched once;
+ * the MFMA operands are then read from LDS.  Per K block, lane l
+ * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once and feeds it,
+ * as the A operand, to 8 MFMAs for each row group, whose B operand is
+ * q[r0 + c][32kb + 8g + i] (i = 0..7, the int8 or 4-bit codes converted
+ * exactly to fp32); each group's block product is scaled by its row's block
+ * scale and added in block order, as the reference scales each block's dot
+ * product (forward.metal:575-623).  D layout: lane l holds batch rows
+ * 4*(l/16)+v of output row l%16.  Problem p reads BT rows of C floats at
+ * X + x_off (row stride C) and writes BT rows of OC floats at Y + y_off
+ * (row stride OC). */
+typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int BMV_GROUPS = 4;             /* 16-row groups per wave */
+constexpr int BMV_ROWS = 16 * BMV_GROUPS; /* output rows per workgroup */
+constexpr int BMV_U = 4;                  /* K blocks per step */
+
+template <int QF>
+__global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restrict__ W, const float* __restrict__ X,
+                                                  float* __restrict__ Y, const MvDesc* __restrict__ desc,
+                                                  const unsigned int* __restrict__ tile_map, int BT) {
+    constexpr int BYTES = QFmt<QF>::BYTES;
+    constexpr int SPAN = BMV_U * BYTES;   /* bytes of one row per step: 144 (Q8_0), 80 (Q4_0) */
+    constexpr int CPR = SPAN / 16;        /* 16-byte chunks per row span */
+    constexpr int LDR = SPAN + 16;        /* LDS row pitch */
+    constexpr int LANE_OFF = QF == QF_Q4 ? 4 : 8; /* code bytes per lane and block */
+    static_assert(SPAN % 16 == 0, "row span must be whole 16-byte chunks");
+    __shared__ __attribute__((aligned(16))) unsigned char tile[BMV_ROWS * LDR];
+    const int lane = threadIdx.x;
+    const int c = lane & 15, g = lane >> 4;
+    const MvDesc d = desc[tile_map[blockIdx.x]];
+    const int row0 = ((int)blockIdx.x - d.tile0) * BMV_ROWS;
+    const int b0 = 16 * (int)blockIdx.y;
+    const int nb = d.C / 32;
+    const size_t row_bytes = (size_t)nb * BYTES;
+    /* this lane's chunks: chunk q = lane + 64 t of the 64 x CPR chunk grid;
+     * rows past OC (and batch rows past BT) are clamped: they feed outputs
+     * that are never stored */
+    const unsigned char* src[CPR];
+    int lofs[CPR], cofs[CPR];
+#pragma unroll
+    for (int t = 0; t < CPR; t++) {
+        const int q = lane + 64 * t, r = q / CPR;
+        cofs[t] = 16 * (q - r * CPR);
+        lofs[t] = r * LDR;
+        src[t] = W + d.w_off + (size_t)min(row0 + r, d.OC - 1) * row_bytes;
+    }
+    const float* xr = X + d.x_off + (size_t)min(b0 + c, BT - 1) * (size_t)d.C + 8 * g;
+
+    bmm_f32x4 acc[BMV_GROUPS];
+#pragma unroll
+    for (int j = 0; j < BMV_GROUPS; j++) acc[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb0 = 0; kb0 < nb; kb0 += BMV_U) {
+        /* bytes of this step inside the row; a chunk reaching past them is
+         * moved back to end there (and stored at the same place, so the
+         * overlap is written twice with equal bytes): no load leaves the row */
+        const int valid = min(BMV_U, nb - kb0) * BYTES;
+        uint4 ch[CPR];
+        int at[CPR];
+#pragma unroll
+        for (int t = 0; t < CPR; t++) {
+            at[t] = min(cofs[t], valid - 16);
+            __builtin_memcpy(&ch[t], __builtin_assume_aligned(src[t] + (size_t)kb0 * BYTES + at[t], 4), 16);
+        }
+        float4 xa[BMV_U], xb[BMV_U];
+#pragma unroll
+        for (int u = 0; u < BMV_U; u++) {
+            const int kb = min(kb0 + u, nb - 1);
+            __builtin_memcpy(&xa[u], __builtin_assume_aligned(xr + 32 * kb, 16), 16);
+            __builtin_memcpy(&xb[u], __builtin_assume_aligned(xr + 32 * kb + 4, 16), 16);
+        }
+        __syncthreads(); /* the previous step's LDS reads are done */
+#pragma unroll
+        for (int t = 0; t < CPR; t++) {
+            unsigned int w4[4] = {ch[t].x, ch[t].y, ch[t].z, ch[t].w};
+            /* 4-byte stores: a moved-back chunk is 4-byte but not 16-byte aligned */
+#pragma unroll
+            for (int e = 0; e < 4; e++) *(unsigned int*)&tile[lofs[t] + at[t] + 4 * e] = w4[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < BMV_U; u++) {
+            const float xv[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+            const bool live = kb0 + u < nb;
+#pragma unroll
+            for (int j = 0; j < BMV_GROUPS; j++) {
+                const unsigned char* blk = &tile[(16 * j + c) * LDR + u * BYTES];
+                const float sc = live ? *(const float*)blk : 0.0f;
+                const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
+                const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
+                float wv[8];
+                if (QF == QF_Q4) {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) wv[i] = q4_code(q0, i);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        wv[i] = q8_byte(q0, i);
+                        wv[4 + i] = q8_byte(q1, i);
+                    }
+                }
+                bmm_f32x4 dd = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 8; i++) dd = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], dd, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sc, dd[v], acc[j][v]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < BMV_GROUPS; j++) {
+        const int row = row0 + 16 * j + c;
+        if (row < d.OC) {
+            float* y = Y + d.y_off + row;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int b = b0 + 4 * g + v;
+                if (b < BT) y[(size_t)b * d.OC] = acc[j][v];
+            }
+        }
+    }
+}
+
 } // namespace
+
+/* The batched multi-matrix launch; the caller has checked the plan against
+ * the arenas. */
+static int launch_bmv_multi(int qf, const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
+                            const unsigned int* d_tile_map, int n_tiles, int BT, hipStream_t s) {
+    if (n_tiles <= 0 || BT < 2 || BT > DEC_MAX_B) return -1;
+    const dim3 grid((unsigned)n_tiles, (unsigned)((BT + 15) / 16));
+    if (qf == QF_Q4)
+        hipLaunchKernelGGL(k_bmv_multi<QF_Q4>, grid, dim3(64), 0, s, W, X, Y, d_desc, d_tile_map, BT);
+    else
+        hipLaunchKernelGGL(k_bmv_multi<QF_Q8>, grid, dim3(64), 0, s, W, X, Y, d_desc, d_tile_map, BT);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
 
 /* ------------------------------------------------------------------ */
 
@@ -279,13 +423,18 @@ extern "C" int mv_launch_multi(const unsigned char* W, const float* X, float* Y,
  *          2 weight arena (Q8 blocks), 3 activation arena f32, 4 output arena f32}.
  * Every descriptor and tile-map entry is checked against the arena sizes
  * before anything is launched. */
+extern "C" int bm_q8_bmv_tiles(int OC, int C);
+
 template <int QF>
 static int launch_matvec_multi(const bmk_launch_t* a) {
     const int BYTES = QFmt<QF>::BYTES;
     const int U = QF == QF_Q4 ? MV_U_Q4 : MV_U_WIDE;
     BMK_NEED_BYTES(a, 0, 8, "params");
     const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
+    /* optional third parameter: rows per problem (BT >= 2: the batched kernel, plan from bm_q8_bmv_plan) */
+    const int BT = a->bytes[0] >= 12 ? bmk_pi(a, 0, 2) : 1;
     BMK_REQUIRE(nprob >= 0 && n_tiles >= 0, "q8 matvec multi: bad counts nprob=%d n_tiles=%d", nprob, n_tiles);
+    BMK_REQUIRE(BT >= 1 && BT <= DEC_MAX_B, "q8 matvec multi: BT=%d outside [1, %d]", BT, DEC_MAX_B);
     if (nprob == 0 || n_tiles == 0) return 0;
     const size_t desc_bytes = (size_t)nprob * sizeof(MvDesc);
     BMK_NEED_BYTES(a, 1, desc_bytes + (size_t)n_tiles * 4, "plan");
@@ -298,13 +447,15 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
     for (int i = 0; i < nprob; i++) {
         const MvDesc& d = desc[i];
         BMK_REQUIRE(d.OC > 0 && d.C > 0 && d.C % 32 == 0, "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, d.OC, d.C);
-        BMK_REQUIRE(d.tiles == mv_tiles_for(d.OC, d.C, U) && d.tile0 == next_tile,
-                    "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
-                    mv_tiles_for(d.OC, d.C, U), next_tile);
+        const int want = BT > 1 ? bm_q8_bmv_tiles(d.OC, d.C) : mv_tiles_for(d.OC, d.C, U);
+        BMK_REQUIRE(d.tiles == want && d.tile0 == next_tile, "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld",
+                    i, d.tiles, d.tile0, want, next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 matvec multi: problem %d weight offset not 4-byte aligned", i);
+        /* the batched kernel loads activations 16 bytes at a time */
+        BMK_REQUIRE(BT == 1 || (d.x_off & 3) == 0, "q8 matvec multi: problem %d activation offset not 16-byte aligned", i);
         BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * BYTES <= a->bytes[2] &&
-                    d.x_off + (unsigned long long)d.C <= a->bytes[3] / 4 &&
-                    d.y_off + (unsigned long long)d.OC <= a->bytes[4] / 4,
+                    d.x_off + (unsigned long long)BT * d.C <= a->bytes[3] / 4 &&
+                    d.y_off + (unsigned long long)BT * d.OC <= a->bytes[4] / 4,
                     "q8 matvec multi: problem %d lies outside its arenas", i);
         next_tile += d.tiles;
     }
@@ -312,6 +463,14 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
     for (int i = 0; i < nprob; i++)
         for (int t = desc[i].tile0; t < desc[i].tile0 + desc[i].tiles; t++)
             BMK_REQUIRE(tmap[t] == (unsigned)i, "q8 matvec multi: tile_map[%d]=%u, expected %d", t, tmap[t], i);
+    if (BT > 1) {
+        BMK_REQUIRE(((uintptr_t)a->dev[3] & 15) == 0, "q8 matvec multi: activation arena not 16-byte aligned");
+        BMK_REQUIRE(launch_bmv_multi(QF, (const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
+                                     (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
+                                     n_tiles, BT, a->stream) == 0,
+                    "q8 matvec multi: batched launch failed (BT=%d)", BT);
+        return 0;
+    }
     return launch_multi<QF>((const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
                             (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
                             n_tiles, a->stream);

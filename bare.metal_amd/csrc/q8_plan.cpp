@@ -22,13 +22,23 @@ static int mv_tiles_u(int OC, int C, int U) {
 extern "C" int bm_q8_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_WIDE); }
 extern "C" int bm_q4_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_Q4); }
 
-/* U: rows in flight per lane of the kernel the plan is for */
+/* Batched (BT >= 2) multi-matrix launch: 64 output rows per workgroup. */
+#define MV_U_BATCHED (-1)
+extern "C" int bm_q8_bmv_tiles(int OC, int C) {
+    if (OC <= 0 || C <= 0 || C % 32) return -1;
+    return (OC + 63) / 64;
+}
+
+static int plan_tiles(int OC, int C, int U) { return U == MV_U_BATCHED ? bm_q8_bmv_tiles(OC, C) : mv_tiles_u(OC, C, U); }
+
+/* U: rows in flight per lane of the kernel the plan is for (MV_U_BATCHED:
+ * the batched kernel) */
 static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                       const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
     if (nprob < 0 || (nprob > 0 && (!w_off || !x_off || !y_off || !OC || !C))) return -1;
     long tiles = 0;
     for (int i = 0; i < nprob; i++) {
-        int t = mv_tiles_u(OC[i], C[i], U);
+        int t = plan_tiles(OC[i], C[i], U);
         if (t < 0) return -1;
         tiles += t;
     }
@@ -47,7 +57,7 @@ static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x
         d[i].OC = OC[i];
         d[i].C = C[i];
         d[i].tile0 = t0;
-        d[i].tiles = mv_tiles_for(OC[i], C[i], U);
+        d[i].tiles = plan_tiles(OC[i], C[i], U);
         for (int k = 0; k < d[i].tiles; k++) map[t0 + k] = (unsigned int)i;
         t0 += d[i].tiles;
     }
@@ -57,6 +67,11 @@ static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x
 extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                               const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
     return mv_plan_u(MV_U_WIDE, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
+}
+
+extern "C" long bm_q8_bmv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
+                               const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
+    return mv_plan_u(MV_U_BATCHED, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
 }
 
 extern "C" long bm_q4_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,

@@ -186,6 +186,59 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+def batched_leg(be, wl: Workload, BT: int, steps: int, warmup: int):
+    """Config 3 at batch BT: the same weights (already packed in HBM), BT
+    activation rows per matrix, one matmul_forward_q8_vec_multi launch with
+    params {nprob, n_tiles, BT} per step (each weight read once for all BT
+    rows, fp32 MFMA)."""
+    Csum, OCsum = int(wl.C.astype(np.int64).sum()), int(wl.OC.astype(np.int64).sum())
+    x_off, y_off = (BT * wl.x_off).astype(np.uint64), (BT * wl.y_off).astype(np.uint64)
+    X = be.upload(bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, 7, BT, 0), 1.0, BT * Csum))
+    Y = be.alloc(4 * BT * OCsum)
+    plan, n_tiles = bmhip.mv_plan(wl.w_off, x_off, y_off, wl.OC, wl.C, bt=BT)
+    args = [be.params(len(wl.probs), n_tiles, BT), be.upload(plan), wl.W, X, Y]
+    k = be.kernel(wl.kname)
+
+    def run(n):
+        enc = be.encoder()
+        for _ in range(n):
+            if enc.dispatch(k, args, (n_tiles * 256,), (256,)) != 0:
+                raise RuntimeError("batched multi launch rejected")
+        return enc.wait_timed()
+
+    run(max(warmup, 1))
+    y_all = Y.read(np.float32)
+    for i in (1, 6, len(wl.probs) - 1):  # against the matrix's own matmul_forward_q8 launch at BT rows
+        OC, C = int(wl.OC[i]), int(wl.C[i])
+        y = be.alloc(4 * BT * OC)
+        rc = be.dispatch("matmul_forward_q8", [X, wl.W, y, y, be.params(BT, C, OC, 0)], ((OC + 31) & ~31, BT), (32,),
+                         offsets=[4 * int(x_off[i]), int(wl.w_off[i]), 0, 0, 0])
+        yo = int(y_off[i])
+        ref = y.read(np.float32)
+        # both accumulate in fp32, in different orders (normwise 1e-5)
+        if rc != 0 or np.abs(ref - y_all[yo:yo + BT * OC]).max() > 1e-5 * np.abs(ref).max():
+            raise RuntimeError(f"batched multi launch differs from matmul_forward_q8 on {wl.probs[i][0]}")
+    be.synchronize()
+    t0 = time.perf_counter()
+    ev_ms = run(steps)
+    be.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = ev_ms / steps
+    bps = wl.w_bytes + 4 * BT * (Csum + OCsum)
+    achieved = bps / (kern_ms * 1e-3) / 1e9
+    log(f"[bench] batch {BT}: {kern_ms * 1e3:.1f} us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
+    X.free()
+    Y.free()
+    return {
+        "workload": f"the main line's projections at batch {BT}: {BT} N(0,1) activation rows per matrix, one "
+                    f"matmul_forward_q8_vec_multi launch (params nprob, n_tiles, BT) per step, fp32 MFMA",
+        "bytes_per_step": bps, "steps": steps, "workgroups": n_tiles * ((BT + 15) // 16),
+        "kernel_us": round(kern_ms * 1e3, 3), "ms_per_step": round(wall * 1e3 / steps, 5),
+        "achieved_gbps": round(achieved, 2), "frac_hbm_peak": round(achieved / HBM_PEAK_GBS, 4),
+        "rows_per_s": round(BT / (wall / steps), 1),
+    }
+
+
 def q4_leg(model: str, steps: int, warmup: int):
     """Q4_0 decode projections of one token (the same matrices as the main line,
     reference forward.metal:654-858), one matmul_forward_q4_vec_multi launch
@@ -427,6 +480,7 @@ def main():
     ap.add_argument("--gemm", type=int, default=1, help="also time the config-4 prefill GEMM (0: skip)")
     ap.add_argument("--prefill", type=int, default=1, help="also time bm_forward prompt prefill (0: skip)")
     ap.add_argument("--q4", type=int, default=1, help="also time the Q4_0 decode matvec (0: skip)")
+    ap.add_argument("--batch8", type=int, default=1, help="also time the main line's matrices at batch 8 (0: skip)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
@@ -480,6 +534,8 @@ def main():
     log(f"[bench] wall {ms_step * 1e3:.1f} us/step, events {kern_ms * 1e3:.1f} us/launch, "
         f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of HBM peak)")
 
+    batch8 = batched_leg(be, wl, 8, args.steps, args.warmup) if args.batch8 else None
+
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(wl, args.cpu_seconds, args.cpu_threads)
@@ -532,6 +588,7 @@ def main():
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
         "pack_gbps_incl_upload": pack_gbps,
+        "batch8": batch8,
         "q4_matvec": q4,
         "prefill_gemm": gemm,
         "prefill": prefill,

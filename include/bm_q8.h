@@ -11,8 +11,11 @@
  *   "quantize_q8"        {src f32 [n], dst Q8 blocks [n/32], params int{n}}
  *   "quantize_q8_bf16"   {src bf16 [n], dst Q8 blocks [n/32], params int{n}}
  *   "matmul_forward_q8_vec_multi"
- *                        {params int{nprob, n_tiles}, plan (bm_q8_mv_plan),
- *                         weight arena, activation arena f32, output arena f32}
+ *                        {params int{nprob, n_tiles[, BT]}, plan (bm_q8_mv_plan;
+ *                         bm_q8_bmv_plan when BT >= 2), weight arena,
+ *                         activation arena f32, output arena f32}; BT (default
+ *                         1, at most 64) rows per problem, row-major with
+ *                         strides C (activations) and OC (outputs)
  *   "quantize_q4"        {src f32 [n], dst Q4 blocks [n/32], params int{n}}
  *   "quantize_q4_bf16"   {src bf16 [n], dst Q4 blocks [n/32], params int{n}}
  *   "matmul_forward_q4_vec_multi"
@@ -48,6 +51,14 @@ int  bm_q8_mv_tiles(int OC, int C);
  * receives the launch's workgroup count. */
 long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                    const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
+
+/* The same two for a matmul_forward_q8_vec_multi (or _q4_vec_multi) launch
+ * with BT >= 2 rows per problem (64 output rows per workgroup, each weight
+ * read once for up to 16 rows; the same tiling for Q8_0 and Q4_0): several
+ * decode sequences' projections in one launch. */
+int  bm_q8_bmv_tiles(int OC, int C);
+long bm_q8_bmv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
+                    const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
 
 /* The same two for a matmul_forward_q4_vec_multi launch over Q4_0 rows
  * (20-byte blocks; w_off in bytes). */

@@ -154,3 +154,80 @@ def test_matvec_multi_rejects_bad_plans(be):
     assert be.dispatch(k, [be.params(1, nt2), be.upload(big), W, X, Y], (nt2 * 256,), (256,)) == -1
     assert be.dispatch(k, [be.params(1, n_tiles + 1), be.upload(plan), W, X, Y], (n_tiles * 256,), (256,)) == -1
     assert not Y.read(np.float32).any()
+
+
+def _batched_problems(seed, shapes, BT, quant=po.quantize_q8):
+    ws, xs = [], []
+    for i, (OC, C) in enumerate(shapes):
+        ws.append(quant(bmhip.synth_normal(bmhip.synth_seed(seed, 0, i, 0), 0.02, OC * C)))
+        xs.append(bmhip.synth_normal(bmhip.synth_seed(seed, 0, i, 1), 1.0, BT * C))
+    w_off = np.cumsum([0] + [w.size for w in ws[:-1]])
+    x_off = np.cumsum([0] + [x.size for x in xs[:-1]])
+    y_off = np.cumsum([0] + [BT * s[0] for s in shapes[:-1]])
+    return ws, xs, w_off, x_off, y_off
+
+
+BATCHED_SHAPES = [(960, 960), (320, 960), (17, 64), (2560, 960), (960, 2560), (1, 32), (1536, 576), (100, 8224)]
+
+
+@pytest.mark.parametrize("BT", [2, 8, 16, 17, 33, 64])
+def test_matvec_multi_batched(be, BT):
+    """matmul_forward_q8_vec_multi with BT rows per problem (params {nprob, n_tiles, BT},
+    plan from bm_q8_bmv_plan) vs the fp64 oracle, and against each problem's own
+    matmul_forward_q8 launch at the same BT (the same bar: another summation order)."""
+    shapes = BATCHED_SHAPES
+    ws, xs, w_off, x_off, y_off = _batched_problems(61 + BT, shapes, BT)
+    plan, n_tiles = bmhip.mv_plan(w_off, x_off, y_off, [s[0] for s in shapes], [s[1] for s in shapes], bt=BT)
+    assert n_tiles == sum((s[0] + 63) // 64 for s in shapes)
+    W, X = be.upload(np.concatenate(ws)), be.upload(np.concatenate(xs))
+    Y = be.alloc(4 * BT * sum(s[0] for s in shapes))
+    rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(len(shapes), n_tiles, BT), be.upload(plan), W, X, Y],
+                     (n_tiles * 256,), (256,))
+    assert rc == 0
+    y = Y.read(np.float32)
+    for i, (OC, C) in enumerate(shapes):
+        got = y[y_off[i]:y_off[i] + BT * OC]
+        r = po.q8_matvec_f64(ws[i], xs[i], BT, C, OC)
+        assert normwise(got, r) <= RTOL, (i, normwise(got, r))
+        if i in (0, 2, 4) and BT < 16:  # BT >= 16 routes matmul_forward_q8 to the GEMM
+            single = run_mv(be, ws[i], xs[i], BT, C, OC, kernel="matmul_forward_q8")
+            assert normwise(got, single) <= RTOL, i
+
+
+def test_matvec_multi_batched_q4(be):
+    shapes = BATCHED_SHAPES
+    BT = 8
+    ws, xs, w_off, x_off, y_off = _batched_problems(67, shapes, BT, po.quantize_q4)
+    plan, n_tiles = bmhip.mv_plan(w_off, x_off, y_off, [s[0] for s in shapes], [s[1] for s in shapes], "q4", bt=BT)
+    W, X = be.upload(np.concatenate(ws)), be.upload(np.concatenate(xs))
+    Y = be.alloc(4 * BT * sum(s[0] for s in shapes))
+    rc = be.dispatch("matmul_forward_q4_vec_multi", [be.params(len(shapes), n_tiles, BT), be.upload(plan), W, X, Y],
+                     (n_tiles * 256,), (256,))
+    assert rc == 0
+    y = Y.read(np.float32)
+    for i, (OC, C) in enumerate(shapes):
+        got = y[y_off[i]:y_off[i] + BT * OC]
+        assert normwise(got, po.q4_matvec_f64(ws[i], xs[i], BT, C, OC)) <= RTOL, i
+
+
+def test_matvec_multi_batched_rejects(be):
+    OC, C, BT = 200, 576, 8
+    w = po.quantize_q8(bmhip.synth_normal(71, 0.02, OC * C))
+    W, X, Y = be.upload(w), be.upload(np.ones(BT * C, np.float32)), be.alloc(BT * OC * 4)
+    k = "matmul_forward_q8_vec_multi"
+    plan, nt = bmhip.mv_plan([0], [0], [0], [OC], [C], bt=BT)
+    up = be.upload(plan)
+    # more rows than the activation / output arenas hold
+    assert be.dispatch(k, [be.params(1, nt, BT + 1), up, W, X, Y], (nt * 256,), (256,)) == -1
+    # BT above 64
+    assert be.dispatch(k, [be.params(1, nt, 65), up, W, X, Y], (nt * 256,), (256,)) == -1
+    # a BT = 1 plan (other tiling) with BT = 8, and a batched plan with BT = 1
+    p1, nt1 = bmhip.mv_plan([0], [0], [0], [OC], [C])
+    assert nt1 != nt
+    assert be.dispatch(k, [be.params(1, nt1, BT), be.upload(p1), W, X, Y], (nt1 * 256,), (256,)) == -1
+    assert be.dispatch(k, [be.params(1, nt), up, W, X, Y], (nt * 256,), (256,)) == -1
+    # activation offset not a multiple of 4 floats
+    X2 = be.upload(np.ones(BT * C + 4, np.float32))
+    p2, _ = bmhip.mv_plan([0], [2], [0], [OC], [C], bt=BT)
+    assert be.dispatch(k, [be.params(1, nt, BT), be.upload(p2), W, X2, Y], (nt * 256,), (256,)) == -1
+    assert not Y.read(np.float32).any()
