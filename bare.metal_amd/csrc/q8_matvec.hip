@@ -293,29 +293,38 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
         for (int u = 0; u < BMV_U; u++) {
             const float xv[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
             const bool live = kb0 + u < nb;
+            /* the 4 groups' codes first, then their MFMAs interleaved: 4
+             * independent accumulation chains keep the matrix pipe busy */
+            float wv[BMV_GROUPS][8], sc[BMV_GROUPS];
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++) {
                 const unsigned char* blk = &tile[(16 * j + c) * LDR + u * BYTES];
-                const float sc = live ? *(const float*)blk : 0.0f;
+                sc[j] = live ? *(const float*)blk : 0.0f;
                 const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
                 const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
-                float wv[8];
                 if (QF == QF_Q4) {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) wv[i] = q4_code(q0, i);
+                    for (int i = 0; i < 8; i++) wv[j][i] = q4_code(q0, i);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        wv[i] = q8_byte(q0, i);
-                        wv[4 + i] = q8_byte(q1, i);
+                        wv[j][i] = q8_byte(q0, i);
+                        wv[j][4 + i] = q8_byte(q1, i);
                     }
                 }
-                bmm_f32x4 dd = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int i = 0; i < 8; i++) dd = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[i], dd, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sc, dd[v], acc[j][v]);
             }
+            bmm_f32x4 dd[BMV_GROUPS];
+#pragma unroll
+            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < BMV_GROUPS; j++)
+                    dd[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[j][i], dd[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < BMV_GROUPS; j++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sc[j], dd[j][v], acc[j][v]);
         }
     }
 #pragma unroll
