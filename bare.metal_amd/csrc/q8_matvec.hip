@@ -203,8 +203,8 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
 }
 
 /* matmul_forward_q8_vec_multi / _q4_vec_multi with BT >= 2 rows per problem
- * (several decode sequences' projections in one launch), on fp32 MFMA
- * (v_mfma_f32_16x16x4_f32, D[16][16] += A[16][4] x B[4][16]).
+ * (several decode sequences' projections in one launch), on bf16 MFMA
+ * (v_mfma_f32_16x16x32_bf16, D[16][16] += A[16][32] x B[32][16], fp32 sum).
  *
  * A workgroup is one wave; it runs the 64-row tile blockIdx.x - tile0 of
  * problem tile_map[blockIdx.x] (4 groups of 16 output rows) for batch rows
@@ -212,16 +212,20 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
  * the wave copies the 64 rows' spans of BMV_U blocks (contiguous in each
  * row) into LDS with 16-byte loads, so every weight byte is fetched once;
  * the MFMA operands are then read from LDS.  Per K block, lane l
- * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once and feeds it,
- * as the A operand, to 8 MFMAs for each row group, whose B operand is
- * q[r0 + c][32kb + 8g + i] (i = 0..7, the int8 or 4-bit codes converted
- * exactly to fp32); each group's block product is scaled by its row's block
- * scale and added in block order, as the reference scales each block's dot
- * product (forward.metal:575-623).  D layout: lane l holds batch rows
- * 4*(l/16)+v of output row l%16.  Problem p reads BT rows of C floats at
- * X + x_off (row stride C) and writes BT rows of OC floats at Y + y_off
- * (row stride OC). */
+ * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once, splits it into
+ * two bf16 terms (high part and residual) and feeds both, as the A operand,
+ * to two MFMAs for each row group, whose B operand is
+ * q[r0 + c][32kb + 8g .. +7] (the int8 or 4-bit codes, exact in bf16).  The
+ * products are exact and summed in fp32, so the only rounding beyond the
+ * fp32 reference's is the activations' 16-bit split (relative 2^-17).  Each
+ * group's block product is scaled by its row's block scale and added in
+ * block order, as the reference scales each block's dot product
+ * (forward.metal:575-623).  D layout: lane l holds batch rows 4*(l/16)+v of
+ * output row l%16.  Problem p reads BT rows of C floats at X + x_off (row
+ * stride C) and writes BT rows of OC floats at Y + y_off (row stride OC). */
 typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
+typedef float bmm_f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int BMV_GROUPS = 4;             /* 16-row groups per wave */
 constexpr int BMV_ROWS = 16 * BMV_GROUPS; /* output rows per workgroup */
 constexpr int BMV_U = 4;                  /* K blocks per step */
@@ -291,36 +295,40 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < BMV_U; u++) {
-            const float xv[8] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+            /* x = hi + lo in bf16 (round to nearest even each): 16 significant
+             * bits, relative error <= 2^-17 per activation; the codes are
+             * exact in bf16 and every product is exact in the fp32 sum */
+            const bmm_f32x8 xf = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+            const bmm_bf16x8 xh = __builtin_convertvector(xf, bmm_bf16x8);
+            const bmm_bf16x8 xl = __builtin_convertvector(xf - __builtin_convertvector(xh, bmm_f32x8), bmm_bf16x8);
             const bool live = kb0 + u < nb;
-            /* the 4 groups' codes first, then their MFMAs interleaved: 4
-             * independent accumulation chains keep the matrix pipe busy */
-            float wv[BMV_GROUPS][8], sc[BMV_GROUPS];
+            bmm_bf16x8 wv[BMV_GROUPS];
+            float sc[BMV_GROUPS];
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++) {
                 const unsigned char* blk = &tile[(16 * j + c) * LDR + u * BYTES];
                 sc[j] = live ? *(const float*)blk : 0.0f;
                 const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
                 const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
+                bmm_f32x8 w;
                 if (QF == QF_Q4) {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) wv[j][i] = q4_code(q0, i);
+                    for (int i = 0; i < 8; i++) w[i] = q4_code(q0, i);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
-                        wv[j][i] = q8_byte(q0, i);
-                        wv[j][4 + i] = q8_byte(q1, i);
+                        w[i] = q8_byte(q0, i);
+                        w[4 + i] = q8_byte(q1, i);
                     }
                 }
+                wv[j] = __builtin_convertvector(w, bmm_bf16x8);
             }
             bmm_f32x4 dd[BMV_GROUPS];
 #pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < BMV_GROUPS; j++)
+                dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[j], bmm_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < BMV_GROUPS; j++)
-                    dd[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], wv[j][i], dd[j], 0, 0, 0);
+            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[j], dd[j], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++)
 #pragma unroll
