@@ -190,7 +190,8 @@ def batched_leg(be, wl: Workload, BT: int, steps: int, warmup: int):
     """Config 3 at batch BT: the same weights (already packed in HBM), BT
     activation rows per matrix, one matmul_forward_q8_vec_multi launch with
     params {nprob, n_tiles, BT} per step (each weight read once for all BT
-    rows, fp32 MFMA)."""
+    rows; bf16 MFMA on the exact codes with the activations split into two
+    bf16 terms, fp32 sums)."""
     Csum, OCsum = int(wl.C.astype(np.int64).sum()), int(wl.OC.astype(np.int64).sum())
     x_off, y_off = (BT * wl.x_off).astype(np.uint64), (BT * wl.y_off).astype(np.uint64)
     X = be.upload(bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, 7, BT, 0), 1.0, BT * Csum))
@@ -231,7 +232,8 @@ def batched_leg(be, wl: Workload, BT: int, steps: int, warmup: int):
     Y.free()
     return {
         "workload": f"the main line's projections at batch {BT}: {BT} N(0,1) activation rows per matrix, one "
-                    f"matmul_forward_q8_vec_multi launch (params nprob, n_tiles, BT) per step, fp32 MFMA",
+                    f"matmul_forward_q8_vec_multi launch (params nprob, n_tiles, BT) per step: bf16 MFMA on the exact "
+                    f"codes, activations as two bf16 terms, fp32 sums",
         "bytes_per_step": bps, "steps": steps, "workgroups": n_tiles * ((BT + 15) // 16),
         "kernel_us": round(kern_ms * 1e3, 3), "ms_per_step": round(wall * 1e3 / steps, 5),
         "achieved_gbps": round(achieved, 2), "frac_hbm_peak": round(achieved / HBM_PEAK_GBS, 4),
