@@ -237,7 +237,7 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
     constexpr int BYTES = QFmt<QF>::BYTES;
     constexpr int SPAN = BMV_U * BYTES;   /* bytes of one row per step: 144 (Q8_0), 80 (Q4_0) */
     constexpr int CPR = SPAN / 16;        /* 16-byte chunks per row span */
-    constexpr int LDR = SPAN + 16;        /* LDS row pitch */
+    constexpr int LDR = SPAN + 4;         /* LDS row pitch: an odd number of dwords spreads the rows over the banks */
     constexpr int LANE_OFF = QF == QF_Q4 ? 4 : 8; /* code bytes per lane and block */
     static_assert(SPAN % 16 == 0, "row span must be whole 16-byte chunks");
     __shared__ __attribute__((aligned(16))) unsigned char tile[BMV_ROWS * LDR];
