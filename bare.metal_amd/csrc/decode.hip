@@ -94,10 +94,17 @@ __device__ __forceinline__ float rms_inv(const float* x, int C, float eps, float
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
 
 /* Order-preserving packing of (value, index) for an atomicMax argmax in
- * which the larger value wins and, on equal values, the smaller index. */
+ * which the larger value wins and, on equal values, the smaller index: the
+ * result of the reference's scan 'if (v[i] > v[best]) best = i' from
+ * best = 0 (tools/run.c:56-60, sampler.c:36-39).  That scan treats -0 and
+ * +0 as equal, never moves to a NaN, and never moves away from a NaN at
+ * index 0; so -0 packs as +0, a NaN packs below every number, and a NaN at
+ * index 0 above every number. */
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
     unsigned int u = __float_as_uint(v);
-    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    if (u == 0x80000000u) u = 0u;
+    if (v != v) u = idx == 0 ? 0xFFFFFFFFu : 0u;
+    else u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned int)idx);
 }
 __device__ __forceinline__ int argmax_key_index(unsigned long long k) {

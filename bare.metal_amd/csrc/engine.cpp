@@ -32,6 +32,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <time.h>
 #include <string.h>
 
 #include <algorithm>
@@ -1065,7 +1066,15 @@ extern "C" long bm_profile_phases(bm_session_t* S, double* ms) {
 }
 
 /* ------------------------------------------------------------------ */
-/* sampler: reference src/baremetal/sampler.c:33-81 and tools/run.c:53-104 */
+/* sampler: reference src/baremetal/sampler.c:33-81 (bm_sample) and
+ * tools/run.c:53-104 (the driver's draw).  Both run temperature -> softmax
+ * -> top-k mask -> top-p mask -> one hashed-LCG draw over the cumulative
+ * sum; they differ in three places, kept here as the reference has them:
+ * bm_sample's sampler starts with top_k = 40 (reference api.c:85), chains
+ * its state (the hash output becomes the next state, sampler.c:74-76) and
+ * returns n - 1 when the cumulative sum never reaches the target
+ * (sampler.c:80); the driver hashes seed, seed + 1, ... (run.c:172) and
+ * returns 0 there (run.c:100). */
 
 struct bm_sampler_s {
     int vocab_size;
@@ -1084,7 +1093,9 @@ extern "C" bm_sampler_t* bm_create_sampler(int vocab_size, float temp, float top
     s->vocab_size = vocab_size;
     s->temperature = temp;
     s->topp = topp;
+    s->top_k = 40;
     s->rng = (unsigned int)seed;
+    if (seed == 0) s->rng = (unsigned int)(uintptr_t)s; /* non-zero default, as the reference */
     s->probs = (float*)malloc((size_t)vocab_size * sizeof(float));
     s->idx = (int*)malloc((size_t)vocab_size * sizeof(int));
     if (!s->probs || !s->idx) {
@@ -1114,37 +1125,48 @@ static int cmp_desc(const void* a, const void* b) {
     return fa > fb ? -1 : (fa < fb ? 1 : 0);
 }
 
-/* temperature -> softmax -> top-k mask -> top-p mask -> inverse-CDF draw */
-static int sample_probs(float* p, int* idx, int n, float temperature, int top_k, float top_p, unsigned int rng_state,
-                        const float* logits) {
+/* The hashed LCG step of both samplers. */
+static unsigned int lcg_hash(unsigned int state) {
+    unsigned int r = state * 1664525u + 1013904223u;
+    r ^= r >> 13;
+    r *= 1274126177u;
+    r ^= r >> 16;
+    return r;
+}
+
+/* temperature -> softmax -> top-k mask -> top-p mask -> inverse-CDF draw
+ * with the hash value r; `fallback` when the cumulative sum never reaches
+ * the target (a NaN logit).  Ties in the sort do not change the result:
+ * the threshold and the cut depend on the sorted values only. */
+static int sample_probs(float* p, int* idx, int n, float temperature, int top_k, float top_p, unsigned int r,
+                        int fallback, const float* logits) {
     if (temperature <= 0.0f) return argmax_first(logits, n);
+    for (int i = 0; i < n; i++) p[i] = logits[i] / temperature;
     float mx = -INFINITY;
-    for (int i = 0; i < n; i++) {
-        p[i] = logits[i] / temperature;
+    for (int i = 0; i < n; i++)
         if (p[i] > mx) mx = p[i];
-    }
     float sum = 0.0f;
     for (int i = 0; i < n; i++) {
         p[i] = expf(p[i] - mx);
         sum += p[i];
     }
     for (int i = 0; i < n; i++) p[i] /= sum;
-    if ((top_k > 0 && top_k < n) || (top_p > 0.0f && top_p < 1.0f)) {
+    if (top_k > 0 && top_k < n) {
         for (int i = 0; i < n; i++) idx[i] = i;
         g_sort_vals = p;
         qsort(idx, n, sizeof(int), cmp_desc);
-    }
-    if (top_k > 0 && top_k < n) {
         const float thresh = p[idx[top_k - 1]];
-        float s = 0.0f;
-        for (int i = 0; i < n; i++) {
+        for (int i = 0; i < n; i++)
             if (p[i] < thresh) p[i] = 0.0f;
-            s += p[i];
-        }
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += p[i];
         if (s > 0.0f)
             for (int i = 0; i < n; i++) p[i] /= s;
     }
     if (top_p > 0.0f && top_p < 1.0f) {
+        for (int i = 0; i < n; i++) idx[i] = i;
+        g_sort_vals = p;
+        qsort(idx, n, sizeof(int), cmp_desc);
         float cum = 0.0f, cut = 0.0f;
         for (int i = 0; i < n; i++) {
             cum += p[idx[i]];
@@ -1153,32 +1175,31 @@ static int sample_probs(float* p, int* idx, int n, float temperature, int top_k,
                 break;
             }
         }
-        float s = 0.0f;
-        for (int i = 0; i < n; i++) {
+        for (int i = 0; i < n; i++)
             if (p[i] < cut) p[i] = 0.0f;
-            s += p[i];
-        }
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s += p[i];
         if (s > 0.0f)
             for (int i = 0; i < n; i++) p[i] /= s;
     }
-    float sum2 = 0.0f;
-    for (int i = 0; i < n; i++) sum2 += p[i];
-    unsigned int r = rng_state * 1664525u + 1013904223u;
-    r ^= r >> 13;
-    r *= 1274126177u;
-    r ^= r >> 16;
-    const float target = ((float)(r & 0xFFFFFF) / (float)0x1000000) * sum2;
+    float total = 0.0f;
+    for (int i = 0; i < n; i++) total += p[i];
+    const float target = ((float)(r & 0xFFFFFF) / (float)0x1000000) * total;
     float c = 0.0f;
     for (int i = 0; i < n; i++) {
         c += p[i];
-        if (c >= target && p[i] > 0.0f) return i;
+        if (c >= target) return i;
     }
-    return argmax_first(logits, n);
+    return fallback;
 }
 
 extern "C" int bm_sample(bm_sampler_t* s, const float* logits) {
     if (!s || !logits) return 0;
-    return sample_probs(s->probs, s->idx, s->vocab_size, s->temperature, s->top_k, s->topp, s->rng++, logits);
+    if (s->temperature <= 0.0f) return argmax_first(logits, s->vocab_size);
+    const unsigned int r = lcg_hash(s->rng);
+    s->rng = r;
+    return sample_probs(s->probs, s->idx, s->vocab_size, s->temperature, s->top_k, s->topp, r, s->vocab_size - 1,
+                        logits);
 }
 
 /* ------------------------------------------------------------------ */
@@ -1201,7 +1222,7 @@ extern "C" int bm_run_tokens(bm_context_t* ctx, bm_model_t* m, const int* prompt
             if (callback && callback(toks[i], user_data)) break;
         free(toks);
     } else {
-        if (seed == 0) seed = 1;
+        if (seed == 0) seed = (uint64_t)time(NULL); /* as the reference driver, run.c:135 */
         unsigned int rng_state = (unsigned int)seed;
         float* p = (float*)malloc((size_t)m->V * sizeof(float));
         int* idx = (int*)malloc((size_t)m->V * sizeof(int));
@@ -1214,7 +1235,7 @@ extern "C" int bm_run_tokens(bm_context_t* ctx, bm_model_t* m, const int* prompt
                 break;
             }
             if (pos >= n_prompt - 1) {
-                next = sample_probs(p, idx, m->V, temperature, top_k, top_p, rng_state++, logits);
+                next = sample_probs(p, idx, m->V, temperature, top_k, top_p, lcg_hash(rng_state++), 0, logits);
                 if (callback && callback(next, user_data)) break;
             }
         }

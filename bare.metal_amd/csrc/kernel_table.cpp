@@ -21,6 +21,7 @@ int bmk_launch_q8_matvec(const bmk_launch_t* a);
 int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
 int bmk_launch_copy_buffer(const bmk_launch_t* a);
+int bmk_launch_stream_read(const bmk_launch_t* a);
 int bmk_launch_q8_gemm_multi(const bmk_launch_t* a);
 int bmk_launch_cast_bf16(const bmk_launch_t* a);
 int bmk_launch_rmsnorm(const bmk_launch_t* a);
@@ -70,6 +71,8 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"cast_f32_bf16", 3, B(2), B(1), bmk_launch_cast_bf16, 0},
     /* new: device-to-device copy; {src, dst, params int64{nbytes}} */
     {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
+    /* new: read-only stream (HBM read ceiling); {src, sink u32[4*wg], params int64{nbytes, wg}} */
+    {"stream_read", 3, B(2), B(1), bmk_launch_stream_read, 0},
     /* decode-step kernels (buffer orders: reference scheduler.c:835-947) */
     /* reference forward.metal:1019-1060; {inp, weight, out, params{N,C}, eps} */
     {"rmsnorm_forward_v2", 5, B(3) | B(4), B(2), bmk_launch_rmsnorm, 0},

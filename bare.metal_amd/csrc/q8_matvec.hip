@@ -212,12 +212,12 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
  * the wave copies the 64 rows' spans of BMV_U blocks (contiguous in each
  * row) into LDS with 16-byte loads, so every weight byte is fetched once;
  * the MFMA operands are then read from LDS.  Per K block, lane l
- * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once, splits it into
- * two bf16 terms (high part and residual) and feeds both, as the A operand,
- * to two MFMAs for each row group, whose B operand is
- * q[r0 + c][32kb + 8g .. +7] (the int8 or 4-bit codes, exact in bf16).  The
- * products are exact and summed in fp32, so the only rounding beyond the
- * fp32 reference's is the activations' 16-bit split (relative 2^-17).  Each
+ * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once, splits it
+ * exactly into three bf16 terms (split3) and feeds each, as the A operand,
+ * to one MFMA per row group, whose B operand is q[r0 + c][32kb + 8g .. +7]
+ * (the int8 or 4-bit codes, exact in bf16).  Every product is exact, so
+ * the block sums are fp32 sums of the exact x * q products, as in the fp32
+ * reference (only the summation order differs).  Each
  * group's block product is scaled by its row's block scale and added in
  * block order, as the reference scales each block's dot product
  * (forward.metal:575-623).  D layout: lane l holds batch rows 4*(l/16)+v of
@@ -229,6 +229,39 @@ typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int BMV_GROUPS = 4;             /* 16-row groups per wave */
 constexpr int BMV_ROWS = 16 * BMV_GROUPS; /* output rows per workgroup */
 constexpr int BMV_U = 4;                  /* K blocks per step */
+
+/* x = hi + mid + lo with three bf16 terms: hi keeps the top 8 significant
+ * bits of x (truncated, so no term overflows), mid the top 8 of x - hi and
+ * lo the at most 8 bits left; both subtractions are exact in fp32, so the
+ * split is exact for every finite x whose lowest significant bit lies at or
+ * above bf16's smallest normal (|x| >= 2^-102 suffices).  A non-finite x
+ * goes whole into hi (a NaN kept a NaN) with mid = lo = 0, so its products
+ * are the fp32 ones (Inf * 0 = NaN, Inf * q = Inf). */
+__device__ __forceinline__ void split3(const bmm_f32x8& x, bmm_bf16x8& hi, bmm_bf16x8& mid, bmm_bf16x8& lo) {
+    unsigned int h[8], m[8], l[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const unsigned int u = __float_as_uint(x[i]);
+        const bool fin = (u & 0x7f800000u) != 0x7f800000u;
+        const unsigned int hb = (fin ? u : (u | ((u & 0x007fffffu) ? 0x00400000u : 0u))) & 0xffff0000u;
+        const float r1 = fin ? x[i] - __uint_as_float(hb) : 0.0f;
+        const unsigned int mb = __float_as_uint(r1) & 0xffff0000u;
+        const float r2 = r1 - __uint_as_float(mb);
+        h[i] = hb;
+        m[i] = mb;
+        l[i] = __float_as_uint(r2) & 0xffff0000u;
+    }
+    unsigned int ph[4], pm[4], pl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        ph[i] = (h[2 * i] >> 16) | h[2 * i + 1];
+        pm[i] = (m[2 * i] >> 16) | m[2 * i + 1];
+        pl[i] = (l[2 * i] >> 16) | l[2 * i + 1];
+    }
+    __builtin_memcpy(&hi, ph, 16);
+    __builtin_memcpy(&mid, pm, 16);
+    __builtin_memcpy(&lo, pl, 16);
+}
 
 template <int QF>
 __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restrict__ W, const float* __restrict__ X,
@@ -295,19 +328,20 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < BMV_U; u++) {
-            /* x = hi + lo in bf16 (round to nearest even each): 16 significant
-             * bits, relative error <= 2^-17 per activation; the codes are
-             * exact in bf16 and every product is exact in the fp32 sum */
+            /* x = hi + mid + lo exactly; the codes are exact in bf16 and
+             * every product is exact in the fp32 sum */
+            /* blocks past the row (last step only; the same for the whole
+             * wave) are skipped, not weighted by 0: 0 * Inf would be NaN */
+            if (kb0 + u >= nb) break;
             const bmm_f32x8 xf = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
-            const bmm_bf16x8 xh = __builtin_convertvector(xf, bmm_bf16x8);
-            const bmm_bf16x8 xl = __builtin_convertvector(xf - __builtin_convertvector(xh, bmm_f32x8), bmm_bf16x8);
-            const bool live = kb0 + u < nb;
+            bmm_bf16x8 xh, xm, xl;
+            split3(xf, xh, xm, xl);
             bmm_bf16x8 wv[BMV_GROUPS];
             float sc[BMV_GROUPS];
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++) {
                 const unsigned char* blk = &tile[(16 * j + c) * LDR + u * BYTES];
-                sc[j] = live ? *(const float*)blk : 0.0f;
+                sc[j] = *(const float*)blk;
                 const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
                 const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
                 bmm_f32x8 w;
@@ -327,6 +361,8 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++)
                 dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[j], bmm_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wv[j], dd[j], 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++) dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[j], dd[j], 0, 0, 0);
 #pragma unroll

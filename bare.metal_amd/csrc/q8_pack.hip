@@ -24,7 +24,9 @@
  * Mapping: 8 lanes per block, each lane owns 4 consecutive elements (one
  * 16-byte load), so a wave reads 1 KiB of contiguous source and writes 288
  * contiguous bytes of blocks.  The block max is a 3-step xor shuffle inside
- * the 8-lane group.  HBM-bound: 4 (or 2) + 1.125 bytes per element.
+ * the 8-lane group.  A Q8 workgroup packs 8 such 32-block groups, with all 8
+ * source loads of a lane issued before the first reduction.  HBM-bound: 4
+ * (or 2) + 1.125 bytes per element.
  */
 #include "bmk.h"
 
@@ -57,17 +59,9 @@ __device__ __forceinline__ void load4(const void* src, long e, float v[4]) {
     }
 }
 
-template <bool SRC_BF16>
-__global__ __launch_bounds__(256) void k_quantize_q8(const void* __restrict__ src, unsigned char* __restrict__ dst,
-                                                     long nblocks) {
-    const long gt = (long)blockIdx.x * 256 + threadIdx.x;
-    const long blk = gt >> 3;
-    const int j = threadIdx.x & 7;
-    const bool active = blk < nblocks;
-
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (active) load4<SRC_BF16>(src, blk * 32 + 4 * j, v);
-
+/* One block's scale and this lane's 4 packed codes from the lane's 4
+ * elements; the block max meets over the 8-lane group. */
+__device__ __forceinline__ unsigned int q8_pack4(const float v[4], float& scale_out) {
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -79,7 +73,6 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const void* __restrict__ sr
         float o = __shfl_xor(m, off, 8);
         m = (o > m) ? o : m;
     }
-
     const float scale = m / 127.0f;
     unsigned int packed = 0u;
     if (scale != 0.0f) {
@@ -90,13 +83,43 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const void* __restrict__ sr
             packed |= ((unsigned int)q & 0xffu) << (8 * i);
         }
     }
-    if (active) {
-        unsigned char* b = dst + blk * 36;
-        unsigned int* bw = (unsigned int*)__builtin_assume_aligned(b, 4);
-        bw[1 + j] = packed;
-        if (j == 0) bw[0] = __float_as_uint(scale);
+    scale_out = scale;
+    return packed;
+}
+
+/* A workgroup packs PK_U groups of 32 consecutive blocks: step u covers
+ * blocks (blockIdx.x * PK_U + u) * 32 + lane / 8.  Every step's source load
+ * is issued before the first block is reduced, so a lane has PK_U 16-byte
+ * loads (8-byte for bf16) in flight; each step's loads are still one
+ * contiguous 4 KiB (2 KiB) span per workgroup. */
+constexpr int PK_U = 8;
+
+template <bool SRC_BF16>
+__global__ __launch_bounds__(256) void k_quantize_q8(const void* __restrict__ src, unsigned char* __restrict__ dst,
+                                                     long nblocks) {
+    const int j = threadIdx.x & 7;
+    const long blk0 = (long)blockIdx.x * (PK_U * 32) + (threadIdx.x >> 3);
+    float v[PK_U][4];
+#pragma unroll
+    for (int u = 0; u < PK_U; u++) {
+        const long blk = blk0 + 32 * u;
+        v[u][0] = v[u][1] = v[u][2] = v[u][3] = 0.0f;
+        if (blk < nblocks) load4<SRC_BF16>(src, blk * 32 + 4 * j, v[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < PK_U; u++) {
+        const long blk = blk0 + 32 * u;
+        float scale;
+        const unsigned int packed = q8_pack4(v[u], scale);
+        if (blk < nblocks) {
+            unsigned int* bw = (unsigned int*)__builtin_assume_aligned(dst + blk * 36, 4);
+            bw[1 + j] = packed;
+            if (j == 0) bw[0] = __float_as_uint(scale);
+        }
     }
 }
+
+static unsigned pack_grid(long nblocks) { return (unsigned)((nblocks + PK_U * 32 - 1) / (PK_U * 32)); }
 
 template <bool SRC_BF16>
 int launch_quantize(const bmk_launch_t* a) {
@@ -109,9 +132,7 @@ int launch_quantize(const bmk_launch_t* a) {
     BMK_NEED_BYTES(a, 1, nblocks * 36, "dst");
     BMK_REQUIRE(((uintptr_t)a->dev[0] & (SRC_BF16 ? 7 : 3)) == 0 && ((uintptr_t)a->dev[1] & 3) == 0,
                 "quantize_q8: misaligned src/dst offset");
-    const long threads = nblocks * 8;
-    const unsigned grid = (unsigned)((threads + 255) / 256);
-    hipLaunchKernelGGL(k_quantize_q8<SRC_BF16>, dim3(grid), dim3(256), 0, a->stream, (const void*)a->dev[0],
+    hipLaunchKernelGGL(k_quantize_q8<SRC_BF16>, dim3(pack_grid(nblocks)), dim3(256), 0, a->stream, (const void*)a->dev[0],
                        (unsigned char*)a->dev[1], nblocks);
     BMK_LAUNCH_CHECK();
     return 0;
@@ -213,9 +234,7 @@ extern "C" int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStre
 /* Engine-side pack of n bf16 values (the reference's bmt_quantize_q8_bf16;
  * src 8-byte aligned, n a positive multiple of 32). */
 extern "C" int q8_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s) {
-    const long nblocks = n / 32;
-    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
-    hipLaunchKernelGGL(k_quantize_q8<true>, dim3(grid), dim3(256), 0, s, src, dst, nblocks);
+    hipLaunchKernelGGL(k_quantize_q8<true>, dim3(pack_grid(n / 32)), dim3(256), 0, s, src, dst, n / 32);
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -226,9 +245,7 @@ extern "C" int bmk_launch_quantize_q8_bf16(const bmk_launch_t* a) { return launc
 /* Engine-side pack of n fp32 values (n a positive multiple of 32, src 4-byte
  * and dst 4-byte aligned; checked by the caller). */
 extern "C" int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s) {
-    const long nblocks = n / 32;
-    const unsigned grid = (unsigned)((nblocks * 8 + 255) / 256);
-    hipLaunchKernelGGL(k_quantize_q8<false>, dim3(grid), dim3(256), 0, s, (const void*)src, dst, nblocks);
+    hipLaunchKernelGGL(k_quantize_q8<false>, dim3(pack_grid(n / 32)), dim3(256), 0, s, (const void*)src, dst, n / 32);
     BMK_LAUNCH_CHECK();
     return 0;
 }

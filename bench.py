@@ -79,7 +79,10 @@ FORMATS = {  # block bytes, pack kernel, multi-matvec kernel
 class Workload:
     """Quantized weights, activations and outputs of one token's projections in three arenas."""
 
-    def __init__(self, be: bmhip.Backend, probs, fmt: str = "q8", seed: int = BASE_SEED):
+    def __init__(self, be: bmhip.Backend, probs, fmt: str = "q8", seed: int = BASE_SEED, src=None):
+        """src: optional device buffer already holding every matrix's fp32
+        weights back to back in problem order (the pack leg's source), packed
+        from there instead of being generated again."""
         self.be = be
         self.probs = probs
         self.fmt, self.seed = fmt, seed
@@ -97,25 +100,27 @@ class Workload:
         self.X = be.alloc(4 * int(C.sum()))
         self.Y = be.alloc(4 * int(OC.sum()))
         self.pack_ms = 0.0
-        self._fill()
+        self._fill(src)
         plan, self.n_tiles = bmhip.mv_plan(self.w_off, self.x_off, self.y_off, self.OC, self.C, fmt)
         self.plan = be.upload(plan)
         self.params = be.params(len(probs), self.n_tiles)
         self.kname = kname
         self.k = be.kernel(kname)
 
-    def _fill(self):
+    def _fill(self, src=None):
         be = self.be
         big = max(int(o) * int(c) for o, c in zip(self.OC, self.C))
-        stage = be.alloc(4 * big)
+        stage = be.alloc(4 * big) if src is None else src
         xs = np.empty(int(self.C.sum()), np.float32)
+        s_off = 0
         for i, (name, mid, l, m, OC, C) in enumerate(self.probs):
             n = OC * C
-            w32 = bmhip.synth_normal(bmhip.synth_seed(self.seed, mid, l, m), 0.02, n)
-            stage.write(w32)
+            if src is None:
+                stage.write(bmhip.synth_normal(bmhip.synth_seed(self.seed, mid, l, m), 0.02, n))
             enc = be.encoder()
             rc = enc.dispatch(be.kernel(self.pack_kernel), [stage, self.W, be.params(n)], (n // 4,), (256,),
-                              offsets=[0, int(self.w_off[i]), 0])
+                              offsets=[0 if src is None else 4 * s_off, int(self.w_off[i]), 0])
+            s_off += n
             if rc != 0:
                 raise RuntimeError(f"{self.pack_kernel} failed for {name}")
             self.pack_ms += enc.wait_timed()
@@ -123,10 +128,14 @@ class Workload:
             xs[xo:xo + C] = bmhip.synth_normal(bmhip.synth_seed(self.seed, mid, l, 100 + m), 1.0, C)
         self.X.write(xs)
         self.pack_elems = int((self.OC.astype(np.int64) * self.C).sum())
-        stage.free()
+        if src is None:
+            stage.free()
 
-    def launch(self, enc) -> None:
-        rc = enc.dispatch(self.k, [self.params, self.plan, self.W, self.X, self.Y], (self.n_tiles * 256,), (256,))
+    def launch(self, enc, w_byte_off: int = 0) -> None:
+        """One launch; w_byte_off selects a replica of the weight arena laid
+        out at that byte offset of a larger buffer (self.W then points there)."""
+        rc = enc.dispatch(self.k, [self.params, self.plan, self.W, self.X, self.Y], (self.n_tiles * 256,), (256,),
+                          offsets=[0, 0, w_byte_off, 0, 0] if w_byte_off else None)
         if rc != 0:
             raise RuntimeError(f"{self.kname} dispatch rejected")
 
@@ -147,7 +156,36 @@ def check_against_single(be, wl: Workload, idx):
             raise RuntimeError(f"multi launch differs from the single launch on {wl.probs[i][0]}")
 
 
+def host_cpu():
+    """The host CPU the baselines run on: model string, online and usable core counts."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "online": os.sysconf("SC_NPROCESSORS_ONLN"), "usable": len(os.sched_getaffinity(0))}
+
+
+def _timed_loop(fn, budget: float):
+    """Calls fn() until budget seconds have passed (after one untimed call); returns (calls, seconds)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= budget:
+            return n, dt
+
+
 def cpu_baseline(wl: Workload, seconds: float, threads: int):
+    """The main line's whole token on the host: the oracle's fp32 SIMD +
+    OpenMP restatement of the same Q8 arithmetic, at 1 thread and at
+    `threads` (the GPU box's CPU share), over a time-bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle as po
 
@@ -155,73 +193,230 @@ def cpu_baseline(wl: Workload, seconds: float, threads: int):
     x = wl.X.read(np.float32)
     y = np.zeros(int(wl.OC.sum()), np.float32)
     args = (wl.w_off, wl.x_off, wl.y_off, wl.OC, wl.C)
-    def timed(nthreads, budget):
-        po.cpu_q8_matvec_multi(w, x, y, *args, nthreads)  # warm caches / threads
-        n, t0 = 0, time.perf_counter()
-        while True:
-            po.cpu_q8_matvec_multi(w, x, y, *args, nthreads)
-            n += 1
-            dt = time.perf_counter() - t0
-            if dt >= budget:
-                return n, dt
-
-    # the survey asks for one core and all cores: one core gets a quarter of the budget
-    n1, dt1 = timed(1, seconds / 4)
-    n, dt = timed(threads, seconds)
+    n1, dt1 = _timed_loop(lambda: po.cpu_q8_matvec_multi(w, x, y, *args, 1), seconds / 4)
+    n, dt = _timed_loop(lambda: po.cpu_q8_matvec_multi(w, x, y, *args, threads), seconds)
     gpu_y = wl.Y.read(np.float32)
     rel = float(np.abs(y - gpu_y).max() / np.abs(gpu_y).max())
+    cpu = host_cpu()
     return {
         "value": round(wl.bytes_per_step * n / dt / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} whole tokens ({len(wl.probs)} Q8 matvecs each) in {dt:.1f} s, "
+        "sample": f"{n} whole tokens ({len(wl.probs)} Q8 matvecs each) in {dt:.1f} s on {threads} threads, "
                   f"fp32 SIMD ({po.oracle().orc_cpu_isa().decode()}) + OpenMP over rows; "
                   f"max rel diff vs GPU {rel:.1e}",
         "value_1core": round(wl.bytes_per_step * n1 / dt1 / 1e9, 3),
         "sample_1core": f"{n1} whole tokens in {dt1:.1f} s on 1 thread",
+        "cpu_model": cpu["model"], "cpus_online": cpu["online"], "cpus_usable": cpu["usable"],
     }
+
+
+def stream_ceiling(be, mib: int = 2048, reps: int = 10):
+    """stream_read over `mib` MiB: the HBM read rate a plain streaming kernel
+    reaches on this part (each byte read once per launch; 2 GiB >> MALL)."""
+    n = mib << 20
+    wg = 4096
+    src, sink = be.alloc(n), be.alloc(16 * wg)
+    k = be.kernel("stream_read")
+    p = be.params(n, wg, dtype=np.int64)
+    enc = be.encoder()
+    for _ in range(2):
+        if enc.dispatch(k, [src, sink, p], (wg * 256,), (256,)):
+            raise RuntimeError("stream_read rejected")
+    enc.wait_timed()
+    enc = be.encoder()
+    for _ in range(reps):
+        enc.dispatch(k, [src, sink, p], (wg * 256,), (256,))
+    ms = enc.wait_timed() / reps
+    src.free()
+    sink.free()
+    return {"bytes_read": n, "us_per_read": round(ms * 1e3, 2), "gbps": round(n / (ms * 1e-3) / 1e9, 1)}
+
+
+def replicate(be, src, nbytes: int, copies: int):
+    """A buffer holding `copies` back-to-back copies of src's first nbytes
+    (nbytes a multiple of 16), written by copy_buffer on the device."""
+    big = be.alloc(nbytes * copies)
+    enc = be.encoder()
+    for c in range(copies):
+        if enc.dispatch(be.kernel("copy_buffer"), [src, big, be.params(nbytes, dtype=np.int64)], (nbytes // 16,),
+                        (256,), offsets=[0, c * nbytes, 0]):
+            raise RuntimeError("copy_buffer rejected")
+    enc.wait_timed()
+    return big
+
+
+def per_call_us(be, kname, bufs, grid, tg, offsets_list):
+    """GPU time of each call in its own encoder (HIP events on the launch
+    stream around one dispatch), for single launches too short to keep the
+    GPU busy from Python; median in microseconds."""
+    k = be.kernel(kname)
+    ts = []
+    for offs in offsets_list:
+        enc = be.encoder()
+        if enc.dispatch(k, bufs, grid, tg, offsets=offs) != 0:
+            raise RuntimeError(f"{kname} dispatch rejected")
+        ts.append(enc.wait_timed())
+    return float(np.median(ts)) * 1e3
+
+
+def single_matvec_leg(be, OC: int, C: int, seed_ids, min_bytes: int = 1 << 30, passes: int = 2,
+                      cpu_threads: int = 16, cpu_seconds: float = 0.0):
+    """One Q8 matvec y = W x through matmul_forward_q8_vec (reference
+    forward.metal:575-623), timed per call: W packed on the device from
+    seeded N(0,0.02) weights, then copied to enough distinct addresses that
+    the rotation spans >= 1 GiB (each call reads weights that no cache
+    holds), and also the same copy call after call (MALL/L2-warm).
+    Optionally the same call on the host CPU (1 thread and cpu_threads)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle as po
+
+    n = OC * C
+    wbytes = n // 32 * 36
+    w32 = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, *seed_ids), 0.02, n)
+    x = bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, seed_ids[0], seed_ids[1], 100 + seed_ids[2]), 1.0, C)
+    src = be.upload(w32)
+    wq = be.alloc(wbytes)
+    if be.dispatch("quantize_q8", [src, wq, be.params(n)], (n // 4,), (256,)) != 0:
+        raise RuntimeError("quantize_q8 rejected")
+    wq_host = wq.read(np.uint8)
+    if not np.array_equal(wq_host, po.quantize_q8(w32)):
+        raise RuntimeError("device pack differs from the oracle")
+    copies = max(2, -(-min_bytes // wbytes))
+    big = replicate(be, wq, wbytes, copies)
+    bx, by = be.upload(x), be.alloc(4 * OC)
+    bufs = [bx, big, by, by, be.params(1, C, OC, 0)]
+    grid, tg = (OC * 128, 1), (128,)
+    per_call_us(be, "matmul_forward_q8_vec", bufs, grid, tg, [[0, 0, 0, 0, 0]] * 5)
+    y = by.read(np.float32)
+    r = po.q8_matvec_f64(wq_host, x, 1, C, OC)
+    err = float(np.abs(y - r).max() / np.abs(r).max())
+    if err > 1e-3:
+        raise RuntimeError(f"matvec normwise error {err}")
+    rot = [[0, c * wbytes, 0, 0, 0] for c in range(copies)] * passes
+    cold = per_call_us(be, "matmul_forward_q8_vec", bufs, grid, tg, rot)
+    warm = per_call_us(be, "matmul_forward_q8_vec", bufs, grid, tg, [[0, 0, 0, 0, 0]] * 200)
+    bpc = wbytes + 4 * C + 4 * OC
+    big.free()
+    out = {
+        "workload": f"one {OC}x{C} Q8 matvec (matmul_forward_q8_vec), N(0,0.02) weights packed on the device; "
+                    f"cold: {copies} copies at distinct addresses ({copies * wbytes / 2**30:.2f} GiB) called in "
+                    f"turn, {passes} passes; warm: the same copy 200 times; GPU time per call from HIP events "
+                    f"around each dispatch",
+        "bytes_per_call": bpc, "normwise_err": err,
+        "cold_us_per_call": round(cold, 3), "cold_gbps": round(bpc / (cold * 1e-6) / 1e9, 1),
+        "warm_us_per_call": round(warm, 3), "warm_gbps": round(bpc / (warm * 1e-6) / 1e9, 1),
+    }
+    if cpu_seconds > 0:
+        y = np.zeros(OC, np.float32)
+        for nt in (1, cpu_threads):
+            k, dt = _timed_loop(lambda: po.oracle().orc_cpu_q8_matvec_f32(po._p(wq_host), po._p(x), po._p(y), C, OC,
+                                                                          nt), cpu_seconds / 2)
+            out[f"cpu_{nt}t_us_per_call"] = round(dt / k * 1e6, 2)
+            out[f"cpu_{nt}t_gbps"] = round(bpc * k / dt / 1e9, 2)
+    log(f"[bench] matvec {OC}x{C}: cold {cold:.2f} us/call ({bpc / (cold * 1e-6) / 1e9:.0f} GB/s), "
+        f"warm {warm:.2f} us/call")
+    return out
+
+
+def pack_legs(be, src, n_all: int, packed_ref, steps: int = 10):
+    """The Q8 pack (quantize_q8, reference quant.c:10-29,54-60) on a source
+    already resident in HBM: (a) every weight of the main line's model in one
+    launch (n_all elements, packed bytes compared with the per-matrix packs
+    of the same weights), (b) LM-head-sized launches (49152 x D elements)
+    rotated over distinct source / destination windows.  Algorithmic bytes:
+    4 read + 1.125 written per element."""
+    out_bytes = n_all // 32 * 36
+    dst = be.alloc(out_bytes)
+    k = be.kernel("quantize_q8")
+    p_all = be.params(n_all)
+    enc = be.encoder()
+    enc.dispatch(k, [src, dst, p_all], (n_all // 4,), (256,))
+    enc.wait_timed()
+    if not np.array_equal(dst.read(np.uint8), packed_ref):
+        raise RuntimeError("whole-model pack differs from the per-matrix packs")
+    enc = be.encoder()
+    for _ in range(steps):
+        enc.dispatch(k, [src, dst, p_all], (n_all // 4,), (256,))
+    ms_all = enc.wait_timed() / steps
+    res = {"whole_model": {"elements": n_all, "bytes": 5.125 * n_all, "us_per_launch": round(ms_all * 1e3, 2),
+                           "gbps": round(5.125 * n_all / (ms_all * 1e-3) / 1e9, 1)}}
+    nh = V * 960
+    windows = min(n_all // nh, out_bytes // (nh // 32 * 36))
+    p_h = be.params(nh)
+    offs = [[4 * w * nh, w * (nh // 32 * 36), 0] for w in range(windows)]
+    enc = be.encoder()
+    for o in offs:
+        enc.dispatch(k, [src, dst, p_h], (nh // 4,), (256,), offsets=o)
+    enc.wait_timed()
+    reps = 4
+    enc = be.encoder()
+    for _ in range(reps):
+        for o in offs:
+            enc.dispatch(k, [src, dst, p_h], (nh // 4,), (256,), offsets=o)
+    ms_h = enc.wait_timed() / (reps * len(offs))
+    res["lm_head"] = {"elements": nh, "bytes": 5.125 * nh, "windows": windows, "us_per_launch": round(ms_h * 1e3, 2),
+                      "gbps": round(5.125 * nh / (ms_h * 1e-3) / 1e9, 1)}
+    dst.free()
+    for key in ("whole_model", "lm_head"):
+        g = res[key]["gbps"]
+        res[key]["roofline"] = {"bound": "hbm", "achieved": g, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(g / HBM_PEAK_GBS, 4)}
+        log(f"[bench] pack {key}: {res[key]['us_per_launch']} us, {g} GB/s ({g / HBM_PEAK_GBS:.1%})")
+    res["workload"] = ("quantize_q8 on a device-resident fp32 source: (a) all of the main line's weights "
+                       f"({n_all} elements) in one launch; (b) {nh}-element launches (the 49152x960 LM head) "
+                       f"over {windows} distinct source/destination windows in turn; 5.125 B/element")
+    return res
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
-def batched_leg(be, wl: Workload, BT: int, steps: int, warmup: int):
-    """Config 3 at batch BT: the same weights (already packed in HBM), BT
-    activation rows per matrix, one matmul_forward_q8_vec_multi launch with
-    params {nprob, n_tiles, BT} per step (each weight read once for all BT
-    rows; bf16 MFMA on the exact codes with the activations split into two
-    bf16 terms, fp32 sums)."""
+def batched_leg(be, wls, BT: int, steps: int, warmup: int):
+    """Config 3 at batch BT: the main line's weight copies (already packed in
+    HBM, launched in turn as the main line is), BT activation rows per
+    matrix, one matmul_forward_q8_vec_multi launch with params {nprob,
+    n_tiles, BT} per step (each weight read once for all BT rows; bf16 MFMA
+    on the exact codes with each activation split exactly into three bf16
+    terms, fp32 sums)."""
+    wl = wls[0]
     Csum, OCsum = int(wl.C.astype(np.int64).sum()), int(wl.OC.astype(np.int64).sum())
     x_off, y_off = (BT * wl.x_off).astype(np.uint64), (BT * wl.y_off).astype(np.uint64)
     X = be.upload(bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, 7, BT, 0), 1.0, BT * Csum))
     Y = be.alloc(4 * BT * OCsum)
     plan, n_tiles = bmhip.mv_plan(wl.w_off, x_off, y_off, wl.OC, wl.C, bt=BT)
-    args = [be.params(len(wl.probs), n_tiles, BT), be.upload(plan), wl.W, X, Y]
+    pbuf, params = be.upload(plan), be.params(len(wl.probs), n_tiles, BT)
     k = be.kernel(wl.kname)
 
-    def run(n):
+    def run(n, copies):
         enc = be.encoder()
-        for _ in range(n):
-            if enc.dispatch(k, args, (n_tiles * 256,), (256,)) != 0:
+        for i in range(n):
+            if enc.dispatch(k, [params, pbuf, copies[i % len(copies)].W, X, Y], (n_tiles * 256,), (256,)) != 0:
                 raise RuntimeError("batched multi launch rejected")
         return enc.wait_timed()
 
-    run(max(warmup, 1))
-    y_all = Y.read(np.float32)
-    for i in (1, 6, len(wl.probs) - 1):  # against the matrix's own matmul_forward_q8 launch at BT rows
-        OC, C = int(wl.OC[i]), int(wl.C[i])
-        y = be.alloc(4 * BT * OC)
-        rc = be.dispatch("matmul_forward_q8", [X, wl.W, y, y, be.params(BT, C, OC, 0)], ((OC + 31) & ~31, BT), (32,),
-                         offsets=[4 * int(x_off[i]), int(wl.w_off[i]), 0, 0, 0])
-        yo = int(y_off[i])
-        ref = y.read(np.float32)
-        # both accumulate in fp32, in different orders (normwise 1e-5)
-        if rc != 0 or np.abs(ref - y_all[yo:yo + BT * OC]).max() > 1e-5 * np.abs(ref).max():
-            raise RuntimeError(f"batched multi launch differs from matmul_forward_q8 on {wl.probs[i][0]}")
+    worst = 0.0
+    for w in wls:
+        run(1, [w])
+        y_all = Y.read(np.float32)
+        for i in (1, 6, len(w.probs) - 1):  # against the matrix's own matmul_forward_q8 launch at BT rows
+            OC, C = int(w.OC[i]), int(w.C[i])
+            y = be.alloc(4 * BT * OC)
+            rc = be.dispatch("matmul_forward_q8", [X, w.W, y, y, be.params(BT, C, OC, 0)], ((OC + 31) & ~31, BT),
+                             (32,), offsets=[4 * int(x_off[i]), int(w.w_off[i]), 0, 0, 0])
+            yo = int(y_off[i])
+            ref = y.read(np.float32)
+            # both are fp32 sums of x * q products in different orders: the batched
+            # launch's products are exact (three-term split), the fp32 path's rounded
+            err = float(np.abs(ref - y_all[yo:yo + BT * OC]).max() / np.abs(ref).max())
+            worst = max(worst, err)
+            if rc != 0 or err > 1e-5:
+                raise RuntimeError(f"batched multi launch differs from matmul_forward_q8 on {w.probs[i][0]}: {err}")
+    run(max(warmup, len(wls)), wls)
     be.synchronize()
     t0 = time.perf_counter()
-    ev_ms = run(steps)
+    ev_ms = run(steps, wls)
     be.synchronize()
     wall = time.perf_counter() - t0
     kern_ms = ev_ms / steps
@@ -231,14 +426,54 @@ def batched_leg(be, wl: Workload, BT: int, steps: int, warmup: int):
     X.free()
     Y.free()
     return {
-        "workload": f"the main line's projections at batch {BT}: {BT} N(0,1) activation rows per matrix, one "
-                    f"matmul_forward_q8_vec_multi launch (params nprob, n_tiles, BT) per step: bf16 MFMA on the exact "
-                    f"codes, activations as two bf16 terms, fp32 sums",
+        "workload": f"the main line's projections at batch {BT} ({len(wls)} weight copies in turn): {BT} N(0,1) "
+                    f"activation rows per matrix, one matmul_forward_q8_vec_multi launch (params nprob, n_tiles, "
+                    f"BT) per step: bf16 MFMA on the exact codes, each activation split exactly into three bf16 "
+                    f"terms, fp32 sums",
         "bytes_per_step": bps, "steps": steps, "workgroups": n_tiles * ((BT + 15) // 16),
         "kernel_us": round(kern_ms * 1e3, 3), "ms_per_step": round(wall * 1e3 / steps, 5),
         "achieved_gbps": round(achieved, 2), "frac_hbm_peak": round(achieved / HBM_PEAK_GBS, 4),
-        "rows_per_s": round(BT / (wall / steps), 1),
+        "rows_per_s": round(BT / (wall / steps), 1), "max_normwise_vs_fp32_path": worst,
     }
+
+
+def config2_leg(steps: int, warmup: int):
+    """Config 2: every Q8 projection of one SmolLM2-135M decode token at
+    batch 1 (+ the Q8 LM head 49152x576) in one matmul_forward_q8_vec_multi
+    launch.  The 151 MB set fits in the 256 MB Infinity Cache, which is
+    where a 135M decode finds it: 'warm' relaunches one copy; 'cold' launches
+    device-made copies at distinct addresses in turn (>= 1 GiB)."""
+    be = bmhip.Backend()
+    probs = problem_list("135m")
+    wl = Workload(be, probs)
+    enc = be.encoder()
+    wl.launch(enc)
+    enc.wait_timed()
+    check_against_single(be, wl, [1, 6, len(probs) - 1])
+    copies = max(2, -(-(1 << 30) // wl.w_bytes))
+    big = replicate(be, wl.W, wl.w_bytes, copies)
+    wl.W = big
+
+    def run(n, rotate):
+        enc = be.encoder()
+        for i in range(n):
+            wl.launch(enc, (i % copies) * wl.w_bytes if rotate else 0)
+        return enc.wait_timed() / n
+
+    run(max(warmup, copies), True)
+    cold = run(steps, True)
+    run(warmup, False)
+    warm = run(steps, False)
+    be.close()
+    bps = wl.bytes_per_step
+    res = {"workload": "SmolLM2-135M Q8 decode projections + Q8 LM head 49152x576, batch 1, one "
+                       f"matmul_forward_q8_vec_multi launch per token; cold: {copies} copies in turn",
+           "bytes_per_step": bps, "copies": copies,
+           "warm_kernel_us": round(warm * 1e3, 3), "warm_gbps": round(bps / (warm * 1e-3) / 1e9, 1),
+           "cold_kernel_us": round(cold * 1e3, 3), "cold_gbps": round(bps / (cold * 1e-3) / 1e9, 1)}
+    log(f"[bench] 135m token: warm {res['warm_kernel_us']} us ({res['warm_gbps']} GB/s), "
+        f"cold {res['cold_kernel_us']} us ({res['cold_gbps']} GB/s)")
+    return res
 
 
 def q4_leg(model: str, steps: int, warmup: int):
@@ -456,16 +691,25 @@ def e2e_decode(cpu_steps: int, cpu_threads: int, graph: bool = True):
         for src, dst in (("wq", "wq"), ("wk", "wk"), ("wv", "wv"), ("wo", "wo"), ("w_gate", "wg"),
                          ("w_up", "wu"), ("w_down", "wd")):
             arrs[dst] = po.quantize_q8(w[src])
-        dec = po.Decoder(dict(dims, MS=n_prompt + n_gen), arrs, nthreads=cpu_threads)
         prompt = bmhip.synth_uniform_int(seed, 0, dims["V"], n_prompt)
-        dec.step(int(prompt[0]), 0)
-        t0 = time.perf_counter()
-        for pos in range(1, cpu_steps + 1):
-            dec.step(int(prompt[pos]), pos)
-        dt = time.perf_counter() - t0
-        out["cpu_port_b1"] = {"tok_s": round(cpu_steps / dt, 2), "cores": cpu_threads, "kind": "port",
-                              "sample": f"{cpu_steps} decode steps of the C oracle (fp64 reductions)"}
-        dec.close()
+        cpu = host_cpu()
+        res = {"kind": "port", "cpu_model": cpu["model"], "cpus_online": cpu["online"],
+               "sample": "the config-5 decode step on the host (oracle/cpu_baseline.c: fp32, Q8 matvecs and the "
+                         "fp32 head vectorised like the matvec baseline, rows split over OpenMP threads), "
+                         "prompt tokens stepped from position 0"}
+        for nt, n in ((1, max(cpu_steps // 4, 2)), (cpu_threads, cpu_steps)):
+            dec = po.Decoder(dict(dims, MS=n_prompt + n_gen), arrs, nthreads=nt, fast=True)
+            dec.step(int(prompt[0]), 0)
+            t0 = time.perf_counter()
+            for pos in range(1, n + 1):
+                dec.step(int(prompt[pos]), pos)
+            dt = time.perf_counter() - t0
+            dec.close()
+            res[f"tok_s_{nt}t"] = round(n / dt, 2)
+            res[f"steps_{nt}t"] = n
+        res["tok_s"], res["cores"] = res[f"tok_s_{cpu_threads}t"], cpu_threads
+        out["cpu_port_b1"] = res
+        log(f"[bench] e2e cpu: {res['tok_s']} tok/s on {cpu_threads} threads, {res['tok_s_1t']} on 1")
     return out
 
 
@@ -486,6 +730,10 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="only run copy_buffer over this many MiB, 5 times (calibrates HBM byte counters)")
     ap.add_argument("--e2e-cpu-steps", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=3, help="independently seeded weight copies of the main line")
+    ap.add_argument("--pack", type=int, default=1, help="also time the device pack (0: skip)")
+    ap.add_argument("--singles", type=int, default=1, help="also time config 1 and the LM head alone (0: skip)")
+    ap.add_argument("--config2", type=int, default=1, help="also time the SmolLM2-135M token (0: skip)")
     ap.add_argument("--e2e-graph", type=int, default=1,
                     help="0: decode steps launched eagerly instead of replaying the captured graph (for kernel traces)")
     args = ap.parse_args()
@@ -509,48 +757,72 @@ def main():
     be = bmhip.Backend()
     probs = problem_list(args.model)
     t0 = time.perf_counter()
-    wl = Workload(be, probs)
-    log(f"[bench] {args.model}: {len(probs)} matrices, {wl.w_bytes / 1e6:.1f} MB Q8, "
-        f"{wl.n_tiles} workgroups per launch, setup {time.perf_counter() - t0:.1f} s")
+    # every matrix's fp32 weights of copy 0, resident on the device: the pack leg's source
+    n_all = int(sum(p[4] * p[5] for p in probs))
+    src = be.alloc(4 * n_all)
+    off = 0
+    for name, mid, l, m, OC, C in probs:
+        src.write(bmhip.synth_normal(bmhip.synth_seed(BASE_SEED, mid, l, m), 0.02, OC * C), offset=4 * off)
+        off += OC * C
+    wls = [Workload(be, probs, "q8", BASE_SEED, src=src)]
+    wls += [Workload(be, probs, "q8", BASE_SEED + k) for k in range(1, args.copies)]
+    wl = wls[0]
+    log(f"[bench] {args.model}: {len(probs)} matrices, {wl.w_bytes / 1e6:.1f} MB Q8 x {len(wls)} independently "
+        f"seeded copies, {wl.n_tiles} workgroups per launch, setup {time.perf_counter() - t0:.1f} s")
 
     enc = be.encoder()
-    for _ in range(max(args.warmup, 1)):
-        wl.launch(enc)
+    for i in range(max(args.warmup, len(wls))):
+        wls[i % len(wls)].launch(enc)
     enc.wait_timed()
-    check_against_single(be, wl, [1, 6, len(probs) - 1])
-    log("[bench] multi launch matches the single-matrix launch bit for bit")
+    for w in wls:
+        check_against_single(be, w, [1, 6, len(probs) - 1])
+    log("[bench] multi launch matches the single-matrix launch bit for bit on every copy")
 
-    be.synchronize()
-    t0 = time.perf_counter()
-    enc = be.encoder()
-    for _ in range(args.steps):
-        wl.launch(enc)
-    ev_ms = enc.wait_timed()  # HIP events on the launch stream around the K launches
-    be.synchronize()
-    wall = time.perf_counter() - t0
+    def timed(copies, steps):
+        be.synchronize()
+        t0 = time.perf_counter()
+        enc = be.encoder()
+        for i in range(steps):
+            copies[i % len(copies)].launch(enc)
+        ev = enc.wait_timed()  # HIP events on the launch stream around the launches
+        be.synchronize()
+        return ev, time.perf_counter() - t0
 
+    ev_ms, wall = timed(wls, args.steps)
     ms_step = wall * 1e3 / args.steps
     kern_ms = ev_ms / args.steps
     value = wl.bytes_per_step / (ms_step * 1e-3) / 1e9
     achieved = wl.bytes_per_step / (kern_ms * 1e-3) / 1e9
-    log(f"[bench] wall {ms_step * 1e3:.1f} us/step, events {kern_ms * 1e3:.1f} us/launch, "
-        f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of HBM peak)")
+    log(f"[bench] rotated over {len(wls)} copies: wall {ms_step * 1e3:.1f} us/step, events {kern_ms * 1e3:.1f} "
+        f"us/launch, {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of HBM peak)")
+    ev1, _ = timed(wls[:1], args.steps)
+    single_us = ev1 / args.steps * 1e3
+    log(f"[bench] one copy, launch after launch: {single_us:.1f} us/launch")
+    ceiling = stream_ceiling(be)
+    log(f"[bench] stream_read ceiling: {ceiling['gbps']} GB/s")
 
-    batch8 = batched_leg(be, wl, 8, args.steps, args.warmup) if args.batch8 else None
+    pack = pack_legs(be, src, n_all, wl.W.read(np.uint8)) if args.pack else None
+    src.free()
+    batch8 = batched_leg(be, wls, 8, args.steps, args.warmup) if args.batch8 else None
 
     cpu = None
     if args.cpu_seconds > 0:
         cpu = cpu_baseline(wl, args.cpu_seconds, args.cpu_threads)
-        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads, {cpu['value_1core']} on 1")
     bytes_per_step, w_bytes = wl.bytes_per_step, wl.w_bytes
-    pack_gbps = round(5.125 * wl.pack_elems / (wl.pack_ms * 1e-3) / 1e9, 2) if wl.pack_ms > 0 else None
-    del wl
+    del wl, wls
+    config1 = lm_head = None
+    if args.singles:
+        config1 = single_matvec_leg(be, 1536, 576, (1, 0, 5), cpu_threads=args.cpu_threads,
+                                    cpu_seconds=min(args.cpu_seconds, 4.0))
+        mid, D = MODELS[args.model][:2]
+        lm_head = single_matvec_leg(be, V, D, (mid, 0xFFFF, 7), passes=4)
     be.close()
 
+    config2 = config2_leg(args.steps, args.warmup) if args.config2 else None
     q4 = q4_leg(args.model, args.steps, args.warmup) if args.q4 else None
     gemm = gemm_leg(max(args.steps // 10, 10), 3) if args.gemm else None
     prefill = prefill_leg(graph=bool(args.e2e_graph)) if args.prefill else None
-    ceiling = copy_ceiling()
     e2e = (e2e_decode(args.e2e_cpu_steps if args.cpu_seconds > 0 else 0, args.cpu_threads, bool(args.e2e_graph))
            if args.e2e else None)
 
@@ -571,9 +843,12 @@ def main():
         "config": {
             "workload": f"SmolLM2-{args.model.upper()} Q8 decode projections, batch 1: {L} layers x "
                         f"(q,k,v,o,gate,up,down) + Q8 LM head {V}x{D}, one matmul_forward_q8_vec_multi "
-                        f"launch per token",
+                        f"launch per token, {args.copies} independently seeded weight copies launched in turn "
+                        f"({args.copies * w_bytes / 2**30:.2f} GiB, so no launch finds its weights in the 256 MB "
+                        f"Infinity Cache)",
             "bytes_per_step": bytes_per_step,
             "q8_weight_bytes": w_bytes,
+            "weight_copies": args.copies,
             "matrices": len(probs),
             "weights": "int8 Q8_0 blocks (32 x int8 + fp32 scale), N(0,0.02) quantized on device",
             "activations": "fp32 N(0,1), one vector per matrix",
@@ -585,11 +860,17 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": measured_traffic(args.model),
-            "copy_ceiling_gbps": ceiling["gbps"],
+            "kernel_us": round(kern_ms * 1e3, 3),
+            "read_stream_ceiling_gbps": ceiling["gbps"],
+            "frac_of_read_stream": round(achieved / ceiling["gbps"], 4),
         },
         "cpu_baseline": cpu,
         "kernel_us": round(kern_ms * 1e3, 3),
-        "pack_gbps_incl_upload": pack_gbps,
+        "one_copy_kernel_us": round(single_us, 3),
+        "pack": pack,
+        "config1_matvec": config1,
+        "lm_head_matvec": lm_head,
+        "config2_135m": config2,
         "batch8": batch8,
         "q4_matvec": q4,
         "prefill_gemm": gemm,

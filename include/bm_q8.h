@@ -27,6 +27,8 @@
  *                         weight arena, output arena f32}
  *   "cast_f32_bf16"      {src f32 [n], dst bf16 [n], params int64{n}} (round to nearest even)
  *   "copy_buffer"        {src, dst, params int64{nbytes}}
+ *   "stream_read"        {src, sink u32 [4 * workgroups], params int64{nbytes, workgroups}}
+ *                        (reads src once; the HBM read ceiling)
  */
 #ifndef BM_Q8_H
 #define BM_Q8_H

@@ -78,3 +78,171 @@ const char* orc_cpu_isa(void) {
     if (__builtin_cpu_supports("avx2")) return "avx2";
     return "x86-64";
 }
+
+/* ---- fp32 SIMD decode step (the config-5 CPU baseline) ----------------
+ * The reference's decode graph (src/baremetal/graph.c:126-226) on the host
+ * in fp32, as the GPU computes it: RMSNorm (forward.metal:1019-1060),
+ * q/k/v Q8 matvecs (:575-623), rotate-half RoPE (:1260-1313), KV store and
+ * GQA attention with scale 1/sqrt(HD) over S = pos + 1 keys (:1317-1465),
+ * o matvec + residual, RMSNorm, gate/up, SiLU gate (:1179-1190), down +
+ * residual, final RMSNorm and the fp32 tied LM head (:1636-1689).  Every
+ * matvec is split over the threads by rows and vectorised like rows_f32;
+ * the other ops are serial (they are a small part of a token).  This is a
+ * timing baseline; the fp64 decoder in decode_oracle.c is the checker. */
+#include "decode_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+
+typedef struct {
+    orc_model_t m;
+    float *kv, *x, *xn, *q, *k, *v, *att, *o, *g, *u, *dn, *sc, *logits;
+    int nt;
+} cpu_dec_t;
+
+__attribute__((target_clones("avx512f", "avx2", "default")))
+static void head_rows(const float* w, const float* x, float* y, int C, int r0, int r1) {
+    for (int r = r0; r < r1; r++) {
+        const float* row = w + (size_t)r * C;
+        float p[16] = {0};
+        for (int j = 0; j < C; j++) p[j & 15] += row[j] * x[j];
+        float acc = 0.0f;
+        for (int j = 0; j < 16; j++) acc += p[j];
+        y[r] = acc;
+    }
+}
+
+static void cpu_mv(const uint8_t* w, const float* x, float* y, int C, int OC, int nt) {
+#pragma omp parallel num_threads(nt)
+    {
+        int t = omp_get_thread_num(), n = omp_get_num_threads();
+        rows_f32(w, x, y, C, (int)((long)OC * t / n), (int)((long)OC * (t + 1) / n));
+    }
+}
+
+static void cpu_rmsnorm(const float* x, const float* w, float* out, int C, float eps) {
+    float ss = 0.0f;
+    for (int j = 0; j < C; j++) ss += x[j] * x[j];
+    const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+    for (int j = 0; j < C; j++) out[j] = (x[j] * inv) * w[j];
+}
+
+void* orc_cpu_decoder_create(const void* mp, int nthreads) {
+    const orc_model_t* m = (const orc_model_t*)mp;
+    if (m->qbits == 4 || m->head_q8) return NULL; /* Q8 projections + fp32 head only */
+    cpu_dec_t* d = (cpu_dec_t*)calloc(1, sizeof(cpu_dec_t));
+    if (!d) return NULL;
+    d->m = *m;
+    d->nt = nthreads > 0 ? nthreads : 1;
+    const int KV = m->NKV * m->HD, QD = m->NH * m->HD;
+    d->kv = (float*)calloc((size_t)m->L * 2 * m->MS * KV, sizeof(float));
+    d->x = (float*)calloc(m->D, 4);
+    d->xn = (float*)calloc(m->H > m->D ? m->H : m->D, 4);
+    d->q = (float*)calloc(QD, 4);
+    d->k = (float*)calloc(KV, 4);
+    d->v = (float*)calloc(KV, 4);
+    d->att = (float*)calloc(QD, 4);
+    d->o = (float*)calloc(m->D, 4);
+    d->g = (float*)calloc(m->H, 4);
+    d->u = (float*)calloc(m->H, 4);
+    d->dn = (float*)calloc(m->D, 4);
+    d->sc = (float*)calloc(m->MS, 4);
+    d->logits = (float*)calloc(m->V, 4);
+    if (!d->kv || !d->x || !d->xn || !d->q || !d->k || !d->v || !d->att || !d->o || !d->g || !d->u || !d->dn ||
+        !d->sc || !d->logits) {
+        orc_cpu_decoder_destroy(d);
+        return NULL;
+    }
+    return d;
+}
+
+void orc_cpu_decoder_destroy(void* p) {
+    cpu_dec_t* d = (cpu_dec_t*)p;
+    if (!d) return;
+    free(d->kv); free(d->x); free(d->xn); free(d->q); free(d->k); free(d->v); free(d->att);
+    free(d->o); free(d->g); free(d->u); free(d->dn); free(d->sc); free(d->logits);
+    free(d);
+}
+
+/* One token at position pos; returns the greedy pick (first maximum) or -1. */
+int orc_cpu_decoder_step(void* p, int token, int pos, float* logits_out) {
+    cpu_dec_t* d = (cpu_dec_t*)p;
+    const orc_model_t* m = &d->m;
+    const int D = m->D, H = m->H, NH = m->NH, NKV = m->NKV, HD = m->HD, V = m->V, MS = m->MS;
+    const int KV = NKV * HD, QD = NH * HD, kv_mul = NH / NKV, nt = d->nt;
+    const size_t bD = (size_t)(D / 32) * 36, bH = (size_t)(H / 32) * 36, bQ = (size_t)(QD / 32) * 36;
+    if (token < 0 || token >= V || pos < 0 || pos >= MS) return -1;
+    memcpy(d->x, m->emb + (size_t)token * D, (size_t)D * 4);
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int l = 0; l < m->L; l++) {
+        cpu_rmsnorm(d->x, m->ln1 + (size_t)l * D, d->xn, D, m->eps);
+        cpu_mv(m->wq + (size_t)l * QD * bD, d->xn, d->q, D, QD, nt);
+        cpu_mv(m->wk + (size_t)l * KV * bD, d->xn, d->k, D, KV, nt);
+        cpu_mv(m->wv + (size_t)l * KV * bD, d->xn, d->v, D, KV, nt);
+        for (int i = 0; i < HD / 2; i++) {
+            const float ang = (float)pos * (1.0f / powf(m->theta, (float)(2 * i) / (float)HD));
+            const float c = cosf(ang), s = sinf(ang);
+            for (int h = 0; h < NH; h++) {
+                float* qh = d->q + h * HD;
+                const float a0 = qh[i], a1 = qh[i + HD / 2];
+                qh[i] = a0 * c - a1 * s;
+                qh[i + HD / 2] = a0 * s + a1 * c;
+            }
+            for (int h = 0; h < NKV; h++) {
+                float* kh = d->k + h * HD;
+                const float b0 = kh[i], b1 = kh[i + HD / 2];
+                kh[i] = b0 * c - b1 * s;
+                kh[i + HD / 2] = b0 * s + b1 * c;
+            }
+        }
+        float* kc = d->kv + (size_t)l * 2 * MS * KV;
+        float* vc = kc + (size_t)MS * KV;
+        memcpy(kc + (size_t)pos * KV, d->k, (size_t)KV * 4);
+        memcpy(vc + (size_t)pos * KV, d->v, (size_t)KV * 4);
+        const int S = pos + 1;
+        for (int h = 0; h < NH; h++) {
+            const int kh = h / kv_mul;
+            const float* qh = d->q + h * HD;
+            float mx = -INFINITY;
+            for (int t = 0; t < S; t++) {
+                const float* kr = kc + (size_t)t * KV + kh * HD;
+                float sd = 0.0f;
+                for (int i = 0; i < HD; i++) sd += qh[i] * kr[i];
+                d->sc[t] = sd * scale;
+                mx = d->sc[t] > mx ? d->sc[t] : mx;
+            }
+            float den = 0.0f;
+            for (int t = 0; t < S; t++) {
+                d->sc[t] = expf(d->sc[t] - mx);
+                den += d->sc[t];
+            }
+            float* ah = d->att + h * HD;
+            for (int i = 0; i < HD; i++) ah[i] = 0.0f;
+            for (int t = 0; t < S; t++) {
+                const float* vr = vc + (size_t)t * KV + kh * HD;
+                const float wgt = d->sc[t] / den;
+                for (int i = 0; i < HD; i++) ah[i] += wgt * vr[i];
+            }
+        }
+        cpu_mv(m->wo + (size_t)l * D * bQ, d->att, d->o, QD, D, nt);
+        for (int j = 0; j < D; j++) d->x[j] += d->o[j];
+        cpu_rmsnorm(d->x, m->ln2 + (size_t)l * D, d->xn, D, m->eps);
+        cpu_mv(m->wg + (size_t)l * H * bD, d->xn, d->g, D, H, nt);
+        cpu_mv(m->wu + (size_t)l * H * bD, d->xn, d->u, D, H, nt);
+        for (int j = 0; j < H; j++) d->g[j] = d->g[j] / (1.0f + expf(-d->g[j])) * d->u[j];
+        cpu_mv(m->wd + (size_t)l * D * bH, d->g, d->dn, H, D, nt);
+        for (int j = 0; j < D; j++) d->x[j] += d->dn[j];
+    }
+    cpu_rmsnorm(d->x, m->lnf, d->xn, D, m->eps);
+    const float* hw = m->head_f32 ? m->head_f32 : m->emb;
+#pragma omp parallel num_threads(nt)
+    {
+        int t = omp_get_thread_num(), n = omp_get_num_threads();
+        head_rows(hw, d->xn, d->logits, D, (int)((long)V * t / n), (int)((long)V * (t + 1) / n));
+    }
+    int best = 0;
+    for (int i = 1; i < V; i++)
+        if (d->logits[i] > d->logits[best]) best = i;
+    if (logits_out) memcpy(logits_out, d->logits, (size_t)V * 4);
+    return best;
+}

@@ -117,6 +117,24 @@ static float rope_freq(float theta, int i, int HD) {
     return 1.0f / powf(theta, (float)(2 * i) / (float)HD);
 }
 
+/* Rotate-half RoPE of nheads heads of HD floats at position pos (reference
+ * forward.metal:1260-1263 frequencies, :1302-1310 rotation): element i of a
+ * head pairs with element i + HD/2, angle pos * theta^(-2i/HD) taken in
+ * fp32, cos/sin of that angle. */
+void orc_rope(float* v, int nheads, int HD, int pos, float theta) {
+    for (int i = 0; i < HD / 2; i++) {
+        float fr = rope_freq(theta, i, HD);
+        float ang = (float)pos * fr;
+        float c = (float)cos((double)ang), s = (float)sin((double)ang);
+        for (int h = 0; h < nheads; h++) {
+            float* vh = v + h * HD;
+            float a0 = vh[i], a1 = vh[i + HD / 2];
+            vh[i] = a0 * c - a1 * s;
+            vh[i + HD / 2] = a0 * s + a1 * c;
+        }
+    }
+}
+
 orc_decoder_t* orc_decoder_create(const orc_model_t* m, int nthreads) {
     orc_decoder_t* d = (orc_decoder_t*)calloc(1, sizeof(orc_decoder_t));
     if (!d) return NULL;
@@ -167,23 +185,8 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
         proj_mv(m, m->wk + (size_t)l * KV * nbD * bb, d->xn, d->k, D, KV, nt);
         proj_mv(m, m->wv + (size_t)l * KV * nbD * bb, d->xn, d->v, D, KV, nt);
 
-        for (int i = 0; i < HD / 2; i++) {
-            float fr = rope_freq(m->theta, i, HD);
-            float ang = (float)pos * fr;
-            float c = (float)cos((double)ang), s = (float)sin((double)ang);
-            for (int h = 0; h < NH; h++) {
-                float* qh = d->q + h * HD;
-                float a0 = qh[i], a1 = qh[i + HD / 2];
-                qh[i] = a0 * c - a1 * s;
-                qh[i + HD / 2] = a0 * s + a1 * c;
-                if (h < NKV) {
-                    float* kh = d->k + h * HD;
-                    float b0 = kh[i], b1 = kh[i + HD / 2];
-                    kh[i] = b0 * c - b1 * s;
-                    kh[i + HD / 2] = b0 * s + b1 * c;
-                }
-            }
-        }
+        orc_rope(d->q, NH, HD, pos, m->theta);
+        orc_rope(d->k, NKV, HD, pos, m->theta);
 
         float* kc = d->kv + (size_t)l * 2 * MS * KV;
         float* vc = kc + (size_t)MS * KV;
@@ -240,6 +243,12 @@ int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits) {
         f32_mv(m->head_f32 ? m->head_f32 : m->emb, d->xn, logits, D, V, nt);
     }
     return 0;
+}
+
+/* The attention output (NH*HD floats, before the o projection) of the last
+ * layer of the last step; for tests that look inside the step. */
+void orc_decoder_last_attention(const orc_decoder_t* d, float* out) {
+    memcpy(out, d->att, (size_t)d->m.NH * d->m.HD * sizeof(float));
 }
 
 int orc_argmax_first(const double* v, int n, double* top1, double* top2) {

@@ -38,6 +38,10 @@ void orc_decoder_destroy(orc_decoder_t* d);
 /* One token at position pos; writes V logits.  Returns 0 or -1. */
 int orc_decoder_step(orc_decoder_t* d, int token, int pos, double* logits);
 int orc_argmax_first(const double* v, int n, double* top1, double* top2);
+/* Rotate-half RoPE in place (the step's own), and the last layer's attention
+ * output of the last step (NH*HD floats). */
+void orc_rope(float* v, int nheads, int HD, int pos, float theta);
+void orc_decoder_last_attention(const orc_decoder_t* d, float* out);
 /* Greedy run in the reference's driver order (tools/run.c:121-185): step
  * prompt tokens, then the previous pick (or forced[] when non-NULL, for
  * teacher forcing).  Emits steps-n_prompt+1 tokens and their top-2 margins;

@@ -28,5 +28,10 @@ void     orc_cpu_q8_matvec_multi(const uint8_t* w, const float* x, float* y, int
                                  int nthreads);
 int      orc_cpu_max_threads(void);
 const char* orc_cpu_isa(void);
+/* fp32 SIMD decoder (config-5 CPU baseline, cpu_baseline.c); m is an
+ * orc_model_t (decode_oracle.h) with Q8 projections and an fp32 head. */
+void*    orc_cpu_decoder_create(const void* m, int nthreads);
+void     orc_cpu_decoder_destroy(void* d);
+int      orc_cpu_decoder_step(void* d, int token, int pos, float* logits_out);
 
 #endif

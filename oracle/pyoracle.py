@@ -1,5 +1,6 @@
 # SPDX-License-Identifier: MPL-2.0
-"""ctypes binding of oracle/liboracle.so and oracle/_ref/libref_quant.so.
+"""ctypes binding of oracle/liboracle.so and of the reference's own quant.c
+and sampler.c built into oracle/_ref/ (libref_quant.so, libref_sampler.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
 bench.py's cpu_baseline leg, as the checker or the timed CPU baseline.
@@ -58,8 +59,22 @@ def oracle() -> C.CDLL:
         L.orc_argmax_first.argtypes = [vp, i, vp, vp]
         L.orc_generate.restype = i
         L.orc_generate.argtypes = [vp, vp, i, i, vp, vp, vp]
+        L.orc_rope.argtypes = [vp, i, i, i, C.c_float]
+        L.orc_decoder_last_attention.argtypes = [vp, vp]
+        L.orc_cpu_decoder_create.restype = vp
+        L.orc_cpu_decoder_create.argtypes = [vp, i]
+        L.orc_cpu_decoder_destroy.argtypes = [vp]
+        L.orc_cpu_decoder_step.restype = i
+        L.orc_cpu_decoder_step.argtypes = [vp, i, i, vp]
         _o = L
     return _o
+
+
+def rope(v: np.ndarray, nheads: int, HD: int, pos: int, theta: float) -> np.ndarray:
+    """The decode oracle's rotate-half RoPE applied to a copy of v."""
+    out = np.ascontiguousarray(v, dtype=np.float32).copy()
+    oracle().orc_rope(_p(out), nheads, HD, pos, theta)
+    return out
 
 
 def ref_quant():
@@ -79,6 +94,41 @@ def ref_quant():
         L.bmt_quantize_q4_bf16.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
         _r = L
     return _r
+
+
+REF_SAMPLER_PATH = os.path.join(HERE, "_ref", "libref_sampler.so")
+_rs = None
+
+
+class RefSamplerState(C.Structure):
+    """struct bm_sampler_s as the reference lays it out (src/baremetal/sampler.h:14-21)."""
+    _fields_ = [("vocab_size", C.c_int), ("temperature", C.c_float), ("topp", C.c_float), ("top_k", C.c_int),
+                ("rng_state", C.c_uint), ("probs", C.c_void_p)]
+
+
+def ref_sampler():
+    """The reference's own sampler.c built by oracle/Makefile (None if absent)."""
+    global _rs
+    if _rs is None:
+        if not os.path.exists(REF_SAMPLER_PATH):
+            return None
+        L = C.CDLL(REF_SAMPLER_PATH)
+        L.bm_sample.restype = C.c_int
+        L.bm_sample.argtypes = [C.c_void_p, C.c_void_p]
+        _rs = L
+    return _rs
+
+
+def ref_sample_sequence(logits: np.ndarray, temp: float, topp: float, top_k: int, state: int, draws: int):
+    """draws calls of the reference's bm_sample on one logits vector, the
+    state chained as bm_sample chains it; None if the library is absent."""
+    L = ref_sampler()
+    if L is None:
+        return None
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    probs = np.zeros(lg.size, dtype=np.float32)
+    st = RefSamplerState(lg.size, temp, topp, top_k, state & 0xFFFFFFFF, probs.ctypes.data)
+    return np.array([L.bm_sample(C.byref(st), _p(lg)) for _ in range(draws)], dtype=np.int32)
 
 
 # ---------------------------------------------------------------- helpers
@@ -216,9 +266,11 @@ class OrcModel(C.Structure):
 
 
 class Decoder:
-    """Keeps the numpy arrays alive for as long as the C decoder uses them."""
+    """Keeps the numpy arrays alive for as long as the C decoder uses them.
+    fast=True: the fp32 SIMD decoder of cpu_baseline.c (the timed CPU
+    baseline; step() then returns float32 logits), else the fp64 checker."""
 
-    def __init__(self, dims: dict, arrays: dict, nthreads: int = 8):
+    def __init__(self, dims: dict, arrays: dict, nthreads: int = 8, fast: bool = False):
         self._keep = dict(arrays)
         m = OrcModel()
         for k in ("D", "H", "NH", "NKV", "HD", "L", "V", "MS"):
@@ -231,14 +283,30 @@ class Decoder:
             setattr(m, k, a.ctypes.data if a is not None else None)
         self._m = m
         self.V = int(dims["V"])
-        self.h = oracle().orc_decoder_create(C.byref(m), nthreads)
+        self.fast = fast
+        if fast:
+            self.h = oracle().orc_cpu_decoder_create(C.byref(m), nthreads)
+        else:
+            self.h = oracle().orc_decoder_create(C.byref(m), nthreads)
         if not self.h:
-            raise MemoryError("orc_decoder_create failed")
+            raise MemoryError("decoder create failed")
 
     def step(self, token: int, pos: int) -> np.ndarray:
+        if self.fast:
+            out = np.zeros(self.V, dtype=np.float32)
+            if oracle().orc_cpu_decoder_step(self.h, token, pos, _p(out)) < 0:
+                raise ValueError("orc_cpu_decoder_step rejected its input")
+            return out
         out = np.zeros(self.V, dtype=np.float64)
         if oracle().orc_decoder_step(self.h, token, pos, _p(out)) != 0:
             raise ValueError("orc_decoder_step rejected its input")
+        return out
+
+    def last_attention(self) -> np.ndarray:
+        """The last layer's attention output of the last step (fp64 checker only)."""
+        assert not self.fast
+        out = np.zeros(int(self._m.NH) * int(self._m.HD), dtype=np.float32)
+        oracle().orc_decoder_last_attention(self.h, _p(out))
         return out
 
     def generate(self, prompt, steps: int, forced=None):
@@ -257,7 +325,10 @@ class Decoder:
 
     def close(self):
         if self.h:
-            oracle().orc_decoder_destroy(self.h)
+            if self.fast:
+                oracle().orc_cpu_decoder_destroy(self.h)
+            else:
+                oracle().orc_decoder_destroy(self.h)
             self.h = None
 
     def __del__(self):

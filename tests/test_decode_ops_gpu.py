@@ -325,3 +325,32 @@ def test_argmax_first_index(be):
         v = rng.standard_normal(49152).astype(np.float32)
         assert be.dispatch("argmax_f32", [be.upload(v), out, be.params(v.size)], (1024,), (1024,)) == 0
         assert out.read(np.int32)[0] == int(np.argmax(v))
+
+
+def _reference_scan(v):
+    """The reference's greedy pick (tools/run.c:56-60): best = 0, move on a strictly larger value."""
+    best = 0
+    for i in range(1, len(v)):
+        if v[i] > v[best]:
+            best = i
+    return best
+
+
+def test_argmax_nan_and_signed_zero(be):
+    """NaN never wins unless it sits at index 0 (where the scan never leaves
+    it), and -0 equals +0 (the first one wins)."""
+    nan, inf = np.nan, np.inf
+    cases = [[nan, 5, 7], [1, nan, 7, nan], [-0.0, 0.0, -1], [-1, -0.0, 0.0], [nan] * 5, [-inf, nan, -inf],
+             [3, nan, 3], [0.0, -0.0]]
+    rng = np.random.default_rng(9)
+    big = rng.standard_normal(5000).astype(np.float32)
+    big[rng.integers(0, 5000, 40)] = nan
+    cases.append(big)
+    big2 = big.copy()
+    big2[0] = nan
+    cases.append(big2)
+    out = be.alloc(4)
+    for c in cases:
+        v = np.array(c, np.float32)
+        assert be.dispatch("argmax_f32", [be.upload(v), out, be.params(v.size)], (1024,), (1024,)) == 0
+        assert out.read(np.int32)[0] == _reference_scan(v), c if len(c) < 10 else "random"

@@ -132,3 +132,100 @@ def test_step_rejects_bad_token_or_position(bad):
     dec = oracle_decoder(TINY, weights(TINY), 16)
     with pytest.raises(ValueError):
         dec.step(*bad)
+
+
+# ------------------------------------------------------------------ GQA head map and RoPE, pinned
+
+GQA = dict(D=64, H=128, NH=4, NKV=2, HD=16, L=1, V=256)
+
+
+@pytest.mark.parametrize("dead", [0, 1])
+def test_gqa_query_heads_share_their_kv_head(dead):
+    """NH = 4 query heads over NKV = 2 KV heads (kv_mul = 2): query head h
+    reads KV head h / kv_mul (reference forward.metal:1381).  With KV head
+    `dead`'s v rows zero, exactly query heads 2*dead and 2*dead+1 lose their
+    attention output at every position; the other two keep theirs.  The map
+    h % NKV would silence heads dead and dead+2 instead."""
+    HD = GQA["HD"]
+    w = weights(GQA, seed=5)
+    wv = w["wv"].reshape(GQA["NKV"] * HD, GQA["D"])
+    wv[dead * HD:(dead + 1) * HD] = 0.0
+    w["wv"] = wv.ravel()
+    dec = oracle_decoder(GQA, w, 8)
+    for pos, tok in enumerate([3, 90, 17, 200]):
+        dec.step(tok, pos)
+        att = dec.last_attention().reshape(GQA["NH"], HD)
+        for h in range(GQA["NH"]):
+            silent = h // 2 == dead
+            assert (np.abs(att[h]).max() == 0.0) == silent, (pos, h, att[h])
+
+
+def test_rope_pairs_element_i_with_i_plus_half():
+    """Unit vector e_0 at position p: frequency theta^0 = 1, so the angle is p
+    and the vector becomes cos(p) e_0 + sin(p) e_{HD/2} (rotate-half pairing,
+    reference forward.metal:1302-1310); e_{HD/2} becomes -sin(p) e_0 +
+    cos(p) e_{HD/2}.  Interleaved pairs (2i, 2i+1) would move e_0 into e_1."""
+    HD = 64
+    for p in (1, 2, 5, 31):
+        e0 = np.zeros(HD, np.float32)
+        e0[0] = 1.0
+        r = po.rope(e0, 1, HD, p, 10000.0)
+        want = np.zeros(HD)
+        want[0], want[HD // 2] = np.cos(p), np.sin(p)
+        np.testing.assert_allclose(r, want, atol=2e-7)
+        eh = np.zeros(HD, np.float32)
+        eh[HD // 2] = 1.0
+        r = po.rope(eh, 1, HD, p, 10000.0)
+        want = np.zeros(HD)
+        want[0], want[HD // 2] = -np.sin(p), np.cos(p)
+        np.testing.assert_allclose(r, want, atol=2e-7)
+
+
+def test_rope_frequency_exponent():
+    """Pair i turns by pos * theta^(-2i/HD) (reference forward.metal:1261-1263).
+    At i = HD/4 that is theta^(-1/2) = 1/100 for theta = 10^4, so position 100
+    turns pair HD/4 by 1 radian; an exponent of i/HD would give 10 radians.
+    Theta 4 and i = HD/4: frequency 1/2, position 2 turns by 1 radian too."""
+    HD = 64
+    i = HD // 4
+    for theta, pos in ((10000.0, 100), (4.0, 2)):
+        e = np.zeros(HD, np.float32)
+        e[i] = 1.0
+        r = po.rope(e, 1, HD, pos, theta)
+        assert abs(r[i] - np.cos(1.0)) < 2e-6 and abs(r[i + HD // 2] - np.sin(1.0)) < 2e-6, (theta, r[i])
+        assert np.abs(np.delete(r, [i, i + HD // 2])).max() == 0.0
+
+
+def test_rope_is_relative_and_identity_at_zero():
+    """q(m).k(n) = q(m+d).k(n+d) for every head (a rotation by position), and
+    position 0 leaves vectors unchanged; checked on random heads in fp64 of
+    the fp32 results (rounding of the fp32 angle grows with the position)."""
+    rng = np.random.default_rng(4)
+    HD, NH = 64, 3
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    k = rng.standard_normal(NH * HD).astype(np.float32)
+    assert np.array_equal(po.rope(q, NH, HD, 0, 10000.0), q)
+    for m, n, dlt in ((5, 2, 7), (40, 3, 11), (0, 9, 100)):
+        a = po.rope(q, NH, HD, m, 10000.0).reshape(NH, HD).astype(np.float64)
+        b = po.rope(k, NH, HD, n, 10000.0).reshape(NH, HD).astype(np.float64)
+        c = po.rope(q, NH, HD, m + dlt, 10000.0).reshape(NH, HD).astype(np.float64)
+        d = po.rope(k, NH, HD, n + dlt, 10000.0).reshape(NH, HD).astype(np.float64)
+        np.testing.assert_allclose((a * b).sum(1), (c * d).sum(1), rtol=0, atol=2e-4)
+        # and it is not trivially constant: the score does change with the offset m - n
+        e = po.rope(k, NH, HD, n + 1, 10000.0).reshape(NH, HD).astype(np.float64)
+        assert np.abs((a * b).sum(1) - (a * e).sum(1)).max() > 1e-2
+
+
+def test_cpu_decoder_matches_oracle():
+    """The fp32 SIMD decoder (the timed CPU baseline of the config-5 leg)
+    against the fp64 checker: logits within 1e-5 normwise, same argmax."""
+    dims = dict(D=128, H=256, NH=4, NKV=2, HD=32, L=2, V=1000)
+    w = weights(dims, seed=6)
+    from decode_util import q8_arrays
+    arrs = q8_arrays(w)
+    slow = po.Decoder(dict(dims, MS=32), arrs, nthreads=4)
+    fast = po.Decoder(dict(dims, MS=32), arrs, nthreads=4, fast=True)
+    for pos, tok in enumerate([5, 700, 3, 999, 42, 42]):
+        a, b = slow.step(tok, pos), fast.step(tok, pos)
+        assert np.abs(a - b).max() / np.abs(a).max() <= 1e-5
+        assert int(np.argmax(a)) == int(np.argmax(b))

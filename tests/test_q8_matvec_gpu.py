@@ -231,3 +231,65 @@ def test_matvec_multi_batched_rejects(be):
     p2, _ = bmhip.mv_plan([0], [2], [0], [OC], [C], bt=BT)
     assert be.dispatch(k, [be.params(1, nt, BT), be.upload(p2), W, X2, Y], (nt * 256,), (256,)) == -1
     assert not Y.read(np.float32).any()
+
+
+def _split2_rne(x):
+    """What a two-term bf16 split (round to nearest even) keeps of x: used to
+    show the exact-split test below would catch a split that drops bits."""
+    def bf16(v):
+        u = v.astype(np.float32).view(np.uint32).astype(np.uint64)
+        r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+        return r.astype(np.uint32).view(np.float32)
+    h = bf16(x)
+    return h.astype(np.float64) + bf16((x - h).astype(np.float32)).astype(np.float64)
+
+
+@pytest.mark.parametrize("BT", [3, 8])
+def test_matvec_multi_batched_exact_split_bitwise(be, BT):
+    """Activations with 18 significant bits (beyond what two bf16 terms carry),
+    codes in {-1, 0, 1}, power-of-two scales: every product and partial sum is
+    exact in fp32, so the batched launch must equal the fp64 oracle bit for
+    bit.  The same inputs through a two-term split would not."""
+    rng = np.random.default_rng(90 + BT)
+    OC, C = 130, 32
+    blk = np.zeros((OC, 36), np.uint8)
+    blk[:, :4] = (2.0 ** rng.integers(-4, 1, OC)).astype(np.float32).view(np.uint8).reshape(-1, 4)
+    blk[:, 4:] = rng.integers(-1, 2, (OC, 32)).astype(np.int8).view(np.uint8)
+    w = blk.ravel()
+    k = rng.integers(1 << 17, 1 << 18, BT * C) * rng.choice([-1, 1], BT * C)
+    x = (k.astype(np.float64) * 2.0 ** -16).astype(np.float32)
+    r = po.q8_matvec_f64(w, x, BT, C, OC)
+    r2 = po.q8_matvec_f64(w, _split2_rne(x).astype(np.float32), BT, C, OC)
+    assert not np.array_equal(r, r2)  # the inputs need the third term
+    plan, n_tiles = bmhip.mv_plan([0], [0], [0], [OC], [C], bt=BT)
+    Y = be.alloc(4 * BT * OC)
+    rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(1, n_tiles, BT), be.upload(plan), be.upload(w),
+                                                     be.upload(x), Y], (n_tiles * 256,), (256,))
+    assert rc == 0
+    assert np.array_equal(Y.read(np.float32).astype(np.float64), r)
+
+
+def test_matvec_multi_batched_nonfinite(be):
+    """A +Inf, a -Inf and a NaN activation, and large finite ones: the batched
+    launch gives NaN / +-Inf / finite where the fp32 products of the reference
+    do (Inf * 0 = NaN, Inf * q = +-Inf), and matches the oracle elsewhere."""
+    BT, OC, C = 4, 64, 64
+    w = po.quantize_q8(bmhip.synth_normal(95, 0.02, OC * C))
+    x = bmhip.synth_normal(96, 1.0, BT * C).reshape(BT, C)
+    x[0, 5] = np.inf
+    x[1, 40] = -np.inf
+    x[2, 7] = np.nan
+    x[3, :] *= 1e30
+    x = x.ravel()
+    plan, n_tiles = bmhip.mv_plan([0], [0], [0], [OC], [C], bt=BT)
+    Y = be.alloc(4 * BT * OC)
+    rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(1, n_tiles, BT), be.upload(plan), be.upload(w),
+                                                     be.upload(x), Y], (n_tiles * 256,), (256,))
+    assert rc == 0
+    y = Y.read(np.float32).reshape(BT, OC)
+    with np.errstate(invalid="ignore"):
+        r = po.q8_matvec_f64(w, x, BT, C, OC).reshape(BT, OC)
+    bad = np.argwhere(np.isnan(y) != np.isnan(r))
+    assert bad.size == 0, [(int(b), int(n), float(y[b, n]), float(r[b, n])) for b, n in bad[:12]]
+    assert np.array_equal(np.isposinf(y), np.isposinf(r)) and np.array_equal(np.isneginf(y), np.isneginf(r))
+    assert normwise(y[3], r[3]) <= RTOL
