@@ -79,6 +79,7 @@ def lib() -> C.CDLL:
         "bm_step": (C.POINTER(C.c_float), [vp, i]),
         "bm_step_batch": (C.POINTER(C.c_float), [vp, vp]),
         "bm_forward": (C.POINTER(C.c_float), [vp, vp, i]),
+        "bm_forward_noalloc": (C.POINTER(C.c_float), [vp, vp, i]),
         "bm_reset_session": (None, [vp]),
         "bm_destroy_session": (None, [vp]),
         "bm_profile_begin": (None, [vp]),
@@ -454,6 +455,15 @@ class Engine:
         p = lib().bm_forward(self.sess, _ptr(t), int(t.size))
         if not p:
             raise BackendError("bm_forward failed")
+        return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
+
+    def forward_noalloc(self, tokens):
+        """bm_forward_noalloc: the one-pass prefill with its workspace in the
+        library's static per-GPU array; None when the call is rejected."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        p = lib().bm_forward_noalloc(self.sess, _ptr(t), int(t.size))
+        if not p:
+            return None
         return np.ctypeslib.as_array(p, shape=(self.V,)).copy()
 
     def step_batch(self, tokens) -> np.ndarray:

@@ -794,6 +794,22 @@ struct PfGemm {
     int nprob, n_tiles, ks; /* ks: K slices, each writing its own copy of C */
 };
 
+/* The prefill's workspace: the residual stream, the split-K copies of each
+ * GEMM output, the attention output, bf16 activations, tokens and GEMM plans
+ * on the device, and the plans' host staging.  bm_forward keeps it in
+ * session buffers allocated on the first prefill; bm_forward_noalloc carves
+ * it from the library's static per-GPU array. */
+struct PfWork {
+    float *x, *qkv, *att, *o, *gu;
+    unsigned short* a16;
+    int* tok;
+    unsigned char* plan;   /* device plans */
+    unsigned char* h_plan; /* host staging of the plans */
+    size_t plan_cap;       /* bytes of plan and h_plan */
+};
+
+#define PF_MAX_LAYERS 256
+
 /* Prefill GEMM launches with fewer C tiles than this are split along K (at
  * most GM_KSPLIT_MAX slices): a per-layer launch at prompt lengths of a few
  * hundred tokens has tens of 128x128 tiles, and a tile's K loop takes about
@@ -804,7 +820,7 @@ struct PfGemm {
 
 /* Sizes (g == NULL) or appends the plan of one multi-GEMM launch to the
  * staging buffer; kmax = 1 keeps the launch whole. */
-static int pf_plan(bm_session_t* S, size_t* used, PfGemm* g, int nprob, const uint64_t* a_off, const uint64_t* w_off,
+static int pf_plan(const PfWork* w, size_t* used, PfGemm* g, int nprob, const uint64_t* a_off, const uint64_t* w_off,
                    const uint64_t* c_off, const int* M, const int* N, const int* K, const int* lda, const int* ldc,
                    int kmax) {
     int nt = 0, ks = 1;
@@ -813,8 +829,8 @@ static int pf_plan(bm_session_t* S, size_t* used, PfGemm* g, int nprob, const ui
     if (need < 0) return -1;
     const size_t at = (*used + 7) & ~(size_t)7;
     if (g) {
-        if (at + (size_t)need > S->pf_plan_cap) return -1;
-        if (gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, S->h_plan + at,
+        if (at + (size_t)need > w->plan_cap) return -1;
+        if (gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, w->h_plan + at,
                           (size_t)need, &nt, &ks) != need)
             return -1;
         g->off = at;
@@ -826,60 +842,62 @@ static int pf_plan(bm_session_t* S, size_t* used, PfGemm* g, int nprob, const ui
     return 0;
 }
 
-static int prefill(bm_session_t* S, const int* tokens, int n) {
-    bm_model_t* m = S->m;
-    hipStream_t s = S->ctx->s;
+/* Device bytes of the workspace for n tokens, and each part's offset (in
+ * bytes, 256-aligned) when off != NULL: x, qkv, att, o, gu, a16, tok. */
+static size_t pf_work_layout(const bm_model_t* m, int n, size_t off[7]) {
+    const size_t N = (size_t)n;
+    const size_t widest = (size_t)std::max(std::max(m->D, m->H), m->QD);
+    const size_t sz[7] = {N * m->D * 4, GM_KSPLIT_MAX * N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4,
+                          GM_KSPLIT_MAX * N * m->D * 4, GM_KSPLIT_MAX * N * 2 * (size_t)m->H * 4, N * widest * 2,
+                          N * 4};
+    size_t at = 0;
+    for (int i = 0; i < 7; i++) {
+        if (off) off[i] = at;
+        at += (sz[i] + 255) & ~(size_t)255;
+    }
+    return at;
+}
+
+/* The GEMM plans of the whole prefill, per layer q/k/v, o, gate/up, down:
+ * with g == NULL only sized (*used), else written to w->h_plan. */
+static int pf_plans(const bm_model_t* m, const PfWork* w, int n, PfGemm* g, size_t* used) {
     const int D = m->D, H = m->H, QD = m->QD, KV = m->KV, L = m->L;
-    const float eps = 1e-5f; /* reference graph.c:134,175,219 */
-    for (int i = 0; i < n; i++)
-        if (tokens[i] < 0 || tokens[i] >= m->V) {
-            BMK_ERR("bm_forward: token %d outside [0, %d)", tokens[i], m->V);
-            return -1;
-        }
-    if (prefill_buffers(S, n)) return -1;
-    /* GEMM plans, per layer: q/k/v, o, gate/up, down; a first pass sizes
-     * the plan buffer and the split-K workspace, the second fills them */
-    std::vector<PfGemm> g((size_t)4 * L);
     const uint64_t nn = (uint64_t)n;
     /* q/k/v stay whole when the attention cannot read split copies (head size other than 64) */
     const int kq = m->HD == 64 ? GM_KSPLIT_MAX : 1;
-    auto plans = [&](bool fill, size_t* used) -> int {
-        *used = 0;
-        for (int l = 0; l < L; l++) {
-            const uint64_t lw = (uint64_t)l * m->layer_bytes;
-            {
-                const uint64_t a[3] = {0, 0, 0}, w[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
-                const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
-                const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
-                if (pf_plan(S, used, fill ? &g[4 * l + 0] : NULL, 3, a, w, c, M, N, K, lda, N, kq)) return -1;
-            }
-            {
-                const uint64_t a = 0, w = lw + m->off[3], c = 0;
-                const int M = n, N = D, K = QD;
-                if (pf_plan(S, used, fill ? &g[4 * l + 1] : NULL, 1, &a, &w, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
-                    return -1;
-            }
-            {
-                const uint64_t a[2] = {0, 0}, w[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
-                const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
-                if (pf_plan(S, used, fill ? &g[4 * l + 2] : NULL, 2, a, w, c, M, N, K, K, N, GM_KSPLIT_MAX)) return -1;
-            }
-            {
-                const uint64_t a = 0, w = lw + m->off[6], c = 0;
-                const int M = n, N = D, K = H;
-                if (pf_plan(S, used, fill ? &g[4 * l + 3] : NULL, 1, &a, &w, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
-                    return -1;
-            }
+    *used = 0;
+    for (int l = 0; l < L; l++) {
+        const uint64_t lw = (uint64_t)l * m->layer_bytes;
+        {
+            const uint64_t a[3] = {0, 0, 0}, wo[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
+            const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
+            const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
+            if (pf_plan(w, used, g ? &g[4 * l + 0] : NULL, 3, a, wo, c, M, N, K, lda, N, kq)) return -1;
         }
-        return 0;
-    };
-    size_t used = 0;
-    if (plans(false, &used)) {
-        BMK_ERR("bm_forward: prefill GEMM plans rejected (%d tokens)", n);
-        return -1;
+        {
+            const uint64_t a = 0, wo = lw + m->off[3], c = 0;
+            const int M = n, N = D, K = QD;
+            if (pf_plan(w, used, g ? &g[4 * l + 1] : NULL, 1, &a, &wo, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
+                return -1;
+        }
+        {
+            const uint64_t a[2] = {0, 0}, wo[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
+            const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
+            if (pf_plan(w, used, g ? &g[4 * l + 2] : NULL, 2, a, wo, c, M, N, K, K, N, GM_KSPLIT_MAX)) return -1;
+        }
+        {
+            const uint64_t a = 0, wo = lw + m->off[6], c = 0;
+            const int M = n, N = D, K = H;
+            if (pf_plan(w, used, g ? &g[4 * l + 3] : NULL, 1, &a, &wo, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
+                return -1;
+        }
     }
-    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
-    const size_t plan_bytes = used + 64;
+    return 0;
+}
+
+/* bm_forward's workspace: session buffers, grown to n tokens and plan_bytes. */
+static int pf_session_work(bm_session_t* S, int n, size_t plan_bytes, PfWork* w) {
+    if (prefill_buffers(S, n)) return -1;
     if (S->pf_plan_cap < plan_bytes) {
         hipFree(S->pf_plan);
         if (S->h_plan) hipHostFree(S->h_plan);
@@ -894,15 +912,76 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
         }
         S->pf_plan_cap = plan_bytes;
     }
-    if (plans(true, &used)) return -1;
+    w->x = S->pf_x; w->qkv = S->pf_qkv; w->att = S->pf_att; w->o = S->pf_o; w->gu = S->pf_gu;
+    w->a16 = S->pf_a16; w->tok = S->pf_tok;
+    w->plan = S->pf_plan; w->h_plan = S->h_plan; w->plan_cap = S->pf_plan_cap;
+    return 0;
+}
+
+extern "C" void* bmk_noalloc_scratch(int device);
+
+/* Host staging of bm_forward_noalloc's plans (static: no allocation at call
+ * time; shared by all calls, which must not overlap). */
+#define PF_NOALLOC_PLAN_BYTES (1u << 20)
+alignas(64) static unsigned char s_noalloc_h_plan[PF_NOALLOC_PLAN_BYTES];
+
+/* bm_forward_noalloc's workspace: carved from the GPU's static array, the
+ * plans last; -1 (logged) when n tokens do not fit. */
+static int pf_noalloc_work(bm_session_t* S, int n, size_t plan_bytes, PfWork* w) {
+    const int dev = (int)(intptr_t)S->ctx->be->device;
+    unsigned char* base = (unsigned char*)bmk_noalloc_scratch(dev);
+    if (!base) return -1;
+    size_t off[7];
+    const size_t act = pf_work_layout(S->m, n, off);
+    if (plan_bytes > PF_NOALLOC_PLAN_BYTES || act + plan_bytes > BM_NOALLOC_SCRATCH_BYTES) {
+        BMK_ERR("bm_forward_noalloc: %d tokens need %zu workspace bytes (+%zu of plans), the static array holds %u "
+                "(plans at most %u)",
+                n, act, plan_bytes, (unsigned)BM_NOALLOC_SCRATCH_BYTES, (unsigned)PF_NOALLOC_PLAN_BYTES);
+        return -1;
+    }
+    w->x = (float*)(base + off[0]); w->qkv = (float*)(base + off[1]); w->att = (float*)(base + off[2]);
+    w->o = (float*)(base + off[3]); w->gu = (float*)(base + off[4]);
+    w->a16 = (unsigned short*)(base + off[5]); w->tok = (int*)(base + off[6]);
+    w->plan = base + act;
+    w->h_plan = s_noalloc_h_plan;
+    w->plan_cap = plan_bytes;
+    return 0;
+}
+
+static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
+    bm_model_t* m = S->m;
+    hipStream_t s = S->ctx->s;
+    const int D = m->D, H = m->H, QD = m->QD, KV = m->KV, L = m->L;
+    const float eps = 1e-5f; /* reference graph.c:134,175,219 */
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->V) {
+            BMK_ERR("bm_forward: token %d outside [0, %d)", tokens[i], m->V);
+            return -1;
+        }
+    if (L > PF_MAX_LAYERS) {
+        BMK_ERR("bm_forward: %d layers, the prefill handles at most %d", L, PF_MAX_LAYERS);
+        return -1;
+    }
+    /* a first pass sizes the plans, the second writes them */
+    PfGemm g[4 * PF_MAX_LAYERS];
+    PfWork w;
+    memset(&w, 0, sizeof w);
+    size_t used = 0;
+    if (pf_plans(m, &w, n, NULL, &used)) {
+        BMK_ERR("bm_forward: prefill GEMM plans rejected (%d tokens)", n);
+        return -1;
+    }
+    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
+    if ((noalloc ? pf_noalloc_work(S, n, used + 64, &w) : pf_session_work(S, n, used + 64, &w)) != 0) return -1;
+    if (pf_plans(m, &w, n, g, &used)) return -1;
     memcpy(S->h_io, tokens, (size_t)n * 4);
-    HIP_TRY(hipMemcpyAsync(S->pf_tok, S->h_io, (size_t)n * 4, hipMemcpyHostToDevice, s), "token write", return -1);
-    HIP_TRY(hipMemcpyAsync(S->pf_plan, S->h_plan, used, hipMemcpyHostToDevice, s), "plan write", return -1);
+    HIP_TRY(hipMemcpyAsync(w.tok, S->h_io, (size_t)n * 4, hipMemcpyHostToDevice, s), "token write", return -1);
+    HIP_TRY(hipMemcpyAsync(w.plan, w.h_plan, used, hipMemcpyHostToDevice, s), "plan write", return -1);
 
     DecAttn at;
     memset(&at, 0, sizeof at);
     at.kvc = S->kvc;
-    at.out = S->pf_att;
+    at.out = w.att;
     const float rp[6] = {m->arch.rope_theta, m->arch.rope_factor, m->arch.rope_low_freq_factor,
                          m->arch.rope_high_freq_factor, m->arch.rope_original_max,
                          m->arch.rope_scaling == BM_ROPE_LLAMA3 ? 1.0f : 0.0f};
@@ -910,43 +989,43 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     at.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
     at.NH = m->NH; at.NKV = m->NKV; at.HD = m->HD; at.KV = KV; at.MS = S->MS; at.L = L;
 
-    float* q = S->pf_qkv;
+    float* q = w.qkv;
     float* k = q + (size_t)n * QD;
     float* v = k + (size_t)n * KV;
-    float* gt = S->pf_gu;
+    float* gt = w.gu;
     float* up = gt + (size_t)n * H;
     /* floats between the split-K copies of each GEMM output */
     const long st_qkv = (long)n * (QD + 2 * KV), st_o = (long)n * D, st_gu = (long)n * 2 * H;
     auto gemm = [&](const PfGemm& p, float* C, long stride) {
-        return gm_launch_split_qf(S->pf_a16, 1, m->quant_bits == 4, m->d_q8, C, S->pf_plan + p.off, p.nprob,
+        return gm_launch_split_qf(w.a16, 1, m->quant_bits == 4, m->d_q8, C, w.plan + p.off, p.nprob,
                                   p.n_tiles, (size_t)stride, s);
     };
-    if (dec_pf_embed(S->pf_tok, m->d_emb, S->pf_x, n, D, s)) return -1;
+    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, s)) return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
         at.pf_ks = g[4 * l + 0].ks;
         at.pf_stride = st_qkv;
         const int ks_down = l ? g[4 * l - 1].ks : 1;
         /* residual of the previous layer's down projection, RMSNorm, q/k/v */
-        if (dec_pf_norm_bf16(S->pf_x, l ? S->pf_o : NULL, m->d_ln1 + (size_t)l * D, S->pf_a16, n, D, eps, ks_down,
+        if (dec_pf_norm_bf16(w.x, l ? w.o : NULL, m->d_ln1 + (size_t)l * D, w.a16, n, D, eps, ks_down,
                              st_o, s) ||
-            gemm(g[4 * l + 0], S->pf_qkv, st_qkv) ||
+            gemm(g[4 * l + 0], w.qkv, st_qkv) ||
             /* RoPE, cache append, causal attention */
-            dec_pf_attention(&at, q, k, v, n, S->pf_a16, s) ||
+            dec_pf_attention(&at, q, k, v, n, w.a16, s) ||
             /* o, residual, RMSNorm, gate/up, SwiGLU, down */
-            gemm(g[4 * l + 1], S->pf_o, st_o) ||
-            dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_ln2 + (size_t)l * D, S->pf_a16, n, D, eps, g[4 * l + 1].ks, st_o,
+            gemm(g[4 * l + 1], w.o, st_o) ||
+            dec_pf_norm_bf16(w.x, w.o, m->d_ln2 + (size_t)l * D, w.a16, n, D, eps, g[4 * l + 1].ks, st_o,
                              s) ||
-            gemm(g[4 * l + 2], S->pf_gu, st_gu) ||
-            dec_pf_swiglu_bf16(gt, up, S->pf_a16, (long)n * H, g[4 * l + 2].ks, st_gu, s) ||
-            gemm(g[4 * l + 3], S->pf_o, st_o))
+            gemm(g[4 * l + 2], w.gu, st_gu) ||
+            dec_pf_swiglu_bf16(gt, up, w.a16, (long)n * H, g[4 * l + 2].ks, st_gu, s) ||
+            gemm(g[4 * l + 3], w.o, st_o))
             return -1;
     }
     /* last residual (the bf16 output is not used), then the head on the last position */
-    if (dec_pf_norm_bf16(S->pf_x, S->pf_o, m->d_lnf, S->pf_a16, n, D, eps, g[4 * L - 1].ks, st_o, s)) return -1;
+    if (dec_pf_norm_bf16(w.x, w.o, m->d_lnf, w.a16, n, D, eps, g[4 * L - 1].ks, st_o, s)) return -1;
     DecHead hd;
     memset(&hd, 0, sizeof hd);
-    hd.x = S->pf_x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
+    hd.x = w.x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
     hd.wq = m->q8_head ? m->d_head8 : NULL;
     hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
     hd.logits = S->logits; hd.st = NULL; hd.out_tokens = NULL;
@@ -966,30 +1045,49 @@ static int prefill(bm_session_t* S, const int* tokens, int n) {
     return 0;
 }
 
+/* One timed one-pass prefill (the session is at position 0, batch 1). */
+static float* forward_prefill(bm_session_t* S, const int* tokens, int n_tokens, bool noalloc) {
+    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+    HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
+    if (prefill(S, tokens, n_tokens, noalloc) != 0) return NULL;
+    float ms = 0.f;
+    /* prefill ends synchronized on the logits read: ev0 to now is its GPU span */
+    if (hipEventRecord(S->ev1, S->ctx->s) == hipSuccess && hipEventSynchronize(S->ev1) == hipSuccess &&
+        hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess)
+        S->busy_ms += ms;
+    S->launches++;
+    return S->h_logits;
+}
+
 /* Reference session.c:141-149: a prompt at position 0 of a batch-1 session
  * is prefilled in one pass (bf16-MFMA projections); anything else steps
  * token by token. */
 extern "C" float* bm_forward(bm_session_t* S, const int* tokens, int n_tokens) {
     if (!S || (!tokens && n_tokens > 0)) return NULL;
     if (n_tokens <= 0) return S->h_logits;
-    if (n_tokens > 1 && S->pos == 0 && S->B == 1 && n_tokens <= S->MS && (size_t)n_tokens <= S->h_io_cap) {
-        HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
-        HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
-        if (prefill(S, tokens, n_tokens) != 0) return NULL;
-        float ms = 0.f;
-        /* prefill ends synchronized on the logits read: ev0 to now is its GPU span */
-        if (hipEventRecord(S->ev1, S->ctx->s) == hipSuccess && hipEventSynchronize(S->ev1) == hipSuccess &&
-            hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess)
-            S->busy_ms += ms;
-        S->launches++;
-        return S->h_logits;
-    }
+    if (n_tokens > 1 && S->pos == 0 && S->B == 1 && n_tokens <= S->MS && (size_t)n_tokens <= S->h_io_cap)
+        return forward_prefill(S, tokens, n_tokens, false);
     float* out = S->h_logits;
     for (int i = 0; i < n_tokens; i++) {
         out = bm_step(S, tokens[i]);
         if (!out) return NULL;
     }
     return out;
+}
+
+/* bm_forward's one-pass prefill with its workspace in the library's static
+ * per-GPU array (include/baremetal.h): no allocation of any kind. */
+extern "C" float* bm_forward_noalloc(bm_session_t* S, const int* tokens, int n_tokens) {
+    if (!S || !tokens || n_tokens < 2) {
+        BMK_ERR("bm_forward_noalloc: needs a session and at least 2 tokens (got %d)", n_tokens);
+        return NULL;
+    }
+    if (S->pos != 0 || S->B != 1 || n_tokens > S->MS || (size_t)n_tokens > S->h_io_cap) {
+        BMK_ERR("bm_forward_noalloc: a prompt of %d tokens at position 0 of a batch-1 session with room for it "
+                "(position %d, batch %d, max %d)", n_tokens, S->pos, S->B, S->MS);
+        return NULL;
+    }
+    return forward_prefill(S, tokens, n_tokens, true);
 }
 
 extern "C" int bm_session_gpu_stats(bm_session_t* S, double* busy_ms, unsigned long long* launches, int reset) {

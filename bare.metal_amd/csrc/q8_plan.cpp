@@ -9,7 +9,6 @@
 #include "q8_matvec.h"
 #include "q8_gemm.h"
 
-#include <vector>
 #include "../../include/bm_q8.h"
 
 #include <string.h>
@@ -111,14 +110,14 @@ static int gemm_split(int nprob, const int* M, const int* N, const int* K, int t
 }
 
 /* Workgroups per XCD queue: every (problem, N tile, K slice) group goes to
- * one XCD, round robin, with its M tiles consecutive. */
-static long gemm_queue_len(int nprob, const int* M, const int* N, const int* ks, long* per_xcd) {
+ * one XCD, round robin, with its M tiles consecutive; ks K slices per problem. */
+static long gemm_queue_len(int nprob, const int* M, const int* N, int ks, long* per_xcd) {
     for (int x = 0; x < GM_XCDS; x++) per_xcd[x] = 0;
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
         for (int n = 0; n < tn; n++)
-            for (int k = 0; k < ks[i]; k++, pair++) per_xcd[pair % GM_XCDS] += tm;
+            for (int k = 0; k < ks; k++, pair++) per_xcd[pair % GM_XCDS] += tm;
     }
     long longest = 0;
     for (int x = 0; x < GM_XCDS; x++) longest = per_xcd[x] > longest ? per_xcd[x] : longest;
@@ -137,16 +136,17 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
         const int t = bm_q8_gemm_tiles(M[i], N[i], K[i]);
         if (t < 0 || t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
     }
-    const int kss = target > 0 ? gemm_split(nprob, M, N, K, target, kmax) : 1;
-    std::vector<int> ks((size_t)(nprob > 0 ? nprob : 1), kss);
+    /* one split factor for every problem of the launch (no host allocation here:
+     * the engine's prefill plans are also made by the no-allocation entry point) */
+    const int ks = target > 0 ? gemm_split(nprob, M, N, K, target, kmax) : 1;
     for (int i = 0; i < nprob; i++)
-        if ((long)gm_tiles_for(M[i], N[i]) * kss > 0xffff) return -1;
+        if ((long)gm_tiles_for(M[i], N[i]) * ks > 0xffff) return -1;
     long per_xcd[GM_XCDS];
-    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, ks.data(), per_xcd);
+    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, ks, per_xcd);
     if (slots > 0x7fffffffL) return -1;
     const size_t need = (size_t)nprob * sizeof(GmDesc) + (size_t)slots * 4;
     if (n_tiles_out) *n_tiles_out = (int)slots;
-    if (ksplit_out) *ksplit_out = kss;
+    if (ksplit_out) *ksplit_out = ks;
     if (!plan) return (long)need;
     if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
     GmDesc* d = (GmDesc*)plan;
@@ -162,8 +162,8 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
         d[i].lda = lda[i];
         d[i].ldc = ldc[i];
         d[i].tile0 = t0;
-        d[i].tiles = gm_tiles_for(M[i], N[i]) * ks[i];
-        d[i].pad_ = ks[i] > 1 ? ks[i] : 0;
+        d[i].tiles = gm_tiles_for(M[i], N[i]) * ks;
+        d[i].pad_ = ks > 1 ? ks : 0;
         t0 += d[i].tiles;
     }
     for (long b = 0; b < slots; b++) map[b] = GM_IDLE_TILE;
@@ -172,7 +172,7 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
         for (int n = 0; n < tn; n++)
-            for (int k = 0; k < ks[i]; k++, pair++) {
+            for (int k = 0; k < ks; k++, pair++) {
                 const int x = (int)(pair % GM_XCDS);
                 for (int m = 0; m < tm; m++)
                     map[(long)GM_XCDS * fill[x]++ + x] =

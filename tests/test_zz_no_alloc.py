@@ -1,0 +1,53 @@
+# SPDX-License-Identifier: MPL-2.0
+"""bm_forward_noalloc (include/baremetal.h): the one-pass prefill whose
+workspace lives in the library's static per-GPU array.  Through the C ABI,
+against bm_forward on an identical session: the same logits bit for bit
+(same kernels, same plans), the same KV cache (the next step's logits equal
+too), on two calls in a row with the second prompt shorter than the first,
+so the array still holds the first call's data; and a prompt whose
+workspace exceeds the array is rejected."""
+import numpy as np
+import pytest
+
+import bmhip
+from decode_util import SMALL
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(dims, ms, seed):
+    return (bmhip.Engine(dims, max_seq_len=ms, seed=seed, graph=False),
+            bmhip.Engine(dims, max_seq_len=ms, seed=seed, graph=False))
+
+
+@pytest.mark.parametrize("dims,lens", [(SMALL, (70, 17)), (bmhip.SMOLLM2_135M, (128, 40))], ids=["small", "135m"])
+def test_noalloc_prefill_equals_bm_forward(dims, lens):
+    ref, na = _pair(dims, 256, 77)
+    try:
+        for n in lens:  # two calls in a row, the second shorter
+            toks = bmhip.synth_uniform_int(300 + n, 0, dims["V"], n)
+            ref.reset()
+            na.reset()
+            want = ref.forward(toks)
+            got = na.forward_noalloc(toks)
+            assert got is not None
+            assert np.array_equal(got, want), n
+            nxt = int(toks[0])
+            assert np.array_equal(na.step(nxt), ref.step(nxt)), n
+    finally:
+        ref.close()
+        na.close()
+
+
+def test_noalloc_prefill_rejects():
+    dims = bmhip.SMOLLM2_135M
+    eng = bmhip.Engine(dims, max_seq_len=1024, seed=5, graph=False)
+    try:
+        # about 82 KB of workspace per token at these shapes: 1000 tokens exceed 64 MiB
+        assert eng.forward_noalloc(bmhip.synth_uniform_int(1, 0, dims["V"], 1000)) is None
+        assert eng.forward_noalloc(np.array([3], np.int32)) is None  # one token: not a prefill
+        toks = bmhip.synth_uniform_int(2, 0, dims["V"], 64)
+        assert eng.forward_noalloc(toks) is not None
+        assert eng.forward_noalloc(toks) is None  # past position 0
+    finally:
+        eng.close()
