@@ -206,18 +206,23 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
  * (several decode sequences' projections in one launch), on bf16 MFMA
  * (v_mfma_f32_16x16x32_bf16, D[16][16] += A[16][32] x B[32][16], fp32 sum).
  *
- * A workgroup is one wave; it runs the 64-row tile blockIdx.x - tile0 of
- * problem tile_map[blockIdx.x] (4 groups of 16 output rows) for batch rows
- * 16*blockIdx.y .. +15 over the whole K range.  Per step of BMV_U K blocks
- * the wave copies the 64 rows' spans of BMV_U blocks (contiguous in each
- * row) into LDS with 16-byte loads, so every weight byte is fetched once;
- * the MFMA operands are then read from LDS.  Per K block, lane l
- * (c = l%16, g = l/16) loads x[b0 + c][32kb + 8g .. +7] once, splits it
- * exactly into three bf16 terms (split3) and feeds each, as the A operand,
- * to one MFMA per row group, whose B operand is q[r0 + c][32kb + 8g .. +7]
- * (the int8 or 4-bit codes, exact in bf16).  Every product is exact, so
- * the block sums are fp32 sums of the exact x * q products, as in the fp32
- * reference (only the summation order differs).  Each
+ * A workgroup is BMV_WAVES waves; it runs the BMV_TILE_ROWS-row tile
+ * blockIdx.x - tile0 of problem tile_map[blockIdx.x] for batch rows
+ * 16*blockIdx.y .. +15 over the whole K range, each wave 64 output rows
+ * (4 groups of 16).  Per step of BMV_U K blocks:
+ *   - each wave copies its 64 rows' spans of BMV_U blocks (contiguous in
+ *     each row) into its own part of LDS with 16-byte loads, so every
+ *     weight byte is fetched once;
+ *   - the workgroup loads the step's activations once (lane t: batch row
+ *     t/16, 8 consecutive columns), splits each exactly into three bf16
+ *     terms (split3) and stores them in LDS in the MFMA A-operand order, so
+ *     the split is paid once per 256 output rows;
+ *   - per K block, lane l (c = l%16, g = l/16) reads its three A slots
+ *     (x[b0 + c][32kb + 8g .. +7] as hi, mid, lo) and, per row group, the
+ *     B operand q[r0 + c][32kb + 8g .. +7] (the int8 or 4-bit codes, exact
+ *     in bf16) and its block scale from LDS, and chains three MFMAs.
+ * Every product is exact, so each block sum is an fp32 sum of the exact
+ * x * q products, as in the fp32 reference (only the order differs).  Each
  * group's block product is scaled by its row's block scale and added in
  * block order, as the reference scales each block's dot product
  * (forward.metal:575-623).  D layout: lane l holds batch rows 4*(l/16)+v of
@@ -226,9 +231,8 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
 typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
 typedef float bmm_f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
-constexpr int BMV_GROUPS = 4;             /* 16-row groups per wave */
-constexpr int BMV_ROWS = 16 * BMV_GROUPS; /* output rows per workgroup */
-constexpr int BMV_U = 4;                  /* K blocks per step */
+constexpr int BMV_GROUPS = 4; /* 16-row groups per wave */
+constexpr int BMV_U = 4;      /* K blocks per step */
 
 /* x = hi + mid + lo with three bf16 terms: hi keeps the top 8 significant
  * bits of x (truncated, so no term overflows), mid the top 8 of x - hi and
@@ -237,7 +241,7 @@ constexpr int BMV_U = 4;                  /* K blocks per step */
  * above bf16's smallest normal (|x| >= 2^-102 suffices).  A non-finite x
  * goes whole into hi (a NaN kept a NaN) with mid = lo = 0, so its products
  * are the fp32 ones (Inf * 0 = NaN, Inf * q = Inf). */
-__device__ __forceinline__ void split3(const bmm_f32x8& x, bmm_bf16x8& hi, bmm_bf16x8& mid, bmm_bf16x8& lo) {
+__device__ __forceinline__ void split3(const bmm_f32x8& x, uint4& hi, uint4& mid, uint4& lo) {
     unsigned int h[8], m[8], l[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -251,96 +255,153 @@ __device__ __forceinline__ void split3(const bmm_f32x8& x, bmm_bf16x8& hi, bmm_b
         m[i] = mb;
         l[i] = __float_as_uint(r2) & 0xffff0000u;
     }
-    unsigned int ph[4], pm[4], pl[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        ph[i] = (h[2 * i] >> 16) | h[2 * i + 1];
-        pm[i] = (m[2 * i] >> 16) | m[2 * i + 1];
-        pl[i] = (l[2 * i] >> 16) | l[2 * i + 1];
-    }
-    __builtin_memcpy(&hi, ph, 16);
-    __builtin_memcpy(&mid, pm, 16);
-    __builtin_memcpy(&lo, pl, 16);
+    hi = make_uint4((h[0] >> 16) | h[1], (h[2] >> 16) | h[3], (h[4] >> 16) | h[5], (h[6] >> 16) | h[7]);
+    mid = make_uint4((m[0] >> 16) | m[1], (m[2] >> 16) | m[3], (m[4] >> 16) | m[5], (m[6] >> 16) | m[7]);
+    lo = make_uint4((l[0] >> 16) | l[1], (l[2] >> 16) | l[3], (l[4] >> 16) | l[5], (l[6] >> 16) | l[7]);
 }
 
 template <int QF>
-__global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restrict__ W, const float* __restrict__ X,
-                                                  float* __restrict__ Y, const MvDesc* __restrict__ desc,
-                                                  const unsigned int* __restrict__ tile_map, int BT) {
+__global__ __launch_bounds__(64 * BMV_WAVES) void k_bmv_multi(const unsigned char* __restrict__ W,
+                                                              const float* __restrict__ X, float* __restrict__ Y,
+                                                              const MvDesc* __restrict__ desc,
+                                                              const unsigned int* __restrict__ tile_map, int BT) {
     constexpr int BYTES = QFmt<QF>::BYTES;
     constexpr int SPAN = BMV_U * BYTES;   /* bytes of one row per step: 144 (Q8_0), 80 (Q4_0) */
     constexpr int CPR = SPAN / 16;        /* 16-byte chunks per row span */
     constexpr int LDR = SPAN + 4;         /* LDS row pitch: an odd number of dwords spreads the rows over the banks */
     constexpr int LANE_OFF = QF == QF_Q4 ? 4 : 8; /* code bytes per lane and block */
     static_assert(SPAN % 16 == 0, "row span must be whole 16-byte chunks");
-    __shared__ __attribute__((aligned(16))) unsigned char tile[BMV_ROWS * LDR];
-    const int lane = threadIdx.x;
+    static_assert(BMV_U * 32 * 16 == 64 * BMV_WAVES * 8, "one 8-column activation slot per lane and step");
+    __shared__ __attribute__((aligned(16))) unsigned char tile[BMV_WAVES][64 * LDR];
+    __shared__ uint4 xs[3][BMV_U][64]; /* A operands: term, block, lane */
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int c = lane & 15, g = lane >> 4;
     const MvDesc d = desc[tile_map[blockIdx.x]];
-    const int row0 = ((int)blockIdx.x - d.tile0) * BMV_ROWS;
+    const int row0 = ((int)blockIdx.x - d.tile0) * BMV_TILE_ROWS + 64 * wave;
+    const bool wave_live = row0 < d.OC; /* the same for the whole wave */
     const int b0 = 16 * (int)blockIdx.y;
+    const int nbt = min(16, BT - b0); /* batch rows of this tile */
     const int nb = d.C / 32;
     const size_t row_bytes = (size_t)nb * BYTES;
-    /* this lane's chunks: chunk q = lane + 64 t of the 64 x CPR chunk grid;
-     * rows past OC (and batch rows past BT) are clamped: they feed outputs
-     * that are never stored */
-    const unsigned char* src[CPR];
-    int lofs[CPR], cofs[CPR];
+    unsigned char* wt = tile[wave];
+    /* this lane's weight chunks: chunk q = lane + 64 t of the wave's 64 x CPR
+     * chunk grid, row q / CPR, byte 16 (q % CPR) of the row's span; rows past
+     * OC are clamped (they feed outputs never stored).  Kept as 32-bit
+     * offsets from the wave's first row and LDS addresses, to spare VGPRs. */
+    const unsigned char* wbase = W + d.w_off + (size_t)(wave_live ? row0 : 0) * row_bytes;
+    unsigned int goff[CPR];
+    int ldsa[CPR];
+    int cbo[CPR]; /* the chunk's byte offset in the span, + 16 */
 #pragma unroll
     for (int t = 0; t < CPR; t++) {
-        const int q = lane + 64 * t, r = q / CPR;
-        cofs[t] = 16 * (q - r * CPR);
-        lofs[t] = r * LDR;
-        src[t] = W + d.w_off + (size_t)min(row0 + r, d.OC - 1) * row_bytes;
+        const int q = lane + 64 * t, r = q / CPR, cb = 16 * (q - r * CPR);
+        goff[t] = wave_live ? (unsigned int)((size_t)(min(row0 + r, d.OC - 1) - row0) * row_bytes) + cb : 0u;
+        ldsa[t] = r * LDR + cb;
+        cbo[t] = cb + 16;
     }
-    const float* xr = X + d.x_off + (size_t)min(b0 + c, BT - 1) * (size_t)d.C + 8 * g;
+    /* this lane's activation slot: batch row xb, columns 8 * xk .. +7 of the step */
+    const int xb = tid >> 4, xk = tid & 15, xu = xk >> 2, xg = xk & 3;
+    const bool x_on = xb < nbt;
+    const float* xr = X + d.x_off + (size_t)(b0 + (x_on ? xb : 0)) * (size_t)d.C + 8 * xk;
+    /* batch rows past BT stay zero in every A slot */
+    if (!x_on) {
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        xs[0][xu][xb + 16 * xg] = z;
+        xs[1][xu][xb + 16 * xg] = z;
+        xs[2][xu][xb + 16 * xg] = z;
+    }
+
+    /* Loads of step kb0 into registers: the weight chunks of this wave's
+     * rows (a chunk reaching past the step's bytes is moved back to end
+     * there, and stored at the same place, so the overlap is written twice
+     * with equal bytes: no load leaves the row) and this lane's activations. */
+    /* Registers of one step's loads: the weight chunks of this wave's rows
+     * (a chunk reaching past the step's bytes is moved back to end there, and
+     * stored at the same place, so the overlap is written twice with equal
+     * bytes: no load leaves the row) and this lane's activations.  Two sets
+     * alternate, so two steps' loads are in flight while one is computed. */
+    struct Stage {
+        uint4 ch[CPR];
+        float4 xa, xc;
+        bool x_live;
+    };
+    Stage st0, st1;
+    const int nsteps = (nb + BMV_U - 1) / BMV_U;
+    /* -(bytes) a chunk moves back in a step whose row span ends `valid`
+     * bytes in: 0 for a full step */
+    auto chunk_shift = [&](int t, int valid) { return min(0, valid - cbo[t]); };
+    /* Issues the loads of step `step` into S: every lane issues the same
+     * loads whatever the step, so no branch separates two steps' loads (a
+     * step past the last reads 16 bytes at the wave's first row instead, and
+     * idle waves read there too); the loaded bytes of such steps are never
+     * used.  Activations: a slot past the row or the batch reads the row's
+     * first columns instead and is not stored. */
+    auto load_step = [&](Stage& S, int step) {
+        const bool real = step < nsteps;
+        const int kb0 = step * BMV_U;
+        S.x_live = real && x_on && kb0 + xu < nb;
+        const float* xp = xr + (S.x_live ? 32 * kb0 : 0);
+        __builtin_memcpy(&S.xa, __builtin_assume_aligned(xp, 16), 16);
+        __builtin_memcpy(&S.xc, __builtin_assume_aligned(xp + 4, 16), 16);
+        const int valid = min(BMV_U, nb - kb0) * BYTES;
+        const bool wl = real && wave_live;
+        const unsigned char* sb = wbase + (wl ? (size_t)kb0 * BYTES : 0);
+#pragma unroll
+        for (int t = 0; t < CPR; t++) {
+            const int o = wl ? (int)goff[t] + chunk_shift(t, valid) : 0;
+            __builtin_memcpy(&S.ch[t], __builtin_assume_aligned(sb + o, 4), 16);
+        }
+    };
 
     bmm_f32x4 acc[BMV_GROUPS];
 #pragma unroll
     for (int j = 0; j < BMV_GROUPS; j++) acc[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kb0 = 0; kb0 < nb; kb0 += BMV_U) {
-        /* bytes of this step inside the row; a chunk reaching past them is
-         * moved back to end there (and stored at the same place, so the
-         * overlap is written twice with equal bytes): no load leaves the row */
-        const int valid = min(BMV_U, nb - kb0) * BYTES;
-        uint4 ch[CPR];
-        int at[CPR];
-#pragma unroll
-        for (int t = 0; t < CPR; t++) {
-            at[t] = min(cofs[t], valid - 16);
-            __builtin_memcpy(&ch[t], __builtin_assume_aligned(src[t] + (size_t)kb0 * BYTES + at[t], 4), 16);
-        }
-        float4 xa[BMV_U], xb[BMV_U];
-#pragma unroll
-        for (int u = 0; u < BMV_U; u++) {
-            const int kb = min(kb0 + u, nb - 1);
-            __builtin_memcpy(&xa[u], __builtin_assume_aligned(xr + 32 * kb, 16), 16);
-            __builtin_memcpy(&xb[u], __builtin_assume_aligned(xr + 32 * kb + 4, 16), 16);
-        }
+
+    /* One step: stage S (the loads of step `step`) into LDS, issue the loads
+     * of step + 2 into S, then the step's products. */
+    auto run_step = [&](Stage& S, int step) {
+        const int kb0 = step * BMV_U;
         __syncthreads(); /* the previous step's LDS reads are done */
+        if (wave_live) {
+            const int valid = min(BMV_U, nb - kb0) * BYTES;
 #pragma unroll
-        for (int t = 0; t < CPR; t++) {
-            unsigned int w4[4] = {ch[t].x, ch[t].y, ch[t].z, ch[t].w};
-            /* 4-byte stores: a moved-back chunk is 4-byte but not 16-byte aligned */
+            for (int t = 0; t < CPR; t++) {
+                const int la = ldsa[t] + chunk_shift(t, valid);
+                unsigned int w4[4] = {S.ch[t].x, S.ch[t].y, S.ch[t].z, S.ch[t].w};
+                /* 4-byte stores: a moved-back chunk is 4-byte but not 16-byte aligned */
 #pragma unroll
-            for (int e = 0; e < 4; e++) *(unsigned int*)&tile[lofs[t] + at[t] + 4 * e] = w4[e];
+                for (int e = 0; e < 4; e++) *(unsigned int*)&wt[la + 4 * e] = w4[e];
+            }
+        }
+        if (S.x_live) {
+            const bmm_f32x8 xf = {S.xa.x, S.xa.y, S.xa.z, S.xa.w, S.xc.x, S.xc.y, S.xc.z, S.xc.w};
+            uint4 th, tm, tl;
+            split3(xf, th, tm, tl);
+            xs[0][xu][xb + 16 * xg] = th;
+            xs[1][xu][xb + 16 * xg] = tm;
+            xs[2][xu][xb + 16 * xg] = tl;
         }
         __syncthreads();
+        /* the loads two steps ahead fly while this step's products run */
+        load_step(S, step + 2);
+        if (!wave_live) return;
 #pragma unroll
         for (int u = 0; u < BMV_U; u++) {
-            /* x = hi + mid + lo exactly; the codes are exact in bf16 and
-             * every product is exact in the fp32 sum */
             /* blocks past the row (last step only; the same for the whole
              * wave) are skipped, not weighted by 0: 0 * Inf would be NaN */
             if (kb0 + u >= nb) break;
-            const bmm_f32x8 xf = {xa[u].x, xa[u].y, xa[u].z, xa[u].w, xb[u].x, xb[u].y, xb[u].z, xb[u].w};
             bmm_bf16x8 xh, xm, xl;
-            split3(xf, xh, xm, xl);
+            {
+                const uint4 a0 = xs[0][u][lane], a1 = xs[1][u][lane], a2 = xs[2][u][lane];
+                __builtin_memcpy(&xh, &a0, 16);
+                __builtin_memcpy(&xm, &a1, 16);
+                __builtin_memcpy(&xl, &a2, 16);
+            }
             bmm_bf16x8 wv[BMV_GROUPS];
             float sc[BMV_GROUPS];
 #pragma unroll
             for (int j = 0; j < BMV_GROUPS; j++) {
-                const unsigned char* blk = &tile[(16 * j + c) * LDR + u * BYTES];
+                const unsigned char* blk = &wt[(16 * j + c) * LDR + u * BYTES];
                 sc[j] = *(const float*)blk;
                 const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
                 const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
@@ -370,7 +431,17 @@ __global__ __launch_bounds__(64) void k_bmv_multi(const unsigned char* __restric
 #pragma unroll
                 for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sc[j], dd[j][v], acc[j][v]);
         }
+    };
+
+    load_step(st0, 0);
+    load_step(st1, 1);
+    int step = 0;
+    for (; step + 1 < nsteps; step += 2) {
+        run_step(st0, step);
+        run_step(st1, step + 1);
     }
+    if (step < nsteps) run_step(st0, step);
+    if (!wave_live) return;
 #pragma unroll
     for (int j = 0; j < BMV_GROUPS; j++) {
         const int row = row0 + 16 * j + c;
@@ -394,9 +465,9 @@ static int launch_bmv_multi(int qf, const unsigned char* W, const float* X, floa
     if (n_tiles <= 0 || BT < 2 || BT > DEC_MAX_B) return -1;
     const dim3 grid((unsigned)n_tiles, (unsigned)((BT + 15) / 16));
     if (qf == QF_Q4)
-        hipLaunchKernelGGL(k_bmv_multi<QF_Q4>, grid, dim3(64), 0, s, W, X, Y, d_desc, d_tile_map, BT);
+        hipLaunchKernelGGL(k_bmv_multi<QF_Q4>, grid, dim3(64 * BMV_WAVES), 0, s, W, X, Y, d_desc, d_tile_map, BT);
     else
-        hipLaunchKernelGGL(k_bmv_multi<QF_Q8>, grid, dim3(64), 0, s, W, X, Y, d_desc, d_tile_map, BT);
+        hipLaunchKernelGGL(k_bmv_multi<QF_Q8>, grid, dim3(64 * BMV_WAVES), 0, s, W, X, Y, d_desc, d_tile_map, BT);
     BMK_LAUNCH_CHECK();
     return 0;
 }

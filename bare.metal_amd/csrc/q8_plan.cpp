@@ -21,11 +21,11 @@ static int mv_tiles_u(int OC, int C, int U) {
 extern "C" int bm_q8_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_WIDE); }
 extern "C" int bm_q4_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_Q4); }
 
-/* Batched (BT >= 2) multi-matrix launch: 64 output rows per workgroup. */
+/* Batched (BT >= 2) multi-matrix launch: BMV_TILE_ROWS output rows per workgroup. */
 #define MV_U_BATCHED (-1)
 extern "C" int bm_q8_bmv_tiles(int OC, int C) {
     if (OC <= 0 || C <= 0 || C % 32) return -1;
-    return (OC + 63) / 64;
+    return (OC + BMV_TILE_ROWS - 1) / BMV_TILE_ROWS;
 }
 
 static int plan_tiles(int OC, int C, int U) { return U == MV_U_BATCHED ? bm_q8_bmv_tiles(OC, C) : mv_tiles_u(OC, C, U); }

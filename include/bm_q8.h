@@ -55,7 +55,7 @@ long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, cons
                    const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles);
 
 /* The same two for a matmul_forward_q8_vec_multi (or _q4_vec_multi) launch
- * with BT >= 2 rows per problem (64 output rows per workgroup, each weight
+ * with BT >= 2 rows per problem (256 output rows per workgroup, each weight
  * read once for up to 16 rows; the same tiling for Q8_0 and Q4_0): several
  * decode sequences' projections in one launch. */
 int  bm_q8_bmv_tiles(int OC, int C);

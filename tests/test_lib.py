@@ -167,16 +167,16 @@ def test_gemm_split_plan():
 
 
 def test_bmv_plan_layout():
-    """Plans of the batched (BT >= 2) multi-matrix matvec: 64 output rows per
+    """Plans of the batched (BT >= 2) multi-matrix matvec: 256 output rows per
     workgroup, problems in order, the tile map naming each workgroup's problem."""
     import numpy as np
 
-    assert bmhip.lib().bm_q8_bmv_tiles(960, 960) == 15
-    assert bmhip.lib().bm_q8_bmv_tiles(65, 64) == 2
+    assert bmhip.lib().bm_q8_bmv_tiles(960, 960) == 4
+    assert bmhip.lib().bm_q8_bmv_tiles(257, 64) == 2 and bmhip.lib().bm_q8_bmv_tiles(256, 64) == 1
     assert bmhip.lib().bm_q8_bmv_tiles(16, 48) == -1
-    plan, n = bmhip.mv_plan([0, 100], [0, 8 * 960], [0, 8 * 960], [960, 65], [960, 64], bt=8)
-    assert n == 17
+    plan, n = bmhip.mv_plan([0, 100], [0, 8 * 960], [0, 8 * 960], [960, 257], [960, 64], bt=8)
+    assert n == 6
     desc = np.frombuffer(plan[:80].tobytes(), dtype=np.int32).reshape(2, 10)  # MvDesc is 40 bytes
-    assert desc[:, 6:].tolist() == [[960, 960, 0, 15], [65, 64, 15, 2]]  # OC, C, tile0, tiles
+    assert desc[:, 6:].tolist() == [[960, 960, 0, 4], [257, 64, 4, 2]]  # OC, C, tile0, tiles
     tmap = np.frombuffer(plan[80:].tobytes(), dtype=np.uint32)
-    assert list(tmap) == [0] * 15 + [1] * 2
+    assert list(tmap) == [0] * 4 + [1] * 2

@@ -178,7 +178,7 @@ def test_matvec_multi_batched(be, BT):
     shapes = BATCHED_SHAPES
     ws, xs, w_off, x_off, y_off = _batched_problems(61 + BT, shapes, BT)
     plan, n_tiles = bmhip.mv_plan(w_off, x_off, y_off, [s[0] for s in shapes], [s[1] for s in shapes], bt=BT)
-    assert n_tiles == sum((s[0] + 63) // 64 for s in shapes)
+    assert n_tiles == sum((s[0] + 255) // 256 for s in shapes)
     W, X = be.upload(np.concatenate(ws)), be.upload(np.concatenate(xs))
     Y = be.alloc(4 * BT * sum(s[0] for s in shapes))
     rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(len(shapes), n_tiles, BT), be.upload(plan), W, X, Y],
