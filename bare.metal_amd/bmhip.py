@@ -102,6 +102,7 @@ def lib() -> C.CDLL:
         "bm_model_init_synthetic": (i, [vp, u64]),
         "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
         "bm_session_set_graph": (i, [vp, i]),
+        "bm_session_set_persistent": (i, [vp, i]),
         "bm_profile_phases": (C.c_long, [vp, vp]),
     }
     for name, (res, args) in sig.items():
@@ -441,6 +442,10 @@ class Engine:
     def set_graph(self, on: bool):
         lib().bm_session_set_graph(self.sess, 1 if on else 0)
 
+    def set_persistent(self, on: bool) -> bool:
+        """Persistent one-kernel layers (batch 1, Q8, MI355X); False when not available."""
+        return lib().bm_session_set_persistent(self.sess, 1 if on else 0) == 0
+
     def step(self, token: int) -> np.ndarray:
         p = lib().bm_step(self.sess, int(token))
         if not p:
@@ -491,11 +496,11 @@ class Engine:
         lib().bm_profile_begin(self.sess)
 
     PHASES = ("embed", "rmsnorm_qkv", "rope_kv_attention", "o_residual", "rmsnorm_gateup_swiglu",
-              "down_residual", "norm_head_argmax")
+              "down_residual", "norm_head_argmax", "layers_persistent")
 
     def profile_end(self) -> dict:
         """Ends profiling; per-phase ms per step and the reference-style split."""
-        ms = (C.c_double * 7)()
+        ms = (C.c_double * len(self.PHASES))()
         n = lib().bm_profile_phases(self.sess, ms)
         a, m, o = C.c_double(), C.c_double(), C.c_double()
         lib().bm_profile_end(self.sess, C.byref(a), C.byref(m), C.byref(o))

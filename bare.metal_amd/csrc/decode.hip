@@ -639,6 +639,7 @@ __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
     __shared__ int tok_s;
     DecState* st = a.st;
     const int b = blockIdx.x, pos = st->pos;
+    if (b == 0 && threadIdx.x == 0) st->bar = 0; /* the persistent step kernel's barrier counter */
     if (threadIdx.x == 0) {
         int tok;
         if (st->host_mode) tok = st->host_token[b];

@@ -1,0 +1,734 @@
+/* SPDX-License-Identifier: MPL-2.0
+ *
+ * decode_persist.hip — every layer of a batch-1 decode step in one
+ * persistent kernel on one XCD of MI355X.
+ *
+ * The reference runs a decode step as one dispatch per graph node
+ * (reference src/baremetal/graph.c:126-226, scheduler.c:712-996): per
+ * layer RMSNorm, the q/k/v projections, RoPE, KV store, attention, the
+ * o projection, the residual add, RMSNorm, gate/up, SwiGLU, down and the
+ * residual add.  At batch 1 on MI355X each such launch is bound by its
+ * fixed cost (about 2.5 us from one kernel's end to the next one's first
+ * useful load) rather than by its bytes, so this kernel runs the whole
+ * layer stack as five phases per layer separated by grid barriers inside
+ * one launch:
+ *   1. RMSNorm(x) and q, k, v (Q8 matvecs of 960 rows at SmolLM2-135M);
+ *   2. RoPE, KV append and attention, split into (KV head, key chunk)
+ *      pieces that write online-softmax partials (max, sum, P.V);
+ *   3. the partials merged per query head, o projection, residual;
+ *   4. RMSNorm, gate and up, SwiGLU;
+ *   5. down projection, residual.
+ * A phase costs a chain of memory round trips rather than bytes, so each
+ * one is cut to a single round trip after its barrier.  Vector memory
+ * requests of a CU leave in order, and one counter covers a wave's loads and
+ * stores, so the order of issue decides what waits for what:
+ *   - every staging step (the input vector, the attention partials, the
+ *     q/k/v of a KV head with the first keys and values of its chunk)
+ *     issues all of its loads before it waits on any, with in-bounds
+ *     addresses for unused lanes so that the compiler can count them;
+ *   - the weights of the next matvec phase are issued right after a
+ *     phase's staging loads (o in phase 1, the second RMSNorm in phase 2,
+ *     gate/up in phase 3, down in phase 4, the next layer's q/k/v and first
+ *     RMSNorm in phase 5), so they stream in behind the activations while
+ *     the phase computes, and into registers of their own (per-phase pass
+ *     counts P_QKV, P_O, P_GU, P_DN);
+ *   - barriers inside a workgroup order LDS only (an LDS fence), so they
+ *     do not wait for those weights;
+ *   - a workgroup keeps in registers the rows of the residual stream it
+ *     owns (the o and down projections split the rows of x the same way),
+ *     so a residual add reads nothing.
+ *
+ * One XCD: MI355X hands workgroup b to XCD b % 8.  The grid has 8 x
+ * DEC_PERSIST_WGS workgroups; those with blockIdx.x % 8 == 0 work and the
+ * rest return at once, so every working workgroup shares one L2.  Writes of
+ * one phase then reach every reader through that L2: a barrier is a relaxed
+ * device-scope atomic add after the workgroup's stores have completed and
+ * a poll of the counter (about 1 us for 32 workgroups, against 2.7 us for
+ * release/acquire fences across XCDs).  What a phase reads of the previous
+ * phase's results (x, h, q/k/v, the attention partials) it reads with
+ * agent-scope loads, which miss the CU's L1 (whose lines may be stale) and
+ * hit the shared L2.  No cache is invalidated: an agent-scope acquire fence
+ * would invalidate this CU's L1 but made the step 2.6x slower, and a
+ * workgroup-scope one leaves the L1 alone.  The barrier's spin is bounded
+ * in time: on timeout a workgroup sets DecState.sync_error and leaves; the
+ * others cannot pass that barrier either and time out there too, so the
+ * grid always drains.
+ *
+ * Arithmetic: fp32 throughout, the reference's formulas (RMSNorm
+ * (x * inv) * w with eps from graph.c:134, rotate-half RoPE, scale
+ * 1/sqrt(HD), first-max softmax merge, SiLU x/(1+e^-x)); the Q8 block dot
+ * products are those of the other decode kernels (per block sum, times
+ * the scale, blocks added in order).  Only the summation orders differ.
+ */
+#include "bmk.h"
+#include "decode_state.h"
+#include "q8_common.h"
+
+namespace {
+
+using bmk::Blk;
+using bmk::block_dot;
+using bmk::load_block;
+
+constexpr int PT = 256;              /* threads per workgroup */
+constexpr int P_QKV = 4;             /* most row passes of a lane: q/k/v phase */
+constexpr int P_O = 2;               /*   o projection */
+constexpr int P_GU = 7;              /*   gate/up (two local rows per output) */
+constexpr int P_DN = 4;              /*   down projection */
+constexpr int P_MAX = 8;
+constexpr int XS_MAX = 4096;         /* floats of the staged input vector */
+constexpr int XR = XS_MAX / PT;      /* its elements per thread */
+constexpr int NW = 8;                /* RMSNorm elements per thread: D <= 2048 */
+constexpr int HD = 64;               /* head size */
+constexpr int KCH = 64;              /* keys of one attention sub-chunk (one per lane) */
+constexpr int APS_MAX = 8192;        /* floats of the staged attention partials */
+constexpr int APR = HD + 2;          /* one partial: max, sum, P.V[HD] */
+constexpr float SPIN_SECONDS = 0.2f;
+
+/* threadIdx.x, opaque to the compiler: address arithmetic built on it is
+ * redone in every phase instead of being hoisted out of the layer loop and
+ * held in registers for the whole kernel (that would crowd out the weight
+ * stages). */
+__device__ __forceinline__ int tid() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+static_assert(2 * KCH * HD <= APS_MAX, "the K and V sub-chunks share the partials' LDS");
+static_assert((DEC_PERSIST_NCH * APR) % 4 == 0, "partials are staged as float4");
+static_assert(P_QKV <= P_MAX && P_O <= P_MAX && P_GU <= P_MAX && P_DN <= P_MAX, "pass caps");
+
+/* Keeps the compiler from moving instructions across this point: loads
+ * issued before it leave before the ones after it (the CU serves them in
+ * order). */
+__device__ __forceinline__ void issue_order() { __builtin_amdgcn_sched_barrier(0); }
+
+/* Workgroup barrier for LDS data only: loads from global memory in flight
+ * stay in flight (__syncthreads would wait for them). */
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+/* DPP lane moves inside rows of 16 lanes (every source lane valid). */
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+constexpr int DPP_XOR1 = 0xB1;        /* quad_perm [1,0,3,2] */
+constexpr int DPP_XOR2 = 0x4E;        /* quad_perm [2,3,0,1] */
+constexpr int DPP_HALF_MIRROR = 0x141; /* lane i <- 7 - i within 8 */
+constexpr int DPP_MIRROR = 0x140;      /* lane i <- 15 - i within 16 */
+
+/* Sum / max over the 64 lanes of a wave (every lane gets it; all lanes active). */
+__device__ __forceinline__ float wsum(float v) {
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    v += dpp<DPP_HALF_MIRROR>(v);
+    v += dpp<DPP_MIRROR>(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float wmax(float v) {
+    v = fmaxf(v, dpp<DPP_XOR1>(v));
+    v = fmaxf(v, dpp<DPP_XOR2>(v));
+    v = fmaxf(v, dpp<DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp<DPP_MIRROR>(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+/* Sum over the workgroup (every thread gets it). */
+__device__ __forceinline__ float bsum(float v, float* sh) {
+    v = wsum(v);
+    lds_barrier(); /* earlier readers of sh are done */
+    if ((tid() & 63) == 0) sh[tid() >> 6] = v;
+    lds_barrier();
+    float r = 0.f;
+#pragma unroll
+    for (int i = 0; i < PT / 64; i++) r += sh[i];
+    return r;
+}
+
+/* Grid barrier among the working workgroups (see the file comment), in two
+ * halves: grid_arrive waits for every thread's loads and stores (the
+ * workgroup barrier's fence) and counts the workgroup in; grid_wait has
+ * thread 0 poll until `target` workgroups have arrived, then drops stale L1
+ * lines.  Returns false when this or another workgroup has given up.  The
+ * poll is a vector load, so it waits behind this CU's loads in flight:
+ * prefetches are issued early in a phase, and grid_arrive waits for them. */
+__device__ __forceinline__ void grid_arrive(DecState* st) {
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(&st->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool grid_wait(DecState* st, unsigned int target, int* flag) {
+    if (threadIdx.x == 0) {
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime(); /* 100 MHz */
+        const unsigned long long limit = (unsigned long long)(SPIN_SECONDS * 1e8f);
+        int ok = 1;
+        /* only the clock is checked while polling (a load of sync_error
+         * would add a round trip per poll): a workgroup stuck behind one that
+         * gave up gives up on its own clock */
+        while (__hip_atomic_load(&st->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+                __hip_atomic_store(&st->sync_error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        *flag = ok;
+    }
+    lds_barrier();
+    asm volatile("" ::: "memory"); /* no load moves above the wait */
+    return *flag != 0;
+}
+
+/* One workgroup's share of a matvec phase: output rows [r0, r1) of
+ * y = W xs (xs staged in LDS), or for SwiGLU the pairs (gate row j, up row
+ * j), j in [r0, r1), interleaved as local rows 2(j-r0) and 2(j-r0)+1.
+ * Lane t owns block column t % nb of row slot t / nb (nb <= PT); local row
+ * i = pass * slots + slot. */
+struct MvShare {
+    const unsigned char* w0; /* rows of W (gate for SwiGLU) */
+    const unsigned char* w1; /* up rows for SwiGLU */
+    int nb, r0, r1, glu;
+};
+
+__device__ __forceinline__ int mv_rows(const MvShare& j) { return (j.r1 - j.r0) * (j.glu ? 2 : 1); }
+
+/* Issues the share's block loads (one block per pass) into blk.  Every lane
+ * loads: lanes without a row of their own load the share's first block
+ * (row 0 of the matrix for an empty share) and their product is dropped. */
+template <int NP>
+__device__ __forceinline__ void mv_fetch(const MvShare& j, Blk (&blk)[NP]) {
+    const int t = tid(), nb = j.nb, slots = PT / nb, slot = t / nb, bc = t - slot * nb;
+    const int n = mv_rows(j);
+    const size_t row_bytes = (size_t)nb * 36;
+#pragma unroll
+    for (int p = 0; p < NP; p++) {
+        const int i = p * slots + slot;
+        const bool own = slot < slots && i < n;
+        const int ic = own ? i : 0;
+        const unsigned char* w = j.glu ? ((ic & 1) ? j.w1 : j.w0) : j.w0;
+        const int r = n > 0 ? j.r0 + (j.glu ? (ic >> 1) : ic) : 0;
+        blk[p] = load_block(w + (size_t)r * row_bytes + (size_t)(own ? bc : 0) * 36);
+    }
+}
+
+/* The block products of the fetched blocks with xs into red[local row][nb]. */
+template <int NP>
+__device__ __forceinline__ void mv_products(int n, int nb, const Blk (&blk)[NP], const float* xs, float* red) {
+    const int t = tid(), slots = PT / nb, slot = t / nb, bc = t - slot * nb;
+    if (slot < slots) {
+        float xv[32];
+#pragma unroll
+        for (int i = 0; i < 32; i += 4) {
+            const float4 v = *(const float4*)&xs[32 * bc + i];
+            xv[i] = v.x; xv[i + 1] = v.y; xv[i + 2] = v.z; xv[i + 3] = v.w;
+        }
+#pragma unroll
+        for (int p = 0; p < NP; p++) {
+            const int i = p * slots + slot;
+            if (i < n) red[i * nb + bc] = block_dot(blk[p], xv);
+        }
+    }
+    lds_barrier();
+}
+
+/* A row's block products added in block order. */
+__device__ __forceinline__ float row_sum(const float* rp, int nb) {
+    float acc = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < nb; k++) acc += rp[k];
+    return acc;
+}
+
+/* Products of the fetched blocks with xs, per-row sums, and the outputs of
+ * thread o < r1 - r0: y[r0 + o] = sum, or with a residual (the thread's
+ * row of the residual stream in *xres) y[r0 + o] = *xres += sum, or for
+ * SwiGLU y[r0 + o] = silu(gate) * up. */
+template <int NP>
+__device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP], const float* xs, float* red,
+                                          float* y, float* xres) {
+    const int nb = j.nb, o = tid();
+    mv_products(mv_rows(j), nb, blk, xs, red);
+    if (o < j.r1 - j.r0) {
+        if (j.glu) {
+            const float g = row_sum(red + (2 * o) * nb, nb), u = row_sum(red + (2 * o + 1) * nb, nb);
+            y[j.r0 + o] = (g / (1.0f + expf(-g))) * u;
+        } else {
+            const float acc = row_sum(red + o * nb, nb);
+            if (xres) {
+                *xres += acc;
+                y[j.r0 + o] = *xres;
+            } else {
+                y[j.r0 + o] = acc;
+            }
+        }
+    }
+}
+
+/* Loads of N elements per thread of a read-only vector of C floats (element
+ * threadIdx + k * PT; past the end: element C - 1, masked by the users). */
+template <int N>
+__device__ __forceinline__ void load_vec(const float* x, int C, float (&v)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; k++) v[k] = x[min(tid() + k * PT, C - 1)];
+}
+
+/* A float another CU wrote in the previous phase: an agent-scope load,
+ * which misses this CU's L1 and reads the XCD's L2 (a plain load could hit
+ * a stale L1 line). */
+__device__ __forceinline__ float ld_agent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+/* load_vec for a vector written in the previous phase. */
+template <int N>
+__device__ __forceinline__ void load_act(const float* x, int C, float (&v)[N]) {
+#pragma unroll
+    for (int k = 0; k < N; k++) v[k] = ld_agent(x + min(tid() + k * PT, C - 1));
+}
+
+/* xs = RMSNorm(x) * nw from x's loaded elements, C <= NW * PT (reference
+ * forward.metal:1019-1060: inv = 1/sqrt(mean(x^2) + eps), (x * inv) * w). */
+__device__ __forceinline__ void norm_to_lds(const float (&v)[NW], int C, const float (&nw)[NW], float eps, float* xs,
+                                            float* sh) {
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+        const float e = tid() + k * PT < C ? v[k] : 0.f;
+        ss = fmaf(e, e, ss);
+    }
+    ss = bsum(ss, sh);
+    const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+#pragma unroll
+    for (int k = 0; k < NW; k++) {
+        const int i = tid() + k * PT;
+        if (i < C) xs[i] = (v[k] * inv) * nw[k];
+    }
+    lds_barrier();
+}
+
+/* xs = x from its loaded elements, C <= XS_MAX. */
+__device__ __forceinline__ void vec_to_lds(const float (&v)[XR], int C, float* xs) {
+#pragma unroll
+    for (int k = 0; k < XR; k++) {
+        const int i = tid() + k * PT;
+        if (i < C) xs[i] = v[k];
+    }
+    lds_barrier();
+}
+
+/* The workgroup's rows of a matrix with R rows: an even split over DEC_PERSIST_WGS. */
+__device__ __forceinline__ void share_rows(int R, int w, int& r0, int& r1) {
+    r0 = (int)((long)R * w / DEC_PERSIST_WGS);
+    r1 = (int)((long)R * (w + 1) / DEC_PERSIST_WGS);
+}
+
+/* One attention piece (KV head kh, key chunk c of the keys 0..pos):
+ * keys [k0, k1), of which those below lim are in the cache and key pos (if
+ * here) is this step's. */
+struct Piece {
+    int kh, c, kv_mul, nq, nraw, k0, k1, lim;
+    float* kT; /* the KV head's K cache, [HD/4][MS] float4 */
+    float* vc; /* its V cache rows, stride KV */
+};
+
+__device__ __forceinline__ Piece make_piece(const DecPersist& a, int layer, int w, int pos) {
+    Piece p;
+    p.kh = w / DEC_PERSIST_NCH;
+    p.c = w % DEC_PERSIST_NCH;
+    p.kv_mul = a.NH / a.NKV;
+    p.nq = p.kv_mul * HD;
+    p.nraw = p.nq + 2 * HD;
+    const int S = pos + 1, cs = (S + DEC_PERSIST_NCH - 1) / DEC_PERSIST_NCH;
+    p.k0 = p.c * cs;
+    p.k1 = min(S, p.k0 + cs);
+    p.lim = min(p.k1, pos);
+    const size_t slab = (size_t)a.MS * a.KV;
+    p.kT = a.kvc + (size_t)layer * 2 * slab + (size_t)p.kh * HD * a.MS;
+    p.vc = a.kvc + ((size_t)layer * 2 + 1) * slab + p.kh * HD;
+    return p;
+}
+
+/* Keys and values of one attention sub-chunk from the cache, 4 float4 of
+ * each per thread on their way to LDS (K as [HD/4][KCH] float4, V as
+ * [KCH][HD]); q, k, v of the KV head (raw, [q heads | k | v]). */
+constexpr int KV4 = KCH * HD / 4 / PT;
+typedef float f4 __attribute__((ext_vector_type(4))); /* plain vector loads and stores (no memcpy) */
+struct AttnRegs {
+    f4 k[KV4];
+    f4 v[KV4];
+    float r0, r1;
+};
+
+__device__ __forceinline__ void load_kv(const DecPersist& a, const Piece& p, int base, AttnRegs& r) {
+    const int t = tid();
+#pragma unroll
+    for (int j = 0; j < KV4; j++) {
+        const int f = t + PT * j;
+        const int kkey = base + f % KCH, jj = f / KCH;
+        r.k[j] = *(const f4*)(p.kT + ((size_t)jj * a.MS + (kkey < p.lim ? kkey : 0)) * 4);
+        const int vkey = base + f / (HD / 4);
+        r.v[j] = *(const f4*)(p.vc + (size_t)(vkey < p.lim ? vkey : 0) * a.KV + (f % (HD / 4)) * 4);
+    }
+}
+
+/* Issues every load of a piece's first sub-chunk: q, k, v and the cached keys and values. */
+__device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, AttnRegs& r) {
+    const int t = tid();
+    auto raw = [&](int i) {
+        i = min(i, p.nraw - 1);
+        return ld_agent(i < p.nq ? a.q + (size_t)p.kh * p.nq + i
+                                 : i < p.nq + HD ? a.k + p.kh * HD + i - p.nq : a.v + p.kh * HD + i - p.nq - HD);
+    };
+    r.r0 = raw(t);
+    r.r1 = raw(t + PT);
+    load_kv(a, p, p.k0, r);
+}
+
+/* The sub-chunk's cached keys and values into LDS. */
+__device__ __forceinline__ void put_kv(const Piece& p, int base, const AttnRegs& r, f4* kst, float* vst) {
+#pragma unroll
+    for (int j = 0; j < KV4; j++) {
+        const int f = tid() + PT * j;
+        if (base + f % KCH < p.lim) kst[f] = r.k[j];
+        const int kk = f / (HD / 4);
+        if (base + kk < p.lim) *(f4*)&vst[kk * HD + (f % (HD / 4)) * 4] = r.v[j];
+    }
+}
+
+/* Attention piece (see Piece) of one layer: RoPE of the group's query heads
+ * and of the current key (in registers: lane d of a head's wave pairs with
+ * lane d ^ 32; rc, rs = cos, sin of the lane's rotation angle), the KV
+ * append by the piece holding pos, then per query head (one wave each) the
+ * online softmax over the chunk's keys in sub-chunks of KCH (lane = key for
+ * the scores, lane = dimension for P.V, the sub-chunk's values in LDS),
+ * written as (max, sum, P.V[HD]) to the partial buffer. */
+__device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p, int pos, float rc, float rs, AttnRegs& r,
+                             float* lds, float* kvs) {
+    const int t = tid(), wave = t >> 6, lane = t & 63;
+    const int qk = p.nq + HD; /* roped elements */
+    f4* kst = (f4*)kvs;
+    float* vst = kvs + KCH * HD;
+    {
+        const float x0 = r.r0, x1 = r.r1;
+        const float y0 = __shfl_xor(x0, 32, 64), y1 = __shfl_xor(x1, 32, 64);
+        const float o0 = t >= qk ? x0 : lane < 32 ? x0 * rc - y0 * rs : y0 * rs + x0 * rc;
+        const float o1 = t + PT >= qk ? x1 : lane < 32 ? x1 * rc - y1 * rs : y1 * rs + x1 * rc;
+        if (t < p.nraw) lds[t] = o0;
+        if (t + PT < p.nraw) lds[t + PT] = o1;
+        /* this step's key column and value row of the sub-chunk */
+        if (pos < p.k0 + KCH && p.k1 == pos + 1) {
+            const int kk = pos - p.k0;
+            float* row = vst + kk * HD;
+            if (t >= p.nq && t < qk) ((float*)&kst[((t - p.nq) >> 2) * KCH + kk])[(t - p.nq) & 3] = o0;
+            if (t + PT >= p.nq && t + PT < qk) ((float*)&kst[((t + PT - p.nq) >> 2) * KCH + kk])[(t + PT - p.nq) & 3] = o1;
+            if (t >= qk && t < p.nraw) row[t - qk] = x0;
+            if (t + PT >= qk && t + PT < p.nraw) row[t + PT - qk] = x1;
+        }
+    }
+    put_kv(p, p.k0, r, kst, vst);
+    lds_barrier();
+    const float* kc = lds + p.nq;      /* roped current key */
+    const float* vr = lds + p.nq + HD; /* current value */
+    if (p.k1 == pos + 1 && t < HD) { /* this piece holds position pos: append it */
+        p.kT[((size_t)(t >> 2) * a.MS + pos) * 4 + (t & 3)] = kc[t];
+        p.vc[(size_t)pos * a.KV + t] = vr[t];
+    }
+    const float* q = lds + wave * HD;
+    float m_run = -INFINITY, l_run = 0.f, acc = 0.f;
+    for (int base = p.k0;;) {
+        const int n = min(KCH, p.k1 - base);
+        if (wave < p.kv_mul) {
+            float s = -INFINITY;
+            if (lane < n) {
+                float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < HD / 4; jj++) {
+                    const f4 k4 = kst[jj * KCH + lane];
+                    s0 = fmaf(q[4 * jj + 0], k4.x, s0);
+                    s1 = fmaf(q[4 * jj + 1], k4.y, s1);
+                    s2 = fmaf(q[4 * jj + 2], k4.z, s2);
+                    s3 = fmaf(q[4 * jj + 3], k4.w, s3);
+                }
+                s = ((s0 + s1) + (s2 + s3)) * a.scale;
+            }
+            const float cmax = wmax(s);
+            const float pe = lane < n ? expf(s - cmax) : 0.f;
+            const float csum = wsum(pe);
+            const float m_new = fmaxf(m_run, cmax);
+            const float a_old = expf(m_run - m_new), a_new = expf(cmax - m_new);
+            float part = 0.f;
+#pragma unroll 8
+            for (int jk = 0; jk < n; jk++) part = fmaf(lane_value(pe, jk), vst[jk * HD + lane], part);
+            l_run = l_run * a_old + csum * a_new;
+            acc = acc * a_old + part * a_new;
+            m_run = m_new;
+        }
+        base += KCH;
+        if (base >= p.k1) break;
+        lds_barrier(); /* every wave is done with this sub-chunk's keys and values */
+        load_kv(a, p, base, r);
+        put_kv(p, base, r, kst, vst);
+        if (pos >= base && pos < base + KCH && p.k1 == pos + 1 && t < HD) {
+            ((float*)&kst[(t >> 2) * KCH + pos - base])[t & 3] = kc[t];
+            vst[(pos - base) * HD + t] = vr[t];
+        }
+        lds_barrier();
+    }
+    if (wave < p.kv_mul) {
+        float* pr = a.apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        pr[2 + lane] = acc;
+        if (lane == 0) {
+            pr[0] = m_run;
+            pr[1] = l_run;
+        }
+    }
+}
+
+/* The partials of a chunk without keys. */
+__device__ __forceinline__ void attn_empty(const DecPersist& a, const Piece& p) {
+    const int wave = tid() >> 6, lane = tid() & 63;
+    if (wave < p.kv_mul) {
+        float* pr = a.apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        pr[2 + lane] = 0.f;
+        if (lane == 0) {
+            pr[0] = -INFINITY;
+            pr[1] = 0.f;
+        }
+    }
+}
+
+/* Attention output of every query head from the partials of its chunks,
+ * staged into LDS with one round of loads (after_loads then issues more
+ * loads, once the partials' registers are free):
+ * out[h][d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c, the
+ * weights e^(m_c - M) computed once per (head, chunk) (ew). */
+template <typename F>
+__device__ __forceinline__ void attn_merge(const DecPersist& a, float* aps, float* ew, float* xs, F&& after_loads) {
+    const int total4 = a.NH * DEC_PERSIST_NCH * APR / 4;
+    const f4* src = (const f4*)a.apart;
+    f4 v[APS_MAX / 4 / PT];
+#pragma unroll
+    for (int k = 0; k < APS_MAX / 4 / PT; k++) {
+        const float* e = (const float*)(src + min(tid() + k * PT, total4 - 1));
+        v[k] = f4{ld_agent(e), ld_agent(e + 1), ld_agent(e + 2), ld_agent(e + 3)};
+    }
+    issue_order();
+#pragma unroll
+    for (int k = 0; k < APS_MAX / 4 / PT; k++) {
+        const int i = tid() + k * PT;
+        if (i < total4) ((f4*)aps)[i] = v[k];
+    }
+    issue_order();
+    after_loads();
+    lds_barrier();
+    /* ew[h][c] = e^(m_c - M_h), one thread per (head, chunk); 0 for a chunk
+     * without keys */
+    if (tid() < a.NH * DEC_PERSIST_NCH) {
+        const int h = tid() / DEC_PERSIST_NCH, c = tid() - h * DEC_PERSIST_NCH;
+        const float* pr = aps + h * DEC_PERSIST_NCH * APR;
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < DEC_PERSIST_NCH; k++) M = fmaxf(M, pr[k * APR]);
+        const float m = pr[c * APR];
+        ew[tid()] = m == -INFINITY ? 0.f : expf(m - M);
+    }
+    lds_barrier();
+    for (int i = tid(); i < a.NH * HD; i += PT) {
+        const int h = i / HD, d = i - h * HD;
+        const float* pr = aps + h * DEC_PERSIST_NCH * APR;
+        const float* e = ew + h * DEC_PERSIST_NCH;
+        float L = 0.f, A = 0.f;
+#pragma unroll
+        for (int c = 0; c < DEC_PERSIST_NCH; c++) {
+            L = fmaf(e[c], pr[c * APR + 1], L);
+            A = fmaf(e[c], pr[c * APR + 2 + d], A);
+        }
+        xs[i] = A / L;
+    }
+    lds_barrier();
+}
+
+__global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
+    if (blockIdx.x % 8) return; /* the working workgroups all sit on XCD 0 */
+    const int w = (int)blockIdx.x / 8;
+    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
+    __shared__ float red[P_MAX * PT];
+    __shared__ __attribute__((aligned(16))) float big[APS_MAX]; /* attention partials, or one K and V sub-chunk */
+    __shared__ float sh[PT / 64];
+    __shared__ float ew[XS_MAX / HD * DEC_PERSIST_NCH]; /* attention merge weights */
+    __shared__ int flag;
+    DecState* st = a.st;
+    const int pos = st->pos;
+    const int D = a.D, H = a.H, QD = a.QD, KV = a.KV;
+    const bool has_piece = w < a.NKV * DEC_PERSIST_NCH;
+    unsigned int target = 0;
+
+    /* cos, sin of the step's RoPE angle for rotary pair lane % 32 */
+    float rc, rs;
+    {
+        const float ang = (float)pos * a.inv_freq[tid() & (HD / 2 - 1)];
+        rc = cosf(ang);
+        rs = sinf(ang);
+    }
+    /* the rows of x this workgroup updates (o and down split D the same way) */
+    float xres = 0.f;
+    {
+        int r0, r1;
+        share_rows(D, w, r0, r1);
+        if (tid() < r1 - r0) xres = a.x[r0 + tid()];
+    }
+
+    /* the shares of this workgroup in the four matvec phases of a layer */
+    auto shares = [&](int l, MvShare& qkv0, MvShare& qkv1, MvShare& qkv2, MvShare& o, MvShare& gu, MvShare& dn) {
+        const unsigned char* wl = a.w + (size_t)l * a.layer_bytes;
+        const int nbD = D / 32;
+        int r0, r1;
+        /* q, k, v as one list of QD + 2 KV rows split evenly */
+        share_rows(QD + 2 * KV, w, r0, r1);
+        qkv0 = {wl + a.off[0], nullptr, nbD, min(r0, QD), min(r1, QD), 0};
+        qkv1 = {wl + a.off[1], nullptr, nbD, min(max(r0 - QD, 0), KV), min(max(r1 - QD, 0), KV), 0};
+        qkv2 = {wl + a.off[2], nullptr, nbD, min(max(r0 - QD - KV, 0), KV), min(max(r1 - QD - KV, 0), KV), 0};
+        share_rows(D, w, r0, r1);
+        o = {wl + a.off[3], nullptr, QD / 32, r0, r1, 0};
+        share_rows(H, w, r0, r1);
+        gu = {wl + a.off[4], wl + a.off[5], nbD, r0, r1, 1};
+        share_rows(D, w, r0, r1);
+        dn = {wl + a.off[6], nullptr, H / 32, r0, r1, 0};
+    };
+    /* q, k and v rows of one workgroup come from at most three matrices:
+     * their blocks share one register stage, each matrix's rows in order;
+     * lanes without a row load the first one (or row 0 of q) */
+    auto fetch_qkv = [&](const MvShare& s0, const MvShare& s1, const MvShare& s2, Blk(&blk)[P_QKV]) {
+        const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0;
+        const int t = tid(), nb = s0.nb, slots = PT / nb, slot = t / nb, bc = t - slot * nb;
+        const int n = n0 + n1 + (s2.r1 - s2.r0);
+        const size_t row_bytes = (size_t)nb * 36;
+#pragma unroll
+        for (int p = 0; p < P_QKV; p++) {
+            const int i = p * slots + slot;
+            const bool own = slot < slots && i < n;
+            const unsigned char* base = s0.w0;
+            int r = 0;
+            if (own) {
+                if (i < n0) { base = s0.w0; r = s0.r0 + i; }
+                else if (i < n0 + n1) { base = s1.w0; r = s1.r0 + i - n0; }
+                else { base = s2.w0; r = s2.r0 + i - n0 - n1; }
+            }
+            blk[p] = load_block(base + (size_t)r * row_bytes + (size_t)(own ? bc : 0) * 36);
+        }
+    };
+    auto finish_qkv = [&](const MvShare& s0, const MvShare& s1, const MvShare& s2, const Blk(&blk)[P_QKV]) {
+        const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0, n2 = s2.r1 - s2.r0;
+        const int nb = s0.nb, o = tid();
+        mv_products(n0 + n1 + n2, nb, blk, xs, red);
+        if (o < n0 + n1 + n2) {
+            const float acc = row_sum(red + o * nb, nb);
+            if (o < n0) a.q[s0.r0 + o] = acc;
+            else if (o < n0 + n1) a.k[s1.r0 + o - n0] = acc;
+            else a.v[s2.r0 + o - n0 - n1] = acc;
+        }
+    };
+    auto fetch_norm = [&](const float* nwp, float(&nw)[NW]) { load_vec(nwp, D, nw); };
+
+    Blk bq[P_QKV], bo[P_O], bg[P_GU], bd[P_DN];
+    float nw[NW];
+    MvShare q0, q1, q2, so, sg, sd;
+    shares(0, q0, q1, q2, so, sg, sd);
+    fetch_qkv(q0, q1, q2, bq);
+    fetch_norm(a.ln1, nw);
+    for (int l = 0; l < a.L; l++) {
+        /* 1. RMSNorm + q, k, v; o's weights stream in behind x */
+        {
+            float v[NW];
+            load_act(a.x, D, v);
+            issue_order();
+            mv_fetch(so, bo);
+            norm_to_lds(v, D, nw, a.eps, xs, sh);
+        }
+        finish_qkv(q0, q1, q2, bq);
+        grid_arrive(st);
+        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        /* 2. RoPE + KV append + attention pieces */
+        {
+            const Piece pc = make_piece(a, l, w, pos);
+            const bool live = has_piece && pc.k0 < pc.k1;
+            AttnRegs ar;
+            if (live) attn_load(a, pc, ar);
+            issue_order();
+            fetch_norm(a.ln2 + (size_t)l * D, nw);
+            if (live) attn_compute(a, pc, pos, rc, rs, ar, xs, big);
+            else if (has_piece) attn_empty(a, pc);
+        }
+        grid_arrive(st);
+        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        /* 3. merge + o + residual; gate/up weights stream in behind the partials */
+        attn_merge(a, big, ew, xs, [&] { mv_fetch(sg, bg); });
+        mv_finish(so, bo, xs, red, a.x, &xres);
+        grid_arrive(st);
+        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        /* 4. RMSNorm + gate, up + SwiGLU; down's weights stream in behind x */
+        {
+            float v[NW];
+            load_act(a.x, D, v);
+            issue_order();
+            mv_fetch(sd, bd);
+            norm_to_lds(v, D, nw, a.eps, xs, sh);
+        }
+        mv_finish(sg, bg, xs, red, a.h, nullptr);
+        grid_arrive(st);
+        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        /* 5. down + residual; the next layer's q, k, v and first RMSNorm
+         * weights stream in behind h (after the last layer: the last
+         * layer's again, unused; no branch, so that h's loads stay first) */
+        {
+            float v[XR];
+            load_act(a.h, H, v);
+            issue_order();
+            const int ln = min(l + 1, a.L - 1);
+            shares(ln, q0, q1, q2, so, sg, sd);
+            fetch_qkv(q0, q1, q2, bq);
+            fetch_norm(a.ln1 + (size_t)ln * D, nw);
+            issue_order();
+            vec_to_lds(v, H, xs);
+        }
+        mv_finish(sd, bd, xs, red, a.x, &xres);
+        grid_arrive(st);
+        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+    }
+}
+
+} // namespace
+
+/* Whether the persistent step can run this shape: head size 64, every
+ * phase's share within its register stage, one output row per thread, and
+ * the vectors within their LDS stages. */
+extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
+    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XS_MAX ||
+        NH * HD > XS_MAX || NH * DEC_PERSIST_NCH * APR > APS_MAX || MS <= 0)
+        return 0;
+    const int QD = NH * HD, KV = NKV * HD;
+    auto passes = [](int rows_per_wg, int nb) { return nb > PT ? P_MAX + 1 : (rows_per_wg + PT / nb - 1) / (PT / nb); };
+    const int w = DEC_PERSIST_WGS;
+    const int qkv = (QD + 2 * KV + w - 1) / w, dr = (D + w - 1) / w, hr = (H + w - 1) / w;
+    if (qkv > PT || dr > PT || hr > PT) return 0;
+    if (passes(qkv, D / 32) > P_QKV) return 0;
+    if (passes(dr, QD / 32) > P_O) return 0;
+    if (passes(2 * hr, D / 32) > P_GU) return 0;
+    if (passes(dr, H / 32) > P_DN) return 0;
+    if (NKV * DEC_PERSIST_NCH > w) return 0;
+    return 1;
+}
+
+extern "C" int dec_launch_persist(const DecPersist* a, hipStream_t s) {
+    hipLaunchKernelGGL(k_dec_persist, dim3(8 * DEC_PERSIST_WGS), dim3(PT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}

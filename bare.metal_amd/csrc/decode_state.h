@@ -37,6 +37,8 @@ typedef struct {
     unsigned int done;/* head workgroups finished in the current step */
     int B;
     int bad_token;    /* set when an input token was outside [0, V) (0 was used instead) */
+    int sync_error;   /* set (and kept) when a barrier of the persistent step kernel timed out */
+    unsigned int bar; /* barrier counter of the persistent step kernel, zeroed by the embedding kernel */
     int pad_;
     int token[DEC_MAX_B];        /* input token of the current step */
     int host_token[DEC_MAX_B];
@@ -101,6 +103,30 @@ typedef struct {
     int D, V, B, tiles;
     float eps;
 } DecHead;
+
+/* Every layer of a batch-1 decode step in one persistent kernel on one
+ * XCD (decode_persist.hip): DEC_PERSIST_WGS working workgroups, attention
+ * split into DEC_PERSIST_NCH key chunks per KV head. */
+#define DEC_PERSIST_WGS 32
+#define DEC_PERSIST_NCH 10
+typedef struct {
+    float* x;                  /* [D] residual stream */
+    float* q;                  /* [NH*HD] */
+    float* k;                  /* [KV] */
+    float* v;                  /* [KV] */
+    float* h;                  /* [H] */
+    float* apart;              /* [NH][DEC_PERSIST_NCH][HD + 2] attention partials (max, sum, P.V) */
+    float* kvc;                /* the session's KV cache, batch row 0 */
+    DecState* st;
+    const unsigned char* w;    /* Q8 arena of layer 0; layer l at w + l * layer_bytes */
+    unsigned long long layer_bytes;
+    unsigned long long off[7]; /* q, k, v, o, gate, up, down within a layer */
+    const float* ln1;          /* [L][D] */
+    const float* ln2;          /* [L][D] */
+    float inv_freq[DEC_MAX_HD / 2];
+    float scale, eps;
+    int D, H, NH, NKV, HD, KV, QD, MS, L;
+} DecPersist;
 
 /* Input embedding of a decode step: x[b] = emb[token_b]. */
 typedef struct {

@@ -59,6 +59,8 @@ int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C,
                     int n_tiles, hipStream_t s);
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
+int dec_persist_ok(int D, int H, int NH, int NKV, int HD, int MS);
+int dec_launch_persist(const DecPersist* a, hipStream_t s);
 int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q8_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
 }
@@ -131,6 +133,8 @@ struct bm_session_s {
     size_t h_io_cap;
     int pos;             /* host mirror of the position */
     int use_graph;
+    int persist;         /* 1: the layers of a step run as one persistent kernel (B = 1, Q8, MI355X) */
+    float* apart;        /* attention partials of the persistent kernel */
     hipGraph_t graph;
     hipGraphExec_t gexec;
     int prof_on;
@@ -414,7 +418,8 @@ static int model_compile(bm_model_t* m) {
     const size_t per[7] = {(size_t)QD * D, (size_t)KV * D, (size_t)KV * D, (size_t)D * QD,
                            (size_t)H * D, (size_t)H * D, (size_t)D * H};
     const int src_t[7] = {T_WQ, T_WK, T_WV, T_WO, T_WG, T_WU, T_WD};
-    size_t stage_n = (size_t)H * D;
+    size_t stage_n = 0; /* the largest matrix staged (q and o are the largest when QD > H) */
+    for (int i = 0; i < 7; i++) stage_n = per[i] > stage_n ? per[i] : stage_n;
     if (m->q8_head) stage_n = (size_t)m->V * D > stage_n ? (size_t)m->V * D : stage_n;
     float* stage = NULL;
     HIP_TRY(hipMalloc(&stage, stage_n * sizeof(float)), "hipMalloc", { model_free_device(m); return -1; });
@@ -470,7 +475,7 @@ extern "C" const char* bm_get_arch_name(const bm_model_t* m) { return m ? "llama
 /* session */
 
 /* Kernel kinds of a step, in launch order within a layer. */
-enum { PH_EMBED, PH_QKV, PH_ATTN, PH_O, PH_GATEUP, PH_DOWN, PH_HEAD };
+enum { PH_EMBED, PH_QKV, PH_ATTN, PH_O, PH_GATEUP, PH_DOWN, PH_HEAD, PH_LAYERS };
 
 /* Profiled steps: an event after every kernel, tagged with the phase the
  * interval before it belongs to (-1: the step's first event). */
@@ -495,7 +500,24 @@ static int enqueue_step(bm_session_t* S) {
     e.B = B;
     if (mark(S, -1) || dec_launch_embed(&e, s) || mark(S, PH_EMBED)) return -1;
     const float eps = 1e-5f; /* reference graph.c:134,175,219 */
-    for (int l = 0; l < m->L; l++) {
+    if (S->persist == 1) {
+        DecPersist pa;
+        memset(&pa, 0, sizeof pa);
+        pa.x = S->x; pa.q = S->q; pa.k = S->k; pa.v = S->v; pa.h = S->h; pa.apart = S->apart; pa.kvc = S->kvc;
+        pa.st = S->st; pa.w = m->d_q8; pa.layer_bytes = m->layer_bytes;
+        for (int i = 0; i < 7; i++) pa.off[i] = m->off[i];
+        pa.ln1 = m->d_ln1; pa.ln2 = m->d_ln2;
+        const float rp[6] = {m->arch.rope_theta, m->arch.rope_factor, m->arch.rope_low_freq_factor,
+                             m->arch.rope_high_freq_factor, m->arch.rope_original_max,
+                             m->arch.rope_scaling == BM_ROPE_LLAMA3 ? 1.0f : 0.0f};
+        bmk_rope_table(rp, m->HD, pa.inv_freq);
+        pa.scale = 1.0f / sqrtf((float)m->HD); /* reference scheduler.c:914 */
+        pa.eps = eps;
+        pa.D = D; pa.H = m->H; pa.NH = m->NH; pa.NKV = m->NKV; pa.HD = m->HD; pa.KV = m->KV; pa.QD = m->QD;
+        pa.MS = S->MS; pa.L = m->L;
+        if (dec_launch_persist(&pa, s) || mark(S, PH_LAYERS)) return -1;
+    }
+    for (int l = 0; l < (S->persist == 1 ? 0 : m->L); l++) {
         const unsigned char* wl = m->d_q8 + (size_t)l * m->layer_bytes;
         DecMv mv;
         memset(&mv, 0, sizeof mv);
@@ -559,6 +581,7 @@ static void session_free(bm_session_t* S) {
     if (!S) return;
     if (S->ctx) hipStreamSynchronize(S->ctx->s);
     if (S->gexec) hipGraphExecDestroy(S->gexec);
+    hipFree(S->apart);
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
     hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->prompt); hipFree(S->out_tokens);
@@ -627,6 +650,15 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
         S->h_io_cap = B * (size_t)S->MS + 64;
         ok = hipHostMalloc(&S->h_io, S->h_io_cap * 4, hipHostMallocDefault) == hipSuccess;
     }
+    /* The persistent step kernel keeps its workgroups on one XCD by launching
+     * 8 per working one (MI355X places workgroup b on XCD b % 8): only on
+     * gfx950 with the whole device's 256 CUs, batch 1, Q8 projections and a
+     * shape it handles. */
+    if (ok && batch == 1 && m->quant_bits == 8 && strncmp(ctx->be->dev_name, "gfx950", 6) == 0 &&
+        ctx->be->dev_cu_count == 256 && dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
+        ok = hipMalloc(&S->apart, (size_t)m->NH * DEC_PERSIST_NCH * (m->HD + 2) * 4) == hipSuccess;
+        S->persist = ok;
+    }
     /* a cache slot is written before it is read, but start from zeros anyway */
     if (ok) ok = hipMemsetAsync(S->kvc, 0, kv_elems * 4, ctx->s) == hipSuccess;
     if (ok) ok = session_reset_state(S, 1, 0) == 0;
@@ -649,6 +681,20 @@ extern "C" void bm_destroy_session(bm_session_t* S) { session_free(S); }
 extern "C" int bm_session_set_graph(bm_session_t* S, int on) {
     if (!S) return -1;
     S->use_graph = on != 0;
+    return 0;
+}
+
+extern "C" int bm_session_set_persistent(bm_session_t* S, int on) {
+    if (!S) return -1;
+    if (S->persist == 0) return on ? -1 : 0; /* not available for this session */
+    const int want = on ? 1 : 2;
+    if (S->persist != want && S->gexec) { /* the captured step is the other form */
+        hipGraphExecDestroy(S->gexec);
+        hipGraphDestroy(S->graph);
+        S->gexec = NULL;
+        S->graph = NULL;
+    }
+    S->persist = want;
     return 0;
 }
 
@@ -739,7 +785,14 @@ static float* step_host(bm_session_t* S, const int* tokens) {
     HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "event", return NULL);
     HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)S->B * m->V * 4, hipMemcpyDeviceToHost, S->ctx->s),
             "logits read", return NULL);
+    if (S->persist == 1)
+        HIP_TRY(hipMemcpyAsync(&S->h_st->sync_error, &S->st->sync_error, 4, hipMemcpyDeviceToHost, S->ctx->s),
+                "state read", return NULL);
     HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+    if (S->persist == 1 && S->h_st->sync_error) {
+        BMK_ERR("decode step: a barrier of the persistent step kernel timed out (the step's results are void)");
+        return NULL;
+    }
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess) S->busy_ms += ms;
     S->launches++;
@@ -1132,9 +1185,9 @@ extern "C" int bm_generate_greedy(bm_session_t* S, const int* prompt, int n_prom
     HIP_TRY(hipMemcpyAsync(S->h_st, S->st, sizeof(DecState), hipMemcpyDeviceToHost, S->ctx->s), "state read",
             return -1);
     HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
-    if (S->h_st->n_out != n_out || S->h_st->pos != steps || S->h_st->bad_token) {
-        BMK_ERR("bm_generate_greedy: device state n_out=%d pos=%d bad_token=%d, expected n_out=%d pos=%d",
-                S->h_st->n_out, S->h_st->pos, S->h_st->bad_token, n_out, steps);
+    if (S->h_st->n_out != n_out || S->h_st->pos != steps || S->h_st->bad_token || S->h_st->sync_error) {
+        BMK_ERR("bm_generate_greedy: device state n_out=%d pos=%d bad_token=%d sync_error=%d, expected n_out=%d pos=%d",
+                S->h_st->n_out, S->h_st->pos, S->h_st->bad_token, S->h_st->sync_error, n_out, steps);
         return -1;
     }
     memcpy(out_tokens, S->h_io, nt * 4);

@@ -220,6 +220,15 @@ int            bm_generate_greedy(bm_session_t* sess, const int* prompt, int n_p
  * captured graph (same kernels, same results).  Default 1. */
 int            bm_session_set_graph(bm_session_t* sess, int on);
 
+/* 1 (default where available): a batch-1 session with Q8 projections on
+ * MI355X runs every layer of a decode step as one persistent kernel on one
+ * XCD (five phases per layer separated by in-kernel barriers); 0: one
+ * kernel per fused phase, as batched sessions do.  Both compute the same
+ * formulas in fp32 (summation orders differ).  Returns 0, or -1 when the
+ * persistent form is not available for the session (then only 0 is
+ * accepted). */
+int            bm_session_set_persistent(bm_session_t* sess, int on);
+
 /* GPU time (HIP events around each submission) and submissions of the
  * session's host-driven steps and one-pass prefills, the counterpart of the
  * reference backend's busy time and command-buffer count
@@ -230,8 +239,10 @@ int            bm_session_gpu_stats(bm_session_t* sess, double* busy_ms, unsigne
 /* Per-kernel-kind GPU ms accumulated since bm_profile_begin, in step order:
  * [0] embedding, [1] RMSNorm + q/k/v, [2] RoPE + KV append + attention,
  * [3] o + residual, [4] RMSNorm + gate/up + SwiGLU, [5] down + residual,
- * [6] final norm + LM head + argmax.  Returns the number of profiled steps. */
-#define BM_PROF_PHASES 7
+ * [6] final norm + LM head + argmax, [7] every layer as one persistent
+ * kernel (batch-1 sessions that use it; [1]..[5] are then 0).  Returns the
+ * number of profiled steps. */
+#define BM_PROF_PHASES 8
 long           bm_profile_phases(bm_session_t* sess, double* ms);
 
 /* No counterpart in the reference.  For callers that cannot allocate device

@@ -413,6 +413,8 @@ def test_smollm2_135m_config5_greedy():
     assert max(errs) <= LOGIT_TOL, max(errs)
     n, ties = check_tokens(got1, toks, marg, abs_err)
     print(f"135M greedy: {n}/{n_gen} tokens identical before any tie (tie stops: {ties}), max logit err {max(errs):.2e}")
+    # every one of the 256 tokens equals the oracle's (no near-tie on this sequence)
+    assert (n, ties) == (n_gen, 0), (n, ties)
     eng.close()
     eb = bmhip.Engine(dims, max_seq_len=384, seed=seed, batch=B)
     gotb = eb.generate(prompts, steps)
@@ -484,3 +486,101 @@ def test_q4_from_bf16_checkpoint(tmp_path):
         worst = max(worst, normwise(eng.step(int(t)), orc.step(int(t), pos)))
     eng.close()
     assert worst <= LOGIT_TOL, worst
+
+
+def test_smollm2_135m_batch32_rows_match_oracle():
+    """The B = 32 engine at SmolLM2-135M shapes (batched fp32-MFMA matvecs,
+    attention per KV-head group, batched head) against the oracle, teacher
+    forced: rows 0, 17 and 31, each fed its own config-5 prompt tokens, give
+    each position's logits within the per-step bar of the oracle run over
+    the same tokens."""
+    dims = bmhip.SMOLLM2_135M
+    seed, B, n = 2025, 32, 24
+    prompts = bmhip.synth_uniform_int(seed, 0, dims["V"], B * 128).reshape(B, 128)
+    w = bmhip.synthetic_weights(dims, seed)
+    eb = bmhip.Engine(dims, max_seq_len=64, seed=seed, batch=B)
+    rows = (0, 17, 31)
+    orcs = {b: oracle_decoder(dims, w, 64, nthreads=16) for b in rows}
+    worst = 0.0
+    for pos in range(n):
+        lg = eb.step_batch(prompts[:, pos])
+        for b in rows:
+            err = normwise(lg[b], orcs[b].step(int(prompts[b, pos]), pos))
+            worst = max(worst, err)
+            assert err <= LOGIT_TOL, (pos, b, err)
+    eb.close()
+    print(f"135M B=32 rows {rows}: max normwise logit error {worst:.2e} over {n} positions")
+
+
+def test_persistent_step_matches_phase_kernels_and_oracle():
+    """Batch-1 SmolLM2-135M steps with every layer in one persistent kernel
+    (bm_session_set_persistent) against the same session's per-phase
+    kernels and the oracle: logits per step within the per-step bar, over
+    140 positions (the attention's key chunks and sub-chunks of 64 all in
+    use), then greedy generation identical in both forms."""
+    dims = bmhip.SMOLLM2_135M
+    seed = 2025
+    w = bmhip.synthetic_weights(dims, seed)
+    toks = bmhip.synth_uniform_int(77, 0, dims["V"], 140)
+    a = bmhip.Engine(dims, max_seq_len=192, seed=seed)
+    b = bmhip.Engine(dims, max_seq_len=192, seed=seed)
+    if not a.set_persistent(True):
+        a.close()
+        b.close()
+        pytest.skip("the persistent step kernel is not available on this device")
+    assert b.set_persistent(False)
+    orc = oracle_decoder(dims, w, 192, nthreads=16)
+    worst = worst_o = 0.0
+    for pos, t in enumerate(toks):
+        ya, yb = a.step(int(t)), b.step(int(t))
+        worst = max(worst, normwise(ya, yb.astype(np.float64)))
+        if pos % 7 == 0 or pos >= 128:
+            worst_o = max(worst_o, normwise(ya, orc.step(int(t), pos)))
+        else:
+            orc.step(int(t), pos)
+    assert worst <= LOGIT_TOL and worst_o <= LOGIT_TOL, (worst, worst_o)
+    prompt = toks[:20]
+    a.reset()
+    b.reset()
+    ga, gb = a.generate(prompt, 100), b.generate(prompt, 100)
+    assert np.array_equal(ga, gb)
+    a.close()
+    b.close()
+    print(f"persistent vs phase kernels {worst:.2e}, vs oracle {worst_o:.2e}")
+
+
+# Small head-64 shapes: little weight traffic per CU, so a CU's L1 keeps the
+# activation lines of earlier phases (a read of another workgroup's result
+# that hit L1 would see stale data here, not at 135M); NH9 has q/o larger
+# than gate/up/down (QD * D > H * D), uploaded from host weights.
+@pytest.mark.parametrize("dims,host_weights", [
+    (dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024), False),
+    (dict(D=256, H=256, NH=4, NKV=2, HD=64, L=1, V=1024), False),
+    (dict(D=512, H=512, NH=4, NKV=2, HD=64, L=3, V=1024), False),
+    (dict(D=256, H=512, NH=9, NKV=3, HD=64, L=2, V=1024), True),
+], ids=["d256-h512", "d256-h256", "d512-h512", "d256-nh9-host"])
+def test_persistent_step_small_shapes(dims, host_weights):
+    """The persistent step against the per-phase kernels over 150 positions
+    (three sub-chunks of keys per piece at the end) and against the oracle
+    at the last position."""
+    w = bmhip.synthetic_weights(dims, 91)
+    kw = dict(weights=w) if host_weights else dict(seed=91)
+    a = bmhip.Engine(dims, max_seq_len=160, **kw)
+    b = bmhip.Engine(dims, max_seq_len=160, **kw)
+    if not a.set_persistent(True):
+        a.close()
+        b.close()
+        pytest.skip("the persistent step kernel is not available on this device")
+    assert b.set_persistent(False)
+    orc = oracle_decoder(dims, w, 160)
+    worst = 0.0
+    n = 150
+    for pos in range(n):
+        t = (37 * pos + 11) % dims["V"]
+        ya, yb = a.step(t), b.step(t)
+        worst = max(worst, normwise(ya, yb.astype(np.float64)))
+        r = orc.step(t, pos)
+    assert worst <= LOGIT_TOL, worst
+    assert normwise(ya, r) <= LOGIT_TOL, normwise(ya, r)
+    a.close()
+    b.close()
