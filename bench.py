@@ -433,7 +433,9 @@ def batched_leg(be, wls, BT: int, steps: int, warmup: int):
         "bytes_per_step": bps, "steps": steps, "workgroups": n_tiles * ((BT + 15) // 16),
         "kernel_us": round(kern_ms * 1e3, 3), "ms_per_step": round(wall * 1e3 / steps, 5),
         "achieved_gbps": round(achieved, 2), "frac_hbm_peak": round(achieved / HBM_PEAK_GBS, 4),
-        "rows_per_s": round(BT / (wall / steps), 1), "max_normwise_vs_fp32_path": worst,
+        "max_normwise_vs_fp32_path": worst,
+        "scope": "projections only, through the named kernel; the engine's batched decode runs its own fused "
+                 "per-phase kernels (k_dec_bmv), so this is not a decode-step rate",
     }
 
 
