@@ -154,13 +154,19 @@ __device__ __forceinline__ float bsum(float v, float* sh) {
 }
 
 /* Grid barrier among the working workgroups (see the file comment), in two
- * halves: grid_arrive waits for every thread's loads and stores (the
- * workgroup barrier's fence) and counts the workgroup in; grid_wait has
- * thread 0 poll until `target` workgroups have arrived, then drops stale L1
- * lines.  Returns false when this or another workgroup has given up.  The
- * poll is a vector load, so it waits behind this CU's loads in flight:
- * prefetches are issued early in a phase, and grid_arrive waits for them. */
+ * halves: grid_arrive has every wave wait for its loads and stores to
+ * complete (so the phase's results are in L2) and counts the workgroup in;
+ * grid_wait has thread 0 poll until `target` workgroups have arrived.  The
+ * next phase reads the results with agent-scope loads (ld_agent), which miss
+ * the L1.  Returns false when this workgroup has given up.  A wave's loads
+ * and stores complete in order, so the arrival also waits for the weight
+ * prefetch issued early in the phase (which has had the phase to land). */
 __device__ __forceinline__ void grid_arrive(DecState* st) {
+    /* every wave's stores of the phase have reached L2 before the count: a
+     * workgroup-scope fence does not wait for them (a workgroup's waves
+     * share the CU's L1), and the readers sit on other CUs.  vmcnt(0),
+     * expcnt and lgkmcnt left at their maxima. */
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(&st->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -561,8 +561,8 @@ def test_persistent_step_matches_phase_kernels_and_oracle():
 ], ids=["d256-h512", "d256-h256", "d512-h512", "d256-nh9-host"])
 def test_persistent_step_small_shapes(dims, host_weights):
     """The persistent step against the per-phase kernels over 150 positions
-    (three sub-chunks of keys per piece at the end) and against the oracle
-    at the last position."""
+    (a piece's key chunk grows to 15 keys) and against the oracle at the
+    last position."""
     w = bmhip.synthetic_weights(dims, 91)
     kw = dict(weights=w) if host_weights else dict(seed=91)
     a = bmhip.Engine(dims, max_seq_len=160, **kw)
@@ -584,3 +584,35 @@ def test_persistent_step_small_shapes(dims, host_weights):
     assert normwise(ya, r) <= LOGIT_TOL, normwise(ya, r)
     a.close()
     b.close()
+
+
+def test_persistent_step_long_context():
+    """Positions past 640: each of the ten key chunks of an attention piece
+    holds more than 64 keys, so a piece walks several sub-chunks (keys and
+    values of the next sub-chunk loaded into LDS after the previous one's
+    P.V), and the piece holding the current position sees it in a later
+    sub-chunk.  Against the per-phase kernels at every 16th position from
+    600 on and the oracle at the last, up to 1400 (three sub-chunks)."""
+    dims = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
+    n = 1400
+    w = bmhip.synthetic_weights(dims, 17)
+    a = bmhip.Engine(dims, max_seq_len=n, seed=17)
+    b = bmhip.Engine(dims, max_seq_len=n, seed=17)
+    if not a.set_persistent(True):
+        a.close()
+        b.close()
+        pytest.skip("the persistent step kernel is not available on this device")
+    assert b.set_persistent(False)
+    orc = oracle_decoder(dims, w, n)
+    worst = 0.0
+    for pos in range(n):
+        t = (53 * pos + 7) % dims["V"]
+        ya, yb = a.step(t), b.step(t)
+        if pos >= 600 and (pos % 16 == 0 or pos >= n - 3):
+            worst = max(worst, normwise(ya, yb.astype(np.float64)))
+        r = orc.step(t, pos)
+    assert worst <= LOGIT_TOL, worst
+    assert normwise(ya, r) <= LOGIT_TOL, normwise(ya, r)
+    a.close()
+    b.close()
+    print(f"persistent vs phase kernels past 640 keys: {worst:.2e}")
