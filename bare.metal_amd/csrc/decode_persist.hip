@@ -77,8 +77,10 @@ constexpr int P_GU = 7;              /*   gate/up (two local rows per output) */
 constexpr int P_DN = 4;              /*   down projection */
 constexpr int P_MAX = 8;
 constexpr int XS_MAX = 4096;         /* floats of the staged input vector */
-constexpr int XR = XS_MAX / PT;      /* its elements per thread */
-constexpr int NW = 8;                /* RMSNorm elements per thread: D <= 2048 */
+constexpr int XR = 8;                /* elements of the hidden vector h per thread: H <= 2048 */
+constexpr int NW = 4;                /* RMSNorm elements per thread: D <= 1024 */
+constexpr int BUF_FLAGS = 0x00020000; /* word 3 of a raw buffer resource (32-bit data format) */
+constexpr int CPOL_SC1 = 16;         /* buffer load cache policy: agent scope (misses the L1) */
 constexpr int HD = 64;               /* head size */
 constexpr int KCH = 64;              /* keys of one attention sub-chunk (one per lane) */
 constexpr int APS_MAX = 8192;        /* floats of the staged attention partials */
@@ -246,34 +248,48 @@ __device__ __forceinline__ void mv_products(int n, int nb, const Blk (&blk)[NP],
     lds_barrier();
 }
 
-/* A row's block products added in block order. */
-__device__ __forceinline__ float row_sum(const float* rp, int nb) {
+/* Sum of local row `row`'s nb block products by the four lanes of a quad:
+ * lane j of the quad adds blocks j, j + 4, ..., then the quad's partial
+ * sums are added by two DPP steps, so every lane of the quad holds the
+ * row's sum.  All four lanes must be active (callers clamp `row`). */
+__device__ __forceinline__ float quad_row_sum(const float* red, int row, int nb) {
+    const float* rp = red + row * nb;
     float acc = 0.f;
-#pragma unroll 8
-    for (int k = 0; k < nb; k++) acc += rp[k];
+#pragma unroll 4
+    for (int k = tid() & 3; k < nb; k += 4) acc += rp[k];
+    acc += dpp<DPP_XOR1>(acc);
+    acc += dpp<DPP_XOR2>(acc);
     return acc;
 }
 
-/* Products of the fetched blocks with xs, per-row sums, and the outputs of
- * thread o < r1 - r0: y[r0 + o] = sum, or with a residual (the thread's
- * row of the residual stream in *xres) y[r0 + o] = *xres += sum, or for
- * SwiGLU y[r0 + o] = silu(gate) * up. */
+/* Products of the fetched blocks with xs, per-row sums (a quad of lanes
+ * per row), and the outputs: y[r0 + o] = sum, or with a residual (row o
+ * of the residual stream in *xres of thread 4o, o < 64) y[r0 + o] = *xres
+ * += sum, or for SwiGLU y[r0 + o] = silu(gate) * up (gate row 2o in quad
+ * 2o, up row 2o + 1 in the next quad). */
 template <int NP>
 __device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP], const float* xs, float* red,
                                           float* y, float* xres) {
-    const int nb = j.nb, o = tid();
+    const int nb = j.nb, nout = j.r1 - j.r0, t = tid();
     mv_products(mv_rows(j), nb, blk, xs, red);
-    if (o < j.r1 - j.r0) {
-        if (j.glu) {
-            const float g = row_sum(red + (2 * o) * nb, nb), u = row_sum(red + (2 * o + 1) * nb, nb);
-            y[j.r0 + o] = (g / (1.0f + expf(-g))) * u;
-        } else {
-            const float acc = row_sum(red + o * nb, nb);
-            if (xres) {
-                *xres += acc;
-                y[j.r0 + o] = *xres;
-            } else {
-                y[j.r0 + o] = acc;
+    if (j.glu) {
+        for (int o0 = 0; o0 < nout; o0 += PT / 8) {
+            const int o = o0 + (t >> 3), row = min(2 * o + ((t >> 2) & 1), 2 * nout - 1);
+            const float sum = quad_row_sum(red, row, nb);
+            const float up = dpp<DPP_HALF_MIRROR>(sum); /* lane i of 8 <- 7 - i: the other quad's sum */
+            if ((t & 7) == 0 && o < nout) y[j.r0 + o] = (sum / (1.0f + expf(-sum))) * up;
+        }
+    } else {
+        for (int o0 = 0; o0 < nout; o0 += PT / 4) {
+            const int o = o0 + (t >> 2);
+            const float sum = quad_row_sum(red, min(o, nout - 1), nb);
+            if ((t & 3) == 0 && o < nout) {
+                if (xres) {
+                    *xres += sum;
+                    y[j.r0 + o] = *xres;
+                } else {
+                    y[j.r0 + o] = sum;
+                }
             }
         }
     }
@@ -320,7 +336,7 @@ __device__ __forceinline__ void norm_to_lds(const float (&v)[NW], int C, const f
     lds_barrier();
 }
 
-/* xs = x from its loaded elements, C <= XS_MAX. */
+/* xs = x from its loaded elements, C <= XR * PT. */
 __device__ __forceinline__ void vec_to_lds(const float (&v)[XR], int C, float* xs) {
 #pragma unroll
     for (int k = 0; k < XR; k++) {
@@ -519,13 +535,13 @@ __device__ __forceinline__ void attn_empty(const DecPersist& a, const Piece& p) 
 template <typename F>
 __device__ __forceinline__ void attn_merge(const DecPersist& a, float* aps, float* ew, float* xs, F&& after_loads) {
     const int total4 = a.NH * DEC_PERSIST_NCH * APR / 4;
-    const f4* src = (const f4*)a.apart;
+    /* 16-byte agent-scope loads (sc1: miss the L1) through a buffer
+     * resource over the partials; past its end a buffer load returns 0 */
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.apart, (short)0, total4 * 16, BUF_FLAGS);
     f4 v[APS_MAX / 4 / PT];
 #pragma unroll
-    for (int k = 0; k < APS_MAX / 4 / PT; k++) {
-        const float* e = (const float*)(src + min(tid() + k * PT, total4 - 1));
-        v[k] = f4{ld_agent(e), ld_agent(e + 1), ld_agent(e + 2), ld_agent(e + 3)};
-    }
+    for (int k = 0; k < APS_MAX / 4 / PT; k++)
+        v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (tid() + k * PT), 0, CPOL_SC1));
     issue_order();
 #pragma unroll
     for (int k = 0; k < APS_MAX / 4 / PT; k++) {
@@ -584,12 +600,13 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
         rc = cosf(ang);
         rs = sinf(ang);
     }
-    /* the rows of x this workgroup updates (o and down split D the same way) */
+    /* the rows of x this workgroup updates (o and down split D the same way):
+     * row o in thread 4o, the lane that writes it */
     float xres = 0.f;
     {
         int r0, r1;
         share_rows(D, w, r0, r1);
-        if (tid() < r1 - r0) xres = a.x[r0 + tid()];
+        if ((tid() & 3) == 0 && (tid() >> 2) < r1 - r0) xres = a.x[r0 + (tid() >> 2)];
     }
 
     /* the shares of this workgroup in the four matvec phases of a layer */
@@ -635,11 +652,14 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
         const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0, n2 = s2.r1 - s2.r0;
         const int nb = s0.nb, o = tid();
         mv_products(n0 + n1 + n2, nb, blk, xs, red);
-        if (o < n0 + n1 + n2) {
-            const float acc = row_sum(red + o * nb, nb);
-            if (o < n0) a.q[s0.r0 + o] = acc;
-            else if (o < n0 + n1) a.k[s1.r0 + o - n0] = acc;
-            else a.v[s2.r0 + o - n0 - n1] = acc;
+        for (int r0 = 0; r0 < n0 + n1 + n2; r0 += PT / 4) {
+            const int r = r0 + (o >> 2);
+            const float acc = quad_row_sum(red, min(r, n0 + n1 + n2 - 1), nb);
+            if ((o & 3) == 0 && r < n0 + n1 + n2) {
+                if (r < n0) a.q[s0.r0 + r] = acc;
+                else if (r < n0 + n1) a.k[s1.r0 + r - n0] = acc;
+                else a.v[s2.r0 + r - n0 - n1] = acc;
+            }
         }
     };
     auto fetch_norm = [&](const float* nwp, float(&nw)[NW]) { load_vec(nwp, D, nw); };
@@ -717,14 +737,14 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
  * phase's share within its register stage, one output row per thread, and
  * the vectors within their LDS stages. */
 extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
-    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XS_MAX ||
+    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT ||
         NH * HD > XS_MAX || NH * DEC_PERSIST_NCH * APR > APS_MAX || MS <= 0)
         return 0;
     const int QD = NH * HD, KV = NKV * HD;
     auto passes = [](int rows_per_wg, int nb) { return nb > PT ? P_MAX + 1 : (rows_per_wg + PT / nb - 1) / (PT / nb); };
     const int w = DEC_PERSIST_WGS;
     const int qkv = (QD + 2 * KV + w - 1) / w, dr = (D + w - 1) / w, hr = (H + w - 1) / w;
-    if (qkv > PT || dr > PT || hr > PT) return 0;
+    if (qkv > PT || dr > PT / 4 || hr > PT) return 0; /* residual rows: one per quad of lanes */
     if (passes(qkv, D / 32) > P_QKV) return 0;
     if (passes(dr, QD / 32) > P_O) return 0;
     if (passes(2 * hr, D / 32) > P_GU) return 0;
