@@ -406,12 +406,13 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
         const float* xb = a.x + (size_t)b * D;
         constexpr int SEG = WF == HW_F32 ? 16 : 32;
         float xs[SEG], nw[SEG];
+        const bool norm = a.norm_w != nullptr; /* the same for the whole launch */
         if (lane_on) {
 #pragma unroll
             for (int i = 0; i < SEG; i += 4) {
-                float4 v4, g4;
+                float4 v4, g4 = make_float4(1.f, 1.f, 1.f, 1.f);
                 __builtin_memcpy(&v4, __builtin_assume_aligned(xb + SEG * sg + i, 4), 16);
-                __builtin_memcpy(&g4, __builtin_assume_aligned(a.norm_w + SEG * sg + i, 4), 16);
+                if (norm) __builtin_memcpy(&g4, __builtin_assume_aligned(a.norm_w + SEG * sg + i, 4), 16);
                 xs[i] = v4.x; xs[i + 1] = v4.y; xs[i + 2] = v4.z; xs[i + 3] = v4.w;
                 nw[i] = g4.x; nw[i + 1] = g4.y; nw[i + 2] = g4.z; nw[i + 3] = g4.w;
             }
@@ -419,16 +420,18 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
 #pragma unroll
             for (int i = 0; i < SEG; i++) xs[i] = nw[i] = 0.0f;
         }
-        /* RMSNorm from registers: the lanes of row slot 0 hold every column once */
-        float ss = 0.0f;
-        if (lane_on && slot == 0) {
+        if (norm) {
+            /* RMSNorm from registers: the lanes of row slot 0 hold every column once */
+            float ss = 0.0f;
+            if (lane_on && slot == 0) {
 #pragma unroll
-            for (int i = 0; i < SEG; i++) ss = fmaf(xs[i], xs[i], ss);
+                for (int i = 0; i < SEG; i++) ss = fmaf(xs[i], xs[i], ss);
+            }
+            ss = block_sum(ss, sh);
+            const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+            for (int i = 0; i < SEG; i++) xs[i] = (xs[i] * inv) * nw[i];
         }
-        ss = block_sum(ss, sh);
-        const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
-#pragma unroll
-        for (int i = 0; i < SEG; i++) xs[i] = (xs[i] * inv) * nw[i];
 #pragma unroll
         for (int u = 0; u < HEAD_U; u++) {
             float p;
@@ -466,6 +469,7 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
                 const float* rp = red + rl * nseg;
                 float acc = 0.0f;
                 for (int k = 0; k < nseg; k++) acc += rp[k];
+                if (a.bias) acc += a.bias[r];
                 a.logits[(size_t)b * a.V + r] = acc;
                 const unsigned long long kk = argmax_key(acc, (int)r);
                 best = kk > best ? kk : best;
@@ -2074,6 +2078,50 @@ static int launch_rmsnorm_matmul(const bmk_launch_t* a, int wf) {
 
 extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_F32); }
 extern "C" int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_BF16); }
+
+/* The plain fp32 and bf16 matmul kernels: {inp [BT][C], weight [OC][C] (fp32
+ * or bf16), bias [OC], out [BT][OC], params int{BT, C, OC, has_bias}}
+ * (reference forward.metal:23-37 matmul_forward_naive, 513-560
+ * matmul_forward_tiled, 449-503 matmul_forward_fp32_tiled, 52-89
+ * matmul_forward_bf16_vec, 91-110 matmul_forward_bf16).  The reference's
+ * prefill takes them for the LM head of its last position (graph.c:373-380,
+ * selected by scheduler.c:1118-1145 and registry.c:60-67).  Served by the
+ * LM-head kernel with the RMSNorm off: each workgroup loads its weight rows
+ * once and applies them to all BT input rows.  The grid the caller passes is
+ * not used.  C must be a multiple of 16 up to 4096 (fp32) or of 32 up to 8192
+ * (bf16); other shapes are rejected. */
+static int launch_matmul_rows(const bmk_launch_t* a, int wf) {
+    const char* name = wf == HW_F32 ? "matmul_forward (fp32)" : "matmul_forward_bf16";
+    const size_t esz = wf == HW_F32 ? 4 : 2;
+    BMK_NEED_BYTES(a, 4, 16, "params");
+    const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), hb = bmk_pi(a, 4, 3);
+    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0 && head_shape_ok(C, wf), "%s: BT=%d OC=%d, C=%d must be a multiple of %d up to %d",
+                name, BT, OC, C, wf == HW_F32 ? 16 : 32, wf == HW_F32 ? 4096 : 8192);
+    if (BT == 0 || OC == 0) return 0;
+    BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
+    BMK_NEED_BYTES(a, 1, (size_t)OC * C * esz, "weight");
+    if (hb) BMK_NEED_BYTES(a, 2, (size_t)OC * 4, "bias");
+    BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
+    BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1]) & 3) == 0, "%s: misaligned operand", name);
+    DecHead h;
+    memset(&h, 0, sizeof h);
+    h.x = (const float*)a->dev[0];
+    if (wf == HW_F32) h.w = (const float*)a->dev[1];
+    else h.wh = (const unsigned short*)a->dev[1];
+    h.bias = hb ? (const float*)a->dev[2] : nullptr;
+    h.logits = (float*)a->dev[3];
+    h.D = C;
+    h.V = OC;
+    h.B = BT;
+    h.tiles = head_tiles(C, OC, wf);
+    if (wf == HW_F32) hipLaunchKernelGGL(k_head<HW_F32>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    else hipLaunchKernelGGL(k_head<HW_BF16>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int bmk_launch_matmul_f32(const bmk_launch_t* a) { return launch_matmul_rows(a, HW_F32); }
+extern "C" int bmk_launch_matmul_bf16(const bmk_launch_t* a) { return launch_matmul_rows(a, HW_BF16); }
 
 /* argmax_f32 {values f32 [n], out int [1], params int{n}} */
 extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {

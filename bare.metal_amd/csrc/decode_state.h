@@ -90,10 +90,12 @@ typedef struct {
 } DecAttn;
 
 /* Final RMSNorm + LM head + argmax.  Rows: Q8 when wq != NULL, else bf16
- * when wh != NULL, else fp32. */
+ * when wh != NULL, else fp32.  norm_w == NULL: no RMSNorm (a plain
+ * out[b][r] = bias[r] + x[b] . W[r], the named fp32/bf16 matmul kernels). */
 typedef struct {
     const float* x;      /* [B][D] */
     const float* norm_w;
+    const float* bias;   /* [V] added to each output, or NULL */
     const float* w;      /* fp32 [V][D] */
     const unsigned char* wq; /* Q8 [V][D/32] blocks, or NULL */
     const unsigned short* wh; /* bf16 [V][D], or NULL */

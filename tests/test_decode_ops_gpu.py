@@ -314,6 +314,49 @@ def test_rmsnorm_matmul_forward_bf16_vec_rejects(be):
     assert be.dispatch("rmsnorm_matmul_forward_bf16_vec", bufs, (512,), (512,)) == -1
 
 
+@pytest.mark.parametrize("BT,C,OC,has_bias", [(1, 576, 49152, 0), (1, 128, 1024, 0), (3, 64, 100, 1),
+                                              (40, 960, 77, 1)])
+@pytest.mark.parametrize("name", ["matmul_forward_naive", "matmul_forward_tiled", "matmul_forward_fp32_tiled",
+                                  "matmul_forward_bf16_vec", "matmul_forward_bf16"])
+def test_plain_matmul_forward(be, BT, C, OC, has_bias, name):
+    """The plain fp32 / bf16-weight matmuls (reference forward.metal:23-110,
+    449-560; the reference prefill's LM head after COPY_LAST):
+    out[bt][oc] = bias[oc] + inp[bt] . W[oc], fp32 sums, vs fp64 over the
+    same (bf16-widened) weights.  Launched with the reference's grids."""
+    rng = np.random.default_rng(BT * 7 + C + OC)
+    x = rng.standard_normal(BT * C).astype(np.float32)
+    W = (rng.standard_normal(OC * C) * 0.02).astype(np.float32)
+    bias = rng.standard_normal(OC).astype(np.float32) if has_bias else np.zeros(1, np.float32)
+    bf16 = "bf16" in name
+    if bf16:
+        W = po.bf16_rne(W)
+        wbuf = be.upload((W.view(np.uint32) >> 16).astype(np.uint16))
+    else:
+        wbuf = be.upload(W)
+    out = be.alloc(BT * OC * 4)
+    grid = ((OC * 128, BT), (128,)) if name == "matmul_forward_bf16_vec" else (((OC + 31) & ~31, BT), (32,))
+    rc = be.dispatch(name, [be.upload(x), wbuf, be.upload(bias), out, be.params(BT, C, OC, has_bias)], *grid)
+    assert rc == 0
+    ref = x.reshape(BT, C).astype(np.float64) @ W.reshape(OC, C).astype(np.float64).T
+    if has_bias:
+        ref += bias.astype(np.float64)
+    assert nw(out.read(np.float32).reshape(BT, OC), ref) <= TOL
+
+
+def test_plain_matmul_forward_rejects(be):
+    """A width the row kernel does not tile, a short weight and a short bias
+    are rejected with nothing launched."""
+    out = be.alloc(4 * 10)
+    x = be.upload(np.ones(48, np.float32))
+    assert be.dispatch("matmul_forward_bf16_vec", [x, be.upload(np.zeros(480, np.uint16)), x, out,
+                                                   be.params(1, 48, 10, 0)], (1280,), (128,)) == -1
+    assert be.dispatch("matmul_forward_tiled", [be.upload(np.ones(64, np.float32)), be.upload(np.ones(9 * 64, np.float32)),
+                                                x, out, be.params(1, 64, 10, 0)], (32,), (32,)) == -1
+    assert be.dispatch("matmul_forward_tiled", [be.upload(np.ones(64, np.float32)), be.upload(np.ones(10 * 64, np.float32)),
+                                                be.upload(np.ones(9, np.float32)), out, be.params(1, 64, 10, 1)],
+                       (32,), (32,)) == -1
+
+
 def test_argmax_first_index(be):
     v = np.zeros(49152, np.float32)
     v[[10, 40000, 7]] = 2.5
