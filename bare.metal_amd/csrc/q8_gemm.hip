@@ -13,10 +13,10 @@
  * v_cvt_pk_bf16_f32 performs both roundings, two values per instruction.
  *
  * Tiling: a 256-lane workgroup (4 waves as 2x2) computes a 128x128 tile of
- * C; each wave owns 64x64 = 4x4 tiles of v_mfma_f32_16x16x32_bf16.  The K
+ * C; each wave owns 64x64 = 2x2 tiles of v_mfma_f32_32x32x16_bf16.  The K
  * loop steps 64 (two Q8 blocks).  LDS holds two buffers of the bf16 A slab
  * (128x64) and the dequantised weight slab (128x64), rows padded to 72
- * elements.  The global loads of step s+2 are issued before the 32 MFMAs
+ * elements.  The global loads of step s+2 are issued before the 16 MFMAs
  * of step s, and step s+1 is converted into the other LDS buffer after
  * them: two steps of MFMA work cover each load's latency, with one
  * barrier per step (details at gemm_tile).
@@ -97,7 +97,7 @@ __device__ __forceinline__ uint4 dq4(const uint4& q, int part, float s) {
  *
  * K runs in steps of 64 (two Q8 blocks).  The nb/2 full steps form a
  * two-stage pipeline: the global loads of step s+2 are issued before the
- * 32 MFMAs of step s, and step s+1 is stored into the other LDS buffer
+ * 16 MFMAs of step s, and step s+1 is stored into the other LDS buffer
  * after them, with one barrier per step.  The loop body has no data
  * dependent selects and issues the same loads on every path (past the
  * last step it reloads that step, an L2 hit that is never stored), so the
@@ -185,28 +185,31 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
         }
     };
 
-    f32x4 acc[4][4];
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    f32x16 acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    const int kq = (lane >> 4) * 8;
+    const int kq = (lane >> 5) * 8;
     auto mfma_step = [&](int buf) {
         const unsigned short* As = lds + buf * 2 * SLAB;
         const unsigned short* Bs = As + SLAB;
 #pragma unroll
-        for (int ks = 0; ks < GEMM_BK; ks += 32) {
-            bf16x8 fa[4], fb[4];
+        for (int ks = 0; ks < GEMM_BK; ks += 16) {
+            bf16x8 fa[2], fb[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) fa[i] = *(const bf16x8*)&As[(wm + 16 * i + (lane & 15)) * LDK + ks + kq];
+            for (int i = 0; i < 2; i++) fa[i] = *(const bf16x8*)&As[(wm + 32 * i + (lane & 31)) * LDK + ks + kq];
 #pragma unroll
-            for (int j = 0; j < 4; j++) fb[j] = *(const bf16x8*)&Bs[(wn + 16 * j + (lane & 15)) * LDK + ks + kq];
+            for (int j = 0; j < 2; j++) fb[j] = *(const bf16x8*)&Bs[(wn + 32 * j + (lane & 31)) * LDK + ks + kq];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 2; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -253,35 +256,37 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
         mfma_step(buf);
     }
 
-    /* Epilogue, 16x16 D layout: lane holds rows 4*(lane/16)+v, column
-     * lane%16.  Interior tiles store without bounds checks from one base
-     * with 32-bit offsets (each wave instruction writes 4 rows x 64 bytes).
-     * C is written once and not read back by this launch, so the stores are
-     * nontemporal: they stream past the caches instead of evicting the
-     * weight panels that the other M tiles still read (measured 8-10%
-     * faster on the 135M prefill set).  Staging the tile through LDS for
-     * whole-row stores, and 16-byte stores of a transposed accumulator,
-     * both measured slower. */
-    float* Ct = Cm + (size_t)(m0 + wm + 4 * (lane >> 4)) * ldc + n0 + wn + (lane & 15);
+    /* Epilogue, 32x32 D layout: register r of a tile holds row
+     * 8*(r/4) + 4*(lane/32) + r%4, column lane%32, so each wave instruction
+     * writes 2 rows x 128 bytes: whole 128-byte lines of C when the row
+     * pitch is a multiple of 32 floats (measured 2-3% faster than the
+     * half-line stores of the 16x16 layout).  Interior tiles store without
+     * bounds checks from one base with 32-bit offsets.  C is written once
+     * and not read back by this launch, so the stores are nontemporal: they
+     * stream past the caches instead of evicting the weight panels that the
+     * other M tiles still read (measured 8-10% faster on the 135M prefill
+     * set).  Staging the tile through LDS for whole-row stores, and 16-byte
+     * stores of a transposed accumulator, both measured slower. */
+    float* Ct = Cm + (size_t)(m0 + wm + 4 * (lane >> 5)) * ldc + n0 + wn + (lane & 31);
     if (m0 + BM <= M && n0 + BN <= N) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
+            for (int j = 0; j < 2; j++)
 #pragma unroll
-                for (int v = 0; v < 4; v++)
-                    __builtin_nontemporal_store(acc[i][j][v], &Ct[(unsigned)(16 * i + v) * (unsigned)ldc + 16 * j]);
+                for (int r = 0; r < 16; r++)
+                    __builtin_nontemporal_store(acc[i][j][r], &Ct[(unsigned)(32 * i + 8 * (r >> 2) + (r & 3)) * (unsigned)ldc + 32 * j]);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int col = n0 + wn + 16 * j + (lane & 15);
+            for (int j = 0; j < 2; j++) {
+                const int col = n0 + wn + 32 * j + (lane & 31);
                 if (col >= N) continue;
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const int row = m0 + wm + 16 * i + 4 * (lane >> 4) + v;
-                    if (row < M) Cm[(size_t)row * ldc + col] = acc[i][j][v];
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + wm + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (row < M) Cm[(size_t)row * ldc + col] = acc[i][j][r];
                 }
             }
     }
