@@ -481,11 +481,14 @@ extern "C" int mv_tiles_for(int OC, int C, int U) {
     return (OC + rows - 1) / rows;
 }
 
-/* Tiles at MV_U above which a launch uses MV_U_WIDE rows per lane: enough
- * workgroups to give each of MI355X's 256 CUs several even at the wider tile.
- * More bytes in flight per lane is what lifts a streaming matvec toward the
- * HBM roofline; fewer, wider tiles would starve the CUs on small matrices. */
-#define MV_WIDE_MIN_TILES 4096
+/* Tiles at MV_U from which a launch uses MV_U_WIDE rows per lane: at least
+ * 384 workgroups at the wider tile, 1.5 per CU of MI355X's 256.  More bytes
+ * in flight per lane is what lifts a streaming matvec toward the HBM
+ * roofline; fewer, wider tiles would starve the CUs on small matrices.
+ * Measured on the 49152-row LM heads, launch after launch over weights no
+ * cache holds: 12.9 us at 8 rows per lane against 14.1 at 4 (x960), 9.5
+ * against 9.8 (x576); 1 or 2 rows per lane are slower, 16 too. */
+#define MV_WIDE_MIN_TILES 768
 
 template <int QF>
 static int launch_group(MvGroup* g, hipStream_t s) {

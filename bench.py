@@ -297,16 +297,34 @@ def single_matvec_leg(be, OC: int, C: int, seed_ids, min_bytes: int = 1 << 30, p
     rot = [[0, c * wbytes, 0, 0, 0] for c in range(copies)] * passes
     cold = per_call_us(be, "matmul_forward_q8_vec", bufs, grid, tg, rot)
     warm = per_call_us(be, "matmul_forward_q8_vec", bufs, grid, tg, [[0, 0, 0, 0, 0]] * 200)
+    kern = be.kernel("matmul_forward_q8_vec")
+
+    def back_to_back(offs):
+        """Mean GPU time per call of calls issued back to back in one
+        encoder (as a decode step issues them): no per-call event pair."""
+        enc = be.encoder()
+        for o in offs:
+            if enc.dispatch(kern, bufs, grid, tg, offsets=o) != 0:
+                raise RuntimeError("matmul_forward_q8_vec dispatch rejected")
+        return enc.wait_timed() * 1e3 / len(offs)
+
+    back_to_back(rot)
+    b2b_cold = back_to_back(rot)
+    b2b_warm = back_to_back([[0, 0, 0, 0, 0]] * 200)
     bpc = wbytes + 4 * C + 4 * OC
     big.free()
     out = {
         "workload": f"one {OC}x{C} Q8 matvec (matmul_forward_q8_vec), N(0,0.02) weights packed on the device; "
                     f"cold: {copies} copies at distinct addresses ({copies * wbytes / 2**30:.2f} GiB) called in "
                     f"turn, {passes} passes; warm: the same copy 200 times; GPU time per call from HIP events "
-                    f"around each dispatch",
+                    f"around each dispatch; back_to_back_*: the same calls issued in one encoder, mean per call",
         "bytes_per_call": bpc, "normwise_err": err,
         "cold_us_per_call": round(cold, 3), "cold_gbps": round(bpc / (cold * 1e-6) / 1e9, 1),
         "warm_us_per_call": round(warm, 3), "warm_gbps": round(bpc / (warm * 1e-6) / 1e9, 1),
+        "back_to_back_cold_us_per_call": round(b2b_cold, 3),
+        "back_to_back_cold_gbps": round(bpc / (b2b_cold * 1e-6) / 1e9, 1),
+        "back_to_back_warm_us_per_call": round(b2b_warm, 3),
+        "back_to_back_warm_gbps": round(bpc / (b2b_warm * 1e-6) / 1e9, 1),
     }
     if cpu_seconds > 0:
         y = np.zeros(OC, np.float32)
@@ -316,7 +334,8 @@ def single_matvec_leg(be, OC: int, C: int, seed_ids, min_bytes: int = 1 << 30, p
             out[f"cpu_{nt}t_us_per_call"] = round(dt / k * 1e6, 2)
             out[f"cpu_{nt}t_gbps"] = round(bpc * k / dt / 1e9, 2)
     log(f"[bench] matvec {OC}x{C}: cold {cold:.2f} us/call ({bpc / (cold * 1e-6) / 1e9:.0f} GB/s), "
-        f"warm {warm:.2f} us/call")
+        f"warm {warm:.2f} us/call; back to back: cold {b2b_cold:.2f} us ({bpc / (b2b_cold * 1e-6) / 1e9:.0f} GB/s), "
+        f"warm {b2b_warm:.2f} us")
     return out
 
 
