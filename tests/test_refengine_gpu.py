@@ -117,6 +117,45 @@ def test_reference_engine_greedy_matches_oracle(tmp_path):
     assert same == len(got) or marg[same] <= 1e-3
 
 
+def _ref_test(name):
+    exe = os.path.join(ROOT, "oracle", "_ref", name)
+    if not os.path.exists(exe):
+        pytest.skip(f"oracle/_ref/{name} is not built (needs the reference tree at build time)")
+    return exe
+
+
+def test_reference_prefill_test_program(tmp_path):
+    """The reference's own test/prefill_test.c, compiled unchanged and linked
+    against this library: a one-pass prefill of 64 tokens against stepwise
+    decode, then one more step from the copied KV cache; its criteria are
+    cosine > 0.9999 and equal argmax of both logit vectors.  It loads the
+    model from data/smollm2-135m under its working directory: a random-init
+    llama checkpoint at SmolLM2-135M widths with 4 layers is written there
+    (the real weights are not available offline).  The program runs the
+    reference's fp32-weight path (it sets no quantization)."""
+    exe = _ref_test("ref_prefill_test")
+    dims = dict(bmhip.SMOLLM2_135M)
+    dims["L"] = 4
+    w = bmhip.synthetic_weights(dims, 309)
+    write_checkpoint(str(tmp_path / "data" / "smollm2-135m"), dims, w, dtype="F32")
+    print("reference prefill_test", flush=True)
+    r = subprocess.run([exe], cwd=str(tmp_path), capture_output=True, text=True, timeout=300)
+    print(r.stdout[-600:])
+    assert r.returncode == 0 and "=== prefill: PASS ===" in r.stdout, (r.returncode, r.stdout[-2000:], r.stderr[-3000:])
+
+
+def test_reference_attn_prefill_test_program():
+    """The reference's own test/attn_prefill_test.c, compiled unchanged: its
+    two prefill attention kernels by name at 11 sequence lengths, with its
+    own buffers, parameter blocks and grids, agree within 1e-5."""
+    exe = _ref_test("ref_attn_prefill_test")
+    print("reference attn_prefill_test", flush=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    print(r.stdout[-400:])
+    assert r.returncode == 0 and "=== attn_prefill: PASS ===" in r.stdout, (r.returncode, r.stdout[-2000:],
+                                                                            r.stderr[-3000:])
+
+
 def test_reference_engine_q4_decode_matches_oracle(tmp_path):
     """The reference scheduler's Q4_0 decode (quant 4: matmul_forward_q4_vec4 /
     _vec by name) against the oracle decoder in Q4 mode."""
