@@ -401,7 +401,9 @@ __device__ __forceinline__ void load_kv(const DecPersist& a, const Piece& p, int
     }
 }
 
-/* Issues every load of a piece's first sub-chunk: q, k, v and the cached keys and values. */
+/* Issues the loads of the piece's q, k and v (this step's, written by the
+ * previous phase); its first sub-chunk's cached keys and values are loaded
+ * by load_kv before the barrier that precedes the phase. */
 __device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, AttnRegs& r) {
     const int t = tid();
     auto raw = [&](int i) {
@@ -411,7 +413,6 @@ __device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, A
     };
     r.r0 = raw(t);
     r.r1 = raw(t + PT);
-    load_kv(a, p, p.k0, r);
 }
 
 /* The sub-chunk's cached keys and values into LDS. */
@@ -681,12 +682,15 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
         }
         finish_qkv(q0, q1, q2, bq);
         grid_arrive(st);
-        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
-        /* 2. RoPE + KV append + attention pieces */
+        /* 2. RoPE + KV append + attention pieces.  The piece's cached keys and
+         * values (positions before pos, written by earlier steps) do not
+         * depend on this step's q, k, v: their loads fly during the wait. */
         {
             const Piece pc = make_piece(a, l, w, pos);
             const bool live = has_piece && pc.k0 < pc.k1;
             AttnRegs ar;
+            if (live) load_kv(a, pc, pc.k0, ar);
+            if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
             if (live) attn_load(a, pc, ar);
             issue_order();
             fetch_norm(a.ln2 + (size_t)l * D, nw);
