@@ -643,7 +643,8 @@ __global__ __launch_bounds__(NT) void k_embed(DecEmbed a) {
     __shared__ int tok_s;
     DecState* st = a.st;
     const int b = blockIdx.x, pos = st->pos;
-    if (b == 0 && threadIdx.x == 0) st->bar = 0; /* the persistent step kernel's barrier counter */
+    /* a new step: new epochs for the values the persistent step kernel exchanges */
+    if (a.steps && b == 0 && threadIdx.x == 0) *a.steps += 1u;
     if (threadIdx.x == 0) {
         int tok;
         if (st->host_mode) tok = st->host_token[b];

@@ -10,8 +10,7 @@
  * residual add.  At batch 1 on MI355X each such launch is bound by its
  * fixed cost (about 2.5 us from one kernel's end to the next one's first
  * useful load) rather than by its bytes, so this kernel runs the whole
- * layer stack as five phases per layer separated by grid barriers inside
- * one launch:
+ * layer stack as five phases per layer inside one launch:
  *   1. RMSNorm(x) and q, k, v (Q8 matvecs of 960 rows at SmolLM2-135M);
  *   2. RoPE, KV append and attention, split into (KV head, key chunk)
  *      pieces that write online-softmax partials (max, sum, P.V);
@@ -19,19 +18,19 @@
  *   4. RMSNorm, gate and up, SwiGLU;
  *   5. down projection, residual.
  * A phase costs a chain of memory round trips rather than bytes, so each
- * one is cut to a single round trip after its barrier.  Vector memory
+ * one is cut to a single round trip for its inputs.  Vector memory
  * requests of a CU leave in order, and one counter covers a wave's loads and
  * stores, so the order of issue decides what waits for what:
  *   - every staging step (the input vector, the attention partials, the
- *     q/k/v of a KV head with the first keys and values of its chunk)
- *     issues all of its loads before it waits on any, with in-bounds
- *     addresses for unused lanes so that the compiler can count them;
+ *     q/k/v of a KV head) issues all of its loads before it waits on any,
+ *     with in-bounds addresses for unused lanes so that the compiler can
+ *     count them; an attention piece's cached keys and values go first;
  *   - the weights of the next matvec phase are issued right after a
- *     phase's staging loads (o in phase 1, the second RMSNorm in phase 2,
- *     gate/up in phase 3, down in phase 4, the next layer's q/k/v and first
- *     RMSNorm in phase 5), so they stream in behind the activations while
- *     the phase computes, and into registers of their own (per-phase pass
- *     counts P_QKV, P_O, P_GU, P_DN);
+ *     phase's inputs have arrived (o in phase 1, the second RMSNorm in phase
+ *     2, gate/up in phase 3, down in phase 4, the next layer's q/k/v and
+ *     first RMSNorm in phase 5), so they stream in while the phase computes,
+ *     into registers of their own (per-phase pass counts P_QKV, P_O, P_GU,
+ *     P_DN);
  *   - barriers inside a workgroup order LDS only (an LDS fence), so they
  *     do not wait for those weights;
  *   - a workgroup keeps in registers the rows of the residual stream it
@@ -40,18 +39,24 @@
  *
  * One XCD: MI355X hands workgroup b to XCD b % 8.  The grid has 8 x
  * DEC_PERSIST_WGS workgroups; those with blockIdx.x % 8 == 0 work and the
- * rest return at once, so every working workgroup shares one L2.  Writes of
- * one phase then reach every reader through that L2: a barrier is a relaxed
- * device-scope atomic add after the workgroup's stores have completed and
- * a poll of the counter (about 1 us for 32 workgroups, against 2.7 us for
- * release/acquire fences across XCDs).  What a phase reads of the previous
- * phase's results (x, h, q/k/v, the attention partials) it reads with
- * agent-scope loads, which miss the CU's L1 (whose lines may be stale) and
- * hit the shared L2.  No cache is invalidated: an agent-scope acquire fence
- * would invalidate this CU's L1 but made the step 2.6x slower, and a
- * workgroup-scope one leaves the L1 alone.  The barrier's spin is bounded
- * in time: on timeout a workgroup sets DecState.sync_error and leaves; the
- * others cannot pass that barrier either and time out there too, so the
+ * rest return at once, so every working workgroup shares one L2.
+ *
+ * No grid barrier: every value one phase hands to another workgroup (x, h,
+ * q/k/v, the attention partials) is stored together with the epoch of the
+ * phase that wrote it, in one 8-byte store, and a reader loads the values
+ * themselves with agent-scope loads (which miss the CU's L1, whose lines may
+ * be stale, and read the shared L2) until every one carries the epoch it
+ * waits for.  A reader thus proceeds as soon as its own inputs are written,
+ * one round trip after the last of them, where a barrier cost a counter
+ * update after the writers' stores had completed, a poll, and then the
+ * loads (≈6% per step).  Epochs are unique per (step, layer, phase): the
+ * step count lives in the exchange buffer, which the host never writes.
+ * Reuse of a buffer is safe without barriers: every phase's output depends,
+ * through the chain of phases, on every workgroup's previous use of the
+ * buffer (a workgroup writes x in phase 5 only after reading all of h, which
+ * every workgroup wrote after reading x in phase 4, and so on).  The spins
+ * are bounded in time: on timeout a workgroup sets DecState.sync_error and
+ * leaves; the workgroups waiting for its values time out in turn, so the
  * grid always drains.
  *
  * Arithmetic: fp32 throughout, the reference's formulas (RMSNorm
@@ -98,7 +103,7 @@ __device__ __forceinline__ int tid() {
 }
 
 static_assert(2 * KCH * HD <= APS_MAX, "the K and V sub-chunks share the partials' LDS");
-static_assert((DEC_PERSIST_NCH * APR) % 4 == 0, "partials are staged as float4");
+static_assert((DEC_PERSIST_NCH * APR) % 2 == 0, "partials load as 16-byte pairs of exchanged values");
 static_assert(P_QKV <= P_MAX && P_O <= P_MAX && P_GU <= P_MAX && P_DN <= P_MAX, "pass caps");
 
 /* Keeps the compiler from moving instructions across this point: loads
@@ -155,45 +160,64 @@ __device__ __forceinline__ float bsum(float v, float* sh) {
     return r;
 }
 
-/* Grid barrier among the working workgroups (see the file comment), in two
- * halves: grid_arrive has every wave wait for its loads and stores to
- * complete (so the phase's results are in L2) and counts the workgroup in;
- * grid_wait has thread 0 poll until `target` workgroups have arrived.  The
- * next phase reads the results with agent-scope loads (ld_agent), which miss
- * the L1.  Returns false when this workgroup has given up.  A wave's loads
- * and stores complete in order, so the arrival also waits for the weight
- * prefetch issued early in the phase (which has had the phase to land). */
-__device__ __forceinline__ void grid_arrive(DecState* st) {
-    /* every wave's stores of the phase have reached L2 before the count: a
-     * workgroup-scope fence does not wait for them (a workgroup's waves
-     * share the CU's L1), and the readers sit on other CUs.  vmcnt(0),
-     * expcnt and lgkmcnt left at their maxima. */
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(&st->bar, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+/* Values exchanged between phases (see the file comment): the float's bits
+ * in the low word, the epoch of the phase that wrote it in the high word,
+ * stored and loaded as one 8-byte access at agent scope (the load misses
+ * this CU's L1, whose lines may be stale, and reads the XCD's L2). */
+typedef unsigned long long xv_t;
+
+__device__ __forceinline__ void put_xv(xv_t* p, float v, unsigned int ep) {
+    /* one 8-byte store, single-copy atomic (value and epoch land together).
+     * At wavefront scope it compiles to a plain global_store_dwordx2, which
+     * lands in the XCD's shared L2 (the L1 does not hold writes), where the
+     * readers' agent-scope loads find it; an agent-scope store (sc1) made the
+     * step 14% slower. */
+    __hip_atomic_store(p, ((xv_t)ep << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+__device__ __forceinline__ xv_t get_xv(const xv_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float xv_val(xv_t u) { return __uint_as_float((unsigned int)u); }
+
+/* Until `ready(k)` holds for every k of every lane of the wave, reloads
+ * (reload(k)) the elements not yet ready.  The spin is bounded in time: on
+ * timeout it sets DecState.sync_error and *bad (LDS, read by the workgroup
+ * after its next barrier) and leaves the values as they are. */
+template <int N, typename Ready, typename Reload>
+__device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, DecState* st, int* bad) {
+    auto all_ready = [&] {
+        bool ok = true;
+#pragma unroll
+        for (int k = 0; k < N; k++) ok = ok && ready(k);
+        return __all(ok);
+    };
+    if (all_ready()) return;
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime(); /* 100 MHz */
+    const unsigned long long limit = (unsigned long long)(SPIN_SECONDS * 1e8f);
+    for (;;) {
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if (!ready(k)) reload(k);
+        if (all_ready()) return;
+        if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
+            __hip_atomic_store(&st->sync_error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *bad = 1;
+            return;
+        }
+    }
 }
 
-__device__ __forceinline__ bool grid_wait(DecState* st, unsigned int target, int* flag) {
-    if (threadIdx.x == 0) {
-        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime(); /* 100 MHz */
-        const unsigned long long limit = (unsigned long long)(SPIN_SECONDS * 1e8f);
-        int ok = 1;
-        /* only the clock is checked while polling (a load of sync_error
-         * would add a round trip per poll): a workgroup stuck behind one that
-         * gave up gives up on its own clock */
-        while (__hip_atomic_load(&st->bar, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
-                __hip_atomic_store(&st->sync_error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        *flag = ok;
-    }
-    lds_barrier();
-    asm volatile("" ::: "memory"); /* no load moves above the wait */
-    return *flag != 0;
+/* Elements tid + k * PT (clamped to C - 1) of an exchanged vector of C
+ * values, once they carry epoch ep: one round of loads, then polls. */
+template <int N>
+__device__ __forceinline__ void get_vec(const xv_t* x, int C, unsigned int ep, float (&v)[N], DecState* st, int* bad) {
+    xv_t u[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) u[k] = get_xv(x + min(tid() + k * PT, C - 1));
+    poll_xv<N>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; },
+               [&](int k) { u[k] = get_xv(x + min(tid() + k * PT, C - 1)); }, st, bad);
+#pragma unroll
+    for (int k = 0; k < N; k++) v[k] = xv_val(u[k]);
 }
 
 /* One workgroup's share of a matvec phase: output rows [r0, r1) of
@@ -263,13 +287,14 @@ __device__ __forceinline__ float quad_row_sum(const float* red, int row, int nb)
 }
 
 /* Products of the fetched blocks with xs, per-row sums (a quad of lanes
- * per row), and the outputs: y[r0 + o] = sum, or with a residual (row o
- * of the residual stream in *xres of thread 4o, o < 64) y[r0 + o] = *xres
- * += sum, or for SwiGLU y[r0 + o] = silu(gate) * up (gate row 2o in quad
+ * per row), and the outputs, exchanged with epoch ep: y[r0 + o] = sum, or
+ * with a residual (row o of the residual stream in *xres of thread 4o,
+ * o < 64) y[r0 + o] = *xres += sum (also stored to plain[r0 + o] when plain
+ * is given), or for SwiGLU y[r0 + o] = silu(gate) * up (gate row 2o in quad
  * 2o, up row 2o + 1 in the next quad). */
 template <int NP>
 __device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP], const float* xs, float* red,
-                                          float* y, float* xres) {
+                                          xv_t* y, unsigned int ep, float* xres, float* plain) {
     const int nb = j.nb, nout = j.r1 - j.r0, t = tid();
     mv_products(mv_rows(j), nb, blk, xs, red);
     if (j.glu) {
@@ -277,7 +302,7 @@ __device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP]
             const int o = o0 + (t >> 3), row = min(2 * o + ((t >> 2) & 1), 2 * nout - 1);
             const float sum = quad_row_sum(red, row, nb);
             const float up = dpp<DPP_HALF_MIRROR>(sum); /* lane i of 8 <- 7 - i: the other quad's sum */
-            if ((t & 7) == 0 && o < nout) y[j.r0 + o] = (sum / (1.0f + expf(-sum))) * up;
+            if ((t & 7) == 0 && o < nout) put_xv(y + j.r0 + o, (sum / (1.0f + expf(-sum))) * up, ep);
         }
     } else {
         for (int o0 = 0; o0 < nout; o0 += PT / 4) {
@@ -286,9 +311,10 @@ __device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP]
             if ((t & 3) == 0 && o < nout) {
                 if (xres) {
                     *xres += sum;
-                    y[j.r0 + o] = *xres;
+                    put_xv(y + j.r0 + o, *xres, ep);
+                    if (plain) plain[j.r0 + o] = *xres;
                 } else {
-                    y[j.r0 + o] = sum;
+                    put_xv(y + j.r0 + o, sum, ep);
                 }
             }
         }
@@ -301,19 +327,6 @@ template <int N>
 __device__ __forceinline__ void load_vec(const float* x, int C, float (&v)[N]) {
 #pragma unroll
     for (int k = 0; k < N; k++) v[k] = x[min(tid() + k * PT, C - 1)];
-}
-
-/* A float another CU wrote in the previous phase: an agent-scope load,
- * which misses this CU's L1 and reads the XCD's L2 (a plain load could hit
- * a stale L1 line). */
-__device__ __forceinline__ float ld_agent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-/* load_vec for a vector written in the previous phase. */
-template <int N>
-__device__ __forceinline__ void load_act(const float* x, int C, float (&v)[N]) {
-#pragma unroll
-    for (int k = 0; k < N; k++) v[k] = ld_agent(x + min(tid() + k * PT, C - 1));
 }
 
 /* xs = RMSNorm(x) * nw from x's loaded elements, C <= NW * PT (reference
@@ -401,18 +414,21 @@ __device__ __forceinline__ void load_kv(const DecPersist& a, const Piece& p, int
     }
 }
 
-/* Issues the loads of the piece's q, k and v (this step's, written by the
- * previous phase); its first sub-chunk's cached keys and values are loaded
- * by load_kv before the barrier that precedes the phase. */
-__device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, AttnRegs& r) {
-    const int t = tid();
-    auto raw = [&](int i) {
+/* The piece's q, k and v (this step's, exchanged by the previous phase with
+ * epoch ep: q at qkv[0, QD), k at qkv[QD, QD + KV), v after it): two
+ * elements per thread, polled until they carry ep. */
+__device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, AttnRegs& r, const xv_t* qkv,
+                                          unsigned int ep, DecState* st, int* bad) {
+    auto addr = [&](int i) {
         i = min(i, p.nraw - 1);
-        return ld_agent(i < p.nq ? a.q + (size_t)p.kh * p.nq + i
-                                 : i < p.nq + HD ? a.k + p.kh * HD + i - p.nq : a.v + p.kh * HD + i - p.nq - HD);
+        return i < p.nq ? qkv + (size_t)p.kh * p.nq + i
+                        : i < p.nq + HD ? qkv + a.QD + p.kh * HD + i - p.nq : qkv + a.QD + a.KV + p.kh * HD + i - p.nq - HD;
     };
-    r.r0 = raw(t);
-    r.r1 = raw(t + PT);
+    xv_t u[2] = {get_xv(addr(tid())), get_xv(addr(tid() + PT))};
+    poll_xv<2>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; },
+               [&](int k) { u[k] = get_xv(addr(tid() + k * PT)); }, st, bad);
+    r.r0 = xv_val(u[0]);
+    r.r1 = xv_val(u[1]);
 }
 
 /* The sub-chunk's cached keys and values into LDS. */
@@ -434,7 +450,7 @@ __device__ __forceinline__ void put_kv(const Piece& p, int base, const AttnRegs&
  * the scores, lane = dimension for P.V, the sub-chunk's values in LDS),
  * written as (max, sum, P.V[HD]) to the partial buffer. */
 __device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p, int pos, float rc, float rs, AttnRegs& r,
-                             float* lds, float* kvs) {
+                             float* lds, float* kvs, xv_t* apart, unsigned int ep) {
     const int t = tid(), wave = t >> 6, lane = t & 63;
     const int qk = p.nq + HD; /* roped elements */
     f4* kst = (f4*)kvs;
@@ -506,48 +522,57 @@ __device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p
         lds_barrier();
     }
     if (wave < p.kv_mul) {
-        float* pr = a.apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
-        pr[2 + lane] = acc;
+        xv_t* pr = apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        put_xv(pr + 2 + lane, acc, ep);
         if (lane == 0) {
-            pr[0] = m_run;
-            pr[1] = l_run;
+            put_xv(pr, m_run, ep);
+            put_xv(pr + 1, l_run, ep);
         }
     }
 }
 
 /* The partials of a chunk without keys. */
-__device__ __forceinline__ void attn_empty(const DecPersist& a, const Piece& p) {
+__device__ __forceinline__ void attn_empty(const Piece& p, xv_t* apart, unsigned int ep) {
     const int wave = tid() >> 6, lane = tid() & 63;
     if (wave < p.kv_mul) {
-        float* pr = a.apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
-        pr[2 + lane] = 0.f;
+        xv_t* pr = apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        put_xv(pr + 2 + lane, 0.f, ep);
         if (lane == 0) {
-            pr[0] = -INFINITY;
-            pr[1] = 0.f;
+            put_xv(pr, -INFINITY, ep);
+            put_xv(pr + 1, 0.f, ep);
         }
     }
 }
 
-/* Attention output of every query head from the partials of its chunks,
- * staged into LDS with one round of loads (after_loads then issues more
- * loads, once the partials' registers are free):
- * out[h][d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c, the
- * weights e^(m_c - M) computed once per (head, chunk) (ew). */
+/* Attention output of every query head from the partials of its chunks
+ * (exchanged with epoch ep), staged into LDS with one round of loads and
+ * polls (after_loads then issues more loads, once the partials' registers
+ * are free): out[h][d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c,
+ * the weights e^(m_c - M) computed once per (head, chunk) (ew). */
 template <typename F>
-__device__ __forceinline__ void attn_merge(const DecPersist& a, float* aps, float* ew, float* xs, F&& after_loads) {
-    const int total4 = a.NH * DEC_PERSIST_NCH * APR / 4;
-    /* 16-byte agent-scope loads (sc1: miss the L1) through a buffer
-     * resource over the partials; past its end a buffer load returns 0 */
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(a.apart, (short)0, total4 * 16, BUF_FLAGS);
-    f4 v[APS_MAX / 4 / PT];
+__device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apart, unsigned int ep, float* aps, float* ew,
+                                           float* xs, DecState* st, int* bad, F&& after_loads) {
+    const int total2 = a.NH * DEC_PERSIST_NCH * APR / 2; /* 16-byte loads of two exchanged values */
+    /* agent-scope (sc1: miss the L1) loads through a buffer resource over the
+     * partials; past its end a buffer load returns 0 (such slots count as
+     * ready) */
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)apart, (short)0, total2 * 16, BUF_FLAGS);
+    constexpr int NL = APS_MAX / 2 / PT;
+    f4 v[NL];
+    auto load = [&](int k) {
+        v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * (tid() + k * PT), 0, CPOL_SC1));
+    };
 #pragma unroll
-    for (int k = 0; k < APS_MAX / 4 / PT; k++)
-        v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (tid() + k * PT), 0, CPOL_SC1));
-    issue_order();
+    for (int k = 0; k < NL; k++) load(k);
+    poll_xv<NL>([&](int k) {
+                    return tid() + k * PT >= total2 ||
+                           (__float_as_uint(v[k].y) == ep && __float_as_uint(v[k].w) == ep);
+                },
+                load, st, bad);
 #pragma unroll
-    for (int k = 0; k < APS_MAX / 4 / PT; k++) {
+    for (int k = 0; k < NL; k++) {
         const int i = tid() + k * PT;
-        if (i < total4) ((f4*)aps)[i] = v[k];
+        if (i < total2) ((float2*)aps)[i] = make_float2(v[k].x, v[k].z);
     }
     issue_order();
     after_loads();
@@ -587,12 +612,22 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     __shared__ __attribute__((aligned(16))) float big[APS_MAX]; /* attention partials, or one K and V sub-chunk */
     __shared__ float sh[PT / 64];
     __shared__ float ew[XS_MAX / HD * DEC_PERSIST_NCH]; /* attention merge weights */
-    __shared__ int flag;
+    __shared__ int bad; /* a wave of this workgroup timed out waiting for a value */
     DecState* st = a.st;
     const int pos = st->pos;
     const int D = a.D, H = a.H, QD = a.QD, KV = a.KV;
     const bool has_piece = w < a.NKV * DEC_PERSIST_NCH;
-    unsigned int target = 0;
+    /* the exchanged vectors, and the epochs of this step's phases: phase p
+     * (1..5) of layer l writes with epoch (steps << 8) + 5 l + p, where steps
+     * (advanced by the embedding kernel before every step, never reset) is
+     * the same for every workgroup of the launch */
+    xv_t* xf = a.ex + 1;
+    xv_t* hf = xf + D;
+    xv_t* qkvf = hf + H;
+    xv_t* apf = qkvf + QD + 2 * KV;
+    const unsigned int ep0 = __hip_atomic_load((const unsigned int*)a.ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 8;
+    auto ep = [&](int l, int ph) { return ep0 + (unsigned int)(5 * l + ph); };
+    if (tid() == 0) bad = 0;
 
     /* cos, sin of the step's RoPE angle for rotary pair lane % 32 */
     float rc, rs;
@@ -649,7 +684,8 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             blk[p] = load_block(base + (size_t)r * row_bytes + (size_t)(own ? bc : 0) * 36);
         }
     };
-    auto finish_qkv = [&](const MvShare& s0, const MvShare& s1, const MvShare& s2, const Blk(&blk)[P_QKV]) {
+    auto finish_qkv = [&](const MvShare& s0, const MvShare& s1, const MvShare& s2, const Blk(&blk)[P_QKV],
+                          unsigned int e) {
         const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0, n2 = s2.r1 - s2.r0;
         const int nb = s0.nb, o = tid();
         mv_products(n0 + n1 + n2, nb, blk, xs, red);
@@ -657,9 +693,9 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             const int r = r0 + (o >> 2);
             const float acc = quad_row_sum(red, min(r, n0 + n1 + n2 - 1), nb);
             if ((o & 3) == 0 && r < n0 + n1 + n2) {
-                if (r < n0) a.q[s0.r0 + r] = acc;
-                else if (r < n0 + n1) a.k[s1.r0 + r - n0] = acc;
-                else a.v[s2.r0 + r - n0 - n1] = acc;
+                if (r < n0) put_xv(qkvf + s0.r0 + r, acc, e);
+                else if (r < n0 + n1) put_xv(qkvf + QD + s1.r0 + r - n0, acc, e);
+                else put_xv(qkvf + QD + KV + s2.r0 + r - n0 - n1, acc, e);
             }
         }
     };
@@ -672,55 +708,57 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     fetch_qkv(q0, q1, q2, bq);
     fetch_norm(a.ln1, nw);
     for (int l = 0; l < a.L; l++) {
-        /* 1. RMSNorm + q, k, v; o's weights stream in behind x */
+        /* 1. RMSNorm + q, k, v; o's weights stream in behind x.  At the first
+         * layer x is the embedding kernel's output (plain). */
         {
             float v[NW];
-            load_act(a.x, D, v);
+            if (l == 0) load_vec(a.x, D, v);
+            else get_vec(xf, D, ep(l - 1, 5), v, st, &bad);
             issue_order();
             mv_fetch(so, bo);
             norm_to_lds(v, D, nw, a.eps, xs, sh);
         }
-        finish_qkv(q0, q1, q2, bq);
-        grid_arrive(st);
+        if (bad) return;
+        finish_qkv(q0, q1, q2, bq, ep(l, 1));
         /* 2. RoPE + KV append + attention pieces.  The piece's cached keys and
          * values (positions before pos, written by earlier steps) do not
-         * depend on this step's q, k, v: their loads fly during the wait. */
+         * depend on this step's q, k, v: their loads go first. */
         {
             const Piece pc = make_piece(a, l, w, pos);
             const bool live = has_piece && pc.k0 < pc.k1;
             AttnRegs ar;
-            if (live) load_kv(a, pc, pc.k0, ar);
-            if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
-            if (live) attn_load(a, pc, ar);
+            if (live) {
+                load_kv(a, pc, pc.k0, ar);
+                attn_load(a, pc, ar, qkvf, ep(l, 1), st, &bad);
+            }
             issue_order();
             fetch_norm(a.ln2 + (size_t)l * D, nw);
-            if (live) attn_compute(a, pc, pos, rc, rs, ar, xs, big);
-            else if (has_piece) attn_empty(a, pc);
+            lds_barrier();
+            if (bad) return;
+            if (live) attn_compute(a, pc, pos, rc, rs, ar, xs, big, apf, ep(l, 2));
+            else if (has_piece) attn_empty(pc, apf, ep(l, 2));
         }
-        grid_arrive(st);
-        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
         /* 3. merge + o + residual; gate/up weights stream in behind the partials */
-        attn_merge(a, big, ew, xs, [&] { mv_fetch(sg, bg); });
-        mv_finish(so, bo, xs, red, a.x, &xres);
-        grid_arrive(st);
-        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        attn_merge(a, apf, ep(l, 2), big, ew, xs, st, &bad, [&] { mv_fetch(sg, bg); });
+        if (bad) return;
+        mv_finish(so, bo, xs, red, xf, ep(l, 3), &xres, nullptr);
         /* 4. RMSNorm + gate, up + SwiGLU; down's weights stream in behind x */
         {
             float v[NW];
-            load_act(a.x, D, v);
+            get_vec(xf, D, ep(l, 3), v, st, &bad);
             issue_order();
             mv_fetch(sd, bd);
             norm_to_lds(v, D, nw, a.eps, xs, sh);
         }
-        mv_finish(sg, bg, xs, red, a.h, nullptr);
-        grid_arrive(st);
-        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        if (bad) return;
+        mv_finish(sg, bg, xs, red, hf, ep(l, 4), nullptr, nullptr);
         /* 5. down + residual; the next layer's q, k, v and first RMSNorm
          * weights stream in behind h (after the last layer: the last
-         * layer's again, unused; no branch, so that h's loads stay first) */
+         * layer's again, unused; no branch, so that h's loads stay first).
+         * The last layer also writes x plain, for the LM head. */
         {
             float v[XR];
-            load_act(a.h, H, v);
+            get_vec(hf, H, ep(l, 4), v, st, &bad);
             issue_order();
             const int ln = min(l + 1, a.L - 1);
             shares(ln, q0, q1, q2, so, sg, sd);
@@ -729,9 +767,8 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             issue_order();
             vec_to_lds(v, H, xs);
         }
-        mv_finish(sd, bd, xs, red, a.x, &xres);
-        grid_arrive(st);
-        if (!grid_wait(st, target += DEC_PERSIST_WGS, &flag)) return;
+        if (bad) return;
+        mv_finish(sd, bd, xs, red, xf, ep(l, 5), &xres, l == a.L - 1 ? a.x : nullptr);
     }
 }
 
@@ -758,6 +795,8 @@ extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
 }
 
 extern "C" int dec_launch_persist(const DecPersist* a, hipStream_t s) {
+    BMK_REQUIRE(a->L >= 1 && a->L <= DEC_PERSIST_MAX_L && a->ex, "persistent step: L=%d outside [1, %d] or no exchange buffer",
+                a->L, DEC_PERSIST_MAX_L);
     hipLaunchKernelGGL(k_dec_persist, dim3(8 * DEC_PERSIST_WGS), dim3(PT), 0, s, *a);
     BMK_LAUNCH_CHECK();
     return 0;

@@ -37,9 +37,8 @@ typedef struct {
     unsigned int done;/* head workgroups finished in the current step */
     int B;
     int bad_token;    /* set when an input token was outside [0, V) (0 was used instead) */
-    int sync_error;   /* set (and kept) when a barrier of the persistent step kernel timed out */
-    unsigned int bar; /* barrier counter of the persistent step kernel, zeroed by the embedding kernel */
-    int pad_;
+    int sync_error;   /* set (and kept) when the persistent step kernel timed out waiting for a value */
+    int pad_[2];
     int token[DEC_MAX_B];        /* input token of the current step */
     int host_token[DEC_MAX_B];
     int last_token[DEC_MAX_B];   /* argmax of the last finished step */
@@ -108,16 +107,26 @@ typedef struct {
 
 /* Every layer of a batch-1 decode step in one persistent kernel on one
  * XCD (decode_persist.hip): DEC_PERSIST_WGS working workgroups, attention
- * split into DEC_PERSIST_NCH key chunks per KV head. */
+ * split into DEC_PERSIST_NCH key chunks per KV head, at most
+ * DEC_PERSIST_MAX_L layers (the epochs of one step's phases stay below 256).
+ *
+ * The exchange buffer carries what the phases pass between workgroups, each
+ * float with the epoch of the phase that wrote it (8 bytes: the float's bits
+ * in the low word, the epoch in the high word), after a first 8-byte word
+ * whose low half counts the steps (advanced by the embedding kernel; the
+ * host never writes it):
+ *   [1, 1 + D)            x, the residual stream after a phase
+ *   [.., + H)             h, the SwiGLU output
+ *   [.., + NH*HD + 2 KV)  q, k, v
+ *   [.., + NH*NCH*(HD+2)) the attention partials (max, sum, P.V[HD]) */
 #define DEC_PERSIST_WGS 32
 #define DEC_PERSIST_NCH 10
+#define DEC_PERSIST_MAX_L 50
+#define DEC_PERSIST_EX_WORDS(D, H, QD, KV, NH, HD) \
+    (1 + (size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) + (size_t)(NH) * DEC_PERSIST_NCH * ((HD) + 2))
 typedef struct {
-    float* x;                  /* [D] residual stream */
-    float* q;                  /* [NH*HD] */
-    float* k;                  /* [KV] */
-    float* v;                  /* [KV] */
-    float* h;                  /* [H] */
-    float* apart;              /* [NH][DEC_PERSIST_NCH][HD + 2] attention partials (max, sum, P.V) */
+    float* x;                  /* [D] residual stream: the embedding at the first layer, the result after the last */
+    unsigned long long* ex;    /* the exchange buffer (above), zeroed when allocated */
     float* kvc;                /* the session's KV cache, batch row 0 */
     DecState* st;
     const unsigned char* w;    /* Q8 arena of layer 0; layer l at w + l * layer_bytes */
@@ -136,6 +145,7 @@ typedef struct {
     const int* prompt;   /* [B][n_prompt] (generation mode) */
     float* x;            /* [B][D] */
     DecState* st;
+    unsigned int* steps; /* the persistent step kernel's step counter (advanced here), or NULL */
     int D, V, B;         /* B: the session's batch (one workgroup per sequence) */
 } DecEmbed;
 

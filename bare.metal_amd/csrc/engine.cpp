@@ -134,7 +134,7 @@ struct bm_session_s {
     int pos;             /* host mirror of the position */
     int use_graph;
     int persist;         /* 1: the layers of a step run as one persistent kernel (B = 1, Q8, MI355X) */
-    float* apart;        /* attention partials of the persistent kernel */
+    unsigned long long* pex; /* the persistent kernel's exchange buffer (decode_state.h) */
     hipGraph_t graph;
     hipGraphExec_t gexec;
     int prof_on;
@@ -495,6 +495,7 @@ static int enqueue_step(bm_session_t* S) {
     e.prompt = S->prompt;
     e.x = S->x;
     e.st = S->st;
+    e.steps = S->pex ? (unsigned int*)S->pex : NULL;
     e.D = D;
     e.V = m->V;
     e.B = B;
@@ -503,7 +504,7 @@ static int enqueue_step(bm_session_t* S) {
     if (S->persist == 1) {
         DecPersist pa;
         memset(&pa, 0, sizeof pa);
-        pa.x = S->x; pa.q = S->q; pa.k = S->k; pa.v = S->v; pa.h = S->h; pa.apart = S->apart; pa.kvc = S->kvc;
+        pa.x = S->x; pa.ex = S->pex; pa.kvc = S->kvc;
         pa.st = S->st; pa.w = m->d_q8; pa.layer_bytes = m->layer_bytes;
         for (int i = 0; i < 7; i++) pa.off[i] = m->off[i];
         pa.ln1 = m->d_ln1; pa.ln2 = m->d_ln2;
@@ -581,7 +582,7 @@ static void session_free(bm_session_t* S) {
     if (!S) return;
     if (S->ctx) hipStreamSynchronize(S->ctx->s);
     if (S->gexec) hipGraphExecDestroy(S->gexec);
-    hipFree(S->apart);
+    hipFree(S->pex);
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
     hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->prompt); hipFree(S->out_tokens);
@@ -655,8 +656,10 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
      * gfx950 with the whole device's 256 CUs, batch 1, Q8 projections and a
      * shape it handles. */
     if (ok && batch == 1 && m->quant_bits == 8 && strncmp(ctx->be->dev_name, "gfx950", 6) == 0 &&
-        ctx->be->dev_cu_count == 256 && dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
-        ok = hipMalloc(&S->apart, (size_t)m->NH * DEC_PERSIST_NCH * (m->HD + 2) * 4) == hipSuccess;
+        ctx->be->dev_cu_count == 256 && m->L <= DEC_PERSIST_MAX_L &&
+        dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
+        const size_t ex = DEC_PERSIST_EX_WORDS(m->D, m->H, m->QD, m->KV, m->NH, m->HD) * 8;
+        ok = hipMalloc(&S->pex, ex) == hipSuccess && hipMemsetAsync(S->pex, 0, ex, ctx->s) == hipSuccess;
         S->persist = ok;
     }
     /* a cache slot is written before it is read, but start from zeros anyway */
