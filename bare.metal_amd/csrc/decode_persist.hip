@@ -90,6 +90,7 @@ constexpr int HD = 64;               /* head size */
 constexpr int KCH = 64;              /* keys of one attention sub-chunk (one per lane) */
 constexpr int APS_MAX = 8192;        /* floats of the staged attention partials */
 constexpr int APR = HD + 2;          /* one partial: max, sum, P.V[HD] */
+constexpr int PS_OFF = 1024;         /* attention: the waves' key probabilities in the staged-vector LDS, past q, k, v */
 constexpr float SPIN_SECONDS = 0.2f;
 
 /* threadIdx.x, opaque to the compiler: address arithmetic built on it is
@@ -103,6 +104,7 @@ __device__ __forceinline__ int tid() {
 }
 
 static_assert(2 * KCH * HD <= APS_MAX, "the K and V sub-chunks share the partials' LDS");
+static_assert(4 * HD + 2 * HD <= PS_OFF && PS_OFF + (PT / 64) * KCH <= XS_MAX, "q, k, v and the probabilities share xs");
 static_assert((DEC_PERSIST_NCH * APR) % 2 == 0, "partials load as 16-byte pairs of exchanged values");
 static_assert(P_QKV <= P_MAX && P_O <= P_MAX && P_GU <= P_MAX && P_DN <= P_MAX, "pass caps");
 
@@ -503,9 +505,27 @@ __device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p
             const float csum = wsum(pe);
             const float m_new = fmaxf(m_run, cmax);
             const float a_old = expf(m_run - m_new), a_new = expf(cmax - m_new);
+            /* P.V: the probabilities through LDS (a broadcast read per key)
+             * and each batch of 8 keys' reads issued before its FMAs, added
+             * in key order; a rolled loop would wait out one LDS round trip
+             * per key */
+            float* ps = lds + PS_OFF + wave * KCH;
+            ps[lane] = pe;
+            __builtin_amdgcn_wave_barrier();
             float part = 0.f;
-#pragma unroll 8
-            for (int jk = 0; jk < n; jk++) part = fmaf(lane_value(pe, jk), vst[jk * HD + lane], part);
+            for (int j0 = 0; j0 < n; j0 += 8) {
+                float pp[8], vv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int jk = min(j0 + u, n - 1);
+                    pp[u] = ps[jk];
+                    vv[u] = vst[jk * HD + lane];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (j0 + u < n) part = fmaf(pp[u], vv[u], part);
+            }
+            __builtin_amdgcn_wave_barrier(); /* ps is rewritten by the next sub-chunk */
             l_run = l_run * a_old + csum * a_new;
             acc = acc * a_old + part * a_new;
             m_run = m_new;
