@@ -22,6 +22,7 @@ int bmk_launch_q8_matmul(const bmk_launch_t* a);
 int bmk_launch_q8_matvec_multi(const bmk_launch_t* a);
 int bmk_launch_copy_buffer(const bmk_launch_t* a);
 int bmk_launch_stream_read(const bmk_launch_t* a);
+int bmk_launch_mfma_ceiling(const bmk_launch_t* a);
 int bmk_launch_q8_gemm_multi(const bmk_launch_t* a);
 int bmk_launch_cast_bf16(const bmk_launch_t* a);
 int bmk_launch_rmsnorm(const bmk_launch_t* a);
@@ -75,6 +76,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
     /* new: read-only stream (HBM read ceiling); {src, sink u32[4*wg], params int64{nbytes, wg}} */
     {"stream_read", 3, B(2), B(1), bmk_launch_stream_read, 0},
+    /* new: bf16 matrix-core rate (mode 0 register operands, 1 the GEMM's LDS-fed 2x2 wave tile);
+     * {sink f32[256*wg], params int{wg, iters, mode}} */
+    {"mfma_ceiling", 2, B(1), B(0), bmk_launch_mfma_ceiling, 0},
     /* decode-step kernels (buffer orders: reference scheduler.c:835-947) */
     /* reference forward.metal:1019-1060; {inp, weight, out, params{N,C}, eps} */
     {"rmsnorm_forward_v2", 5, B(3) | B(4), B(2), bmk_launch_rmsnorm, 0},

@@ -546,6 +546,31 @@ def q4_leg(model: str, steps: int, warmup: int):
     }
 
 
+def mfma_ceiling(be, reps: int = 5):
+    """mfma_ceiling: the bf16 32x32x16 MFMA rate of this part with register
+    operands (mode 0) and with the prefill GEMM's LDS-fed 2x2 wave tile and
+    no global traffic (mode 1), TFLOP/s; beside the GEMM's MFMA fraction as
+    stream_read is beside the matvec's bandwidth."""
+    out = {}
+    k = be.kernel("mfma_ceiling")
+    for mode, wg, iters in ((0, 2048, 2000), (1, 1024, 2000)):
+        sink = be.alloc(4 * 256 * wg)
+        p = be.params(wg, iters, mode)
+        enc = be.encoder()
+        if enc.dispatch(k, [sink, p], (wg * 256,), (256,)):
+            raise RuntimeError("mfma_ceiling rejected")
+        enc.wait_timed()
+        enc = be.encoder()
+        for _ in range(reps):
+            enc.dispatch(k, [sink, p], (wg * 256,), (256,))
+        ms = enc.wait_timed() / reps
+        sink.free()
+        tf = wg * 4.0 * iters * 8 * 32768 / (ms * 1e-3) / 1e12
+        out["registers" if mode == 0 else "lds_2x2"] = {"tflops": round(tf, 1),
+                                                         "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
 def gemm_leg(steps: int, warmup: int):
     """Config 4: prefill Q8 GEMM at SmolLM2-135M shapes, M = 512 tokens, all
     30 layers x (q,k,v,o,gate,up,down) in one matmul_forward_q8_multi launch.
@@ -620,7 +645,10 @@ def gemm_leg(steps: int, warmup: int):
     bytes_ = float(wbytes.sum()) + 4.0 * M * float(K.sum()) + 4.0 * float(c_sizes.sum())
     tflops = flops / (ms * 1e-3) / 1e12
     bound = min(MFMA_BF16_PEAK_TFLOPS, flops / bytes_ * HBM_PEAK_GBS / 1e3)
+    ceil = mfma_ceiling(be)
     be.close()
+    log(f"[bench] mfma_ceiling: {ceil['registers']['tflops']} TFLOP/s on register operands, "
+        f"{ceil['lds_2x2']['tflops']} with the GEMM's LDS-fed 2x2 wave tile")
     log(f"[bench] prefill GEMM: {ms * 1e3:.1f} us per 30-layer launch, {tflops:.1f} TFLOP/s "
         f"({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of bf16 MFMA peak, {tflops / bound:.1%} of min(peak, AI*BW)); "
         f"step with the bf16 cast {ms_step * 1e3:.1f} us")
@@ -634,6 +662,7 @@ def gemm_leg(steps: int, warmup: int):
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "min_peak_ai_bw": round(bound, 1), "frac_of_min_bound": round(tflops / bound, 4)},
+        "mfma_ceiling": ceil,
         "workgroups": n_tiles,
     }
 

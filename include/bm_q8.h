@@ -29,6 +29,10 @@
  *   "copy_buffer"        {src, dst, params int64{nbytes}}
  *   "stream_read"        {src, sink u32 [4 * workgroups], params int64{nbytes, workgroups}}
  *                        (reads src once; the HBM read ceiling)
+ *   "mfma_ceiling"       {sink f32 [256 * workgroups], params int{workgroups, iters, mode}}
+ *                        (bf16 32x32x16 MFMAs, workgroups x 4 waves x iters x 8 per launch;
+ *                        mode 0 register operands, 1 operands read from LDS as the prefill
+ *                        GEMM's 2x2 wave tile reads them; the matrix-core ceilings)
  */
 #ifndef BM_Q8_H
 #define BM_Q8_H

@@ -139,3 +139,19 @@ def test_gemm_multi_bf16_activations_match_fp32_path(be):
     for i, (M, K, N) in enumerate(shapes):
         rb = po.q8_gemm_bf16_f64(ws[i], as_[i], M, K, N)
         assert normwise(c16[c_off[i]:c_off[i] + M * N], rb) <= 1e-4
+
+
+def test_mfma_ceiling_kernel(be):
+    """The matrix-core ceiling probe bench.py reports beside the GEMM: both
+    modes run, every lane's accumulator sum is finite and equal across
+    workgroups (same inputs), and bad parameters are rejected."""
+    for mode in (0, 1):
+        wg, iters = 16, 8
+        sink = be.alloc(4 * 256 * wg)
+        assert be.dispatch("mfma_ceiling", [sink, be.params(wg, iters, mode)], (wg * 256,), (256,)) == 0
+        got = sink.read(np.float32).reshape(wg, 256)
+        assert np.isfinite(got).all() and np.abs(got).max() > 0
+        assert (got == got[0]).all()
+    sink = be.alloc(4 * 256)
+    assert be.dispatch("mfma_ceiling", [sink, be.params(1, 1, 2)], (256,), (256,)) == -1
+    assert be.dispatch("mfma_ceiling", [sink, be.params(2, 1, 0)], (512,), (256,)) == -1  # sink too small
