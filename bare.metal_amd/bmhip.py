@@ -68,6 +68,8 @@ def lib() -> C.CDLL:
         "bm_q4_mv_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_q8_gemm_tiles": (i, [i, i, i]),
         "bm_q8_gemm_plan": (C.c_long, [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
+        "bm_q8_gemm_tiles_frag": (i, [i, i, i]),
+        "bm_q8_gemm_plan_frag": (C.c_long, [i, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
         "bm_create": (vp, [i]),
         "bm_destroy": (None, [vp]),
         "bm_get_supported_precision": (i, [vp]),
@@ -174,20 +176,39 @@ def mv_plan(w_off, x_off, y_off, OC, C_, fmt: str = "q8", bt: int = 1):
     return plan.view(np.uint8)[:need].copy(), nt.value
 
 
-def gemm_plan(a_off, w_off, c_off, M, N, K, lda, ldc):
-    """Plan table (bytes) and workgroup count of a matmul_forward_q8_multi launch."""
+def gemm_plan(a_off, w_off, c_off, M, N, K, lda, ldc, frag: bool = False):
+    """Plan table (bytes) and workgroup count of a matmul_forward_q8_multi launch
+    (frag: over fragment-ordered activations, layout 2)."""
     n = len(M)
     u = [np.ascontiguousarray(v, dtype=np.uint64) for v in (a_off, w_off, c_off)]
     ints = [np.ascontiguousarray(v, dtype=np.int32) for v in (M, N, K, lda, ldc)]
     nt = C.c_int(0)
     args = [_ptr(v) for v in u] + [_ptr(v) for v in ints]
-    need = lib().bm_q8_gemm_plan(n, *args, None, 0, C.byref(nt))
+    fn = lib().bm_q8_gemm_plan_frag if frag else lib().bm_q8_gemm_plan
+    need = fn(n, *args, None, 0, C.byref(nt))
     if need < 0:
-        raise ValueError("bm_q8_gemm_plan rejected the problem list")
+        raise ValueError("gemm plan rejected the problem list")
     plan = np.zeros((need + 7) // 8, dtype=np.uint64)
-    if lib().bm_q8_gemm_plan(n, *args, _ptr(plan), plan.nbytes, C.byref(nt)) != need:
-        raise ValueError("bm_q8_gemm_plan failed")
+    if fn(n, *args, _ptr(plan), plan.nbytes, C.byref(nt)) != need:
+        raise ValueError("gemm plan failed")
     return plan.view(np.uint8)[:need].copy(), nt.value
+
+
+def frag_elems(M: int, K: int) -> int:
+    """bf16 values of one matrix in fragment order (cast_f32_bf16_frag)."""
+    return ((M + 31) // 32) * ((K + 63) // 64) * 2048
+
+
+def frag_layout(a: np.ndarray, M: int, K: int, lda: int) -> np.ndarray:
+    """The fragment order of cast_f32_bf16_frag as a host restatement of the
+    indexing (values unrounded): out[((rb*nks + ks)*4 + s)*512 + 8*l + j] =
+    A[32*rb + l%32][64*ks + 32*(l//32) + 8*s + j], zero past M or K."""
+    nrb, nks = (M + 31) // 32, (K + 63) // 64
+    A = np.zeros((nrb * 32, nks * 64), dtype=a.dtype)
+    A[:M, :K] = a.reshape(M, lda)[:, :K]
+    # [rb, r, ks, h, s, j] -> [rb, ks, s, h, r, j]
+    t = A.reshape(nrb, 32, nks, 2, 4, 8).transpose(0, 2, 4, 3, 1, 5)
+    return np.ascontiguousarray(t).reshape(-1)
 
 
 # ---------------------------------------------------------------- backend

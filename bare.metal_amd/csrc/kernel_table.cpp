@@ -25,6 +25,7 @@ int bmk_launch_stream_read(const bmk_launch_t* a);
 int bmk_launch_mfma_ceiling(const bmk_launch_t* a);
 int bmk_launch_q8_gemm_multi(const bmk_launch_t* a);
 int bmk_launch_cast_bf16(const bmk_launch_t* a);
+int bmk_launch_cast_bf16_frag(const bmk_launch_t* a);
 int bmk_launch_rmsnorm(const bmk_launch_t* a);
 int bmk_launch_rope(const bmk_launch_t* a);
 int bmk_launch_kv_store(const bmk_launch_t* a);
@@ -72,6 +73,9 @@ extern "C" const bmk_desc_t bmk_table[] = {
     {"matmul_forward_q8_multi", 5, B(0) | B(1), B(4), bmk_launch_q8_gemm_multi, B(1)},
     /* new: fp32 -> bf16 activation cast (RNE); {src, dst, params int64{n}} */
     {"cast_f32_bf16", 3, B(2), B(1), bmk_launch_cast_bf16, 0},
+    /* new: fp32 -> bf16 (RNE) into MFMA fragment order (matmul_forward_q8_multi layout 2);
+     * {src f32 [M][lda], dst, params int{M, K, lda}} */
+    {"cast_f32_bf16_frag", 3, B(2), B(1), bmk_launch_cast_bf16_frag, 0},
     /* new: device-to-device copy; {src, dst, params int64{nbytes}} */
     {"copy_buffer", 3, B(2), B(1), bmk_launch_copy_buffer, 0},
     /* new: read-only stream (HBM read ceiling); {src, sink u32[4*wg], params int64{nbytes, wg}} */

@@ -14,6 +14,11 @@
 #define GM_BN 128   /* C tile columns (output features) per workgroup */
 #define GM_IDLE_TILE 0xffffffffu /* tile-map entry of a workgroup with no tile */
 #define GM_KSPLIT_MAX 4          /* K slices of a split C tile at most */
+#define GM_FBM 256  /* fragment-ordered activations (layout 2): C tile rows per workgroup */
+#define GM_FBN 96   /*   and columns (576, 192 and 1536 are multiples of 96) */
+#define GM_A_F32 0  /* activation layouts of matmul_forward_q8_multi: fp32 row-major */
+#define GM_A_BF16 1 /*   bf16 row-major */
+#define GM_A_FRAG 2 /*   bf16 in MFMA fragment order (cast_f32_bf16_frag) */
 
 /* C[M][N] (row stride ldc) = A[M][K] (row stride lda) x W^T, W = N rows of K/32 Q8 blocks. */
 typedef struct {
@@ -42,6 +47,8 @@ typedef struct {
 extern "C" {
 #endif
 int gm_tiles_for(int M, int N);
+/* workgroups of one problem over fragment-ordered activations (GM_FBM x GM_FBN tiles) */
+int gm_tiles_frag(int M, int N);
 /* dst = bf16(src), round to nearest even, n elements */
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int gm_launch_group(GmGroup* g, hipStream_t s);

@@ -292,6 +292,220 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     }
 }
 
+/* Fragment-ordered activations (layout GM_A_FRAG).  A[M][K] in bf16 is
+ * stored as 32-row blocks rb and 64-column K steps ks of four 16-deep MFMA
+ * A fragments each: fragment (rb, ks, s) is 512 values at
+ * ((rb * nks + ks) * 4 + s) * 512, lane l's eight at + 8 l, holding
+ * A[32 rb + l % 32][64 ks + 32 (l / 32) + 8 s + j], j < 8; nks = lda / 64
+ * (lda: K rounded up to 64), rows past M and columns past K are zero
+ * (cast_f32_bf16_frag writes the layout).  The K order inside a step is thus
+ * permuted alike in A and W: lane half h of MFMA s takes k = 32 h + 8 s + j,
+ * so a wave loads an A fragment with one coalesced 1 KB instruction,
+ * straight into registers, and LDS carries the weights only.
+ *
+ * Tiles of GM_FBM x GM_FBN (256 x 96): 4 waves along M, each 64 x 96 = 2 x 3
+ * tiles of v_mfma_f32_32x32x16_bf16.  At M = 512 every weight is
+ * dequantised twice (once per 256 rows) and the 96-row weight slab (two
+ * buffers) is the whole of LDS; lanes below 192 stage one Q8/Q4 block of it
+ * per K step.  Pipeline as gemm_tile: the loads of step s+1 (A) and s+2 (W)
+ * are in flight during step s, one barrier per step.  Measured on the 135M
+ * M = 512 set against 128 x 128 tiles over row-major bf16: 164-174 us
+ * against 207-223 us on the same boxes; the same tiles over row-major A
+ * (each wave instruction then touches 32 rows' lines) 210 us, 128 x 128
+ * tiles over fragment-ordered A 220 us, 512 x 96 tiles on 8 waves 183 us,
+ * 256 x 128 tiles (64 x 128 per wave) 167-171 us. */
+constexpr int FB_SLAB = GM_FBN * LDK;
+
+template <int QF>
+__device__ __forceinline__ void gemm_tile_frag(const unsigned short* __restrict__ A, const unsigned char* __restrict__ W,
+                                               float* __restrict__ Cm, int M, int N, int K, int lda, int ldc, int tm,
+                                               int tn, unsigned short* lds) {
+    constexpr unsigned BYTES = QFmt<QF>::BYTES;
+    const int t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int m0 = tm * GM_FBM, n0 = tn * GM_FBN;
+    const int nb = K / 32, nfull = nb >> 1;
+    const int nks = lda / 64, nrb = (M + 31) / 32;
+    unsigned int aoff[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int rb = min((m0 + 64 * wave + 32 * i) / 32, nrb - 1); /* row blocks past M feed no stored C */
+        aoff[i] = (unsigned)(rb * nks) * 2048u + 8u * (unsigned)lane;
+    }
+    const bool wst = t < 2 * GM_FBN; /* W loader lanes: row t/2, block t%2 of the step's pair */
+    const int lr = wst ? t >> 1 : 0, lh = t & 1;
+    const unsigned int woff = (unsigned)min(n0 + lr, N - 1) * (unsigned)(nb * BYTES) + (unsigned)lh * BYTES;
+
+    struct WSt {
+        float s;
+        uint4 q[QF == QF_Q4 ? 1 : 2];
+    };
+    typedef bf16x8 AFr[2][4];
+    auto load_a = [&](int step, AFr& fa) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+                __builtin_memcpy(&fa[i][s], __builtin_assume_aligned(A + aoff[i] + (unsigned)step * 2048u + 512u * s, 16), 16);
+    };
+    auto load_w = [&](const unsigned char* blk, WSt& w) {
+        __builtin_memcpy(&w.s, __builtin_assume_aligned(blk, 4), 4);
+        __builtin_memcpy(&w.q[0], __builtin_assume_aligned(blk + 4, 4), 16);
+        if (QF == QF_Q8) __builtin_memcpy(&w.q[QF == QF_Q8 ? 1 : 0], __builtin_assume_aligned(blk + 20, 4), 16);
+    };
+    auto load_wstep = [&](int step, WSt& w) { load_w(W + woff + (unsigned)step * (2u * BYTES), w); };
+    auto store_w = [&](int buf, const WSt& w) {
+        if (!wst) return;
+        uint4* bp = (uint4*)&lds[buf * FB_SLAB + lr * LDK + 32 * lh];
+        if (QF == QF_Q4) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) bp[j] = dq4(w.q[0], j, w.s);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                bp[2 * i] = dq8(w.q[QF == QF_Q8 ? i : 0], 0, w.s);
+                bp[2 * i + 1] = dq8(w.q[QF == QF_Q8 ? i : 0], 1, w.s);
+            }
+        }
+    };
+
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    f32x16 acc[2][3];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    auto mfma_step = [&](int buf, const AFr& fa) {
+        const unsigned short* Bs = lds + buf * FB_SLAB;
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            bf16x8 fb[3];
+#pragma unroll
+            for (int j = 0; j < 3; j++) fb[j] = *(const bf16x8*)&Bs[(32 * j + r32) * LDK + 32 * h + 8 * s];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 3; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][s], fb[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    if (nfull > 0) {
+        AFr fa0, fa1;
+        WSt w0, w1;
+        load_wstep(0, w0);
+        load_a(0, fa0);
+        load_wstep(min(1, nfull - 1), w1);
+        store_w(0, w0);
+        __syncthreads();
+        int step = 0;
+        /* two steps per iteration so that the register stages are named
+         * statically; past the last step the loads repeat it (cache hits,
+         * never used) */
+        for (; step + 2 <= nfull; step += 2) {
+            load_a(min(step + 1, nfull - 1), fa1);
+            load_wstep(min(step + 2, nfull - 1), w0);
+            __builtin_amdgcn_sched_barrier(0); /* keep the loads ahead of the MFMAs */
+            mfma_step(0, fa0);
+            __builtin_amdgcn_sched_barrier(0);
+            store_w(1, w1);
+            __syncthreads();
+            load_a(min(step + 2, nfull - 1), fa0);
+            load_wstep(min(step + 3, nfull - 1), w1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_step(1, fa1);
+            __builtin_amdgcn_sched_barrier(0);
+            store_w(0, w0);
+            __syncthreads();
+        }
+        if (step < nfull) mfma_step(0, fa0); /* odd step count: the last step sits in buffer 0 */
+    }
+    if (nb & 1) {
+        /* half step (block nb-1 = 2*nfull): A's columns past K are zero in
+         * the layout; block 2*nfull + 1 would lie past the row, so lh = 1
+         * reads block nb-1 again with scale 0 (which zeroes its finite
+         * codes).  Buffer nfull & 1 is free: its last reader was followed by
+         * a barrier. */
+        AFr fa;
+        WSt w;
+        const int buf = nfull & 1;
+        load_a(nfull, fa);
+        load_w(W + woff + (unsigned)nfull * (2u * BYTES) - (unsigned)lh * BYTES, w);
+        if (lh) w.s = 0.0f;
+        store_w(buf, w);
+        __syncthreads();
+        mfma_step(buf, fa);
+    }
+
+    /* epilogue, 32x32 D layout as in gemm_tile: whole 128-byte C row lines,
+     * nontemporal stores for interior tiles */
+    float* Ct = Cm + (size_t)(m0 + 64 * wave + 4 * h) * ldc + n0 + r32;
+    if (m0 + GM_FBM <= M && n0 + GM_FBN <= N) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    __builtin_nontemporal_store(acc[i][j][r], &Ct[(unsigned)(32 * i + 8 * (r >> 2) + (r & 3)) * (unsigned)ldc + 32 * j]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const int col = n0 + 32 * j + r32;
+                if (col >= N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = m0 + 64 * wave + 32 * i + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (row < M) Cm[(size_t)row * ldc + col] = acc[i][j][r];
+                }
+            }
+    }
+}
+
+template <int QF>
+__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_multi_frag(
+    const void* __restrict__ A, const unsigned char* __restrict__ W, float* __restrict__ C,
+    const GmDesc* __restrict__ desc, const unsigned int* __restrict__ tile_map) {
+    __shared__ __attribute__((aligned(16))) unsigned short lds[2 * FB_SLAB];
+    const unsigned int tm_ = tile_map[blockIdx.x];
+    if (tm_ == GM_IDLE_TILE) return;
+    const GmDesc d = desc[tm_ >> 16];
+    const int tile = (int)(tm_ & 0xffffu);
+    const int tiles_n = (d.N + GM_FBN - 1) / GM_FBN;
+    gemm_tile_frag<QF>((const unsigned short*)A + d.a_off, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc,
+                       tile / tiles_n, tile % tiles_n, lds);
+}
+
+/* fp32 [M][lda] -> bf16 in fragment order (see gemm_tile_frag), round to
+ * nearest even; one 16-byte fragment slot (8 values) per lane. */
+__global__ __launch_bounds__(NTH) void k_cast_bf16_frag(const float* __restrict__ src, unsigned short* __restrict__ dst,
+                                                        int M, int K, int lda, int nks, long nslots) {
+    const long i = (long)blockIdx.x * NTH + threadIdx.x;
+    if (i >= nslots) return;
+    const int lane = (int)(i & 63), s = (int)((i >> 6) & 3);
+    const long rk = i >> 8;
+    const int ks = (int)(rk % nks), rb = (int)(rk / nks);
+    const int row = 32 * rb + (lane & 31), col = 64 * ks + 32 * (lane >> 5) + 8 * s;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < M && col < K) { /* K is a multiple of 32: the slot's 8 columns are all inside */
+        float4 a, b;
+        const float* sp = src + (size_t)row * lda + col;
+        __builtin_memcpy(&a, __builtin_assume_aligned(sp, 4), 16);
+        __builtin_memcpy(&b, __builtin_assume_aligned(sp + 4, 4), 16);
+        v.x = pk_bf16(a.x, a.y);
+        v.y = pk_bf16(a.z, a.w);
+        v.z = pk_bf16(b.x, b.y);
+        v.w = pk_bf16(b.z, b.w);
+    }
+    __builtin_memcpy(dst + 8 * i, &v, 16);
+}
+
 template <int QF>
 __device__ __forceinline__ void gemm_group_body(const GmGroup& g, unsigned short* lds) {
     int tile = blockIdx.x;
@@ -399,6 +613,7 @@ __global__ __launch_bounds__(NTH) void k_cast_bf16(const float* __restrict__ src
 } // namespace
 
 extern "C" int gm_tiles_for(int M, int N) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
+extern "C" int gm_tiles_frag(int M, int N) { return ((M + GM_FBM - 1) / GM_FBM) * ((N + GM_FBN - 1) / GM_FBN); }
 
 /* The tile loaders address a problem with 32-bit offsets. */
 static bool gm_offsets_fit(int M, int N, int K, int lda) {
@@ -454,10 +669,12 @@ static int launch_gemm_multi(const bmk_launch_t* a) {
     constexpr unsigned BYTES = QFmt<QF>::BYTES;
     BMK_NEED_BYTES(a, 0, 8, "params");
     const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
-    const int a_bf16 = a->bytes[0] >= 12 ? bmk_pi(a, 0, 2) : 0;
+    const int layout = a->bytes[0] >= 12 ? bmk_pi(a, 0, 2) : GM_A_F32;
+    const int a_bf16 = layout != GM_A_F32;
+    const bool frag = layout == GM_A_FRAG;
     const unsigned long long esz = a_bf16 ? 2 : 4; /* bytes per activation element */
-    BMK_REQUIRE(nprob >= 0 && n_tiles >= 0 && (a_bf16 == 0 || a_bf16 == 1),
-                "q8 gemm multi: bad params nprob=%d n_tiles=%d a_bf16=%d", nprob, n_tiles, a_bf16);
+    BMK_REQUIRE(nprob >= 0 && n_tiles >= 0 && layout >= GM_A_F32 && layout <= GM_A_FRAG,
+                "q8 gemm multi: bad params nprob=%d n_tiles=%d layout=%d", nprob, n_tiles, layout);
     if (nprob == 0 || n_tiles == 0) return 0;
     const size_t desc_bytes = (size_t)nprob * sizeof(GmDesc);
     BMK_NEED_BYTES(a, 1, desc_bytes + (size_t)n_tiles * 4, "plan");
@@ -473,15 +690,23 @@ static int launch_gemm_multi(const bmk_launch_t* a) {
         BMK_REQUIRE(d.M > 0 && d.N > 0 && d.K > 0 && d.K % 32 == 0 && d.lda >= d.K && d.ldc >= d.N,
                     "q8 gemm multi: problem %d bad shape M=%d N=%d K=%d lda=%d ldc=%d", i, d.M, d.N, d.K, d.lda, d.ldc);
         BMK_REQUIRE(d.pad_ == 0, "q8 gemm multi: problem %d has a nonzero reserved field", i);
-        BMK_REQUIRE(d.tiles == gm_tiles_for(d.M, d.N) && d.tile0 == next_tile,
-                    "q8 gemm multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0,
-                    gm_tiles_for(d.M, d.N), next_tile);
+        const int want_tiles = frag ? gm_tiles_frag(d.M, d.N) : gm_tiles_for(d.M, d.N);
+        BMK_REQUIRE(d.tiles == want_tiles && d.tile0 == next_tile,
+                    "q8 gemm multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0, want_tiles,
+                    next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 gemm multi: problem %d weight offset not 4-byte aligned", i);
         BMK_REQUIRE(gm_offsets_fit_q(d.M, d.N, d.K, d.lda, BYTES),
                     "q8 gemm multi: problem %d too large for 32-bit tile offsets", i);
         BMK_REQUIRE((!a_bf16 || (d.a_off % 8 == 0 && d.lda % 8 == 0)),
                     "q8 gemm multi: problem %d bf16 rows must start 16-byte aligned", i);
-        BMK_REQUIRE(d.a_off + (unsigned long long)(d.M - 1) * d.lda + d.K <= a->bytes[2] / esz &&
+        /* fragment order: lda = K rounded up to 64, ceil(M/32) blocks of 32 rows, 1 KB-aligned fragments */
+        const unsigned long long a_end = frag ? d.a_off + (unsigned long long)((d.M + 31) / 32) * 32ull * d.lda
+                                              : d.a_off + (unsigned long long)(d.M - 1) * d.lda + d.K;
+        BMK_REQUIRE(!frag || (d.lda % 64 == 0 && d.lda < d.K + 64 && d.a_off % 512 == 0 &&
+                              (unsigned long long)((d.M + 31) / 32) * 32ull * d.lda < 0x80000000ull),
+                    "q8 gemm multi: problem %d fragment-order activations need lda = K rounded up to 64 and "
+                    "a 512-element-aligned offset (lda=%d K=%d a_off=%llu)", i, d.lda, d.K, d.a_off);
+        BMK_REQUIRE(a_end <= a->bytes[2] / esz &&
                         d.w_off + (unsigned long long)d.N * (d.K / 32) * BYTES <= a->bytes[3] &&
                         d.c_off + (unsigned long long)(d.M - 1) * d.ldc + d.N <= a->bytes[4] / 4,
                     "q8 gemm multi: problem %d lies outside its arenas", i);
@@ -514,7 +739,9 @@ static int launch_gemm_multi(const bmk_launch_t* a) {
     const void* A = (const void*)a->dev[2];
     const unsigned char* W = (const unsigned char*)a->dev[3];
     float* C = (float*)a->dev[4];
-    if (QF == QF_Q4) {
+    if (frag) {
+        hipLaunchKernelGGL(k_gemm_multi_frag<QF>, grid, tb, 0, a->stream, A, W, C, dd, dt);
+    } else if (QF == QF_Q4) {
         if (a_bf16) hipLaunchKernelGGL(k_q4_gemm_multi<true>, grid, tb, 0, a->stream, A, W, C, dd, dt);
         else hipLaunchKernelGGL(k_q4_gemm_multi<false>, grid, tb, 0, a->stream, A, W, C, dd, dt);
     } else {
@@ -544,6 +771,28 @@ extern "C" int bmk_launch_cast_bf16(const bmk_launch_t* a) {
     const long threads = n8 + 1;
     hipLaunchKernelGGL(k_cast_bf16, dim3((unsigned)((threads + NTH - 1) / NTH)), dim3(NTH), 0, a->stream,
                        (const float*)a->dev[0], (unsigned short*)a->dev[1], n8, (long)n);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* cast_f32_bf16_frag {src f32 [M][lda], dst bf16 in fragment order, params int{M, K, lda}}:
+ * the activations of a matmul_forward_q8_multi problem with layout 2 (the
+ * destination holds ceil(M/32) x ceil(K/64) x 2048 values, padding zeroed;
+ * the problem's lda is K rounded up to 64). */
+extern "C" int bmk_launch_cast_bf16_frag(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 12, "params");
+    const int M = bmk_pi(a, 2, 0), K = bmk_pi(a, 2, 1), lda = bmk_pi(a, 2, 2);
+    BMK_REQUIRE(M > 0 && K > 0 && K % 32 == 0 && lda >= K, "cast_f32_bf16_frag: bad params M=%d K=%d lda=%d", M, K,
+                lda);
+    const long nrb = (M + 31) / 32, nks = (K + 63) / 64;
+    const long nslots = nrb * nks * 256; /* 16-byte slots: 4 fragments x 64 lanes per (block, step) */
+    BMK_REQUIRE(nrb * 32 * nks * 64 < 0x80000000L, "cast_f32_bf16_frag: %d x %d is too large", M, K);
+    BMK_NEED_BYTES(a, 0, ((size_t)(M - 1) * lda + K) * 4, "src");
+    BMK_NEED_BYTES(a, 1, (size_t)nslots * 16, "dst");
+    BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 15) == 0,
+                "cast_f32_bf16_frag: src must be 4-byte and dst 16-byte aligned");
+    hipLaunchKernelGGL(k_cast_bf16_frag, dim3((unsigned)((nslots + NTH - 1) / NTH)), dim3(NTH), 0, a->stream,
+                       (const float*)a->dev[0], (unsigned short*)a->dev[1], M, K, lda, (int)nks, nslots);
     BMK_LAUNCH_CHECK();
     return 0;
 }

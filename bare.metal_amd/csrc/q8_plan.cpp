@@ -83,6 +83,19 @@ extern "C" int bm_q8_gemm_tiles(int M, int N, int K) {
     return gm_tiles_for(M, N);
 }
 
+/* The same for fragment-ordered activations (GM_FBM x GM_FBN tiles). */
+extern "C" int bm_q8_gemm_tiles_frag(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32) return -1;
+    return gm_tiles_frag(M, N);
+}
+
+/* C tile geometry of a plan: rows and columns per tile */
+struct GmGeo {
+    int bm, bn;
+    int tiles(int M, int N) const { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+};
+static const GmGeo GEO_ROWMAJOR = {GM_BM, GM_BN}, GEO_FRAG = {GM_FBM, GM_FBN};
+
 /* Workgroup order of a multi-GEMM launch.  MI355X dispatches workgroup b
  * to XCD b % 8, and each XCD has its own L2.  Every (problem, N tile) pair
  * is given to one XCD, round-robin, and its M tiles run back to back
@@ -98,9 +111,9 @@ extern "C" int bm_q8_gemm_tiles(int M, int N, int K) {
 /* Split-K factor of a launch, the same for all its problems: 1, unless
  * the launch has fewer than `target` C tiles; then enough K slices to reach
  * it, at most kmax and at most one slice per two K blocks of any problem. */
-static int gemm_split(int nprob, const int* M, const int* N, const int* K, int target, int kmax) {
+static int gemm_split(const GmGeo& g, int nprob, const int* M, const int* N, const int* K, int target, int kmax) {
     long total = 0;
-    for (int i = 0; i < nprob; i++) total += gm_tiles_for(M[i], N[i]);
+    for (int i = 0; i < nprob; i++) total += g.tiles(M[i], N[i]);
     int want = 1;
     if (total > 0 && total < target) want = (int)((target + total - 1) / total);
     if (want > kmax) want = kmax;
@@ -111,11 +124,11 @@ static int gemm_split(int nprob, const int* M, const int* N, const int* K, int t
 
 /* Workgroups per XCD queue: every (problem, N tile, K slice) group goes to
  * one XCD, round robin, with its M tiles consecutive; ks K slices per problem. */
-static long gemm_queue_len(int nprob, const int* M, const int* N, int ks, long* per_xcd) {
+static long gemm_queue_len(const GmGeo& g, int nprob, const int* M, const int* N, int ks, long* per_xcd) {
     for (int x = 0; x < GM_XCDS; x++) per_xcd[x] = 0;
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
-        const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
+        const int tm = (M[i] + g.bm - 1) / g.bm, tn = (N[i] + g.bn - 1) / g.bn;
         for (int n = 0; n < tn; n++)
             for (int k = 0; k < ks; k++, pair++) per_xcd[pair % GM_XCDS] += tm;
     }
@@ -127,22 +140,23 @@ static long gemm_queue_len(int nprob, const int* M, const int* N, int ks, long* 
 /* Plan of one multi-GEMM launch: GmDesc[nprob], then the tile map.  A
  * problem with ksplit > 1 (GmDesc.pad_) has tiles = C tiles * ksplit, tile
  * index = slice * C tiles + C tile. */
-static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                            const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
                            int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
     if (nprob < 0 || nprob > 0xffff || (nprob > 0 && (!a_off || !w_off || !c_off || !M || !N || !K || !lda || !ldc)))
         return -1;
     for (int i = 0; i < nprob; i++) {
-        const int t = bm_q8_gemm_tiles(M[i], N[i], K[i]);
-        if (t < 0 || t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
+        if (M[i] <= 0 || N[i] <= 0 || K[i] <= 0 || K[i] % 32) return -1;
+        const int t = g.tiles(M[i], N[i]);
+        if (t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
     }
     /* one split factor for every problem of the launch (no host allocation here:
      * the engine's prefill plans are also made by the no-allocation entry point) */
-    const int ks = target > 0 ? gemm_split(nprob, M, N, K, target, kmax) : 1;
+    const int ks = target > 0 ? gemm_split(g, nprob, M, N, K, target, kmax) : 1;
     for (int i = 0; i < nprob; i++)
-        if ((long)gm_tiles_for(M[i], N[i]) * ks > 0xffff) return -1;
+        if ((long)g.tiles(M[i], N[i]) * ks > 0xffff) return -1;
     long per_xcd[GM_XCDS];
-    const long slots = (long)GM_XCDS * gemm_queue_len(nprob, M, N, ks, per_xcd);
+    const long slots = (long)GM_XCDS * gemm_queue_len(g, nprob, M, N, ks, per_xcd);
     if (slots > 0x7fffffffL) return -1;
     const size_t need = (size_t)nprob * sizeof(GmDesc) + (size_t)slots * 4;
     if (n_tiles_out) *n_tiles_out = (int)slots;
@@ -162,7 +176,7 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
         d[i].lda = lda[i];
         d[i].ldc = ldc[i];
         d[i].tile0 = t0;
-        d[i].tiles = gm_tiles_for(M[i], N[i]) * ks;
+        d[i].tiles = g.tiles(M[i], N[i]) * ks;
         d[i].pad_ = ks > 1 ? ks : 0;
         t0 += d[i].tiles;
     }
@@ -170,7 +184,7 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
     long fill[GM_XCDS] = {0};
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
-        const int tm = (M[i] + GM_BM - 1) / GM_BM, tn = (N[i] + GM_BN - 1) / GM_BN;
+        const int tm = (M[i] + g.bm - 1) / g.bm, tn = (N[i] + g.bn - 1) / g.bn;
         for (int n = 0; n < tn; n++)
             for (int k = 0; k < ks; k++, pair++) {
                 const int x = (int)(pair % GM_XCDS);
@@ -185,8 +199,18 @@ static long gemm_plan_impl(int nprob, const uint64_t* a_off, const uint64_t* w_o
 extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                                 const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
                                 size_t plan_bytes, int* n_tiles_out) {
-    return gemm_plan_impl(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes, n_tiles_out,
-                          nullptr);
+    return gemm_plan_impl(GEO_ROWMAJOR, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes,
+                          n_tiles_out, nullptr);
+}
+
+/* The plan of a launch over fragment-ordered activations (layout 2): a_off[i]
+ * in elements of the bf16 fragment arena (a multiple of 512), lda[i] = K[i]
+ * rounded up to 64. */
+extern "C" long bm_q8_gemm_plan_frag(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                                     const int* M, const int* N, const int* K, const int* lda, const int* ldc,
+                                     void* plan, size_t plan_bytes, int* n_tiles_out) {
+    return gemm_plan_impl(GEO_FRAG, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes,
+                          n_tiles_out, nullptr);
 }
 
 /* The engine's prefill plans: split-K when the launch has fewer than
@@ -194,6 +218,6 @@ extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t
 extern "C" long gm_plan_split(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                               const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
                               int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
-    return gemm_plan_impl(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, target, kmax, plan, plan_bytes, n_tiles_out,
-                          ksplit_out);
+    return gemm_plan_impl(GEO_ROWMAJOR, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, target, kmax, plan, plan_bytes,
+                          n_tiles_out, ksplit_out);
 }

@@ -22,10 +22,19 @@
  *                        as matmul_forward_q8_vec_multi over Q4_0 rows, plan from
  *                        bm_q4_mv_plan
  *   "matmul_forward_q8_multi"
- *                        {params int{nprob, n_tiles[, a_bf16]}, plan (bm_q8_gemm_plan),
- *                         activation arena (f32, or bf16 when a_bf16 = 1),
- *                         weight arena, output arena f32}
+ *                        {params int{nprob, n_tiles[, layout]}, plan, activation arena,
+ *                         weight arena, output arena f32}; layout 0: f32 row-major,
+ *                         1: bf16 row-major (plans from bm_q8_gemm_plan), 2: bf16 in
+ *                         MFMA fragment order written by cast_f32_bf16_frag (plans from
+ *                         bm_q8_gemm_plan_frag)
  *   "cast_f32_bf16"      {src f32 [n], dst bf16 [n], params int64{n}} (round to nearest even)
+ *   "cast_f32_bf16_frag" {src f32 [M][lda], dst bf16, params int{M, K, lda}}: the same
+ *                        rounding into fragment order: 32-row blocks rb, 64-column steps ks
+ *                        (nks = ceil(K/64) per block), four fragments s of 512 values each,
+ *                        value j of lane l of fragment (rb, ks, s) at
+ *                        ((rb * nks + ks) * 4 + s) * 512 + 8 l + j holding
+ *                        A[32 rb + l % 32][64 ks + 32 (l / 32) + 8 s + j]; rows past M and
+ *                        columns past K are zero (ceil(M/32) * nks * 2048 values)
  *   "copy_buffer"        {src, dst, params int64{nbytes}}
  *   "stream_read"        {src, sink u32 [4 * workgroups], params int64{nbytes, workgroups}}
  *                        (reads src once; the HBM read ceiling)
@@ -85,6 +94,14 @@ int  bm_q8_gemm_tiles(int M, int N, int K);
 long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                      const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
                      size_t plan_bytes, int* n_tiles);
+
+/* The same over fragment-ordered activations (layout 2: 256 x 96 output
+ * tiles): a_off[i] is the element offset of problem i's fragment block (a
+ * multiple of 512) and lda[i] its K rounded up to 64. */
+int  bm_q8_gemm_tiles_frag(int M, int N, int K);
+long bm_q8_gemm_plan_frag(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
+                          const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
+                          size_t plan_bytes, int* n_tiles);
 
 #ifdef __cplusplus
 }

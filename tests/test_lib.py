@@ -180,3 +180,25 @@ def test_bmv_plan_layout():
     assert desc[:, 6:].tolist() == [[960, 960, 0, 4], [257, 64, 4, 2]]  # OC, C, tile0, tiles
     tmap = np.frombuffer(plan[80:].tobytes(), dtype=np.uint32)
     assert list(tmap) == [0] * 4 + [1] * 2
+
+
+def test_gemm_frag_plan():
+    """Plans over fragment-ordered activations (layout 2): 256 x 96 C tiles,
+    every (problem, tile) named once, and the M tiles of one (problem, N tile)
+    pair on one XCD, as in the row-major plans."""
+    import numpy as np
+
+    t = bmhip.lib().bm_q8_gemm_tiles_frag
+    assert t(512, 576, 576) == 12 and t(512, 192, 576) == 4 and t(512, 1536, 576) == 32
+    assert t(257, 97, 64) == 4 and t(16, 48, 48) == -1
+    M, N, K = [512, 300], [576, 200], [576, 224]
+    plan, n = bmhip.gemm_plan([0, 8192], [0, 0], [0, 0], M, N, K, [576, 256], N, frag=True)
+    desc = np.frombuffer(plan[:112].tobytes(), dtype=np.int32).reshape(2, 14)  # GmDesc is 56 bytes
+    assert desc[:, 6:].tolist() == [[512, 576, 576, 576, 576, 0, 12, 0], [300, 200, 224, 256, 200, 12, 6, 0]]
+    tmap = np.frombuffer(plan[112:].tobytes(), dtype=np.uint32)
+    assert n == tmap.size and n % 8 == 0
+    live = [(b, int(v) >> 16, int(v) & 0xFFFF) for b, v in enumerate(tmap) if v != 0xFFFFFFFF]
+    assert sorted((p, tl) for _, p, tl in live) == [(0, i) for i in range(12)] + [(1, i) for i in range(6)]
+    for p, tn in ((0, 6), (1, 3)):
+        for nt in range(tn):  # tile = m * tiles_n + n: the pair's M tiles share an XCD
+            assert len({b % 8 for b, q, tl in live if q == p and tl % tn == nt}) == 1

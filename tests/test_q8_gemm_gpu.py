@@ -155,3 +155,139 @@ def test_mfma_ceiling_kernel(be):
     sink = be.alloc(4 * 256)
     assert be.dispatch("mfma_ceiling", [sink, be.params(1, 1, 2)], (256,), (256,)) == -1
     assert be.dispatch("mfma_ceiling", [sink, be.params(2, 1, 0)], (512,), (256,)) == -1  # sink too small
+
+
+# ------------------------------------------------- fragment-ordered activations (layout 2)
+
+def _frag_arena(be, mats):
+    """Casts each fp32 matrix (a, M, K, lda) into its own block of one
+    fragment-order arena with cast_f32_bf16_frag; returns (arena, element
+    offsets, padded K per matrix)."""
+    offs, ldas, tot = [], [], 0
+    for a, M, K, lda in mats:
+        offs.append(tot)
+        ldas.append((K + 63) // 64 * 64)
+        tot += bmhip.frag_elems(M, K)
+    F = be.alloc(2 * tot)
+    for (a, M, K, lda), off in zip(mats, offs):
+        rc = be.dispatch("cast_f32_bf16_frag", [be.upload(a), F, be.params(M, K, lda)], (1,), (256,),
+                         offsets=[0, 2 * off, 0])
+        assert rc == 0
+    return F, offs, ldas
+
+
+@pytest.mark.parametrize("M,K,lda", [(1, 32, 32), (33, 96, 100), (100, 96, 96), (512, 576, 576), (40, 160, 192)])
+def test_cast_frag_layout(be, M, K, lda):
+    """cast_f32_bf16_frag writes each value bf16(RNE) where the fragment
+    order puts it (a host restatement of the indexing, bmhip.frag_layout) and
+    zeros in the padding past M and K."""
+    a = bmhip.synth_normal(bmhip.synth_seed(91, M, K, lda), 1.0, M * lda)
+    F, offs, _ = _frag_arena(be, [(a, M, K, lda)])
+    got = F.read(np.uint16)
+    want = (po.bf16_rne(bmhip.frag_layout(a, M, K, lda)).view(np.uint32) >> 16).astype(np.uint16)
+    assert got.size == want.size == bmhip.frag_elems(M, K)
+    assert np.array_equal(got, want)
+
+
+def test_cast_frag_rejects(be):
+    a = be.upload(np.ones(64 * 64, np.float32))
+    F = be.alloc(2 * bmhip.frag_elems(64, 64))
+    k = "cast_f32_bf16_frag"
+    assert be.dispatch(k, [a, F, be.params(64, 48, 64)], (1,), (256,)) == -1      # K not a multiple of 32
+    assert be.dispatch(k, [a, F, be.params(64, 64, 32)], (1,), (256,)) == -1      # lda < K
+    assert be.dispatch(k, [a, F, be.params(65, 64, 64)], (1,), (256,)) == -1      # source too short
+    assert be.dispatch(k, [a, be.alloc(16), be.params(64, 64, 64)], (1,), (256,)) == -1  # destination too short
+
+
+@pytest.mark.parametrize("qf", ["q8", "q4"])
+def test_gemm_multi_frag_launch(be, qf):
+    """matmul_forward_q8_multi / _q4_multi over fragment-ordered activations
+    (layout 2, 256x96 tiles) on mixed shapes: ragged M and N, odd block counts
+    (a half step), a source row stride wider than K; against the
+    bf16-operand oracle (<= 1e-4) and the exact product (<= 1e-2), and
+    against the row-major bf16 launch of the same problems (the same
+    operands; only the order of each step's 64 products differs)."""
+    shapes = [(512, 576, 576), (512, 576, 192), (100, 96, 70), (513, 64, 65), (64, 1536, 576), (17, 32, 300),
+              (40, 160, 96), (300, 224, 200)]
+    quant = po.quantize_q8 if qf == "q8" else po.quantize_q4
+    ws, as_, lda = [], [], []
+    for i, (M, K, N) in enumerate(shapes):
+        ws.append(quant(bmhip.synth_normal(bmhip.synth_seed(97, 0, i, 0), 0.02, N * K)))
+        ld = K + (32 if i == 2 else 0)
+        as_.append(bmhip.synth_normal(bmhip.synth_seed(97, 0, i, 1), 1.0, M * ld))
+        lda.append(ld)
+    F, f_off, f_lda = _frag_arena(be, [(a, M, K, ld) for a, (M, K, N), ld in zip(as_, shapes, lda)])
+    w_off = np.cumsum([0] + [w.size for w in ws[:-1]])
+    c_off = np.cumsum([0] + [M * N for (M, K, N) in shapes[:-1]])
+    M_, K_, N_ = [s[0] for s in shapes], [s[1] for s in shapes], [s[2] for s in shapes]
+    plan, nt = bmhip.gemm_plan(f_off, w_off, c_off, M_, N_, K_, f_lda, N_, frag=True)
+    assert nt >= sum(bmhip.lib().bm_q8_gemm_tiles_frag(M, N, K) for (M, K, N) in shapes)
+    W = be.upload(np.concatenate(ws))
+    ctot = sum(M * N for (M, K, N) in shapes)
+    Cb = be.alloc(4 * ctot)
+    k = "matmul_forward_q8_multi" if qf == "q8" else "matmul_forward_q4_multi"
+    assert be.dispatch(k, [be.params(len(shapes), nt, 2), be.upload(plan), F, W, Cb], (nt * 256,), (256,)) == 0
+    c = Cb.read(np.float32)
+    # the row-major bf16 launch of the same problems
+    a16 = [po.bf16_rne(a) for a in as_]
+    a_off = np.cumsum([0] + [a.size for a in as_[:-1]])
+    plan_r, nt_r = bmhip.gemm_plan(a_off, w_off, c_off, M_, N_, K_, lda, N_)
+    A16 = be.upload((np.concatenate(a16).view(np.uint32) >> 16).astype(np.uint16))
+    Cr = be.alloc(4 * ctot)
+    assert be.dispatch(k, [be.params(len(shapes), nt_r, 1), be.upload(plan_r), A16, W, Cr], (nt_r * 256,),
+                       (256,)) == 0
+    cr = Cr.read(np.float32)
+    gemm_bf16 = po.q8_gemm_bf16_f64 if qf == "q8" else po.q4_gemm_bf16_f64
+    exact = po.q8_matvec_f64 if qf == "q8" else po.q4_matvec_f64
+    for i, (M, K, N) in enumerate(shapes):
+        a = as_[i].reshape(M, lda[i])[:, :K].copy().ravel()
+        got = c[c_off[i]:c_off[i] + M * N]
+        rb = gemm_bf16(ws[i], a, M, K, N)
+        assert normwise(got, rb) <= 1e-4, (i, normwise(got, rb))
+        assert normwise(got, exact(ws[i], a, M, K, N)) <= 1e-2, i
+        assert normwise(got, cr[c_off[i]:c_off[i] + M * N].astype(np.float64)) <= 1e-5, i
+
+
+def test_gemm_multi_frag_integer_exact(be):
+    """On integer-exact operands every product and partial sum is exact in
+    fp32, so the fragment-order launch equals the fp64 product bit for bit."""
+    rng = np.random.default_rng(12)
+    M, K, N = 300, 224, 200
+    nb = K // 32
+    blk = np.zeros((N * nb, 36), np.uint8)
+    blk[:, :4] = (2.0 ** rng.integers(-2, 2, N * nb)).astype(np.float32).view(np.uint8).reshape(-1, 4)
+    blk[:, 4:] = rng.integers(-20, 21, (N * nb, 32)).astype(np.int8).view(np.uint8)
+    w = blk.ravel()
+    a = rng.integers(-3, 4, M * K).astype(np.float32)
+    F, f_off, f_lda = _frag_arena(be, [(a, M, K, K)])
+    plan, nt = bmhip.gemm_plan(f_off, [0], [0], [M], [N], [K], f_lda, [N], frag=True)
+    Cb = be.alloc(4 * M * N)
+    assert be.dispatch("matmul_forward_q8_multi", [be.params(1, nt, 2), be.upload(plan), F, be.upload(w), Cb],
+                       (nt * 256,), (256,)) == 0
+    assert np.array_equal(Cb.read(np.float32).astype(np.float64), po.q8_gemm_bf16_f64(w, a, M, K, N))
+
+
+def test_gemm_multi_frag_rejects(be):
+    """Layout 2 needs fragment-order plans: a row-major plan (other tile
+    counts), an lda that is not K rounded up to 64, or a fragment block not
+    aligned to 512 values is rejected before launch; an unknown layout too."""
+    M, K, N = 64, 96, 64
+    w = be.upload(po.quantize_q8(bmhip.synth_normal(77, 0.02, N * K)))
+    F = be.alloc(2 * (bmhip.frag_elems(M, K) + 512))
+    Cb = be.alloc(4 * M * N)
+    k = "matmul_forward_q8_multi"
+
+    def run(plan, nt, layout=2):
+        return be.dispatch(k, [be.params(1, nt, layout), be.upload(plan), F, w, Cb], (nt * 256,), (256,))
+
+    plan, nt = bmhip.gemm_plan([0], [0], [0], [M], [N], [K], [128], [N], frag=True)
+    assert run(plan, nt) == 0
+    assert run(plan, nt, 3) == -1
+    p_row, nt_row = bmhip.gemm_plan([0], [0], [0], [M], [N + 64], [K], [128], [N + 64])  # 1 row-major tile, 2 frag
+    assert run(p_row, nt_row) == -1
+    bad_lda, nt2 = bmhip.gemm_plan([0], [0], [0], [M], [N], [K], [192], [N], frag=True)
+    assert run(bad_lda, nt2) == -1
+    bad_off, nt3 = bmhip.gemm_plan([256], [0], [0], [M], [N], [K], [128], [N], frag=True)
+    assert run(bad_off, nt3) == -1
+    past, nt4 = bmhip.gemm_plan([1024], [0], [0], [M], [N], [K], [128], [N], frag=True)  # runs past the arena
+    assert run(past, nt4) == -1
