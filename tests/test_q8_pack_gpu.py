@@ -58,6 +58,35 @@ def test_pack_bf16_random(be):
     assert np.array_equal(gpu_pack(be, hb, bf16=True), po.quantize_q8_bf16(hb))
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("src_off,dst_off", [(0, 0), (4, 4), (8, 36), (16, 8), (0, 20)])
+@pytest.mark.parametrize("nblocks", [1, 63, 64, 65, 1000])
+def test_pack_offsets_and_partial_groups(be, bf16, src_off, dst_off, nblocks):
+    """Source and destination at 4-byte (bf16: 8-byte) offsets that are not 16-byte aligned
+    take the kernel's 4-byte store path, aligned ones its 16-byte path; block counts around
+    the 64 blocks of a workgroup end in a partial group.  Bytes outside the destination
+    span stay untouched."""
+    if bf16 and src_off % 8:
+        pytest.skip("bf16 sources are 8-byte aligned")
+    n = 32 * nblocks
+    rng = np.random.default_rng(nblocks * 131 + src_off * 7 + dst_off)
+    x = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    if bf16:
+        x = (x.view(np.uint32) >> 16).astype(np.uint16)
+    raw = x.view(np.uint8)
+    src = be.upload(np.concatenate([np.zeros(src_off, np.uint8), raw]))
+    span = nblocks * 36
+    fill = np.full(dst_off + span + 64, 0xA5, np.uint8)
+    dst = be.upload(fill)
+    rc = be.dispatch("quantize_q8_bf16" if bf16 else "quantize_q8", [src, dst, be.params(n)], (n // 4,), (256,),
+                     offsets=[src_off, dst_off, 0])
+    assert rc == 0
+    got = dst.read(np.uint8, fill.size)
+    want = po.quantize_q8_bf16(x) if bf16 else po.quantize_q8(x)
+    assert np.array_equal(got[dst_off:dst_off + span], want)
+    assert (got[:dst_off] == 0xA5).all() and (got[dst_off + span:] == 0xA5).all()
+
+
 def test_pack_rejects_bad_lengths(be):
     """n % 32 != 0 or n == 0: rejected before launch (reference quant.c:55 returns 0)."""
     src = be.upload(np.ones(64, np.float32))
