@@ -660,10 +660,16 @@ def gemm_leg(steps: int, warmup: int):
         e2.commit()
         encs.append((e1, e2))
     ms_cast = ms = 0.0
+    per = []
     for e1, e2 in encs:
         ms_cast += e1.wait_timed() / steps
-        ms += e2.wait_timed() / steps
+        per.append(e2.wait_timed())
+        ms += per[-1] / steps
     wall = (time.perf_counter() - t0) * 1e3 / steps
+    nq = max(1, steps // 5)
+    stats = {"median": round(float(np.median(per)) * 1e3, 2), "min": round(min(per) * 1e3, 2),
+             "max": round(max(per) * 1e3, 2), "first_fifth_mean": round(float(np.mean(per[:nq])) * 1e3, 2),
+             "last_fifth_mean": round(float(np.mean(per[-nq:])) * 1e3, 2), "steps": steps}
     ms_step = ms_cast + ms
     flops = 2.0 * M * float((OC * K).sum())
     bytes_ = float(wbytes.sum()) + 4.0 * M * float(K.sum()) + 4.0 * float(c_sizes.sum())
@@ -675,7 +681,8 @@ def gemm_leg(steps: int, warmup: int):
         f"{ceil['lds_2x2']['tflops']} with the GEMM's LDS-fed 2x2 wave tile")
     log(f"[bench] prefill GEMM: {ms * 1e3:.1f} us per 30-layer launch, {tflops:.1f} TFLOP/s "
         f"({tflops / MFMA_BF16_PEAK_TFLOPS:.1%} of bf16 MFMA peak, {tflops / bound:.1%} of min(peak, AI*BW)); "
-        f"step with the bf16 cast {ms_step * 1e3:.1f} us")
+        f"step with the bf16 cast {ms_step * 1e3:.1f} us; per launch median {stats['median']} us, first fifth "
+        f"{stats['first_fifth_mean']} us, last fifth {stats['last_fifth_mean']} us over {steps} steps")
     return {
         "workload": "SmolLM2-135M prefill Q8 GEMM, M=512: 30 layers x (q,k,v,o,gate,up,down) in one launch, "
                     "bf16 MFMA with fp32 accumulate; a step = cast of the two fp32 activation matrices to bf16 in "
@@ -684,7 +691,8 @@ def gemm_leg(steps: int, warmup: int):
                     "and the GEMM (HIP events around each)",
         "check_vs_single_normwise": worst,
         "flops_per_launch": flops, "flops_per_layer": flops / L, "bytes_per_launch": bytes_,
-        "us_per_launch": round(ms * 1e3, 2), "cast_us": round(ms_cast * 1e3, 2), "step_us": round(ms_step * 1e3, 2),
+        "us_per_launch": round(ms * 1e3, 2), "us_per_launch_stats": stats, "cast_us": round(ms_cast * 1e3, 2),
+        "step_us": round(ms_step * 1e3, 2),
         "wall_us_per_step": round(wall * 1e3, 2),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
