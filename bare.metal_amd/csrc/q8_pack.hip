@@ -22,8 +22,8 @@
  * sequence, and fp32 denormals are kept.
  *
  * Mapping: 8 lanes per block, each lane owns 4 consecutive elements (one
- * 16-byte load), so a wave reads 1 KiB of contiguous source and writes 288
- * contiguous bytes of blocks.  The block max is a 3-step xor shuffle inside
+ * 16-byte load), so a wave reads 1 KiB of contiguous source (8 blocks) per
+ * load instruction.  The block max is a 3-step xor shuffle inside
  * the 8-lane group.  A Q8 workgroup packs 2 such 32-block groups, with both
  * source loads of a lane issued before the first reduction, and writes its
  * blocks from LDS as whole 16-byte stores.  HBM-bound: 4 (or 2) + 1.125
