@@ -42,7 +42,10 @@ using namespace bmk;
 constexpr int NT = 256;     /* threads per workgroup (4 waves) */
 typedef float bmv_f32x4 __attribute__((ext_vector_type(4))); /* fp32 MFMA accumulator tile */
 constexpr int ATT_CH = 2048; /* keys per softmax chunk held in LDS */
-constexpr int HEAD_U = 8;   /* rows in flight per lane in the LM head (bandwidth-bound: 113 MB fp32 at 135M) */
+/* rows in flight per lane in the B = 1 LM head (bandwidth-bound: 113 MB fp32 at 135M): 12 for fp32 rows
+ * (256 VGPRs; 0.5% more decode tok/s at 135M than 8, 4 measured 0.8% less), 8 for Q8 and bf16 rows, whose
+ * wider per-lane segments would need more than 256 registers at 12 */
+constexpr int head_u(int wf) { return wf == 0 ? 12 : 8; }
 
 /* Sum of v over the 256 threads; every thread gets the result.  sh: 4 floats of LDS. */
 __device__ __forceinline__ float block_sum(float v, float* sh) {
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
 /* ================================================================== */
 /* LM head: logits[b][r] = sum_j (x[b][j] * inv_b * nw[j]) * W[r][j].
  * fp32 rows: a lane owns 16 consecutive columns (4 dwordx4 loads per row),
- * D/16 lanes cover a row, 256/(D/16) rows per pass, HEAD_U passes in flight.
+ * D/16 lanes cover a row, 256/(D/16) rows per pass, head_u(WF) passes in flight.
  * Q8 rows: a lane owns one 32-column block, as in the Q8 matvec.
  * bf16 rows: a lane owns 32 consecutive columns (4 dwordx4 loads per row),
  * each weight widened to fp32 exactly (bits << 16).
@@ -367,6 +370,7 @@ __device__ __forceinline__ float bf16_hi(unsigned int u) { return __uint_as_floa
 
 template <int WF>
 __global__ __launch_bounds__(NT) void k_head(DecHead a) {
+    constexpr int HEAD_U = head_u(WF);
     __shared__ float red[NT * HEAD_U];
     __shared__ float sh[4];
     __shared__ unsigned long long shk[NT / 64];
@@ -2031,7 +2035,7 @@ extern "C" int bmk_launch_swiglu(const bmk_launch_t* a) {
 
 static int head_tiles(int D, int V, int wf) {
     const int nseg = wf == HW_F32 ? D / 16 : D / 32;
-    const int rows = (NT / nseg) * HEAD_U;
+    const int rows = (NT / nseg) * head_u(wf);
     return (V + rows - 1) / rows;
 }
 
