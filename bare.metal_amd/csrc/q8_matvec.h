@@ -11,6 +11,8 @@
 #define MV_MAX_PROBS 8
 #define MV_U 4        /* rows in flight per lane for small launches */
 #define MV_U_WIDE 8   /* rows in flight per lane when the launch has work for every CU many times over */
+#define MV_U_HUGE 12  /* rows in flight per lane in a matmul_forward_q8_vec_multi launch of at least */
+#define MV_HUGE_MIN_TILES 4096 /* this many MV_U_WIDE tiles (a 360M token: 5888; a 135M token: about 2200) */
 #define MV_U_Q4 16    /* rows in flight per lane of the multi-matrix Q4 launch (20-byte blocks) */
 #define BMV_WAVES 4   /* waves per workgroup of the batched (BT >= 2) multi-matrix launch */
 #define BMV_TILE_ROWS (64 * BMV_WAVES) /* output rows per workgroup of that launch, 64 per wave */

@@ -525,10 +525,13 @@ extern "C" int mv_launch_list(const MvProb* d_probs, const unsigned int* d_tile_
 
 template <int QF>
 static int launch_multi(const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
-                        const unsigned int* d_tile_map, int n_tiles, hipStream_t s) {
+                        const unsigned int* d_tile_map, int n_tiles, hipStream_t s, int U = MV_U_WIDE) {
     if (n_tiles <= 0) return 0;
     if (QF == QF_Q4)
         hipLaunchKernelGGL(k_q4_matvec_multi<MV_U_Q4>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y,
+                           d_desc, d_tile_map);
+    else if (U == MV_U_HUGE)
+        hipLaunchKernelGGL(k_q8_matvec_multi<MV_U_HUGE>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y,
                            d_desc, d_tile_map);
     else
         hipLaunchKernelGGL(k_q8_matvec_multi<MV_U_WIDE>, dim3((unsigned)n_tiles), dim3(MV_THREADS), 0, s, W, X, Y,
@@ -555,7 +558,6 @@ extern "C" int bm_q8_bmv_tiles(int OC, int C);
 template <int QF>
 static int launch_matvec_multi(const bmk_launch_t* a) {
     const int BYTES = QFmt<QF>::BYTES;
-    const int U = QF == QF_Q4 ? MV_U_Q4 : MV_U_WIDE;
     BMK_NEED_BYTES(a, 0, 8, "params");
     const int nprob = bmk_pi(a, 0, 0), n_tiles = bmk_pi(a, 0, 1);
     /* optional third parameter: rows per problem (BT >= 2: the batched kernel, plan from bm_q8_bmv_plan) */
@@ -570,6 +572,18 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
                 "q8 matvec multi: misaligned arena offset");
     const MvDesc* desc = (const MvDesc*)a->val[1];
     const unsigned int* tmap = (const unsigned int*)((const char*)a->val[1] + desc_bytes);
+    /* rows in flight per lane, as bm_q8_mv_plan chose them: MV_U_HUGE when the
+     * problems take at least MV_HUGE_MIN_TILES workgroups at MV_U_WIDE */
+    int U = QF == QF_Q4 ? MV_U_Q4 : MV_U_WIDE;
+    if (QF == QF_Q8 && BT == 1) {
+        long wide = 0;
+        for (int i = 0; i < nprob; i++) {
+            BMK_REQUIRE(desc[i].OC > 0 && desc[i].C > 0 && desc[i].C % 32 == 0,
+                        "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, desc[i].OC, desc[i].C);
+            wide += mv_tiles_for(desc[i].OC, desc[i].C, MV_U_WIDE);
+        }
+        if (wide >= MV_HUGE_MIN_TILES) U = MV_U_HUGE;
+    }
     long next_tile = 0;
     for (int i = 0; i < nprob; i++) {
         const MvDesc& d = desc[i];
@@ -600,7 +614,7 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
     }
     return launch_multi<QF>((const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],
                             (const MvDesc*)a->dev[1], (const unsigned int*)((const char*)a->dev[1] + desc_bytes),
-                            n_tiles, a->stream);
+                            n_tiles, a->stream, U);
 }
 
 extern "C" int bmk_launch_q8_matvec_multi(const bmk_launch_t* a) { return launch_matvec_multi<QF_Q8>(a); }

@@ -65,7 +65,15 @@ static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x
 
 extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                               const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
-    return mv_plan_u(MV_U_WIDE, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
+    /* a launch with work for every CU many times over keeps more rows in flight per lane */
+    long wide = 0;
+    for (int i = 0; i < nprob && OC && C; i++) {
+        const int t = mv_tiles_u(OC[i], C[i], MV_U_WIDE);
+        if (t < 0) return -1;
+        wide += t;
+    }
+    const int U = wide >= MV_HUGE_MIN_TILES ? MV_U_HUGE : MV_U_WIDE;
+    return mv_plan_u(U, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
 }
 
 extern "C" long bm_q8_bmv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,

@@ -54,7 +54,10 @@ extern "C" {
 #endif
 
 /* Workgroups one y = W x problem of OC rows and C columns takes in a
- * matmul_forward_q8_vec_multi launch; -1 if C is not a positive multiple of 32. */
+ * matmul_forward_q8_vec_multi launch; -1 if C is not a positive multiple of 32.
+ * A launch whose problems take 4096 or more such workgroups in total keeps 12
+ * rows in flight per lane instead of 8 and so takes fewer (the n_tiles that
+ * bm_q8_mv_plan returns is the launch's count). */
 int  bm_q8_mv_tiles(int OC, int C);
 
 /* Writes the plan table of a matmul_forward_q8_vec_multi launch over nprob

@@ -141,6 +141,43 @@ def test_matvec_multi_launch(be):
         assert normwise(got, r) <= RTOL, (i, normwise(got, r))
 
 
+def test_matvec_multi_launch_wide(be):
+    """A launch of 4096 or more workgroups at 8 rows per lane (six 49152x960 LM heads: 4608) is
+    planned and run with 12 rows per lane: fewer workgroups, and every output bit-identical to
+    the single-matrix launch of the same problem (each row's block products are added in block
+    order either way), within tolerance of the fp64 oracle on sampled rows."""
+    OC, C, n = 49152, 960, 6
+    nb = C // 32
+    rng = np.random.default_rng(77)
+    blocks = np.empty((n * OC * nb, 36), np.uint8)
+    blocks[:, 4:] = rng.integers(-127, 128, (n * OC * nb, 32), dtype=np.int8).view(np.uint8)
+    blocks[:, :4] = (rng.random(n * OC * nb, dtype=np.float32) * 1e-3 + 1e-4).view(np.uint8).reshape(-1, 4)
+    w = blocks.reshape(-1)
+    xs = [bmhip.synth_normal(bmhip.synth_seed(78, 0, i, 0), 1.0, C) for i in range(n)]
+    per = OC * nb * 36
+    wide = n * bmhip.lib().bm_q8_mv_tiles(OC, C)
+    assert wide >= 4096
+    plan, n_tiles = bmhip.mv_plan([i * per for i in range(n)], [i * C for i in range(n)], [i * OC for i in range(n)],
+                                  [OC] * n, [C] * n)
+    assert n_tiles < wide  # 12 rows in flight per lane instead of 8
+    W, X, Y = be.upload(w), be.upload(np.concatenate(xs)), be.alloc(4 * n * OC)
+    rc = be.dispatch("matmul_forward_q8_vec_multi", [be.params(n, n_tiles), be.upload(plan), W, X, Y],
+                     (n_tiles * 256,), (256,))
+    assert rc == 0
+    y = Y.read(np.float32)
+    rows = np.r_[0:64, OC // 2:OC // 2 + 64, OC - 64:OC]
+    for i in range(n):
+        single = be.alloc(4 * OC)
+        rc = be.dispatch("matmul_forward_q8_vec", [be.upload(xs[i]), W, be.alloc(4 * OC), single, be.params(1, C, OC, 0)],
+                         (OC * 128, 1), (128,), offsets=[0, i * per, 0, 0, 0])
+        assert rc == 0
+        got = y[i * OC:(i + 1) * OC]
+        assert np.array_equal(got.view(np.uint32), single.read(np.float32).view(np.uint32)), i
+        sub = w[i * per:(i + 1) * per].reshape(OC, nb * 36)[rows].reshape(-1)
+        r = po.q8_matvec_f64(sub, xs[i], 1, C, len(rows))
+        assert normwise(got[rows], r) <= RTOL, i
+
+
 def test_matvec_multi_rejects_bad_plans(be):
     OC, C = 64, 576
     w = po.quantize_q8(bmhip.synth_normal(51, 0.02, OC * C))
