@@ -15,7 +15,14 @@
 #define MV_HUGE_MIN_TILES 4096 /* this many MV_U_WIDE tiles (a 360M token: 5888; a 135M token: about 2200) */
 #define MV_U_Q4 16    /* rows in flight per lane of the multi-matrix Q4 launch (20-byte blocks) */
 #define BMV_WAVES 4   /* waves per workgroup of the batched (BT >= 2) multi-matrix launch */
-#define BMV_TILE_ROWS (64 * BMV_WAVES) /* output rows per workgroup of that launch, 64 per wave */
+#ifndef BMV_SUBTILES
+#define BMV_SUBTILES 2 /* sub-tiles of 16 rows per wave in a plan tile of that launch, run one after the other */
+#endif
+#define BMV_TILE_ROWS (16 * BMV_WAVES * BMV_SUBTILES) /* output rows per plan tile of that launch */
+#ifndef BMV_WSTAGES
+#define BMV_WSTAGES 2  /* weight register sets of that launch: loads this many steps ahead */
+#endif
+#define BMV_IDLE_TILE 0xffffffffu /* tile-map entry of a workgroup of that launch with nothing to do */
 
 /* One y = W x (+ bias) problem; W is OC rows of nb 36-byte Q8 blocks. */
 typedef struct {

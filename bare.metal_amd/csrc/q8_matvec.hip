@@ -33,6 +33,7 @@
 #include "q8_common.h"
 
 #include <string.h>
+#include <vector>
 
 namespace {
 
@@ -208,249 +209,399 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
  *
  * A workgroup is BMV_WAVES waves; it runs the BMV_TILE_ROWS-row tile
  * blockIdx.x - tile0 of problem tile_map[blockIdx.x] for batch rows
- * 16*blockIdx.y .. +15 over the whole K range, each wave 64 output rows
- * (4 groups of 16).  Per step of BMV_U K blocks:
- *   - each wave copies its 64 rows' spans of BMV_U blocks (contiguous in
- *     each row) into its own part of LDS with 16-byte loads, so every
- *     weight byte is fetched once;
- *   - the workgroup loads the step's activations once (lane t: batch row
- *     t/16, 8 consecutive columns), splits each exactly into three bf16
- *     terms (split3) and stores them in LDS in the MFMA A-operand order, so
- *     the split is paid once per 256 output rows;
- *   - per K block, lane l (c = l%16, g = l/16) reads its three A slots
- *     (x[b0 + c][32kb + 8g .. +7] as hi, mid, lo) and, per row group, the
- *     B operand q[r0 + c][32kb + 8g .. +7] (the int8 or 4-bit codes, exact
- *     in bf16) and its block scale from LDS, and chains three MFMAs.
+ * 16*blockIdx.y .. +15 over the whole K range, each wave 16 output rows.
+ * Weights never pass through LDS:
+ *   - per step of 8 K blocks, lane (c = l%16, h = l/16) of a wave loads
+ *     whole blocks h and 4 + h of its row c (a dwordx4, a dwordx4 and a
+ *     dword each), so a wave streams 288 contiguous bytes of each of its
+ *     16 rows per step: few rows at a time, long runs in each, which is
+ *     what keeps HBM near its streaming rate (64 rows per wave with
+ *     144-byte runs streamed at 42% of the peak, 16 rows with 288-byte
+ *     runs at 73-76%, loads alone);
+ *   - a 4x4 transpose over the lane quarters (v_permlane32_swap, then
+ *     v_permlane16_swap) leaves lane (c, g) holding codes 8g .. 8g+7 of
+ *     row c for each of a quad's 4 blocks: the MFMA B operand, with no LDS
+ *     store, barrier or bank conflict; the block scales are gathered
+ *     across the quarters the same way;
+ *   - the workgroup loads each step's activations once and splits each
+ *     exactly into three bf16 terms (split3), stored in LDS in the MFMA
+ *     A-operand order (double-buffered, one barrier per step), so the split
+ *     is paid once per 64 output rows.
  * Every product is exact, so each block sum is an fp32 sum of the exact
  * x * q products, as in the fp32 reference (only the order differs).  Each
- * group's block product is scaled by its row's block scale and added in
- * block order, as the reference scales each block's dot product
+ * block product is scaled by its row's block scale and added in block
+ * order, as the reference scales each block's dot product
  * (forward.metal:575-623).  D layout: lane l holds batch rows 4*(l/16)+v of
  * output row l%16.  Problem p reads BT rows of C floats at X + x_off (row
  * stride C) and writes BT rows of OC floats at Y + y_off (row stride OC). */
 typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
 typedef float bmm_f32x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
-constexpr int BMV_GROUPS = 4; /* 16-row groups per wave */
-constexpr int BMV_U = 4;      /* K blocks per step */
+constexpr int BMV_QUADS = 2; /* quads of 4 K blocks per step */
 
 /* x = hi + mid + lo with three bf16 terms: hi keeps the top 8 significant
  * bits of x (truncated, so no term overflows), mid the top 8 of x - hi and
  * lo the at most 8 bits left; both subtractions are exact in fp32, so the
  * split is exact for every finite x whose lowest significant bit lies at or
- * above bf16's smallest normal (|x| >= 2^-102 suffices).  A non-finite x
- * goes whole into hi (a NaN kept a NaN) with mid = lo = 0, so its products
- * are the fp32 ones (Inf * 0 = NaN, Inf * q = Inf). */
-__device__ __forceinline__ void split3(const bmm_f32x8& x, uint4& hi, uint4& mid, uint4& lo) {
-    unsigned int h[8], m[8], l[8];
+ * above bf16's smallest normal (|x| >= 2^-102 suffices).  Each term pair is
+ * packed by one v_perm_b32 (the upper halves of two fp32 words).  Returns
+ * the lanes of the wave with a value that is not finite: those need
+ * split3_exact. */
+__device__ __forceinline__ unsigned int hi16_pair(unsigned int lo_word, unsigned int hi_word) {
+    return __builtin_amdgcn_perm(hi_word, lo_word, 0x07060302u);
+}
+__device__ __forceinline__ unsigned long long split3(const bmm_f32x8& x, uint4& hi, uint4& mid, uint4& lo) {
+    unsigned int u[8], m[8], l[8];
+    unsigned long long nf = 0; /* lanes of the wave holding a non-finite value (one v_cmp_class each) */
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const unsigned int u = __float_as_uint(x[i]);
-        const bool fin = (u & 0x7f800000u) != 0x7f800000u;
-        const unsigned int hb = (fin ? u : (u | ((u & 0x007fffffu) ? 0x00400000u : 0u))) & 0xffff0000u;
-        const float r1 = fin ? x[i] - __uint_as_float(hb) : 0.0f;
-        const unsigned int mb = __float_as_uint(r1) & 0xffff0000u;
-        const float r2 = r1 - __uint_as_float(mb);
-        h[i] = hb;
-        m[i] = mb;
-        l[i] = __float_as_uint(r2) & 0xffff0000u;
+        u[i] = __float_as_uint(x[i]);
+        nf |= __builtin_amdgcn_ballot_w64(!__builtin_isfinite(x[i]));
+        const float r1 = x[i] - __uint_as_float(u[i] & 0xffff0000u);
+        m[i] = __float_as_uint(r1);
+        l[i] = __float_as_uint(r1 - __uint_as_float(m[i] & 0xffff0000u));
     }
-    hi = make_uint4((h[0] >> 16) | h[1], (h[2] >> 16) | h[3], (h[4] >> 16) | h[5], (h[6] >> 16) | h[7]);
-    mid = make_uint4((m[0] >> 16) | m[1], (m[2] >> 16) | m[3], (m[4] >> 16) | m[5], (m[6] >> 16) | m[7]);
-    lo = make_uint4((l[0] >> 16) | l[1], (l[2] >> 16) | l[3], (l[4] >> 16) | l[5], (l[6] >> 16) | l[7]);
+    hi = make_uint4(hi16_pair(u[0], u[1]), hi16_pair(u[2], u[3]), hi16_pair(u[4], u[5]), hi16_pair(u[6], u[7]));
+    mid = make_uint4(hi16_pair(m[0], m[1]), hi16_pair(m[2], m[3]), hi16_pair(m[4], m[5]), hi16_pair(m[6], m[7]));
+    lo = make_uint4(hi16_pair(l[0], l[1]), hi16_pair(l[2], l[3]), hi16_pair(l[4], l[5]), hi16_pair(l[6], l[7]));
+    return nf;
+}
+/* The same split with non-finite values handled: a non-finite x goes
+ * whole into hi (a NaN kept a NaN) with mid = lo = 0, so its products are
+ * the fp32 ones (Inf * 0 = NaN, Inf * q = Inf). */
+__device__ __forceinline__ void split3_exact(const bmm_f32x8& x, uint4& hi, uint4& mid, uint4& lo) {
+    unsigned int u[8], m[8], l[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        u[i] = __float_as_uint(x[i]);
+        const bool fin = __builtin_isfinite(x[i]);
+        const float r1 = fin ? x[i] - __uint_as_float(u[i] & 0xffff0000u) : 0.0f;
+        if (!fin && (u[i] & 0x007fffffu)) u[i] |= 0x00400000u;
+        m[i] = __float_as_uint(r1);
+        l[i] = __float_as_uint(r1 - __uint_as_float(m[i] & 0xffff0000u));
+    }
+    hi = make_uint4(hi16_pair(u[0], u[1]), hi16_pair(u[2], u[3]), hi16_pair(u[4], u[5]), hi16_pair(u[6], u[7]));
+    mid = make_uint4(hi16_pair(m[0], m[1]), hi16_pair(m[2], m[3]), hi16_pair(m[4], m[5]), hi16_pair(m[6], m[7]));
+    lo = make_uint4(hi16_pair(l[0], l[1]), hi16_pair(l[2], l[3]), hi16_pair(l[4], l[5]), hi16_pair(l[6], l[7]));
 }
 
+/* Exchange between lane halves / quarters (gfx950 v_permlane32_swap:
+ * lanes 32..63 of a with lanes 0..31 of b; v_permlane16_swap: lanes 16..31
+ * of a with lanes 0..15 of b, and lanes 48..63 of a with 32..47 of b). */
+__device__ __forceinline__ void swap32(unsigned int& a, unsigned int& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void swap16(unsigned int& a, unsigned int& b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+/* One quad of one 16-row group in registers: lane (c, h) holds the scale
+ * and code dwords of block h of row c; after bmv_transpose, code dwords
+ * CW*u .. CW*u+CW-1 are codes 8g .. 8g+7 of block u for lane (c, g) and
+ * s[u] is block u's scale of row c. */
+template <int QF> struct BmvQuad {
+    static constexpr int CW = QF == QF_Q8 ? 2 : 1; /* dwords per 8 codes */
+    unsigned int s[4];
+    unsigned int d[4 * CW];
+};
+
 template <int QF>
+__device__ __forceinline__ void bmv_load(BmvQuad<QF>& Q, const unsigned char* p) {
+    if (QF == QF_Q8) {
+        uint4 a, b;
+        __builtin_memcpy(&a, __builtin_assume_aligned(p, 4), 16);
+        __builtin_memcpy(&b, __builtin_assume_aligned(p + 16, 4), 16);
+        __builtin_memcpy(&Q.d[7], __builtin_assume_aligned(p + 32, 4), 4);
+        Q.s[0] = a.x;
+        Q.d[0] = a.y; Q.d[1] = a.z; Q.d[2] = a.w;
+        Q.d[3] = b.x; Q.d[4] = b.y; Q.d[5] = b.z; Q.d[6] = b.w;
+    } else {
+        uint4 a;
+        __builtin_memcpy(&Q.s[0], __builtin_assume_aligned(p, 4), 4);
+        __builtin_memcpy(&a, __builtin_assume_aligned(p + 4, 4), 16);
+        Q.d[0] = a.x; Q.d[1] = a.y; Q.d[2] = a.z; Q.d[3] = a.w;
+    }
+}
+
+/* The 4x4 transpose of 8-code pieces (row = lane quarter, column = piece)
+ * and the all-gather of the quarter's scales, both in two swap stages. */
+template <int QF>
+__device__ __forceinline__ void bmv_transpose(BmvQuad<QF>& Q) {
+    constexpr int CW = BmvQuad<QF>::CW;
+#pragma unroll
+    for (int e = 0; e < 2 * CW; e++) swap32(Q.d[e], Q.d[2 * CW + e]);
+#pragma unroll
+    for (int e = 0; e < CW; e++) {
+        swap16(Q.d[e], Q.d[CW + e]);
+        swap16(Q.d[2 * CW + e], Q.d[3 * CW + e]);
+    }
+    unsigned int b = Q.s[0];
+    swap32(Q.s[0], b); /* quarters 0..3: s[0] = s0 s1 s0 s1, b = s2 s3 s2 s3 */
+    Q.s[1] = Q.s[0];
+    Q.s[3] = b;
+    swap16(Q.s[0], Q.s[1]);
+    Q.s[2] = b;
+    swap16(Q.s[2], Q.s[3]);
+}
+
+/* codes 8g .. 8g+7 of block u as the bf16 B operand (exact) */
+template <int QF>
+__device__ __forceinline__ bmm_bf16x8 bmv_codes(const BmvQuad<QF>& Q, int u) {
+    bmm_f32x8 w;
+    if (QF == QF_Q4) {
+        const unsigned int q0 = Q.d[u];
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = q4_code(q0, i);
+    } else {
+        const unsigned int q0 = Q.d[2 * u], q1 = Q.d[2 * u + 1];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w[i] = q8_byte(q0, i);
+            w[4 + i] = q8_byte(q1, i);
+        }
+    }
+    return __builtin_convertvector(w, bmm_bf16x8);
+}
+
+/* A-operand layouts of the batched kernel, per K block:
+ *   NSLOT 1 (at most 8 batch rows): A1 = [hi of rows 0..7; mid of rows
+ *     0..7], A2 = [lo of rows 0..7; zeros]: two MFMAs per block, rows 8..15
+ *     of D carry the mid products of rows 0..7, added at the end;
+ *   NSLOT 2 (up to 16 rows): hi, mid and lo of all 16 rows: three MFMAs.
+ * Slot s of a block's area is 16 bytes: 8 bf16 of one A row. */
+template <int NSLOT> struct BmvA;
+template <> struct BmvA<1> {
+    static constexpr int TERMS = 2, SLOTS = 64 + 33; /* A1: slot r + 16g; A2: slot r + 8g (r < 8), 32 = zeros */
+    static constexpr int CB = 16;                     /* K blocks per activation chunk */
+};
+template <> struct BmvA<2> {
+    static constexpr int TERMS = 3, SLOTS = 3 * 64;   /* term t: slot 64t + r + 16g */
+    static constexpr int CB = 16;
+};
+
+template <int QF, int NSLOT>
 __global__ __launch_bounds__(64 * BMV_WAVES) void k_bmv_multi(const unsigned char* __restrict__ W,
                                                               const float* __restrict__ X, float* __restrict__ Y,
                                                               const MvDesc* __restrict__ desc,
-                                                              const unsigned int* __restrict__ tile_map, int BT) {
+                                                              const unsigned int* __restrict__ tile_map, int n_tiles,
+                                                              int BT) {
+    typedef BmvA<NSLOT> L;
     constexpr int BYTES = QFmt<QF>::BYTES;
-    constexpr int SPAN = BMV_U * BYTES;   /* bytes of one row per step: 144 (Q8_0), 80 (Q4_0) */
-    constexpr int CPR = SPAN / 16;        /* 16-byte chunks per row span */
-    constexpr int LDR = SPAN + 4;         /* LDS row pitch: an odd number of dwords spreads the rows over the banks */
-    constexpr int LANE_OFF = QF == QF_Q4 ? 4 : 8; /* code bytes per lane and block */
-    static_assert(SPAN % 16 == 0, "row span must be whole 16-byte chunks");
-    static_assert(BMV_U * 32 * 16 == 64 * BMV_WAVES * 8, "one 8-column activation slot per lane and step");
-    __shared__ __attribute__((aligned(16))) unsigned char tile[BMV_WAVES][64 * LDR];
-    __shared__ uint4 xs[3][BMV_U][64]; /* A operands: term, block, lane */
+    constexpr int KS = 4 * BMV_QUADS;    /* K blocks per step */
+    constexpr int AR = 8 * NSLOT;        /* batch rows per launch tile */
+    constexpr int CB = L::CB;            /* K blocks per activation chunk */
+    constexpr int SPC = CB / KS;         /* steps per sub-tile and chunk */
+    constexpr int T = BMV_SUBTILES;      /* 16 x BMV_WAVES-row sub-tiles of a plan tile */
+    constexpr int XSL = CB * 4 * AR / (64 * BMV_WAVES); /* 8-column activation slots per lane and chunk */
+    static_assert(XSL * 64 * BMV_WAVES == CB * 4 * AR, "chunk shape");
+    __shared__ uint4 xs[CB][L::SLOTS];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c = lane & 15, g = lane >> 4;
-    const MvDesc d = desc[tile_map[blockIdx.x]];
-    const int row0 = ((int)blockIdx.x - d.tile0) * BMV_TILE_ROWS + 64 * wave;
-    const bool wave_live = row0 < d.OC; /* the same for the whole wave */
-    const int b0 = 16 * (int)blockIdx.y;
-    const int nbt = min(16, BT - b0); /* batch rows of this tile */
+    const int c = lane & 15, h = lane >> 4;
+    const int b0 = AR * (int)blockIdx.y;
+    const int nbt = min(AR, BT - b0); /* batch rows of this launch tile */
+    if (NSLOT == 1 && tid < CB) xs[tid][64 + 32] = make_uint4(0u, 0u, 0u, 0u);
+
+    /* A workgroup runs the plan tile tile_map[blockIdx.x] = (problem << 16)
+     * | tile (or nothing: BMV_IDLE_TILE), chunk after chunk; within a chunk,
+     * sub-tile after sub-tile (wave w: rows 16w .. 16w+15 of each), all on
+     * the chunk's one staging of the activations.  Cur is one chunk; past
+     * the last, it reads its loads at the tile's first bytes and computes
+     * nothing. */
+    const unsigned int m = tile_map[blockIdx.x];
+    if (m == BMV_IDLE_TILE) return;
+    const MvDesc d = desc[m >> 16];
+    struct Cur {
+        int ch;
+        bool live;
+    };
     const int nb = d.C / 32;
-    const size_t row_bytes = (size_t)nb * BYTES;
-    unsigned char* wt = tile[wave];
-    /* this lane's weight chunks: chunk q = lane + 64 t of the wave's 64 x CPR
-     * chunk grid, row q / CPR, byte 16 (q % CPR) of the row's span; rows past
-     * OC are clamped (they feed outputs never stored).  Kept as 32-bit
-     * offsets from the wave's first row and LDS addresses, to spare VGPRs. */
-    const unsigned char* wbase = W + d.w_off + (size_t)(wave_live ? row0 : 0) * row_bytes;
-    unsigned int goff[CPR];
-    int ldsa[CPR];
-    int cbo[CPR]; /* the chunk's byte offset in the span, + 16 */
-#pragma unroll
-    for (int t = 0; t < CPR; t++) {
-        const int q = lane + 64 * t, r = q / CPR, cb = 16 * (q - r * CPR);
-        goff[t] = wave_live ? (unsigned int)((size_t)(min(row0 + r, d.OC - 1) - row0) * row_bytes) + cb : 0u;
-        ldsa[t] = r * LDR + cb;
-        cbo[t] = cb + 16;
-    }
-    /* this lane's activation slot: batch row xb, columns 8 * xk .. +7 of the step */
-    const int xb = tid >> 4, xk = tid & 15, xu = xk >> 2, xg = xk & 3;
-    const bool x_on = xb < nbt;
-    const float* xr = X + d.x_off + (size_t)(b0 + (x_on ? xb : 0)) * (size_t)d.C + 8 * xk;
-    /* batch rows past BT stay zero in every A slot */
-    if (!x_on) {
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        xs[0][xu][xb + 16 * xg] = z;
-        xs[1][xu][xb + 16 * xg] = z;
-        xs[2][xu][xb + 16 * xg] = z;
-    }
-
-    /* Loads of step kb0 into registers: the weight chunks of this wave's
-     * rows (a chunk reaching past the step's bytes is moved back to end
-     * there, and stored at the same place, so the overlap is written twice
-     * with equal bytes: no load leaves the row) and this lane's activations. */
-    /* Registers of one step's loads: the weight chunks of this wave's rows
-     * (a chunk reaching past the step's bytes is moved back to end there, and
-     * stored at the same place, so the overlap is written twice with equal
-     * bytes: no load leaves the row) and this lane's activations.  Two sets
-     * alternate, so two steps' loads are in flight while one is computed. */
-    struct Stage {
-        uint4 ch[CPR];
-        float4 xa, xc;
-        bool x_live;
+    const int nch = (nb + CB - 1) / CB;
+    const int row0 = (int)(m & 0xffffu) * BMV_TILE_ROWS + 16 * wave; /* in sub-tile 0 */
+    auto advance = [&](Cur& k) {
+        k.ch++;
+        k.live = k.ch < nch;
     };
-    Stage st0, st1;
-    const int nsteps = (nb + BMV_U - 1) / BMV_U;
-    /* -(bytes) a chunk moves back in a step whose row span ends `valid`
-     * bytes in: 0 for a full step */
-    auto chunk_shift = [&](int t, int valid) { return min(0, valid - cbo[t]); };
-    /* Issues the loads of step `step` into S: every lane issues the same
-     * loads whatever the step, so no branch separates two steps' loads (a
-     * step past the last reads 16 bytes at the wave's first row instead, and
-     * idle waves read there too); the loaded bytes of such steps are never
-     * used.  Activations: a slot past the row or the batch reads the row's
-     * first columns instead and is not stored. */
-    auto load_step = [&](Stage& S, int step) {
-        const bool real = step < nsteps;
-        const int kb0 = step * BMV_U;
-        S.x_live = real && x_on && kb0 + xu < nb;
-        const float* xp = xr + (S.x_live ? 32 * kb0 : 0);
-        __builtin_memcpy(&S.xa, __builtin_assume_aligned(xp, 16), 16);
-        __builtin_memcpy(&S.xc, __builtin_assume_aligned(xp + 4, 16), 16);
-        const int valid = min(BMV_U, nb - kb0) * BYTES;
-        const bool wl = real && wave_live;
-        const unsigned char* sb = wbase + (wl ? (size_t)kb0 * BYTES : 0);
+
+    /* Weight loads of step s2 of sub-tile j of chunk k, lane (c, h): whole
+     * blocks h and 4 + h of the step's 8 of its row c.  Every lane issues
+     * the same loads whatever the step; a block past the row (or a row or
+     * chunk past the end) reads the tile's first block instead (one line
+     * for the whole wave; its product is skipped), so no branch separates
+     * two steps' loads. */
+    auto load_w = [&](BmvQuad<QF> (&S)[BMV_QUADS], const Cur& k, int j, int s2) {
+        const unsigned char* wp = W + d.w_off;
+        const int row = row0 + 16 * BMV_WAVES * j + c;
+        const unsigned int roff = (unsigned int)row * (unsigned int)(nb * BYTES);
+        const bool on = k.live && row < d.OC;
 #pragma unroll
-        for (int t = 0; t < CPR; t++) {
-            const int o = wl ? (int)goff[t] + chunk_shift(t, valid) : 0;
-            __builtin_memcpy(&S.ch[t], __builtin_assume_aligned(sb + o, 4), 16);
+        for (int u = 0; u < BMV_QUADS; u++) {
+            const int kb = CB * k.ch + KS * s2 + 4 * u + h;
+            bmv_load<QF>(S[u], wp + (on && kb < nb ? roff + (unsigned int)kb * BYTES : 0u));
         }
     };
 
-    bmm_f32x4 acc[BMV_GROUPS];
+    /* Activations of chunk k: slot i = tid + 256 r of the chunk's AR x 4*CB
+     * slots is batch row i % AR (a row past the batch reads row 0: it only
+     * reaches output rows that are never stored), 8-column group i / AR (a
+     * group past the row reads the row's first columns: its blocks are
+     * skipped).  load_x issues them a chunk ahead, into registers of their
+     * own, so that waiting for them never waits for the weight loads issued
+     * after them. */
+    struct XChunk {
+        float4 a[XSL], b[XSL];
+    };
+    auto load_x = [&](XChunk& Xc, const Cur& k) {
 #pragma unroll
-    for (int j = 0; j < BMV_GROUPS; j++) acc[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
-
-    /* One step: stage S (the loads of step `step`) into LDS, issue the loads
-     * of step + 2 into S, then the step's products. */
-    auto run_step = [&](Stage& S, int step) {
-        const int kb0 = step * BMV_U;
-        __syncthreads(); /* the previous step's LDS reads are done */
-        if (wave_live) {
-            const int valid = min(BMV_U, nb - kb0) * BYTES;
-#pragma unroll
-            for (int t = 0; t < CPR; t++) {
-                const int la = ldsa[t] + chunk_shift(t, valid);
-                unsigned int w4[4] = {S.ch[t].x, S.ch[t].y, S.ch[t].z, S.ch[t].w};
-                /* 4-byte stores: a moved-back chunk is 4-byte but not 16-byte aligned */
-#pragma unroll
-                for (int e = 0; e < 4; e++) *(unsigned int*)&wt[la + 4 * e] = w4[e];
-            }
+        for (int r = 0; r < XSL; r++) {
+            const int i = tid + 64 * BMV_WAVES * r, b = i % AR, g8 = i / AR;
+            const int col = 32 * CB * k.ch + 8 * g8;
+            const size_t o = k.live ? (size_t)(b0 + (b < nbt ? b : 0)) * (size_t)d.C + (col < d.C ? col : 0) : 0;
+            const float* p = X + d.x_off + o;
+            __builtin_memcpy(&Xc.a[r], __builtin_assume_aligned(p, 16), 16);
+            __builtin_memcpy(&Xc.b[r], __builtin_assume_aligned(p + 4, 16), 16);
         }
-        if (S.x_live) {
-            const bmm_f32x8 xf = {S.xa.x, S.xa.y, S.xa.z, S.xa.w, S.xc.x, S.xc.y, S.xc.z, S.xc.w};
+    };
+    /* Split into LDS.  The exact split of non-finite values runs, and
+     * rewrites the slots, only when some lane of the wave holds one: a
+     * branch around stores, which the compiler keeps as a branch. */
+    auto put = [&](int u, int b, int g, const uint4& th, const uint4& tm, const uint4& tl) {
+        if (NSLOT == 1) {
+            xs[u][b + 16 * g] = th;
+            xs[u][b + 8 + 16 * g] = tm;
+            xs[u][64 + b + 8 * g] = tl;
+        } else {
+            xs[u][b + 16 * g] = th;
+            xs[u][64 + b + 16 * g] = tm;
+            xs[u][128 + b + 16 * g] = tl;
+        }
+    };
+    auto stage_x = [&](const XChunk& Xc) {
+#pragma unroll
+        for (int r = 0; r < XSL; r++) {
+            const int i = tid + 64 * BMV_WAVES * r, b = i % AR, g8 = i / AR, u = g8 >> 2, g = g8 & 3;
             uint4 th, tm, tl;
-            split3(xf, th, tm, tl);
-            xs[0][xu][xb + 16 * xg] = th;
-            xs[1][xu][xb + 16 * xg] = tm;
-            xs[2][xu][xb + 16 * xg] = tl;
-        }
-        __syncthreads();
-        /* the loads two steps ahead fly while this step's products run */
-        load_step(S, step + 2);
-        if (!wave_live) return;
-#pragma unroll
-        for (int u = 0; u < BMV_U; u++) {
-            /* blocks past the row (last step only; the same for the whole
-             * wave) are skipped, not weighted by 0: 0 * Inf would be NaN */
-            if (kb0 + u >= nb) break;
-            bmm_bf16x8 xh, xm, xl;
-            {
-                const uint4 a0 = xs[0][u][lane], a1 = xs[1][u][lane], a2 = xs[2][u][lane];
-                __builtin_memcpy(&xh, &a0, 16);
-                __builtin_memcpy(&xm, &a1, 16);
-                __builtin_memcpy(&xl, &a2, 16);
+            const bmm_f32x8 xf = {Xc.a[r].x, Xc.a[r].y, Xc.a[r].z, Xc.a[r].w, Xc.b[r].x, Xc.b[r].y, Xc.b[r].z, Xc.b[r].w};
+            const unsigned long long nf = split3(xf, th, tm, tl);
+            put(u, b, g, th, tm, tl);
+            if (nf) {
+                split3_exact(xf, th, tm, tl);
+                put(u, b, g, th, tm, tl);
             }
-            bmm_bf16x8 wv[BMV_GROUPS];
-            float sc[BMV_GROUPS];
-#pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++) {
-                const unsigned char* blk = &wt[(16 * j + c) * LDR + u * BYTES];
-                sc[j] = *(const float*)blk;
-                const unsigned int q0 = *(const unsigned int*)(blk + 4 + LANE_OFF * g);
-                const unsigned int q1 = QF == QF_Q8 ? *(const unsigned int*)(blk + 8 + LANE_OFF * g) : 0u;
-                bmm_f32x8 w;
-                if (QF == QF_Q4) {
-#pragma unroll
-                    for (int i = 0; i < 8; i++) w[i] = q4_code(q0, i);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        w[i] = q8_byte(q0, i);
-                        w[4 + i] = q8_byte(q1, i);
-                    }
-                }
-                wv[j] = __builtin_convertvector(w, bmm_bf16x8);
-            }
-            bmm_f32x4 dd[BMV_GROUPS];
-#pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++)
-                dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, wv[j], bmm_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, wv[j], dd[j], 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++) dd[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, wv[j], dd[j], 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < BMV_GROUPS; j++)
-#pragma unroll
-                for (int v = 0; v < 4; v++) acc[j][v] = fmaf(sc[j], dd[j][v], acc[j][v]);
         }
     };
 
-    load_step(st0, 0);
-    load_step(st1, 1);
-    int step = 0;
-    for (; step + 1 < nsteps; step += 2) {
-        run_step(st0, step);
-        run_step(st1, step + 1);
-    }
-    if (step < nsteps) run_step(st0, step);
-    if (!wave_live) return;
+    bmm_f32x4 acc[T];
 #pragma unroll
-    for (int j = 0; j < BMV_GROUPS; j++) {
-        const int row = row0 + 16 * j + c;
-        if (row < d.OC) {
+    for (int j = 0; j < T; j++) acc[j] = bmm_f32x4{0.f, 0.f, 0.f, 0.f};
+    /* this lane's A slots: NSLOT 1: A1 row c (hi of row c, or mid of row
+     * c - 8), A2 row c (lo of row c, or zeros); NSLOT 2: row c of each term */
+    const int a_slot0 = c + 16 * h;
+    const int a_slot1 = NSLOT == 1 ? (c < 8 ? 64 + c + 8 * h : 64 + 32) : 64 + c + 16 * h;
+    const int a_slot2 = 128 + c + 16 * h;
+
+    /* The products of step s2 of chunk k from registers S and the chunk's
+     * LDS operands into A, block after block (the waves of a SIMD hide each
+     * other's MFMA latency; one block's operands at a time keeps the
+     * registers for loads in flight). */
+    auto compute = [&](BmvQuad<QF> (&S)[BMV_QUADS], const Cur& k, int s2, bmm_f32x4& A) {
+        const int kb0 = CB * k.ch + KS * s2; /* the step's first block */
+        const int nb_ = nb;
+#pragma unroll
+        for (int u = 0; u < BMV_QUADS; u++) bmv_transpose<QF>(S[u]);
+#pragma unroll
+        for (int p = 0; p < KS; p++) {
+            /* blocks past the row (the same for the whole wave) are skipped,
+             * not weighted by 0: 0 * Inf would be NaN */
+            if (kb0 + p >= nb_) break;
+            bmm_bf16x8 xa[L::TERMS];
+#pragma unroll
+            for (int t = 0; t < L::TERMS; t++) {
+                const uint4 a = xs[KS * s2 + p][t == 0 ? a_slot0 : t == 1 ? a_slot1 : a_slot2];
+                __builtin_memcpy(&xa[t], &a, 16);
+            }
+            const bmm_bf16x8 wv = bmv_codes<QF>(S[p >> 2], p & 3);
+            bmm_f32x4 dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[0], wv, bmm_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int t = 1; t < L::TERMS; t++) dd = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[t], wv, dd, 0, 0, 0);
+            const float sc = __uint_as_float(S[p >> 2].s[p & 3]);
+#pragma unroll
+            for (int v = 0; v < 4; v++) A[v] = fmaf(sc, dd[v], A[v]);
+        }
+    };
+
+    /* Every wave issues its weight loads, a wave past the last row too (its
+     * lanes read the tile's first block): a load behind a branch makes the
+     * compiler wait for every earlier load at the join.  Weights stream
+     * BMV_WSTAGES steps ahead in (chunk, sub-tile, step) order, across
+     * sub-tile, chunk and tile boundaries; per chunk, the workgroup
+     * stages the chunk's activations (loaded during the previous chunk)
+     * before a barrier, and a barrier after the chunk's products frees the
+     * LDS for the next.  Scheduling barriers keep every load group where it
+     * stands in program order: the compiler would otherwise sink a stage's
+     * loads below the next step's products, and the next step would then
+     * wait for both sets.  Nothing between two waits may itself wait for a
+     * load (a spilled register reloaded, say): loads complete in order, so
+     * that wait would drain every weight load in flight. */
+    /* NS register sets: the steps of a chunk (T sub-tiles x SPC steps) take
+     * them in turn, the loads of step f going to step f + NS */
+    constexpr int NS = BMV_WSTAGES;
+    constexpr int FPC = T * SPC; /* steps per chunk */
+    static_assert(FPC % NS == 0, "register sets cycle within a chunk");
+    BmvQuad<QF> w[NS][BMV_QUADS];
+    XChunk xn;
+    Cur cur = {0, true}, nxt = cur;
+    advance(nxt);
+    load_x(xn, cur);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int f = 0; f < NS; f++) load_w(w[f], cur, f / SPC, f % SPC);
+    __builtin_amdgcn_sched_barrier(0);
+    while (cur.live) {
+        stage_x(xn);
+        __builtin_amdgcn_sched_barrier(0);
+        load_x(xn, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+#pragma unroll
+        for (int f = 0; f < FPC; f++) {
+            const int j = f / SPC, s2 = f % SPC;
+            /* the same for the whole wave */
+            const bool sub_live = row0 + 16 * BMV_WAVES * j < d.OC;
+            if (sub_live && CB * cur.ch + KS * s2 < nb) compute(w[f % NS], cur, s2, acc[j]);
+            __builtin_amdgcn_sched_barrier(0);
+            /* the step NS ahead: in this chunk, or in the next */
+            const int f2 = f + NS;
+            if (f2 < FPC) load_w(w[f % NS], cur, f2 / SPC, f2 % SPC);
+            else load_w(w[f % NS], nxt, (f2 - FPC) / SPC, (f2 - FPC) % SPC);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        cur = nxt;
+        advance(nxt);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < T; j++) {
+        const int row = row0 + 16 * BMV_WAVES * j + c;
+        bmm_f32x4 yv = acc[j];
+        if (NSLOT == 1) {
+            /* D rows 8..15 (lanes 32..63) carry the mid products of rows 0..7 */
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                unsigned int lo_half = __float_as_uint(yv[v]), hi_half = lo_half;
+                swap32(lo_half, hi_half); /* lanes 0..31 now see lanes 32..63's value in hi_half */
+                yv[v] += __uint_as_float(hi_half);
+            }
+        }
+        if (row < d.OC && (NSLOT == 2 || h < 2)) {
             float* y = Y + d.y_off + row;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int b = b0 + 4 * g + v;
-                if (b < BT) y[(size_t)b * d.OC] = acc[j][v];
+                const int b = b0 + 4 * h + v;
+                if (b < BT) y[(size_t)b * d.OC] = yv[v];
             }
         }
     }
@@ -463,11 +614,15 @@ __global__ __launch_bounds__(64 * BMV_WAVES) void k_bmv_multi(const unsigned cha
 static int launch_bmv_multi(int qf, const unsigned char* W, const float* X, float* Y, const MvDesc* d_desc,
                             const unsigned int* d_tile_map, int n_tiles, int BT, hipStream_t s) {
     if (n_tiles <= 0 || BT < 2 || BT > DEC_MAX_B) return -1;
-    const dim3 grid((unsigned)n_tiles, (unsigned)((BT + 15) / 16));
-    if (qf == QF_Q4)
-        hipLaunchKernelGGL(k_bmv_multi<QF_Q4>, grid, dim3(64 * BMV_WAVES), 0, s, W, X, Y, d_desc, d_tile_map, BT);
-    else
-        hipLaunchKernelGGL(k_bmv_multi<QF_Q8>, grid, dim3(64 * BMV_WAVES), 0, s, W, X, Y, d_desc, d_tile_map, BT);
+    /* at most 8 rows: one launch tile of 8 rows; above: tiles of 16 rows */
+    const dim3 grid((unsigned)n_tiles, (unsigned)(BT <= 8 ? 1 : (BT + 15) / 16)), tb(64 * BMV_WAVES);
+    if (qf == QF_Q4) {
+        if (BT <= 8) hipLaunchKernelGGL((k_bmv_multi<QF_Q4, 1>), grid, tb, 0, s, W, X, Y, d_desc, d_tile_map, n_tiles, BT);
+        else hipLaunchKernelGGL((k_bmv_multi<QF_Q4, 2>), grid, tb, 0, s, W, X, Y, d_desc, d_tile_map, n_tiles, BT);
+    } else {
+        if (BT <= 8) hipLaunchKernelGGL((k_bmv_multi<QF_Q8, 1>), grid, tb, 0, s, W, X, Y, d_desc, d_tile_map, n_tiles, BT);
+        else hipLaunchKernelGGL((k_bmv_multi<QF_Q8, 2>), grid, tb, 0, s, W, X, Y, d_desc, d_tile_map, n_tiles, BT);
+    }
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -584,14 +739,21 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
         }
         if (wide >= MV_HUGE_MIN_TILES) U = MV_U_HUGE;
     }
+    /* BT == 1: every problem owns the run of workgroups tile_map[t] == i for
+     * t in [tile0, tile0 + tiles), the runs in problem order.  BT >= 2: each
+     * tile-map entry names (problem << 16) | tile or is BMV_IDLE_TILE, and
+     * every tile of every problem appears exactly once. */
     long next_tile = 0;
     for (int i = 0; i < nprob; i++) {
         const MvDesc& d = desc[i];
         BMK_REQUIRE(d.OC > 0 && d.C > 0 && d.C % 32 == 0, "q8 matvec multi: problem %d bad shape OC=%d C=%d", i, d.OC, d.C);
         const int want = BT > 1 ? bm_q8_bmv_tiles(d.OC, d.C) : mv_tiles_for(d.OC, d.C, U);
-        BMK_REQUIRE(d.tiles == want && d.tile0 == next_tile, "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld",
-                    i, d.tiles, d.tile0, want, next_tile);
+        BMK_REQUIRE(d.tiles == want && (BT > 1 || d.tile0 == next_tile),
+                    "q8 matvec multi: problem %d tiles %d@%d, expected %d@%ld", i, d.tiles, d.tile0, want, next_tile);
         BMK_REQUIRE((d.w_off & 3) == 0, "q8 matvec multi: problem %d weight offset not 4-byte aligned", i);
+        /* the batched kernel addresses a problem's rows with 32-bit offsets */
+        BMK_REQUIRE(BT == 1 || (unsigned long long)d.OC * (d.C / 32) * BYTES <= 0xffffffffull,
+                    "q8 matvec multi: problem %d spans 4 GiB or more", i);
         /* the batched kernel loads activations 16 bytes at a time */
         BMK_REQUIRE(BT == 1 || (d.x_off & 3) == 0, "q8 matvec multi: problem %d activation offset not 16-byte aligned", i);
         BMK_REQUIRE(d.w_off + (unsigned long long)d.OC * (d.C / 32) * BYTES <= a->bytes[2] &&
@@ -600,10 +762,32 @@ static int launch_matvec_multi(const bmk_launch_t* a) {
                     "q8 matvec multi: problem %d lies outside its arenas", i);
         next_tile += d.tiles;
     }
-    BMK_REQUIRE(next_tile == n_tiles, "q8 matvec multi: tiles sum to %ld, n_tiles=%d", next_tile, n_tiles);
-    for (int i = 0; i < nprob; i++)
-        for (int t = desc[i].tile0; t < desc[i].tile0 + desc[i].tiles; t++)
-            BMK_REQUIRE(tmap[t] == (unsigned)i, "q8 matvec multi: tile_map[%d]=%u, expected %d", t, tmap[t], i);
+    if (BT == 1) {
+        BMK_REQUIRE(next_tile == n_tiles, "q8 matvec multi: tiles sum to %ld, n_tiles=%d", next_tile, n_tiles);
+        for (int i = 0; i < nprob; i++)
+            for (int t = desc[i].tile0; t < desc[i].tile0 + desc[i].tiles; t++)
+                BMK_REQUIRE(tmap[t] == (unsigned)i, "q8 matvec multi: tile_map[%d]=%u, expected %d", t, tmap[t], i);
+    } else {
+        BMK_REQUIRE(nprob <= 0x10000 && next_tile <= n_tiles, "q8 matvec multi: %d problems, %ld tiles in %d workgroups",
+                    nprob, next_tile, n_tiles);
+        std::vector<long> first((size_t)nprob);
+        long acc = 0;
+        for (int i = 0; i < nprob; i++) {
+            first[i] = acc;
+            acc += desc[i].tiles;
+        }
+        std::vector<unsigned char> seen((size_t)acc, 0);
+        long named = 0;
+        for (int b = 0; b < n_tiles; b++) {
+            if (tmap[b] == BMV_IDLE_TILE) continue;
+            const unsigned int pi = tmap[b] >> 16, t = tmap[b] & 0xffffu;
+            BMK_REQUIRE(pi < (unsigned)nprob && t < (unsigned)desc[pi].tiles && !seen[first[pi] + t],
+                        "q8 matvec multi: tile_map[%d]=0x%08x names no tile left to run", b, tmap[b]);
+            seen[first[pi] + t] = 1;
+            named++;
+        }
+        BMK_REQUIRE(named == acc, "q8 matvec multi: the tile map runs %ld of %ld tiles", named, acc);
+    }
     if (BT > 1) {
         BMK_REQUIRE(((uintptr_t)a->dev[3] & 15) == 0, "q8 matvec multi: activation arena not 16-byte aligned");
         BMK_REQUIRE(launch_bmv_multi(QF, (const unsigned char*)a->dev[2], (const float*)a->dev[3], (float*)a->dev[4],

@@ -22,16 +22,14 @@ extern "C" int bm_q8_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_WID
 extern "C" int bm_q4_mv_tiles(int OC, int C) { return mv_tiles_u(OC, C, MV_U_Q4); }
 
 /* Batched (BT >= 2) multi-matrix launch: BMV_TILE_ROWS output rows per workgroup. */
-#define MV_U_BATCHED (-1)
 extern "C" int bm_q8_bmv_tiles(int OC, int C) {
     if (OC <= 0 || C <= 0 || C % 32) return -1;
     return (OC + BMV_TILE_ROWS - 1) / BMV_TILE_ROWS;
 }
 
-static int plan_tiles(int OC, int C, int U) { return U == MV_U_BATCHED ? bm_q8_bmv_tiles(OC, C) : mv_tiles_u(OC, C, U); }
+static int plan_tiles(int OC, int C, int U) { return mv_tiles_u(OC, C, U); }
 
-/* U: rows in flight per lane of the kernel the plan is for (MV_U_BATCHED:
- * the batched kernel) */
+/* U: rows in flight per lane of the kernel the plan is for */
 static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                       const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
     if (nprob < 0 || (nprob > 0 && (!w_off || !x_off || !y_off || !OC || !C))) return -1;
@@ -48,15 +46,17 @@ static long mv_plan_u(int U, int nprob, const uint64_t* w_off, const uint64_t* x
     if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
     MvDesc* d = (MvDesc*)plan;
     unsigned int* map = (unsigned int*)((char*)plan + (size_t)nprob * sizeof(MvDesc));
-    int t0 = 0;
     for (int i = 0; i < nprob; i++) {
         d[i].w_off = w_off[i];
         d[i].x_off = x_off[i];
         d[i].y_off = y_off[i];
         d[i].OC = OC[i];
         d[i].C = C[i];
-        d[i].tile0 = t0;
         d[i].tiles = plan_tiles(OC[i], C[i], U);
+    }
+    int t0 = 0;
+    for (int i = 0; i < nprob; i++) {
+        d[i].tile0 = t0;
         for (int k = 0; k < d[i].tiles; k++) map[t0 + k] = (unsigned int)i;
         t0 += d[i].tiles;
     }
@@ -76,9 +76,82 @@ extern "C" long bm_q8_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* 
     return mv_plan_u(U, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
 }
 
+/* The batched launch (BT >= 2): each workgroup runs one BMV_TILE_ROWS-row
+ * tile of a problem over its whole K range, staging the problem's
+ * activations in LDS.  MI355X dispatches workgroup b to XCD b % 8, and each
+ * XCD has its own L2: a problem whose tiles ran on every XCD would have its
+ * activations fetched into all eight.  So each problem goes whole to one XCD
+ * (greedy, the largest first, onto the least loaded XCD by weight bytes),
+ * except one larger than a 32nd of the launch (an LM head), whose tiles are
+ * cut into eight runs, one per XCD.  Within an XCD's queue the tiles run
+ * longest first (decreasing C, a problem's tiles together), so the launch
+ * ends on its shortest workgroups.  tile_map[8 j + x] = (problem << 16) |
+ * tile is the j-th entry of XCD x's queue; shorter queues are padded with
+ * BMV_IDLE_TILE (the workgroup returns at once). */
+#include <algorithm>
+#include <vector>
+#define BMV_XCDS 8
 extern "C" long bm_q8_bmv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,
                                const int* OC, const int* C, void* plan, size_t plan_bytes, int* n_tiles_out) {
-    return mv_plan_u(MV_U_BATCHED, nprob, w_off, x_off, y_off, OC, C, plan, plan_bytes, n_tiles_out);
+    if (nprob < 0 || nprob > 0xffff || (nprob > 0 && (!w_off || !x_off || !y_off || !OC || !C))) return -1;
+    std::vector<int> tiles((size_t)nprob);
+    double total = 0;
+    for (int i = 0; i < nprob; i++) {
+        tiles[i] = bm_q8_bmv_tiles(OC[i], C[i]);
+        if (tiles[i] < 0 || tiles[i] > 0xffff) return -1;
+        total += (double)tiles[i] * C[i];
+    }
+    std::vector<int> order((size_t)nprob);
+    for (int i = 0; i < nprob; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) {
+        return (double)tiles[a] * C[a] > (double)tiles[b] * C[b];
+    });
+    struct Ent { int p, t; };
+    std::vector<Ent> q[BMV_XCDS];
+    double load[BMV_XCDS] = {0};
+    for (int i : order) {
+        const double cost = (double)tiles[i] * C[i];
+        if (cost * 32 > total && tiles[i] >= BMV_XCDS) {
+            for (int x = 0; x < BMV_XCDS; x++) {
+                const int t0 = (int)((long)tiles[i] * x / BMV_XCDS), t1 = (int)((long)tiles[i] * (x + 1) / BMV_XCDS);
+                for (int t = t0; t < t1; t++) q[x].push_back({i, t});
+                load[x] += (double)(t1 - t0) * C[i];
+            }
+        } else {
+            int best = 0;
+            for (int x = 1; x < BMV_XCDS; x++)
+                if (load[x] < load[best]) best = x;
+            for (int t = 0; t < tiles[i]; t++) q[best].push_back({i, t});
+            load[best] += cost;
+        }
+    }
+    size_t longest = 0;
+    for (int x = 0; x < BMV_XCDS; x++) {
+        std::stable_sort(q[x].begin(), q[x].end(), [&](const Ent& a, const Ent& b) { return C[a.p] > C[b.p]; });
+        longest = std::max(longest, q[x].size());
+    }
+    const size_t slots = BMV_XCDS * longest;
+    if (slots > 0x7fffffff) return -1;
+    const size_t need = (size_t)nprob * sizeof(MvDesc) + slots * 4;
+    if (n_tiles_out) *n_tiles_out = (int)slots;
+    if (!plan) return (long)need;
+    if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
+    MvDesc* d = (MvDesc*)plan;
+    unsigned int* map = (unsigned int*)((char*)plan + (size_t)nprob * sizeof(MvDesc));
+    for (int i = 0; i < nprob; i++) {
+        d[i].w_off = w_off[i];
+        d[i].x_off = x_off[i];
+        d[i].y_off = y_off[i];
+        d[i].OC = OC[i];
+        d[i].C = C[i];
+        d[i].tile0 = 0;
+        d[i].tiles = tiles[i];
+    }
+    for (size_t j = 0; j < longest; j++)
+        for (int x = 0; x < BMV_XCDS; x++)
+            map[BMV_XCDS * j + x] = j < q[x].size() ? ((unsigned int)q[x][j].p << 16) | (unsigned int)q[x][j].t
+                                                    : BMV_IDLE_TILE;
+    return (long)need;
 }
 
 extern "C" long bm_q4_mv_plan(int nprob, const uint64_t* w_off, const uint64_t* x_off, const uint64_t* y_off,

@@ -167,19 +167,49 @@ def test_gemm_split_plan():
 
 
 def test_bmv_plan_layout():
-    """Plans of the batched (BT >= 2) multi-matrix matvec: 256 output rows per
-    workgroup, problems in order, the tile map naming each workgroup's problem."""
+    """Plans of the batched (BT >= 2) multi-matrix matvec: 128 output rows per
+    tile; every problem whole on one XCD (workgroup b runs on XCD b % 8),
+    except one larger than a 32nd of the launch, cut into eight runs; each
+    XCD's queue longest (largest C) first; idle entries pad the queues."""
     import numpy as np
 
-    assert bmhip.lib().bm_q8_bmv_tiles(960, 960) == 4
-    assert bmhip.lib().bm_q8_bmv_tiles(257, 64) == 2 and bmhip.lib().bm_q8_bmv_tiles(256, 64) == 1
-    assert bmhip.lib().bm_q8_bmv_tiles(16, 48) == -1
-    plan, n = bmhip.mv_plan([0, 100], [0, 8 * 960], [0, 8 * 960], [960, 257], [960, 64], bt=8)
-    assert n == 6
-    desc = np.frombuffer(plan[:80].tobytes(), dtype=np.int32).reshape(2, 10)  # MvDesc is 40 bytes
-    assert desc[:, 6:].tolist() == [[960, 960, 0, 4], [257, 64, 4, 2]]  # OC, C, tile0, tiles
-    tmap = np.frombuffer(plan[80:].tobytes(), dtype=np.uint32)
-    assert list(tmap) == [0] * 4 + [1] * 2
+    L = bmhip.lib()
+    assert L.bm_q8_bmv_tiles(960, 960) == 8
+    assert L.bm_q8_bmv_tiles(129, 64) == 2 and L.bm_q8_bmv_tiles(128, 64) == 1
+    assert L.bm_q8_bmv_tiles(16, 48) == -1
+    # five 360M layers' projections and a 49152-row head (the head alone is
+    # larger than a 32nd of the launch)
+    OC = [960, 320, 320, 960, 2560, 2560, 960] * 5 + [49152]
+    C = [960, 960, 960, 960, 960, 960, 2560] * 5 + [960]
+    n = len(OC)
+    plan, nt = bmhip.mv_plan([0] * n, [0] * n, [0] * n, OC, C, bt=8)
+    desc = np.frombuffer(plan[:40 * n].tobytes(), dtype=np.int32).reshape(n, 10)  # MvDesc is 40 bytes
+    tiles = [L.bm_q8_bmv_tiles(o, c) for o, c in zip(OC, C)]
+    assert desc[:, 9].tolist() == tiles and desc[:, 8].tolist() == [0] * n  # tiles, tile0
+    tmap = np.frombuffer(plan[40 * n:].tobytes(), dtype=np.uint32)
+    assert nt == len(tmap) and nt % 8 == 0
+    idle = 0xFFFFFFFF
+    seen = set()
+    xcds = {i: set() for i in range(n)}
+    for b, m in enumerate(tmap):
+        if m == idle:
+            continue
+        p, t = int(m) >> 16, int(m) & 0xFFFF
+        assert t < tiles[p] and (p, t) not in seen
+        seen.add((p, t))
+        xcds[p].add(b % 8)
+    assert len(seen) == sum(tiles)  # every tile exactly once
+    assert all(len(xcds[p]) == 1 for p in range(n - 1))  # the projections: one XCD each
+    assert xcds[n - 1] == set(range(8))  # the head: all eight
+    for x in range(8):  # each queue: C never increases, idle entries only at its end
+        q = [int(m) for m in tmap[x::8]]
+        live = [m for m in q if m != idle]
+        assert q[:len(live)] == live
+        cs = [C[m >> 16] for m in live]
+        assert cs == sorted(cs, reverse=True)
+    # the queues' weight loads balance within the largest single problem
+    load = [sum(C[int(m) >> 16] for m in tmap[x::8] if m != idle) for x in range(8)]
+    assert max(load) - min(load) <= max(t * c for t, c in zip(tiles[:-1], C[:-1]))
 
 
 def test_gemm_frag_plan():
