@@ -22,7 +22,7 @@
  * Host code only: no device calls here (bm_compile uploads).
  */
 #include "bmk.h"
-#include "../../include/baremetal.h"
+#include "baremetal.h"
 
 #include <dirent.h>
 #include <fcntl.h>

@@ -810,8 +810,8 @@ __global__ __launch_bounds__(WT) void k_dec_mv4(DecMv a) {
  * squares rides along with the x loads (each x element is loaded by exactly
  * one lane per batch tile).  D layout: lane l holds rows 4*(l/16)+v (batch
  * rows) of column l%16 (output row). */
-constexpr int BMV_WAVES = 8;              /* waves per workgroup, splitting the K blocks */
-constexpr int BMV_NT = 64 * BMV_WAVES;
+constexpr int DBMV_WAVES = 8;              /* waves per workgroup, splitting the K blocks */
+constexpr int DBMV_NT = 64 * DBMV_WAVES;
 
 template <int NBT, int QF>
 __device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[NBT][64], float (*ssq)[16 * NBT]) {
@@ -843,7 +843,7 @@ __device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[N
         acc[bt] = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
         ss[bt] = 0.f;
     }
-    for (int kb = wave; kb < nb; kb += BMV_WAVES) {
+    for (int kb = wave; kb < nb; kb += DBMV_WAVES) {
         const unsigned char* blk = wrow + (size_t)kb * BYTES;
         float s;
         unsigned int q0, q1 = 0u;
@@ -910,7 +910,7 @@ __device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[N
     for (int bt = 0; bt < NBT; bt++) {
         bmv_f32x4 y = part[0][bt][lane];
 #pragma unroll
-        for (int w = 1; w < BMV_WAVES; w++) y += part[w][bt][lane];
+        for (int w = 1; w < DBMV_WAVES; w++) y += part[w][bt][lane];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int b = b0 + 16 * bt + 4 * g + v;
@@ -919,7 +919,7 @@ __device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[N
                 const int bi = 4 * g + v + 16 * bt;
                 float sq = ssq[0][bi];
 #pragma unroll
-                for (int w = 1; w < BMV_WAVES; w++) sq += ssq[w][bi];
+                for (int w = 1; w < DBMV_WAVES; w++) sq += ssq[w][bi];
                 val *= 1.0f / sqrtf(sq / (float)a.C + a.eps);
             }
             if (glu) {
@@ -935,17 +935,17 @@ __device__ __forceinline__ void dec_bmv_body(const DecMv& a, bmv_f32x4 (*part)[N
 }
 
 template <int NBT>
-__global__ __launch_bounds__(BMV_NT) void k_dec_bmv(DecMv a) {
-    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
-    __shared__ float ssq[BMV_WAVES][16 * NBT];
+__global__ __launch_bounds__(DBMV_NT) void k_dec_bmv(DecMv a) {
+    __shared__ bmv_f32x4 part[DBMV_WAVES][NBT][64];
+    __shared__ float ssq[DBMV_WAVES][16 * NBT];
     dec_bmv_body<NBT, QF_Q8>(a, part, ssq);
 }
 
 /* The same over Q4_0 weights: a lane's 8 codes of a block are one dword. */
 template <int NBT>
-__global__ __launch_bounds__(BMV_NT) void k_dec_bmv4(DecMv a) {
-    __shared__ bmv_f32x4 part[BMV_WAVES][NBT][64];
-    __shared__ float ssq[BMV_WAVES][16 * NBT];
+__global__ __launch_bounds__(DBMV_NT) void k_dec_bmv4(DecMv a) {
+    __shared__ bmv_f32x4 part[DBMV_WAVES][NBT][64];
+    __shared__ float ssq[DBMV_WAVES][16 * NBT];
     dec_bmv_body<NBT, QF_Q4>(a, part, ssq);
 }
 
@@ -2194,8 +2194,8 @@ extern "C" int dec_launch_mv(const DecMv* a_in, hipStream_t s) {
         /* one workgroup per (row tile, 16 batch rows): more workgroups than
          * one per row tile, each weight tile is read from L2 again */
         const dim3 grid(a.tile0[a.nmat], (a.B + 15) / 16);
-        if (a.qf == QF_Q4) hipLaunchKernelGGL(k_dec_bmv4<1>, grid, dim3(BMV_NT), 0, s, a);
-        else hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(BMV_NT), 0, s, a);
+        if (a.qf == QF_Q4) hipLaunchKernelGGL(k_dec_bmv4<1>, grid, dim3(DBMV_NT), 0, s, a);
+        else hipLaunchKernelGGL(k_dec_bmv<1>, grid, dim3(DBMV_NT), 0, s, a);
         BMK_LAUNCH_CHECK();
         return 0;
     }

@@ -24,11 +24,11 @@
 #include "bmk.h"
 #include "decode_state.h"
 #include "q8_gemm.h"
-#include "../../include/bm_q8.h"
-#include "../../include/backend.h"
-#include "../../include/backend_hip_device.h"
-#include "../../include/baremetal.h"
-#include "../../include/bm_synth.h"
+#include "bm_q8.h"
+#include "backend.h"
+#include "backend_hip_device.h"
+#include "baremetal.h"
+#include "bm_synth.h"
 
 #include <math.h>
 #include <stdlib.h>

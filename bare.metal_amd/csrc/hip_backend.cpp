@@ -16,8 +16,8 @@
  *     newFunctionWithName lookup).
  */
 #include "bmk.h"
-#include "../../include/backend.h"
-#include "../../include/backend_hip_device.h"
+#include "backend.h"
+#include "backend_hip_device.h"
 
 #include <stdarg.h>
 #include <stdio.h>

@@ -13,7 +13,7 @@
  * is ever handed to kernels or copies.
  */
 #include "bmk.h"
-#include "../../include/baremetal.h"
+#include "baremetal.h"
 
 #include <mutex>
 

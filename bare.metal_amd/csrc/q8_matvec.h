@@ -14,13 +14,18 @@
 #define MV_U_HUGE 12  /* rows in flight per lane in a matmul_forward_q8_vec_multi launch of at least */
 #define MV_HUGE_MIN_TILES 4096 /* this many MV_U_WIDE tiles (a 360M token: 5888; a 135M token: about 2200) */
 #define MV_U_Q4 16    /* rows in flight per lane of the multi-matrix Q4 launch (20-byte blocks) */
+#ifndef BMV_WAVES
 #define BMV_WAVES 4   /* waves per workgroup of the batched (BT >= 2) multi-matrix launch */
+#endif
 #ifndef BMV_SUBTILES
 #define BMV_SUBTILES 2 /* sub-tiles of 16 rows per wave in a plan tile of that launch, run one after the other */
 #endif
 #define BMV_TILE_ROWS (16 * BMV_WAVES * BMV_SUBTILES) /* output rows per plan tile of that launch */
 #ifndef BMV_WSTAGES
 #define BMV_WSTAGES 2  /* weight register sets of that launch: loads this many steps ahead */
+#endif
+#ifndef BMV_CB
+#define BMV_CB 16      /* K blocks per activation chunk of that launch (staged in LDS once per chunk) */
 #endif
 #define BMV_IDLE_TILE 0xffffffffu /* tile-map entry of a workgroup of that launch with nothing to do */
 

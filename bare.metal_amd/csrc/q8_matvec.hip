@@ -207,26 +207,30 @@ __global__ __launch_bounds__(MV_THREADS) void k_q4_matvec_multi(const unsigned c
  * (several decode sequences' projections in one launch), on bf16 MFMA
  * (v_mfma_f32_16x16x32_bf16, D[16][16] += A[16][32] x B[32][16], fp32 sum).
  *
- * A workgroup is BMV_WAVES waves; it runs the BMV_TILE_ROWS-row tile
- * blockIdx.x - tile0 of problem tile_map[blockIdx.x] for batch rows
- * 16*blockIdx.y .. +15 over the whole K range, each wave 16 output rows.
- * Weights never pass through LDS:
+ * A workgroup is BMV_WAVES waves; it runs the plan tile tile_map[blockIdx.x]
+ * (problem << 16 | tile, from bm_q8_bmv_plan: each XCD's workgroups take
+ * whole problems, longest rows first) for batch rows 16*blockIdx.y .. +15
+ * (8 when BT <= 8) over the whole K range.  A tile is BMV_TILE_ROWS rows:
+ * BMV_SUBTILES sub-tiles of 16 rows per wave.  K runs in chunks of CB
+ * blocks; per chunk the workgroup splits the chunk's activations once into
+ * LDS and every sub-tile's steps use them.  Weights never pass through LDS:
  *   - per step of 8 K blocks, lane (c = l%16, h = l/16) of a wave loads
  *     whole blocks h and 4 + h of its row c (a dwordx4, a dwordx4 and a
  *     dword each), so a wave streams 288 contiguous bytes of each of its
  *     16 rows per step: few rows at a time, long runs in each, which is
  *     what keeps HBM near its streaming rate (64 rows per wave with
  *     144-byte runs streamed at 42% of the peak, 16 rows with 288-byte
- *     runs at 73-76%, loads alone);
+ *     runs at 73-76%, loads alone); loads run BMV_WSTAGES steps ahead in
+ *     registers of their own;
  *   - a 4x4 transpose over the lane quarters (v_permlane32_swap, then
  *     v_permlane16_swap) leaves lane (c, g) holding codes 8g .. 8g+7 of
  *     row c for each of a quad's 4 blocks: the MFMA B operand, with no LDS
  *     store, barrier or bank conflict; the block scales are gathered
  *     across the quarters the same way;
- *   - the workgroup loads each step's activations once and splits each
- *     exactly into three bf16 terms (split3), stored in LDS in the MFMA
- *     A-operand order (double-buffered, one barrier per step), so the split
- *     is paid once per 64 output rows.
+ *   - each activation is split exactly into three bf16 terms (split3) and
+ *     stored in LDS in the MFMA A-operand order, so the split is paid once
+ *     per BMV_TILE_ROWS output rows; a barrier before a chunk's products
+ *     and one after them are the only workgroup barriers.
  * Every product is exact, so each block sum is an fp32 sum of the exact
  * x * q products, as in the fp32 reference (only the order differs).  Each
  * block product is scaled by its row's block scale and added in block
@@ -376,11 +380,11 @@ __device__ __forceinline__ bmm_bf16x8 bmv_codes(const BmvQuad<QF>& Q, int u) {
 template <int NSLOT> struct BmvA;
 template <> struct BmvA<1> {
     static constexpr int TERMS = 2, SLOTS = 64 + 33; /* A1: slot r + 16g; A2: slot r + 8g (r < 8), 32 = zeros */
-    static constexpr int CB = 16;                     /* K blocks per activation chunk */
+    static constexpr int CB = BMV_CB;                 /* K blocks per activation chunk */
 };
 template <> struct BmvA<2> {
     static constexpr int TERMS = 3, SLOTS = 3 * 64;   /* term t: slot 64t + r + 16g */
-    static constexpr int CB = 16;
+    static constexpr int CB = BMV_CB;
 };
 
 template <int QF, int NSLOT>

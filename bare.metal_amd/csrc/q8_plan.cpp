@@ -9,7 +9,7 @@
 #include "q8_matvec.h"
 #include "q8_gemm.h"
 
-#include "../../include/bm_q8.h"
+#include "bm_q8.h"
 
 #include <string.h>
 
