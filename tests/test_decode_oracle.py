@@ -61,6 +61,52 @@ def test_single_key_attention_returns_v():
     np.testing.assert_allclose(dec.step(9, 0), want, rtol=2e-5, atol=1e-6)
 
 
+def _q8_diag(w_flat, n, L):
+    """Per-layer diagonals of n x n Q8-dequantized matrices (one nonzero per
+    row, so each row's block holding it is that entry times 127 codes)."""
+    blocks = po.quantize_q8(w_flat).reshape(-1, 36)
+    s = blocks[:, :4].copy().view(np.float32).ravel().astype(np.float64)
+    q = blocks[:, 4:].view(np.int8).astype(np.float64)
+    m = (q * s[:, None]).reshape(L, n, n)
+    return np.stack([np.diag(m[l]) for l in range(L)])
+
+
+def test_mlp_closed_form_gate_up_down():
+    """H = D, wv = 0 (attention adds 0), w_gate = c I, w_up = w_down = I: each
+    layer adds sd * silu(cg * xn) * (su * xn) with xn = rmsnorm(x) and cg,
+    su, sd the Q8-dequantized diagonal entries (c and 1 as 127-codes of their
+    block scale).  c != 1 makes gate and up different, so a model that swaps
+    them (silu on the up projection) or drops the gate fails it
+    (graph.c:184-206, forward.metal:1179-1190)."""
+    D = TINY["D"]
+    dims = dict(TINY, H=D)
+    L = dims["L"]
+    c = 2.5
+    w = weights(dims, zero=("wv",))
+    eye = np.eye(D, dtype=np.float32).ravel()
+    w["w_gate"] = np.tile(np.float32(c) * eye, L)
+    w["w_up"] = np.tile(eye, L)
+    w["w_down"] = np.tile(eye, L)
+    cg, su, sd = _q8_diag(w["w_gate"], D, L), _q8_diag(w["w_up"], D, L), _q8_diag(w["w_down"], D, L)
+    assert np.allclose(cg, c, rtol=1e-6) and np.allclose(su, 1.0, rtol=1e-6)
+    E = w["token_embedding"].reshape(dims["V"], D).astype(np.float64)
+    dec = oracle_decoder(dims, w, 8)
+    silu = lambda v: v / (1.0 + np.exp(-v))
+    for pos, tok in enumerate([9, 40]):
+        x = xs = E[tok].copy()  # xs: the same model with gate and up swapped
+        for l in range(L):
+            xn = rms(x.astype(np.float32), 1.0)
+            x = x + sd[l] * (silu(cg[l] * xn) * (su[l] * xn))
+            xsn = rms(xs.astype(np.float32), 1.0)
+            xs = xs + sd[l] * (silu(su[l] * xsn) * (cg[l] * xsn))
+        want = E @ rms(x.astype(np.float32), 1.0)
+        swapped = E @ rms(xs.astype(np.float32), 1.0)
+        got = dec.step(tok, pos)
+        np.testing.assert_allclose(got, want, rtol=2e-5, atol=1e-6)
+        # the check tells the two orders apart by far more than its tolerance
+        assert np.abs(swapped - want).max() > 100 * (1e-6 + 2e-5 * np.abs(want).max())
+
+
 def _attn_layer_logits(dims, w, toks):
     dec = oracle_decoder(dims, w, 32)
     return [dec.step(t, p) for p, t in enumerate(toks)]

@@ -203,12 +203,14 @@ def test_cast_frag_rejects(be):
 def test_gemm_multi_frag_launch(be, qf):
     """matmul_forward_q8_multi / _q4_multi over fragment-ordered activations
     (layout 2, 256x96 tiles) on mixed shapes: ragged M and N, odd block counts
-    (a half step), a source row stride wider than K; against the
+    (a half step), a source row stride wider than K, and every projection
+    shape of the 135M prefill at 512 tokens (q/o, k/v, gate/up, down); against the
     bf16-operand oracle (<= 1e-4) and the exact product (<= 1e-2), and
     against the row-major bf16 launch of the same problems (the same
     operands; only the order of each step's 64 products differs)."""
+    # (M, K, N); the first two and the last two are the 135M prefill's projections at 512 tokens
     shapes = [(512, 576, 576), (512, 576, 192), (100, 96, 70), (513, 64, 65), (64, 1536, 576), (17, 32, 300),
-              (40, 160, 96), (300, 224, 200)]
+              (40, 160, 96), (300, 224, 200), (512, 576, 1536), (512, 1536, 576)]
     quant = po.quantize_q8 if qf == "q8" else po.quantize_q4
     ws, as_, lda = [], [], []
     for i, (M, K, N) in enumerate(shapes):
