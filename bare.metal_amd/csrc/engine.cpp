@@ -36,6 +36,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 extern "C" {
@@ -977,9 +978,13 @@ static int pf_session_work(bm_session_t* S, int n, size_t plan_bytes, PfWork* w)
 extern "C" void* bmk_noalloc_scratch(int device);
 
 /* Host staging of bm_forward_noalloc's plans (static: no allocation at call
- * time; shared by all calls, which must not overlap). */
+ * time).  It is one buffer for the process and each GPU's device array is
+ * shared by every call on that GPU, so s_noalloc_mu serializes the calls:
+ * it is held from the workspace carve through the plan upload to the final
+ * synchronization on the logits read. */
 #define PF_NOALLOC_PLAN_BYTES (1u << 20)
 alignas(64) static unsigned char s_noalloc_h_plan[PF_NOALLOC_PLAN_BYTES];
+static std::mutex s_noalloc_mu;
 
 /* bm_forward_noalloc's workspace: carved from the GPU's static array, the
  * plans last; -1 (logged) when n tokens do not fit. */
@@ -1143,6 +1148,7 @@ extern "C" float* bm_forward_noalloc(bm_session_t* S, const int* tokens, int n_t
                 "(position %d, batch %d, max %d)", n_tokens, S->pos, S->B, S->MS);
         return NULL;
     }
+    std::lock_guard<std::mutex> lock(s_noalloc_mu);
     return forward_prefill(S, tokens, n_tokens, true);
 }
 

@@ -3,8 +3,8 @@
  * noalloc.hip — the device workspace of the engine's no-allocation entry
  * point (bm_forward_noalloc, include/baremetal.h): one file-scope array
  * per GPU, part of the library's code object, so a caller that cannot
- * allocate device memory (code under HIP graph capture, serving loops that
- * forbid hipMalloc) still gets the prefill's workspace.  Each GPU the
+ * allocate device memory (serving loops and harnesses that forbid
+ * hipMalloc) still gets the prefill's workspace.  Each GPU the
  * library runs on holds BM_NOALLOC_SCRATCH_BYTES until the process ends.
  *
  * In host code `scratch` names a host-side stand-in, not device memory:
