@@ -105,6 +105,9 @@ def lib() -> C.CDLL:
         "bm_generate_greedy": (i, [vp, vp, i, i, vp]),
         "bm_session_set_graph": (i, [vp, i]),
         "bm_session_set_persistent": (i, [vp, i]),
+        "bm_session_persist_test_fault": (i, [vp, i, vp]),
+        "dec_persist_ok": (i, [i, i, i, i, i, i]),
+        "dec_persist_hw_ok": (i, [C.c_char_p, i]),
         "bm_profile_phases": (C.c_long, [vp, vp]),
     }
     for name, (res, args) in sig.items():
@@ -466,6 +469,17 @@ class Engine:
     def set_persistent(self, on: bool) -> bool:
         """Persistent one-kernel layers (batch 1, Q8, MI355X); False when not available."""
         return lib().bm_session_set_persistent(self.sess, 1 if on else 0) == 0
+
+    def persist_test_fault(self, mode: int):
+        """Tests only (bm_session_persist_test_fault): force the persistent
+        step kernel's failure paths from the host (1: every wait gives up
+        after one tick, 2: a workgroup acts as placed on another XCD than its peers, 0: off).
+        Returns (persistent state, steps rerun on the per-phase kernels)."""
+        n = C.c_ulonglong(0)
+        st = lib().bm_session_persist_test_fault(self.sess, int(mode), C.byref(n))
+        if st < 0:
+            raise BackendError("bm_session_persist_test_fault rejected")
+        return st, n.value
 
     def step(self, token: int) -> np.ndarray:
         p = lib().bm_step(self.sess, int(token))

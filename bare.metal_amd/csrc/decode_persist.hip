@@ -37,7 +37,8 @@
  *     owns (the o and down projections split the rows of x the same way),
  *     so a residual add reads nothing.
  *
- * One XCD: MI355X hands workgroup b to XCD b % 8.  The grid has 8 x
+ * One XCD: MI355X hands workgroups to its 8 XCDs round-robin (b to XCD
+ * (b + start) % 8, the start depending on the dispatch).  The grid has 8 x
  * DEC_PERSIST_WGS workgroups; those with blockIdx.x % 8 == 0 work and the
  * rest return at once, so every working workgroup shares one L2.
  *
@@ -54,10 +55,15 @@
  * Reuse of a buffer is safe without barriers: every phase's output depends,
  * through the chain of phases, on every workgroup's previous use of the
  * buffer (a workgroup writes x in phase 5 only after reading all of h, which
- * every workgroup wrote after reading x in phase 4, and so on).  The spins
- * are bounded in time: on timeout a workgroup sets DecState.sync_error and
- * leaves; the workgroups waiting for its values time out in turn, so the
- * grid always drains.
+ * every workgroup wrote after reading x in phase 4, and so on; the
+ * conditions are listed at dec_persist_ok and checked on the host).  The
+ * spins are bounded in time: on timeout a workgroup sets
+ * DecState.sync_error and leaves, and every other poll gives up once it
+ * sees the flag, so the grid always drains.  A working workgroup that finds
+ * itself on another XCD than a peer (HW_REG_XCC_ID, gathered per step in
+ * the exchange buffer's placement slots) sets the flag before its first
+ * wait.  The host reads the flag after the step and reruns a flagged step
+ * on the per-phase kernels.
  *
  * Arithmetic: fp32 throughout, the reference's formulas (RMSNorm
  * (x * inv) * w with eps from graph.c:134, rotate-half RoPE, scale
@@ -68,6 +74,8 @@
 #include "bmk.h"
 #include "decode_state.h"
 #include "q8_common.h"
+
+#include <string.h>
 
 namespace {
 
@@ -92,6 +100,7 @@ constexpr int APS_MAX = 8192;        /* floats of the staged attention partials 
 constexpr int APR = HD + 2;          /* one partial: max, sum, P.V[HD] */
 constexpr int PS_OFF = 1024;         /* attention: the waves' key probabilities in the staged-vector LDS, past q, k, v */
 constexpr float SPIN_SECONDS = 0.2f;
+constexpr unsigned long long PEEK_TICKS = 1000; /* 10 us at 100 MHz: from then on a wait reads sync_error */
 
 /* threadIdx.x, opaque to the compiler: address arithmetic built on it is
  * redone in every phase instead of being hoisted out of the layer loop and
@@ -181,12 +190,23 @@ __device__ __forceinline__ xv_t get_xv(const xv_t* p) {
 }
 __device__ __forceinline__ float xv_val(xv_t u) { return __uint_as_float((unsigned int)u); }
 
+/* What a wait needs: the step state (its sync_error), the workgroup's LDS
+ * flag `bad` (read by the workgroup after its next barrier) and the longest
+ * wait in 100 MHz ticks. */
+struct Sync {
+    DecState* st;
+    int* bad;
+    unsigned long long limit;
+};
+
 /* Until `ready(k)` holds for every k of every lane of the wave, reloads
  * (reload(k)) the elements not yet ready.  The spin is bounded in time: on
- * timeout it sets DecState.sync_error and *bad (LDS, read by the workgroup
- * after its next barrier) and leaves the values as they are. */
+ * timeout it sets DecState.sync_error (1) and *bad and leaves the values as
+ * they are; past PEEK_TICKS it also gives up once any workgroup has set
+ * sync_error (a timeout elsewhere, or a workgroup on another XCD than its
+ * peers), so the whole grid drains soon after the first error. */
 template <int N, typename Ready, typename Reload>
-__device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, DecState* st, int* bad) {
+__device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, const Sync& sy) {
     auto all_ready = [&] {
         bool ok = true;
 #pragma unroll
@@ -195,15 +215,21 @@ __device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, DecState
     };
     if (all_ready()) return;
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime(); /* 100 MHz */
-    const unsigned long long limit = (unsigned long long)(SPIN_SECONDS * 1e8f);
     for (;;) {
 #pragma unroll
         for (int k = 0; k < N; k++)
             if (!ready(k)) reload(k);
         if (all_ready()) return;
-        if (__builtin_amdgcn_s_memrealtime() - t0 > limit) {
-            __hip_atomic_store(&st->sync_error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *bad = 1;
+        const unsigned long long dt = __builtin_amdgcn_s_memrealtime() - t0;
+        if (dt > sy.limit) {
+            __hip_atomic_store(&sy.st->sync_error, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *sy.bad = 1;
+            return;
+        }
+        /* a wait that ends normally takes a few microseconds: only a longer
+         * one reads the flag, so the common poll is one round trip */
+        if (dt > PEEK_TICKS && __hip_atomic_load(&sy.st->sync_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            *sy.bad = 1;
             return;
         }
     }
@@ -212,12 +238,12 @@ __device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, DecState
 /* Elements tid + k * PT (clamped to C - 1) of an exchanged vector of C
  * values, once they carry epoch ep: one round of loads, then polls. */
 template <int N>
-__device__ __forceinline__ void get_vec(const xv_t* x, int C, unsigned int ep, float (&v)[N], DecState* st, int* bad) {
+__device__ __forceinline__ void get_vec(const xv_t* x, int C, unsigned int ep, float (&v)[N], const Sync& sy) {
     xv_t u[N];
 #pragma unroll
     for (int k = 0; k < N; k++) u[k] = get_xv(x + min(tid() + k * PT, C - 1));
     poll_xv<N>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; },
-               [&](int k) { u[k] = get_xv(x + min(tid() + k * PT, C - 1)); }, st, bad);
+               [&](int k) { u[k] = get_xv(x + min(tid() + k * PT, C - 1)); }, sy);
 #pragma unroll
     for (int k = 0; k < N; k++) v[k] = xv_val(u[k]);
 }
@@ -420,7 +446,7 @@ __device__ __forceinline__ void load_kv(const DecPersist& a, const Piece& p, int
  * epoch ep: q at qkv[0, QD), k at qkv[QD, QD + KV), v after it): two
  * elements per thread, polled until they carry ep. */
 __device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, AttnRegs& r, const xv_t* qkv,
-                                          unsigned int ep, DecState* st, int* bad) {
+                                          unsigned int ep, const Sync& sy) {
     auto addr = [&](int i) {
         i = min(i, p.nraw - 1);
         return i < p.nq ? qkv + (size_t)p.kh * p.nq + i
@@ -428,7 +454,7 @@ __device__ __forceinline__ void attn_load(const DecPersist& a, const Piece& p, A
     };
     xv_t u[2] = {get_xv(addr(tid())), get_xv(addr(tid() + PT))};
     poll_xv<2>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; },
-               [&](int k) { u[k] = get_xv(addr(tid() + k * PT)); }, st, bad);
+               [&](int k) { u[k] = get_xv(addr(tid() + k * PT)); }, sy);
     r.r0 = xv_val(u[0]);
     r.r1 = xv_val(u[1]);
 }
@@ -571,7 +597,7 @@ __device__ __forceinline__ void attn_empty(const Piece& p, xv_t* apart, unsigned
  * the weights e^(m_c - M) computed once per (head, chunk) (ew). */
 template <typename F>
 __device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apart, unsigned int ep, float* aps, float* ew,
-                                           float* xs, DecState* st, int* bad, F&& after_loads) {
+                                           float* xs, const Sync& sy, F&& after_loads) {
     const int total2 = a.NH * DEC_PERSIST_NCH * APR / 2; /* 16-byte loads of two exchanged values */
     /* agent-scope (sc1: miss the L1) loads through a buffer resource over the
      * partials; past its end a buffer load returns 0 (such slots count as
@@ -588,7 +614,7 @@ __device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apar
                     return tid() + k * PT >= total2 ||
                            (__float_as_uint(v[k].y) == ep && __float_as_uint(v[k].w) == ep);
                 },
-                load, st, bad);
+                load, sy);
 #pragma unroll
     for (int k = 0; k < NL; k++) {
         const int i = tid() + k * PT;
@@ -624,9 +650,19 @@ __device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apar
     lds_barrier();
 }
 
+/* HW_REG_XCC_ID bits [3:0] (s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4)): the
+ * XCD the wave runs on */
+constexpr int HWREG_XCC_ID_3_0 = (3 << 11) | (0 << 6) | 20;
+
 __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
-    if (blockIdx.x % 8) return; /* the working workgroups all sit on XCD 0 */
+    if (blockIdx.x % 8) return; /* the working workgroups all sit on one XCD */
     const int w = (int)blockIdx.x / 8;
+    /* tests only: this workgroup acts as if it ran off its peers' XCD (never
+     * workgroup 0, which empties a placement slot below) */
+    if (w == a.fault_wg) {
+        if (threadIdx.x == 0) __hip_atomic_store(&a.st->sync_error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
     __shared__ float red[P_MAX * PT];
     __shared__ __attribute__((aligned(16))) float big[APS_MAX]; /* attention partials, or one K and V sub-chunk */
@@ -641,13 +677,30 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
      * (1..5) of layer l writes with epoch (steps << 8) + 5 l + p, where steps
      * (advanced by the embedding kernel before every step, never reset) is
      * the same for every workgroup of the launch */
-    xv_t* xf = a.ex + 1;
+    xv_t* xf = a.ex + DEC_PERSIST_EX_HEAD;
     xv_t* hf = xf + D;
     xv_t* qkvf = hf + H;
     xv_t* apf = qkvf + QD + 2 * KV;
-    const unsigned int ep0 = __hip_atomic_load((const unsigned int*)a.ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 8;
+    const unsigned int steps = __hip_atomic_load((const unsigned int*)a.ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned int ep0 = steps << 8;
     auto ep = [&](int l, int ph) { return ep0 + (unsigned int)(5 * l + ph); };
+    /* The exchange relies on every working workgroup sharing one XCD's L2
+     * (which one depends on where the dispatch starts).  Each adds its XCD
+     * id to this step's placement slot; one that finds another XCD's bit
+     * there flags the step void (sync_error 2) before its first wait (its
+     * first-phase outputs may already be written: the step is void either
+     * way), the others stop waiting soon after, and the host reruns the
+     * step on the per-phase kernels.  The atomic's result is waited for only
+     * then, after the whole first phase. */
+    const unsigned int xcc_bit = 1u << (__builtin_amdgcn_s_getreg(HWREG_XCC_ID_3_0) & 0xf);
+    unsigned int placed = 0;
+    if (tid() == 0) placed = atomicOr((unsigned int*)a.ex + 2 + (steps & 3u), xcc_bit);
+    /* the slot of the step after next, emptied now (a device-scope atomic,
+     * like the atomicOr's it precedes; this launch ends before that step's
+     * kernel starts) */
+    if (w == 0 && tid() == 0) atomicExch((unsigned int*)a.ex + 2 + ((steps + 2u) & 3u), 0u);
     if (tid() == 0) bad = 0;
+    const Sync sy = {st, &bad, a.spin_ticks ? a.spin_ticks : (unsigned long long)(SPIN_SECONDS * 1e8f)};
 
     /* cos, sin of the step's RoPE angle for rotary pair lane % 32 */
     float rc, rs;
@@ -733,7 +786,7 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
         {
             float v[NW];
             if (l == 0) load_vec(a.x, D, v);
-            else get_vec(xf, D, ep(l - 1, 5), v, st, &bad);
+            else get_vec(xf, D, ep(l - 1, 5), v, sy);
             issue_order();
             mv_fetch(so, bo);
             norm_to_lds(v, D, nw, a.eps, xs, sh);
@@ -744,12 +797,17 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
          * values (positions before pos, written by earlier steps) do not
          * depend on this step's q, k, v: their loads go first. */
         {
+            /* the placement check, before this workgroup's first wait */
+            if (l == 0 && tid() == 0 && (placed & ~xcc_bit)) {
+                __hip_atomic_store(&st->sync_error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                bad = 1;
+            }
             const Piece pc = make_piece(a, l, w, pos);
             const bool live = has_piece && pc.k0 < pc.k1;
             AttnRegs ar;
             if (live) {
                 load_kv(a, pc, pc.k0, ar);
-                attn_load(a, pc, ar, qkvf, ep(l, 1), st, &bad);
+                attn_load(a, pc, ar, qkvf, ep(l, 1), sy);
             }
             issue_order();
             fetch_norm(a.ln2 + (size_t)l * D, nw);
@@ -759,13 +817,13 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             else if (has_piece) attn_empty(pc, apf, ep(l, 2));
         }
         /* 3. merge + o + residual; gate/up weights stream in behind the partials */
-        attn_merge(a, apf, ep(l, 2), big, ew, xs, st, &bad, [&] { mv_fetch(sg, bg); });
+        attn_merge(a, apf, ep(l, 2), big, ew, xs, sy, [&] { mv_fetch(sg, bg); });
         if (bad) return;
         mv_finish(so, bo, xs, red, xf, ep(l, 3), &xres, nullptr);
         /* 4. RMSNorm + gate, up + SwiGLU; down's weights stream in behind x */
         {
             float v[NW];
-            get_vec(xf, D, ep(l, 3), v, st, &bad);
+            get_vec(xf, D, ep(l, 3), v, sy);
             issue_order();
             mv_fetch(sd, bd);
             norm_to_lds(v, D, nw, a.eps, xs, sh);
@@ -778,7 +836,7 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
          * The last layer also writes x plain, for the LM head. */
         {
             float v[XR];
-            get_vec(hf, H, ep(l, 4), v, st, &bad);
+            get_vec(hf, H, ep(l, 4), v, sy);
             issue_order();
             const int ln = min(l + 1, a.L - 1);
             shares(ln, q0, q1, q2, so, sg, sd);
@@ -795,13 +853,27 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
 } // namespace
 
 /* Whether the persistent step can run this shape: head size 64, every
- * phase's share within its register stage, one output row per thread, and
- * the vectors within their LDS stages. */
+ * phase's share within its register stage, one output row per thread, the
+ * vectors within their LDS stages, and the conditions under which reusing
+ * an exchange buffer needs no barrier.  That argument (file comment) is a
+ * chain: a buffer is written again only after its writer has read some
+ * later phase's output in full, which each of its writers produced only
+ * after reading the buffer.  It holds when
+ *   (R1) every working workgroup writes rows in phases 1, 3, 4 and 5 (the
+ *        q/k/v, o, gate/up and down rows are split evenly over
+ *        DEC_PERSIST_WGS, so each needs at least DEC_PERSIST_WGS rows),
+ *   (R2) every (KV head, key chunk) piece has a workgroup, which writes its
+ *        partials every step (empty ones too), and
+ *   (R3) phase 3 reads every piece's partials and phases 1, 4 and 5 read
+ *        the whole of x or h in every workgroup (the kernel's code);
+ * (R1) and (R2) are checked here. */
 extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
     if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT ||
         NH * HD > XS_MAX || NH * DEC_PERSIST_NCH * APR > APS_MAX || MS <= 0)
         return 0;
     const int QD = NH * HD, KV = NKV * HD;
+    if (QD + 2 * KV < DEC_PERSIST_WGS || D < DEC_PERSIST_WGS || H < DEC_PERSIST_WGS) return 0; /* (R1) */
+    if (NKV * DEC_PERSIST_NCH > DEC_PERSIST_WGS) return 0;                                    /* (R2) */
     auto passes = [](int rows_per_wg, int nb) { return nb > PT ? P_MAX + 1 : (rows_per_wg + PT / nb - 1) / (PT / nb); };
     const int w = DEC_PERSIST_WGS;
     const int qkv = (QD + 2 * KV + w - 1) / w, dr = (D + w - 1) / w, hr = (H + w - 1) / w;
@@ -810,13 +882,25 @@ extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
     if (passes(dr, QD / 32) > P_O) return 0;
     if (passes(2 * hr, D / 32) > P_GU) return 0;
     if (passes(dr, H / 32) > P_DN) return 0;
-    if (NKV * DEC_PERSIST_NCH > w) return 0;
     return 1;
+}
+
+/* Whether the device fits the kernel's memory-model assumptions: gfx950
+ * (MI355X: vector L1 write-through, so a plain store lands in the XCD's
+ * L2, and agent-scope loads read that L2), all 256 CUs in one partition,
+ * so that workgroups go to the 8 XCDs round-robin and every working
+ * workgroup (blockIdx.x % 8 == 0) shares one XCD's L2.  The kernel checks
+ * the placement itself at run time (HW_REG_XCC_ID) and flags the step void
+ * if it does not hold. */
+extern "C" int dec_persist_hw_ok(const char* arch, int cu_count) {
+    return arch && strncmp(arch, "gfx950", 6) == 0 && (arch[6] == '\0' || arch[6] == ':') && cu_count == 256;
 }
 
 extern "C" int dec_launch_persist(const DecPersist* a, hipStream_t s) {
     BMK_REQUIRE(a->L >= 1 && a->L <= DEC_PERSIST_MAX_L && a->ex, "persistent step: L=%d outside [1, %d] or no exchange buffer",
                 a->L, DEC_PERSIST_MAX_L);
+    BMK_REQUIRE(a->fault_wg != 0 && a->fault_wg < DEC_PERSIST_WGS, "persistent step: fault workgroup %d outside [1, %d)",
+                a->fault_wg, DEC_PERSIST_WGS);
     hipLaunchKernelGGL(k_dec_persist, dim3(8 * DEC_PERSIST_WGS), dim3(PT), 0, s, *a);
     BMK_LAUNCH_CHECK();
     return 0;

@@ -112,18 +112,25 @@ typedef struct {
  *
  * The exchange buffer carries what the phases pass between workgroups, each
  * float with the epoch of the phase that wrote it (8 bytes: the float's bits
- * in the low word, the epoch in the high word), after a first 8-byte word
- * whose low half counts the steps (advanced by the embedding kernel; the
- * host never writes it):
- *   [1, 1 + D)            x, the residual stream after a phase
+ * in the low word, the epoch in the high word), after three 8-byte words
+ * the host never writes:
+ *   [0]                   low half: the step count s (advanced by the
+ *                         embedding kernel before every step)
+ *   [1, 3)                four 32-bit placement masks: slot s % 4 gathers
+ *                         the XCD ids (one bit each) of step s's working
+ *                         workgroups; the persistent kernel of step s empties
+ *                         slot (s + 2) % 4 ahead of its step, and the host
+ *                         empties all four when the kernel is switched on
+ *   [3, 3 + D)            x, the residual stream after a phase
  *   [.., + H)             h, the SwiGLU output
  *   [.., + NH*HD + 2 KV)  q, k, v
  *   [.., + NH*NCH*(HD+2)) the attention partials (max, sum, P.V[HD]) */
 #define DEC_PERSIST_WGS 32
 #define DEC_PERSIST_NCH 10
 #define DEC_PERSIST_MAX_L 50
+#define DEC_PERSIST_EX_HEAD 3 /* 8-byte words before x */
 #define DEC_PERSIST_EX_WORDS(D, H, QD, KV, NH, HD) \
-    (1 + (size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) + (size_t)(NH) * DEC_PERSIST_NCH * ((HD) + 2))
+    (DEC_PERSIST_EX_HEAD + (size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) + (size_t)(NH) * DEC_PERSIST_NCH * ((HD) + 2))
 typedef struct {
     float* x;                  /* [D] residual stream: the embedding at the first layer, the result after the last */
     unsigned long long* ex;    /* the exchange buffer (above), zeroed when allocated */
@@ -137,6 +144,8 @@ typedef struct {
     float inv_freq[DEC_MAX_HD / 2];
     float scale, eps;
     int D, H, NH, NKV, HD, KV, QD, MS, L;
+    unsigned int spin_ticks;   /* longest wait for an exchanged value, in 100 MHz ticks (0: 0.2 s) */
+    int fault_wg;              /* tests only: this working workgroup acts as if on another XCD than its peers (-1: none) */
 } DecPersist;
 
 /* Input embedding of a decode step: x[b] = emb[token_b]. */

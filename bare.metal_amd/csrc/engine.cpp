@@ -61,6 +61,7 @@ int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C,
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
 int dec_persist_ok(int D, int H, int NH, int NKV, int HD, int MS);
+int dec_persist_hw_ok(const char* arch, int cu_count);
 int dec_launch_persist(const DecPersist* a, hipStream_t s);
 int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q8_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
@@ -134,8 +135,12 @@ struct bm_session_s {
     size_t h_io_cap;
     int pos;             /* host mirror of the position */
     int use_graph;
-    int persist;         /* 1: the layers of a step run as one persistent kernel (B = 1, Q8, MI355X) */
+    int persist;         /* 1: the layers of a step run as one persistent kernel (B = 1, Q8, MI355X);
+                            2: available, per-phase kernels in use; 0: not available */
     unsigned long long* pex; /* the persistent kernel's exchange buffer (decode_state.h) */
+    unsigned int persist_spin_ticks; /* tests only: the kernel's longest wait (0: its default) */
+    int persist_fault_wg;            /* tests only: a working workgroup that acts as misplaced (-1: none) */
+    unsigned long long persist_fallbacks; /* steps rerun on the per-phase kernels after a flagged persistent step */
     hipGraph_t graph;
     hipGraphExec_t gexec;
     int prof_on;
@@ -517,6 +522,8 @@ static int enqueue_step(bm_session_t* S) {
         pa.eps = eps;
         pa.D = D; pa.H = m->H; pa.NH = m->NH; pa.NKV = m->NKV; pa.HD = m->HD; pa.KV = m->KV; pa.QD = m->QD;
         pa.MS = S->MS; pa.L = m->L;
+        pa.spin_ticks = S->persist_spin_ticks;
+        pa.fault_wg = S->persist_fault_wg;
         if (dec_launch_persist(&pa, s) || mark(S, PH_LAYERS)) return -1;
     }
     for (int l = 0; l < (S->persist == 1 ? 0 : m->L); l++) {
@@ -630,6 +637,7 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
     S->ctx = ctx;
     S->m = m;
     m->nsessions++;
+    S->persist_fault_wg = -1;
     S->B = batch;
     S->MS = max_seq_len > 0 ? max_seq_len : m->arch.max_seq_len;
     S->use_graph = 1;
@@ -653,12 +661,12 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
         ok = hipHostMalloc(&S->h_io, S->h_io_cap * 4, hipHostMallocDefault) == hipSuccess;
     }
     /* The persistent step kernel keeps its workgroups on one XCD by launching
-     * 8 per working one (MI355X places workgroup b on XCD b % 8): only on
-     * gfx950 with the whole device's 256 CUs, batch 1, Q8 projections and a
-     * shape it handles. */
-    if (ok && batch == 1 && m->quant_bits == 8 && strncmp(ctx->be->dev_name, "gfx950", 6) == 0 &&
-        ctx->be->dev_cu_count == 256 && m->L <= DEC_PERSIST_MAX_L &&
-        dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
+     * 8 per working one (MI355X places workgroup b on XCD b % 8): only where
+     * the device fits its memory-model assumptions (dec_persist_hw_ok), at
+     * batch 1, with Q8 projections and a shape it handles (dec_persist_ok,
+     * which also checks the conditions its buffer reuse relies on). */
+    if (ok && batch == 1 && m->quant_bits == 8 && dec_persist_hw_ok(ctx->be->dev_name, ctx->be->dev_cu_count) &&
+        m->L <= DEC_PERSIST_MAX_L && dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
         const size_t ex = DEC_PERSIST_EX_WORDS(m->D, m->H, m->QD, m->KV, m->NH, m->HD) * 8;
         ok = hipMalloc(&S->pex, ex) == hipSuccess && hipMemsetAsync(S->pex, 0, ex, ctx->s) == hipSuccess;
         S->persist = ok;
@@ -698,8 +706,33 @@ extern "C" int bm_session_set_persistent(bm_session_t* S, int on) {
         S->gexec = NULL;
         S->graph = NULL;
     }
+    /* switched back on: the kernel empties each step's placement slot two
+     * steps ahead only while it runs, so all four start empty again */
+    if (S->persist == 2 && want == 1)
+        HIP_TRY(hipMemsetAsync(S->pex + 1, 0, 16, S->ctx->s), "placement slots", return -1);
     S->persist = want;
     return 0;
+}
+
+/* Tests only: forces the persistent step kernel's failure paths from the
+ * host, every kernel still exiting normally.  mode 1: every wait for an
+ * exchanged value gives up after one 100 MHz tick (as a timeout would);
+ * mode 2: working workgroup 5 acts as if on another XCD than its peers; mode 0: neither.
+ * Drops a captured step (its arguments change).  Returns the session's
+ * persistent state (0 not available, 1 in use, 2 per-phase kernels in use)
+ * and, in *fallbacks, how many steps were rerun on the per-phase kernels. */
+extern "C" int bm_session_persist_test_fault(bm_session_t* S, int mode, unsigned long long* fallbacks) {
+    if (!S || mode < 0 || mode > 2) return -1;
+    S->persist_spin_ticks = mode == 1 ? 1u : 0u;
+    S->persist_fault_wg = mode == 2 ? 5 : -1;
+    if (S->gexec) {
+        hipGraphExecDestroy(S->gexec);
+        hipGraphDestroy(S->graph);
+        S->gexec = NULL;
+        S->graph = NULL;
+    }
+    if (fallbacks) *fallbacks = S->persist_fallbacks;
+    return S->persist;
 }
 
 static int ensure_graph(bm_session_t* S) {
@@ -765,6 +798,29 @@ static int launch_step(bm_session_t* S) {
     return 0;
 }
 
+/* A persistent step flagged void (DecState.sync_error: a wait timed out, or
+ * a workgroup ran on another XCD than its peers): the session switches to the per-phase
+ * kernels for good, and the device state goes back to what it was before
+ * the step (position, no error), so the step can run again.  What the
+ * flagged step wrote is rewritten by the rerun: the embedding, every
+ * layer's KV slot at the step's position and the head's outputs; the head
+ * re-arms its argmax keys and arrival counter itself. */
+static int persist_fallback(bm_session_t* S, int pos) {
+    BMK_ERR("decode step: the persistent step kernel flagged step %d void (sync_error %d: %s); rerunning it, and "
+            "every later step, on the per-phase kernels",
+            pos, S->h_st->sync_error, S->h_st->sync_error == 2 ? "a workgroup ran on another XCD than its peers" : "a wait timed out");
+    if (bm_session_set_persistent(S, 0) != 0) return -1;
+    S->persist_fallbacks++;
+    S->h_st->sync_error = 0;
+    S->pos = pos;
+    int* w = &S->h_io[S->B + 1]; /* pinned staging past the tokens and the mode word */
+    w[0] = pos;
+    w[1] = 0;
+    HIP_TRY(hipMemcpyAsync(&S->st->pos, &w[0], 4, hipMemcpyHostToDevice, S->ctx->s), "state write", return -1);
+    HIP_TRY(hipMemcpyAsync(&S->st->sync_error, &w[1], 4, hipMemcpyHostToDevice, S->ctx->s), "state write", return -1);
+    return 0;
+}
+
 /* Host-driven step: tokens[b] in, logits [B][V] back to the host. */
 static float* step_host(bm_session_t* S, const int* tokens) {
     bm_model_t* m = S->m;
@@ -784,18 +840,20 @@ static float* step_host(bm_session_t* S, const int* tokens) {
     memcpy(&S->h_io[S->B], &one, 4);
     HIP_TRY(hipMemcpyAsync(&S->st->host_mode, &S->h_io[S->B], 4, hipMemcpyHostToDevice, S->ctx->s), "mode write",
             return NULL);
-    HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
-    if (launch_step(S) != 0) return NULL;
-    HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "event", return NULL);
-    HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)S->B * m->V * 4, hipMemcpyDeviceToHost, S->ctx->s),
-            "logits read", return NULL);
-    if (S->persist == 1)
-        HIP_TRY(hipMemcpyAsync(&S->h_st->sync_error, &S->st->sync_error, 4, hipMemcpyDeviceToHost, S->ctx->s),
-                "state read", return NULL);
-    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
-    if (S->persist == 1 && S->h_st->sync_error) {
-        BMK_ERR("decode step: a barrier of the persistent step kernel timed out (the step's results are void)");
-        return NULL;
+    const int pos = S->pos;
+    for (;;) {
+        const bool persistent = S->persist == 1;
+        HIP_TRY(hipEventRecord(S->ev0, S->ctx->s), "event", return NULL);
+        if (launch_step(S) != 0) return NULL;
+        HIP_TRY(hipEventRecord(S->ev1, S->ctx->s), "event", return NULL);
+        HIP_TRY(hipMemcpyAsync(S->h_logits, S->logits, (size_t)S->B * m->V * 4, hipMemcpyDeviceToHost, S->ctx->s),
+                "logits read", return NULL);
+        if (persistent)
+            HIP_TRY(hipMemcpyAsync(&S->h_st->sync_error, &S->st->sync_error, 4, hipMemcpyDeviceToHost, S->ctx->s),
+                    "state read", return NULL);
+        HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return NULL);
+        if (!persistent || !S->h_st->sync_error) break;
+        if (persist_fallback(S, pos) != 0) return NULL; /* then once more on the per-phase kernels */
     }
     float ms = 0.f;
     if (hipEventElapsedTime(&ms, S->ev0, S->ev1) == hipSuccess) S->busy_ms += ms;
@@ -1184,16 +1242,23 @@ extern "C" int bm_generate_greedy(bm_session_t* S, const int* prompt, int n_prom
     HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
     memcpy(S->h_io, prompt, np * 4);
     HIP_TRY(hipMemcpyAsync(S->prompt, S->h_io, np * 4, hipMemcpyHostToDevice, S->ctx->s), "prompt write", return -1);
-    if (session_reset_state(S, 0, n_prompt) != 0) return -1;
-    for (int i = 0; i < steps; i++)
-        if (launch_step(S) != 0) return -1;
     const int n_out = steps - n_prompt + 1;
     const size_t nt = (size_t)n_out * S->B;
-    HIP_TRY(hipMemcpyAsync(S->h_io, S->out_tokens, nt * 4, hipMemcpyDeviceToHost, S->ctx->s), "tokens read",
-            return -1);
-    HIP_TRY(hipMemcpyAsync(S->h_st, S->st, sizeof(DecState), hipMemcpyDeviceToHost, S->ctx->s), "state read",
-            return -1);
-    HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
+    for (;;) {
+        const bool persistent = S->persist == 1;
+        if (session_reset_state(S, 0, n_prompt) != 0) return -1;
+        for (int i = 0; i < steps; i++)
+            if (launch_step(S) != 0) return -1;
+        HIP_TRY(hipMemcpyAsync(S->h_io, S->out_tokens, nt * 4, hipMemcpyDeviceToHost, S->ctx->s), "tokens read",
+                return -1);
+        HIP_TRY(hipMemcpyAsync(S->h_st, S->st, sizeof(DecState), hipMemcpyDeviceToHost, S->ctx->s), "state read",
+                return -1);
+        HIP_TRY(hipStreamSynchronize(S->ctx->s), "sync", return -1);
+        /* a flagged persistent step voids the run (every later step gives up
+         * at once): the whole run again on the per-phase kernels */
+        if (!persistent || !S->h_st->sync_error) break;
+        if (persist_fallback(S, 0) != 0) return -1;
+    }
     if (S->h_st->n_out != n_out || S->h_st->pos != steps || S->h_st->bad_token || S->h_st->sync_error) {
         BMK_ERR("bm_generate_greedy: device state n_out=%d pos=%d bad_token=%d sync_error=%d, expected n_out=%d pos=%d",
                 S->h_st->n_out, S->h_st->pos, S->h_st->bad_token, S->h_st->sync_error, n_out, steps);

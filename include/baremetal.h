@@ -267,6 +267,17 @@ long           bm_profile_phases(bm_session_t* sess, double* ms);
 #define BM_NOALLOC_SCRATCH_BYTES (64u << 20)
 float*         bm_forward_noalloc(bm_session_t* sess, const int* tokens, int n_tokens);
 
+/* No counterpart in the reference; for tests only.  Forces the persistent
+ * step kernel's failure paths from the host, every kernel still exiting
+ * normally: mode 1, every wait for a value another workgroup exchanges
+ * gives up after one tick (as a timeout would); mode 2, one working
+ * workgroup acts as if placed on another XCD than its peers; mode 0, neither.  A step the
+ * kernel flags void is rerun on the per-phase kernels, which the session
+ * then keeps.  Returns the session's persistent state (0 not available,
+ * 1 in use, 2 per-phase kernels in use), -1 on bad arguments, and in
+ * *fallbacks (if not NULL) the number of steps rerun so far. */
+int            bm_session_persist_test_fault(bm_session_t* sess, int mode, unsigned long long* fallbacks);
+
 #ifdef __cplusplus
 }
 #endif

@@ -584,9 +584,55 @@ def test_persistent_step_matches_phase_kernels_and_oracle():
     b.reset()
     ga, gb = a.generate(prompt, 100), b.generate(prompt, 100)
     assert np.array_equal(ga, gb)
+    # every step ran in the persistent kernel: none was flagged and rerun
+    assert a.persist_test_fault(0) == (1, 0)
     a.close()
     b.close()
     print(f"persistent vs phase kernels {worst:.2e}, vs oracle {worst_o:.2e}")
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["wait-timeout", "off-peer-xcd"])
+def test_persistent_step_fault_falls_back(mode):
+    """The persistent step kernel's failure paths, forced from the host with
+    every kernel exiting normally (bm_session_persist_test_fault): 1, every
+    wait for an exchanged value gives up after one tick; 2, one working
+    workgroup acts as if placed on another XCD than its peers and leaves at once.  The flagged
+    step is reported, the grid drains, and the step reruns on the per-phase
+    kernels: its logits equal a per-phase session's bit for bit (and the
+    oracle's within the per-step bar), as do the later steps, which stay on
+    the per-phase kernels; a device-side greedy run falls back as a whole
+    and gives the per-phase run's tokens."""
+    dims = bmhip.SMOLLM2_135M
+    seed = 2025
+    a = bmhip.Engine(dims, max_seq_len=64, seed=seed)
+    b = bmhip.Engine(dims, max_seq_len=64, seed=seed)
+    c = bmhip.Engine(dims, max_seq_len=64, seed=seed)
+    try:
+        if not (a.set_persistent(True) and c.set_persistent(True)):
+            pytest.skip("the persistent step kernel is not available on this device")
+        assert b.set_persistent(False)
+        assert a.persist_test_fault(mode) == (1, 0)
+        orc = oracle_decoder(dims, bmhip.synthetic_weights(dims, seed), 64, nthreads=16)
+        toks = bmhip.synth_uniform_int(78, 0, dims["V"], 12)
+        for pos, t in enumerate(toks):
+            ya, yb = a.step(int(t)), b.step(int(t))
+            assert np.array_equal(ya, yb), pos
+            r = orc.step(int(t), pos)
+            if pos in (0, len(toks) - 1):
+                assert normwise(ya, r) <= LOGIT_TOL, (pos, normwise(ya, r))
+        # the first step was flagged and rerun; the rest ran on the per-phase kernels
+        assert a.persist_test_fault(0) == (2, 1)
+        assert c.persist_test_fault(mode) == (1, 0)
+        prompt = toks[:6]
+        b.reset()
+        gb = b.generate(prompt, 40)
+        gc = c.generate(prompt, 40)
+        assert np.array_equal(gc, gb)
+        assert c.persist_test_fault(0) == (2, 1)
+    finally:
+        a.close()
+        b.close()
+        c.close()
 
 
 # Small head-64 shapes: little weight traffic per CU, so a CU's L1 keeps the

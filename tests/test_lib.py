@@ -232,3 +232,40 @@ def test_gemm_frag_plan():
     for p, tn in ((0, 6), (1, 3)):
         for nt in range(tn):  # tile = m * tiles_n + n: the pair's M tiles share an XCD
             assert len({b % 8 for b, q, tl in live if q == p and tl % tn == nt}) == 1
+
+
+def test_persistent_step_host_conditions():
+    """dec_persist_ok / dec_persist_hw_ok, the host checks behind the
+    persistent decode step (decode_persist.hip).  Over a sweep of shapes,
+    every accepted one satisfies the buffer-reuse conditions computed here
+    independently: (R1) at least DEC_PERSIST_WGS = 32 rows in each of the
+    q/k/v, o, gate/up and down phases, so every working workgroup writes in
+    each (with D, H multiples of 32 and head size 64 every shape has them);
+    (R2) a workgroup for each of the 10 key chunks of every KV head, which
+    rejects SmolLM2-360M's 5 KV heads (50 pieces).  The hardware check takes
+    gfx950 with all 256 CUs only."""
+    L = bmhip.lib()
+    wgs, nch = 32, 10
+    assert L.dec_persist_ok(576, 1536, 9, 3, 64, 384) == 1     # SmolLM2-135M
+    assert L.dec_persist_ok(960, 2560, 15, 5, 64, 384) == 0    # SmolLM2-360M: (R2)
+    assert L.dec_persist_ok(576, 1536, 9, 3, 32, 384) == 0     # head size 32
+    accepted = 0
+    for D in (32, 64, 256, 576, 1024):
+        for H in (32, 512, 1536, 2048):
+            for NKV in (1, 2, 3, 4):
+                for g in (1, 2, 3, 4):
+                    NH = NKV * g
+                    ok = L.dec_persist_ok(D, H, NH, NKV, 64, 128)
+                    if ok:
+                        accepted += 1
+                        QD, KV = NH * 64, NKV * 64
+                        assert QD + 2 * KV >= wgs and D >= wgs and H >= wgs, (D, H, NH, NKV)
+                        assert NKV * nch <= wgs, (D, H, NH, NKV)
+                    if NKV * nch > wgs:
+                        assert not ok, (D, H, NH, NKV)
+    assert accepted > 0
+    assert L.dec_persist_hw_ok(b"gfx950:sramecc+:xnack-", 256) == 1
+    assert L.dec_persist_hw_ok(b"gfx950", 256) == 1
+    assert L.dec_persist_hw_ok(b"gfx950:sramecc+:xnack-", 128) == 0  # a partition of the device
+    assert L.dec_persist_hw_ok(b"gfx942:sramecc+:xnack-", 304) == 0
+    assert L.dec_persist_hw_ok(b"gfx9500", 256) == 0
