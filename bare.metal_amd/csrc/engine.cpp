@@ -1308,7 +1308,7 @@ struct bm_sampler_s {
     int top_k;
     unsigned int rng;
     float* probs;
-    int* idx;
+    float* sorted; /* scratch: the probabilities in descending order */
 };
 
 extern "C" bm_sampler_t* bm_create_sampler(int vocab_size, float temp, float topp, uint64_t seed) {
@@ -1322,8 +1322,8 @@ extern "C" bm_sampler_t* bm_create_sampler(int vocab_size, float temp, float top
     s->rng = (unsigned int)seed;
     if (seed == 0) s->rng = (unsigned int)(uintptr_t)s; /* non-zero default, as the reference */
     s->probs = (float*)malloc((size_t)vocab_size * sizeof(float));
-    s->idx = (int*)malloc((size_t)vocab_size * sizeof(int));
-    if (!s->probs || !s->idx) {
+    s->sorted = (float*)malloc((size_t)vocab_size * sizeof(float));
+    if (!s->probs || !s->sorted) {
         bm_destroy_sampler(s);
         return NULL;
     }
@@ -1333,7 +1333,7 @@ extern "C" bm_sampler_t* bm_create_sampler(int vocab_size, float temp, float top
 extern "C" void bm_destroy_sampler(bm_sampler_t* s) {
     if (!s) return;
     free(s->probs);
-    free(s->idx);
+    free(s->sorted);
     free(s);
 }
 
@@ -1344,9 +1344,10 @@ static int argmax_first(const float* v, int n) {
     return best;
 }
 
-static const float* g_sort_vals;
+/* qsort order of floats, largest first (no shared state: samplers on
+ * several threads sort at once) */
 static int cmp_desc(const void* a, const void* b) {
-    const float fa = g_sort_vals[*(const int*)a], fb = g_sort_vals[*(const int*)b];
+    const float fa = *(const float*)a, fb = *(const float*)b;
     return fa > fb ? -1 : (fa < fb ? 1 : 0);
 }
 
@@ -1361,9 +1362,11 @@ static unsigned int lcg_hash(unsigned int state) {
 
 /* temperature -> softmax -> top-k mask -> top-p mask -> inverse-CDF draw
  * with the hash value r; `fallback` when the cumulative sum never reaches
- * the target (a NaN logit).  Ties in the sort do not change the result:
- * the threshold and the cut depend on the sorted values only. */
-static int sample_probs(float* p, int* idx, int n, float temperature, int top_k, float top_p, unsigned int r,
+ * the target (a NaN logit).  The threshold and the cut depend on the
+ * sorted values only, so a sorted copy of the values (in `sorted`, n
+ * floats of the caller's) stands for the reference's sorted (value, index)
+ * pairs, ties included. */
+static int sample_probs(float* p, float* sorted, int n, float temperature, int top_k, float top_p, unsigned int r,
                         int fallback, const float* logits) {
     if (temperature <= 0.0f) return argmax_first(logits, n);
     for (int i = 0; i < n; i++) p[i] = logits[i] / temperature;
@@ -1377,10 +1380,9 @@ static int sample_probs(float* p, int* idx, int n, float temperature, int top_k,
     }
     for (int i = 0; i < n; i++) p[i] /= sum;
     if (top_k > 0 && top_k < n) {
-        for (int i = 0; i < n; i++) idx[i] = i;
-        g_sort_vals = p;
-        qsort(idx, n, sizeof(int), cmp_desc);
-        const float thresh = p[idx[top_k - 1]];
+        memcpy(sorted, p, (size_t)n * sizeof(float));
+        qsort(sorted, n, sizeof(float), cmp_desc);
+        const float thresh = sorted[top_k - 1];
         for (int i = 0; i < n; i++)
             if (p[i] < thresh) p[i] = 0.0f;
         float s = 0.0f;
@@ -1389,14 +1391,13 @@ static int sample_probs(float* p, int* idx, int n, float temperature, int top_k,
             for (int i = 0; i < n; i++) p[i] /= s;
     }
     if (top_p > 0.0f && top_p < 1.0f) {
-        for (int i = 0; i < n; i++) idx[i] = i;
-        g_sort_vals = p;
-        qsort(idx, n, sizeof(int), cmp_desc);
+        memcpy(sorted, p, (size_t)n * sizeof(float));
+        qsort(sorted, n, sizeof(float), cmp_desc);
         float cum = 0.0f, cut = 0.0f;
         for (int i = 0; i < n; i++) {
-            cum += p[idx[i]];
+            cum += sorted[i];
             if (cum >= top_p) {
-                cut = p[idx[i]];
+                cut = sorted[i];
                 break;
             }
         }
@@ -1423,7 +1424,7 @@ extern "C" int bm_sample(bm_sampler_t* s, const float* logits) {
     if (s->temperature <= 0.0f) return argmax_first(logits, s->vocab_size);
     const unsigned int r = lcg_hash(s->rng);
     s->rng = r;
-    return sample_probs(s->probs, s->idx, s->vocab_size, s->temperature, s->top_k, s->topp, r, s->vocab_size - 1,
+    return sample_probs(s->probs, s->sorted, s->vocab_size, s->temperature, s->top_k, s->topp, r, s->vocab_size - 1,
                         logits);
 }
 
@@ -1450,9 +1451,9 @@ extern "C" int bm_run_tokens(bm_context_t* ctx, bm_model_t* m, const int* prompt
         if (seed == 0) seed = (uint64_t)time(NULL); /* as the reference driver, run.c:135 */
         unsigned int rng_state = (unsigned int)seed;
         float* p = (float*)malloc((size_t)m->V * sizeof(float));
-        int* idx = (int*)malloc((size_t)m->V * sizeof(int));
+        float* sorted = (float*)malloc((size_t)m->V * sizeof(float));
         int next = -1;
-        for (int pos = 0; pos < steps && p && idx; pos++) {
+        for (int pos = 0; pos < steps && p && sorted; pos++) {
             const int tok = pos < n_prompt ? prompt_ids[pos] : next;
             float* logits = bm_step(S, tok);
             if (!logits) {
@@ -1460,13 +1461,13 @@ extern "C" int bm_run_tokens(bm_context_t* ctx, bm_model_t* m, const int* prompt
                 break;
             }
             if (pos >= n_prompt - 1) {
-                next = sample_probs(p, idx, m->V, temperature, top_k, top_p, lcg_hash(rng_state++), 0, logits);
+                next = sample_probs(p, sorted, m->V, temperature, top_k, top_p, lcg_hash(rng_state++), 0, logits);
                 if (callback && callback(next, user_data)) break;
             }
         }
-        if (!p || !idx) rc = -1;
+        if (!p || !sorted) rc = -1;
         free(p);
-        free(idx);
+        free(sorted);
     }
     bm_destroy_session(S);
     return rc;

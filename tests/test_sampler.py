@@ -72,3 +72,28 @@ def test_sampler_seed_zero_is_not_fixed():
     lg = np.linspace(0, 1, 100).astype(np.float32)
     z = our_draws(lg, 1.0, 0.0, 0, 8)
     assert z.size == 8 and ((z >= 0) & (z < 100)).all()
+
+
+def test_samplers_on_two_threads():
+    """Samplers on two threads at once (ctypes releases the GIL around each
+    bm_sample, so the top-k and top-p sorts overlap): every draw equals the
+    same sampler's draws on one thread.  The two cases differ in
+    vocabulary size and cut, so sorts that shared state would mix them."""
+    import threading
+    rng = np.random.default_rng(77)
+    cases = [((rng.standard_normal(49152) * 3).astype(np.float32), 1.0, 0.9, 11, 400),
+             ((rng.standard_normal(1000) * 2).astype(np.float32), 0.7, 0.5, 12, 4000)]
+    want = [our_draws(lg, t, p, s, n) for lg, t, p, s, n in cases]
+    got = [None, None]
+
+    def run(i):
+        lg, t, p, s, n = cases[i]
+        got[i] = our_draws(lg, t, p, s, n)
+
+    ths = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    for i in range(2):
+        assert np.array_equal(got[i], want[i]), i
