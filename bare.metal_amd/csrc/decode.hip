@@ -2085,6 +2085,30 @@ static int launch_rmsnorm_matmul(const bmk_launch_t* a, int wf) {
 extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_F32); }
 extern "C" int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_BF16); }
 
+/* The plain matmul for any C the LM-head kernel does not tile: one
+ * workgroup per output row r, the BT input rows in turn, each dot product
+ * strided over C by the 256 threads with fp32 sums (as the reference's
+ * naive kernel, forward.metal:23-37, one thread per output). */
+template <int WF>
+__global__ __launch_bounds__(NT) void k_matmul_rows_any(const float* __restrict__ x, const void* __restrict__ w,
+                                                        const float* __restrict__ bias, float* __restrict__ out,
+                                                        int BT, int C, int OC) {
+    __shared__ float sh[NT / 64];
+    const int r = blockIdx.x;
+    const float* wf = (const float*)w + (size_t)r * C;
+    const unsigned short* wh = (const unsigned short*)w + (size_t)r * C;
+    for (int b = 0; b < BT; b++) {
+        const float* xb = x + (size_t)b * C;
+        float s = 0.f;
+        for (int k = threadIdx.x; k < C; k += NT) {
+            const float wv = WF == HW_F32 ? wf[k] : __uint_as_float((unsigned int)wh[k] << 16);
+            s = fmaf(xb[k], wv, s);
+        }
+        s = block_sum(s, sh);
+        if (threadIdx.x == 0) out[(size_t)b * OC + r] = bias ? bias[r] + s : s;
+    }
+}
+
 /* The plain fp32 and bf16 matmul kernels: {inp [BT][C], weight [OC][C] (fp32
  * or bf16), bias [OC], out [BT][OC], params int{BT, C, OC, has_bias}}
  * (reference forward.metal:23-37 matmul_forward_naive, 513-560
@@ -2092,22 +2116,34 @@ extern "C" int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a) { return la
  * matmul_forward_bf16_vec, 91-110 matmul_forward_bf16).  The reference's
  * prefill takes them for the LM head of its last position (graph.c:373-380,
  * selected by scheduler.c:1118-1145 and registry.c:60-67).  Served by the
- * LM-head kernel with the RMSNorm off: each workgroup loads its weight rows
- * once and applies them to all BT input rows.  The grid the caller passes is
- * not used.  C must be a multiple of 16 up to 4096 (fp32) or of 32 up to 8192
- * (bf16); other shapes are rejected. */
+ * LM-head kernel with the RMSNorm off where it tiles C (a multiple of 16 up
+ * to 4096 for fp32 rows, of 32 up to 8192 for bf16): each workgroup loads
+ * its weight rows once and applies them to all BT input rows.  Any other C
+ * takes k_matmul_rows_any.  The grid the caller passes is not used. */
 static int launch_matmul_rows(const bmk_launch_t* a, int wf) {
     const char* name = wf == HW_F32 ? "matmul_forward (fp32)" : "matmul_forward_bf16";
     const size_t esz = wf == HW_F32 ? 4 : 2;
     BMK_NEED_BYTES(a, 4, 16, "params");
     const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), hb = bmk_pi(a, 4, 3);
-    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0 && head_shape_ok(C, wf), "%s: BT=%d OC=%d, C=%d must be a multiple of %d up to %d",
-                name, BT, OC, C, wf == HW_F32 ? 16 : 32, wf == HW_F32 ? 4096 : 8192);
+    BMK_REQUIRE(BT >= 0 && OC >= 0 && C > 0, "%s: BT=%d C=%d OC=%d", name, BT, C, OC);
     if (BT == 0 || OC == 0) return 0;
     BMK_NEED_BYTES(a, 0, (size_t)BT * C * 4, "inp");
     BMK_NEED_BYTES(a, 1, (size_t)OC * C * esz, "weight");
     if (hb) BMK_NEED_BYTES(a, 2, (size_t)OC * 4, "bias");
     BMK_NEED_BYTES(a, 3, (size_t)BT * OC * 4, "out");
+    if (!head_shape_ok(C, wf)) {
+        BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & (esz - 1)) == 0,
+                    "%s: misaligned operand", name);
+        const float* bias = hb ? (const float*)a->dev[2] : nullptr;
+        if (wf == HW_F32)
+            hipLaunchKernelGGL(k_matmul_rows_any<HW_F32>, dim3(OC), dim3(NT), 0, a->stream, (const float*)a->dev[0],
+                               (const void*)a->dev[1], bias, (float*)a->dev[3], BT, C, OC);
+        else
+            hipLaunchKernelGGL(k_matmul_rows_any<HW_BF16>, dim3(OC), dim3(NT), 0, a->stream, (const float*)a->dev[0],
+                               (const void*)a->dev[1], bias, (float*)a->dev[3], BT, C, OC);
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
     BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1]) & 3) == 0, "%s: misaligned operand", name);
     DecHead h;
     memset(&h, 0, sizeof h);

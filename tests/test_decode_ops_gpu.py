@@ -315,14 +315,19 @@ def test_rmsnorm_matmul_forward_bf16_vec_rejects(be):
 
 
 @pytest.mark.parametrize("BT,C,OC,has_bias", [(1, 576, 49152, 0), (1, 128, 1024, 0), (3, 64, 100, 1),
-                                              (40, 960, 77, 1)])
+                                              (40, 960, 77, 1), (2, 4100, 300, 1), (1, 8224, 64, 0), (3, 100, 50, 1),
+                                              (1, 48, 10, 0), (2, 7, 33, 1)])
 @pytest.mark.parametrize("name", ["matmul_forward_naive", "matmul_forward_tiled", "matmul_forward_fp32_tiled",
                                   "matmul_forward_bf16_vec", "matmul_forward_bf16"])
 def test_plain_matmul_forward(be, BT, C, OC, has_bias, name):
     """The plain fp32 / bf16-weight matmuls (reference forward.metal:23-110,
     449-560; the reference prefill's LM head after COPY_LAST):
     out[bt][oc] = bias[oc] + inp[bt] . W[oc], fp32 sums, vs fp64 over the
-    same (bf16-widened) weights.  Launched with the reference's grids."""
+    same (bf16-widened) weights.  Launched with the reference's grids.  The
+    widths cover both kernels behind the names: the LM-head kernel (C a
+    multiple of 16 up to 4096 for fp32 rows, of 32 up to 8192 for bf16) and
+    the plain one for every other C (4100, 8224, 100, 48, 7), as the
+    reference's kernels take any C."""
     rng = np.random.default_rng(BT * 7 + C + OC)
     x = rng.standard_normal(BT * C).astype(np.float32)
     W = (rng.standard_normal(OC * C) * 0.02).astype(np.float32)
@@ -344,11 +349,13 @@ def test_plain_matmul_forward(be, BT, C, OC, has_bias, name):
 
 
 def test_plain_matmul_forward_rejects(be):
-    """A width the row kernel does not tile, a short weight and a short bias
-    are rejected with nothing launched."""
+    """A zero width, a short weight (for either kernel behind the name) and a
+    short bias are rejected with nothing launched."""
     out = be.alloc(4 * 10)
     x = be.upload(np.ones(48, np.float32))
     assert be.dispatch("matmul_forward_bf16_vec", [x, be.upload(np.zeros(480, np.uint16)), x, out,
+                                                   be.params(1, 0, 10, 0)], (1280,), (128,)) == -1
+    assert be.dispatch("matmul_forward_bf16_vec", [x, be.upload(np.zeros(479, np.uint16)), x, out,
                                                    be.params(1, 48, 10, 0)], (1280,), (128,)) == -1
     assert be.dispatch("matmul_forward_tiled", [be.upload(np.ones(64, np.float32)), be.upload(np.ones(9 * 64, np.float32)),
                                                 x, out, be.params(1, 64, 10, 0)], (32,), (32,)) == -1
