@@ -358,8 +358,9 @@ __device__ __forceinline__ void head_key_max(unsigned long long* key, unsigned l
     __atomic_signal_fence(__ATOMIC_SEQ_CST); /* the compiler keeps later accesses after the wait */
 }
 
-/* Weight formats of the LM head rows. */
-enum { HW_F32 = 0, HW_Q8 = 1, HW_BF16 = 2 };
+/* Weight formats of the LM head rows: fp32, Q8_0 blocks, and two 16-bit
+ * formats (bf16, IEEE fp16), each widened exactly to fp32. */
+enum { HW_F32 = 0, HW_Q8 = 1, HW_BF16 = 2, HW_F16 = 3 };
 
 template <int WF>
 __device__ __forceinline__ int head_lanes(int D) { return WF == HW_F32 ? D / 16 : D / 32; }
@@ -367,6 +368,15 @@ __device__ __forceinline__ int head_lanes(int D) { return WF == HW_F32 ? D / 16 
 /* the two bf16 values of a dword, widened exactly to fp32 */
 __device__ __forceinline__ float bf16_lo(unsigned int u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(unsigned int u) { return __uint_as_float(u & 0xffff0000u); }
+/* the same for the 16-bit formats: bf16, or IEEE fp16 (v_cvt_f32_f16, exact) */
+template <int WF>
+__device__ __forceinline__ float h16_lo(unsigned int u) {
+    return WF == HW_F16 ? (float)__builtin_bit_cast(_Float16, (unsigned short)(u & 0xffffu)) : bf16_lo(u);
+}
+template <int WF>
+__device__ __forceinline__ float h16_hi(unsigned int u) {
+    return WF == HW_F16 ? (float)__builtin_bit_cast(_Float16, (unsigned short)(u >> 16)) : bf16_hi(u);
+}
 
 template <int WF>
 __global__ __launch_bounds__(NT) void k_head(DecHead a) {
@@ -456,10 +466,10 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
 #pragma unroll
                 for (int i = 0; i < 16; i += 2) {
                     const unsigned int w0 = __float_as_uint(wf[u][i]), w1 = __float_as_uint(wf[u][i + 1]);
-                    p0 = fmaf(xs[2 * i], bf16_lo(w0), p0);
-                    p1 = fmaf(xs[2 * i + 1], bf16_hi(w0), p1);
-                    p2 = fmaf(xs[2 * i + 2], bf16_lo(w1), p2);
-                    p3 = fmaf(xs[2 * i + 3], bf16_hi(w1), p3);
+                    p0 = fmaf(xs[2 * i], h16_lo<WF>(w0), p0);
+                    p1 = fmaf(xs[2 * i + 1], h16_hi<WF>(w0), p1);
+                    p2 = fmaf(xs[2 * i + 2], h16_lo<WF>(w1), p2);
+                    p3 = fmaf(xs[2 * i + 3], h16_hi<WF>(w1), p3);
                 }
                 p = (p0 + p1) + (p2 + p3);
             }
@@ -543,10 +553,10 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
         } else {
             uint4 h4;
             __builtin_memcpy(&h4, __builtin_assume_aligned(a.wh + (size_t)rc * D + 32 * kb + 8 * g, 4), 16);
-            o.wv[0] = bf16_lo(h4.x); o.wv[1] = bf16_hi(h4.x);
-            o.wv[2] = bf16_lo(h4.y); o.wv[3] = bf16_hi(h4.y);
-            o.wv[4] = bf16_lo(h4.z); o.wv[5] = bf16_hi(h4.z);
-            o.wv[6] = bf16_lo(h4.w); o.wv[7] = bf16_hi(h4.w);
+            o.wv[0] = h16_lo<WF>(h4.x); o.wv[1] = h16_hi<WF>(h4.x);
+            o.wv[2] = h16_lo<WF>(h4.y); o.wv[3] = h16_hi<WF>(h4.y);
+            o.wv[4] = h16_lo<WF>(h4.z); o.wv[5] = h16_hi<WF>(h4.z);
+            o.wv[6] = h16_lo<WF>(h4.w); o.wv[7] = h16_hi<WF>(h4.w);
         }
         __builtin_memcpy(&o.gv[0], __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
         __builtin_memcpy(&o.gv[4], __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
@@ -2049,19 +2059,75 @@ static bool head_shape_ok(int D, int wf) {
  * params int{C, V}, eps float} (reference forward.metal:1532-1581,
  * 1636-1689; scheduler.c:931-940).  The grid the caller passes is not used:
  * the launch covers V rows by itself. */
+/* k_head over one of the unquantized row formats */
+static void launch_head_rows(const DecHead& h, int wf, hipStream_t s) {
+    if (wf == HW_F32) hipLaunchKernelGGL(k_head<HW_F32>, dim3(h.tiles), dim3(NT), 0, s, h);
+    else if (wf == HW_BF16) hipLaunchKernelGGL(k_head<HW_BF16>, dim3(h.tiles), dim3(NT), 0, s, h);
+    else hipLaunchKernelGGL(k_head<HW_F16>, dim3(h.tiles), dim3(NT), 0, s, h);
+}
+
+static const char* row_format_name(int wf) { return wf == HW_F32 ? "fp32" : wf == HW_BF16 ? "bf16" : "fp16"; }
+
+/* RMSNorm + matmul for any C the LM-head kernel does not tile: one
+ * workgroup per output row, the RMS of x recomputed in each (x is short
+ * next to a row of the head), the dot product strided over C. */
+template <int WF>
+__global__ __launch_bounds__(NT) void k_rmsnorm_matmul_rows_any(const float* __restrict__ x,
+                                                                const float* __restrict__ g, const void* __restrict__ w,
+                                                                float* __restrict__ out, int C, float eps) {
+    __shared__ float sh[NT / 64];
+    const int r = blockIdx.x;
+    float ss = 0.f;
+    for (int k = threadIdx.x; k < C; k += NT) ss = fmaf(x[k], x[k], ss);
+    const float inv = 1.0f / sqrtf(block_sum(ss, sh) / (float)C + eps);
+    const float* wf = (const float*)w + (size_t)r * C;
+    const unsigned short* wh = (const unsigned short*)w + (size_t)r * C;
+    float s = 0.f;
+    for (int k = threadIdx.x; k < C; k += NT) {
+        const float wv = WF == HW_F32 ? wf[k] : h16_lo<WF>(wh[k]);
+        s = fmaf((x[k] * inv) * g[k], wv, s);
+    }
+    s = block_sum(s, sh);
+    if (threadIdx.x == 0) out[r] = s;
+}
+
+/* rmsnorm_matmul_forward{,_bf16,_bf16_vec,_fp16,_fp16_vec} {x [C], norm
+ * weight [C], wcls [V][C] (fp32, bf16 or fp16), logits [V], params
+ * int{C, V}, eps} (reference forward.metal:1532-1581, 1585-1634,
+ * 1636-1689, 1692-1745, 1748-1801): the fused final norm and LM head.  The LM-head kernel where
+ * it tiles C (fp32 rows: a multiple of 16 up to 4096; 16-bit rows: of 32 up
+ * to 8192), k_rmsnorm_matmul_rows_any for any other C. */
 static int launch_rmsnorm_matmul(const bmk_launch_t* a, int wf) {
-    const char* name = wf == HW_F32 ? "rmsnorm_matmul" : "rmsnorm_matmul_bf16";
+    const char* name = wf == HW_F32 ? "rmsnorm_matmul" : wf == HW_BF16 ? "rmsnorm_matmul_bf16" : "rmsnorm_matmul_fp16";
     const size_t esz = wf == HW_F32 ? 4 : 2;
     BMK_NEED_BYTES(a, 4, 8, "params");
     BMK_NEED_BYTES(a, 5, 4, "eps");
     const int C = bmk_pi(a, 4, 0), V = bmk_pi(a, 4, 1);
-    BMK_REQUIRE(C > 0 && V >= 0 && head_shape_ok(C, wf), "%s: C=%d must be a multiple of %d up to %d", name, C,
-                wf == HW_F32 ? 16 : 32, wf == HW_F32 ? 4096 : 8192);
+    BMK_REQUIRE(C > 0 && V >= 0, "%s: C=%d V=%d", name, C, V);
     if (V == 0) return 0;
     BMK_NEED_BYTES(a, 0, (size_t)C * 4, "x");
     BMK_NEED_BYTES(a, 1, (size_t)C * 4, "norm weight");
     BMK_NEED_BYTES(a, 2, (size_t)V * C * esz, "wcls");
     BMK_NEED_BYTES(a, 3, (size_t)V * 4, "logits");
+    if (!head_shape_ok(C, wf)) {
+        BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1]) & 3) == 0 && ((uintptr_t)a->dev[2] & (esz - 1)) == 0,
+                    "%s: misaligned operand", name);
+        const float* x = (const float*)a->dev[0];
+        const float* g = (const float*)a->dev[1];
+        float* out = (float*)a->dev[3];
+        const float eps = bmk_pf(a, 5, 0);
+        if (wf == HW_F32)
+            hipLaunchKernelGGL(k_rmsnorm_matmul_rows_any<HW_F32>, dim3(V), dim3(NT), 0, a->stream, x, g,
+                               (const void*)a->dev[2], out, C, eps);
+        else if (wf == HW_BF16)
+            hipLaunchKernelGGL(k_rmsnorm_matmul_rows_any<HW_BF16>, dim3(V), dim3(NT), 0, a->stream, x, g,
+                               (const void*)a->dev[2], out, C, eps);
+        else
+            hipLaunchKernelGGL(k_rmsnorm_matmul_rows_any<HW_F16>, dim3(V), dim3(NT), 0, a->stream, x, g,
+                               (const void*)a->dev[2], out, C, eps);
+        BMK_LAUNCH_CHECK();
+        return 0;
+    }
     BMK_REQUIRE((((uintptr_t)a->dev[0] | (uintptr_t)a->dev[1] | (uintptr_t)a->dev[2]) & 3) == 0,
                 "%s: misaligned operand", name);
     DecHead h;
@@ -2076,14 +2142,14 @@ static int launch_rmsnorm_matmul(const bmk_launch_t* a, int wf) {
     h.B = 1;
     h.eps = bmk_pf(a, 5, 0);
     h.tiles = head_tiles(C, V, wf);
-    if (wf == HW_F32) hipLaunchKernelGGL(k_head<HW_F32>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
-    else hipLaunchKernelGGL(k_head<HW_BF16>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    launch_head_rows(h, wf, a->stream);
     BMK_LAUNCH_CHECK();
     return 0;
 }
 
 extern "C" int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_F32); }
 extern "C" int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_BF16); }
+extern "C" int bmk_launch_rmsnorm_matmul_fp16(const bmk_launch_t* a) { return launch_rmsnorm_matmul(a, HW_F16); }
 
 /* The plain matmul for any C the LM-head kernel does not tile: one
  * workgroup per output row r, the BT input rows in turn, each dot product
@@ -2101,7 +2167,7 @@ __global__ __launch_bounds__(NT) void k_matmul_rows_any(const float* __restrict_
         const float* xb = x + (size_t)b * C;
         float s = 0.f;
         for (int k = threadIdx.x; k < C; k += NT) {
-            const float wv = WF == HW_F32 ? wf[k] : __uint_as_float((unsigned int)wh[k] << 16);
+            const float wv = WF == HW_F32 ? wf[k] : h16_lo<WF>(wh[k]);
             s = fmaf(xb[k], wv, s);
         }
         s = block_sum(s, sh);
@@ -2109,11 +2175,13 @@ __global__ __launch_bounds__(NT) void k_matmul_rows_any(const float* __restrict_
     }
 }
 
-/* The plain fp32 and bf16 matmul kernels: {inp [BT][C], weight [OC][C] (fp32
- * or bf16), bias [OC], out [BT][OC], params int{BT, C, OC, has_bias}}
- * (reference forward.metal:23-37 matmul_forward_naive, 513-560
- * matmul_forward_tiled, 449-503 matmul_forward_fp32_tiled, 52-89
- * matmul_forward_bf16_vec, 91-110 matmul_forward_bf16).  The reference's
+/* The plain fp32, bf16 and fp16 matmul kernels: {inp [BT][C], weight
+ * [OC][C] (fp32, bf16 or fp16), bias [OC], out [BT][OC], params int{BT, C,
+ * OC, has_bias}} (reference forward.metal:23-37 matmul_forward_naive,
+ * 513-560 matmul_forward_tiled, 449-503 matmul_forward_fp32_tiled, 52-89
+ * matmul_forward_bf16_vec, 91-110 matmul_forward_bf16, 116-319
+ * matmul_forward_bf16_tiled / _tiled64 / _simd, 327-442
+ * matmul_forward_fp16_vec / _fp16 / _fp16_tiled).  The reference's
  * prefill takes them for the LM head of its last position (graph.c:373-380,
  * selected by scheduler.c:1118-1145 and registry.c:60-67).  Served by the
  * LM-head kernel with the RMSNorm off where it tiles C (a multiple of 16 up
@@ -2121,7 +2189,7 @@ __global__ __launch_bounds__(NT) void k_matmul_rows_any(const float* __restrict_
  * its weight rows once and applies them to all BT input rows.  Any other C
  * takes k_matmul_rows_any.  The grid the caller passes is not used. */
 static int launch_matmul_rows(const bmk_launch_t* a, int wf) {
-    const char* name = wf == HW_F32 ? "matmul_forward (fp32)" : "matmul_forward_bf16";
+    const char* name = wf == HW_F32 ? "matmul_forward (fp32)" : wf == HW_BF16 ? "matmul_forward_bf16" : "matmul_forward_fp16";
     const size_t esz = wf == HW_F32 ? 4 : 2;
     BMK_NEED_BYTES(a, 4, 16, "params");
     const int BT = bmk_pi(a, 4, 0), C = bmk_pi(a, 4, 1), OC = bmk_pi(a, 4, 2), hb = bmk_pi(a, 4, 3);
@@ -2138,8 +2206,11 @@ static int launch_matmul_rows(const bmk_launch_t* a, int wf) {
         if (wf == HW_F32)
             hipLaunchKernelGGL(k_matmul_rows_any<HW_F32>, dim3(OC), dim3(NT), 0, a->stream, (const float*)a->dev[0],
                                (const void*)a->dev[1], bias, (float*)a->dev[3], BT, C, OC);
-        else
+        else if (wf == HW_BF16)
             hipLaunchKernelGGL(k_matmul_rows_any<HW_BF16>, dim3(OC), dim3(NT), 0, a->stream, (const float*)a->dev[0],
+                               (const void*)a->dev[1], bias, (float*)a->dev[3], BT, C, OC);
+        else
+            hipLaunchKernelGGL(k_matmul_rows_any<HW_F16>, dim3(OC), dim3(NT), 0, a->stream, (const float*)a->dev[0],
                                (const void*)a->dev[1], bias, (float*)a->dev[3], BT, C, OC);
         BMK_LAUNCH_CHECK();
         return 0;
@@ -2156,14 +2227,14 @@ static int launch_matmul_rows(const bmk_launch_t* a, int wf) {
     h.V = OC;
     h.B = BT;
     h.tiles = head_tiles(C, OC, wf);
-    if (wf == HW_F32) hipLaunchKernelGGL(k_head<HW_F32>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
-    else hipLaunchKernelGGL(k_head<HW_BF16>, dim3(h.tiles), dim3(NT), 0, a->stream, h);
+    launch_head_rows(h, wf, a->stream);
     BMK_LAUNCH_CHECK();
     return 0;
 }
 
 extern "C" int bmk_launch_matmul_f32(const bmk_launch_t* a) { return launch_matmul_rows(a, HW_F32); }
 extern "C" int bmk_launch_matmul_bf16(const bmk_launch_t* a) { return launch_matmul_rows(a, HW_BF16); }
+extern "C" int bmk_launch_matmul_fp16(const bmk_launch_t* a) { return launch_matmul_rows(a, HW_F16); }
 
 /* argmax_f32 {values f32 [n], out int [1], params int{n}} */
 extern "C" int bmk_launch_argmax(const bmk_launch_t* a) {
@@ -2287,11 +2358,12 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
         if (a.B > DEC_MAX_B || a.D % 32) return -1;
         a.tiles = (a.V + 63) / 64;
         const dim3 grid(a.tiles);
-        const int wf = a.wq ? HW_Q8 : (a.wh ? HW_BF16 : HW_F32);
+        const int wf = a.wq ? HW_Q8 : (a.wh ? (a.wh_f16 ? HW_F16 : HW_BF16) : HW_F32);
 #define HEAD_B(NBT)                                                                          \
         do {                                                                                 \
             if (wf == HW_Q8) hipLaunchKernelGGL((k_head_b<NBT, HW_Q8>), grid, dim3(NT), 0, s, a);  \
             else if (wf == HW_BF16) hipLaunchKernelGGL((k_head_b<NBT, HW_BF16>), grid, dim3(NT), 0, s, a); \
+            else if (wf == HW_F16) hipLaunchKernelGGL((k_head_b<NBT, HW_F16>), grid, dim3(NT), 0, s, a); \
             else hipLaunchKernelGGL((k_head_b<NBT, HW_F32>), grid, dim3(NT), 0, s, a);        \
         } while (0)
         if (a.B <= 16) HEAD_B(1);
@@ -2305,10 +2377,29 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
     const DecHead* a = a_in;
     if (a->wq)
         hipLaunchKernelGGL(k_head<HW_Q8>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    else if (a->wh && a->wh_f16)
+        hipLaunchKernelGGL(k_head<HW_F16>, dim3(a->tiles), dim3(NT), 0, s, *a);
     else if (a->wh)
         hipLaunchKernelGGL(k_head<HW_BF16>, dim3(a->tiles), dim3(NT), 0, s, *a);
     else
         hipLaunchKernelGGL(k_head<HW_F32>, dim3(a->tiles), dim3(NT), 0, s, *a);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
+/* fp32 -> IEEE fp16 over n elements, rounded to nearest even (v_cvt_f16_f32;
+ * values past the fp16 range become infinities), as the reference's fp16
+ * upload converts (scheduler.c:410-417) */
+__global__ __launch_bounds__(NT) void k_cast_f16(const float* __restrict__ src, unsigned short* __restrict__ dst,
+                                                 long n) {
+    for (long i = (long)blockIdx.x * NT + threadIdx.x; i < n; i += (long)gridDim.x * NT)
+        dst[i] = __builtin_bit_cast(unsigned short, (_Float16)src[i]);
+}
+
+extern "C" int dec_cast_f16(const float* src, unsigned short* dst, long n, hipStream_t s) {
+    if (n <= 0) return 0;
+    const long blocks = std::min<long>((n + NT - 1) / NT, 4096);
+    hipLaunchKernelGGL(k_cast_f16, dim3((unsigned)blocks), dim3(NT), 0, s, src, dst, n);
     BMK_LAUNCH_CHECK();
     return 0;
 }

@@ -97,12 +97,13 @@ typedef struct {
     const float* bias;   /* [V] added to each output, or NULL */
     const float* w;      /* fp32 [V][D] */
     const unsigned char* wq; /* Q8 [V][D/32] blocks, or NULL */
-    const unsigned short* wh; /* bf16 [V][D], or NULL */
+    const unsigned short* wh; /* 16-bit rows [V][D] (bf16, or IEEE fp16 when wh_f16), or NULL */
     float* logits;       /* [B][V] */
     DecState* st;
     int* out_tokens;     /* [n_gen][B] (generation mode) */
     int D, V, B, tiles;
     float eps;
+    int wh_f16;          /* wh holds IEEE fp16 rows (the reference's fp16 precision) */
 } DecHead;
 
 /* Every layer of a batch-1 decode step in one persistent kernel on one

@@ -59,6 +59,7 @@ int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W
 int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C, const void* plan, int nprob,
                     int n_tiles, hipStream_t s);
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
+int dec_cast_f16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
 int dec_persist_ok(int D, int H, int NH, int NKV, int HD, int MS);
 int dec_persist_hw_ok(const char* arch, int cu_count);
@@ -105,7 +106,7 @@ struct bm_model_s {
     float* d_headw;          /* untied LM head rows (fp32); NULL when tied */
     unsigned char* d_q8;     /* all projections: per layer q, k, v, o, gate, up, down (Q8_0 or Q4_0 blocks) */
     unsigned char* d_head8;  /* Q8 head rows (q8_head) */
-    unsigned short* d_headh; /* bf16 head rows (precision BF16, no q8_head) */
+    unsigned short* d_headh; /* 16-bit head rows: bf16 (precision BF16) or fp16 (FP16), no q8_head */
     size_t off[7];           /* byte offset of each matrix inside one layer's slice */
     size_t layer_bytes;
     int nsessions;
@@ -219,8 +220,8 @@ extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
         BMK_ERR("bm_create_model: only RMSNorm + SwiGLU + RoPE models without biases are supported");
         return NULL;
     }
-    if (a->precision != BM_PRECISION_FP32 && a->precision != BM_PRECISION_BF16) {
-        BMK_ERR("bm_create_model: precision %d: the LM head runs in fp32 or bf16", (int)a->precision);
+    if (a->precision != BM_PRECISION_FP32 && a->precision != BM_PRECISION_BF16 && a->precision != BM_PRECISION_FP16) {
+        BMK_ERR("bm_create_model: precision %d: the LM head runs in fp32, bf16 or fp16", (int)a->precision);
         return NULL;
     }
     const int QD = NH * HD, KV = NKV * HD;
@@ -285,13 +286,15 @@ extern "C" int bm_model_set_quant_bits(bm_model_t* m, int bits) {
     return 0;
 }
 
-/* Head rows in use: 1 Q8, 2 bf16, 0 fp32 (decode.hip's head formats). */
-static int head_format(const bm_model_t* m) { return m->q8_head ? 1 : (m->precision == BM_PRECISION_BF16 ? 2 : 0); }
+/* Head rows in use: 1 Q8, 2 bf16, 3 fp16, 0 fp32 (decode.hip's head formats). */
+static int head_format(const bm_model_t* m) {
+    return m->q8_head ? 1 : m->precision == BM_PRECISION_BF16 ? 2 : m->precision == BM_PRECISION_FP16 ? 3 : 0;
+}
 
 extern "C" int bm_model_set_precision(bm_model_t* m, bm_precision_t p) {
     if (!m) return -1;
-    if (p != BM_PRECISION_FP32 && p != BM_PRECISION_BF16) {
-        BMK_ERR("bm_model_set_precision: the MI355X path runs the LM head in fp32 or bf16 (got %d)", (int)p);
+    if (p != BM_PRECISION_FP32 && p != BM_PRECISION_BF16 && p != BM_PRECISION_FP16) {
+        BMK_ERR("bm_model_set_precision: the MI355X path runs the LM head in fp32, bf16 or fp16 (got %d)", (int)p);
         return -1;
     }
     if (m->compiled && p != m->precision) model_free_device(m);
@@ -447,11 +450,13 @@ static int model_compile(bm_model_t* m) {
     if (rc == 0 && m->q8_head) {
         if (hipMalloc(&m->d_head8, q8_bytes((size_t)m->V * D)) != hipSuccess) rc = -1;
         else rc = q8_pack_f32(head_src, m->d_head8, (long)m->V * D, s);
-    } else if (rc == 0 && head_format(m) == 2) {
-        /* bf16 rows of the head (the tied embedding or lm_head), rounded to
-         * nearest even as the reference's bf16 upload does (scheduler.c:369-371,395-402) */
+    } else if (rc == 0 && head_format(m) >= 2) {
+        /* 16-bit rows of the head (the tied embedding or lm_head), rounded to
+         * nearest even as the reference's bf16 / fp16 uploads do
+         * (scheduler.c:369-374, 395-418) */
         if (hipMalloc(&m->d_headh, (size_t)m->V * D * 2) != hipSuccess) rc = -1;
-        else rc = gm_cast_bf16(head_src, m->d_headh, (long)m->V * D, s);
+        else if (head_format(m) == 2) rc = gm_cast_bf16(head_src, m->d_headh, (long)m->V * D, s);
+        else rc = dec_cast_f16(head_src, m->d_headh, (long)m->V * D, s);
     }
     if (hipStreamSynchronize(s) != hipSuccess) rc = -1;
     hipFree(stage);
@@ -578,7 +583,8 @@ static int enqueue_step(bm_session_t* S) {
     memset(&hd, 0, sizeof hd);
     hd.x = S->x; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
     hd.wq = m->q8_head ? m->d_head8 : NULL;
-    hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
+    hd.wh = head_format(m) >= 2 ? m->d_headh : NULL;
+    hd.wh_f16 = head_format(m) == 3;
     hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
     hd.tiles = dec_head_tiles(D, m->V, head_format(m));
@@ -1146,7 +1152,8 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
     memset(&hd, 0, sizeof hd);
     hd.x = w.x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;
     hd.wq = m->q8_head ? m->d_head8 : NULL;
-    hd.wh = head_format(m) == 2 ? m->d_headh : NULL;
+    hd.wh = head_format(m) >= 2 ? m->d_headh : NULL;
+    hd.wh_f16 = head_format(m) == 3;
     hd.logits = S->logits; hd.st = NULL; hd.out_tokens = NULL;
     hd.D = D; hd.V = m->V; hd.B = 1; hd.eps = eps;
     hd.tiles = dec_head_tiles(D, m->V, head_format(m));

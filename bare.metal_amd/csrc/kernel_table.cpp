@@ -36,9 +36,11 @@ int bmk_launch_add(const bmk_launch_t* a);
 int bmk_launch_swiglu(const bmk_launch_t* a);
 int bmk_launch_rmsnorm_matmul(const bmk_launch_t* a);
 int bmk_launch_rmsnorm_matmul_bf16(const bmk_launch_t* a);
+int bmk_launch_rmsnorm_matmul_fp16(const bmk_launch_t* a);
 int bmk_launch_argmax(const bmk_launch_t* a);
 int bmk_launch_matmul_f32(const bmk_launch_t* a);
 int bmk_launch_matmul_bf16(const bmk_launch_t* a);
+int bmk_launch_matmul_fp16(const bmk_launch_t* a);
 }
 
 #define B(i) (1u << (i))
@@ -115,15 +117,27 @@ extern "C" const bmk_desc_t bmk_table[] = {
     /* reference forward.metal:1691-1735, the same head with one thread per row
      * (scheduler.c:782-783 takes it at bf16 precision); same buffers and launch */
     {"rmsnorm_matmul_forward_bf16", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_bf16, 0},
-    /* the plain fp32 / bf16-weight matmuls, which the reference's prefill takes
-     * for the LM head of its last position (graph.c:373-380, scheduler.c:1118-1145,
-     * registry.c:60-67): reference forward.metal:23-37, 513-560, 449-503 (fp32),
-     * 52-89, 91-110 (bf16); {inp, weight, bias, out, params{BT,C,OC,has_bias}} */
+    /* reference forward.metal:1585-1634 and 1748-1801: the same heads over fp16
+     * rows (scheduler.c:779-785 takes them at fp16 precision); same buffers */
+    {"rmsnorm_matmul_forward_fp16_vec", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_fp16, 0},
+    {"rmsnorm_matmul_forward_fp16", 6, B(4) | B(5), B(3), bmk_launch_rmsnorm_matmul_fp16, 0},
+    /* the plain fp32 / bf16 / fp16-weight matmuls, which the reference's
+     * scheduler takes for unquantized projections and its prefill for the LM
+     * head of the last position (graph.c:373-380, scheduler.c:764-775,
+     * 1117-1141, registry.c:60-67): reference forward.metal:23-37, 513-560,
+     * 449-503 (fp32), 52-89, 91-110, 116-319 (bf16), 327-442 (fp16);
+     * {inp, weight, bias, out, params{BT,C,OC,has_bias}} */
     {"matmul_forward_naive", 5, B(4), B(3), bmk_launch_matmul_f32, 0},
     {"matmul_forward_tiled", 5, B(4), B(3), bmk_launch_matmul_f32, 0},
     {"matmul_forward_fp32_tiled", 5, B(4), B(3), bmk_launch_matmul_f32, 0},
     {"matmul_forward_bf16_vec", 5, B(4), B(3), bmk_launch_matmul_bf16, 0},
     {"matmul_forward_bf16", 5, B(4), B(3), bmk_launch_matmul_bf16, 0},
+    {"matmul_forward_bf16_tiled", 5, B(4), B(3), bmk_launch_matmul_bf16, 0},
+    {"matmul_forward_bf16_tiled64", 5, B(4), B(3), bmk_launch_matmul_bf16, 0},
+    {"matmul_forward_bf16_simd", 5, B(4), B(3), bmk_launch_matmul_bf16, 0},
+    {"matmul_forward_fp16_vec", 5, B(4), B(3), bmk_launch_matmul_fp16, 0},
+    {"matmul_forward_fp16", 5, B(4), B(3), bmk_launch_matmul_fp16, 0},
+    {"matmul_forward_fp16_tiled", 5, B(4), B(3), bmk_launch_matmul_fp16, 0},
     /* new: greedy pick on the device (reference tools/run.c:56-60); {values, out int, params{n}} */
     {"argmax_f32", 3, B(2), B(1), bmk_launch_argmax, 0},
     {nullptr, 0, 0, 0, nullptr, 0},

@@ -23,7 +23,7 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(ROOT, "bare.metal_amd"))
+sys.path.insert(0, ROOT)
 
 import numpy as np  # noqa: E402
 

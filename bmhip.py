@@ -16,7 +16,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libbaremetal_hip.so")
+LIB_PATH = os.path.join(HERE, "bare.metal_amd", "libbaremetal_hip.so")
 
 _lib = None
 

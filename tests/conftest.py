@@ -5,8 +5,7 @@ import sys
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-for sub in ("bare.metal_amd", "oracle"):
-    p = os.path.join(ROOT, sub)
+for p in (ROOT, os.path.join(ROOT, "oracle")):  # bmhip (the ctypes wrapper) and the oracle
     if p not in sys.path:
         sys.path.insert(0, p)
 

@@ -22,15 +22,18 @@ def q8_arrays(w: dict, qbits: int = 8) -> dict:
 
 def oracle_decoder(dims: dict, w: dict, ms: int, q8_head: bool = False, nthreads: int = 8,
                    precision: str = "fp32", head_f32=None, qbits: int = 8) -> po.Decoder:
-    """precision "bf16": the head rows are rounded to bf16 (reference
-    scheduler.c:395-402), widened back to fp32 exactly.  head_f32: the rows of
-    an untied head (default: the tied embedding)."""
+    """precision "bf16" / "fp16": the head rows are rounded to bf16 or IEEE
+    fp16, to nearest even (reference scheduler.c:395-418), and widened back to
+    fp32 exactly.  head_f32: the rows of an untied head (default: the tied
+    embedding)."""
     arrs = q8_arrays(w, qbits)
     head = w["token_embedding"] if head_f32 is None else np.ascontiguousarray(head_f32, np.float32)
     if q8_head:
         arrs["head_q8"] = po.quantize_q8(head)
     elif precision == "bf16":
         arrs["head_f32"] = po.bf16_rne(head)
+    elif precision == "fp16":
+        arrs["head_f32"] = head.astype(np.float16).astype(np.float32)
     elif head_f32 is not None:
         arrs["head_f32"] = head
     d = dict(dims)

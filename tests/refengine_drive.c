@@ -20,7 +20,7 @@
  *   mode "greedy":  bm_run_tokens with temperature 0 for <steps> = the first
  *                   token argument, the prompt = the remaining tokens; the
  *                   generated ids to <out> (int32).
- *   precision: fp32 | bf16; quant: 8 | 4 | 0.
+ *   precision: fp32 | bf16 | fp16; quant: 8 | 4 | 0.
  * Exit status 0 on success; 2 on a usage error; 3 if the engine failed.
  */
 #include "baremetal.h"
@@ -73,7 +73,9 @@ int main(int argc, char** argv) {
         return 3;
     }
     model->quant_bits = quant;
-    model->precision = strcmp(prec, "bf16") == 0 ? BM_PRECISION_BF16 : BM_PRECISION_FP32;
+    model->precision = strcmp(prec, "bf16") == 0   ? BM_PRECISION_BF16
+                       : strcmp(prec, "fp16") == 0 ? BM_PRECISION_FP16
+                                                   : BM_PRECISION_FP32;
     if (max_seq > 0 && model->arch.max_seq_len > max_seq) model->arch.max_seq_len = max_seq;
     const int V = model->arch.vocab_size;
 

@@ -265,7 +265,7 @@ def test_add_and_swiglu(be):
     assert nw(o.read(np.float32), g / (1 + np.exp(-g)) * b) <= TOL
 
 
-@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300)])
+@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300), (4100, 40), (100, 33), (7, 5)])
 def test_rmsnorm_matmul_forward(be, C, V):
     rng = np.random.default_rng(C)
     x = rng.standard_normal(C).astype(np.float32)
@@ -280,18 +280,30 @@ def test_rmsnorm_matmul_forward(be, C, V):
     assert nw(out.read(np.float32), W.reshape(V, C).astype(np.float64) @ xn) <= TOL
 
 
-@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300), (32, 17)])
-@pytest.mark.parametrize("name", ["rmsnorm_matmul_forward_bf16_vec", "rmsnorm_matmul_forward_bf16"])
+def _h16(w, name):
+    """w rounded to the name's 16-bit row format: (its values as fp32, its bits)."""
+    if "fp16" in name:
+        h = w.astype(np.float16)
+        return h.astype(np.float32), h.view(np.uint16)
+    r = po.bf16_rne(w)
+    return r, (r.view(np.uint32) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("C,V", [(576, 49152), (960, 1000), (64, 300), (32, 17), (8224, 20), (48, 10), (100, 7)])
+@pytest.mark.parametrize("name", ["rmsnorm_matmul_forward_bf16_vec", "rmsnorm_matmul_forward_bf16",
+                                  "rmsnorm_matmul_forward_fp16_vec", "rmsnorm_matmul_forward_fp16"])
 def test_rmsnorm_matmul_forward_bf16_vec(be, C, V, name):
-    """bf16 head rows (reference forward.metal:1532-1581, and the one-thread-
-    per-row rmsnorm_matmul_forward_bf16 of :1691-1735 with the same buffers):
-    each weight widened exactly, fp32 products and sums; vs fp64 over the same
-    bf16 values."""
+    """16-bit head rows: bf16 (reference forward.metal:1532-1581, and the
+    one-thread-per-row rmsnorm_matmul_forward_bf16 of :1692-1745 with the
+    same buffers) and IEEE fp16 (:1585-1634, :1748-1801, taken at the
+    reference's fp16 precision): each weight widened exactly, fp32 products
+    and sums; vs fp64 over the same 16-bit values.  The widths cover the
+    LM-head kernel (multiples of 32 up to 8192) and the plain kernel for any
+    other C (8224, 48, 100)."""
     rng = np.random.default_rng(C + 1)
     x = rng.standard_normal(C).astype(np.float32)
     g = rng.uniform(0.5, 1.5, C).astype(np.float32)
-    Wr = po.bf16_rne((rng.standard_normal(V * C) * 0.02).astype(np.float32))  # bf16 values as fp32
-    bits = (Wr.view(np.uint32) >> 16).astype(np.uint16)
+    Wr, bits = _h16((rng.standard_normal(V * C) * 0.02).astype(np.float32), name)
     out = be.alloc(V * 4)
     rc = be.dispatch(name, [be.upload(x), be.upload(g), be.upload(bits), out,
                             be.params(C, V), be.upload(f32(1e-5))],
@@ -303,10 +315,10 @@ def test_rmsnorm_matmul_forward_bf16_vec(be, C, V, name):
 
 
 def test_rmsnorm_matmul_forward_bf16_vec_rejects(be):
-    C, V = 48, 10  # C not a multiple of 32
+    C, V = 0, 10  # no columns
     out = be.alloc(V * 4)
-    bufs = [be.upload(np.ones(C, np.float32)), be.upload(np.ones(C, np.float32)),
-            be.upload(np.zeros(V * C, np.uint16)), out, be.params(C, V), be.upload(f32(1e-5))]
+    bufs = [be.upload(np.ones(4, np.float32)), be.upload(np.ones(4, np.float32)),
+            be.upload(np.zeros(V * 4, np.uint16)), out, be.params(C, V), be.upload(f32(1e-5))]
     assert be.dispatch("rmsnorm_matmul_forward_bf16_vec", bufs, (512,), (512,)) == -1
     C = 64  # wcls one row short
     bufs = [be.upload(np.ones(C, np.float32)), be.upload(np.ones(C, np.float32)),
@@ -318,10 +330,13 @@ def test_rmsnorm_matmul_forward_bf16_vec_rejects(be):
                                               (40, 960, 77, 1), (2, 4100, 300, 1), (1, 8224, 64, 0), (3, 100, 50, 1),
                                               (1, 48, 10, 0), (2, 7, 33, 1)])
 @pytest.mark.parametrize("name", ["matmul_forward_naive", "matmul_forward_tiled", "matmul_forward_fp32_tiled",
-                                  "matmul_forward_bf16_vec", "matmul_forward_bf16"])
+                                  "matmul_forward_bf16_vec", "matmul_forward_bf16", "matmul_forward_bf16_tiled",
+                                  "matmul_forward_bf16_tiled64", "matmul_forward_bf16_simd", "matmul_forward_fp16_vec",
+                                  "matmul_forward_fp16", "matmul_forward_fp16_tiled"])
 def test_plain_matmul_forward(be, BT, C, OC, has_bias, name):
-    """The plain fp32 / bf16-weight matmuls (reference forward.metal:23-110,
-    449-560; the reference prefill's LM head after COPY_LAST):
+    """The plain fp32 / bf16 / fp16-weight matmuls (reference
+    forward.metal:23-442, 449-560; the reference prefill's LM head after
+    COPY_LAST, and its unquantized projections at bf16 or fp16 precision):
     out[bt][oc] = bias[oc] + inp[bt] . W[oc], fp32 sums, vs fp64 over the
     same (bf16-widened) weights.  Launched with the reference's grids.  The
     widths cover both kernels behind the names: the LM-head kernel (C a
@@ -332,10 +347,9 @@ def test_plain_matmul_forward(be, BT, C, OC, has_bias, name):
     x = rng.standard_normal(BT * C).astype(np.float32)
     W = (rng.standard_normal(OC * C) * 0.02).astype(np.float32)
     bias = rng.standard_normal(OC).astype(np.float32) if has_bias else np.zeros(1, np.float32)
-    bf16 = "bf16" in name
-    if bf16:
-        W = po.bf16_rne(W)
-        wbuf = be.upload((W.view(np.uint32) >> 16).astype(np.uint16))
+    if "bf16" in name or "fp16" in name:
+        W, bits = _h16(W, name)
+        wbuf = be.upload(bits)
     else:
         wbuf = be.upload(W)
     out = be.alloc(BT * OC * 4)

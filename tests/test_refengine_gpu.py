@@ -46,13 +46,15 @@ def _model(tmp_path, dims, seed, dtype="F32"):
     return w
 
 
-@pytest.mark.parametrize("precision", ["fp32", "bf16"])
+@pytest.mark.parametrize("precision", ["fp32", "bf16", "fp16"])
 @pytest.mark.parametrize("dims", [TINY, SMALL], ids=["tiny", "small"])
 def test_reference_engine_q8_decode_matches_oracle(tmp_path, dims, precision):
     """bm_step over 24 tokens: the reference scheduler's Q8 decode
     (matmul_forward_q8_vec, rmsnorm_forward_v2, rope_forward, kv_store,
-    attention_forward, add_forward, swiglu_forward and the fp32 or bf16 LM
-    head by name) against the oracle and against this repository's engine."""
+    attention_forward, add_forward, swiglu_forward and the fp32, bf16 or
+    fp16 LM head by name: at fp16 the reference uploads the head as IEEE
+    fp16 and takes rmsnorm_matmul_forward_fp16_vec) against the oracle and
+    against this repository's engine."""
     w = _model(tmp_path / "ckpt", dims, 301)
     toks = bmhip.synth_uniform_int(302, 0, dims["V"], 24)
     out = tmp_path / "logits.bin"
