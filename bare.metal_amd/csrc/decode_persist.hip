@@ -101,6 +101,18 @@ constexpr int APR = HD + 2;          /* one partial: max, sum, P.V[HD] */
 constexpr int PS_OFF = 1024;         /* attention: the waves' key probabilities in the staged-vector LDS, past q, k, v */
 constexpr float SPIN_SECONDS = 0.2f;
 constexpr unsigned long long PEEK_TICKS = 1000; /* 10 us at 100 MHz: from then on a wait reads sync_error */
+/* LDS of an instance running NB sequences (NB = 1 or 2): the staged input
+ * vectors, NB x at most XS_SEQ floats for NB = 2, the block products of
+ * NB vectors, and the attention merge weights (NB = 2: at most EW_B); at
+ * most 80 KB, so that two instances share a CU */
+constexpr int EW_B = 1024;
+constexpr int XS_SEQ = 2048;
+template <int NB>
+struct PLds {
+    static constexpr int XS = NB == 1 ? XS_MAX : NB * XS_SEQ;
+    static constexpr int RED = P_MAX * PT * NB;
+    static constexpr int EW = NB == 1 ? XS_MAX / HD * DEC_PERSIST_NCH : EW_B;
+};
 
 /* threadIdx.x, opaque to the compiler: address arithmetic built on it is
  * redone in every phase instead of being hoisted out of the layer loop and
@@ -114,7 +126,7 @@ __device__ __forceinline__ int tid() {
 
 static_assert(2 * KCH * HD <= APS_MAX, "the K and V sub-chunks share the partials' LDS");
 static_assert(4 * HD + 2 * HD <= PS_OFF && PS_OFF + (PT / 64) * KCH <= XS_MAX, "q, k, v and the probabilities share xs");
-static_assert((DEC_PERSIST_NCH * APR) % 2 == 0, "partials load as 16-byte pairs of exchanged values");
+static_assert(APR % 2 == 0, "partials load as 16-byte pairs of exchanged values");
 static_assert(P_QKV <= P_MAX && P_O <= P_MAX && P_GU <= P_MAX && P_DN <= P_MAX, "pass caps");
 
 /* Keeps the compiler from moving instructions across this point: loads
@@ -159,16 +171,23 @@ __device__ __forceinline__ float wmax(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
-/* Sum over the workgroup (every thread gets it). */
-__device__ __forceinline__ float bsum(float v, float* sh) {
-    v = wsum(v);
-    lds_barrier(); /* earlier readers of sh are done */
-    if ((tid() & 63) == 0) sh[tid() >> 6] = v;
-    lds_barrier();
-    float r = 0.f;
+/* Sums over the workgroup of NB values per thread (every thread gets them). */
+template <int NB>
+__device__ __forceinline__ void bsum(float (&v)[NB], float* sh) {
 #pragma unroll
-    for (int i = 0; i < PT / 64; i++) r += sh[i];
-    return r;
+    for (int j = 0; j < NB; j++) v[j] = wsum(v[j]);
+    lds_barrier(); /* earlier readers of sh are done */
+    if ((tid() & 63) == 0)
+#pragma unroll
+        for (int j = 0; j < NB; j++) sh[j * (PT / 64) + (tid() >> 6)] = v[j];
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        float r = 0.f;
+#pragma unroll
+        for (int i = 0; i < PT / 64; i++) r += sh[j * (PT / 64) + i];
+        v[j] = r;
+    }
 }
 
 /* Values exchanged between phases (see the file comment): the float's bits
@@ -235,17 +254,19 @@ __device__ __forceinline__ void poll_xv(Ready&& ready, Reload&& reload, const Sy
     }
 }
 
-/* Elements tid + k * PT (clamped to C - 1) of an exchanged vector of C
- * values, once they carry epoch ep: one round of loads, then polls. */
-template <int N>
-__device__ __forceinline__ void get_vec(const xv_t* x, int C, unsigned int ep, float (&v)[N], const Sync& sy) {
-    xv_t u[N];
+/* Elements tid + k * PT (clamped to C - 1) of NB exchanged vectors of C
+ * values (vector j at x + j * C), once they carry epoch ep: one round of
+ * loads, then polls. */
+template <int NB, int N>
+__device__ __forceinline__ void get_vec(const xv_t* x, int C, unsigned int ep, float (&v)[NB][N], const Sync& sy) {
+    xv_t u[NB * N];
+    auto addr = [&](int k) { return x + (k / N) * C + min(tid() + (k % N) * PT, C - 1); };
 #pragma unroll
-    for (int k = 0; k < N; k++) u[k] = get_xv(x + min(tid() + k * PT, C - 1));
-    poll_xv<N>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; },
-               [&](int k) { u[k] = get_xv(x + min(tid() + k * PT, C - 1)); }, sy);
+    for (int k = 0; k < NB * N; k++) u[k] = get_xv(addr(k));
+    poll_xv<NB * N>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; }, [&](int k) { u[k] = get_xv(addr(k)); },
+                    sy);
 #pragma unroll
-    for (int k = 0; k < N; k++) v[k] = xv_val(u[k]);
+    for (int k = 0; k < NB * N; k++) v[k / N][k % N] = xv_val(u[k]);
 }
 
 /* One workgroup's share of a matvec phase: output rows [r0, r1) of
@@ -280,21 +301,25 @@ __device__ __forceinline__ void mv_fetch(const MvShare& j, Blk (&blk)[NP]) {
     }
 }
 
-/* The block products of the fetched blocks with xs into red[local row][nb]. */
-template <int NP>
-__device__ __forceinline__ void mv_products(int n, int nb, const Blk (&blk)[NP], const float* xs, float* red) {
+/* The block products of the fetched blocks with each of the NB staged
+ * vectors (vector j at xs + j * C) into red[j][local row][nb]. */
+template <int NB, int NP>
+__device__ __forceinline__ void mv_products(int n, int nb, const Blk (&blk)[NP], const float* xs, int C, float* red) {
     const int t = tid(), slots = PT / nb, slot = t / nb, bc = t - slot * nb;
     if (slot < slots) {
-        float xv[32];
 #pragma unroll
-        for (int i = 0; i < 32; i += 4) {
-            const float4 v = *(const float4*)&xs[32 * bc + i];
-            xv[i] = v.x; xv[i + 1] = v.y; xv[i + 2] = v.z; xv[i + 3] = v.w;
-        }
+        for (int j = 0; j < NB; j++) {
+            float xv[32];
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            const int i = p * slots + slot;
-            if (i < n) red[i * nb + bc] = block_dot(blk[p], xv);
+            for (int i = 0; i < 32; i += 4) {
+                const float4 v = *(const float4*)&xs[j * C + 32 * bc + i];
+                xv[i] = v.x; xv[i + 1] = v.y; xv[i + 2] = v.z; xv[i + 3] = v.w;
+            }
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                const int i = p * slots + slot;
+                if (i < n) red[(j * n + i) * nb + bc] = block_dot(blk[p], xv);
+            }
         }
     }
     lds_barrier();
@@ -314,36 +339,36 @@ __device__ __forceinline__ float quad_row_sum(const float* red, int row, int nb)
     return acc;
 }
 
-/* Products of the fetched blocks with xs, per-row sums (a quad of lanes
- * per row), and the outputs, exchanged with epoch ep: y[r0 + o] = sum, or
- * with a residual (row o of the residual stream in *xres of thread 4o,
- * o < 64) y[r0 + o] = *xres += sum (also stored to plain[r0 + o] when plain
- * is given), or for SwiGLU y[r0 + o] = silu(gate) * up (gate row 2o in quad
- * 2o, up row 2o + 1 in the next quad). */
-template <int NP>
-__device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP], const float* xs, float* red,
-                                          xv_t* y, unsigned int ep, float* xres, float* plain) {
-    const int nb = j.nb, nout = j.r1 - j.r0, t = tid();
-    mv_products(mv_rows(j), nb, blk, xs, red);
+/* Products of the fetched blocks with the NB staged vectors (each C long),
+ * per-row sums (a quad of lanes per row), and the outputs of sequence s,
+ * exchanged with epoch ep at y + s * ldy: for SwiGLU y[r0 + o] = silu(gate)
+ * * up (gate row 2o in one quad, up row 2o + 1 in the next), else with the
+ * residual y[r0 + o] = xres += sum (also stored to plain[s * ldy + r0 + o]
+ * when plain is given).  The residual rows (s, o) a workgroup updates are
+ * entries e = s * nout + o, entry e in xres[e / 64] of thread 4 (e % 64). */
+template <int NB, int NP>
+__device__ __forceinline__ void mv_finish(const MvShare& j, const Blk (&blk)[NP], const float* xs, int C, float* red,
+                                          xv_t* y, int ldy, unsigned int ep, float (&xres)[NB], float* plain) {
+    const int nb = j.nb, nout = j.r1 - j.r0, t = tid(), n = mv_rows(j), tot = NB * nout;
+    mv_products<NB>(n, nb, blk, xs, C, red);
     if (j.glu) {
-        for (int o0 = 0; o0 < nout; o0 += PT / 8) {
-            const int o = o0 + (t >> 3), row = min(2 * o + ((t >> 2) & 1), 2 * nout - 1);
+        for (int e0 = 0; e0 < tot; e0 += PT / 8) {
+            const int e = min(e0 + (t >> 3), tot - 1), s = e / nout, o = e - s * nout;
+            const int row = s * n + min(2 * o + ((t >> 2) & 1), 2 * nout - 1);
             const float sum = quad_row_sum(red, row, nb);
             const float up = dpp<DPP_HALF_MIRROR>(sum); /* lane i of 8 <- 7 - i: the other quad's sum */
-            if ((t & 7) == 0 && o < nout) put_xv(y + j.r0 + o, (sum / (1.0f + expf(-sum))) * up, ep);
+            if ((t & 7) == 0 && e0 + (t >> 3) < tot) put_xv(y + s * ldy + j.r0 + o, (sum / (1.0f + expf(-sum))) * up, ep);
         }
     } else {
-        for (int o0 = 0; o0 < nout; o0 += PT / 4) {
-            const int o = o0 + (t >> 2);
-            const float sum = quad_row_sum(red, min(o, nout - 1), nb);
-            if ((t & 3) == 0 && o < nout) {
-                if (xres) {
-                    *xres += sum;
-                    put_xv(y + j.r0 + o, *xres, ep);
-                    if (plain) plain[j.r0 + o] = *xres;
-                } else {
-                    put_xv(y + j.r0 + o, sum, ep);
-                }
+#pragma unroll
+        for (int it = 0; it < NB; it++) {
+            if (it * (PT / 4) >= tot) break;
+            const int e = it * (PT / 4) + (t >> 2), ec = min(e, tot - 1), s = ec / nout, o = ec - s * nout;
+            const float sum = quad_row_sum(red, s * n + o, nb);
+            if ((t & 3) == 0 && e < tot) {
+                xres[it] += sum;
+                put_xv(y + s * ldy + j.r0 + o, xres[it], ep);
+                if (plain) plain[s * ldy + j.r0 + o] = xres[it];
             }
         }
     }
@@ -357,33 +382,45 @@ __device__ __forceinline__ void load_vec(const float* x, int C, float (&v)[N]) {
     for (int k = 0; k < N; k++) v[k] = x[min(tid() + k * PT, C - 1)];
 }
 
-/* xs = RMSNorm(x) * nw from x's loaded elements, C <= NW * PT (reference
- * forward.metal:1019-1060: inv = 1/sqrt(mean(x^2) + eps), (x * inv) * w). */
-__device__ __forceinline__ void norm_to_lds(const float (&v)[NW], int C, const float (&nw)[NW], float eps, float* xs,
-                                            float* sh) {
-    float ss = 0.f;
+/* xs[j] = RMSNorm(x_j) * nw from the loaded elements of NB vectors, C <=
+ * NW * PT (reference forward.metal:1019-1060: inv = 1/sqrt(mean(x^2) +
+ * eps), (x * inv) * w). */
+template <int NB>
+__device__ __forceinline__ void norm_to_lds(const float (&v)[NB][NW], int C, const float (&nw)[NW], float eps,
+                                            float* xs, float* sh) {
+    float ss[NB];
 #pragma unroll
-    for (int k = 0; k < NW; k++) {
-        const float e = tid() + k * PT < C ? v[k] : 0.f;
-        ss = fmaf(e, e, ss);
+    for (int j = 0; j < NB; j++) {
+        ss[j] = 0.f;
+#pragma unroll
+        for (int k = 0; k < NW; k++) {
+            const float e = tid() + k * PT < C ? v[j][k] : 0.f;
+            ss[j] = fmaf(e, e, ss[j]);
+        }
     }
-    ss = bsum(ss, sh);
-    const float inv = 1.0f / sqrtf(ss / (float)C + eps);
+    bsum<NB>(ss, sh);
 #pragma unroll
-    for (int k = 0; k < NW; k++) {
-        const int i = tid() + k * PT;
-        if (i < C) xs[i] = (v[k] * inv) * nw[k];
+    for (int j = 0; j < NB; j++) {
+        const float inv = 1.0f / sqrtf(ss[j] / (float)C + eps);
+#pragma unroll
+        for (int k = 0; k < NW; k++) {
+            const int i = tid() + k * PT;
+            if (i < C) xs[j * C + i] = (v[j][k] * inv) * nw[k];
+        }
     }
     lds_barrier();
 }
 
-/* xs = x from its loaded elements, C <= XR * PT. */
-__device__ __forceinline__ void vec_to_lds(const float (&v)[XR], int C, float* xs) {
+/* xs[j] = x_j from the loaded elements of NB vectors, C <= XR * PT. */
+template <int NB>
+__device__ __forceinline__ void vec_to_lds(const float (&v)[NB][XR], int C, float* xs) {
 #pragma unroll
-    for (int k = 0; k < XR; k++) {
-        const int i = tid() + k * PT;
-        if (i < C) xs[i] = v[k];
-    }
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int k = 0; k < XR; k++) {
+            const int i = tid() + k * PT;
+            if (i < C) xs[j * C + i] = v[j][k];
+        }
     lds_barrier();
 }
 
@@ -393,29 +430,35 @@ __device__ __forceinline__ void share_rows(int R, int w, int& r0, int& r1) {
     r1 = (int)((long)R * (w + 1) / DEC_PERSIST_WGS);
 }
 
-/* One attention piece (KV head kh, key chunk c of the keys 0..pos):
- * keys [k0, k1), of which those below lim are in the cache and key pos (if
- * here) is this step's. */
+/* One attention piece (sequence s of the instance, KV head kh, key chunk c
+ * of nch over the keys 0..pos): keys [k0, k1), of which those below lim are
+ * in the cache and key pos (if here) is this step's. */
 struct Piece {
-    int kh, c, kv_mul, nq, nraw, k0, k1, lim;
+    int s, kh, c, nch, kv_mul, nq, nraw, k0, k1, lim;
     float* kT; /* the KV head's K cache, [HD/4][MS] float4 */
     float* vc; /* its V cache rows, stride KV */
 };
 
-__device__ __forceinline__ Piece make_piece(const DecPersist& a, int layer, int w, int pos) {
+/* Piece w of the instance whose first sequence is b0 (the session's KV
+ * cache is [B][L][2][MS * KV]). */
+__device__ __forceinline__ Piece make_piece(const DecPersist& a, int layer, int w, int pos, int b0, int nch) {
     Piece p;
-    p.kh = w / DEC_PERSIST_NCH;
-    p.c = w % DEC_PERSIST_NCH;
+    const int per = a.NKV * nch;
+    p.s = w / per;
+    p.kh = (w - p.s * per) / nch;
+    p.c = w - p.s * per - p.kh * nch;
+    p.nch = nch;
     p.kv_mul = a.NH / a.NKV;
     p.nq = p.kv_mul * HD;
     p.nraw = p.nq + 2 * HD;
-    const int S = pos + 1, cs = (S + DEC_PERSIST_NCH - 1) / DEC_PERSIST_NCH;
+    const int S = pos + 1, cs = (S + nch - 1) / nch;
     p.k0 = p.c * cs;
     p.k1 = min(S, p.k0 + cs);
     p.lim = min(p.k1, pos);
     const size_t slab = (size_t)a.MS * a.KV;
-    p.kT = a.kvc + (size_t)layer * 2 * slab + (size_t)p.kh * HD * a.MS;
-    p.vc = a.kvc + ((size_t)layer * 2 + 1) * slab + p.kh * HD;
+    const size_t sl = (size_t)(b0 + p.s) * a.L + layer; /* this sequence's layer */
+    p.kT = a.kvc + sl * 2 * slab + (size_t)p.kh * HD * a.MS;
+    p.vc = a.kvc + (sl * 2 + 1) * slab + p.kh * HD;
     return p;
 }
 
@@ -568,7 +611,7 @@ __device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p
         lds_barrier();
     }
     if (wave < p.kv_mul) {
-        xv_t* pr = apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        xv_t* pr = apart + ((size_t)(p.s * a.NH + p.kh * p.kv_mul + wave) * p.nch + p.c) * APR;
         put_xv(pr + 2 + lane, acc, ep);
         if (lane == 0) {
             put_xv(pr, m_run, ep);
@@ -578,10 +621,10 @@ __device__ __forceinline__ void attn_compute(const DecPersist& a, const Piece& p
 }
 
 /* The partials of a chunk without keys. */
-__device__ __forceinline__ void attn_empty(const Piece& p, xv_t* apart, unsigned int ep) {
+__device__ __forceinline__ void attn_empty(const DecPersist& a, const Piece& p, xv_t* apart, unsigned int ep) {
     const int wave = tid() >> 6, lane = tid() & 63;
     if (wave < p.kv_mul) {
-        xv_t* pr = apart + ((size_t)(p.kh * p.kv_mul + wave) * DEC_PERSIST_NCH + p.c) * APR;
+        xv_t* pr = apart + ((size_t)(p.s * a.NH + p.kh * p.kv_mul + wave) * p.nch + p.c) * APR;
         put_xv(pr + 2 + lane, 0.f, ep);
         if (lane == 0) {
             put_xv(pr, -INFINITY, ep);
@@ -590,15 +633,17 @@ __device__ __forceinline__ void attn_empty(const Piece& p, xv_t* apart, unsigned
     }
 }
 
-/* Attention output of every query head from the partials of its chunks
- * (exchanged with epoch ep), staged into LDS with one round of loads and
- * polls (after_loads then issues more loads, once the partials' registers
- * are free): out[h][d] = sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c,
- * the weights e^(m_c - M) computed once per (head, chunk) (ew). */
-template <typename F>
-__device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apart, unsigned int ep, float* aps, float* ew,
-                                           float* xs, const Sync& sy, F&& after_loads) {
-    const int total2 = a.NH * DEC_PERSIST_NCH * APR / 2; /* 16-byte loads of two exchanged values */
+/* Attention output of every query head of the NB sequences from the
+ * partials of its nch chunks (exchanged with epoch ep), staged into LDS with
+ * one round of loads and polls (after_loads then issues more loads, once
+ * the partials' registers are free): out[h][d] = sum_c e^(m_c - M) acc_c[d]
+ * / sum_c e^(m_c - M) l_c, the weights e^(m_c - M) computed once per (head,
+ * chunk) (ew); sequence j's heads at xs + j * NH * HD. */
+template <int NB, typename F>
+__device__ __forceinline__ void attn_merge(const DecPersist& a, int nch, const xv_t* apart, unsigned int ep, float* aps,
+                                           float* ew, float* xs, const Sync& sy, F&& after_loads) {
+    const int nh = NB * a.NH;                  /* heads of all NB sequences */
+    const int total2 = nh * nch * APR / 2;     /* 16-byte loads of two exchanged values */
     /* agent-scope (sc1: miss the L1) loads through a buffer resource over the
      * partials; past its end a buffer load returns 0 (such slots count as
      * ready) */
@@ -625,23 +670,23 @@ __device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apar
     lds_barrier();
     /* ew[h][c] = e^(m_c - M_h), one thread per (head, chunk); 0 for a chunk
      * without keys */
-    if (tid() < a.NH * DEC_PERSIST_NCH) {
-        const int h = tid() / DEC_PERSIST_NCH, c = tid() - h * DEC_PERSIST_NCH;
-        const float* pr = aps + h * DEC_PERSIST_NCH * APR;
+    for (int i = tid(); i < nh * nch; i += PT) {
+        const int h = i / nch, c = i - h * nch;
+        const float* pr = aps + h * nch * APR;
         float M = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < DEC_PERSIST_NCH; k++) M = fmaxf(M, pr[k * APR]);
+        for (int k = 0; k < nch; k++) M = fmaxf(M, pr[k * APR]);
         const float m = pr[c * APR];
-        ew[tid()] = m == -INFINITY ? 0.f : expf(m - M);
+        ew[i] = m == -INFINITY ? 0.f : expf(m - M);
     }
     lds_barrier();
-    for (int i = tid(); i < a.NH * HD; i += PT) {
+    for (int i = tid(); i < nh * HD; i += PT) {
         const int h = i / HD, d = i - h * HD;
-        const float* pr = aps + h * DEC_PERSIST_NCH * APR;
-        const float* e = ew + h * DEC_PERSIST_NCH;
+        const float* pr = aps + h * nch * APR;
+        const float* e = ew + h * nch;
         float L = 0.f, A = 0.f;
 #pragma unroll
-        for (int c = 0; c < DEC_PERSIST_NCH; c++) {
+        for (int c = 0; c < nch; c++) {
             L = fmaf(e[c], pr[c * APR + 1], L);
             A = fmaf(e[c], pr[c * APR + 2 + d], A);
         }
@@ -654,68 +699,92 @@ __device__ __forceinline__ void attn_merge(const DecPersist& a, const xv_t* apar
  * XCD the wave runs on */
 constexpr int HWREG_XCC_ID_3_0 = (3 << 11) | (0 << 6) | 20;
 
+/* G instances, each on one XCD (two share an XCD when G > 8, each
+ * workgroup of one then sharing a CU with one of the other), each running
+ * NB sequences (b0 = g * NB ...) through every layer; the instance's
+ * exchanged vectors hold NB rows each. */
+template <int NB>
 __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
-    if (blockIdx.x % 8) return; /* the working workgroups all sit on one XCD */
-    const int w = (int)blockIdx.x / 8;
+    /* workgroup b: XCD slot b % 8, then r = b / 8 = 32 h + w: instance g =
+     * b % 8 + 8 h (all of whose workgroups share one XCD), working
+     * workgroup w of it */
+    const int r = (int)(blockIdx.x / 8);
+    const int g = (int)(blockIdx.x % 8) + 8 * (r / DEC_PERSIST_WGS);
+    if (g >= a.G) return;
+    const int w = r % DEC_PERSIST_WGS;
     /* tests only: this workgroup acts as if it ran off its peers' XCD (never
      * workgroup 0, which empties a placement slot below) */
     if (w == a.fault_wg) {
         if (threadIdx.x == 0) __hip_atomic_store(&a.st->sync_error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    __shared__ __attribute__((aligned(16))) float xs[XS_MAX];
-    __shared__ float red[P_MAX * PT];
+    __shared__ __attribute__((aligned(16))) float xs[PLds<NB>::XS]; /* staged input vectors, or the attention's q, k, v */
+    __shared__ __attribute__((aligned(16))) float red[PLds<NB>::RED];
     __shared__ __attribute__((aligned(16))) float big[APS_MAX]; /* attention partials, or one K and V sub-chunk */
-    __shared__ float sh[PT / 64];
-    __shared__ float ew[XS_MAX / HD * DEC_PERSIST_NCH]; /* attention merge weights */
+    __shared__ float sh[NB * (PT / 64)];
+    __shared__ float ew[PLds<NB>::EW]; /* attention merge weights */
     __shared__ int bad; /* a wave of this workgroup timed out waiting for a value */
     DecState* st = a.st;
     const int pos = st->pos;
-    const int D = a.D, H = a.H, QD = a.QD, KV = a.KV;
-    const bool has_piece = w < a.NKV * DEC_PERSIST_NCH;
-    /* the exchanged vectors, and the epochs of this step's phases: phase p
-     * (1..5) of layer l writes with epoch (steps << 8) + 5 l + p, where steps
-     * (advanced by the embedding kernel before every step, never reset) is
-     * the same for every workgroup of the launch */
-    xv_t* xf = a.ex + DEC_PERSIST_EX_HEAD;
-    xv_t* hf = xf + D;
-    xv_t* qkvf = hf + H;
-    xv_t* apf = qkvf + QD + 2 * KV;
+    const int D = a.D, H = a.H, QD = a.QD, KV = a.KV, QKV = QD + 2 * KV;
+    const int nch = NB == 1 ? DEC_PERSIST_NCH : a.nch; /* key chunks per (sequence, KV head) */
+    const int b0 = g * NB;                            /* the instance's first sequence */
+    const bool has_piece = w < NB * a.NKV * nch;
+    /* the instance's exchanged vectors (NB rows each), and the epochs of
+     * this step's phases: phase p (1..5) of layer l writes with epoch
+     * (steps << 8) + 5 l + p, where steps (advanced by the embedding kernel
+     * before every step, never reset; word 0 of the first instance's
+     * buffer) is the same for every workgroup of the launch */
+    xv_t* exg = a.ex + (size_t)g * a.ex_stride;
+    xv_t* xf = exg + DEC_PERSIST_EX_HEAD;
+    xv_t* hf = xf + NB * D;
+    xv_t* qkvf = hf + NB * H;
+    xv_t* apf = qkvf + NB * QKV;
     const unsigned int steps = __hip_atomic_load((const unsigned int*)a.ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned int ep0 = steps << 8;
     auto ep = [&](int l, int ph) { return ep0 + (unsigned int)(5 * l + ph); };
-    /* The exchange relies on every working workgroup sharing one XCD's L2
-     * (which one depends on where the dispatch starts).  Each adds its XCD
-     * id to this step's placement slot; one that finds another XCD's bit
-     * there flags the step void (sync_error 2) before its first wait (its
-     * first-phase outputs may already be written: the step is void either
-     * way), the others stop waiting soon after, and the host reruns the
-     * step on the per-phase kernels.  The atomic's result is waited for only
-     * then, after the whole first phase. */
+    /* The exchange relies on every working workgroup of an instance sharing
+     * one XCD's L2 (which one depends on where the dispatch starts).  Each
+     * adds its XCD id to this step's placement slot of its instance; one
+     * that finds another XCD's bit there flags the step void (sync_error 2)
+     * before its first wait (its first-phase outputs may already be
+     * written: the step is void either way), the others stop waiting soon
+     * after, and the host reruns the step on the per-phase kernels.  The
+     * atomic's result is waited for only then, after the whole first
+     * phase. */
     const unsigned int xcc_bit = 1u << (__builtin_amdgcn_s_getreg(HWREG_XCC_ID_3_0) & 0xf);
     unsigned int placed = 0;
-    if (tid() == 0) placed = atomicOr((unsigned int*)a.ex + 2 + (steps & 3u), xcc_bit);
+    if (tid() == 0) placed = atomicOr((unsigned int*)exg + 2 + (steps & 3u), xcc_bit);
     /* the slot of the step after next, emptied now (a device-scope atomic,
      * like the atomicOr's it precedes; this launch ends before that step's
      * kernel starts) */
-    if (w == 0 && tid() == 0) atomicExch((unsigned int*)a.ex + 2 + ((steps + 2u) & 3u), 0u);
+    if (w == 0 && tid() == 0) atomicExch((unsigned int*)exg + 2 + ((steps + 2u) & 3u), 0u);
     if (tid() == 0) bad = 0;
     const Sync sy = {st, &bad, a.spin_ticks ? a.spin_ticks : (unsigned long long)(SPIN_SECONDS * 1e8f)};
 
-    /* cos, sin of the step's RoPE angle for rotary pair lane % 32 */
+    /* cos, sin of the step's RoPE angle for rotary pair lane % 32 (every
+     * sequence is at the same position) */
     float rc, rs;
     {
         const float ang = (float)pos * a.inv_freq[tid() & (HD / 2 - 1)];
         rc = cosf(ang);
         rs = sinf(ang);
     }
-    /* the rows of x this workgroup updates (o and down split D the same way):
-     * row o in thread 4o, the lane that writes it */
-    float xres = 0.f;
+    /* the rows of x this workgroup updates (o and down split D the same
+     * way): row o of sequence s is entry e = s * (r1 - r0) + o, held in
+     * xres[e / 64] of thread 4 (e % 64), the lane that writes it */
+    float xres[NB];
     {
         int r0, r1;
         share_rows(D, w, r0, r1);
-        if ((tid() & 3) == 0 && (tid() >> 2) < r1 - r0) xres = a.x[r0 + (tid() >> 2)];
+        const int n = r1 - r0;
+#pragma unroll
+        for (int it = 0; it < NB; it++) {
+            xres[it] = 0.f;
+            const int e = it * (PT / 4) + (tid() >> 2);
+            if ((tid() & 3) == 0 && e < NB * n)
+                xres[it] = a.x[(size_t)(b0 + e / n) * D + r0 + e % n];
+        }
     }
 
     /* the shares of this workgroup in the four matvec phases of a layer */
@@ -759,16 +828,17 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     };
     auto finish_qkv = [&](const MvShare& s0, const MvShare& s1, const MvShare& s2, const Blk(&blk)[P_QKV],
                           unsigned int e) {
-        const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0, n2 = s2.r1 - s2.r0;
+        const int n0 = s0.r1 - s0.r0, n1 = s1.r1 - s1.r0, n = n0 + n1 + (s2.r1 - s2.r0), tot = NB * n;
         const int nb = s0.nb, o = tid();
-        mv_products(n0 + n1 + n2, nb, blk, xs, red);
-        for (int r0 = 0; r0 < n0 + n1 + n2; r0 += PT / 4) {
-            const int r = r0 + (o >> 2);
-            const float acc = quad_row_sum(red, min(r, n0 + n1 + n2 - 1), nb);
-            if ((o & 3) == 0 && r < n0 + n1 + n2) {
-                if (r < n0) put_xv(qkvf + s0.r0 + r, acc, e);
-                else if (r < n0 + n1) put_xv(qkvf + QD + s1.r0 + r - n0, acc, e);
-                else put_xv(qkvf + QD + KV + s2.r0 + r - n0 - n1, acc, e);
+        mv_products<NB>(n, nb, blk, xs, D, red);
+        for (int e0 = 0; e0 < tot; e0 += PT / 4) {
+            const int ei = e0 + (o >> 2), ec = min(ei, tot - 1), sq = ec / n, r = ec - sq * n;
+            const float acc = quad_row_sum(red, sq * n + r, nb);
+            if ((o & 3) == 0 && ei < tot) {
+                xv_t* q = qkvf + sq * QKV;
+                if (r < n0) put_xv(q + s0.r0 + r, acc, e);
+                else if (r < n0 + n1) put_xv(q + QD + s1.r0 + r - n0, acc, e);
+                else put_xv(q + QD + KV + s2.r0 + r - n0 - n1, acc, e);
             }
         }
     };
@@ -784,12 +854,16 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
         /* 1. RMSNorm + q, k, v; o's weights stream in behind x.  At the first
          * layer x is the embedding kernel's output (plain). */
         {
-            float v[NW];
-            if (l == 0) load_vec(a.x, D, v);
-            else get_vec(xf, D, ep(l - 1, 5), v, sy);
+            float v[NB][NW];
+            if (l == 0) {
+#pragma unroll
+                for (int j = 0; j < NB; j++) load_vec(a.x + (size_t)(b0 + j) * D, D, v[j]);
+            } else {
+                get_vec<NB>(xf, D, ep(l - 1, 5), v, sy);
+            }
             issue_order();
             mv_fetch(so, bo);
-            norm_to_lds(v, D, nw, a.eps, xs, sh);
+            norm_to_lds<NB>(v, D, nw, a.eps, xs, sh);
         }
         if (bad) return;
         finish_qkv(q0, q1, q2, bq, ep(l, 1));
@@ -802,78 +876,92 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
                 __hip_atomic_store(&st->sync_error, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 bad = 1;
             }
-            const Piece pc = make_piece(a, l, w, pos);
+            const Piece pc = make_piece(a, l, w, pos, b0, nch);
             const bool live = has_piece && pc.k0 < pc.k1;
             AttnRegs ar;
             if (live) {
                 load_kv(a, pc, pc.k0, ar);
-                attn_load(a, pc, ar, qkvf, ep(l, 1), sy);
+                attn_load(a, pc, ar, qkvf + pc.s * QKV, ep(l, 1), sy);
             }
             issue_order();
             fetch_norm(a.ln2 + (size_t)l * D, nw);
             lds_barrier();
             if (bad) return;
             if (live) attn_compute(a, pc, pos, rc, rs, ar, xs, big, apf, ep(l, 2));
-            else if (has_piece) attn_empty(pc, apf, ep(l, 2));
+            else if (has_piece) attn_empty(a, pc, apf, ep(l, 2));
         }
         /* 3. merge + o + residual; gate/up weights stream in behind the partials */
-        attn_merge(a, apf, ep(l, 2), big, ew, xs, sy, [&] { mv_fetch(sg, bg); });
+        attn_merge<NB>(a, nch, apf, ep(l, 2), big, ew, xs, sy, [&] { mv_fetch(sg, bg); });
         if (bad) return;
-        mv_finish(so, bo, xs, red, xf, ep(l, 3), &xres, nullptr);
+        mv_finish<NB>(so, bo, xs, QD, red, xf, D, ep(l, 3), xres, nullptr);
         /* 4. RMSNorm + gate, up + SwiGLU; down's weights stream in behind x */
         {
-            float v[NW];
-            get_vec(xf, D, ep(l, 3), v, sy);
+            float v[NB][NW];
+            get_vec<NB>(xf, D, ep(l, 3), v, sy);
             issue_order();
             mv_fetch(sd, bd);
-            norm_to_lds(v, D, nw, a.eps, xs, sh);
+            norm_to_lds<NB>(v, D, nw, a.eps, xs, sh);
         }
         if (bad) return;
-        mv_finish(sg, bg, xs, red, hf, ep(l, 4), nullptr, nullptr);
+        mv_finish<NB>(sg, bg, xs, D, red, hf, H, ep(l, 4), xres, nullptr);
         /* 5. down + residual; the next layer's q, k, v and first RMSNorm
          * weights stream in behind h (after the last layer: the last
          * layer's again, unused; no branch, so that h's loads stay first).
          * The last layer also writes x plain, for the LM head. */
         {
-            float v[XR];
-            get_vec(hf, H, ep(l, 4), v, sy);
+            float v[NB][XR];
+            get_vec<NB>(hf, H, ep(l, 4), v, sy);
             issue_order();
             const int ln = min(l + 1, a.L - 1);
             shares(ln, q0, q1, q2, so, sg, sd);
             fetch_qkv(q0, q1, q2, bq);
             fetch_norm(a.ln1 + (size_t)ln * D, nw);
             issue_order();
-            vec_to_lds(v, H, xs);
+            vec_to_lds<NB>(v, H, xs);
         }
         if (bad) return;
-        mv_finish(sd, bd, xs, red, xf, ep(l, 5), &xres, l == a.L - 1 ? a.x : nullptr);
+        mv_finish<NB>(sd, bd, xs, H, red, xf, D, ep(l, 5), xres, l == a.L - 1 ? a.x + (size_t)b0 * D : nullptr);
     }
 }
 
 } // namespace
 
-/* Whether the persistent step can run this shape: head size 64, every
- * phase's share within its register stage, one output row per thread, the
- * vectors within their LDS stages, and the conditions under which reusing
- * an exchange buffer needs no barrier.  That argument (file comment) is a
- * chain: a buffer is written again only after its writer has read some
- * later phase's output in full, which each of its writers produced only
- * after reading the buffer.  It holds when
+/* Key chunks per (sequence, KV head) of an instance running NB sequences:
+ * enough pieces for the 32 working workgroups, one workgroup each. */
+extern "C" int dec_persist_nch(int NKV, int NB) {
+    if (NKV <= 0 || NB <= 0) return 0;
+    if (NB == 1) return DEC_PERSIST_NCH;
+    const int c = DEC_PERSIST_WGS / (NKV * NB);
+    return c < DEC_PERSIST_NCH ? c : DEC_PERSIST_NCH;
+}
+
+/* Whether the persistent step can run this shape with NB sequences per
+ * instance (NB = 1 or 2): head size 64, every phase's share within its
+ * register stage, one output row per thread, the vectors within their LDS
+ * stages, and the conditions under which reusing an exchange buffer needs
+ * no barrier.  That argument (file comment) is a chain: a buffer is
+ * written again only after its writer has read some later phase's output
+ * in full, which each of its writers produced only after reading the
+ * buffer.  It holds when
  *   (R1) every working workgroup writes rows in phases 1, 3, 4 and 5 (the
  *        q/k/v, o, gate/up and down rows are split evenly over
  *        DEC_PERSIST_WGS, so each needs at least DEC_PERSIST_WGS rows),
- *   (R2) every (KV head, key chunk) piece has a workgroup, which writes its
- *        partials every step (empty ones too), and
+ *   (R2) every (sequence, KV head, key chunk) piece has a workgroup, which
+ *        writes its partials every step (empty ones too), and
  *   (R3) phase 3 reads every piece's partials and phases 1, 4 and 5 read
  *        the whole of x or h in every workgroup (the kernel's code);
- * (R1) and (R2) are checked here. */
-extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
-    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT ||
-        NH * HD > XS_MAX || NH * DEC_PERSIST_NCH * APR > APS_MAX || MS <= 0)
+ * (R1) and (R2) are checked here.  Instances share nothing but the step
+ * count and the error flag. */
+extern "C" int dec_persist_ok_b(int D, int H, int NH, int NKV, int HD_, int MS, int NB) {
+    if (NB != 1 && NB != 2) return 0;
+    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT || MS <= 0)
         return 0;
+    const int nch = dec_persist_nch(NKV, NB);
     const int QD = NH * HD, KV = NKV * HD;
+    const int xs = NB == 1 ? XS_MAX : NB * XS_SEQ, ew = NB == 1 ? XS_MAX / HD * DEC_PERSIST_NCH : EW_B;
+    if (NB * QD > xs || NB * D > xs || NB * H > xs || NB * NH * nch * APR > APS_MAX || NB * NH * nch > ew) return 0;
     if (QD + 2 * KV < DEC_PERSIST_WGS || D < DEC_PERSIST_WGS || H < DEC_PERSIST_WGS) return 0; /* (R1) */
-    if (NKV * DEC_PERSIST_NCH > DEC_PERSIST_WGS) return 0;                                    /* (R2) */
+    if (nch < 1 || NB * NKV * nch > DEC_PERSIST_WGS) return 0;                               /* (R2) */
     auto passes = [](int rows_per_wg, int nb) { return nb > PT ? P_MAX + 1 : (rows_per_wg + PT / nb - 1) / (PT / nb); };
     const int w = DEC_PERSIST_WGS;
     const int qkv = (QD + 2 * KV + w - 1) / w, dr = (D + w - 1) / w, hr = (H + w - 1) / w;
@@ -883,6 +971,11 @@ extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
     if (passes(2 * hr, D / 32) > P_GU) return 0;
     if (passes(dr, H / 32) > P_DN) return 0;
     return 1;
+}
+
+/* The batch-1 form (one instance, one sequence). */
+extern "C" int dec_persist_ok(int D, int H, int NH, int NKV, int HD_, int MS) {
+    return dec_persist_ok_b(D, H, NH, NKV, HD_, MS, 1);
 }
 
 /* Whether the device fits the kernel's memory-model assumptions: gfx950
@@ -901,7 +994,19 @@ extern "C" int dec_launch_persist(const DecPersist* a, hipStream_t s) {
                 a->L, DEC_PERSIST_MAX_L);
     BMK_REQUIRE(a->fault_wg != 0 && a->fault_wg < DEC_PERSIST_WGS, "persistent step: fault workgroup %d outside [1, %d)",
                 a->fault_wg, DEC_PERSIST_WGS);
-    hipLaunchKernelGGL(k_dec_persist, dim3(8 * DEC_PERSIST_WGS), dim3(PT), 0, s, *a);
+    BMK_REQUIRE(a->G >= 1 && a->G <= 16 && (a->G == 1 || a->ex_stride > 0),
+                "persistent step: %d instances (1..16, each with its own exchange rows)", a->G);
+    BMK_REQUIRE(a->NB == 1 || (a->nch == dec_persist_nch(a->NKV, a->NB) && a->nch >= 1),
+                "persistent step: %d key chunks for %d sequences per instance", a->nch, a->NB);
+    BMK_REQUIRE(dec_persist_ok_b(a->D, a->H, a->NH, a->NKV, a->HD, a->MS, a->NB) && a->QD == a->NH * a->HD &&
+                    a->KV == a->NKV * a->HD,
+                "persistent step: shape D=%d H=%d NH=%d NKV=%d HD=%d with %d sequences per instance not supported", a->D,
+                a->H, a->NH, a->NKV, a->HD, a->NB);
+    /* up to 8 instances one per XCD, up to 16 two per XCD (each CU then
+     * holds a workgroup of both) */
+    const dim3 grid(8 * DEC_PERSIST_WGS * (a->G > 8 ? 2 : 1)), block(PT);
+    if (a->NB == 1) hipLaunchKernelGGL(k_dec_persist<1>, grid, block, 0, s, *a);
+    else hipLaunchKernelGGL(k_dec_persist<2>, grid, block, 0, s, *a);
     BMK_LAUNCH_CHECK();
     return 0;
 }

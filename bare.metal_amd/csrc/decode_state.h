@@ -106,36 +106,43 @@ typedef struct {
     int wh_f16;          /* wh holds IEEE fp16 rows (the reference's fp16 precision) */
 } DecHead;
 
-/* Every layer of a batch-1 decode step in one persistent kernel on one
- * XCD (decode_persist.hip): DEC_PERSIST_WGS working workgroups, attention
- * split into DEC_PERSIST_NCH key chunks per KV head, at most
- * DEC_PERSIST_MAX_L layers (the epochs of one step's phases stay below 256).
+/* Every layer of a decode step in one persistent kernel
+ * (decode_persist.hip): G instances (1..16; two share each XCD when G > 8),
+ * each on one XCD with DEC_PERSIST_WGS working workgroups and NB sequences
+ * (1 or 2; instance g runs sequences g NB .. g NB + NB - 1), attention
+ * split into nch key chunks per (sequence, KV head) (DEC_PERSIST_NCH at
+ * NB = 1), at most DEC_PERSIST_MAX_L layers (the epochs of one step's
+ * phases stay below 256).
  *
- * The exchange buffer carries what the phases pass between workgroups, each
- * float with the epoch of the phase that wrote it (8 bytes: the float's bits
- * in the low word, the epoch in the high word), after three 8-byte words
- * the host never writes:
- *   [0]                   low half: the step count s (advanced by the
- *                         embedding kernel before every step)
+ * The exchange buffer holds G instance regions of ex_stride 8-byte words.
+ * A region carries what its phases pass between workgroups, each float with
+ * the epoch of the phase that wrote it (8 bytes: the float's bits in the
+ * low word, the epoch in the high word), after three 8-byte words the host
+ * never writes:
+ *   [0]                   low half, first region only: the step count s
+ *                         (advanced by the embedding kernel before every step)
  *   [1, 3)                four 32-bit placement masks: slot s % 4 gathers
  *                         the XCD ids (one bit each) of step s's working
- *                         workgroups; the persistent kernel of step s empties
- *                         slot (s + 2) % 4 ahead of its step, and the host
- *                         empties all four when the kernel is switched on
- *   [3, 3 + D)            x, the residual stream after a phase
- *   [.., + H)             h, the SwiGLU output
- *   [.., + NH*HD + 2 KV)  q, k, v
- *   [.., + NH*NCH*(HD+2)) the attention partials (max, sum, P.V[HD]) */
+ *                         workgroups of the instance; the persistent kernel
+ *                         of step s empties slot (s + 2) % 4 ahead of its
+ *                         step, and the host empties all four when the
+ *                         kernel is switched on
+ *   [3, 3 + NB D)         x, the residual stream after a phase, per sequence
+ *   [.., + NB H)          h, the SwiGLU output
+ *   [.., + NB (NH*HD + 2 KV))          q, k, v
+ *   [.., + NB NH nch (HD+2))           the attention partials (max, sum, P.V[HD]) */
 #define DEC_PERSIST_WGS 32
 #define DEC_PERSIST_NCH 10
 #define DEC_PERSIST_MAX_L 50
 #define DEC_PERSIST_EX_HEAD 3 /* 8-byte words before x */
-#define DEC_PERSIST_EX_WORDS(D, H, QD, KV, NH, HD) \
-    (DEC_PERSIST_EX_HEAD + (size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) + (size_t)(NH) * DEC_PERSIST_NCH * ((HD) + 2))
+#define DEC_PERSIST_EX_WORDS_NB(D, H, QD, KV, NH, HD, NB, NCH)                                                 \
+    (DEC_PERSIST_EX_HEAD + (size_t)(NB) * ((size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) +                      \
+                                           (size_t)(NH) * (NCH) * ((HD) + 2)))
+#define DEC_PERSIST_EX_WORDS(D, H, QD, KV, NH, HD) DEC_PERSIST_EX_WORDS_NB(D, H, QD, KV, NH, HD, 1, DEC_PERSIST_NCH)
 typedef struct {
-    float* x;                  /* [D] residual stream: the embedding at the first layer, the result after the last */
+    float* x;                  /* [B][D] residual stream: the embedding at the first layer, the result after the last */
     unsigned long long* ex;    /* the exchange buffer (above), zeroed when allocated */
-    float* kvc;                /* the session's KV cache, batch row 0 */
+    float* kvc;                /* the session's KV cache, [B][L][2][MS * KV] */
     DecState* st;
     const unsigned char* w;    /* Q8 arena of layer 0; layer l at w + l * layer_bytes */
     unsigned long long layer_bytes;
@@ -145,6 +152,8 @@ typedef struct {
     float inv_freq[DEC_MAX_HD / 2];
     float scale, eps;
     int D, H, NH, NKV, HD, KV, QD, MS, L;
+    int NB, G, nch;            /* sequences per instance, instances, key chunks (dec_persist_nch) */
+    unsigned long long ex_stride; /* 8-byte words of one instance's exchange region */
     unsigned int spin_ticks;   /* longest wait for an exchanged value, in 100 MHz ticks (0: 0.2 s) */
     int fault_wg;              /* tests only: this working workgroup acts as if on another XCD than its peers (-1: none) */
 } DecPersist;

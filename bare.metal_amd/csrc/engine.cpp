@@ -61,7 +61,8 @@ int gm_launch_multi(const void* A, int a_bf16, const unsigned char* W, float* C,
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_cast_f16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int dec_launch_head(const DecHead* a, hipStream_t s);
-int dec_persist_ok(int D, int H, int NH, int NKV, int HD, int MS);
+int dec_persist_ok_b(int D, int H, int NH, int NKV, int HD, int MS, int NB);
+int dec_persist_nch(int NKV, int NB);
 int dec_persist_hw_ok(const char* arch, int cu_count);
 int dec_launch_persist(const DecPersist* a, hipStream_t s);
 int q8_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
@@ -136,9 +137,11 @@ struct bm_session_s {
     size_t h_io_cap;
     int pos;             /* host mirror of the position */
     int use_graph;
-    int persist;         /* 1: the layers of a step run as one persistent kernel (B = 1, Q8, MI355X);
+    int persist;         /* 1: the layers of a step run as one persistent kernel (Q8, MI355X);
                             2: available, per-phase kernels in use; 0: not available */
+    int persist_nb, persist_g; /* its sequences per instance and instances (one per XCD) */
     unsigned long long* pex; /* the persistent kernel's exchange buffer (decode_state.h) */
+    size_t pex_stride;       /* 8-byte words of one instance's region of it */
     unsigned int persist_spin_ticks; /* tests only: the kernel's longest wait (0: its default) */
     int persist_fault_wg;            /* tests only: a working workgroup that acts as misplaced (-1: none) */
     unsigned long long persist_fallbacks; /* steps rerun on the per-phase kernels after a flagged persistent step */
@@ -527,6 +530,8 @@ static int enqueue_step(bm_session_t* S) {
         pa.eps = eps;
         pa.D = D; pa.H = m->H; pa.NH = m->NH; pa.NKV = m->NKV; pa.HD = m->HD; pa.KV = m->KV; pa.QD = m->QD;
         pa.MS = S->MS; pa.L = m->L;
+        pa.NB = S->persist_nb; pa.G = S->persist_g; pa.nch = dec_persist_nch(m->NKV, S->persist_nb);
+        pa.ex_stride = S->pex_stride;
         pa.spin_ticks = S->persist_spin_ticks;
         pa.fault_wg = S->persist_fault_wg;
         if (dec_launch_persist(&pa, s) || mark(S, PH_LAYERS)) return -1;
@@ -666,14 +671,22 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
         S->h_io_cap = B * (size_t)S->MS + 64;
         ok = hipHostMalloc(&S->h_io, S->h_io_cap * 4, hipHostMallocDefault) == hipSuccess;
     }
-    /* The persistent step kernel keeps its workgroups on one XCD by launching
-     * 8 per working one (MI355X places workgroup b on XCD b % 8): only where
-     * the device fits its memory-model assumptions (dec_persist_hw_ok), at
-     * batch 1, with Q8 projections and a shape it handles (dec_persist_ok,
-     * which also checks the conditions its buffer reuse relies on). */
-    if (ok && batch == 1 && m->quant_bits == 8 && dec_persist_hw_ok(ctx->be->dev_name, ctx->be->dev_cu_count) &&
-        m->L <= DEC_PERSIST_MAX_L && dec_persist_ok(m->D, m->H, m->NH, m->NKV, m->HD, S->MS)) {
-        const size_t ex = DEC_PERSIST_EX_WORDS(m->D, m->H, m->QD, m->KV, m->NH, m->HD) * 8;
+    /* The persistent step kernel runs instances of 32 workgroups, each
+     * keeping its workgroups on one XCD (MI355X places workgroup b on XCD
+     * (b + start) % 8): up to 16 sequences one per instance, 32 two per
+     * instance, with two instances per XCD past 8.  Only where the device
+     * fits its memory-model assumptions (dec_persist_hw_ok), with Q8
+     * projections and a shape it handles (dec_persist_ok_b, which also
+     * checks the conditions its buffer reuse relies on). */
+    int nb = batch <= 16 ? 1 : (batch <= 32 && batch % 2 == 0) ? 2 : 0;
+    if (ok && nb && m->quant_bits == 8 && dec_persist_hw_ok(ctx->be->dev_name, ctx->be->dev_cu_count) &&
+        m->L <= DEC_PERSIST_MAX_L && dec_persist_ok_b(m->D, m->H, m->NH, m->NKV, m->HD, S->MS, nb)) {
+        S->persist_nb = nb;
+        S->persist_g = batch / nb;
+        /* instance regions start on 256-byte lines */
+        S->pex_stride = (DEC_PERSIST_EX_WORDS_NB(m->D, m->H, m->QD, m->KV, m->NH, m->HD, nb,
+                                                 dec_persist_nch(m->NKV, nb)) + 31) & ~(size_t)31;
+        const size_t ex = S->pex_stride * S->persist_g * 8;
         ok = hipMalloc(&S->pex, ex) == hipSuccess && hipMemsetAsync(S->pex, 0, ex, ctx->s) == hipSuccess;
         S->persist = ok;
     }
@@ -715,7 +728,8 @@ extern "C" int bm_session_set_persistent(bm_session_t* S, int on) {
     /* switched back on: the kernel empties each step's placement slot two
      * steps ahead only while it runs, so all four start empty again */
     if (S->persist == 2 && want == 1)
-        HIP_TRY(hipMemsetAsync(S->pex + 1, 0, 16, S->ctx->s), "placement slots", return -1);
+        for (int g = 0; g < S->persist_g; g++)
+            HIP_TRY(hipMemsetAsync(S->pex + g * S->pex_stride + 1, 0, 16, S->ctx->s), "placement slots", return -1);
     S->persist = want;
     return 0;
 }

@@ -107,6 +107,8 @@ def lib() -> C.CDLL:
         "bm_session_set_persistent": (i, [vp, i]),
         "bm_session_persist_test_fault": (i, [vp, i, vp]),
         "dec_persist_ok": (i, [i, i, i, i, i, i]),
+        "dec_persist_ok_b": (i, [i, i, i, i, i, i, i]),
+        "dec_persist_nch": (i, [i, i]),
         "dec_persist_hw_ok": (i, [C.c_char_p, i]),
         "bm_profile_phases": (C.c_long, [vp, vp]),
     }
@@ -467,7 +469,8 @@ class Engine:
         lib().bm_session_set_graph(self.sess, 1 if on else 0)
 
     def set_persistent(self, on: bool) -> bool:
-        """Persistent one-kernel layers (batch 1, Q8, MI355X); False when not available."""
+        """Persistent one-kernel layers (Q8, MI355X; batch up to 8, 16 in twos or 32 in fours); False when not
+        available."""
         return lib().bm_session_set_persistent(self.sess, 1 if on else 0) == 0
 
     def persist_test_fault(self, mode: int):

@@ -708,3 +708,102 @@ def test_persistent_step_long_context():
     a.close()
     b.close()
     print(f"persistent vs phase kernels past 640 keys: {worst:.2e}")
+
+
+# Batched persistent steps: instances of 32 workgroups, each on one XCD;
+# B <= 8 one sequence per instance and XCD, B = 16 one sequence per
+# instance with two instances per XCD, B = 32 two sequences per instance
+# (attention split into 5 key chunks per sequence at 135M, 10 otherwise).
+@pytest.mark.parametrize("B,n", [(2, 40), (8, 40), (16, 80), (32, 140)], ids=["b2", "b8", "b16", "b32"])
+def test_persistent_batched_matches_phase_kernels(B, n):
+    """Batched SmolLM2-135M steps with every layer in one persistent launch
+    against the same shape's per-phase kernels: every row's logits within
+    the per-step bar at every position (each row fed its own tokens; at
+    B = 32 past 128 positions, so a key chunk holds several sub-chunks of
+    64), then a greedy run of 60 tokens identical in both forms, with no step
+    flagged and rerun."""
+    dims = bmhip.SMOLLM2_135M
+    seed = 2025
+    toks = bmhip.synth_uniform_int(79, 0, dims["V"], B * n).reshape(n, B)
+    a = bmhip.Engine(dims, max_seq_len=max(n, 65) + 8, seed=seed, batch=B)
+    b = bmhip.Engine(dims, max_seq_len=max(n, 65) + 8, seed=seed, batch=B)
+    try:
+        if not a.set_persistent(True):
+            pytest.skip("the persistent step kernel is not available on this device")
+        assert b.set_persistent(False)
+        worst = 0.0
+        for pos in range(n):
+            ya, yb = a.step_batch(toks[pos]), b.step_batch(toks[pos])
+            for r in range(B):
+                err = normwise(ya[r], yb[r].astype(np.float64))
+                worst = max(worst, err)
+                assert err <= LOGIT_TOL, (pos, r, err)
+        prompt = toks[:6].T.copy()
+        a.reset()
+        b.reset()
+        ga, gb = a.generate(prompt, 65), b.generate(prompt, 65)
+        assert np.array_equal(ga, gb)
+        assert a.persist_test_fault(0) == (1, 0)
+        print(f"B={B}: persistent vs phase kernels {worst:.2e}")
+    finally:
+        a.close()
+        b.close()
+
+
+@pytest.mark.parametrize("mode", [1, 2], ids=["wait-timeout", "off-peer-xcd"])
+def test_persistent_batched_fault_falls_back(mode):
+    """The batched persistent step's failure paths forced from the host
+    (bm_session_persist_test_fault) at B = 32: the flagged step reruns on
+    the per-phase kernels, its logits equal a per-phase session's bit for
+    bit, and later steps stay there."""
+    dims = bmhip.SMOLLM2_135M
+    seed, B = 2025, 32
+    a = bmhip.Engine(dims, max_seq_len=32, seed=seed, batch=B)
+    b = bmhip.Engine(dims, max_seq_len=32, seed=seed, batch=B)
+    try:
+        if not a.set_persistent(True):
+            pytest.skip("the persistent step kernel is not available on this device")
+        assert b.set_persistent(False)
+        assert a.persist_test_fault(mode) == (1, 0)
+        toks = bmhip.synth_uniform_int(80, 0, dims["V"], B * 6).reshape(6, B)
+        for pos in range(6):
+            ya, yb = a.step_batch(toks[pos]), b.step_batch(toks[pos])
+            assert np.array_equal(ya, yb), pos
+        assert a.persist_test_fault(0) == (2, 1)
+    finally:
+        a.close()
+        b.close()
+
+
+@pytest.mark.parametrize("B", [16, 32])
+def test_persistent_batched_small_shape_long_context(B):
+    """A head-64 shape with two KV heads (eight key chunks per sequence at
+    B = 32, ten at B = 16) past 300 positions, so each chunk walks
+    several sub-chunks of 64 keys: against the per-phase kernels at every
+    16th position and the oracle for rows 0 and B - 1 at the last."""
+    dims = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
+    n = 330
+    w = bmhip.synthetic_weights(dims, 17)
+    a = bmhip.Engine(dims, max_seq_len=n, seed=17, batch=B)
+    b = bmhip.Engine(dims, max_seq_len=n, seed=17, batch=B)
+    try:
+        if not a.set_persistent(True):
+            pytest.skip("the persistent step kernel is not available on this device")
+        assert b.set_persistent(False)
+        orcs = {r: oracle_decoder(dims, w, n) for r in (0, B - 1)}
+        worst = 0.0
+        for pos in range(n):
+            t = np.array([(53 * pos + 7 + 31 * r) % dims["V"] for r in range(B)], np.int32)
+            ya, yb = a.step_batch(t), b.step_batch(t)
+            if pos % 16 == 0 or pos == n - 1:
+                for r in range(B):
+                    worst = max(worst, normwise(ya[r], yb[r].astype(np.float64)))
+            for r, o in orcs.items():
+                ref = o.step(int(t[r]), pos)
+                if pos == n - 1:
+                    assert normwise(ya[r], ref) <= LOGIT_TOL, (r, normwise(ya[r], ref))
+        assert worst <= LOGIT_TOL, worst
+        assert a.persist_test_fault(0) == (1, 0)
+    finally:
+        a.close()
+        b.close()

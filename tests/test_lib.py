@@ -269,3 +269,36 @@ def test_persistent_step_host_conditions():
     assert L.dec_persist_hw_ok(b"gfx950:sramecc+:xnack-", 128) == 0  # a partition of the device
     assert L.dec_persist_hw_ok(b"gfx942:sramecc+:xnack-", 304) == 0
     assert L.dec_persist_hw_ok(b"gfx9500", 256) == 0
+
+
+def test_persistent_batched_host_conditions():
+    """dec_persist_ok_b / dec_persist_nch for NB sequences per instance (the
+    batched persistent step): key chunks per (sequence, KV head) are the 32
+    working workgroups shared out, capped at 10, so that (R2) every piece
+    has a workgroup; the staged vectors of both sequences and their
+    attention partials fit the kernel's LDS; NB other than 1 and 2 is
+    rejected.  The batch-1 form is NB = 1 (always 10 chunks, so a shape with
+    4 KV heads runs two per instance but not alone)."""
+    L = bmhip.lib()
+    wgs = 32
+    assert [L.dec_persist_nch(3, nb) for nb in (1, 2)] == [10, 5]   # SmolLM2-135M
+    assert [L.dec_persist_nch(2, nb) for nb in (1, 2)] == [10, 8]
+    assert L.dec_persist_nch(5, 2) == 3 and L.dec_persist_nch(17, 2) == 0
+    for nb in (1, 2):
+        assert L.dec_persist_ok_b(576, 1536, 9, 3, 64, 384, nb) == 1     # SmolLM2-135M
+    for nb in (0, 3, 4):
+        assert L.dec_persist_ok_b(576, 1536, 9, 3, 64, 384, nb) == 0
+    # (R2): 17 KV heads x 2 sequences need more than 32 workgroups
+    assert L.dec_persist_ok_b(1088, 2048, 17, 17, 64, 384, 2) == 0
+    for D in (64, 256, 576, 1024):
+        for H in (512, 1536, 2048):
+            for NKV in (1, 2, 3, 4):
+                for g in (1, 2, 3, 4):
+                    NH = NKV * g
+                    one = L.dec_persist_ok_b(D, H, NH, NKV, 64, 128, 1)
+                    assert one == L.dec_persist_ok(D, H, NH, NKV, 64, 128)
+                    ok = L.dec_persist_ok_b(D, H, NH, NKV, 64, 128, 2)
+                    nch = L.dec_persist_nch(NKV, 2)
+                    if ok:
+                        assert nch >= 1 and 2 * NKV * nch <= wgs, (D, H, NH, NKV)
+                        assert 2 * NH * nch * 66 <= 8192 and 2 * max(D, H, NH * 64) <= 4096
