@@ -566,10 +566,13 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
             __builtin_memcpy(&o.xv[bt][4], __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
         }
     };
-    Ops cur, nxt;
-    load(0, cur);
-    for (int kb = 0; kb < nkb; kb++) {
-        load(min(kb + 1, nkb - 1), nxt);
+    /* three stages: blocks kb + 1 and kb + 2 in flight during block kb's
+     * products (past the last block the loads repeat it, unused) */
+    Ops o0, o1, o2;
+    load(0, o0);
+    load(min(1, nkb - 1), o1);
+    __builtin_amdgcn_sched_barrier(0);
+    auto compute = [&](const Ops& cur) {
 #pragma unroll
         for (int bt = 0; bt < NBT; bt++) {
             float xv[8];
@@ -590,7 +593,21 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
                     acc[bt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[i], cur.wv[i], acc[bt], 0, 0, 0);
             }
         }
-        cur = nxt;
+    };
+    /* the scheduling barriers keep each stage's loads ahead of the products
+     * (the compiler would otherwise sink them to their use) */
+    for (int kb = 0; kb < nkb; kb += 3) {
+        load(min(kb + 2, nkb - 1), o2);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(o0);
+        if (kb + 1 >= nkb) break;
+        load(min(kb + 3, nkb - 1), o0);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(o1);
+        if (kb + 2 >= nkb) break;
+        load(min(kb + 4, nkb - 1), o1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(o2);
     }
 #pragma unroll
     for (int bt = 0; bt < NBT; bt++) {

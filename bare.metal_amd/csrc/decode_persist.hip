@@ -851,6 +851,14 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     fetch_qkv(q0, q1, q2, bq);
     fetch_norm(a.ln1, nw);
     for (int l = 0; l < a.L; l++) {
+        /* Two instances per XCD: each CU holds a workgroup of both, and issue
+         * goes to the oldest wave first, so the instance dispatched first
+         * would run ahead and the step wait for the other.  They take the
+         * higher issue priority in turns, one layer each. */
+        if (a.G > 8) {
+            if ((l + (g >> 3)) & 1) __builtin_amdgcn_s_setprio(1);
+            else __builtin_amdgcn_s_setprio(0);
+        }
         /* 1. RMSNorm + q, k, v; o's weights stream in behind x.  At the first
          * layer x is the embedding kernel's output (plain). */
         {
@@ -932,7 +940,7 @@ extern "C" int dec_persist_nch(int NKV, int NB) {
     if (NKV <= 0 || NB <= 0) return 0;
     if (NB == 1) return DEC_PERSIST_NCH;
     const int c = DEC_PERSIST_WGS / (NKV * NB);
-    return c < DEC_PERSIST_NCH ? c : DEC_PERSIST_NCH;
+    return c < DEC_PERSIST_NCH_B ? c : DEC_PERSIST_NCH_B;
 }
 
 /* Whether the persistent step can run this shape with NB sequences per

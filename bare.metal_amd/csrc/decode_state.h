@@ -133,6 +133,9 @@ typedef struct {
  *   [.., + NB NH nch (HD+2))           the attention partials (max, sum, P.V[HD]) */
 #define DEC_PERSIST_WGS 32
 #define DEC_PERSIST_NCH 10
+#ifndef DEC_PERSIST_NCH_B
+#define DEC_PERSIST_NCH_B 10 /* most key chunks per (sequence, KV head) at NB = 2 */
+#endif
 #define DEC_PERSIST_MAX_L 50
 #define DEC_PERSIST_EX_HEAD 3 /* 8-byte words before x */
 #define DEC_PERSIST_EX_WORDS_NB(D, H, QD, KV, NH, HD, NB, NCH)                                                 \
