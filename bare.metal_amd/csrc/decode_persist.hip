@@ -1,7 +1,8 @@
 /* SPDX-License-Identifier: MPL-2.0
  *
- * decode_persist.hip — every layer of a batch-1 decode step in one
- * persistent kernel on one XCD of MI355X.
+ * decode_persist.hip — every layer of a decode step in one persistent
+ * kernel on MI355X: instances of 32 workgroups, each on one XCD, running
+ * one or two sequences.
  *
  * The reference runs a decode step as one dispatch per graph node
  * (reference src/baremetal/graph.c:126-226, scheduler.c:712-996): per
@@ -9,8 +10,9 @@
  * o projection, the residual add, RMSNorm, gate/up, SwiGLU, down and the
  * residual add.  At batch 1 on MI355X each such launch is bound by its
  * fixed cost (about 2.5 us from one kernel's end to the next one's first
- * useful load) rather than by its bytes, so this kernel runs the whole
- * layer stack as five phases per layer inside one launch:
+ * useful load) rather than by its bytes, and at batch 32 still about half
+ * of a step is launch cost, so this kernel runs the whole layer stack as
+ * five phases per layer inside one launch:
  *   1. RMSNorm(x) and q, k, v (Q8 matvecs of 960 rows at SmolLM2-135M);
  *   2. RoPE, KV append and attention, split into (KV head, key chunk)
  *      pieces that write online-softmax partials (max, sum, P.V);
@@ -37,10 +39,16 @@
  *     owns (the o and down projections split the rows of x the same way),
  *     so a residual add reads nothing.
  *
- * One XCD: MI355X hands workgroups to its 8 XCDs round-robin (b to XCD
- * (b + start) % 8, the start depending on the dispatch).  The grid has 8 x
- * DEC_PERSIST_WGS workgroups; those with blockIdx.x % 8 == 0 work and the
- * rest return at once, so every working workgroup shares one L2.
+ * Instances on one XCD each: MI355X hands workgroups to its 8 XCDs
+ * round-robin (b to XCD (b + start) % 8, the start depending on the
+ * dispatch).  The grid has 8 x DEC_PERSIST_WGS workgroups (twice that for
+ * more than 8 instances); instance g takes the workgroups with b % 8 ==
+ * g % 8 in the first or second half, so its working workgroups share one L2,
+ * and workgroups of instances past G return at once.  An instance runs NB
+ * sequences (one or two) through every phase: each weight block's products
+ * with all NB staged vectors, the RMSNorms and residuals per sequence, and
+ * NB x NKV x nch attention pieces.  Instances share nothing but the step
+ * count and the error flag.
  *
  * No grid barrier: every value one phase hands to another workgroup (x, h,
  * q/k/v, the attention partials) is stored together with the epoch of the

@@ -220,13 +220,14 @@ int            bm_generate_greedy(bm_session_t* sess, const int* prompt, int n_p
  * captured graph (same kernels, same results).  Default 1. */
 int            bm_session_set_graph(bm_session_t* sess, int on);
 
-/* 1 (default where available): a batch-1 session with Q8 projections on
- * MI355X runs every layer of a decode step as one persistent kernel on one
- * XCD (five phases per layer separated by in-kernel barriers); 0: one
- * kernel per fused phase, as batched sessions do.  Both compute the same
- * formulas in fp32 (summation orders differ).  Returns 0, or -1 when the
- * persistent form is not available for the session (then only 0 is
- * accepted). */
+/* 1 (default where available): a session with Q8 projections on MI355X
+ * and a batch of up to 16, or an even batch up to 32, runs every layer of a
+ * decode step as one persistent kernel: instances of 32 workgroups, each on
+ * one XCD running one or two sequences through five phases per layer that
+ * hand values over without grid barriers; 0: one kernel per fused phase.
+ * Both compute the same formulas in fp32 (summation orders differ).
+ * Returns 0, or -1 when the persistent form is not available for the
+ * session (then only 0 is accepted). */
 int            bm_session_set_persistent(bm_session_t* sess, int on);
 
 /* GPU time (HIP events around each submission) and submissions of the
