@@ -16,7 +16,8 @@
  *   1. RMSNorm(x) and q, k, v (Q8 matvecs of 960 rows at SmolLM2-135M);
  *   2. RoPE, KV append and attention, split into (KV head, key chunk)
  *      pieces that write online-softmax partials (max, sum, P.V);
- *   3. the partials merged per query head, o projection, residual;
+ *   3. each workgroup merges its share of the attention output from the
+ *      partials and hands it over; then the o projection, residual;
  *   4. RMSNorm, gate and up, SwiGLU;
  *   5. down projection, residual.
  * A phase costs a chain of memory round trips rather than bytes, so each
@@ -24,12 +25,14 @@
  * requests of a CU leave in order, and one counter covers a wave's loads and
  * stores, so the order of issue decides what waits for what:
  *   - every staging step (the input vector, the attention partials, the
- *     q/k/v of a KV head) issues all of its loads before it waits on any,
+ *     merged attention output, the q/k/v of a KV head) issues all of its
+ *     loads before it waits on any,
  *     with in-bounds addresses for unused lanes so that the compiler can
  *     count them; an attention piece's cached keys and values go first;
  *   - the weights of the next matvec phase are issued right after a
  *     phase's inputs have arrived (o in phase 1, the second RMSNorm in phase
- *     2, gate/up in phase 3, down in phase 4, the next layer's q/k/v and
+ *     2, gate/up in phase 3 behind the merged output, down in phase 4, the
+ *     next layer's q/k/v and
  *     first RMSNorm in phase 5), so they stream in while the phase computes,
  *     into registers of their own (per-phase pass counts P_QKV, P_O, P_GU,
  *     P_DN);
@@ -100,26 +103,24 @@ constexpr int P_MAX = 8;
 constexpr int XS_MAX = 4096;         /* floats of the staged input vector */
 constexpr int XR = 8;                /* elements of the hidden vector h per thread: H <= 2048 */
 constexpr int NW = 4;                /* RMSNorm elements per thread: D <= 1024 */
+constexpr int QR = 4;                /* elements of the attention output per thread: NH * HD <= 1024 */
 constexpr int BUF_FLAGS = 0x00020000; /* word 3 of a raw buffer resource (32-bit data format) */
 constexpr int CPOL_SC1 = 16;         /* buffer load cache policy: agent scope (misses the L1) */
 constexpr int HD = 64;               /* head size */
 constexpr int KCH = 64;              /* keys of one attention sub-chunk (one per lane) */
-constexpr int APS_MAX = 8192;        /* floats of the staged attention partials */
+constexpr int KV_LDS = 2 * 64 * 64;  /* floats of one attention sub-chunk's keys and values in LDS */
 constexpr int APR = HD + 2;          /* one partial: max, sum, P.V[HD] */
 constexpr int PS_OFF = 1024;         /* attention: the waves' key probabilities in the staged-vector LDS, past q, k, v */
 constexpr float SPIN_SECONDS = 0.2f;
 constexpr unsigned long long PEEK_TICKS = 1000; /* 10 us at 100 MHz: from then on a wait reads sync_error */
 /* LDS of an instance running NB sequences (NB = 1 or 2): the staged input
- * vectors, NB x at most XS_SEQ floats for NB = 2, the block products of
- * NB vectors, and the attention merge weights (NB = 2: at most EW_B); at
- * most 80 KB, so that two instances share a CU */
-constexpr int EW_B = 1024;
+ * vectors, NB x at most XS_SEQ floats for NB = 2, and the block products
+ * of NB vectors; at most 80 KB, so that two instances share a CU */
 constexpr int XS_SEQ = 2048;
 template <int NB>
 struct PLds {
     static constexpr int XS = NB == 1 ? XS_MAX : NB * XS_SEQ;
     static constexpr int RED = P_MAX * PT * NB;
-    static constexpr int EW = NB == 1 ? XS_MAX / HD * DEC_PERSIST_NCH : EW_B;
 };
 
 /* threadIdx.x, opaque to the compiler: address arithmetic built on it is
@@ -132,7 +133,7 @@ __device__ __forceinline__ int tid() {
     return t;
 }
 
-static_assert(2 * KCH * HD <= APS_MAX, "the K and V sub-chunks share the partials' LDS");
+static_assert(2 * KCH * HD <= KV_LDS, "a sub-chunk's keys and values fit their LDS");
 static_assert(4 * HD + 2 * HD <= PS_OFF && PS_OFF + (PT / 64) * KCH <= XS_MAX, "q, k, v and the probabilities share xs");
 static_assert(APR % 2 == 0, "partials load as 16-byte pairs of exchanged values");
 static_assert(P_QKV <= P_MAX && P_O <= P_MAX && P_GU <= P_MAX && P_DN <= P_MAX, "pass caps");
@@ -419,13 +420,13 @@ __device__ __forceinline__ void norm_to_lds(const float (&v)[NB][NW], int C, con
     lds_barrier();
 }
 
-/* xs[j] = x_j from the loaded elements of NB vectors, C <= XR * PT. */
-template <int NB>
-__device__ __forceinline__ void vec_to_lds(const float (&v)[NB][XR], int C, float* xs) {
+/* xs[j] = x_j from the loaded elements of NB vectors, C <= N * PT. */
+template <int NB, int N>
+__device__ __forceinline__ void vec_to_lds(const float (&v)[NB][N], int C, float* xs) {
 #pragma unroll
     for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int k = 0; k < XR; k++) {
+        for (int k = 0; k < N; k++) {
             const int i = tid() + k * PT;
             if (i < C) xs[j * C + i] = v[j][k];
         }
@@ -641,66 +642,45 @@ __device__ __forceinline__ void attn_empty(const DecPersist& a, const Piece& p, 
     }
 }
 
-/* Attention output of every query head of the NB sequences from the
- * partials of its nch chunks (exchanged with epoch ep), staged into LDS with
- * one round of loads and polls (after_loads then issues more loads, once
- * the partials' registers are free): out[h][d] = sum_c e^(m_c - M) acc_c[d]
- * / sum_c e^(m_c - M) l_c, the weights e^(m_c - M) computed once per (head,
- * chunk) (ew); sequence j's heads at xs + j * NH * HD. */
-template <int NB, typename F>
-__device__ __forceinline__ void attn_merge(const DecPersist& a, int nch, const xv_t* apart, unsigned int ep, float* aps,
-                                           float* ew, float* xs, const Sync& sy, F&& after_loads) {
-    const int nh = NB * a.NH;                  /* heads of all NB sequences */
-    const int total2 = nh * nch * APR / 2;     /* 16-byte loads of two exchanged values */
-    /* agent-scope (sc1: miss the L1) loads through a buffer resource over the
-     * partials; past its end a buffer load returns 0 (such slots count as
-     * ready) */
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)apart, (short)0, total2 * 16, BUF_FLAGS);
-    constexpr int NL = APS_MAX / 2 / PT;
-    f4 v[NL];
-    auto load = [&](int k) {
-        v[k] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * (tid() + k * PT), 0, CPOL_SC1));
+/* This workgroup's share of the attention output of the NB sequences
+ * (elements [o0, o1) of NB x NH*HD, split evenly over the working
+ * workgroups), merged from the partials of its nch chunks (exchanged with
+ * epoch ep) by wave 0, one element per lane, and exchanged with epoch ep at
+ * att: out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c (chunks in
+ * order; e^(m_c - M) = 0 for a chunk without keys).  Lanes past the share
+ * load element o0's values and store nothing. */
+__device__ __forceinline__ void attn_merge_share(const DecPersist& a, int nb, int nch, int w, const xv_t* apart,
+                                                 xv_t* att, unsigned int ep, const Sync& sy) {
+    if (tid() >= 64) return;
+    constexpr int CM = DEC_PERSIST_NCH > DEC_PERSIST_NCH_B ? DEC_PERSIST_NCH : DEC_PERSIST_NCH_B;
+    const int tot = nb * a.QD;
+    const int o0 = (int)((long)tot * w / DEC_PERSIST_WGS), o1 = (int)((long)tot * (w + 1) / DEC_PERSIST_WGS);
+    const int i = o0 + tid(), ic = i < o1 ? i : o0;
+    const int sq = ic / a.QD, e = ic - sq * a.QD, h = e / HD, d = e - h * HD;
+    const xv_t* pr = apart + (size_t)(sq * a.NH + h) * nch * APR;
+    auto addr = [&](int k) {
+        const int c = min(k / 3, nch - 1), f = k - 3 * (k / 3);
+        return pr + c * APR + (f == 2 ? 2 + d : f);
     };
+    xv_t u[3 * CM];
 #pragma unroll
-    for (int k = 0; k < NL; k++) load(k);
-    poll_xv<NL>([&](int k) {
-                    return tid() + k * PT >= total2 ||
-                           (__float_as_uint(v[k].y) == ep && __float_as_uint(v[k].w) == ep);
-                },
-                load, sy);
+    for (int k = 0; k < 3 * CM; k++) u[k] = get_xv(addr(k));
+    poll_xv<3 * CM>([&](int k) { return (unsigned int)(u[k] >> 32) == ep; }, [&](int k) { u[k] = get_xv(addr(k)); },
+                    sy);
+    float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < NL; k++) {
-        const int i = tid() + k * PT;
-        if (i < total2) ((float2*)aps)[i] = make_float2(v[k].x, v[k].z);
-    }
-    issue_order();
-    after_loads();
-    lds_barrier();
-    /* ew[h][c] = e^(m_c - M_h), one thread per (head, chunk); 0 for a chunk
-     * without keys */
-    for (int i = tid(); i < nh * nch; i += PT) {
-        const int h = i / nch, c = i - h * nch;
-        const float* pr = aps + h * nch * APR;
-        float M = -INFINITY;
+    for (int c = 0; c < CM; c++)
+        if (c < nch) M = fmaxf(M, xv_val(u[3 * c]));
+    float L = 0.f, A = 0.f;
 #pragma unroll
-        for (int k = 0; k < nch; k++) M = fmaxf(M, pr[k * APR]);
-        const float m = pr[c * APR];
-        ew[i] = m == -INFINITY ? 0.f : expf(m - M);
-    }
-    lds_barrier();
-    for (int i = tid(); i < nh * HD; i += PT) {
-        const int h = i / HD, d = i - h * HD;
-        const float* pr = aps + h * nch * APR;
-        const float* e = ew + h * nch;
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int c = 0; c < nch; c++) {
-            L = fmaf(e[c], pr[c * APR + 1], L);
-            A = fmaf(e[c], pr[c * APR + 2 + d], A);
+    for (int c = 0; c < CM; c++)
+        if (c < nch) {
+            const float m = xv_val(u[3 * c]);
+            const float wc = m == -INFINITY ? 0.f : expf(m - M);
+            L = fmaf(wc, xv_val(u[3 * c + 1]), L);
+            A = fmaf(wc, xv_val(u[3 * c + 2]), A);
         }
-        xs[i] = A / L;
-    }
-    lds_barrier();
+    if (i < o1) put_xv(att + i, A / L, ep);
 }
 
 /* HW_REG_XCC_ID bits [3:0] (s_getreg_b32 hwreg(HW_REG_XCC_ID, 0, 4)): the
@@ -728,9 +708,8 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     }
     __shared__ __attribute__((aligned(16))) float xs[PLds<NB>::XS]; /* staged input vectors, or the attention's q, k, v */
     __shared__ __attribute__((aligned(16))) float red[PLds<NB>::RED];
-    __shared__ __attribute__((aligned(16))) float big[APS_MAX]; /* attention partials, or one K and V sub-chunk */
+    __shared__ __attribute__((aligned(16))) float big[KV_LDS]; /* one attention sub-chunk's keys and values */
     __shared__ float sh[NB * (PT / 64)];
-    __shared__ float ew[PLds<NB>::EW]; /* attention merge weights */
     __shared__ int bad; /* a wave of this workgroup timed out waiting for a value */
     DecState* st = a.st;
     const int pos = st->pos;
@@ -748,6 +727,7 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
     xv_t* hf = xf + NB * D;
     xv_t* qkvf = hf + NB * H;
     xv_t* apf = qkvf + NB * QKV;
+    xv_t* attf = apf + (size_t)NB * a.NH * nch * APR; /* the merged attention output */
     const unsigned int steps = __hip_atomic_load((const unsigned int*)a.ex, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const unsigned int ep0 = steps << 8;
     auto ep = [&](int l, int ph) { return ep0 + (unsigned int)(5 * l + ph); };
@@ -906,8 +886,16 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             if (live) attn_compute(a, pc, pos, rc, rs, ar, xs, big, apf, ep(l, 2));
             else if (has_piece) attn_empty(a, pc, apf, ep(l, 2));
         }
-        /* 3. merge + o + residual; gate/up weights stream in behind the partials */
-        attn_merge<NB>(a, nch, apf, ep(l, 2), big, ew, xs, sy, [&] { mv_fetch(sg, bg); });
+        /* 3. merge (this workgroup's share) + o + residual; gate/up weights
+         * stream in behind the merged output */
+        attn_merge_share(a, NB, nch, w, apf, attf, ep(l, 2), sy);
+        {
+            float v[NB][QR];
+            get_vec<NB>(attf, QD, ep(l, 2), v, sy);
+            issue_order();
+            mv_fetch(sg, bg);
+            vec_to_lds(v, QD, xs);
+        }
         if (bad) return;
         mv_finish<NB>(so, bo, xs, QD, red, xf, D, ep(l, 3), xres, nullptr);
         /* 4. RMSNorm + gate, up + SwiGLU; down's weights stream in behind x */
@@ -933,7 +921,7 @@ __global__ __launch_bounds__(PT) void k_dec_persist(DecPersist a) {
             fetch_qkv(q0, q1, q2, bq);
             fetch_norm(a.ln1 + (size_t)ln * D, nw);
             issue_order();
-            vec_to_lds<NB>(v, H, xs);
+            vec_to_lds(v, H, xs);
         }
         if (bad) return;
         mv_finish<NB>(sd, bd, xs, H, red, xf, D, ep(l, 5), xres, l == a.L - 1 ? a.x + (size_t)b0 * D : nullptr);
@@ -964,18 +952,21 @@ extern "C" int dec_persist_nch(int NKV, int NB) {
  *        DEC_PERSIST_WGS, so each needs at least DEC_PERSIST_WGS rows),
  *   (R2) every (sequence, KV head, key chunk) piece has a workgroup, which
  *        writes its partials every step (empty ones too), and
- *   (R3) phase 3 reads every piece's partials and phases 1, 4 and 5 read
- *        the whole of x or h in every workgroup (the kernel's code);
+ *   (R3) the merge shares of phase 3 together read every piece's partials,
+ *        every workgroup writes a share of the merged output and reads all
+ *        of it, and phases 1, 4 and 5 read the whole of x or h in every
+ *        workgroup (the kernel's code);
  * (R1) and (R2) are checked here.  Instances share nothing but the step
  * count and the error flag. */
 extern "C" int dec_persist_ok_b(int D, int H, int NH, int NKV, int HD_, int MS, int NB) {
     if (NB != 1 && NB != 2) return 0;
-    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT || MS <= 0)
+    if (HD_ != HD || NKV <= 0 || NH % NKV || NH / NKV > 4 || D % 32 || H % 32 || D > NW * PT || H > XR * PT ||
+        NH * HD > QR * PT || MS <= 0)
         return 0;
     const int nch = dec_persist_nch(NKV, NB);
     const int QD = NH * HD, KV = NKV * HD;
-    const int xs = NB == 1 ? XS_MAX : NB * XS_SEQ, ew = NB == 1 ? XS_MAX / HD * DEC_PERSIST_NCH : EW_B;
-    if (NB * QD > xs || NB * D > xs || NB * H > xs || NB * NH * nch * APR > APS_MAX || NB * NH * nch > ew) return 0;
+    const int xs = NB == 1 ? XS_MAX : NB * XS_SEQ;
+    if (NB * QD > xs || NB * D > xs || NB * H > xs) return 0;
     if (QD + 2 * KV < DEC_PERSIST_WGS || D < DEC_PERSIST_WGS || H < DEC_PERSIST_WGS) return 0; /* (R1) */
     if (nch < 1 || NB * NKV * nch > DEC_PERSIST_WGS) return 0;                               /* (R2) */
     auto passes = [](int rows_per_wg, int nb) { return nb > PT ? P_MAX + 1 : (rows_per_wg + PT / nb - 1) / (PT / nb); };

@@ -130,7 +130,8 @@ typedef struct {
  *   [3, 3 + NB D)         x, the residual stream after a phase, per sequence
  *   [.., + NB H)          h, the SwiGLU output
  *   [.., + NB (NH*HD + 2 KV))          q, k, v
- *   [.., + NB NH nch (HD+2))           the attention partials (max, sum, P.V[HD]) */
+ *   [.., + NB NH nch (HD+2))           the attention partials (max, sum, P.V[HD])
+ *   [.., + NB NH*HD)                   the attention output, merged from the partials */
 #define DEC_PERSIST_WGS 32
 #define DEC_PERSIST_NCH 10
 #ifndef DEC_PERSIST_NCH_B
@@ -139,7 +140,7 @@ typedef struct {
 #define DEC_PERSIST_MAX_L 50
 #define DEC_PERSIST_EX_HEAD 3 /* 8-byte words before x */
 #define DEC_PERSIST_EX_WORDS_NB(D, H, QD, KV, NH, HD, NB, NCH)                                                 \
-    (DEC_PERSIST_EX_HEAD + (size_t)(NB) * ((size_t)(D) + (H) + (QD) + 2 * (size_t)(KV) +                      \
+    (DEC_PERSIST_EX_HEAD + (size_t)(NB) * ((size_t)(D) + (H) + 2 * (size_t)(QD) + 2 * (size_t)(KV) +          \
                                            (size_t)(NH) * (NCH) * ((HD) + 2)))
 #define DEC_PERSIST_EX_WORDS(D, H, QD, KV, NH, HD) DEC_PERSIST_EX_WORDS_NB(D, H, QD, KV, NH, HD, 1, DEC_PERSIST_NCH)
 typedef struct {

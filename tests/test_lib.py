@@ -275,9 +275,9 @@ def test_persistent_batched_host_conditions():
     """dec_persist_ok_b / dec_persist_nch for NB sequences per instance (the
     batched persistent step): key chunks per (sequence, KV head) are the 32
     working workgroups shared out, capped at 10, so that (R2) every piece
-    has a workgroup; the staged vectors of both sequences and their
-    attention partials fit the kernel's LDS; NB other than 1 and 2 is
-    rejected.  The batch-1 form is NB = 1 (always 10 chunks, so a shape with
+    has a workgroup; the staged vectors of both sequences fit the kernel's
+    LDS and the attention output (at most 1024 elements) its per-thread
+    staging; NB other than 1 and 2 is rejected.  The batch-1 form is NB = 1 (always 10 chunks, so a shape with
     4 KV heads runs two per instance but not alone)."""
     L = bmhip.lib()
     wgs = 32
@@ -301,4 +301,4 @@ def test_persistent_batched_host_conditions():
                     nch = L.dec_persist_nch(NKV, 2)
                     if ok:
                         assert nch >= 1 and 2 * NKV * nch <= wgs, (D, H, NH, NKV)
-                        assert 2 * NH * nch * 66 <= 8192 and 2 * max(D, H, NH * 64) <= 4096
+                        assert NH * 64 <= 1024 and 2 * max(D, H, NH * 64) <= 4096
