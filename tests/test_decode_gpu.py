@@ -711,10 +711,12 @@ def test_persistent_step_long_context():
 
 
 # Batched persistent steps: instances of 32 workgroups, each on one XCD;
-# B <= 8 one sequence per instance and XCD, B = 16 one sequence per
-# instance with two instances per XCD, B = 32 two sequences per instance
-# (attention split into 5 key chunks per sequence at 135M, 10 otherwise).
-@pytest.mark.parametrize("B,n", [(2, 40), (8, 40), (16, 80), (32, 140)], ids=["b2", "b8", "b16", "b32"])
+# B <= 8 one sequence per instance and XCD, up to 16 one sequence per
+# instance with two instances per XCD (B = 12: four XCDs hold one), up to 32
+# two sequences per instance (B = 20: ten instances) (attention split into
+# 5 key chunks per sequence at 135M with two sequences, 10 otherwise).
+@pytest.mark.parametrize("B,n", [(2, 40), (8, 40), (12, 40), (16, 80), (20, 40), (32, 140)],
+                         ids=["b2", "b8", "b12", "b16", "b20", "b32"])
 def test_persistent_batched_matches_phase_kernels(B, n):
     """Batched SmolLM2-135M steps with every layer in one persistent launch
     against the same shape's per-phase kernels: every row's logits within
