@@ -94,8 +94,6 @@ __device__ __forceinline__ float rms_inv(const float* x, int C, float eps, float
     return 1.0f / sqrtf(ss / (float)C + eps);
 }
 
-__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
-
 /* Order-preserving packing of (value, index) for an atomicMax argmax in
  * which the larger value wins and, on equal values, the smaller index: the
  * result of the reference's scan 'if (v[i] > v[best]) best = i' from
@@ -311,6 +309,15 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
  * With st != NULL the workgroup's best (logit, index) goes into st->key[b]
  * by atomicMax, and the last workgroup to finish turns the keys into
  * tokens, emits them and advances the position. */
+/* atomicMax of a workgroup's best key, waited for: the returned value is
+ * consumed (into LDS) before the caller's next barrier, so the update has
+ * been performed before the workgroup's arrival is counted. */
+__device__ __forceinline__ void head_key_max(unsigned long long* key, unsigned long long v, int* sink) {
+    const unsigned long long old = atomicMax(key, v);
+    if (old == 0xffffffffffffffffull) *sink = 1;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST); /* the compiler keeps later accesses after the wait */
+}
+
 /* Last workgroup of a head launch (every workgroup calls this after its
  * atomicMax): emit the step's tokens and advance the position.
  *
@@ -326,8 +333,29 @@ __global__ __launch_bounds__(NT) void k_swiglu(const float* gate, const float* u
  * position) are read by later kernels, after the launch boundary. */
 __device__ void head_finish(const DecHead& a, int& last_wg) {
     const int t = threadIdx.x;
-    if (t == 0) {
-        const unsigned int prev = atomicAdd(&a.st->done, 1u);
+    unsigned int* top = a.arr ? &a.arr->cnt[HEAD_GROUPS][0] : &a.st->done;
+    if (a.arr) {
+        /* this workgroup's group, then the group's last arrival counts the
+         * group once (its keys folded into DecState.key, waited for before
+         * the barrier, so before that count) */
+        const unsigned int grp = blockIdx.x % HEAD_GROUPS, nwg = gridDim.x;
+        const unsigned int n_in = nwg / HEAD_GROUPS + (grp < nwg % HEAD_GROUPS ? 1u : 0u);
+        const unsigned int ngrp = nwg < HEAD_GROUPS ? nwg : HEAD_GROUPS;
+        if (t == 0) last_wg = atomicAdd(&a.arr->cnt[grp][0], 1u) == n_in - 1u;
+        __syncthreads();
+        if (!last_wg) return;
+        __syncthreads(); /* every thread has read last_wg */
+        for (int b = t; b < a.B; b += blockDim.x) {
+            const unsigned long long k = atomicExch(&a.arr->key[grp][b], 0ull); /* read and re-arm */
+            head_key_max(&a.st->key[b], k, &last_wg);
+        }
+        __syncthreads();
+        if (t == 0) {
+            atomicExch(&a.arr->cnt[grp][0], 0u);
+            last_wg = atomicAdd(top, 1u) == ngrp - 1u;
+        }
+    } else if (t == 0) {
+        const unsigned int prev = atomicAdd(top, 1u);
         last_wg = (prev == (unsigned int)a.tiles - 1u);
     }
     __syncthreads();
@@ -344,18 +372,15 @@ __device__ void head_finish(const DecHead& a, int& last_wg) {
     __syncthreads();
     if (t == 0) {
         if (emit) st->n_out = st->n_out + 1;
-        atomicExch(&st->done, 0u);
+        atomicExch(top, 0u);
         st->pos = pos + 1;
     }
 }
 
-/* atomicMax of a workgroup's best key, waited for: the returned value is
- * consumed (into LDS) before the caller's next barrier, so the update has
- * been performed before the workgroup's arrival is counted. */
-__device__ __forceinline__ void head_key_max(unsigned long long* key, unsigned long long v, int* sink) {
-    const unsigned long long old = atomicMax(key, v);
-    if (old == 0xffffffffffffffffull) *sink = 1;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST); /* the compiler keeps later accesses after the wait */
+/* Where a workgroup of a head launch folds its best key of batch row b:
+ * its group's key (two-level arrival), or DecState.key. */
+__device__ __forceinline__ unsigned long long* head_key(const DecHead& a, int b) {
+    return a.arr ? &a.arr->key[blockIdx.x % HEAD_GROUPS][b] : &a.st->key[b];
 }
 
 /* Weight formats of the LM head rows: fp32, Q8_0 blocks, and two 16-bit
@@ -491,7 +516,7 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
         }
         if (a.st) {
             best = block_argmax_key(best, shk);
-            if (t == 0) head_key_max(&a.st->key[b], best, &last_wg);
+            if (t == 0) head_key_max(head_key(a, b), best, &last_wg);
         } else {
             __syncthreads(); /* red[] is rewritten for the next row of the batch */
         }
@@ -638,7 +663,7 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
         unsigned long long best = shk[0][b];
 #pragma unroll
         for (int w = 1; w < 4; w++) best = shk[w][b] > best ? shk[w][b] : best;
-        head_key_max(&a.st->key[b], best, &last_wg);
+        head_key_max(head_key(a, b), best, &last_wg);
     }
     __syncthreads();
     head_finish(a, last_wg);
@@ -1492,24 +1517,11 @@ __global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
 
 /* ------------------------------------------------------------------ */
 /* Prefill (bm_forward on a whole prompt at position 0, batch 1): every
- * prompt position at once, the projections on the bf16-MFMA GEMM
- * (q8_gemm.hip), as the reference's prefill graph runs them on its BT > 1
- * Q8 path (graph.c:273-381, scheduler.c:1015-1332). */
-
-/* A prefill GEMM output element: the sum of its ks (<= GM_KSPLIT_MAX)
- * split-K slice copies, stride floats apart, added in slice order.  All
- * GM_KSPLIT_MAX loads are issued before the first add (copies past ks
- * re-read copy 0), so an element costs one memory round trip. */
-__device__ __forceinline__ float ld_slices(const float* __restrict__ p, size_t i, int ks, long stride) {
-    float v[GM_KSPLIT_MAX];
-#pragma unroll
-    for (int k = 0; k < GM_KSPLIT_MAX; k++) v[k] = p[i + (size_t)(k < ks ? k : 0) * stride];
-    float s = v[0];
-#pragma unroll
-    for (int k = 1; k < GM_KSPLIT_MAX; k++)
-        if (k < ks) s += v[k];
-    return s;
-}
+ * prompt position at once, the projections on the bf16-MFMA GEMMs of
+ * pf_gemm.hip, as the reference's prefill graph runs them on its BT > 1 Q8
+ * path (graph.c:273-381, scheduler.c:1015-1332).  The GEMMs' activations
+ * are bf16 in MFMA fragment order (frag_index): the RMSNorm and the
+ * attention write them so. */
 
 /* x[p] = emb[tok[p]] */
 __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, const float* __restrict__ emb,
@@ -1520,26 +1532,27 @@ __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, co
     for (int j = threadIdx.x; j < D; j += NT) xr[j] = er[j];
 }
 
-/* Row p: x += add (when add is given: the residual), then out = bf16 of
- * RMSNorm(x) * w, the activation of the next GEMM. */
-__global__ __launch_bounds__(NT) void k_pf_norm_bf16(float* __restrict__ x, const float* __restrict__ add,
-                                                     const float* __restrict__ w, unsigned short* __restrict__ out,
-                                                     int D, float eps, int ks, long stride) {
+/* Row p: out = bf16 of RMSNorm(x) * w in fragment order, the activation
+ * of the next GEMM (nks = ceil(D / 64); columns past D written as zeros). */
+__global__ __launch_bounds__(NT) void k_pf_norm_bf16(const float* __restrict__ x, const float* __restrict__ w,
+                                                     unsigned short* __restrict__ out, int D, int nks, float eps) {
     __shared__ float sh[4];
     const int p = blockIdx.x;
-    float* xr = x + (size_t)p * D;
+    const float* xr = x + (size_t)p * D;
     float ss = 0.0f;
-    for (int j = threadIdx.x; j < D; j += NT) {
-        float v = xr[j];
-        if (add) {
-            v += ld_slices(add, (size_t)p * D + j, ks, stride);
-            xr[j] = v;
-        }
-        ss = fmaf(v, v, ss);
-    }
+    for (int j = threadIdx.x; j < D; j += NT) ss = fmaf(xr[j], xr[j], ss);
     ss = block_sum(ss, sh);
     const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-    for (int j = threadIdx.x; j < D; j += NT) out[(size_t)p * D + j] = bf16_bits((xr[j] * inv) * w[j]);
+    /* eight consecutive columns per thread: one 16-byte store (D is a multiple of 32) */
+    for (int g = threadIdx.x; g < 8 * nks; g += NT) {
+        unsigned int v[4] = {0u, 0u, 0u, 0u};
+        if (8 * g < D)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                v[c] = (unsigned int)bf16_bits((xr[8 * g + 2 * c] * inv) * w[8 * g + 2 * c]) |
+                       ((unsigned int)bf16_bits((xr[8 * g + 2 * c + 1] * inv) * w[8 * g + 2 * c + 1]) << 16);
+        *(uint4*)(out + frag_index(p, 8 * g, nks)) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
 }
 
 /* RoPE of every position's k and the cache append of k and v (layer a.layer,
@@ -1555,13 +1568,13 @@ __global__ __launch_bounds__(NT) void k_pf_kv(DecAttn a, const float* __restrict
         const float ang = (float)p * a.inv_freq[t];
         const float c = cosf(ang), sn = sinf(ang);
         const size_t kr = (size_t)p * a.KV + kh * HD;
-        const float k0 = ld_slices(k, kr + t, a.pf_ks, a.pf_stride), k1 = ld_slices(k, kr + t + half, a.pf_ks, a.pf_stride);
+        const float k0 = k[kr + t], k1 = k[kr + t + half];
         float* kT = kc + (size_t)kh * HD * a.MS;
         kT[((size_t)(t >> 2) * a.MS + p) * 4 + (t & 3)] = k0 * c - k1 * sn;
         const int t2 = t + half;
         kT[((size_t)(t2 >> 2) * a.MS + p) * 4 + (t2 & 3)] = k0 * sn + k1 * c;
     }
-    for (int i = threadIdx.x; i < a.KV; i += NT) vc[(size_t)p * a.KV + i] = ld_slices(v, (size_t)p * a.KV + i, a.pf_ks, a.pf_stride);
+    for (int i = threadIdx.x; i < a.KV; i += NT) vc[(size_t)p * a.KV + i] = v[(size_t)p * a.KV + i];
 }
 
 /* Causal attention of every prompt position: workgroup (query head h,
@@ -1657,8 +1670,8 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
             const float ang = (float)pp * a.inv_freq[e];
             const float c = cosf(ang), sn = sinf(ang);
             const size_t qr = (size_t)pp * NH * HD + h * HD;
-            const float q0 = ld_slices(q, qr + e, a.pf_ks, a.pf_stride);
-            const float q1 = ld_slices(q, qr + e + HD / 2, a.pf_ks, a.pf_stride);
+            const float q0 = q[qr + e];
+            const float q1 = q[qr + e + HD / 2];
             Qs[r * HD + e] = q0 * c - q1 * sn;
             Qs[r * HD + e + HD / 2] = q0 * sn + q1 * c;
         }
@@ -1808,11 +1821,10 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
         f.out[off + 1] = o1 / den;
         f.out[off + 2] = o2 / den;
         f.out[off + 3] = o3 / den;
-    } else {
-        out16[off + 0] = bf16_bits(o0 / den);
-        out16[off + 1] = bf16_bits(o1 / den);
-        out16[off + 2] = bf16_bits(o2 / den);
-        out16[off + 3] = bf16_bits(o3 / den);
+    } else { /* the o projection's operand: fragment order, four consecutive values */
+        const uint2 o = make_uint2((unsigned int)bf16_bits(o0 / den) | ((unsigned int)bf16_bits(o1 / den) << 16),
+                                   (unsigned int)bf16_bits(o2 / den) | ((unsigned int)bf16_bits(o3 / den) << 16));
+        *(uint2*)(out16 + frag_index(p0 + r, h * HD + 4 * g, (NH * HD + 63) >> 6)) = o;
     }
 }
 
@@ -1857,13 +1869,6 @@ __global__ __launch_bounds__(NT) void k_attn_prefill_wave(PfFlat f, int HD) {
     float* oi = f.out + ((size_t)i * f.NH + h) * HD;
     if (d0) oi[lane] = a0 / l;
     if (d1) oi[lane + 64] = a1 / l;
-}
-
-/* out = bf16(silu(g) * u) */
-__global__ __launch_bounds__(NT) void k_pf_swiglu_bf16(const float* __restrict__ g, const float* __restrict__ u,
-                                                       unsigned short* __restrict__ out, long n, int ks, long stride) {
-    const long i = (long)blockIdx.x * NT + threadIdx.x;
-    if (i < n) out[i] = bf16_bits(silu_mul(ld_slices(g, (size_t)i, ks, stride), ld_slices(u, (size_t)i, ks, stride)));
 }
 
 } // namespace
@@ -2437,18 +2442,20 @@ extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, i
     return 0;
 }
 
-extern "C" int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
-                                int ks, long stride, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, add, w, out, D, eps, ks, stride);
+extern "C" int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps,
+                                hipStream_t s) {
+    BMK_REQUIRE(D % 32 == 0 && ((uintptr_t)out & 15) == 0, "prefill RMSNorm: D %d, output alignment", D);
+    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, w, out, D, (D + 63) / 64, eps);
     BMK_LAUNCH_CHECK();
     return 0;
 }
 
 /* RoPE + cache append of every position, then causal attention; the
- * result goes to out16 as bf16 (the o-projection's operand).  Head size
- * 64: blocks of PQB positions per workgroup, written as bf16 directly;
- * other head sizes: one workgroup per (head, position) into a->out (fp32),
- * then the cast. */
+ * result goes to out16 as bf16 in fragment order (the o-projection's
+ * operand).  Head size 64: blocks of PQB positions per workgroup, written
+ * as bf16 directly; other head sizes: one workgroup per (head, position)
+ * into a->out (fp32), then the fragment-order cast (which also zeroes the
+ * columns past NH * HD). */
 extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n,
                                 unsigned short* out16, hipStream_t s) {
     hipLaunchKernelGGL(k_pf_kv, dim3(n), dim3(NT), 0, s, *a, k, v);
@@ -2458,17 +2465,10 @@ extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k
         BMK_LAUNCH_CHECK();
         return 0;
     }
-    BMK_REQUIRE(a->pf_ks <= 1, "prefill attention: head size %d takes unsplit q/k/v", a->HD);
     const dim3 g(a->NH, n);
     if (a->HD == 128) hipLaunchKernelGGL(k_pf_attn<128>, g, dim3(NT), 0, s, *a, q, k, v);
     else hipLaunchKernelGGL(k_pf_attn<0>, g, dim3(NT), 0, s, *a, q, k, v);
     BMK_LAUNCH_CHECK();
-    return gm_cast_bf16(a->out, out16, (long)n * a->NH * a->HD, s);
+    return gm_cast_bf16_frag(a->out, out16, n, a->NH * a->HD, a->NH * a->HD, s);
 }
 
-extern "C" int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, int ks, long stride,
-                                  hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_swiglu_bf16, dim3((unsigned)((n + NT - 1) / NT)), dim3(NT), 0, s, g, u, out, n, ks, stride);
-    BMK_LAUNCH_CHECK();
-    return 0;
-}

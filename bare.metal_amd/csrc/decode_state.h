@@ -82,11 +82,22 @@ typedef struct {
     float inv_freq[DEC_MAX_HD / 2]; /* RoPE inverse frequency per rotary pair (host table) */
     float scale;
     int NH, NKV, HD, KV, MS, L, layer;
-    /* prefill: the q/k/v rows are the sum of pf_ks copies, pf_stride floats
-     * apart (split-K slices of the projection; 1 copy otherwise) */
-    int pf_ks;
-    long pf_stride;
 } DecAttn;
+
+/* Where the workgroups of an LM head launch meet: HEAD_GROUPS groups
+ * (workgroup w in group w % HEAD_GROUPS), each with its arrival counter on
+ * a 256-byte line of its own and its running argmax keys; the last arrival
+ * of a group folds the group's keys into DecState.key and counts the group
+ * at [HEAD_GROUPS].  Same-address device-scope atomics queue up where the
+ * XCDs meet (about 10 ns apart): one counter for all of a launch's 768
+ * workgroups cost 8 us, sixteen on separate lines under 1 us.  Zeroed when
+ * allocated; every counter and key is re-armed by the arrival that reads
+ * it. */
+#define HEAD_GROUPS 16
+typedef struct {
+    unsigned int cnt[HEAD_GROUPS + 1][64];
+    unsigned long long key[HEAD_GROUPS][DEC_MAX_B];
+} DecHeadArrive;
 
 /* Final RMSNorm + LM head + argmax.  Rows: Q8 when wq != NULL, else bf16
  * when wh != NULL, else fp32.  norm_w == NULL: no RMSNorm (a plain
@@ -104,6 +115,7 @@ typedef struct {
     int D, V, B, tiles;
     float eps;
     int wh_f16;          /* wh holds IEEE fp16 rows (the reference's fp16 precision) */
+    DecHeadArrive* arr;  /* the two-level arrival (with st), or NULL: every workgroup at DecState.key and .done */
 } DecHead;
 
 /* Every layer of a decode step in one persistent kernel

@@ -24,6 +24,7 @@
 #include "bmk.h"
 #include "decode_state.h"
 #include "q8_gemm.h"
+#include "pf_gemm.h"
 #include "bm_q8.h"
 #include "backend.h"
 #include "backend_hip_device.h"
@@ -46,12 +47,9 @@ int dec_launch_embed(const DecEmbed* a, hipStream_t s);
 int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
 int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
-int dec_pf_norm_bf16(float* x, const float* add, const float* w, unsigned short* out, int n, int D, float eps,
-                     int ks, long stride, hipStream_t s);
+int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps, hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
                      hipStream_t s);
-int dec_pf_swiglu_bf16(const float* g, const float* u, unsigned short* out, long n, int ks, long stride,
-                       hipStream_t s);
 int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
 int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
@@ -110,6 +108,9 @@ struct bm_model_s {
     unsigned short* d_headh; /* 16-bit head rows: bf16 (precision BF16) or fp16 (FP16), no q8_head */
     size_t off[7];           /* byte offset of each matrix inside one layer's slice */
     size_t layer_bytes;
+    unsigned char* d_pfw;    /* the same projections in the prefill GEMMs' load order (pf_gemm.h) */
+    size_t pf_off[7];        /* byte offset of each matrix inside one layer's slice of d_pfw */
+    size_t pf_layer_bytes;
     int nsessions;
 };
 
@@ -120,13 +121,9 @@ struct bm_session_s {
     float *x, *q, *k, *v, *att, *h, *logits, *kvc;
     /* prefill buffers, allocated on the first bm_forward over a prompt */
     int pf_cap;              /* rows they hold */
-    float *pf_x, *pf_qkv, *pf_att, *pf_o, *pf_gu;
-    unsigned short* pf_a16;  /* bf16 activations of the next GEMM */
-    int* pf_tok;
-    unsigned char* pf_plan;  /* device GEMM plans */
-    unsigned char* h_plan;   /* pinned staging of the plans */
-    size_t pf_plan_cap;
+    void* pf_buf[6];         /* x, q/k/v, attention output, the two bf16 GEMM operands, tokens */
     DecState* st;
+    DecHeadArrive* harr;  /* where the head's workgroups meet (zeroed once, re-armed by every launch) */
     int* prompt;
     int* out_tokens;
     int prompt_cap;
@@ -208,6 +205,15 @@ static void layer_layout(bm_model_t* m) {
         o += mats[i] / 32 * blk;
     }
     m->layer_bytes = o;
+    /* the prefill copy: every matrix a whole number of 2304- (1280-) byte chunks */
+    const int rows[7] = {m->QD, m->KV, m->KV, m->D, m->H, m->H, m->D};
+    const int cols[7] = {m->D, m->D, m->D, m->QD, m->D, m->D, m->H};
+    o = 0;
+    for (int i = 0; i < 7; i++) {
+        m->pf_off[i] = o;
+        o += pfg_wbytes(rows[i], cols[i], m->quant_bits == 4);
+    }
+    m->pf_layer_bytes = o;
 }
 
 extern "C" bm_model_t* bm_create_model(bm_context_t* ctx, const bm_arch_t* a) {
@@ -258,6 +264,8 @@ static void model_free_device(bm_model_t* m) {
     hipFree(m->d_headw);
     m->d_headw = NULL;
     hipFree(m->d_q8);
+    hipFree(m->d_pfw);
+    m->d_pfw = NULL;
     hipFree(m->d_head8);
     hipFree(m->d_headh);
     m->d_headh = NULL;
@@ -450,6 +458,15 @@ static int model_compile(bm_model_t* m) {
                 else rc = q4 ? q4_pack_f32(stage, dst, (long)per[i], s) : q8_pack_f32(stage, dst, (long)per[i], s);
             }
         }
+    /* the prefill's copy of the projections, in its GEMMs' load order */
+    if (rc == 0 && hipMalloc(&m->d_pfw, m->pf_layer_bytes * m->L) != hipSuccess) rc = -1;
+    for (int l = 0; l < m->L && rc == 0; l++)
+        for (int i = 0; i < 7 && rc == 0; i++) {
+            const int rows[7] = {QD, KV, KV, D, H, H, D}, cols[7] = {D, D, D, QD, D, D, H};
+            rc = pfg_repack(m->d_q8 + (size_t)l * m->layer_bytes + m->off[i],
+                            m->d_pfw + (size_t)l * m->pf_layer_bytes + m->pf_off[i], rows[i], cols[i],
+                            m->quant_bits == 4, s);
+        }
     if (rc == 0 && m->q8_head) {
         if (hipMalloc(&m->d_head8, q8_bytes((size_t)m->V * D)) != hipSuccess) rc = -1;
         else rc = q8_pack_f32(head_src, m->d_head8, (long)m->V * D, s);
@@ -590,7 +607,7 @@ static int enqueue_step(bm_session_t* S) {
     hd.wq = m->q8_head ? m->d_head8 : NULL;
     hd.wh = head_format(m) >= 2 ? m->d_headh : NULL;
     hd.wh_f16 = head_format(m) == 3;
-    hd.logits = S->logits; hd.st = S->st; hd.out_tokens = S->out_tokens;
+    hd.logits = S->logits; hd.st = S->st; hd.arr = S->harr; hd.out_tokens = S->out_tokens;
     hd.D = D; hd.V = m->V; hd.B = B; hd.eps = eps;
     hd.tiles = dec_head_tiles(D, m->V, head_format(m));
     if (dec_launch_head(&hd, s) || mark(S, PH_HEAD)) return -1;
@@ -604,10 +621,8 @@ static void session_free(bm_session_t* S) {
     hipFree(S->pex);
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
-    hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->prompt); hipFree(S->out_tokens);
-    hipFree(S->pf_x); hipFree(S->pf_qkv); hipFree(S->pf_att); hipFree(S->pf_o); hipFree(S->pf_gu);
-    hipFree(S->pf_a16); hipFree(S->pf_tok); hipFree(S->pf_plan);
-    if (S->h_plan) hipHostFree(S->h_plan);
+    hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->harr); hipFree(S->prompt); hipFree(S->out_tokens);
+    for (int i = 0; i < 6; i++) hipFree(S->pf_buf[i]);
     if (S->h_st) hipHostFree(S->h_st);
     if (S->h_logits) hipHostFree(S->h_logits);
     if (S->h_io) hipHostFree(S->h_io);
@@ -660,6 +675,8 @@ extern "C" bm_session_t* bm_create_session_batched(bm_context_t* ctx, bm_model_t
               hipMalloc(&S->att, B * m->QD * 4) == hipSuccess && hipMalloc(&S->h, B * m->H * 4) == hipSuccess &&
               hipMalloc(&S->logits, B * m->V * 4) == hipSuccess && hipMalloc(&S->kvc, kv_elems * 4) == hipSuccess &&
               hipMalloc(&S->st, sizeof(DecState)) == hipSuccess &&
+              hipMalloc(&S->harr, sizeof(DecHeadArrive)) == hipSuccess &&
+              hipMemsetAsync(S->harr, 0, sizeof(DecHeadArrive), ctx->s) == hipSuccess &&
               hipMalloc(&S->out_tokens, B * (size_t)S->MS * 4) == hipSuccess &&
               hipMalloc(&S->prompt, B * (size_t)S->MS * 4) == hipSuccess &&
 
@@ -898,192 +915,87 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
 /* ------------------------------------------------------------------ */
 /* prefill: a whole prompt at position 0 (reference session.c:86-139) */
 
-static int prefill_buffers(bm_session_t* S, int n) {
-    if (S->pf_cap >= n) return 0;
-    bm_model_t* m = S->m;
-    hipFree(S->pf_x); hipFree(S->pf_qkv); hipFree(S->pf_att); hipFree(S->pf_o); hipFree(S->pf_gu);
-    hipFree(S->pf_a16); hipFree(S->pf_tok);
-    S->pf_x = S->pf_qkv = S->pf_att = S->pf_o = S->pf_gu = NULL;
-    S->pf_a16 = NULL;
-    S->pf_tok = NULL;
-    S->pf_cap = 0;
-    const size_t N = (size_t)n;
-    const size_t widest = (size_t)std::max(std::max(m->D, m->H), m->QD);
-    if (hipMalloc(&S->pf_x, N * m->D * 4) != hipSuccess ||
-        hipMalloc(&S->pf_qkv, GM_KSPLIT_MAX * N * (m->QD + 2 * (size_t)m->KV) * 4) != hipSuccess ||
-        hipMalloc(&S->pf_att, N * m->QD * 4) != hipSuccess ||
-        hipMalloc(&S->pf_o, GM_KSPLIT_MAX * N * m->D * 4) != hipSuccess ||
-        hipMalloc(&S->pf_gu, GM_KSPLIT_MAX * N * 2 * (size_t)m->H * 4) != hipSuccess ||
-        hipMalloc(&S->pf_a16, N * widest * 2) != hipSuccess || hipMalloc(&S->pf_tok, N * 4) != hipSuccess) {
-        (void)hipGetLastError();
-        BMK_ERR("bm_forward: prefill buffers for %d tokens could not be allocated", n);
-        return -1;
-    }
-    S->pf_cap = n;
-    return 0;
-}
-
-/* One GEMM launch of the prefill: its plan's place in the plan buffer. */
-struct PfGemm {
-    size_t off;
-    int nprob, n_tiles, ks; /* ks: K slices, each writing its own copy of C */
-};
-
-/* The prefill's workspace: the residual stream, the split-K copies of each
- * GEMM output, the attention output, bf16 activations, tokens and GEMM plans
- * on the device, and the plans' host staging.  bm_forward keeps it in
- * session buffers allocated on the first prefill; bm_forward_noalloc carves
- * it from the library's static per-GPU array. */
+/* The prefill's workspace for n tokens: the residual stream x [n][D], the
+ * q/k/v rows, the attention output (fp32, head sizes other than 64), the
+ * bf16 GEMM operands in MFMA fragment order (rows rounded up to 32, columns
+ * to 64): a16 for the RMSNorm and attention outputs, h16 for the SwiGLU
+ * output, and the tokens.  bm_forward keeps it in session buffers allocated
+ * on the first prefill; bm_forward_noalloc carves it from the library's
+ * static per-GPU array. */
 struct PfWork {
-    float *x, *qkv, *att, *o, *gu;
-    unsigned short* a16;
+    float *x, *qkv, *att;
+    unsigned short *a16, *h16;
     int* tok;
-    unsigned char* plan;   /* device plans */
-    unsigned char* h_plan; /* host staging of the plans */
-    size_t plan_cap;       /* bytes of plan and h_plan */
 };
 
-#define PF_MAX_LAYERS 256
+#define PF_PARTS 6
 
-/* Prefill GEMM launches with fewer C tiles than this are split along K (at
- * most GM_KSPLIT_MAX slices): a per-layer launch at prompt lengths of a few
- * hundred tokens has tens of 128x128 tiles, and a tile's K loop takes about
- * 0.7 us per 64-wide step on its own CU, whatever the cache state.  Each
- * slice writes its own copy of C; the kernels that read the output add the
- * copies in slice order, so no reduction launch is needed. */
-#define PF_SPLIT_TARGET 256
-
-/* Sizes (g == NULL) or appends the plan of one multi-GEMM launch to the
- * staging buffer; kmax = 1 keeps the launch whole. */
-static int pf_plan(const PfWork* w, size_t* used, PfGemm* g, int nprob, const uint64_t* a_off, const uint64_t* w_off,
-                   const uint64_t* c_off, const int* M, const int* N, const int* K, const int* lda, const int* ldc,
-                   int kmax) {
-    int nt = 0, ks = 1;
-    const long need = gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, NULL, 0,
-                                    &nt, &ks);
-    if (need < 0) return -1;
-    const size_t at = (*used + 7) & ~(size_t)7;
-    if (g) {
-        if (at + (size_t)need > w->plan_cap) return -1;
-        if (gm_plan_split(nprob, a_off, w_off, c_off, M, N, K, lda, ldc, PF_SPLIT_TARGET, kmax, w->h_plan + at,
-                          (size_t)need, &nt, &ks) != need)
-            return -1;
-        g->off = at;
-        g->nprob = nprob;
-        g->n_tiles = nt;
-        g->ks = ks;
-    }
-    *used = at + (size_t)need;
-    return 0;
-}
-
-/* Device bytes of the workspace for n tokens, and each part's offset (in
- * bytes, 256-aligned) when off != NULL: x, qkv, att, o, gu, a16, tok. */
-static size_t pf_work_layout(const bm_model_t* m, int n, size_t off[7]) {
-    const size_t N = (size_t)n;
-    const size_t widest = (size_t)std::max(std::max(m->D, m->H), m->QD);
-    const size_t sz[7] = {N * m->D * 4, GM_KSPLIT_MAX * N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4,
-                          GM_KSPLIT_MAX * N * m->D * 4, GM_KSPLIT_MAX * N * 2 * (size_t)m->H * 4, N * widest * 2,
-                          N * 4};
+/* Device bytes of each part for n tokens (sz), and their offsets in one
+ * 256-aligned carve (off, when given); returns the total. */
+static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], size_t off[PF_PARTS]) {
+    const size_t N = (size_t)n, N32 = (N + 31) / 32 * 32;
+    const size_t a_cols = ((size_t)std::max(m->D, m->QD) + 63) / 64 * 64, h_cols = ((size_t)m->H + 63) / 64 * 64;
+    const size_t b[PF_PARTS] = {N * m->D * 4, N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4, N32 * a_cols * 2,
+                                N32 * h_cols * 2, N * 4};
     size_t at = 0;
-    for (int i = 0; i < 7; i++) {
+    for (int i = 0; i < PF_PARTS; i++) {
+        if (sz) sz[i] = b[i];
         if (off) off[i] = at;
-        at += (sz[i] + 255) & ~(size_t)255;
+        at += (b[i] + 255) & ~(size_t)255;
     }
     return at;
 }
 
-/* The GEMM plans of the whole prefill, per layer q/k/v, o, gate/up, down:
- * with g == NULL only sized (*used), else written to w->h_plan. */
-static int pf_plans(const bm_model_t* m, const PfWork* w, int n, PfGemm* g, size_t* used) {
-    const int D = m->D, H = m->H, QD = m->QD, KV = m->KV, L = m->L;
-    const uint64_t nn = (uint64_t)n;
-    /* q/k/v stay whole when the attention cannot read split copies (head size other than 64) */
-    const int kq = m->HD == 64 ? GM_KSPLIT_MAX : 1;
-    *used = 0;
-    for (int l = 0; l < L; l++) {
-        const uint64_t lw = (uint64_t)l * m->layer_bytes;
-        {
-            const uint64_t a[3] = {0, 0, 0}, wo[3] = {lw + m->off[0], lw + m->off[1], lw + m->off[2]};
-            const uint64_t c[3] = {0, nn * QD, nn * QD + nn * KV};
-            const int M[3] = {n, n, n}, N[3] = {QD, KV, KV}, K[3] = {D, D, D}, lda[3] = {D, D, D};
-            if (pf_plan(w, used, g ? &g[4 * l + 0] : NULL, 3, a, wo, c, M, N, K, lda, N, kq)) return -1;
-        }
-        {
-            const uint64_t a = 0, wo = lw + m->off[3], c = 0;
-            const int M = n, N = D, K = QD;
-            if (pf_plan(w, used, g ? &g[4 * l + 1] : NULL, 1, &a, &wo, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
-                return -1;
-        }
-        {
-            const uint64_t a[2] = {0, 0}, wo[2] = {lw + m->off[4], lw + m->off[5]}, c[2] = {0, nn * H};
-            const int M[2] = {n, n}, N[2] = {H, H}, K[2] = {D, D};
-            if (pf_plan(w, used, g ? &g[4 * l + 2] : NULL, 2, a, wo, c, M, N, K, K, N, GM_KSPLIT_MAX)) return -1;
-        }
-        {
-            const uint64_t a = 0, wo = lw + m->off[6], c = 0;
-            const int M = n, N = D, K = H;
-            if (pf_plan(w, used, g ? &g[4 * l + 3] : NULL, 1, &a, &wo, &c, &M, &N, &K, &K, &N, GM_KSPLIT_MAX))
-                return -1;
-        }
-    }
-    return 0;
+static void pf_work_set(PfWork* w, void* const part[PF_PARTS]) {
+    w->x = (float*)part[0]; w->qkv = (float*)part[1]; w->att = (float*)part[2];
+    w->a16 = (unsigned short*)part[3]; w->h16 = (unsigned short*)part[4]; w->tok = (int*)part[5];
 }
 
-/* bm_forward's workspace: session buffers, grown to n tokens and plan_bytes. */
-static int pf_session_work(bm_session_t* S, int n, size_t plan_bytes, PfWork* w) {
-    if (prefill_buffers(S, n)) return -1;
-    if (S->pf_plan_cap < plan_bytes) {
-        hipFree(S->pf_plan);
-        if (S->h_plan) hipHostFree(S->h_plan);
-        S->pf_plan = NULL;
-        S->h_plan = NULL;
-        S->pf_plan_cap = 0;
-        if (hipMalloc(&S->pf_plan, plan_bytes) != hipSuccess ||
-            hipHostMalloc(&S->h_plan, plan_bytes, hipHostMallocDefault) != hipSuccess) {
-            (void)hipGetLastError();
-            BMK_ERR("bm_forward: prefill plan buffers could not be allocated");
-            return -1;
+/* bm_forward's workspace: session buffers, grown to n tokens. */
+static int pf_session_work(bm_session_t* S, int n, PfWork* w) {
+    if (S->pf_cap < n) {
+        for (int i = 0; i < PF_PARTS; i++) {
+            hipFree(S->pf_buf[i]);
+            S->pf_buf[i] = NULL;
         }
-        S->pf_plan_cap = plan_bytes;
+        S->pf_cap = 0;
+        size_t sz[PF_PARTS];
+        pf_work_layout(S->m, n, sz, NULL);
+        for (int i = 0; i < PF_PARTS; i++)
+            if (hipMalloc(&S->pf_buf[i], sz[i]) != hipSuccess) {
+                (void)hipGetLastError();
+                BMK_ERR("bm_forward: prefill buffers for %d tokens could not be allocated", n);
+                return -1;
+            }
+        S->pf_cap = n;
     }
-    w->x = S->pf_x; w->qkv = S->pf_qkv; w->att = S->pf_att; w->o = S->pf_o; w->gu = S->pf_gu;
-    w->a16 = S->pf_a16; w->tok = S->pf_tok;
-    w->plan = S->pf_plan; w->h_plan = S->h_plan; w->plan_cap = S->pf_plan_cap;
+    pf_work_set(w, S->pf_buf);
     return 0;
 }
 
 extern "C" void* bmk_noalloc_scratch(int device);
 
-/* Host staging of bm_forward_noalloc's plans (static: no allocation at call
- * time).  It is one buffer for the process and each GPU's device array is
- * shared by every call on that GPU, so s_noalloc_mu serializes the calls:
- * it is held from the workspace carve through the plan upload to the final
- * synchronization on the logits read. */
-#define PF_NOALLOC_PLAN_BYTES (1u << 20)
-alignas(64) static unsigned char s_noalloc_h_plan[PF_NOALLOC_PLAN_BYTES];
+/* Each GPU's static array is shared by every bm_forward_noalloc call on that
+ * GPU, so s_noalloc_mu serializes the calls: it is held from the workspace
+ * carve to the final synchronization on the logits read. */
 static std::mutex s_noalloc_mu;
 
-/* bm_forward_noalloc's workspace: carved from the GPU's static array, the
- * plans last; -1 (logged) when n tokens do not fit. */
-static int pf_noalloc_work(bm_session_t* S, int n, size_t plan_bytes, PfWork* w) {
+/* bm_forward_noalloc's workspace: carved from the GPU's static array; -1
+ * (logged) when n tokens do not fit. */
+static int pf_noalloc_work(bm_session_t* S, int n, PfWork* w) {
     const int dev = (int)(intptr_t)S->ctx->be->device;
     unsigned char* base = (unsigned char*)bmk_noalloc_scratch(dev);
     if (!base) return -1;
-    size_t off[7];
-    const size_t act = pf_work_layout(S->m, n, off);
-    if (plan_bytes > PF_NOALLOC_PLAN_BYTES || act + plan_bytes > BM_NOALLOC_SCRATCH_BYTES) {
-        BMK_ERR("bm_forward_noalloc: %d tokens need %zu workspace bytes (+%zu of plans), the static array holds %u "
-                "(plans at most %u)",
-                n, act, plan_bytes, (unsigned)BM_NOALLOC_SCRATCH_BYTES, (unsigned)PF_NOALLOC_PLAN_BYTES);
+    size_t off[PF_PARTS];
+    const size_t act = pf_work_layout(S->m, n, NULL, off);
+    if (act > BM_NOALLOC_SCRATCH_BYTES) {
+        BMK_ERR("bm_forward_noalloc: %d tokens need %zu workspace bytes, the static array holds %u", n, act,
+                (unsigned)BM_NOALLOC_SCRATCH_BYTES);
         return -1;
     }
-    w->x = (float*)(base + off[0]); w->qkv = (float*)(base + off[1]); w->att = (float*)(base + off[2]);
-    w->o = (float*)(base + off[3]); w->gu = (float*)(base + off[4]);
-    w->a16 = (unsigned short*)(base + off[5]); w->tok = (int*)(base + off[6]);
-    w->plan = base + act;
-    w->h_plan = s_noalloc_h_plan;
-    w->plan_cap = plan_bytes;
+    void* part[PF_PARTS];
+    for (int i = 0; i < PF_PARTS; i++) part[i] = base + off[i];
+    pf_work_set(w, part);
     return 0;
 }
 
@@ -1097,25 +1009,11 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
             BMK_ERR("bm_forward: token %d outside [0, %d)", tokens[i], m->V);
             return -1;
         }
-    if (L > PF_MAX_LAYERS) {
-        BMK_ERR("bm_forward: %d layers, the prefill handles at most %d", L, PF_MAX_LAYERS);
-        return -1;
-    }
-    /* a first pass sizes the plans, the second writes them */
-    PfGemm g[4 * PF_MAX_LAYERS];
     PfWork w;
-    memset(&w, 0, sizeof w);
-    size_t used = 0;
-    if (pf_plans(m, &w, n, NULL, &used)) {
-        BMK_ERR("bm_forward: prefill GEMM plans rejected (%d tokens)", n);
-        return -1;
-    }
-    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the staging buffers may still be read */
-    if ((noalloc ? pf_noalloc_work(S, n, used + 64, &w) : pf_session_work(S, n, used + 64, &w)) != 0) return -1;
-    if (pf_plans(m, &w, n, g, &used)) return -1;
+    HIP_TRY(hipStreamSynchronize(s), "sync", return -1); /* the token staging buffer may still be read */
+    if ((noalloc ? pf_noalloc_work(S, n, &w) : pf_session_work(S, n, &w)) != 0) return -1;
     memcpy(S->h_io, tokens, (size_t)n * 4);
     HIP_TRY(hipMemcpyAsync(w.tok, S->h_io, (size_t)n * 4, hipMemcpyHostToDevice, s), "token write", return -1);
-    HIP_TRY(hipMemcpyAsync(w.plan, w.h_plan, used, hipMemcpyHostToDevice, s), "plan write", return -1);
 
     DecAttn at;
     memset(&at, 0, sizeof at);
@@ -1131,37 +1029,39 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
     float* q = w.qkv;
     float* k = q + (size_t)n * QD;
     float* v = k + (size_t)n * KV;
-    float* gt = w.gu;
-    float* up = gt + (size_t)n * H;
-    /* floats between the split-K copies of each GEMM output */
-    const long st_qkv = (long)n * (QD + 2 * KV), st_o = (long)n * D, st_gu = (long)n * 2 * H;
-    auto gemm = [&](const PfGemm& p, float* C, long stride) {
-        return gm_launch_split_qf(w.a16, 1, m->quant_bits == 4, m->d_q8, C, w.plan + p.off, p.nprob,
-                                  p.n_tiles, (size_t)stride, s);
-    };
+    const int qf = m->quant_bits == 4;
     if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, s)) return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
-        at.pf_ks = g[4 * l + 0].ks;
-        at.pf_stride = st_qkv;
-        const int ks_down = l ? g[4 * l - 1].ks : 1;
-        /* residual of the previous layer's down projection, RMSNorm, q/k/v */
-        if (dec_pf_norm_bf16(w.x, l ? w.o : NULL, m->d_ln1 + (size_t)l * D, w.a16, n, D, eps, ks_down,
-                             st_o, s) ||
-            gemm(g[4 * l + 0], w.qkv, st_qkv) ||
-            /* RoPE, cache append, causal attention */
+        const uint64_t lw = (uint64_t)l * m->pf_layer_bytes;
+        PfgArgs qkv, o, gu, dn;
+        memset(&qkv, 0, sizeof qkv);
+        qkv.A = w.a16; qkv.W = m->d_pfw; qkv.M = n; qkv.K = D; qkv.nprob = 3;
+        qkv.p[0].w_off = lw + m->pf_off[0]; qkv.p[0].C = q; qkv.p[0].N = QD; qkv.p[0].ldc = QD;
+        qkv.p[1].w_off = lw + m->pf_off[1]; qkv.p[1].C = k; qkv.p[1].N = KV; qkv.p[1].ldc = KV;
+        qkv.p[2].w_off = lw + m->pf_off[2]; qkv.p[2].C = v; qkv.p[2].N = KV; qkv.p[2].ldc = KV;
+        memset(&o, 0, sizeof o);
+        o.A = w.a16; o.W = m->d_pfw; o.x = w.x; o.M = n; o.K = QD; o.nprob = 1;
+        o.p[0].w_off = lw + m->pf_off[3]; o.p[0].N = D; o.p[0].ldc = D;
+        memset(&gu, 0, sizeof gu);
+        gu.A = w.a16; gu.W = m->d_pfw; gu.h = w.h16; gu.M = n; gu.K = D; gu.nprob = 2;
+        gu.p[0].w_off = lw + m->pf_off[4]; gu.p[0].N = H;
+        gu.p[1].w_off = lw + m->pf_off[5]; gu.p[1].N = H;
+        memset(&dn, 0, sizeof dn);
+        dn.A = w.h16; dn.W = m->d_pfw; dn.x = w.x; dn.M = n; dn.K = H; dn.nprob = 1;
+        dn.p[0].w_off = lw + m->pf_off[6]; dn.p[0].N = D; dn.p[0].ldc = D;
+        /* RMSNorm, q/k/v; RoPE, cache append, causal attention; o + residual;
+         * RMSNorm, gate/up + SwiGLU; down + residual */
+        if (dec_pf_norm_bf16(w.x, m->d_ln1 + (size_t)l * D, w.a16, n, D, eps, s) ||
+            pfg_launch(&qkv, qf, PFG_STORE, s) ||
             dec_pf_attention(&at, q, k, v, n, w.a16, s) ||
-            /* o, residual, RMSNorm, gate/up, SwiGLU, down */
-            gemm(g[4 * l + 1], w.o, st_o) ||
-            dec_pf_norm_bf16(w.x, w.o, m->d_ln2 + (size_t)l * D, w.a16, n, D, eps, g[4 * l + 1].ks, st_o,
-                             s) ||
-            gemm(g[4 * l + 2], w.gu, st_gu) ||
-            dec_pf_swiglu_bf16(gt, up, w.a16, (long)n * H, g[4 * l + 2].ks, st_gu, s) ||
-            gemm(g[4 * l + 3], w.o, st_o))
+            pfg_launch(&o, qf, PFG_RESID, s) ||
+            dec_pf_norm_bf16(w.x, m->d_ln2 + (size_t)l * D, w.a16, n, D, eps, s) ||
+            pfg_launch(&gu, qf, PFG_SWIGLU, s) ||
+            pfg_launch(&dn, qf, PFG_RESID, s))
             return -1;
     }
-    /* last residual (the bf16 output is not used), then the head on the last position */
-    if (dec_pf_norm_bf16(w.x, w.o, m->d_lnf, w.a16, n, D, eps, g[4 * L - 1].ks, st_o, s)) return -1;
+    /* the head on the last position (its own final RMSNorm) */
     DecHead hd;
     memset(&hd, 0, sizeof hd);
     hd.x = w.x + (size_t)(n - 1) * D; hd.norm_w = m->d_lnf; hd.w = m->d_headw ? m->d_headw : m->d_emb;

@@ -137,6 +137,21 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+/* Index of A[row][col] in MFMA fragment order, the activation layout the
+ * prefill GEMMs load (q8_gemm.hip's gemm_tile_frag, pf_gemm.hip): 32-row
+ * blocks rb and 64-column steps ks of four 16-deep fragments of 512 values;
+ * fragment (rb, ks, s) starts at ((rb * nks + ks) * 4 + s) * 512 and lane
+ * l's eight values at + 8 l hold A[32 rb + l % 32][64 ks + 32 (l / 32) +
+ * 8 s + j], j < 8 (nks = ceil(K / 64)).  Eight consecutive columns from a
+ * multiple of 8 are eight consecutive values. */
+__host__ __device__ __forceinline__ size_t frag_index(int row, int col, int nks) {
+    const int rb = row >> 5, lr = row & 31, ks = col >> 6, h = (col >> 5) & 1, s = (col >> 3) & 3;
+    return ((size_t)(rb * nks + ks) * 4 + s) * 512 + 8 * (lr + 32 * h) + (col & 7);
+}
+
+/* silu(g) * u, the SwiGLU product (reference forward.metal:1179-1190) */
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
 } // namespace bmk
 
 #endif

@@ -51,6 +51,8 @@ int gm_tiles_for(int M, int N);
 int gm_tiles_frag(int M, int N);
 /* dst = bf16(src), round to nearest even, n elements */
 int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
+/* src fp32 [M][lda] -> dst bf16 [M][K] in MFMA fragment order (frag_index), padding zeroed */
+int gm_cast_bf16_frag(const float* src, unsigned short* dst, int M, int K, int lda, hipStream_t s);
 int gm_launch_group(GmGroup* g, hipStream_t s);
 int gm_launch_group_qf(GmGroup* g, int qf, hipStream_t s);
 /* Plans with split-K for launches with few C tiles (q8_plan.cpp):

@@ -779,22 +779,28 @@ extern "C" int bmk_launch_cast_bf16(const bmk_launch_t* a) {
  * the activations of a matmul_forward_q8_multi problem with layout 2 (the
  * destination holds ceil(M/32) x ceil(K/64) x 2048 values, padding zeroed;
  * the problem's lda is K rounded up to 64). */
-extern "C" int bmk_launch_cast_bf16_frag(const bmk_launch_t* a) {
-    BMK_NEED_BYTES(a, 2, 12, "params");
-    const int M = bmk_pi(a, 2, 0), K = bmk_pi(a, 2, 1), lda = bmk_pi(a, 2, 2);
+extern "C" int gm_cast_bf16_frag(const float* src, unsigned short* dst, int M, int K, int lda, hipStream_t s) {
     BMK_REQUIRE(M > 0 && K > 0 && K % 32 == 0 && lda >= K, "cast_f32_bf16_frag: bad params M=%d K=%d lda=%d", M, K,
                 lda);
     const long nrb = (M + 31) / 32, nks = (K + 63) / 64;
     const long nslots = nrb * nks * 256; /* 16-byte slots: 4 fragments x 64 lanes per (block, step) */
     BMK_REQUIRE(nrb * 32 * nks * 64 < 0x80000000L, "cast_f32_bf16_frag: %d x %d is too large", M, K);
-    BMK_NEED_BYTES(a, 0, ((size_t)(M - 1) * lda + K) * 4, "src");
-    BMK_NEED_BYTES(a, 1, (size_t)nslots * 16, "dst");
-    BMK_REQUIRE(((uintptr_t)a->dev[0] & 3) == 0 && ((uintptr_t)a->dev[1] & 15) == 0,
+    BMK_REQUIRE(((uintptr_t)src & 3) == 0 && ((uintptr_t)dst & 15) == 0,
                 "cast_f32_bf16_frag: src must be 4-byte and dst 16-byte aligned");
-    hipLaunchKernelGGL(k_cast_bf16_frag, dim3((unsigned)((nslots + NTH - 1) / NTH)), dim3(NTH), 0, a->stream,
-                       (const float*)a->dev[0], (unsigned short*)a->dev[1], M, K, lda, (int)nks, nslots);
+    hipLaunchKernelGGL(k_cast_bf16_frag, dim3((unsigned)((nslots + NTH - 1) / NTH)), dim3(NTH), 0, s, src, dst, M, K,
+                       lda, (int)nks, nslots);
     BMK_LAUNCH_CHECK();
     return 0;
+}
+
+extern "C" int bmk_launch_cast_bf16_frag(const bmk_launch_t* a) {
+    BMK_NEED_BYTES(a, 2, 12, "params");
+    const int M = bmk_pi(a, 2, 0), K = bmk_pi(a, 2, 1), lda = bmk_pi(a, 2, 2);
+    BMK_REQUIRE(M > 0 && K > 0 && K % 32 == 0 && lda >= K, "cast_f32_bf16_frag: bad params M=%d K=%d lda=%d", M, K,
+                lda);
+    BMK_NEED_BYTES(a, 0, ((size_t)(M - 1) * lda + K) * 4, "src");
+    BMK_NEED_BYTES(a, 1, (size_t)((M + 31) / 32) * ((K + 63) / 64) * 256 * 16, "dst");
+    return gm_cast_bf16_frag((const float*)a->dev[0], (unsigned short*)a->dev[1], M, K, lda, a->stream);
 }
 
 /* Multi-GEMM launch from a device-resident plan built by bm_q8_gemm_plan

@@ -2,7 +2,7 @@
 """bm_forward_noalloc (include/baremetal.h): the one-pass prefill whose
 workspace lives in the library's static per-GPU array.  Through the C ABI,
 against bm_forward on an identical session: the same logits bit for bit
-(same kernels, same plans), the same KV cache (the next step's logits equal
+(the same kernels on the same inputs), the same KV cache (the next step's logits equal
 too), on two calls in a row with the second prompt shorter than the first,
 so the array still holds the first call's data; the device's free memory
 (hipMemGetInfo) is the same before and after every call, while the same
@@ -50,9 +50,9 @@ def test_noalloc_prefill_equals_bm_forward(dims, lens):
             want = ref.forward(toks)
             free1 = _device_free_bytes()
             if dims is bmhip.SMOLLM2_135M and n == lens[0]:
-                # bm_forward's first prefill allocates its workspace (about 82 KB
+                # bm_forward's first prefill allocates its workspace (about 12.7 KB
                 # a token here): the same check sees it
-                assert free0 - free1 >= 40_000 * n, (free0, free1)
+                assert free0 - free1 >= 10_000 * n, (free0, free1)
             got = na.forward_noalloc(toks)
             assert _device_free_bytes() == free1, n
             assert got is not None
@@ -66,10 +66,10 @@ def test_noalloc_prefill_equals_bm_forward(dims, lens):
 
 def test_noalloc_prefill_rejects():
     dims = bmhip.SMOLLM2_135M
-    eng = bmhip.Engine(dims, max_seq_len=1024, seed=5, graph=False)
+    eng = bmhip.Engine(dims, max_seq_len=6016, seed=5, graph=False)
     try:
-        # about 82 KB of workspace per token at these shapes: 1000 tokens exceed 64 MiB
-        assert eng.forward_noalloc(bmhip.synth_uniform_int(1, 0, dims["V"], 1000)) is None
+        # about 12.7 KB of workspace per token at these shapes: 6000 tokens exceed 64 MiB
+        assert eng.forward_noalloc(bmhip.synth_uniform_int(1, 0, dims["V"], 6000)) is None
         assert eng.forward_noalloc(np.array([3], np.int32)) is None  # one token: not a prefill
         toks = bmhip.synth_uniform_int(2, 0, dims["V"], 64)
         assert eng.forward_noalloc(toks) is not None
