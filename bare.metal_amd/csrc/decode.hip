@@ -1705,18 +1705,24 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
     }
     /* Chunk staging: each thread moves SPT float4 of K (element i: dims
      * 4*(i / PKC), key i % PKC, so a wave reads consecutive keys of one
-     * cache row) and of V (key i / HD4, dims 4*(i % HD4): whole V rows).
+     * cache row) and of V (element i = 64 w + l: keys 16 (w % 4) + l % 16,
+     * dims 4 (4 (w / 4) + l / 16): a wave instruction covers 16 keys x 16
+     * dims, so its transposed writes into Vt fall in distinct banks; with
+     * whole rows per instruction they conflicted 8 ways, 0.7 us per chunk).
      * The loads of chunk c+1 are issued into registers before chunk c is
      * computed, unconditionally (key clamped to n-1; keys at or past n
      * become zeros when written to LDS). */
     constexpr int SPT = PKC * HD4 / PNT;
+    static_assert(HD4 == 16 && PKC % 16 == 0, "V staging map: 16 dim groups, 16-key runs");
+    auto vkey = [](int i) { return 16 * ((i >> 6) % (PKC / 16)) + (i & 15); };
+    auto vgrp = [](int i) { return 4 * ((i >> 6) / (PKC / 16)) + ((i & 63) >> 4); };
     float4 kreg[SPT], vreg[SPT];
     auto fetch = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < SPT; u++) {
             const int i = t + PNT * u;
             const int kk = min(c0 + i % PKC, n - 1), kg = i / PKC;
-            const int vk = min(c0 + i / HD4, n - 1), vg = i % HD4;
+            const int vk = min(c0 + vkey(i), n - 1), vg = vgrp(i);
             __builtin_memcpy(&kreg[u], __builtin_assume_aligned(ksrc + (size_t)kk * kstr + kg * kgstr, 16), 16);
             __builtin_memcpy(&vreg[u], __builtin_assume_aligned(vsrc + (size_t)vk * vstr + 4 * vg, 16), 16);
         }
@@ -1728,7 +1734,7 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
 #pragma unroll
         for (int u = 0; u < SPT; u++) {
             const int i = t + PNT * u;
-            const int kk = i % PKC, kg = i / PKC, vk = i / HD4, vg = i % HD4;
+            const int kk = i % PKC, kg = i / PKC, vk = vkey(i), vg = vgrp(i);
             const bool kin = c0 + kk < n, vin = c0 + vk < n;
             const float4 kv = kreg[u], vv = vreg[u];
             *(float4*)&Ks[kk * LDK + 4 * kg] =
@@ -1744,16 +1750,31 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
             const int k0 = c0 + 16 * sb; /* first key of the sub-block */
             if (k0 >= kend) break;       /* past every query of the block (wave-uniform) */
             /* S^T[key 4*grp + v][query col] */
-            bmv_f32x4 st = bmv_f32x4{0.f, 0.f, 0.f, 0.f};
+            /* four independent chains over the 64 dimensions (a single
+             * chain of 16 dependent MFMAs waits out each one's latency) */
+            bmv_f32x4 sq[4];
             const float* kr = &Ks[(16 * sb + col) * LDK + 16 * grp];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const float4 k4 = *(const float4*)&kr[4 * i];
-                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qf[4 * i + 0], st, 0, 0, 0);
-                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qf[4 * i + 1], st, 0, 0, 0);
-                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qf[4 * i + 2], st, 0, 0, 0);
-                st = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qf[4 * i + 3], st, 0, 0, 0);
+                sq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.x, qf[4 * i + 0], bmv_f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
             }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k4 = *(const float4*)&kr[4 * i];
+                sq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.y, qf[4 * i + 1], sq[i], 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k4 = *(const float4*)&kr[4 * i];
+                sq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.z, qf[4 * i + 2], sq[i], 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k4 = *(const float4*)&kr[4 * i];
+                sq[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(k4.w, qf[4 * i + 3], sq[i], 0, 0, 0);
+            }
+            const bmv_f32x4 st = (sq[0] + sq[1]) + (sq[2] + sq[3]);
             float sv[4];
             float cm = -INFINITY;
 #pragma unroll
