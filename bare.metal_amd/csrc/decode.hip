@@ -1555,6 +1555,19 @@ __global__ __launch_bounds__(NT) void k_pf_norm_bf16(const float* __restrict__ x
     }
 }
 
+/* (cos, sin) of every prompt position p < n and rotary pair t < HD/2, out
+ * [n][HD/2][2]: the angle (float)p * inv_freq[t] as k_pf_kv takes it, for
+ * the q/k/v GEMM epilogue that rotates k (pf_gemm.hip). */
+__global__ __launch_bounds__(NT) void k_pf_rope_table(DecAttn a, int n, float* __restrict__ out) {
+    const int half = a.HD / 2;
+    const long i = (long)blockIdx.x * NT + threadIdx.x;
+    if (i >= (long)n * half) return;
+    const int p = (int)(i / half), t = (int)(i - (long)p * half);
+    const float ang = (float)p * a.inv_freq[t];
+    out[2 * i] = cosf(ang);
+    out[2 * i + 1] = sinf(ang);
+}
+
 /* RoPE of every position's k and the cache append of k and v (layer a.layer,
  * sequence 0): workgroup p, thread (KV head, rotary pair). */
 __global__ __launch_bounds__(NT) void k_pf_kv(DecAttn a, const float* __restrict__ k, const float* __restrict__ v) {
@@ -2463,6 +2476,13 @@ extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, i
     return 0;
 }
 
+extern "C" int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s) {
+    const long cnt = (long)n * (a->HD / 2);
+    hipLaunchKernelGGL(k_pf_rope_table, dim3((unsigned)((cnt + NT - 1) / NT)), dim3(NT), 0, s, *a, n, out);
+    BMK_LAUNCH_CHECK();
+    return 0;
+}
+
 extern "C" int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps,
                                 hipStream_t s) {
     BMK_REQUIRE(D % 32 == 0 && ((uintptr_t)out & 15) == 0, "prefill RMSNorm: D %d, output alignment", D);
@@ -2471,16 +2491,18 @@ extern "C" int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* 
     return 0;
 }
 
-/* RoPE + cache append of every position, then causal attention; the
- * result goes to out16 as bf16 in fragment order (the o-projection's
- * operand).  Head size 64: blocks of PQB positions per workgroup, written
+/* RoPE + cache append of every position (unless the q/k/v GEMM's epilogue
+ * did it: kv_done), then causal attention; the result goes to out16 as
+ * bf16 in fragment order (the o-projection's operand).  Head size 64: blocks of PQB positions per workgroup, written
  * as bf16 directly; other head sizes: one workgroup per (head, position)
  * into a->out (fp32), then the fragment-order cast (which also zeroes the
  * columns past NH * HD). */
 extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n,
-                                unsigned short* out16, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_kv, dim3(n), dim3(NT), 0, s, *a, k, v);
-    BMK_LAUNCH_CHECK();
+                                unsigned short* out16, int kv_done, hipStream_t s) {
+    if (!kv_done) {
+        hipLaunchKernelGGL(k_pf_kv, dim3(n), dim3(NT), 0, s, *a, k, v);
+        BMK_LAUNCH_CHECK();
+    }
     if (a->HD == 64) {
         hipLaunchKernelGGL(k_pf_attn_blk, dim3(a->NH, (n + PQB - 1) / PQB), dim3(PNT), 0, s, *a, q, out16, n);
         BMK_LAUNCH_CHECK();

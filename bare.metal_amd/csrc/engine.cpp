@@ -48,8 +48,9 @@ int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
 int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
 int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps, hipStream_t s);
+int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
-                     hipStream_t s);
+                     int kv_done, hipStream_t s);
 int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
 int q4_pack_bf16(const void* src, unsigned char* dst, long n, hipStream_t s);
 int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
@@ -121,7 +122,7 @@ struct bm_session_s {
     float *x, *q, *k, *v, *att, *h, *logits, *kvc;
     /* prefill buffers, allocated on the first bm_forward over a prompt */
     int pf_cap;              /* rows they hold */
-    void* pf_buf[6];         /* x, q/k/v, attention output, the two bf16 GEMM operands, tokens */
+    void* pf_buf[7];         /* x, q/k/v, attention output, the two bf16 GEMM operands, tokens, RoPE table */
     DecState* st;
     DecHeadArrive* harr;  /* where the head's workgroups meet (zeroed once, re-armed by every launch) */
     int* prompt;
@@ -622,7 +623,7 @@ static void session_free(bm_session_t* S) {
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
     hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->harr); hipFree(S->prompt); hipFree(S->out_tokens);
-    for (int i = 0; i < 6; i++) hipFree(S->pf_buf[i]);
+    for (int i = 0; i < 7; i++) hipFree(S->pf_buf[i]);
     if (S->h_st) hipHostFree(S->h_st);
     if (S->h_logits) hipHostFree(S->h_logits);
     if (S->h_io) hipHostFree(S->h_io);
@@ -919,16 +920,18 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
  * q/k/v rows, the attention output (fp32, head sizes other than 64), the
  * bf16 GEMM operands in MFMA fragment order (rows rounded up to 32, columns
  * to 64): a16 for the RMSNorm and attention outputs, h16 for the SwiGLU
- * output, and the tokens.  bm_forward keeps it in session buffers allocated
+ * output, the tokens, and the RoPE (cos, sin) table of the prompt's
+ * positions.  bm_forward keeps it in session buffers allocated
  * on the first prefill; bm_forward_noalloc carves it from the library's
  * static per-GPU array. */
 struct PfWork {
     float *x, *qkv, *att;
     unsigned short *a16, *h16;
     int* tok;
+    float* rope;
 };
 
-#define PF_PARTS 6
+#define PF_PARTS 7
 
 /* Device bytes of each part for n tokens (sz), and their offsets in one
  * 256-aligned carve (off, when given); returns the total. */
@@ -936,7 +939,7 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
     const size_t N = (size_t)n, N32 = (N + 31) / 32 * 32;
     const size_t a_cols = ((size_t)std::max(m->D, m->QD) + 63) / 64 * 64, h_cols = ((size_t)m->H + 63) / 64 * 64;
     const size_t b[PF_PARTS] = {N * m->D * 4, N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4, N32 * a_cols * 2,
-                                N32 * h_cols * 2, N * 4};
+                                N32 * h_cols * 2, N * 4, N * (size_t)(m->HD / 2) * 8};
     size_t at = 0;
     for (int i = 0; i < PF_PARTS; i++) {
         if (sz) sz[i] = b[i];
@@ -949,6 +952,7 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
 static void pf_work_set(PfWork* w, void* const part[PF_PARTS]) {
     w->x = (float*)part[0]; w->qkv = (float*)part[1]; w->att = (float*)part[2];
     w->a16 = (unsigned short*)part[3]; w->h16 = (unsigned short*)part[4]; w->tok = (int*)part[5];
+    w->rope = (float*)part[6];
 }
 
 /* bm_forward's workspace: session buffers, grown to n tokens. */
@@ -1030,7 +1034,10 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
     float* k = q + (size_t)n * QD;
     float* v = k + (size_t)n * KV;
     const int qf = m->quant_bits == 4;
-    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, s)) return -1;
+    /* head size 64: RoPE and the cache append run in the q/k/v GEMM's epilogue */
+    const int kv_fused = m->HD == 64;
+    const size_t slab = (size_t)S->MS * KV;
+    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, s) || (kv_fused && dec_pf_rope_table(&at, n, w.rope, s))) return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
         const uint64_t lw = (uint64_t)l * m->pf_layer_bytes;
@@ -1040,6 +1047,12 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         qkv.p[0].w_off = lw + m->pf_off[0]; qkv.p[0].C = q; qkv.p[0].N = QD; qkv.p[0].ldc = QD;
         qkv.p[1].w_off = lw + m->pf_off[1]; qkv.p[1].C = k; qkv.p[1].N = KV; qkv.p[1].ldc = KV;
         qkv.p[2].w_off = lw + m->pf_off[2]; qkv.p[2].C = v; qkv.p[2].N = KV; qkv.p[2].ldc = KV;
+        if (kv_fused) {
+            qkv.kc = S->kvc + (size_t)l * 2 * slab;
+            qkv.vc = qkv.kc + slab;
+            qkv.MS = S->MS;
+            qkv.rope = w.rope;
+        }
         memset(&o, 0, sizeof o);
         o.A = w.a16; o.W = m->d_pfw; o.x = w.x; o.M = n; o.K = QD; o.nprob = 1;
         o.p[0].w_off = lw + m->pf_off[3]; o.p[0].N = D; o.p[0].ldc = D;
@@ -1053,8 +1066,8 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         /* RMSNorm, q/k/v; RoPE, cache append, causal attention; o + residual;
          * RMSNorm, gate/up + SwiGLU; down + residual */
         if (dec_pf_norm_bf16(w.x, m->d_ln1 + (size_t)l * D, w.a16, n, D, eps, s) ||
-            pfg_launch(&qkv, qf, PFG_STORE, s) ||
-            dec_pf_attention(&at, q, k, v, n, w.a16, s) ||
+            pfg_launch(&qkv, qf, kv_fused ? PFG_QKV : PFG_STORE, s) ||
+            dec_pf_attention(&at, q, k, v, n, w.a16, kv_fused, s) ||
             pfg_launch(&o, qf, PFG_RESID, s) ||
             dec_pf_norm_bf16(w.x, m->d_ln2 + (size_t)l * D, w.a16, n, D, eps, s) ||
             pfg_launch(&gu, qf, PFG_SWIGLU, s) ||

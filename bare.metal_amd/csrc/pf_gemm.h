@@ -16,6 +16,8 @@
 #define PFG_STORE 0  /* C = A W^T, each problem into its own output */
 #define PFG_RESID 1  /* x += A W^T (the residual stream; one problem) */
 #define PFG_SWIGLU 2 /* h = bf16(silu(A Wg^T) * (A Wu^T)); problem 0 gate, 1 up */
+#define PFG_QKV 3    /* q, k, v of attention heads of size 64: q stored as PFG_STORE does, k rotated
+                      * (RoPE at each row's position) into the K cache, v into the V cache */
 
 /* The prefill's weight layout (pfg_repack): a matrix of N rows of K/32
  * blocks is cut into chunks of 32 rows x one 64-wide K step (two blocks per
@@ -39,6 +41,10 @@ typedef struct {
                               * columns K .. 64 ceil(K / 64) zero */
     const unsigned char* W;  /* prefill weight arena */
     float* x;                /* PFG_RESID: [M][N], row stride p[0].ldc */
+    float* kc;               /* PFG_QKV: this layer's K cache, [KV head][dim / 4][position][4] */
+    float* vc;               /*   and V cache, [position][KV], for positions 0 .. M-1 */
+    const float* rope;       /*   (cos, sin) of each row's position and rotary pair, [M][32][2] */
+    int MS;                  /*   cache positions */
     unsigned short* h;       /* PFG_SWIGLU: bf16 [M][N] in fragment order, columns N .. 64 ceil(N / 64) zero */
     int M, K, NT, nprob;     /* NT: N tiles of the launch (grid: ceil(M / 64) * NT workgroups) */
     PfgProb p[PFG_MAX_PROBS];

@@ -26,10 +26,12 @@
  *  - the four waves of a workgroup split K (contiguous step ranges), with
  *    the loads of three steps in flight, and sum their partial tiles through
  *    LDS once at the end, in wave order (the same bits every run);
- *  - the consumer runs in the epilogue: the plain store (q/k/v), the
- *    residual add (o, down: x += C, one writer per element), or SwiGLU
- *    (gate and up rows of the same outputs in one tile, bf16 out for the
- *    down projection), so no partial copies of C are written or re-read.
+ *  - the consumer runs in the epilogue: the plain store, the q/k/v
+ *    epilogue (k rotated by RoPE and appended to the KV cache with v, as
+ *    the reference's rope and cache-append kernels do, forward.metal:1284-
+ *    1329), the residual add (o, down: x += C, one writer per element), or
+ *    SwiGLU (gate and up rows of the same outputs in one tile, bf16 out for
+ *    the down projection), so no partial copies of C are written or re-read.
  */
 #include "bmk.h"
 #include "pf_gemm.h"
@@ -134,8 +136,11 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     const int r = t >> 2, m = m0 + r, c0 = (t & 3) * 16, j0 = (t & 3) * 8;
     const int ldc = a.p[p].ldc;
     float* dst = EPI == PFG_RESID ? a.x + (size_t)min(m, M - 1) * ldc + n0 + c0
-                                  : (EPI == PFG_STORE ? a.p[p].C + (size_t)min(m, M - 1) * ldc + n0 + c0 : nullptr);
-    const bool whole = EPI != PFG_SWIGLU && n0 + c0 + 16 <= N && ((uintptr_t)dst & 15) == 0;
+                                  : (EPI == PFG_STORE || (EPI == PFG_QKV && p == 0)
+                                         ? a.p[p].C + (size_t)min(m, M - 1) * ldc + n0 + c0
+                                         : nullptr);
+    const bool whole = (EPI == PFG_STORE || EPI == PFG_RESID || (EPI == PFG_QKV && p == 0)) && n0 + c0 + 16 <= N &&
+                       ((uintptr_t)dst & 15) == 0;
     /* the residual rows this thread adds to, loaded before the K loop so
      * that their latency hides behind it */
     float4 res[4];
@@ -238,6 +243,54 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
         }
         const u32x4 ov4 = {o.x, o.y, o.z, o.w};
         __builtin_nontemporal_store(ov4, (u32x4*)(a.h + frag_index(m, n0 + j0, (N + 63) >> 6)));
+    } else if (EPI == PFG_QKV && p == 2) {
+        /* a tile is one KV head (64 columns): v rows into the V cache */
+        float* vr = a.vc + (size_t)m * N + n0 + c0;
+#pragma unroll
+        for (int c = 0; c < 16; c += 4) {
+            float4 v4 = *(const float4*)&part[0][r][c0 + c];
+#pragma unroll
+            for (int w = 1; w < 4; w++) {
+                const float4 pw = *(const float4*)&part[w][r][c0 + c];
+                v4.x += pw.x; v4.y += pw.y; v4.z += pw.z; v4.w += pw.w;
+            }
+            *(float4*)&vr[c] = v4;
+        }
+    } else if (EPI == PFG_QKV && p == 1) {
+        /* k: RoPE pairs (d, d + 32) of the tile's KV head, eight per thread
+         * (d from j0), with the position's cos / sin from the table; the
+         * rotated rows go to the K cache, [dim / 4][position][4] */
+        float k0[8], k1[8];
+#pragma unroll
+        for (int c = 0; c < 8; c += 4) {
+            float4 lo = *(const float4*)&part[0][r][j0 + c], hi = *(const float4*)&part[0][r][32 + j0 + c];
+#pragma unroll
+            for (int w = 1; w < 4; w++) {
+                const float4 lw = *(const float4*)&part[w][r][j0 + c], hw = *(const float4*)&part[w][r][32 + j0 + c];
+                lo.x += lw.x; lo.y += lw.y; lo.z += lw.z; lo.w += lw.w;
+                hi.x += hw.x; hi.y += hw.y; hi.z += hw.z; hi.w += hw.w;
+            }
+            k0[c] = lo.x; k0[c + 1] = lo.y; k0[c + 2] = lo.z; k0[c + 3] = lo.w;
+            k1[c] = hi.x; k1[c + 1] = hi.y; k1[c + 2] = hi.z; k1[c + 3] = hi.w;
+        }
+        float cs[8], sn[8];
+#pragma unroll
+        for (int c = 0; c < 8; c += 2) {
+            const float4 t4 = *(const float4*)&a.rope[((size_t)m * 32 + j0 + c) * 2];
+            cs[c] = t4.x; sn[c] = t4.y; cs[c + 1] = t4.z; sn[c + 1] = t4.w;
+        }
+        float* kT = a.kc + (size_t)(n0 >> 6) * 64 * a.MS;
+#pragma unroll
+        for (int c = 0; c < 8; c += 4) {
+            float e0[4], e1[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                e0[q] = k0[c + q] * cs[c + q] - k1[c + q] * sn[c + q];
+                e1[q] = k0[c + q] * sn[c + q] + k1[c + q] * cs[c + q];
+            }
+            *(float4*)&kT[((size_t)((j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e0[0], e0[1], e0[2], e0[3]);
+            *(float4*)&kT[((size_t)((32 + j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e1[0], e1[1], e1[2], e1[3]);
+        }
     } else {
 #pragma unroll
         for (int c = 0; c < 16; c += 4) {
@@ -313,7 +366,10 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
     BMK_REQUIRE(a->M > 0 && a->K > 0 && a->K % 32 == 0, "pf_gemm: M %d, K %d (K a multiple of 32)", a->M, a->K);
     BMK_REQUIRE(a->nprob >= 1 && a->nprob <= PFG_MAX_PROBS, "pf_gemm: %d problems", a->nprob);
     BMK_REQUIRE(epi == PFG_STORE || (epi == PFG_RESID && a->nprob == 1 && a->x) ||
-                    (epi == PFG_SWIGLU && a->nprob == 2 && a->h && a->p[0].N == a->p[1].N),
+                    (epi == PFG_SWIGLU && a->nprob == 2 && a->h && a->p[0].N == a->p[1].N) ||
+                    (epi == PFG_QKV && a->nprob == 3 && a->kc && a->vc && a->rope && a->M <= a->MS &&
+                     a->p[1].N == a->p[2].N && ((uintptr_t)a->rope & 15) == 0 &&
+                     a->p[1].N % 64 == 0 && ((uintptr_t)a->kc & 15) == 0 && ((uintptr_t)a->vc & 15) == 0),
                 "pf_gemm: epilogue %d does not fit its %d problems", epi, a->nprob);
     BMK_REQUIRE(((uintptr_t)a->A & 15) == 0 && ((uintptr_t)a->W & 15) == 0 && ((uintptr_t)a->h & 15) == 0,
                 "pf_gemm: activations, weights and SwiGLU output must be 16-byte aligned");
@@ -321,7 +377,8 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
     for (int i = 0; i < a->nprob; i++) {
         BMK_REQUIRE(a->p[i].N > 0, "pf_gemm: problem %d has N = %d", i, a->p[i].N);
         BMK_REQUIRE(epi == PFG_SWIGLU || a->p[i].ldc >= a->p[i].N, "pf_gemm: ldc %d < N %d", a->p[i].ldc, a->p[i].N);
-        BMK_REQUIRE(epi != PFG_STORE || a->p[i].C, "pf_gemm: problem %d has no output", i);
+        BMK_REQUIRE((epi != PFG_STORE && !(epi == PFG_QKV && i == 0)) || a->p[i].C, "pf_gemm: problem %d has no output",
+                    i);
         BMK_REQUIRE((a->p[i].w_off & 15) == 0, "pf_gemm: weight offset not 16-byte aligned");
         a->p[i].tile0 = nt;
         if (epi != PFG_SWIGLU) nt += (a->p[i].N + PT - 1) / PT;
@@ -334,10 +391,12 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
     if (qf) {
         if (epi == PFG_STORE) PFG_GO(QF_Q4, PFG_STORE);
         else if (epi == PFG_RESID) PFG_GO(QF_Q4, PFG_RESID);
+        else if (epi == PFG_QKV) PFG_GO(QF_Q4, PFG_QKV);
         else PFG_GO(QF_Q4, PFG_SWIGLU);
     } else {
         if (epi == PFG_STORE) PFG_GO(QF_Q8, PFG_STORE);
         else if (epi == PFG_RESID) PFG_GO(QF_Q8, PFG_RESID);
+        else if (epi == PFG_QKV) PFG_GO(QF_Q8, PFG_QKV);
         else PFG_GO(QF_Q8, PFG_SWIGLU);
     }
 #undef PFG_GO
