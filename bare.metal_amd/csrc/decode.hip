@@ -1523,35 +1523,35 @@ __global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
  * are bf16 in MFMA fragment order (frag_index): the RMSNorm and the
  * attention write them so. */
 
-/* x[p] = emb[tok[p]] */
+/* x[p] = emb[tok[p]], and the first layer's RMSNorm operand as the q/k/v
+ * GEMM takes it (pf_gemm.h): an = bf16(x * g) in fragment order (columns
+ * past D zero) and the row's sum of squares in slot 0 of ss (the other
+ * ss_tiles - 1 slots zero). */
 __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, const float* __restrict__ emb,
-                                                 float* __restrict__ x, int D) {
+                                                 float* __restrict__ x, int D, const float* __restrict__ g,
+                                                 unsigned short* __restrict__ an, float* __restrict__ ss_out,
+                                                 int ss_tiles, int ss_ld) {
+    __shared__ float sh[4];
     const int p = blockIdx.x;
     const float* er = emb + (size_t)tok[p] * D;
     float* xr = x + (size_t)p * D;
-    for (int j = threadIdx.x; j < D; j += NT) xr[j] = er[j];
-}
-
-/* Row p: out = bf16 of RMSNorm(x) * w in fragment order, the activation
- * of the next GEMM (nks = ceil(D / 64); columns past D written as zeros). */
-__global__ __launch_bounds__(NT) void k_pf_norm_bf16(const float* __restrict__ x, const float* __restrict__ w,
-                                                     unsigned short* __restrict__ out, int D, int nks, float eps) {
-    __shared__ float sh[4];
-    const int p = blockIdx.x;
-    const float* xr = x + (size_t)p * D;
     float ss = 0.0f;
-    for (int j = threadIdx.x; j < D; j += NT) ss = fmaf(xr[j], xr[j], ss);
+    for (int j = threadIdx.x; j < D; j += NT) {
+        const float v = er[j];
+        xr[j] = v;
+        ss = fmaf(v, v, ss);
+    }
     ss = block_sum(ss, sh);
-    const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-    /* eight consecutive columns per thread: one 16-byte store (D is a multiple of 32) */
-    for (int g = threadIdx.x; g < 8 * nks; g += NT) {
-        unsigned int v[4] = {0u, 0u, 0u, 0u};
-        if (8 * g < D)
+    if (threadIdx.x < ss_tiles) ss_out[(size_t)threadIdx.x * ss_ld + p] = threadIdx.x == 0 ? ss : 0.0f;
+    const int nks = (D + 63) / 64;
+    for (int c = threadIdx.x; c < 8 * nks; c += NT) {
+        unsigned int w[4] = {0u, 0u, 0u, 0u};
+        if (8 * c < D)
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                v[c] = (unsigned int)bf16_bits((xr[8 * g + 2 * c] * inv) * w[8 * g + 2 * c]) |
-                       ((unsigned int)bf16_bits((xr[8 * g + 2 * c + 1] * inv) * w[8 * g + 2 * c + 1]) << 16);
-        *(uint4*)(out + frag_index(p, 8 * g, nks)) = make_uint4(v[0], v[1], v[2], v[3]);
+            for (int e = 0; e < 4; e++)
+                w[e] = (unsigned int)bf16_bits(er[8 * c + 2 * e] * g[8 * c + 2 * e]) |
+                       ((unsigned int)bf16_bits(er[8 * c + 2 * e + 1] * g[8 * c + 2 * e + 1]) << 16);
+        *(uint4*)(an + frag_index(p, 8 * c, nks)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
 
@@ -2470,8 +2470,11 @@ extern "C" int dec_cast_f16(const float* src, unsigned short* dst, long n, hipSt
 /* ------------------------------------------------------------------ */
 /* Prefill launchers (arguments validated by engine.cpp). */
 
-extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s) {
-    hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(NT), 0, s, tok, emb, x, D);
+extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, const float* g,
+                            unsigned short* an, float* ss, int ss_tiles, int ss_ld, hipStream_t s) {
+    BMK_REQUIRE(D % 32 == 0 && ss_tiles >= 1 && ss_tiles <= NT && ss_ld >= n && ((uintptr_t)an & 15) == 0,
+                "prefill embedding: D %d, %d sum slots", D, ss_tiles);
+    hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(NT), 0, s, tok, emb, x, D, g, an, ss, ss_tiles, ss_ld);
     BMK_LAUNCH_CHECK();
     return 0;
 }
@@ -2479,14 +2482,6 @@ extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, i
 extern "C" int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s) {
     const long cnt = (long)n * (a->HD / 2);
     hipLaunchKernelGGL(k_pf_rope_table, dim3((unsigned)((cnt + NT - 1) / NT)), dim3(NT), 0, s, *a, n, out);
-    BMK_LAUNCH_CHECK();
-    return 0;
-}
-
-extern "C" int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps,
-                                hipStream_t s) {
-    BMK_REQUIRE(D % 32 == 0 && ((uintptr_t)out & 15) == 0, "prefill RMSNorm: D %d, output alignment", D);
-    hipLaunchKernelGGL(k_pf_norm_bf16, dim3(n), dim3(NT), 0, s, x, w, out, D, (D + 63) / 64, eps);
     BMK_LAUNCH_CHECK();
     return 0;
 }

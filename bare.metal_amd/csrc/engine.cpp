@@ -46,8 +46,8 @@ int dec_head_tiles(int D, int V, int wf);
 int dec_launch_embed(const DecEmbed* a, hipStream_t s);
 int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
-int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, hipStream_t s);
-int dec_pf_norm_bf16(const float* x, const float* w, unsigned short* out, int n, int D, float eps, hipStream_t s);
+int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, const float* g, unsigned short* an,
+                 float* ss, int ss_tiles, int ss_ld, hipStream_t s);
 int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
                      int kv_done, hipStream_t s);
@@ -122,7 +122,7 @@ struct bm_session_s {
     float *x, *q, *k, *v, *att, *h, *logits, *kvc;
     /* prefill buffers, allocated on the first bm_forward over a prompt */
     int pf_cap;              /* rows they hold */
-    void* pf_buf[7];         /* x, q/k/v, attention output, the two bf16 GEMM operands, tokens, RoPE table */
+    void* pf_buf[9];         /* the prefill workspace (PfWork) */
     DecState* st;
     DecHeadArrive* harr;  /* where the head's workgroups meet (zeroed once, re-armed by every launch) */
     int* prompt;
@@ -623,7 +623,7 @@ static void session_free(bm_session_t* S) {
     if (S->graph) hipGraphDestroy(S->graph);
     hipFree(S->x); hipFree(S->q); hipFree(S->k); hipFree(S->v); hipFree(S->att); hipFree(S->h);
     hipFree(S->logits); hipFree(S->kvc); hipFree(S->st); hipFree(S->harr); hipFree(S->prompt); hipFree(S->out_tokens);
-    for (int i = 0; i < 7; i++) hipFree(S->pf_buf[i]);
+    for (int i = 0; i < 9; i++) hipFree(S->pf_buf[i]);
     if (S->h_st) hipHostFree(S->h_st);
     if (S->h_logits) hipHostFree(S->h_logits);
     if (S->h_io) hipHostFree(S->h_io);
@@ -919,9 +919,10 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
 /* The prefill's workspace for n tokens: the residual stream x [n][D], the
  * q/k/v rows, the attention output (fp32, head sizes other than 64), the
  * bf16 GEMM operands in MFMA fragment order (rows rounded up to 32, columns
- * to 64): a16 for the RMSNorm and attention outputs, h16 for the SwiGLU
- * output, the tokens, and the RoPE (cos, sin) table of the prompt's
- * positions.  bm_forward keeps it in session buffers allocated
+ * to 64): a16 for the first RMSNorm's and the attention's outputs, h16 for
+ * the SwiGLU output, a16b for the second RMSNorm's; the tokens, the RoPE
+ * (cos, sin) table of the prompt's positions, and the rows' partial sums of
+ * squares [ceil(D / 64)][n] for the RMSNorm scale.  bm_forward keeps it in session buffers allocated
  * on the first prefill; bm_forward_noalloc carves it from the library's
  * static per-GPU array. */
 struct PfWork {
@@ -929,9 +930,11 @@ struct PfWork {
     unsigned short *a16, *h16;
     int* tok;
     float* rope;
+    unsigned short* a16b;
+    float* ss;
 };
 
-#define PF_PARTS 7
+#define PF_PARTS 9
 
 /* Device bytes of each part for n tokens (sz), and their offsets in one
  * 256-aligned carve (off, when given); returns the total. */
@@ -939,7 +942,8 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
     const size_t N = (size_t)n, N32 = (N + 31) / 32 * 32;
     const size_t a_cols = ((size_t)std::max(m->D, m->QD) + 63) / 64 * 64, h_cols = ((size_t)m->H + 63) / 64 * 64;
     const size_t b[PF_PARTS] = {N * m->D * 4, N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4, N32 * a_cols * 2,
-                                N32 * h_cols * 2, N * 4, N * (size_t)(m->HD / 2) * 8};
+                                N32 * h_cols * 2, N * 4, N * (size_t)(m->HD / 2) * 8,
+                                N32 * (((size_t)m->D + 63) / 64 * 64) * 2, ((size_t)m->D + 63) / 64 * N * 4};
     size_t at = 0;
     for (int i = 0; i < PF_PARTS; i++) {
         if (sz) sz[i] = b[i];
@@ -952,7 +956,7 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
 static void pf_work_set(PfWork* w, void* const part[PF_PARTS]) {
     w->x = (float*)part[0]; w->qkv = (float*)part[1]; w->att = (float*)part[2];
     w->a16 = (unsigned short*)part[3]; w->h16 = (unsigned short*)part[4]; w->tok = (int*)part[5];
-    w->rope = (float*)part[6];
+    w->rope = (float*)part[6]; w->a16b = (unsigned short*)part[7]; w->ss = (float*)part[8];
 }
 
 /* bm_forward's workspace: session buffers, grown to n tokens. */
@@ -1037,7 +1041,13 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
     /* head size 64: RoPE and the cache append run in the q/k/v GEMM's epilogue */
     const int kv_fused = m->HD == 64;
     const size_t slab = (size_t)S->MS * KV;
-    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, s) || (kv_fused && dec_pf_rope_table(&at, n, w.rope, s))) return -1;
+    /* RMSNorm runs in the launches around it: the embedding and each
+     * residual GEMM write bf16(x * g) of the next norm and the rows' partial
+     * sums of squares, and the GEMM that takes them scales its rows */
+    const int ss_tiles = (D + 63) / 64;
+    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, m->d_ln1, w.a16, w.ss, ss_tiles, n, s) ||
+        (kv_fused && dec_pf_rope_table(&at, n, w.rope, s)))
+        return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
         const uint64_t lw = (uint64_t)l * m->pf_layer_bytes;
@@ -1047,6 +1057,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         qkv.p[0].w_off = lw + m->pf_off[0]; qkv.p[0].C = q; qkv.p[0].N = QD; qkv.p[0].ldc = QD;
         qkv.p[1].w_off = lw + m->pf_off[1]; qkv.p[1].C = k; qkv.p[1].N = KV; qkv.p[1].ldc = KV;
         qkv.p[2].w_off = lw + m->pf_off[2]; qkv.p[2].C = v; qkv.p[2].N = KV; qkv.p[2].ldc = KV;
+        qkv.ss_in = w.ss; qkv.ss_tiles = ss_tiles; qkv.ss_ld = n; qkv.norm_d = D; qkv.eps = eps;
         if (kv_fused) {
             qkv.kc = S->kvc + (size_t)l * 2 * slab;
             qkv.vc = qkv.kc + slab;
@@ -1056,20 +1067,24 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         memset(&o, 0, sizeof o);
         o.A = w.a16; o.W = m->d_pfw; o.x = w.x; o.M = n; o.K = QD; o.nprob = 1;
         o.p[0].w_off = lw + m->pf_off[3]; o.p[0].N = D; o.p[0].ldc = D;
+        o.an = w.a16b; o.gn = m->d_ln2 + (size_t)l * D; o.ss_out = w.ss; o.ss_ld = n;
         memset(&gu, 0, sizeof gu);
-        gu.A = w.a16; gu.W = m->d_pfw; gu.h = w.h16; gu.M = n; gu.K = D; gu.nprob = 2;
+        gu.A = w.a16b; gu.W = m->d_pfw; gu.h = w.h16; gu.M = n; gu.K = D; gu.nprob = 2;
         gu.p[0].w_off = lw + m->pf_off[4]; gu.p[0].N = H;
         gu.p[1].w_off = lw + m->pf_off[5]; gu.p[1].N = H;
+        gu.ss_in = w.ss; gu.ss_tiles = ss_tiles; gu.ss_ld = n; gu.norm_d = D; gu.eps = eps;
         memset(&dn, 0, sizeof dn);
         dn.A = w.h16; dn.W = m->d_pfw; dn.x = w.x; dn.M = n; dn.K = H; dn.nprob = 1;
         dn.p[0].w_off = lw + m->pf_off[6]; dn.p[0].N = D; dn.p[0].ldc = D;
-        /* RMSNorm, q/k/v; RoPE, cache append, causal attention; o + residual;
-         * RMSNorm, gate/up + SwiGLU; down + residual */
-        if (dec_pf_norm_bf16(w.x, m->d_ln1 + (size_t)l * D, w.a16, n, D, eps, s) ||
-            pfg_launch(&qkv, qf, kv_fused ? PFG_QKV : PFG_STORE, s) ||
+        if (l + 1 < L) {
+            dn.an = w.a16; dn.gn = m->d_ln1 + (size_t)(l + 1) * D; dn.ss_out = w.ss; dn.ss_ld = n;
+        }
+        /* q/k/v (RMSNorm 1); RoPE, cache append, causal attention; o + residual
+         * (RMSNorm 2's operand); gate/up + SwiGLU; down + residual (the next
+         * layer's RMSNorm 1 operand) */
+        if (pfg_launch(&qkv, qf, kv_fused ? PFG_QKV : PFG_STORE, s) ||
             dec_pf_attention(&at, q, k, v, n, w.a16, kv_fused, s) ||
             pfg_launch(&o, qf, PFG_RESID, s) ||
-            dec_pf_norm_bf16(w.x, m->d_ln2 + (size_t)l * D, w.a16, n, D, eps, s) ||
             pfg_launch(&gu, qf, PFG_SWIGLU, s) ||
             pfg_launch(&dn, qf, PFG_RESID, s))
             return -1;

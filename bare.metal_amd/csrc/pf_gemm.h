@@ -11,6 +11,7 @@
 
 #define PFG_MAX_PROBS 3
 #define PFG_TILE 64 /* C tile rows (tokens) and columns (outputs) per workgroup */
+#define PFG_SS_MAX 32 /* partial sums of squares per row at most (the residual width up to 2048) */
 
 /* Epilogues */
 #define PFG_STORE 0  /* C = A W^T, each problem into its own output */
@@ -46,6 +47,19 @@ typedef struct {
     const float* rope;       /*   (cos, sin) of each row's position and rotary pair, [M][32][2] */
     int MS;                  /*   cache positions */
     unsigned short* h;       /* PFG_SWIGLU: bf16 [M][N] in fragment order, columns N .. 64 ceil(N / 64) zero */
+    /* RMSNorm folded into the launches around it.  A launch whose A is
+     * bf16(x * g) of the residual stream scales each row of its products by
+     * 1 / sqrt(ss / norm_d + eps), ss the sum of the ss_tiles partial sums
+     * of squares at ss_in[tile * ss_ld + row].  A PFG_RESID launch with an
+     * set writes those for the next one: an = bf16(x * gn) of the updated
+     * rows in fragment order and each column tile's partial sums at
+     * ss_out[tile * ss_ld + row]. */
+    const float* ss_in;
+    float* ss_out;
+    unsigned short* an;
+    const float* gn;
+    int ss_tiles, ss_ld, norm_d;
+    float eps;
     int M, K, NT, nprob;     /* NT: N tiles of the launch (grid: ceil(M / 64) * NT workgroups) */
     PfgProb p[PFG_MAX_PROBS];
 } PfgArgs;

@@ -104,6 +104,7 @@ __device__ __forceinline__ bf16x8 dq(const uint4* q, int u, float s) {
 template <int QF, int EPI>
 __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     __shared__ float part[4][PT][PLD];
+    __shared__ float sst[PFG_SS_MAX][PT]; /* the tile rows' partial sums of squares */
     constexpr unsigned CH = QF == QF_Q4 ? PFG_CHUNK_Q4 : PFG_CHUNK_Q8;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int col = lane & 31, h = lane >> 5;
@@ -147,6 +148,22 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     if (EPI == PFG_RESID && whole) {
 #pragma unroll
         for (int c = 0; c < 4; c++) res[c] = *(const float4*)&dst[4 * c];
+    }
+    /* The RMSNorm inputs, loaded before the K loop so that their latency
+     * hides behind it: the tile rows' partial sums of squares, straight
+     * into LDS (global_load_lds: one tile's 64 rows per wave instruction,
+     * no registers held across the loop), or, for a residual launch that
+     * writes the next norm's operand, the norm weights of its 16 columns. */
+    if (EPI != PFG_RESID && a.ss_in) {
+        for (int i = wave; i < a.ss_tiles; i += 4)
+            __builtin_amdgcn_global_load_lds(
+                (const __attribute__((address_space(1))) void*)(a.ss_in + (size_t)i * a.ss_ld + min(m0 + lane, M - 1)),
+                (__attribute__((address_space(3))) void*)&sst[i][0], 4, 0, 0);
+    }
+    float gnr[16];
+    if (EPI == PFG_RESID && a.an) {
+#pragma unroll
+        for (int c = 0; c < 16; c++) gnr[c] = a.gn[min(n0 + c0 + c, N - 1)];
     }
 
     auto load = [&](int s, PfgStage<QF>& st) {
@@ -212,8 +229,15 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) part[wave][32 * i + 8 * (r >> 2) + 4 * h + (r & 3)][32 * j + col] = acc[i][j][r];
+    if (EPI != PFG_RESID && a.ss_in) asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* the sums have landed */
     __syncthreads();
     if (m >= M) return;
+    float inv = 1.0f;
+    if (EPI != PFG_RESID && a.ss_in) {
+        float ss = 0.f;
+        for (int i = 0; i < a.ss_tiles; i++) ss += sst[i][r]; /* tile order */
+        inv = 1.0f / sqrtf(ss / (float)a.norm_d + a.eps);
+    }
     /* C is written once and read by the next kernel: the stores stream
      * (nontemporal), leaving less for the end of the launch to write back */
     if (EPI == PFG_SWIGLU) {
@@ -227,8 +251,8 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 gv.x += gw.x; gv.y += gw.y; gv.z += gw.z; gv.w += gw.w;
                 uv.x += uw.x; uv.y += uw.y; uv.z += uw.z; uv.w += uw.w;
             }
-            g[c] = gv.x; g[c + 1] = gv.y; g[c + 2] = gv.z; g[c + 3] = gv.w;
-            u[c] = uv.x; u[c + 1] = uv.y; u[c + 2] = uv.z; u[c + 3] = uv.w;
+            g[c] = gv.x * inv; g[c + 1] = gv.y * inv; g[c + 2] = gv.z * inv; g[c + 3] = gv.w * inv;
+            u[c] = uv.x * inv; u[c + 1] = uv.y * inv; u[c + 2] = uv.z * inv; u[c + 3] = uv.w * inv;
         }
         /* eight consecutive columns: eight consecutive values of the
          * fragment-ordered output; columns past N (up to the next multiple
@@ -254,7 +278,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 const float4 pw = *(const float4*)&part[w][r][c0 + c];
                 v4.x += pw.x; v4.y += pw.y; v4.z += pw.z; v4.w += pw.w;
             }
-            *(float4*)&vr[c] = v4;
+            *(float4*)&vr[c] = make_float4(v4.x * inv, v4.y * inv, v4.z * inv, v4.w * inv);
         }
     } else if (EPI == PFG_QKV && p == 1) {
         /* k: RoPE pairs (d, d + 32) of the tile's KV head, eight per thread
@@ -270,8 +294,8 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 lo.x += lw.x; lo.y += lw.y; lo.z += lw.z; lo.w += lw.w;
                 hi.x += hw.x; hi.y += hw.y; hi.z += hw.z; hi.w += hw.w;
             }
-            k0[c] = lo.x; k0[c + 1] = lo.y; k0[c + 2] = lo.z; k0[c + 3] = lo.w;
-            k1[c] = hi.x; k1[c + 1] = hi.y; k1[c + 2] = hi.z; k1[c + 3] = hi.w;
+            k0[c] = lo.x * inv; k0[c + 1] = lo.y * inv; k0[c + 2] = lo.z * inv; k0[c + 3] = lo.w * inv;
+            k1[c] = hi.x * inv; k1[c + 1] = hi.y * inv; k1[c + 2] = hi.z * inv; k1[c + 3] = hi.w * inv;
         }
         float cs[8], sn[8];
 #pragma unroll
@@ -292,6 +316,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
             *(float4*)&kT[((size_t)((32 + j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e1[0], e1[1], e1[2], e1[3]);
         }
     } else {
+        float xn[16]; /* the stored values (x after the residual add); 0 past N */
 #pragma unroll
         for (int c = 0; c < 16; c += 4) {
             float4 v = *(const float4*)&part[0][r][c0 + c];
@@ -300,18 +325,51 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 const float4 pw = *(const float4*)&part[w][r][c0 + c];
                 v.x += pw.x; v.y += pw.y; v.z += pw.z; v.w += pw.w;
             }
+            if (EPI != PFG_RESID) {
+                v.x *= inv; v.y *= inv; v.z *= inv; v.w *= inv;
+            }
+            float vv[4] = {v.x, v.y, v.z, v.w};
             if (whole) {
                 if (EPI == PFG_RESID) {
                     const float4 o = res[c >> 2];
-                    v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+                    vv[0] += o.x; vv[1] += o.y; vv[2] += o.z; vv[3] += o.w;
                 }
-                const f32x4 v4 = {v.x, v.y, v.z, v.w};
+                const f32x4 v4 = {vv[0], vv[1], vv[2], vv[3]};
                 __builtin_nontemporal_store(v4, (f32x4*)&dst[c]);
             } else {
-                const float vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    if (n0 + c0 + c + e < N) dst[c + e] = EPI == PFG_RESID ? dst[c + e] + vv[e] : vv[e];
+                for (int e = 0; e < 4; e++) {
+                    if (n0 + c0 + c + e < N) {
+                        if (EPI == PFG_RESID) vv[e] += dst[c + e];
+                        dst[c + e] = vv[e];
+                    } else {
+                        vv[e] = 0.f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) xn[c + e] = vv[e];
+        }
+        if (EPI == PFG_RESID && a.an) {
+            /* the next RMSNorm's operand and this tile's partial sum of squares */
+            float ss = 0.f;
+#pragma unroll
+            for (int c = 0; c < 16; c++) ss = fmaf(xn[c], xn[c], ss);
+            ss += __shfl_xor(ss, 1);
+            ss += __shfl_xor(ss, 2); /* the four threads of row r */
+            if ((t & 3) == 0) a.ss_out[(size_t)nt * a.ss_ld + m] = ss;
+            const int nks = (N + 63) >> 6;
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                unsigned int w[4];
+#pragma unroll
+                for (int c = 0; c < 8; c += 2) {
+                    const int cc = n0 + c0 + 8 * hf + c;
+                    const float lo = cc < N ? xn[8 * hf + c] * gnr[8 * hf + c] : 0.f;
+                    const float hi = cc + 1 < N ? xn[8 * hf + c + 1] * gnr[8 * hf + c + 1] : 0.f;
+                    w[c >> 1] = pk2(lo, hi);
+                }
+                *(uint4*)(a.an + frag_index(m, n0 + c0 + 8 * hf, nks)) = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
     }
@@ -371,8 +429,14 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
                      a->p[1].N == a->p[2].N && ((uintptr_t)a->rope & 15) == 0 &&
                      a->p[1].N % 64 == 0 && ((uintptr_t)a->kc & 15) == 0 && ((uintptr_t)a->vc & 15) == 0),
                 "pf_gemm: epilogue %d does not fit its %d problems", epi, a->nprob);
-    BMK_REQUIRE(((uintptr_t)a->A & 15) == 0 && ((uintptr_t)a->W & 15) == 0 && ((uintptr_t)a->h & 15) == 0,
-                "pf_gemm: activations, weights and SwiGLU output must be 16-byte aligned");
+    BMK_REQUIRE(((uintptr_t)a->A & 15) == 0 && ((uintptr_t)a->W & 15) == 0 && ((uintptr_t)a->h & 15) == 0 &&
+                    ((uintptr_t)a->an & 15) == 0,
+                "pf_gemm: activations, weights and bf16 outputs must be 16-byte aligned");
+    BMK_REQUIRE(!a->ss_in || (epi != PFG_RESID && a->ss_tiles > 0 && a->ss_tiles <= PFG_SS_MAX && a->ss_ld >= a->M &&
+                              a->norm_d > 0),
+                "pf_gemm: RMSNorm scale of the rows needs its partial sums");
+    BMK_REQUIRE(!a->an || (epi == PFG_RESID && a->gn && a->ss_out && a->ss_ld >= a->M),
+                "pf_gemm: the next RMSNorm's operand comes from a residual launch with its weights and sums");
     int nt = 0;
     for (int i = 0; i < a->nprob; i++) {
         BMK_REQUIRE(a->p[i].N > 0, "pf_gemm: problem %d has N = %d", i, a->p[i].N);

@@ -174,9 +174,11 @@ def cosine(a, b):
 HD64 = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
 
 
+# hd64-150 / -300 / -520: the attention's longest query blocks split into 2, 3 and 4 key segments
 @pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1), (HD64, 1), (HD64, 17), (HD64, 70),
-                                    (HD64, 150)],
-                         ids=["tiny-12", "small-40", "small-1", "hd64-1", "hd64-17", "hd64-70", "hd64-150"])
+                                    (HD64, 150), (HD64, 300), (HD64, 520)],
+                         ids=["tiny-12", "small-40", "small-1", "hd64-1", "hd64-17", "hd64-70", "hd64-150",
+                              "hd64-300", "hd64-520"])
 def test_prefill_matches_stepwise(dims, n):
     """bm_forward over a prompt at position 0 (one pass, bf16-MFMA projections)
     against stepping the same tokens one by one, as the reference's
