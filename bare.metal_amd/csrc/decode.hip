@@ -1663,7 +1663,9 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
     __shared__ float Ms[PNW * PQB], Ls[PNW * PQB];
     const int NH = MODE == PF_FLAT ? f.NH : a.NH;
     const int kv_mul = MODE == PF_FLAT ? f.kv_mul : a.NH / a.NKV;
-    const float scale = MODE == PF_FLAT ? f.scale : a.scale;
+    /* scores in base 2: softmax weights by v_exp_f32 (exp2) of
+     * s * scale * log2(e), one instruction instead of expf's reduction */
+    const float sl2 = (MODE == PF_FLAT ? f.scale : a.scale) * 1.44269504088896341f;
     /* the last blocks of the prompt have the most keys: they take the first
      * workgroup slots, and the short ones fill in behind them */
     const int h = blockIdx.x, p0 = (int)(gridDim.y - 1 - blockIdx.y) * PQB;
@@ -1792,17 +1794,17 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
             float cm = -INFINITY;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                sv[v] = k0 + 4 * grp + v <= p ? st[v] * scale : -INFINITY;
+                sv[v] = k0 + 4 * grp + v <= p ? st[v] * sl2 : -INFINITY;
                 cm = fmaxf(cm, sv[v]);
             }
             cm = fmaxf(cm, __shfl_xor(cm, 16));
             cm = fmaxf(cm, __shfl_xor(cm, 32));
             const float mn = fmaxf(m, cm);
             const bool live = mn > -INFINITY; /* some key of this query admitted so far */
-            const float fr = live ? expf(m - mn) : 1.0f;
+            const float fr = live ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
             float pv[4];
 #pragma unroll
-            for (int v = 0; v < 4; v++) pv[v] = live ? expf(sv[v] - mn) : 0.0f;
+            for (int v = 0; v < 4; v++) pv[v] = live ? __builtin_amdgcn_exp2f(sv[v] - mn) : 0.0f;
             l = l * fr + ((pv[0] + pv[1]) + (pv[2] + pv[3]));
 #pragma unroll
             for (int ti = 0; ti < 4; ti++) acc[ti] *= fr;
@@ -1841,7 +1843,7 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
 #pragma unroll
     for (int w = 0; w < PNW; w++) {
         const float mv = Ms[w * PQB + r];
-        const float fr = mv == -INFINITY ? 0.0f : expf(mv - mx);
+        const float fr = mv == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mv - mx);
         const float* src = &Ws[(w * HD + 4 * g) * PQB + r];
         den = fmaf(fr, Ls[w * PQB + r], den);
         o0 = fmaf(fr, src[0 * PQB], o0);
