@@ -13,7 +13,6 @@
 #define GM_BM 128   /* C tile rows (tokens) per workgroup */
 #define GM_BN 128   /* C tile columns (output features) per workgroup */
 #define GM_IDLE_TILE 0xffffffffu /* tile-map entry of a workgroup with no tile */
-#define GM_KSPLIT_MAX 4          /* K slices of a split C tile at most */
 #define GM_FBM 256  /* fragment-ordered activations (layout 2): C tile rows per workgroup */
 #define GM_FBN 96   /*   and columns (576, 192 and 1536 are multiples of 96) */
 #define GM_A_F32 0  /* activation layouts of matmul_forward_q8_multi: fp32 row-major */
@@ -55,15 +54,6 @@ int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipStream_t s);
 int gm_cast_bf16_frag(const float* src, unsigned short* dst, int M, int K, int lda, hipStream_t s);
 int gm_launch_group(GmGroup* g, hipStream_t s);
 int gm_launch_group_qf(GmGroup* g, int qf, hipStream_t s);
-/* Plans with split-K for launches with few C tiles (q8_plan.cpp):
- * *ksplit_out = K slices of the launch's problems (1: none split). */
-long gm_plan_split(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off, const int* M,
-                   const int* N, const int* K, const int* lda, const int* ldc, int target, int kmax, void* plan,
-                   size_t plan_bytes, int* n_tiles_out, int* ksplit_out);
-/* A gm_plan_split plan: slice ks of a split problem writes its partial
- * product at C + ks * slice_stride (floats). */
-int gm_launch_split_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan, int nprob,
-                       int n_tiles, size_t slice_stride, hipStream_t s);
 int gm_launch_multi_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
                        int nprob, int n_tiles, hipStream_t s);
 #ifdef __cplusplus

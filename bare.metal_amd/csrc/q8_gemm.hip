@@ -108,12 +108,10 @@ __device__ __forceinline__ uint4 dq4(const uint4& q, int part, float s) {
  * Rows past M (or N) only feed C entries that are never stored, so the
  * loaders clamp them to the last row instead of branching.  Offsets are
  * 32-bit from workgroup-uniform bases (the launchers check that they fit). */
-/* nbr > 0: a split-K slice.  The tile covers K columns of weight rows that
- * are nbr blocks long (the caller offsets A and W to the slice). */
 template <bool ABF16, int QF = QF_Q8>
 __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const unsigned char* __restrict__ W,
                                           float* __restrict__ Cm, int M, int N, int K, int lda, int ldc, int tm,
-                                          int tn, unsigned short* lds, int nbr = 0) {
+                                          int tn, unsigned short* lds) {
     constexpr unsigned BYTES = QFmt<QF>::BYTES; /* bytes per 32-weight block */
     typedef Stage<ABF16, QF> St;
     constexpr int CPR = ABF16 ? GEMM_BK / 8 : GEMM_BK / 4; /* 16-byte chunks of an A row */
@@ -125,7 +123,7 @@ __device__ __forceinline__ void gemm_tile(const void* __restrict__ Av, const uns
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
     const int m0 = tm * BM, n0 = tn * BN;
     const int nb = K / 32;                /* blocks of this tile's K range */
-    const int nrow = nbr > 0 ? nbr : nb;  /* blocks per weight row */
+    const int nrow = nb;                  /* blocks per weight row */
     const int nfull = nb >> 1;
     const int lr = t >> 1, lh = t & 1;    /* W loader: row, block of the pair */
     const int ar = t / CPR, ac = t % CPR; /* A loader: first row, chunk */
@@ -560,37 +558,6 @@ __global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     gemm_multi_body<ABF16, QF_Q4>(A, W, C, desc, tile_map, lds);
 }
 
-/* Multi-GEMM whose problems may be split along K (GmDesc.pad_ = ksplit > 1,
- * plans from gm_plan_split): tile index = slice * C tiles + C tile; slice ks
- * covers K blocks [ks*nb/ksplit, (ks+1)*nb/ksplit) and writes its partial
- * product, row-major like C, to C + ks * slice_stride.  The kernels that
- * read the outputs add the ksplit copies in slice order (the same bits on
- * every run); problems with pad_ <= 1 write C only. */
-template <bool ABF16, int QF>
-__global__ __launch_bounds__(NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_split(
-    const void* __restrict__ A, const unsigned char* __restrict__ W, float* __restrict__ C,
-    const GmDesc* __restrict__ desc, const unsigned int* __restrict__ tile_map, size_t slice_stride) {
-    __shared__ __attribute__((aligned(16))) unsigned short lds[GEMM_LDS];
-    constexpr unsigned BYTES = QFmt<QF>::BYTES;
-    const unsigned int tm_ = tile_map[blockIdx.x];
-    if (tm_ == GM_IDLE_TILE) return;
-    const GmDesc d = desc[tm_ >> 16];
-    const int tile = (int)(tm_ & 0xffffu);
-    const int tiles_n = (d.N + BN - 1) / BN;
-    const int ksplit = d.pad_ > 1 ? d.pad_ : 1;
-    const int tiles_mn = d.tiles / ksplit;
-    const int ks = tile / tiles_mn, tmn = tile - ks * tiles_mn;
-    const int nbr = d.K / 32;
-    const int kb0 = ks * nbr / ksplit, kb1 = (ks + 1) * nbr / ksplit;
-    const size_t acol = d.a_off + (size_t)kb0 * 32;
-    const void* Ad = ABF16 ? (const void*)((const unsigned short*)A + acol) : (const void*)((const float*)A + acol);
-    if (ksplit == 1)
-        gemm_tile<ABF16, QF>(Ad, W + d.w_off, C + d.c_off, d.M, d.N, d.K, d.lda, d.ldc, tmn / tiles_n, tmn % tiles_n, lds);
-    else
-        gemm_tile<ABF16, QF>(Ad, W + d.w_off + (size_t)kb0 * BYTES, C + d.c_off + (size_t)ks * slice_stride, d.M, d.N,
-                             (kb1 - kb0) * 32, d.lda, d.ldc, tmn / tiles_n, tmn % tiles_n, lds, nbr);
-}
-
 /* fp32 -> bf16 (round to nearest even), 8 elements per lane */
 __global__ __launch_bounds__(NTH) void k_cast_bf16(const float* __restrict__ src, unsigned short* __restrict__ dst,
                                                    long n8, long n) {
@@ -833,25 +800,6 @@ extern "C" int gm_cast_bf16(const float* src, unsigned short* dst, long n, hipSt
     if (n <= 0) return 0;
     const long n8 = n / 8;
     hipLaunchKernelGGL(k_cast_bf16, dim3((unsigned)((n8 + NTH) / NTH)), dim3(NTH), 0, s, src, dst, n8, n);
-    BMK_LAUNCH_CHECK();
-    return 0;
-}
-
-/* The engine's prefill launch over a gm_plan_split plan (validated when it
- * was built); slice ks of a split problem writes C + ks * slice_stride. */
-extern "C" int gm_launch_split_qf(const void* A, int a_bf16, int qf, const unsigned char* W, float* C, const void* plan,
-                                  int nprob, int n_tiles, size_t slice_stride, hipStream_t s) {
-    if (nprob <= 0 || n_tiles <= 0) return 0;
-    const GmDesc* desc = (const GmDesc*)plan;
-    const unsigned int* tmap = (const unsigned int*)((const char*)plan + (size_t)nprob * sizeof(GmDesc));
-    const dim3 grid((unsigned)n_tiles), tb(NTH);
-    if (qf) {
-        if (a_bf16) hipLaunchKernelGGL((k_gemm_split<true, QF_Q4>), grid, tb, 0, s, A, W, C, desc, tmap, slice_stride);
-        else hipLaunchKernelGGL((k_gemm_split<false, QF_Q4>), grid, tb, 0, s, A, W, C, desc, tmap, slice_stride);
-    } else {
-        if (a_bf16) hipLaunchKernelGGL((k_gemm_split<true, QF_Q8>), grid, tb, 0, s, A, W, C, desc, tmap, slice_stride);
-        else hipLaunchKernelGGL((k_gemm_split<false, QF_Q8>), grid, tb, 0, s, A, W, C, desc, tmap, slice_stride);
-    }
     BMK_LAUNCH_CHECK();
     return 0;
 }

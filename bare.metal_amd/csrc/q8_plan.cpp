@@ -189,41 +189,24 @@ static const GmGeo GEO_ROWMAJOR = {GM_BM, GM_BN}, GEO_FRAG = {GM_FBM, GM_FBN};
  * the launch has 8 x (longest queue) workgroups. */
 #define GM_XCDS 8
 
-/* Split-K factor of a launch, the same for all its problems: 1, unless
- * the launch has fewer than `target` C tiles; then enough K slices to reach
- * it, at most kmax and at most one slice per two K blocks of any problem. */
-static int gemm_split(const GmGeo& g, int nprob, const int* M, const int* N, const int* K, int target, int kmax) {
-    long total = 0;
-    for (int i = 0; i < nprob; i++) total += g.tiles(M[i], N[i]);
-    int want = 1;
-    if (total > 0 && total < target) want = (int)((target + total - 1) / total);
-    if (want > kmax) want = kmax;
-    for (int i = 0; i < nprob; i++)
-        if (want > K[i] / 64) want = K[i] / 64;
-    return want < 1 ? 1 : want;
-}
-
-/* Workgroups per XCD queue: every (problem, N tile, K slice) group goes to
- * one XCD, round robin, with its M tiles consecutive; ks K slices per problem. */
-static long gemm_queue_len(const GmGeo& g, int nprob, const int* M, const int* N, int ks, long* per_xcd) {
+/* Workgroups per XCD queue: every (problem, N tile) group goes to one XCD,
+ * round robin, with its M tiles consecutive. */
+static long gemm_queue_len(const GmGeo& g, int nprob, const int* M, const int* N, long* per_xcd) {
     for (int x = 0; x < GM_XCDS; x++) per_xcd[x] = 0;
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + g.bm - 1) / g.bm, tn = (N[i] + g.bn - 1) / g.bn;
-        for (int n = 0; n < tn; n++)
-            for (int k = 0; k < ks; k++, pair++) per_xcd[pair % GM_XCDS] += tm;
+        for (int n = 0; n < tn; n++, pair++) per_xcd[pair % GM_XCDS] += tm;
     }
     long longest = 0;
     for (int x = 0; x < GM_XCDS; x++) longest = per_xcd[x] > longest ? per_xcd[x] : longest;
     return longest;
 }
 
-/* Plan of one multi-GEMM launch: GmDesc[nprob], then the tile map.  A
- * problem with ksplit > 1 (GmDesc.pad_) has tiles = C tiles * ksplit, tile
- * index = slice * C tiles + C tile. */
+/* Plan of one multi-GEMM launch: GmDesc[nprob], then the tile map. */
 static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
-                           const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
-                           int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
+                           const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
+                           size_t plan_bytes, int* n_tiles_out) {
     if (nprob < 0 || nprob > 0xffff || (nprob > 0 && (!a_off || !w_off || !c_off || !M || !N || !K || !lda || !ldc)))
         return -1;
     for (int i = 0; i < nprob; i++) {
@@ -231,17 +214,11 @@ static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, con
         const int t = g.tiles(M[i], N[i]);
         if (t > 0xffff || lda[i] < K[i] || ldc[i] < N[i]) return -1;
     }
-    /* one split factor for every problem of the launch (no host allocation here:
-     * the engine's prefill plans are also made by the no-allocation entry point) */
-    const int ks = target > 0 ? gemm_split(g, nprob, M, N, K, target, kmax) : 1;
-    for (int i = 0; i < nprob; i++)
-        if ((long)g.tiles(M[i], N[i]) * ks > 0xffff) return -1;
     long per_xcd[GM_XCDS];
-    const long slots = (long)GM_XCDS * gemm_queue_len(g, nprob, M, N, ks, per_xcd);
+    const long slots = (long)GM_XCDS * gemm_queue_len(g, nprob, M, N, per_xcd);
     if (slots > 0x7fffffffL) return -1;
     const size_t need = (size_t)nprob * sizeof(GmDesc) + (size_t)slots * 4;
     if (n_tiles_out) *n_tiles_out = (int)slots;
-    if (ksplit_out) *ksplit_out = ks;
     if (!plan) return (long)need;
     if (plan_bytes < need || ((uintptr_t)plan & 7)) return -1;
     GmDesc* d = (GmDesc*)plan;
@@ -257,8 +234,8 @@ static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, con
         d[i].lda = lda[i];
         d[i].ldc = ldc[i];
         d[i].tile0 = t0;
-        d[i].tiles = g.tiles(M[i], N[i]) * ks;
-        d[i].pad_ = ks > 1 ? ks : 0;
+        d[i].tiles = g.tiles(M[i], N[i]);
+        d[i].pad_ = 0;
         t0 += d[i].tiles;
     }
     for (long b = 0; b < slots; b++) map[b] = GM_IDLE_TILE;
@@ -266,13 +243,11 @@ static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, con
     long pair = 0;
     for (int i = 0; i < nprob; i++) {
         const int tm = (M[i] + g.bm - 1) / g.bm, tn = (N[i] + g.bn - 1) / g.bn;
-        for (int n = 0; n < tn; n++)
-            for (int k = 0; k < ks; k++, pair++) {
-                const int x = (int)(pair % GM_XCDS);
-                for (int m = 0; m < tm; m++)
-                    map[(long)GM_XCDS * fill[x]++ + x] =
-                        ((unsigned int)i << 16) | (unsigned)(k * tm * tn + m * tn + n);
-            }
+        for (int n = 0; n < tn; n++, pair++) {
+            const int x = (int)(pair % GM_XCDS);
+            for (int m = 0; m < tm; m++)
+                map[(long)GM_XCDS * fill[x]++ + x] = ((unsigned int)i << 16) | (unsigned)(m * tn + n);
+        }
     }
     return (long)need;
 }
@@ -280,8 +255,7 @@ static long gemm_plan_impl(const GmGeo& g, int nprob, const uint64_t* a_off, con
 extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                                 const int* M, const int* N, const int* K, const int* lda, const int* ldc, void* plan,
                                 size_t plan_bytes, int* n_tiles_out) {
-    return gemm_plan_impl(GEO_ROWMAJOR, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes,
-                          n_tiles_out, nullptr);
+    return gemm_plan_impl(GEO_ROWMAJOR, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, plan, plan_bytes, n_tiles_out);
 }
 
 /* The plan of a launch over fragment-ordered activations (layout 2): a_off[i]
@@ -290,15 +264,6 @@ extern "C" long bm_q8_gemm_plan(int nprob, const uint64_t* a_off, const uint64_t
 extern "C" long bm_q8_gemm_plan_frag(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
                                      const int* M, const int* N, const int* K, const int* lda, const int* ldc,
                                      void* plan, size_t plan_bytes, int* n_tiles_out) {
-    return gemm_plan_impl(GEO_FRAG, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, 0, 1, plan, plan_bytes,
-                          n_tiles_out, nullptr);
+    return gemm_plan_impl(GEO_FRAG, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, plan, plan_bytes, n_tiles_out);
 }
 
-/* The engine's prefill plans: split-K when the launch has fewer than
- * `target` C tiles (at most kmax slices, the same for every problem). */
-extern "C" long gm_plan_split(int nprob, const uint64_t* a_off, const uint64_t* w_off, const uint64_t* c_off,
-                              const int* M, const int* N, const int* K, const int* lda, const int* ldc, int target,
-                              int kmax, void* plan, size_t plan_bytes, int* n_tiles_out, int* ksplit_out) {
-    return gemm_plan_impl(GEO_ROWMAJOR, nprob, a_off, w_off, c_off, M, N, K, lda, ldc, target, kmax, plan, plan_bytes,
-                          n_tiles_out, ksplit_out);
-}

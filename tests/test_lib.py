@@ -118,54 +118,6 @@ def test_gemm_plan_layout():
         bmhip.gemm_plan([0], [0], [0], [4], [4], [64], [32], [4])  # lda < K
 
 
-def _split_plan(M, N, K, target, kmax):
-    import ctypes as C
-    import numpy as np
-
-    f = bmhip.lib().gm_plan_split
-    vp = C.c_void_p
-    f.restype = C.c_long
-    f.argtypes = [C.c_int] + [vp] * 8 + [C.c_int, C.c_int, vp, C.c_size_t, vp, vp]
-    n = len(M)
-    z = np.zeros(n, dtype=np.uint64)
-    ints = [np.ascontiguousarray(v, dtype=np.int32) for v in (M, N, K, K, N)]
-    args = [z.ctypes.data] * 3 + [v.ctypes.data for v in ints] + [target, kmax]
-    nt, ks = C.c_int(0), C.c_int(0)
-    need = f(n, *args, None, 0, C.byref(nt), C.byref(ks))
-    assert need > 0
-    plan = np.zeros((need + 7) // 8, dtype=np.uint64)
-    assert f(n, *args, plan.ctypes.data, plan.nbytes, C.byref(nt), C.byref(ks)) == need
-    return plan.view(np.uint8)[:need].copy(), nt.value, ks.value
-
-
-def test_gemm_split_plan():
-    """Split-K plans of the engine's prefill launches: a launch with fewer C
-    tiles than the target gets the same K-slice count for every problem,
-    each (problem, slice, C tile) appears once, and a slice group stays on
-    one XCD."""
-    import numpy as np
-
-    # 4 x 1 C tiles of 128 x 128 with K = 576: 256 / 4 -> capped at kmax = 4
-    plan, n, ks = _split_plan([512], [128], [576], 256, 4)
-    assert ks == 4
-    desc = np.frombuffer(plan[:56].tobytes(), dtype=np.int32)
-    assert desc[12] == 16 and desc[13] == 4  # tiles = C tiles * ksplit, pad_ = ksplit
-    tmap = np.frombuffer(plan[56:].tobytes(), dtype=np.uint32)
-    live = [(b, int(v) & 0xFFFF) for b, v in enumerate(tmap) if v != 0xFFFFFFFF]
-    assert sorted(t for _, t in live) == list(range(16))
-    for s in range(4):  # slice s holds tiles 4s..4s+3, all on one XCD
-        assert len({b % 8 for b, t in live if t // 4 == s}) == 1
-    # K = 128 has two 64-wide K blocks: at most two slices
-    assert _split_plan([512], [128], [128], 256, 4)[2] == 2
-    assert _split_plan([512], [128], [64], 256, 4)[2] == 1
-    # enough C tiles: no split, and the plan equals the plain one
-    M, N, K = [512, 512], [2048, 1536], [576, 576]
-    plan, n, ks = _split_plan(M, N, K, 100, 4)
-    assert ks == 1
-    ref, nref = bmhip.gemm_plan([0, 0], [0, 0], [0, 0], M, N, K, K, N)
-    assert n == nref and plan.tobytes() == ref.tobytes()
-
-
 def test_bmv_plan_layout():
     """Plans of the batched (BT >= 2) multi-matrix matvec: 128 output rows per
     tile; every problem whole on one XCD (workgroup b runs on XCD b % 8),
