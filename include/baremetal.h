@@ -249,20 +249,20 @@ long           bm_profile_phases(bm_session_t* sess, double* ms);
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (serving loops and harnesses that forbid hipMalloc once running):
  * bm_forward's one-pass prefill of a prompt at position 0 of a batch-1
- * session, with the same kernels and results, whose workspace (split-K
- * partial products, bf16 activations, GEMM plans, token staging) lives in a
- * static array of BM_NOALLOC_SCRATCH_BYTES per GPU instead of session
+ * session, with the same kernels and results, whose workspace (residual
+ * stream, q/k/v rows, bf16 GEMM operands, norm sums, RoPE table, tokens)
+ * lives in a static array of BM_NOALLOC_SCRATCH_BYTES per GPU instead of session
  * buffers allocated on the first prefill.  It calls no hipMalloc/hipFree and
  * allocates no host memory.  Like bm_forward it synchronizes the session's
  * stream and copies the logits back to the host, so it cannot be recorded
  * under HIP stream capture.  The caller passes the session (already
  * created), the tokens, and reads the logits returned (the session's
  * [V] floats, as bm_forward).  Rejects, with NULL and an error logged, a
- * prompt whose workspace exceeds the array (about 82 KB per token at
- * SmolLM2-135M shapes: at most 780 tokens there), a session past position
- * 0 or with batch > 1, and n_tokens < 2.  Every call on one GPU shares that
- * GPU's array and all calls share one host staging buffer, so the library
- * serializes bm_forward_noalloc calls with one process-wide lock held until
+ * prompt whose workspace exceeds the array (about 14 KB per token at
+ * SmolLM2-135M shapes: at most about 4,700 tokens there), a session past
+ * position 0 or with batch > 1, and n_tokens < 2.  Every call on one GPU
+ * shares that GPU's array, so the library serializes bm_forward_noalloc
+ * calls with one process-wide lock held until
  * the call returns: concurrent calls (other threads, other sessions or
  * GPUs) wait for each other rather than race. */
 #define BM_NOALLOC_SCRATCH_BYTES (64u << 20)
