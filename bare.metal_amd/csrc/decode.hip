@@ -533,10 +533,11 @@ __global__ __launch_bounds__(NT) void k_head(DecHead a) {
  * maxima: across the 16 columns of a wave by shuffles, across waves through
  * LDS, then one atomicMax per batch row; the last workgroup emits the
  * tokens (head_finish). */
-template <int NBT, int WF>
+template <int NBT, int WF, bool XL>
 __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
     __shared__ unsigned long long shk[4][16 * NBT];
     __shared__ int last_wg;
+    extern __shared__ float4 xs4[]; /* XL: the batch rows in load order, [kb][bt][half][lane] */
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int c = lane & 15, g = lane >> 4;
     const int D = a.D, nkb = D / 32;
@@ -558,7 +559,20 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
     struct Ops {
         float wv[8], s, gv[8], xv[NBT][8];
     };
-    auto load = [&](int kb, Ops& o) {
+    auto load_x = [&](int kb, Ops& o) {
+#pragma unroll
+        for (int bt = 0; bt < NBT; bt++) {
+            if (XL) {
+                const float4 lo = xs4[((kb * NBT + bt) * 2 + 0) * 64 + lane], hi = xs4[((kb * NBT + bt) * 2 + 1) * 64 + lane];
+                o.xv[bt][0] = lo.x; o.xv[bt][1] = lo.y; o.xv[bt][2] = lo.z; o.xv[bt][3] = lo.w;
+                o.xv[bt][4] = hi.x; o.xv[bt][5] = hi.y; o.xv[bt][6] = hi.z; o.xv[bt][7] = hi.w;
+            } else {
+                __builtin_memcpy(&o.xv[bt][0], __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
+                __builtin_memcpy(&o.xv[bt][4], __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
+            }
+        }
+    };
+    auto load_w = [&](int kb, Ops& o) {
         o.s = 1.0f;
         if (WF == HW_Q8) {
             const unsigned char* blk = a.wq + ((size_t)rc * nkb + kb) * 36;
@@ -585,17 +599,37 @@ __global__ __launch_bounds__(NT) void k_head_b(DecHead a) {
         }
         __builtin_memcpy(&o.gv[0], __builtin_assume_aligned(nwp + 32 * kb, 4), 16);
         __builtin_memcpy(&o.gv[4], __builtin_assume_aligned(nwp + 32 * kb + 4, 4), 16);
-#pragma unroll
-        for (int bt = 0; bt < NBT; bt++) {
-            __builtin_memcpy(&o.xv[bt][0], __builtin_assume_aligned(xr[bt] + 32 * kb, 4), 16);
-            __builtin_memcpy(&o.xv[bt][4], __builtin_assume_aligned(xr[bt] + 32 * kb + 4, 4), 16);
-        }
+    };
+    auto load = [&](int kb, Ops& o) {
+        load_w(kb, o);
+        load_x(kb, o);
     };
     /* three stages: blocks kb + 1 and kb + 2 in flight during block kb's
      * products (past the last block the loads repeat it, unused) */
     Ops o0, o1, o2;
-    load(0, o0);
-    load(min(1, nkb - 1), o1);
+    if (XL) {
+        /* The batch rows, read by every wave at every K block, are staged
+         * once per workgroup straight into LDS (global_load_lds, one 1 KB
+         * slice per wave instruction: lane l takes row 16 bt + l % 16,
+         * columns 32 kb + 8 (l / 16) + 4 half .. +3), while the first two
+         * blocks of weights load into registers; each wave streaming all of
+         * x from L2 cost 20 of the head's ~51 us at B = 32. */
+        for (int j = wave; j < nkb * NBT * 2; j += 4) {
+            const int hh = j & 1, bt = (j >> 1) % NBT, kb = (j >> 1) / NBT;
+            const float* src = a.x + (size_t)min(16 * bt + c, a.B - 1) * D + 32 * kb + 8 * g + 4 * hh;
+            __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                             (__attribute__((address_space(3))) void*)&xs4[j * 64], 16, 0, 0);
+        }
+        load_w(0, o0);
+        load_w(min(1, nkb - 1), o1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* the slices have landed */
+        __syncthreads();
+        load_x(0, o0);
+        load_x(min(1, nkb - 1), o1);
+    } else {
+        load(0, o0);
+        load(min(1, nkb - 1), o1);
+    }
     __builtin_amdgcn_sched_barrier(0);
     auto compute = [&](const Ops& cur) {
 #pragma unroll
@@ -2417,6 +2451,9 @@ extern "C" int dec_launch_attn(const DecAttn* a, int B, hipStream_t s) {
     return 0;
 }
 
+/* LDS for the batch rows of a batched head launch at most (two workgroups per CU) */
+#define HEAD_XL_BYTES (76u << 10)
+
 extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
     if (a_in->B >= 2) {
         DecHead a = *a_in;
@@ -2424,18 +2461,26 @@ extern "C" int dec_launch_head(const DecHead* a_in, hipStream_t s) {
         a.tiles = (a.V + 63) / 64;
         const dim3 grid(a.tiles);
         const int wf = a.wq ? HW_Q8 : (a.wh ? (a.wh_f16 ? HW_F16 : HW_BF16) : HW_F32);
-#define HEAD_B(NBT)                                                                          \
-        do {                                                                                 \
-            if (wf == HW_Q8) hipLaunchKernelGGL((k_head_b<NBT, HW_Q8>), grid, dim3(NT), 0, s, a);  \
-            else if (wf == HW_BF16) hipLaunchKernelGGL((k_head_b<NBT, HW_BF16>), grid, dim3(NT), 0, s, a); \
-            else if (wf == HW_F16) hipLaunchKernelGGL((k_head_b<NBT, HW_F16>), grid, dim3(NT), 0, s, a); \
-            else hipLaunchKernelGGL((k_head_b<NBT, HW_F32>), grid, dim3(NT), 0, s, a);        \
+        /* the batch rows in LDS when they fit beside a second workgroup's */
+#define HEAD_B2(NBT, XL, LDSB)                                                                             \
+        do {                                                                                               \
+            if (wf == HW_Q8) hipLaunchKernelGGL((k_head_b<NBT, HW_Q8, XL>), grid, dim3(NT), LDSB, s, a);        \
+            else if (wf == HW_BF16) hipLaunchKernelGGL((k_head_b<NBT, HW_BF16, XL>), grid, dim3(NT), LDSB, s, a); \
+            else if (wf == HW_F16) hipLaunchKernelGGL((k_head_b<NBT, HW_F16, XL>), grid, dim3(NT), LDSB, s, a);  \
+            else hipLaunchKernelGGL((k_head_b<NBT, HW_F32, XL>), grid, dim3(NT), LDSB, s, a);                    \
+        } while (0)
+#define HEAD_B(NBT)                                                                                        \
+        do {                                                                                               \
+            const unsigned xb = (unsigned)a.D * NBT * 64u;                                                 \
+            if (xb <= HEAD_XL_BYTES) HEAD_B2(NBT, true, xb);                                               \
+            else HEAD_B2(NBT, false, 0);                                                                   \
         } while (0)
         if (a.B <= 16) HEAD_B(1);
         else if (a.B <= 32) HEAD_B(2);
         else if (a.B <= 48) HEAD_B(3);
         else HEAD_B(4);
 #undef HEAD_B
+#undef HEAD_B2
         BMK_LAUNCH_CHECK();
         return 0;
     }
