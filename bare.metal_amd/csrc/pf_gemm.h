@@ -10,7 +10,7 @@
 #include <stddef.h>
 
 #define PFG_MAX_PROBS 3
-#define PFG_TILE 64 /* C tile rows (tokens) and columns (outputs) per workgroup */
+#define PFG_TILE 64 /* C tile columns (outputs) per workgroup, and rows (tokens) at most */
 #define PFG_SS_MAX 32 /* partial sums of squares per row at most (the residual width up to 2048) */
 
 /* Epilogues */
@@ -60,7 +60,7 @@ typedef struct {
     const float* gn;
     int ss_tiles, ss_ld, norm_d;
     float eps;
-    int M, K, NT, nprob;     /* NT: N tiles of the launch (grid: ceil(M / 64) * NT workgroups) */
+    int M, K, NT, nprob;     /* NT: N tiles of the launch (grid: M tiles of 32 or 64 rows x NT workgroups) */
     PfgProb p[PFG_MAX_PROBS];
 } PfgArgs;
 

@@ -7,10 +7,10 @@
  *   C[m][n] = sum_k A[m][k] * bf16(q[n][k] * scale[n][k/32])   (A bf16, fp32 accumulation)
  *
  * with the same operand roundings as q8_gemm.hip.  At a prompt of a few
- * hundred tokens a layer's projection has tens to a few hundred 64x64
- * output tiles: each launch runs about one tile per CU, and its time is one
- * tile's dependent chain (loads, dequantisation, MFMAs, stores), not the
- * chip's throughput.  The kernel keeps that chain short:
+ * hundred tokens a layer's projection has tens to a few hundred 32x64 or
+ * 64x64 output tiles: each launch runs about one tile per CU, and its time
+ * is one tile's dependent chain (loads, dequantisation, MFMAs, stores), not
+ * the chip's throughput.  The kernel keeps that chain short:
  *  - no LDS staging and no barrier in the K loop.  Lane l of a wave (MFMA
  *    column l % 32, half h = l / 32) owns one whole 32-wide K block per
  *    64-wide step s, block 2s + h, of its two A rows and its two weight
@@ -69,9 +69,9 @@ __device__ __forceinline__ float sb(unsigned int w, int k) { return (float)(sign
 
 /* One lane's operands of one 64-wide K step: its A block in both row
  * groups (32 bf16 each) and its weight block in both column groups. */
-template <int QF>
+template <int QF, int MI>
 struct PfgStage {
-    uint4 a[2][4];
+    uint4 a[MI][4];
     float s[2];
     uint4 q[2][QF == QF_Q4 ? 1 : 2];
 };
@@ -101,16 +101,17 @@ __device__ __forceinline__ bf16x8 dq(const uint4* q, int u, float s) {
     return b;
 }
 
-template <int QF, int EPI>
+template <int QF, int EPI, int MI>
 __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
-    __shared__ float part[4][PT][PLD];
+    constexpr int PTM = 32 * MI; /* tile rows */
+    __shared__ float part[4][PTM][PLD];
     __shared__ float sst[PFG_SS_MAX][PT]; /* the tile rows' partial sums of squares */
     constexpr unsigned CH = QF == QF_Q4 ? PFG_CHUNK_Q4 : PFG_CHUNK_Q8;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int col = lane & 31, h = lane >> 5;
     const int nt = (int)(blockIdx.x % (unsigned)a.NT), mt = (int)(blockIdx.x / (unsigned)a.NT);
     const int M = a.M, ns = (a.K + 63) >> 6; /* 64-wide K steps (fragment columns per row block) */
-    const int m0 = mt * PT;
+    const int m0 = mt * PTM;
     int p = 0;
     if (EPI != PFG_SWIGLU) {
         if (a.nprob > 1 && nt >= a.p[1].tile0) p = 1;
@@ -122,12 +123,15 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     const int n0 = EPI == PFG_SWIGLU ? nt * 32 : (nt - a.p[p].tile0) * PT;
     /* Rows past M (N) only feed C entries that are never stored: the row
      * blocks (chunks) past the last are clamped to it. */
-    const unsigned short* af[2];
+    const unsigned short* af[MI];
     const unsigned char* wc[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < MI; i++) {
         const int rb = min((m0 >> 5) + i, ((M + 31) >> 5) - 1);
         af[i] = a.A + (size_t)rb * ns * 2048 + 8 * lane;
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
         const int f = min(EPI == PFG_SWIGLU ? nt : (n0 >> 5) + i, nfr - 1);
         wc[i] = a.W + a.p[EPI == PFG_SWIGLU ? i : p].w_off + (size_t)f * ns * CH;
     }
@@ -145,7 +149,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     /* the residual rows this thread adds to, loaded before the K loop so
      * that their latency hides behind it */
     float4 res[4];
-    if (EPI == PFG_RESID && whole) {
+    if (EPI == PFG_RESID && whole && r < PTM) {
 #pragma unroll
         for (int c = 0; c < 4; c++) res[c] = *(const float4*)&dst[4 * c];
     }
@@ -161,14 +165,14 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 (__attribute__((address_space(3))) void*)&sst[i][0], 4, 0, 0);
     }
     float gnr[16];
-    if (EPI == PFG_RESID && a.an) {
+    if (EPI == PFG_RESID && a.an && r < PTM) {
 #pragma unroll
         for (int c = 0; c < 16; c++) gnr[c] = a.gn[min(n0 + c0 + c, N - 1)];
     }
 
-    auto load = [&](int s, PfgStage<QF>& st) {
+    auto load = [&](int s, PfgStage<QF, MI>& st) {
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < MI; i++)
 #pragma unroll
             for (int u = 0; u < 4; u++)
                 __builtin_memcpy(&st.a[i][u], __builtin_assume_aligned(af[i] + (size_t)s * 2048 + 512 * u, 16), 16);
@@ -181,9 +185,9 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
         }
     };
 
-    f32x16 acc[2][2];
+    f32x16 acc[MI][2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -191,16 +195,16 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
 
     /* Past an odd block count the last step's upper half is zero on both
      * sides (the producers' column padding, the layout's zero blocks). */
-    auto compute = [&](const PfgStage<QF>& st) {
+    auto compute = [&](const PfgStage<QF, MI>& st) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            bf16x8 fb[2], fa[2];
+            bf16x8 fb[2], fa[MI];
 #pragma unroll
             for (int j = 0; j < 2; j++) fb[j] = dq<QF>(st.q[j], u, st.s[j]);
 #pragma unroll
-            for (int i = 0; i < 2; i++) __builtin_memcpy(&fa[i], &st.a[i][u], 16);
+            for (int i = 0; i < MI; i++) __builtin_memcpy(&fa[i], &st.a[i][u], 16);
 #pragma unroll
-            for (int i = 0; i < 2; i++)
+            for (int i = 0; i < MI; i++)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
      * the wave's last step they repeat it: an L2 hit, never used, so every
      * path issues the same loads), then each step waits for its own. */
     for (int g = s_beg; g < s_end; g += 3) {
-        PfgStage<QF> s0, s1, s2;
+        PfgStage<QF, MI> s0, s1, s2;
         load(g, s0);
         load(min(g + 1, s_end - 1), s1);
         load(min(g + 2, s_end - 1), s2);
@@ -224,14 +228,14 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     /* Partial tiles to LDS (32x32 D layout: register r of a tile holds row
      * 8 (r / 4) + 4 h + r % 4, column l % 32), then the sum in wave order. */
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) part[wave][32 * i + 8 * (r >> 2) + 4 * h + (r & 3)][32 * j + col] = acc[i][j][r];
     if (EPI != PFG_RESID && a.ss_in) asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* the sums have landed */
     __syncthreads();
-    if (m >= M) return;
+    if (r >= PTM || m >= M) return; /* the epilogue's map: four threads per tile row */
     float inv = 1.0f;
     if (EPI != PFG_RESID && a.ss_in) {
         float ss = 0.f;
@@ -449,9 +453,18 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
     }
     if (epi == PFG_SWIGLU) nt = 2 * ((a->p[0].N + 63) / 64); /* every 64-column step of h, padding included */
     a->NT = nt;
-    const long grid = (long)((a->M + PT - 1) / PT) * nt;
+    /* 32-row tiles (one row fragment per wave) halve each workgroup's chain
+     * (512 tokens: 6.7-6.8 against 7.8-8.1 us per launch); launches that
+     * would then need more than two workgroups per CU take 64-row tiles. */
+    const long grid1 = (long)((a->M + 31) / 32) * nt;
+    const int mi = grid1 > 512 ? 2 : 1;
+    const long grid = mi == 1 ? grid1 : (long)((a->M + 63) / 64) * nt;
     BMK_REQUIRE(grid > 0 && grid < (1L << 31), "pf_gemm: %ld workgroups", grid);
-#define PFG_GO(Q, E) hipLaunchKernelGGL((k_pf_gemm<Q, E>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a)
+#define PFG_GO(Q, E)                                                                                       \
+    do {                                                                                                   \
+        if (mi == 1) hipLaunchKernelGGL((k_pf_gemm<Q, E, 1>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);  \
+        else hipLaunchKernelGGL((k_pf_gemm<Q, E, 2>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);          \
+    } while (0)
     if (qf) {
         if (epi == PFG_STORE) PFG_GO(QF_Q4, PFG_STORE);
         else if (epi == PFG_RESID) PFG_GO(QF_Q4, PFG_RESID);
