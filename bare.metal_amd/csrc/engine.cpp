@@ -922,7 +922,8 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
  * to 64): a16 for the first RMSNorm's and the attention's outputs, h16 for
  * the SwiGLU output, a16b for the second RMSNorm's; the tokens, the RoPE
  * (cos, sin) table of the prompt's positions, and the rows' partial sums of
- * squares [ceil(D / 64)][n] for the RMSNorm scale.  bm_forward keeps it in session buffers allocated
+ * squares [ceil(D / 32)][n] for the RMSNorm scale (one per column tile of
+ * the residual GEMM that wrote them).  bm_forward keeps it in session buffers allocated
  * on the first prefill; bm_forward_noalloc carves it from the library's
  * static per-GPU array. */
 struct PfWork {
@@ -943,7 +944,7 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
     const size_t a_cols = ((size_t)std::max(m->D, m->QD) + 63) / 64 * 64, h_cols = ((size_t)m->H + 63) / 64 * 64;
     const size_t b[PF_PARTS] = {N * m->D * 4, N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4, N32 * a_cols * 2,
                                 N32 * h_cols * 2, N * 4, N * (size_t)(m->HD / 2) * 8,
-                                N32 * (((size_t)m->D + 63) / 64 * 64) * 2, ((size_t)m->D + 63) / 64 * N * 4};
+                                N32 * (((size_t)m->D + 63) / 64 * 64) * 2, ((size_t)m->D + 31) / 32 * N * 4};
     size_t at = 0;
     for (int i = 0; i < PF_PARTS; i++) {
         if (sz) sz[i] = b[i];
@@ -1044,8 +1045,8 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
     /* RMSNorm runs in the launches around it: the embedding and each
      * residual GEMM write bf16(x * g) of the next norm and the rows' partial
      * sums of squares, and the GEMM that takes them scales its rows */
-    const int ss_tiles = (D + 63) / 64;
-    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, m->d_ln1, w.a16, w.ss, ss_tiles, n, s) ||
+    int ss_parts = 1; /* the partial sums per row the last writer left (the embedding: the whole sum) */
+    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, m->d_ln1, w.a16, w.ss, ss_parts, n, s) ||
         (kv_fused && dec_pf_rope_table(&at, n, w.rope, s)))
         return -1;
     for (int l = 0; l < L; l++) {
@@ -1057,7 +1058,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         qkv.p[0].w_off = lw + m->pf_off[0]; qkv.p[0].C = q; qkv.p[0].N = QD; qkv.p[0].ldc = QD;
         qkv.p[1].w_off = lw + m->pf_off[1]; qkv.p[1].C = k; qkv.p[1].N = KV; qkv.p[1].ldc = KV;
         qkv.p[2].w_off = lw + m->pf_off[2]; qkv.p[2].C = v; qkv.p[2].N = KV; qkv.p[2].ldc = KV;
-        qkv.ss_in = w.ss; qkv.ss_tiles = ss_tiles; qkv.ss_ld = n; qkv.norm_d = D; qkv.eps = eps;
+        qkv.ss_in = w.ss; qkv.ss_tiles = ss_parts; qkv.ss_ld = n; qkv.norm_d = D; qkv.eps = eps;
         if (kv_fused) {
             qkv.kc = S->kvc + (size_t)l * 2 * slab;
             qkv.vc = qkv.kc + slab;
@@ -1072,7 +1073,7 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
         gu.A = w.a16b; gu.W = m->d_pfw; gu.h = w.h16; gu.M = n; gu.K = D; gu.nprob = 2;
         gu.p[0].w_off = lw + m->pf_off[4]; gu.p[0].N = H;
         gu.p[1].w_off = lw + m->pf_off[5]; gu.p[1].N = H;
-        gu.ss_in = w.ss; gu.ss_tiles = ss_tiles; gu.ss_ld = n; gu.norm_d = D; gu.eps = eps;
+        gu.ss_in = w.ss; gu.ss_ld = n; gu.norm_d = D; gu.eps = eps;
         memset(&dn, 0, sizeof dn);
         dn.A = w.h16; dn.W = m->d_pfw; dn.x = w.x; dn.M = n; dn.K = H; dn.nprob = 1;
         dn.p[0].w_off = lw + m->pf_off[6]; dn.p[0].N = D; dn.p[0].ldc = D;
@@ -1084,10 +1085,11 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
          * layer's RMSNorm 1 operand) */
         if (pfg_launch(&qkv, qf, kv_fused ? PFG_QKV : PFG_STORE, s) ||
             dec_pf_attention(&at, q, k, v, n, w.a16, kv_fused, s) ||
-            pfg_launch(&o, qf, PFG_RESID, s) ||
-            pfg_launch(&gu, qf, PFG_SWIGLU, s) ||
-            pfg_launch(&dn, qf, PFG_RESID, s))
+            pfg_launch(&o, qf, PFG_RESID, s))
             return -1;
+        gu.ss_tiles = o.NT; /* the o launch's column tiles */
+        if (pfg_launch(&gu, qf, PFG_SWIGLU, s) || pfg_launch(&dn, qf, PFG_RESID, s)) return -1;
+        ss_parts = dn.NT;
     }
     /* the head on the last position (its own final RMSNorm) */
     DecHead hd;

@@ -60,7 +60,8 @@ typedef struct {
     const float* gn;
     int ss_tiles, ss_ld, norm_d;
     float eps;
-    int M, K, NT, nprob;     /* NT: N tiles of the launch (grid: M tiles of 32 or 64 rows x NT workgroups) */
+    int M, K, NT, nprob;     /* NT: N tiles of the launch, of 32 or 64 columns (a residual launch's row sums
+                              * come in NT parts); grid: M tiles of 32 or 64 rows x NT workgroups */
     PfgProb p[PFG_MAX_PROBS];
 } PfgArgs;
 

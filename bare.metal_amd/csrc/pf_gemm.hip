@@ -69,11 +69,11 @@ __device__ __forceinline__ float sb(unsigned int w, int k) { return (float)(sign
 
 /* One lane's operands of one 64-wide K step: its A block in both row
  * groups (32 bf16 each) and its weight block in both column groups. */
-template <int QF, int MI>
+template <int QF, int MI, int NJ>
 struct PfgStage {
     uint4 a[MI][4];
-    float s[2];
-    uint4 q[2][QF == QF_Q4 ? 1 : 2];
+    float s[NJ];
+    uint4 q[NJ][QF == QF_Q4 ? 1 : 2];
 };
 
 /* Codes 8u .. 8u+7 of a block, times its scale, rounded to bf16. */
@@ -101,10 +101,13 @@ __device__ __forceinline__ bf16x8 dq(const uint4* q, int u, float s) {
     return b;
 }
 
-template <int QF, int EPI, int MI>
+template <int QF, int EPI, int MI, int NJ>
 __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
-    constexpr int PTM = 32 * MI; /* tile rows */
-    __shared__ float part[4][PTM][PLD];
+    constexpr int PTM = 32 * MI;  /* tile rows */
+    constexpr int TW = 32 * NJ;   /* tile columns */
+    constexpr int CPT = 8 * NJ;   /* epilogue columns per thread */
+    static_assert(NJ == 2 || EPI == PFG_RESID || EPI == PFG_STORE, "gate/up pairs and RoPE pairs need 64 columns");
+    __shared__ float part[4][PTM][TW + 4];
     __shared__ float sst[PFG_SS_MAX][PT]; /* the tile rows' partial sums of squares */
     constexpr unsigned CH = QF == QF_Q4 ? PFG_CHUNK_Q4 : PFG_CHUNK_Q8;
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
@@ -120,38 +123,38 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
     const int N = a.p[p].N, nfr = (N + 31) >> 5;
     /* SwiGLU: column group 0 holds gate rows n0 .. n0+31, group 1 the up
      * rows of the same outputs */
-    const int n0 = EPI == PFG_SWIGLU ? nt * 32 : (nt - a.p[p].tile0) * PT;
+    const int n0 = EPI == PFG_SWIGLU ? nt * 32 : (nt - a.p[p].tile0) * TW;
     /* Rows past M (N) only feed C entries that are never stored: the row
      * blocks (chunks) past the last are clamped to it. */
     const unsigned short* af[MI];
-    const unsigned char* wc[2];
+    const unsigned char* wc[NJ];
 #pragma unroll
     for (int i = 0; i < MI; i++) {
         const int rb = min((m0 >> 5) + i, ((M + 31) >> 5) - 1);
         af[i] = a.A + (size_t)rb * ns * 2048 + 8 * lane;
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < NJ; i++) {
         const int f = min(EPI == PFG_SWIGLU ? nt : (n0 >> 5) + i, nfr - 1);
         wc[i] = a.W + a.p[EPI == PFG_SWIGLU ? i : p].w_off + (size_t)f * ns * CH;
     }
     const int s_beg = wave * ns / 4, s_end = (wave + 1) * ns / 4;
-    /* Epilogue thread map: row r of the tile; 16 columns from c0 (8 gate and
-     * 8 up columns from j0 for SwiGLU). */
-    const int r = t >> 2, m = m0 + r, c0 = (t & 3) * 16, j0 = (t & 3) * 8;
+    /* Epilogue thread map: row r of the tile; CPT columns from c0 (8 gate
+     * and 8 up columns from j0 for SwiGLU). */
+    const int r = t >> 2, m = m0 + r, c0 = (t & 3) * CPT, j0 = (t & 3) * 8;
     const int ldc = a.p[p].ldc;
     float* dst = EPI == PFG_RESID ? a.x + (size_t)min(m, M - 1) * ldc + n0 + c0
                                   : (EPI == PFG_STORE || (EPI == PFG_QKV && p == 0)
                                          ? a.p[p].C + (size_t)min(m, M - 1) * ldc + n0 + c0
                                          : nullptr);
-    const bool whole = (EPI == PFG_STORE || EPI == PFG_RESID || (EPI == PFG_QKV && p == 0)) && n0 + c0 + 16 <= N &&
+    const bool whole = (EPI == PFG_STORE || EPI == PFG_RESID || (EPI == PFG_QKV && p == 0)) && n0 + c0 + CPT <= N &&
                        ((uintptr_t)dst & 15) == 0;
     /* the residual rows this thread adds to, loaded before the K loop so
      * that their latency hides behind it */
-    float4 res[4];
+    float4 res[CPT / 4];
     if (EPI == PFG_RESID && whole && r < PTM) {
 #pragma unroll
-        for (int c = 0; c < 4; c++) res[c] = *(const float4*)&dst[4 * c];
+        for (int c = 0; c < CPT / 4; c++) res[c] = *(const float4*)&dst[4 * c];
     }
     /* The RMSNorm inputs, loaded before the K loop so that their latency
      * hides behind it: the tile rows' partial sums of squares, straight
@@ -164,20 +167,20 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 (const __attribute__((address_space(1))) void*)(a.ss_in + (size_t)i * a.ss_ld + min(m0 + lane, M - 1)),
                 (__attribute__((address_space(3))) void*)&sst[i][0], 4, 0, 0);
     }
-    float gnr[16];
+    float gnr[CPT];
     if (EPI == PFG_RESID && a.an && r < PTM) {
 #pragma unroll
-        for (int c = 0; c < 16; c++) gnr[c] = a.gn[min(n0 + c0 + c, N - 1)];
+        for (int c = 0; c < CPT; c++) gnr[c] = a.gn[min(n0 + c0 + c, N - 1)];
     }
 
-    auto load = [&](int s, PfgStage<QF, MI>& st) {
+    auto load = [&](int s, PfgStage<QF, MI, NJ>& st) {
 #pragma unroll
         for (int i = 0; i < MI; i++)
 #pragma unroll
             for (int u = 0; u < 4; u++)
                 __builtin_memcpy(&st.a[i][u], __builtin_assume_aligned(af[i] + (size_t)s * 2048 + 512 * u, 16), 16);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             const unsigned char* c = wc[j] + (size_t)s * CH;
             __builtin_memcpy(&st.s[j], __builtin_assume_aligned(c + 4 * lane, 4), 4);
             __builtin_memcpy(&st.q[j][0], __builtin_assume_aligned(c + 256 + 16 * lane, 16), 16);
@@ -185,28 +188,28 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
         }
     };
 
-    f32x16 acc[MI][2];
+    f32x16 acc[MI][NJ];
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     /* Past an odd block count the last step's upper half is zero on both
      * sides (the producers' column padding, the layout's zero blocks). */
-    auto compute = [&](const PfgStage<QF, MI>& st) {
+    auto compute = [&](const PfgStage<QF, MI, NJ>& st) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            bf16x8 fb[2], fa[MI];
+            bf16x8 fb[NJ], fa[MI];
 #pragma unroll
-            for (int j = 0; j < 2; j++) fb[j] = dq<QF>(st.q[j], u, st.s[j]);
+            for (int j = 0; j < NJ; j++) fb[j] = dq<QF>(st.q[j], u, st.s[j]);
 #pragma unroll
             for (int i = 0; i < MI; i++) __builtin_memcpy(&fa[i], &st.a[i][u], 16);
 #pragma unroll
             for (int i = 0; i < MI; i++)
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < NJ; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
         }
     };
@@ -215,7 +218,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
      * the wave's last step they repeat it: an L2 hit, never used, so every
      * path issues the same loads), then each step waits for its own. */
     for (int g = s_beg; g < s_end; g += 3) {
-        PfgStage<QF, MI> s0, s1, s2;
+        PfgStage<QF, MI, NJ> s0, s1, s2;
         load(g, s0);
         load(min(g + 1, s_end - 1), s1);
         load(min(g + 2, s_end - 1), s2);
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
 #pragma unroll
     for (int i = 0; i < MI; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) part[wave][32 * i + 8 * (r >> 2) + 4 * h + (r & 3)][32 * j + col] = acc[i][j][r];
     if (EPI != PFG_RESID && a.ss_in) asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); /* the sums have landed */
@@ -320,9 +323,9 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
             *(float4*)&kT[((size_t)((32 + j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e1[0], e1[1], e1[2], e1[3]);
         }
     } else {
-        float xn[16]; /* the stored values (x after the residual add); 0 past N */
+        float xn[CPT]; /* the stored values (x after the residual add); 0 past N */
 #pragma unroll
-        for (int c = 0; c < 16; c += 4) {
+        for (int c = 0; c < CPT; c += 4) {
             float4 v = *(const float4*)&part[0][r][c0 + c];
 #pragma unroll
             for (int w = 1; w < 4; w++) {
@@ -358,13 +361,13 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
             /* the next RMSNorm's operand and this tile's partial sum of squares */
             float ss = 0.f;
 #pragma unroll
-            for (int c = 0; c < 16; c++) ss = fmaf(xn[c], xn[c], ss);
+            for (int c = 0; c < CPT; c++) ss = fmaf(xn[c], xn[c], ss);
             ss += __shfl_xor(ss, 1);
             ss += __shfl_xor(ss, 2); /* the four threads of row r */
             if ((t & 3) == 0) a.ss_out[(size_t)nt * a.ss_ld + m] = ss;
             const int nks = (N + 63) >> 6;
 #pragma unroll
-            for (int hf = 0; hf < 2; hf++) {
+            for (int hf = 0; hf < CPT / 8; hf++) {
                 unsigned int w[4];
 #pragma unroll
                 for (int c = 0; c < 8; c += 2) {
@@ -441,6 +444,21 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
                 "pf_gemm: RMSNorm scale of the rows needs its partial sums");
     BMK_REQUIRE(!a->an || (epi == PFG_RESID && a->gn && a->ss_out && a->ss_ld >= a->M),
                 "pf_gemm: the next RMSNorm's operand comes from a residual launch with its weights and sums");
+    /* Tiles: 32 rows (one row fragment per wave) halve each workgroup's
+     * chain (512 tokens: 6.4-6.7 against 7.8-8.1 us per launch), unless the
+     * launch would then need more than two workgroups per CU.  A residual
+     * launch of fewer than 128 such tiles also narrows them to 32 columns
+     * (its epilogue has no column pairs; its row sums then come in N / 32
+     * parts): 128 tokens 5.9 -> 4.5 us; at 512 tokens no change. */
+    auto count_tiles = [&](int tw) {
+        int n = 0;
+        for (int i = 0; i < a->nprob; i++) n += (a->p[i].N + tw - 1) / tw;
+        return epi == PFG_SWIGLU ? 2 * ((a->p[0].N + 63) / 64) : n;
+    };
+    const long mt32 = (a->M + 31) / 32;
+    const int nj = epi == PFG_RESID && mt32 * count_tiles(64) < 128 && count_tiles(32) <= PFG_SS_MAX ? 1 : 2;
+    const int tw = 32 * nj;
+    const int mi = mt32 * count_tiles(tw) > 512 ? 2 : 1;
     int nt = 0;
     for (int i = 0; i < a->nprob; i++) {
         BMK_REQUIRE(a->p[i].N > 0, "pf_gemm: problem %d has N = %d", i, a->p[i].N);
@@ -449,34 +467,36 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
                     i);
         BMK_REQUIRE((a->p[i].w_off & 15) == 0, "pf_gemm: weight offset not 16-byte aligned");
         a->p[i].tile0 = nt;
-        if (epi != PFG_SWIGLU) nt += (a->p[i].N + PT - 1) / PT;
+        if (epi != PFG_SWIGLU) nt += (a->p[i].N + tw - 1) / tw;
     }
     if (epi == PFG_SWIGLU) nt = 2 * ((a->p[0].N + 63) / 64); /* every 64-column step of h, padding included */
     a->NT = nt;
-    /* 32-row tiles (one row fragment per wave) halve each workgroup's chain
-     * (512 tokens: 6.7-6.8 against 7.8-8.1 us per launch); launches that
-     * would then need more than two workgroups per CU take 64-row tiles. */
-    const long grid1 = (long)((a->M + 31) / 32) * nt;
-    const int mi = grid1 > 512 ? 2 : 1;
-    const long grid = mi == 1 ? grid1 : (long)((a->M + 63) / 64) * nt;
+    const long grid = (long)((a->M + 32 * mi - 1) / (32 * mi)) * nt;
     BMK_REQUIRE(grid > 0 && grid < (1L << 31), "pf_gemm: %ld workgroups", grid);
-#define PFG_GO(Q, E)                                                                                       \
-    do {                                                                                                   \
-        if (mi == 1) hipLaunchKernelGGL((k_pf_gemm<Q, E, 1>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);  \
-        else hipLaunchKernelGGL((k_pf_gemm<Q, E, 2>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);          \
+#define PFG_GO(Q, E)                                                                                          \
+    do {                                                                                                      \
+        if (mi == 1) hipLaunchKernelGGL((k_pf_gemm<Q, E, 1, 2>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);  \
+        else hipLaunchKernelGGL((k_pf_gemm<Q, E, 2, 2>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);          \
+    } while (0)
+#define PFG_GO_R(Q)                                                                                           \
+    do {                                                                                                      \
+        if (nj == 2) PFG_GO(Q, PFG_RESID);                                                                    \
+        else if (mi == 1) hipLaunchKernelGGL((k_pf_gemm<Q, PFG_RESID, 1, 1>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a); \
+        else hipLaunchKernelGGL((k_pf_gemm<Q, PFG_RESID, 2, 1>), dim3((unsigned)grid), dim3(PNTH), 0, s, *a);  \
     } while (0)
     if (qf) {
         if (epi == PFG_STORE) PFG_GO(QF_Q4, PFG_STORE);
-        else if (epi == PFG_RESID) PFG_GO(QF_Q4, PFG_RESID);
+        else if (epi == PFG_RESID) PFG_GO_R(QF_Q4);
         else if (epi == PFG_QKV) PFG_GO(QF_Q4, PFG_QKV);
         else PFG_GO(QF_Q4, PFG_SWIGLU);
     } else {
         if (epi == PFG_STORE) PFG_GO(QF_Q8, PFG_STORE);
-        else if (epi == PFG_RESID) PFG_GO(QF_Q8, PFG_RESID);
+        else if (epi == PFG_RESID) PFG_GO_R(QF_Q8);
         else if (epi == PFG_QKV) PFG_GO(QF_Q8, PFG_QKV);
         else PFG_GO(QF_Q8, PFG_SWIGLU);
     }
 #undef PFG_GO
+#undef PFG_GO_R
     BMK_LAUNCH_CHECK();
     return 0;
 }
