@@ -174,11 +174,16 @@ def cosine(a, b):
 HD64 = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
 
 
-# hd64-150 / -300 / -520: the attention's longest query blocks split into 2, 3 and 4 key segments
+# widths that are odd multiples of 32 (odd Q8 block counts per row, GEMM tiles and the SwiGLU output cut
+# short of 64 columns, zero-padded operands)
+ODD = dict(D=96, H=160, NH=3, NKV=1, HD=32, L=2, V=512)
+
+
+# hd64-150 / -300 / -520: prompts whose attention blocks walk 2 to 5 key chunks
 @pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1), (HD64, 1), (HD64, 17), (HD64, 70),
-                                    (HD64, 150), (HD64, 300), (HD64, 520)],
+                                    (HD64, 150), (HD64, 300), (HD64, 520), (ODD, 45)],
                          ids=["tiny-12", "small-40", "small-1", "hd64-1", "hd64-17", "hd64-70", "hd64-150",
-                              "hd64-300", "hd64-520"])
+                              "hd64-300", "hd64-520", "odd-45"])
 def test_prefill_matches_stepwise(dims, n):
     """bm_forward over a prompt at position 0 (one pass, bf16-MFMA projections)
     against stepping the same tokens one by one, as the reference's
@@ -210,12 +215,14 @@ def test_prefill_matches_stepwise(dims, n):
             assert top2[1] - top2[0] <= np.abs(a.astype(np.float64) - b).max()
 
 
-def test_prefill_smollm2_135m_prompt():
-    """Config 5's 128-token prompt through bm_forward (one pass) against 128
-    decode steps: the reference's prefill_test.c criteria at full size."""
+@pytest.mark.parametrize("n", [128, 512])
+def test_prefill_smollm2_135m_prompt(n):
+    """Config 5's 128-token prompt, and the bench's 512-token one, through
+    bm_forward (one pass) against n decode steps: the reference's
+    prefill_test.c criteria at full size."""
     dims = bmhip.SMOLLM2_135M
-    toks = bmhip.synth_uniform_int(2025, 0, dims["V"], 128)
-    eng = bmhip.Engine(dims, max_seq_len=160, seed=2025)
+    toks = bmhip.synth_uniform_int(2025, 0, dims["V"], n)
+    eng = bmhip.Engine(dims, max_seq_len=n + 32, seed=2025)
     pre = eng.forward(toks)
     pre_next = eng.step(7)
     eng.reset()
