@@ -1560,13 +1560,23 @@ __global__ __launch_bounds__(64 * AG_WAVES) void k_dec_attn_g(DecAttn a) {
 /* x[p] = emb[tok[p]], and the first layer's RMSNorm operand as the q/k/v
  * GEMM takes it (pf_gemm.h): an = bf16(x * g) in fragment order (columns
  * past D zero) and the row's sum of squares in slot 0 of ss (the other
- * ss_tiles - 1 slots zero). */
+ * ss_tiles - 1 slots zero).  With rope given, also position p's (cos, sin)
+ * per rotary pair, rope[p][HD/2][2] (the angle (float)p * inv_freq[t] as
+ * k_pf_kv takes it), for the q/k/v GEMM epilogue that rotates k. */
 __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, const float* __restrict__ emb,
                                                  float* __restrict__ x, int D, const float* __restrict__ g,
                                                  unsigned short* __restrict__ an, float* __restrict__ ss_out,
-                                                 int ss_tiles, int ss_ld) {
+                                                 int ss_tiles, int ss_ld, DecAttn ra, float* __restrict__ rope) {
     __shared__ float sh[4];
     const int p = blockIdx.x;
+    if (rope) {
+        const int half = ra.HD / 2;
+        for (int i = threadIdx.x; i < half; i += NT) {
+            const float ang = (float)p * ra.inv_freq[i];
+            rope[((size_t)p * half + i) * 2] = cosf(ang);
+            rope[((size_t)p * half + i) * 2 + 1] = sinf(ang);
+        }
+    }
     const float* er = emb + (size_t)tok[p] * D;
     float* xr = x + (size_t)p * D;
     float ss = 0.0f;
@@ -1587,19 +1597,6 @@ __global__ __launch_bounds__(NT) void k_pf_embed(const int* __restrict__ tok, co
                        ((unsigned int)bf16_bits(er[8 * c + 2 * e + 1] * g[8 * c + 2 * e + 1]) << 16);
         *(uint4*)(an + frag_index(p, 8 * c, nks)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-}
-
-/* (cos, sin) of every prompt position p < n and rotary pair t < HD/2, out
- * [n][HD/2][2]: the angle (float)p * inv_freq[t] as k_pf_kv takes it, for
- * the q/k/v GEMM epilogue that rotates k (pf_gemm.hip). */
-__global__ __launch_bounds__(NT) void k_pf_rope_table(DecAttn a, int n, float* __restrict__ out) {
-    const int half = a.HD / 2;
-    const long i = (long)blockIdx.x * NT + threadIdx.x;
-    if (i >= (long)n * half) return;
-    const int p = (int)(i / half), t = (int)(i - (long)p * half);
-    const float ang = (float)p * a.inv_freq[t];
-    out[2 * i] = cosf(ang);
-    out[2 * i + 1] = sinf(ang);
 }
 
 /* RoPE of every position's k and the cache append of k and v (layer a.layer,
@@ -2518,17 +2515,11 @@ extern "C" int dec_cast_f16(const float* src, unsigned short* dst, long n, hipSt
 /* Prefill launchers (arguments validated by engine.cpp). */
 
 extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, const float* g,
-                            unsigned short* an, float* ss, int ss_tiles, int ss_ld, hipStream_t s) {
+                            unsigned short* an, float* ss, int ss_tiles, int ss_ld, const DecAttn* ra, float* rope,
+                            hipStream_t s) {
     BMK_REQUIRE(D % 32 == 0 && ss_tiles >= 1 && ss_tiles <= NT && ss_ld >= n && ((uintptr_t)an & 15) == 0,
                 "prefill embedding: D %d, %d sum slots", D, ss_tiles);
-    hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(NT), 0, s, tok, emb, x, D, g, an, ss, ss_tiles, ss_ld);
-    BMK_LAUNCH_CHECK();
-    return 0;
-}
-
-extern "C" int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s) {
-    const long cnt = (long)n * (a->HD / 2);
-    hipLaunchKernelGGL(k_pf_rope_table, dim3((unsigned)((cnt + NT - 1) / NT)), dim3(NT), 0, s, *a, n, out);
+    hipLaunchKernelGGL(k_pf_embed, dim3(n), dim3(NT), 0, s, tok, emb, x, D, g, an, ss, ss_tiles, ss_ld, *ra, rope);
     BMK_LAUNCH_CHECK();
     return 0;
 }

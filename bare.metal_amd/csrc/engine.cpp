@@ -47,8 +47,7 @@ int dec_launch_embed(const DecEmbed* a, hipStream_t s);
 int dec_launch_mv(const DecMv* a, hipStream_t s);
 int dec_launch_attn(const DecAttn* a, int B, hipStream_t s);
 int dec_pf_embed(const int* tok, const float* emb, float* x, int n, int D, const float* g, unsigned short* an,
-                 float* ss, int ss_tiles, int ss_ld, hipStream_t s);
-int dec_pf_rope_table(const DecAttn* a, int n, float* out, hipStream_t s);
+                 float* ss, int ss_tiles, int ss_ld, const DecAttn* ra, float* rope, hipStream_t s);
 int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n, unsigned short* out16,
                      int kv_done, hipStream_t s);
 int q4_pack_f32(const float* src, unsigned char* dst, long n, hipStream_t s);
@@ -1046,8 +1045,8 @@ static int prefill(bm_session_t* S, const int* tokens, int n, bool noalloc) {
      * residual GEMM write bf16(x * g) of the next norm and the rows' partial
      * sums of squares, and the GEMM that takes them scales its rows */
     int ss_parts = 1; /* the partial sums per row the last writer left (the embedding: the whole sum) */
-    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, m->d_ln1, w.a16, w.ss, ss_parts, n, s) ||
-        (kv_fused && dec_pf_rope_table(&at, n, w.rope, s)))
+    if (dec_pf_embed(w.tok, m->d_emb, w.x, n, D, m->d_ln1, w.a16, w.ss, ss_parts, n, &at, kv_fused ? w.rope : NULL,
+                     s))
         return -1;
     for (int l = 0; l < L; l++) {
         at.layer = l;
