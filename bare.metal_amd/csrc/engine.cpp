@@ -921,8 +921,9 @@ extern "C" float* bm_step_batch(bm_session_t* S, const int* tokens) {
  * to 64): a16 for the first RMSNorm's and the attention's outputs, h16 for
  * the SwiGLU output, a16b for the second RMSNorm's; the tokens, the RoPE
  * (cos, sin) table of the prompt's positions, and the rows' partial sums of
- * squares [ceil(D / 32)][n] for the RMSNorm scale (one per column tile of
- * the residual GEMM that wrote them).  bm_forward keeps it in session buffers allocated
+ * squares [2 ceil(D / 64)][n] for the RMSNorm scale (one per column tile of
+ * the residual GEMM that wrote them: its 32-column tiles cover whole
+ * 64-column steps).  bm_forward keeps it in session buffers allocated
  * on the first prefill; bm_forward_noalloc carves it from the library's
  * static per-GPU array. */
 struct PfWork {
@@ -943,7 +944,7 @@ static size_t pf_work_layout(const bm_model_t* m, int n, size_t sz[PF_PARTS], si
     const size_t a_cols = ((size_t)std::max(m->D, m->QD) + 63) / 64 * 64, h_cols = ((size_t)m->H + 63) / 64 * 64;
     const size_t b[PF_PARTS] = {N * m->D * 4, N * (m->QD + 2 * (size_t)m->KV) * 4, N * m->QD * 4, N32 * a_cols * 2,
                                 N32 * h_cols * 2, N * 4, N * (size_t)(m->HD / 2) * 8,
-                                N32 * (((size_t)m->D + 63) / 64 * 64) * 2, ((size_t)m->D + 31) / 32 * N * 4};
+                                N32 * (((size_t)m->D + 63) / 64 * 64) * 2, ((size_t)m->D + 63) / 64 * 2 * N * 4};
     size_t at = 0;
     for (int i = 0; i < PF_PARTS; i++) {
         if (sz) sz[i] = b[i];
