@@ -1684,7 +1684,7 @@ struct PfFlat {
 
 template <int MODE>
 __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f, const float* __restrict__ q,
-                                              unsigned short* __restrict__ out16, int n) {
+                                              unsigned short* __restrict__ out16, int n, int q_roped) {
     constexpr int HD = 64, HD4 = HD / 4;
     constexpr int LDK = HD + 4, LDVT = PKC + 4;
     constexpr int NSB = PKC / 16; /* sub-blocks per chunk */
@@ -1704,10 +1704,11 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
     const int col = lane & 15, grp = lane >> 4; /* MFMA column (query / key row) and lane group */
     const int kh = h / kv_mul;
     const int p = p0 + col; /* this lane's query position */
-    if (MODE == PF_FLAT) {
+    if (MODE == PF_FLAT || q_roped) { /* q already rotated */
+        const float* Q = MODE == PF_FLAT ? f.Q : q;
         for (int i = t; i < PQB * HD; i += PNT) {
             const int r = i / HD, e = i - r * HD;
-            Qs[i] = f.Q[((size_t)min(p0 + r, n - 1) * NH + h) * HD + e];
+            Qs[i] = Q[((size_t)min(p0 + r, n - 1) * NH + h) * HD + e];
         }
     } else {
         for (int i = t; i < PQB * (HD / 2); i += PNT) {
@@ -1896,14 +1897,14 @@ __device__ __forceinline__ void pf_attn_block(const DecAttn& a, const PfFlat& f,
 }
 
 __global__ __launch_bounds__(PNT) void k_pf_attn_blk(DecAttn a, const float* __restrict__ q,
-                                                    unsigned short* __restrict__ out16, int n) {
+                                                    unsigned short* __restrict__ out16, int n, int q_roped) {
     const PfFlat f = {};
-    pf_attn_block<PF_ENGINE>(a, f, q, out16, n);
+    pf_attn_block<PF_ENGINE>(a, f, q, out16, n, q_roped);
 }
 
 __global__ __launch_bounds__(PNT) void k_attn_prefill64(PfFlat f) {
     const DecAttn a = {};
-    pf_attn_block<PF_FLAT>(a, f, nullptr, nullptr, f.S);
+    pf_attn_block<PF_FLAT>(a, f, nullptr, nullptr, f.S, 0);
 }
 
 /* Any head size up to 128 on the reference's prefill attention ABI: one
@@ -2525,11 +2526,11 @@ extern "C" int dec_pf_embed(const int* tok, const float* emb, float* x, int n, i
 }
 
 /* RoPE + cache append of every position (unless the q/k/v GEMM's epilogue
- * did it: kv_done), then causal attention; the result goes to out16 as
- * bf16 in fragment order (the o-projection's operand).  Head size 64: blocks of PQB positions per workgroup, written
- * as bf16 directly; other head sizes: one workgroup per (head, position)
- * into a->out (fp32), then the fragment-order cast (which also zeroes the
- * columns past NH * HD). */
+ * did it, q's RoPE too: kv_done), then causal attention; the result goes to
+ * out16 as bf16 in fragment order (the o-projection's operand).  Head size
+ * 64: blocks of PQB positions per workgroup, written as bf16 directly; other
+ * head sizes: one workgroup per (head, position) into a->out (fp32), then
+ * the fragment-order cast (which also zeroes the columns past NH * HD). */
 extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k, const float* v, int n,
                                 unsigned short* out16, int kv_done, hipStream_t s) {
     if (!kv_done) {
@@ -2537,7 +2538,8 @@ extern "C" int dec_pf_attention(const DecAttn* a, const float* q, const float* k
         BMK_LAUNCH_CHECK();
     }
     if (a->HD == 64) {
-        hipLaunchKernelGGL(k_pf_attn_blk, dim3(a->NH, (n + PQB - 1) / PQB), dim3(PNT), 0, s, *a, q, out16, n);
+        hipLaunchKernelGGL(k_pf_attn_blk, dim3(a->NH, (n + PQB - 1) / PQB), dim3(PNT), 0, s, *a, q, out16, n,
+                           kv_done);
         BMK_LAUNCH_CHECK();
         return 0;
     }

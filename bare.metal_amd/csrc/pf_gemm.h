@@ -17,8 +17,8 @@
 #define PFG_STORE 0  /* C = A W^T, each problem into its own output */
 #define PFG_RESID 1  /* x += A W^T (the residual stream; one problem) */
 #define PFG_SWIGLU 2 /* h = bf16(silu(A Wg^T) * (A Wu^T)); problem 0 gate, 1 up */
-#define PFG_QKV 3    /* q, k, v of attention heads of size 64: q stored as PFG_STORE does, k rotated
-                      * (RoPE at each row's position) into the K cache, v into the V cache */
+#define PFG_QKV 3    /* q, k, v of attention heads of size 64: q and k rotated (RoPE at each row's
+                      * position), q into its output, k into the K cache, v into the V cache */
 
 /* The prefill's weight layout (pfg_repack): a matrix of N rows of K/32
  * blocks is cut into chunks of 32 rows x one 64-wide K step (two blocks per

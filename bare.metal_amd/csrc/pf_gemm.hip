@@ -287,10 +287,10 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
             }
             *(float4*)&vr[c] = make_float4(v4.x * inv, v4.y * inv, v4.z * inv, v4.w * inv);
         }
-    } else if (EPI == PFG_QKV && p == 1) {
-        /* k: RoPE pairs (d, d + 32) of the tile's KV head, eight per thread
-         * (d from j0), with the position's cos / sin from the table; the
-         * rotated rows go to the K cache, [dim / 4][position][4] */
+    } else if (EPI == PFG_QKV) {
+        /* q and k: RoPE pairs (d, d + 32) of the tile's head, eight per
+         * thread (d from j0), with the position's cos / sin from the table;
+         * rotated q rows go to q, k rows to the K cache, [dim / 4][position][4] */
         float k0[8], k1[8];
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
@@ -311,6 +311,7 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
             cs[c] = t4.x; sn[c] = t4.y; cs[c + 1] = t4.z; sn[c + 1] = t4.w;
         }
         float* kT = a.kc + (size_t)(n0 >> 6) * 64 * a.MS;
+        float* qr = a.p[0].C + (size_t)m * ldc + n0;
 #pragma unroll
         for (int c = 0; c < 8; c += 4) {
             float e0[4], e1[4];
@@ -319,8 +320,14 @@ __global__ __launch_bounds__(PNTH) void k_pf_gemm(PfgArgs a) {
                 e0[q] = k0[c + q] * cs[c + q] - k1[c + q] * sn[c + q];
                 e1[q] = k0[c + q] * sn[c + q] + k1[c + q] * cs[c + q];
             }
-            *(float4*)&kT[((size_t)((j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e0[0], e0[1], e0[2], e0[3]);
-            *(float4*)&kT[((size_t)((32 + j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e1[0], e1[1], e1[2], e1[3]);
+            if (p == 0) {
+                *(float4*)&qr[j0 + c] = make_float4(e0[0], e0[1], e0[2], e0[3]);
+                *(float4*)&qr[32 + j0 + c] = make_float4(e1[0], e1[1], e1[2], e1[3]);
+            } else {
+                *(float4*)&kT[((size_t)((j0 + c) >> 2) * a.MS + m) * 4] = make_float4(e0[0], e0[1], e0[2], e0[3]);
+                *(float4*)&kT[((size_t)((32 + j0 + c) >> 2) * a.MS + m) * 4] =
+                    make_float4(e1[0], e1[1], e1[2], e1[3]);
+            }
         }
     } else {
         float xn[CPT]; /* the stored values (x after the residual add); 0 past N */
@@ -434,7 +441,8 @@ extern "C" int pfg_launch(PfgArgs* a, int qf, int epi, hipStream_t s) {
                     (epi == PFG_SWIGLU && a->nprob == 2 && a->h && a->p[0].N == a->p[1].N) ||
                     (epi == PFG_QKV && a->nprob == 3 && a->kc && a->vc && a->rope && a->M <= a->MS &&
                      a->p[1].N == a->p[2].N && ((uintptr_t)a->rope & 15) == 0 &&
-                     a->p[1].N % 64 == 0 && ((uintptr_t)a->kc & 15) == 0 && ((uintptr_t)a->vc & 15) == 0),
+                     a->p[0].N % 64 == 0 && a->p[1].N % 64 == 0 && a->p[0].ldc % 4 == 0 &&
+                     ((uintptr_t)a->p[0].C & 15) == 0 && ((uintptr_t)a->kc & 15) == 0 && ((uintptr_t)a->vc & 15) == 0),
                 "pf_gemm: epilogue %d does not fit its %d problems", epi, a->nprob);
     BMK_REQUIRE(((uintptr_t)a->A & 15) == 0 && ((uintptr_t)a->W & 15) == 0 && ((uintptr_t)a->h & 15) == 0 &&
                     ((uintptr_t)a->an & 15) == 0,
