@@ -177,13 +177,15 @@ HD64 = dict(D=256, H=512, NH=4, NKV=2, HD=64, L=2, V=1024)
 # widths that are odd multiples of 32 (odd Q8 block counts per row, GEMM tiles and the SwiGLU output cut
 # short of 64 columns, zero-padded operands)
 ODD = dict(D=96, H=160, NH=3, NKV=1, HD=32, L=2, V=512)
+# widths past 12 K steps of 64 (each of the prefill GEMM's four waves walks two groups of load steps)
+WIDE = dict(D=832, H=1024, NH=13, NKV=1, HD=64, L=1, V=512)
 
 
 # hd64-150 / -300 / -520: prompts whose attention blocks walk 2 to 5 key chunks
 @pytest.mark.parametrize("dims,n", [(TINY, 12), (SMALL, 40), (SMALL, 1), (HD64, 1), (HD64, 17), (HD64, 70),
-                                    (HD64, 150), (HD64, 300), (HD64, 520), (ODD, 45)],
+                                    (HD64, 150), (HD64, 300), (HD64, 520), (ODD, 45), (WIDE, 40)],
                          ids=["tiny-12", "small-40", "small-1", "hd64-1", "hd64-17", "hd64-70", "hd64-150",
-                              "hd64-300", "hd64-520", "odd-45"])
+                              "hd64-300", "hd64-520", "odd-45", "wide-40"])
 def test_prefill_matches_stepwise(dims, n):
     """bm_forward over a prompt at position 0 (one pass, bf16-MFMA projections)
     against stepping the same tokens one by one, as the reference's
